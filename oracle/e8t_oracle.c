@@ -1,0 +1,359 @@
+/*
+ * e8t_oracle.c -- CPU restatement of the reference's ternary-E8 (1.5 bit/weight)
+ * codec and of its dequantize-then-matmul forward.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker: only tests/, the smoke
+ * check in __graft_entry__.py and bench.py's cpu_baseline leg load it.  The
+ * product (the HIP library under ojasx-open-source-cuda_amd/) never links it.
+ *
+ * Every function follows the reference's Python (ojasx2/math/lattice.py) step by
+ * step, at fp32 with no FMA contraction except where torch itself fuses (the
+ * vectorised norm).  Build with -ffp-contract=off (see oracle/Makefile).
+ *
+ * Reference anchors:
+ *   codebook            lattice.py:292-332   (rank = raw/2 closed form; checked
+ *                                             against the reference's own C++ LUT,
+ *                                             ojasx_math_core.hpp:549-573, via oracle/_ref)
+ *   encoder             lattice.py:338-384
+ *   decoder             lattice.py:386-419
+ *   portable forward    lattice.py:610-624  (unpack + F.linear)
+ *
+ * Pinning of each function (tests/test_oracle_*.py):
+ *   ojo_f32_to_f16 / ojo_f32_to_bf16   vs numpy / torch conversions (library)
+ *   ojo_e8t_group_scale                vs torch.norm(...)/math.sqrt(gs)+1e-8 (library)
+ *   ojo_e8t_quantize8                  vs exhaustive nearest-point search over the 3,281
+ *                                      codewords in exact arithmetic, plus hand-derived
+ *                                      tie cases (tests/golden/known_answers.json)
+ *   ojo_e8t_encode / _decode           byte layout closed form, the reference tests'
+ *                                      invariants (size, cos > 0.7, row-wise == whole)
+ *   ojo_e8t_gemm_f64                   vs the reference's C++ fused GEMV (oracle/_ref)
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define OJO_API __attribute__((visibility("default")))
+
+static const int32_t kPow3[8] = {1, 3, 9, 27, 81, 243, 729, 2187};
+
+/* ------------------------------------------------------------------------- */
+/* Number format conversions (IEEE binary16 and bfloat16, round-nearest-even) */
+/* ------------------------------------------------------------------------- */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* fp32 -> fp16, RNE, subnormals kept, overflow -> inf, NaN -> quiet NaN.
+ * Same results as torch's Tensor.to(torch.float16) on CPU (pack, lattice.py:384). */
+OJO_API uint16_t ojo_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u));
+    uint32_t e = ax >> 23;
+    if (e < 113) { /* below 2^-14: half subnormal (or zero) */
+        if (e == 0) return (uint16_t)sign; /* fp32 subnormal: far below half range */
+        uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126 - e; /* value / 2^-24 = mant * 2^(e-126) */
+        if (shift > 24) return (uint16_t)sign; /* < 2^-25 (or == with even result) */
+        uint32_t q = mant >> shift;
+        uint32_t rem = mant & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t he = e - 112; /* rebias 127 -> 15 */
+    uint32_t mant = ax & 0x7FFFFFu;
+    uint32_t q = (he << 10) | (mant >> 13);
+    uint32_t rem = mant & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    if (q >= 0x7C00u) q = 0x7C00u; /* overflow to inf */
+    return (uint16_t)(sign | q);
+}
+
+OJO_API float ojo_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    if (e == 0x1F) return u2f(sign | 0x7F800000u | (m << 13));
+    if (e == 0) {
+        /* subnormal: m * 2^-24, exact in fp32 */
+        float v = (float)m * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112) << 23) | (m << 13));
+}
+
+/* fp32 -> bf16, RNE, NaN -> 0x7FC0 (c10::BFloat16 round_to_nearest_even). */
+OJO_API uint16_t ojo_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+OJO_API float ojo_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* ------------------------------------------------------------------------- */
+/* Codebook: D8 cap {-1,0,1}^8 with even coordinate sum, 3,281 points.         */
+/* lattice.py:309-318 enumerates raw = sum (q_i+1) 3^i in increasing order and  */
+/* keeps even-digit-sum entries; since 3^i is odd, digit-sum parity == raw      */
+/* parity, so rank = raw / 2 and raw = 2 * rank.                               */
+/* ------------------------------------------------------------------------- */
+
+OJO_API void ojo_e8t_codeword(int32_t code, int8_t coords[8]) {
+    int32_t raw = 2 * code;
+    for (int i = 0; i < 8; ++i) {
+        coords[i] = (int8_t)(raw % 3 - 1);
+        raw /= 3;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Encoder                                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* Scale of one flat group (lattice.py:355-356):
+ *   s = torch.norm(w_g) / math.sqrt(gs) + 1e-8       (fp32 throughout)
+ * torch's CPU norm over the last dim keeps 8 fp32 FMA lanes, lane j summing
+ * w[j], w[j+8], ... in order, then adds the 8 lanes left to right, then takes a
+ * correctly rounded sqrt.  The python scalar sqrt(gs) is rounded to fp32 before
+ * the (true) division. */
+OJO_API float ojo_e8t_group_scale(const float* w, int64_t gs) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t k = 0; k < gs; k += 8)
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(w[k + j], w[k + j], acc[j]);
+    float sum = acc[0];
+    for (int j = 1; j < 8; ++j) sum = sum + acc[j];
+    float nrm = sqrtf(sum);
+    float root = (float)sqrt((double)gs);
+    float s = nrm / root;
+    return s + 1e-8f;
+}
+
+/* Nearest point of one 8-vector v (already divided by the scale), following
+ * lattice.py:358-373 exactly:
+ *   q   = clamp(round_half_even(v), -1, 1)
+ *   alt = (q == 0) ? (v >= 0 ? +1 : -1) : 0
+ *   pen = (alt - v)^2 - (q - v)^2            (three separately rounded ops)
+ *   if sum(q) is odd: q[first argmin pen] = alt[...]
+ *   code = (sum (q_i + 1) 3^i) / 2
+ * Returns the 12-bit code; writes the chosen coordinates to q_out if non-null. */
+OJO_API int32_t ojo_e8t_quantize8(const float v[8], int8_t q_out[8]) {
+    float q[8], alt[8], pen[8];
+    int sum = 0;
+    for (int i = 0; i < 8; ++i) {
+        float r = rintf(v[i]); /* default rounding mode: nearest-even */
+        if (r < -1.0f) r = -1.0f;
+        if (r > 1.0f) r = 1.0f;
+        q[i] = r;
+        sum += (int)r;
+    }
+    for (int i = 0; i < 8; ++i) {
+        alt[i] = (q[i] == 0.0f) ? (v[i] >= 0.0f ? 1.0f : -1.0f) : 0.0f;
+        float a = alt[i] - v[i];
+        float b = q[i] - v[i];
+        float a2 = a * a;
+        float b2 = b * b;
+        pen[i] = a2 - b2;
+    }
+    if (sum & 1) {
+        int best = 0;
+        for (int i = 1; i < 8; ++i)
+            if (pen[i] < pen[best]) best = i;
+        q[best] = alt[best];
+    }
+    int32_t raw = 0;
+    for (int i = 0; i < 8; ++i) {
+        int d = (int)q[i] + 1;
+        raw += d * kPow3[i];
+        if (q_out) q_out[i] = (int8_t)(d - 1);
+    }
+    return raw >> 1;
+}
+
+static inline void put_pair(uint8_t* dst, int32_t c0, int32_t c1) {
+    /* lattice.py:379-383: two 12-bit codes, little-endian bit stream */
+    dst[0] = (uint8_t)(c0 & 0xFF);
+    dst[1] = (uint8_t)(((c0 >> 8) & 0x0F) | ((c1 & 0x0F) << 4));
+    dst[2] = (uint8_t)((c1 >> 4) & 0xFF);
+}
+
+/* Encode one flat group of gs fp32 weights. */
+static void encode_group(const float* w, int64_t gs, uint8_t* packed, uint16_t* scale16,
+                         float* scale32) {
+    float s = ojo_e8t_group_scale(w, gs);
+    int32_t codes[2];
+    for (int64_t t = 0; t < gs / 8; ++t) {
+        float v[8];
+        for (int i = 0; i < 8; ++i) v[i] = w[8 * t + i] / s;
+        codes[t & 1] = ojo_e8t_quantize8(v, 0);
+        if (t & 1) put_pair(packed + 3 * (t >> 1), codes[0], codes[1]);
+    }
+    *scale16 = ojo_f32_to_f16(s);
+    if (scale32) *scale32 = s;
+}
+
+/* Padded element count used by the reference (flat zero padding to a multiple of gs). */
+OJO_API int64_t ojo_e8t_padded(int64_t numel, int64_t gs) {
+    return numel + ((gs - numel % gs) % gs);
+}
+
+/* Effective group size: the reference silently coerces gs to 16 when it is not a
+ * positive multiple of 16 (lattice.py:346-347). */
+OJO_API int64_t ojo_e8t_effective_gs(int64_t gs) {
+    return (gs <= 0 || gs % 16 != 0) ? 16 : gs;
+}
+
+/* TernaryE8LatticePacker.pack on a flat fp32 array of numel values.
+ * packed: padded*3/16 bytes; scales: padded/gs fp16 bit patterns;
+ * scales32 (optional): the fp32 scales the codes were computed with. */
+OJO_API void ojo_e8t_encode(const float* w, int64_t numel, int64_t gs, uint8_t* packed,
+                            uint16_t* scales, float* scales32, int nthreads) {
+    gs = ojo_e8t_effective_gs(gs);
+    int64_t padded = ojo_e8t_padded(numel, gs);
+    int64_t ngroups = padded / gs;
+    int64_t full = numel / gs;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t g = 0; g < full; ++g)
+        encode_group(w + g * gs, gs, packed + g * gs * 3 / 16, scales + g,
+                     scales32 ? scales32 + g : 0);
+    (void)nthreads;
+    if (full < ngroups) { /* tail group, zero padded (F.pad) */
+        float tmp[4096];
+        float* buf = tmp;
+        if (gs > 4096) return; /* not reachable from the tests */
+        int64_t rem = numel - full * gs;
+        for (int64_t i = 0; i < gs; ++i) buf[i] = i < rem ? w[full * gs + i] : 0.0f;
+        encode_group(buf, gs, packed + full * gs * 3 / 16, scales + full,
+                     scales32 ? scales32 + full : 0);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Decoder                                                                     */
+/* ------------------------------------------------------------------------- */
+
+static inline int32_t get_code(const uint8_t* packed, int64_t t) {
+    const uint8_t* b = packed + 3 * (t >> 1);
+    if ((t & 1) == 0) return (int32_t)b[0] | ((int32_t)(b[1] & 0x0F) << 8);
+    return (int32_t)(b[1] >> 4) | ((int32_t)b[2] << 4);
+}
+
+/* Decoded weight value as the reference's unpack produces it for out dtype
+ * (lattice.py:412-419): coords.to(dtype) * scales.to(dtype).
+ *   dtype 0 (fp32): coord * float(s16)            (exact)
+ *   dtype 1 (fp16): coord * s16                   (exact)
+ *   dtype 2 (bf16): coord * bf16_rne(float(s16))  (exact after the scale cast) */
+static inline float deq_value(int coord, uint16_t s16, int dtype) {
+    float s = ojo_f16_to_f32(s16);
+    if (dtype == 2) s = ojo_bf16_to_f32(ojo_f32_to_bf16(s));
+    return (float)coord * s;
+}
+
+/* Unpack into numel (unpadded prefix) values.  out_dtype: 0 f32, 1 f16 bits,
+ * 2 bf16 bits.  gs is the group size (the reference infers padded/numel(scales)). */
+OJO_API void ojo_e8t_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel,
+                            int64_t gs, int out_dtype, void* out) {
+    int64_t ncodes = (numel + 7) / 8;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t t = 0; t < ncodes; ++t) {
+        int32_t raw = 2 * get_code(packed, t);
+        uint16_t s16 = scales[(8 * t) / gs];
+        for (int i = 0; i < 8; ++i) {
+            int coord = raw % 3 - 1;
+            raw /= 3;
+            int64_t idx = 8 * t + i;
+            if (idx >= numel) break;
+            float v = deq_value(coord, s16, out_dtype);
+            if (out_dtype == 0) ((float*)out)[idx] = v;
+            else if (out_dtype == 1) ((uint16_t*)out)[idx] = ojo_f32_to_f16(v);
+            else ((uint16_t*)out)[idx] = ojo_f32_to_bf16(v);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Dequantize-then-matmul reference (fp64 accumulation)                       */
+/* ------------------------------------------------------------------------- */
+
+/* y[m,n] = sum_k x[m,k] * Wdeq[n,k] + bias[n], accumulated in fp64, with Wdeq
+ * decoded exactly as the reference's portable path decodes for dtype w_dtype
+ * (lattice.py:618-623).  x, bias fp32 (the caller widens bf16/fp16 inputs
+ * exactly).  Requires the row layout K % gs == 0 (one row = whole groups). */
+OJO_API void ojo_e8t_gemm_f64(const float* x, const uint8_t* packed, const uint16_t* scales,
+                              const float* bias, double* y, int64_t M, int64_t N, int64_t K,
+                              int64_t gs, int w_dtype) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t n = 0; n < N; ++n) {
+        double wrow_buf[16384];
+        double* wrow = wrow_buf;
+        if (K > 16384) continue; /* not reachable from the tests */
+        for (int64_t t = 0; t < K / 8; ++t) {
+            int64_t tt = n * (K / 8) + t;
+            int32_t raw = 2 * get_code(packed, tt);
+            uint16_t s16 = scales[(8 * tt) / gs];
+            for (int i = 0; i < 8; ++i) {
+                int coord = raw % 3 - 1;
+                raw /= 3;
+                wrow[8 * t + i] = (double)deq_value(coord, s16, w_dtype);
+            }
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            double acc = bias ? (double)bias[n] : 0.0;
+            const float* xr = x + m * K;
+            for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * wrow[k];
+            y[m * N + n] = acc;
+        }
+    }
+}
+
+/* grad_x[m,k] = sum_n gy[m,n] * Wdeq[n,k] (fp64), the reference's backward
+ * (lattice.py:686-696). */
+OJO_API void ojo_e8t_gemm_bwd_f64(const float* gy, const uint8_t* packed, const uint16_t* scales,
+                                  double* gx, int64_t M, int64_t N, int64_t K, int64_t gs,
+                                  int w_dtype) {
+    memset(gx, 0, sizeof(double) * (size_t)(M * K));
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t t = 0; t < K / 8; ++t) {
+            int64_t tt = n * (K / 8) + t;
+            int32_t raw = 2 * get_code(packed, tt);
+            uint16_t s16 = scales[(8 * tt) / gs];
+            for (int i = 0; i < 8; ++i) {
+                int coord = raw % 3 - 1;
+                raw /= 3;
+                double wv = (double)deq_value(coord, s16, w_dtype);
+                if (wv == 0.0) continue;
+                for (int64_t m = 0; m < M; ++m) gx[m * K + 8 * t + i] += (double)gy[m * N + n] * wv;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Array helpers for the Python test wrapper                                  */
+/* ------------------------------------------------------------------------- */
+
+OJO_API void ojo_f32_to_f16_array(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ojo_f32_to_f16(in[i]);
+}
+OJO_API void ojo_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ojo_f32_to_bf16(in[i]);
+}
+OJO_API void ojo_e8t_group_scale_array(const float* w, int64_t ngroups, int64_t gs, float* out) {
+    for (int64_t g = 0; g < ngroups; ++g) out[g] = ojo_e8t_group_scale(w + g * gs, gs);
+}
+OJO_API void ojo_e8t_quantize8_array(const float* v, int64_t nvec, int32_t* codes) {
+    for (int64_t t = 0; t < nvec; ++t) codes[t] = ojo_e8t_quantize8(v + 8 * t, 0);
+}
