@@ -1,0 +1,95 @@
+/*
+ * ojasx_e8t.h -- C ABI of the MI355X (gfx950) ternary-E8 quantized-weight path.
+ *
+ * Shared library: ojasx-open-source-cuda_amd/lib/libojasx_e8t.so
+ *
+ * Plain pointers and sizes only.  Every pointer argument except `stream` is a
+ * device pointer (HBM) on the current HIP device.  `stream` is a hipStream_t
+ * (NULL = the null stream).  No entry point allocates device memory, takes a
+ * lock or keeps mutable global state; each one enqueues its kernels on `stream`
+ * and returns without synchronising.  Results are ready when the stream is.
+ *
+ * Data layout (identical to the reference's buffers, so existing state_dicts load):
+ *   packed  uint8 [padded * 3 / 16]   two 12-bit codes per 3 bytes, little-endian bit
+ *                                      stream: code t occupies bits [12t, 12t+12)
+ *                                      (ojasx2/math/lattice.py:375-383)
+ *   scales  uint16 [padded / gs]       IEEE binary16 bit patterns, one per flat group of
+ *                                      gs weights (lattice.py:355-356,384)
+ *   padded  = numel rounded up to a multiple of gs (flat zero padding, lattice.py:351-353)
+ *   A weight matrix W[N, K] is flattened row-major; element (n, k) is flat index n*K + k.
+ *   When K % gs == 0 each row owns K*3/16 bytes and K/gs scales (streaming_e8.py:182-192).
+ *
+ * dtype codes: OJX_F32, OJX_F16, OJX_BF16 (activations, outputs, decoded weights).
+ *
+ * Return value: OJX_OK (0) or a negative OJX_E* status; ojx_e8t_last_error() gives the
+ * message of the calling thread's last failure.
+ */
+#ifndef OJASX_E8T_H
+#define OJASX_E8T_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OJX_F32 = 0, OJX_F16 = 1, OJX_BF16 = 2 };
+
+enum {
+    OJX_OK = 0,
+    OJX_EINVAL = -1,  /* null pointer, negative or inconsistent size            */
+    OJX_ELAYOUT = -2, /* group size / shape combination the op does not accept  */
+    OJX_EDTYPE = -3,  /* unknown dtype code                                     */
+    OJX_EHIP = -4,    /* HIP runtime or launch error                            */
+    OJX_EDEVICE = -5  /* current device is not gfx950                           */
+};
+
+/* ABI version (major * 10000 + minor * 100 + patch). */
+int ojx_e8t_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* ojx_e8t_last_error(void);
+
+/* Encoder.  Replaces TernaryE8LatticePacker.pack (ojasx2/math/lattice.py:338-384);
+ * the reference's GPU route for it is a chain of ~25 ATen kernels, its streaming
+ * caller is streaming_e8._pack_row_block (streaming_e8.py:112-123).
+ *   w       [numel] weights of dtype w_dtype (F32, F16 or BF16; widened exactly to fp32)
+ *   gs      group size; must be a positive multiple of 16 (the Python layer applies the
+ *           reference's silent coercion to 16 first, lattice.py:346-347)
+ *   packed  [padded*3/16] out,  scales [padded/gs] out (fp16 bits)
+ * Bit-exact with the reference's CPU pack (ATen AVX2/AVX512 norm order). Inputs must be
+ * finite. */
+int ojx_e8t_encode(const void* w, int w_dtype, int64_t numel, int64_t gs, uint8_t* packed,
+                   uint16_t* scales, void* stream);
+
+/* Decoder.  Replaces TernaryE8LatticePacker.unpack (lattice.py:386-419).
+ * Writes the first `numel` decoded weights in out_dtype:
+ *   F32: coord * float(s16);  F16: coord * s16;  BF16: coord * bf16_rne(float(s16)).
+ * Bit-exact with the reference. */
+int ojx_e8t_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel, int64_t gs,
+                   int out_dtype, void* out, void* stream);
+
+/* Fused forward y[M,N] = x[M,K] . Wdeq[N,K]^T (+ bias[N]), fp32 accumulation, y in dtype.
+ * Replaces fused_ternary_e8_gemm_fwd (ojasx2/math/csrc/ojasx_math_bindings.cpp:407-472,
+ * schema at :594) and dispatch_tilelang_e8_gemm (ojasx2/tilelang_kernels.py:370-419);
+ * called from _FusedE8GEMMFunction.forward (lattice.py:584-608).
+ *   x, y, bias in `dtype`; bias may be NULL.  Wdeq follows the decoder's rule for `dtype`.
+ *   Any K >= 1 (flat layout); the MFMA kernels run when K % 256 == 0 and gs == 32 for
+ *   F16/BF16, other shapes and F32 use a general tiled kernel.  Never declines. */
+int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
+                     const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                     int dtype, void* stream);
+
+/* Fused backward grad_x[M,K] = grad_y[M,N] . Wdeq[N,K], fp32 accumulation, in dtype.
+ * Replaces fused_ternary_e8_gemm_bwd_dx (ojasx_math_bindings.cpp:479-533, schema :594);
+ * called from _FusedE8GEMMFunction.backward (lattice.py:656-696). */
+int ojx_e8t_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_t* scales,
+                        void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OJASX_E8T_H */

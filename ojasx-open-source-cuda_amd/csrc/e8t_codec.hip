@@ -1,0 +1,300 @@
+// e8t_codec.hip -- ternary-E8 encoder and decoder kernels for gfx950.
+//
+// Encoder: bit-exact restatement of TernaryE8LatticePacker.pack
+// (ojasx2/math/lattice.py:338-384) as one fused pass: each weight is read once
+// from HBM (2 B for fp16/bf16) and 0.25 B of codes + scale is written.  The
+// reference's device route runs ~25 ATen element-wise kernels with int64
+// temporaries for the same work.
+//
+// One lane per flat group: the reference's scale is torch's CPU norm, whose
+// summation order is a sequential FMA chain per lane j over w[j], w[j+8], ...
+// (8 fp32 lanes), so a group's norm is inherently serial over its 8-vectors.  One
+// lane owning the group computes it once (gs/8 + 7 adds per group) and then runs
+// the gs/8 nearest-point searches of its 8-vectors; splitting a group across
+// lanes would cost a cross-lane exchange per link of the chain.
+//
+// Decoder: restatement of TernaryE8LatticePacker.unpack (lattice.py:386-419),
+// one lane per code pair (3 bytes -> 16 weights), exact for every dtype.
+
+#include "e8t_device.h"
+#include "e8t_internal.h"
+
+namespace ojx {
+
+// Nearest point of one 8-vector of the group with fp32 scale s, as lattice.py:357-373:
+//   v = w / s (correctly rounded)
+//   q = clamp(rint(v), -1, 1); alt = q == 0 ? (v >= 0 ? 1 : -1) : 0
+//   pen = (alt - v)^2 - (q - v)^2 (three rounded ops, never contracted)
+//   odd sum(q): q[first argmin pen] = alt;  code = sum (q_i + 1) 3^i / 2.
+// All integer-valued quantities are carried in fp32, where they are exact.
+__device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, float s) {
+#pragma clang fp contract(off)
+    const float pow3[8] = {1.f, 3.f, 9.f, 27.f, 81.f, 243.f, 729.f, 2187.f};
+    float v[8], q[8];
+    float qsum = 0.f;
+    float raw = 3280.f;  // sum of 3^i: the "+1" of every digit
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[i] = w[i] / s;
+        float r = __builtin_rintf(v[i]);
+        r = fmaxf(r, -1.f);
+        r = fminf(r, 1.f);
+        q[i] = r;
+        qsum = qsum + r;
+        raw = __builtin_fmaf(r, pow3[i], raw);
+    }
+    float best_pen = 0.f, best_delta = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float alt = (q[i] == 0.f) ? (v[i] >= 0.f ? 1.f : -1.f) : 0.f;
+        float a = alt - v[i];
+        float b = q[i] - v[i];
+        float a2 = a * a;
+        float b2 = b * b;
+        float pen = a2 - b2;
+        float delta = (alt - q[i]) * pow3[i];
+        if (i == 0 || pen < best_pen) {
+            best_pen = pen;
+            best_delta = delta;
+        }
+    }
+    // sum(q) is an integer in [-8, 8]; odd parity applies the best flip
+    int odd = ((int)qsum) & 1;
+    raw = odd ? raw + best_delta : raw;
+    return ((uint32_t)raw) >> 1;
+}
+
+// Group scale (lattice.py:355-356) with torch's CPU norm order:
+// 8 fmaf lanes, lane j over elements j, j+8, ...; lanes summed left to right;
+// correctly rounded sqrt; true division by fp32(sqrt(gs)); + fp32(1e-8).
+template <int GS>
+__device__ __forceinline__ float group_scale(const float* __restrict__ w, float root) {
+#pragma clang fp contract(off)
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = w[j] * w[j];
+#pragma unroll
+    for (int t = 1; t < GS / 8; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(w[8 * t + j], w[8 * t + j], acc[j]);
+    float sum = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) sum = sum + acc[j];
+    float nrm = __builtin_sqrtf(sum);
+    float s = nrm / root;
+    return s + 1e-8f;
+}
+
+template <int WDT>
+__device__ __forceinline__ void load8(const void* __restrict__ w, int64_t base, int64_t numel,
+                                      bool vec_ok, float* out) {
+    if (vec_ok && base + 8 <= numel) {
+        if constexpr (WDT == kF32) {
+            const float4* p = reinterpret_cast<const float4*>((const float*)w + base);
+            float4 a = p[0], b = p[1];
+            out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+            out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+        } else {
+            uint4 a = *reinterpret_cast<const uint4*>((const uint16_t*)w + base);
+            uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (WDT == kF16) {
+                    out[2 * i] = f16_bits_to_f32(u[i] & 0xFFFFu);
+                    out[2 * i + 1] = f16_bits_to_f32(u[i] >> 16);
+                } else {
+                    out[2 * i] = bf16_bits_to_f32(u[i] & 0xFFFFu);
+                    out[2 * i + 1] = bf16_bits_to_f32(u[i] >> 16);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            out[i] = (base + i < numel) ? load_as_f32<WDT>(w, base + i) : 0.f;  // F.pad zeros
+    }
+}
+
+constexpr int kEncThreads = 256;
+
+// GS in {16, 32, 64}: the group stays in registers.
+template <int WDT, int GS>
+__global__ __launch_bounds__(kEncThreads) void encode_kernel(
+    const void* __restrict__ w, int64_t numel, int64_t ngroups, float root, bool vec_ok,
+    uint8_t* __restrict__ packed, uint16_t* __restrict__ scales) {
+    constexpr int NV = GS / 8;
+    constexpr int BYTES = GS * 3 / 16;
+    __shared__ uint8_t stage[kEncThreads * BYTES];
+    const int64_t g0 = (int64_t)blockIdx.x * kEncThreads;
+    const int64_t g = g0 + threadIdx.x;
+    if (g < ngroups) {
+        float x[GS];
+#pragma unroll
+        for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+        const float s = group_scale<GS>(x, root);
+        uint8_t* st = stage + threadIdx.x * BYTES;
+#pragma unroll
+        for (int p = 0; p < NV / 2; ++p) {
+            uint32_t c0 = quantize8(x + 16 * p, s);
+            uint32_t c1 = quantize8(x + 16 * p + 8, s);
+            st[3 * p + 0] = (uint8_t)(c0 & 0xFFu);
+            st[3 * p + 1] = (uint8_t)(((c0 >> 8) & 0x0Fu) | ((c1 & 0x0Fu) << 4));
+            st[3 * p + 2] = (uint8_t)((c1 >> 4) & 0xFFu);
+        }
+        scales[g] = (uint16_t)f32_to_f16_bits(s);
+    }
+    __syncthreads();
+    // coalesced copy-out of the block's packed bytes
+    const int64_t ng = (ngroups - g0) < kEncThreads ? (ngroups - g0) : kEncThreads;
+    const int nbytes = (int)ng * BYTES;
+    uint8_t* dst = packed + g0 * BYTES;
+    if ((((uintptr_t)dst) & 3u) == 0) {
+        const int nwords = nbytes >> 2;
+        const uint32_t* src32 = reinterpret_cast<const uint32_t*>(stage);
+        uint32_t* dst32 = reinterpret_cast<uint32_t*>(dst);
+        for (int i = threadIdx.x; i < nwords; i += kEncThreads) dst32[i] = src32[i];
+        for (int i = (nwords << 2) + threadIdx.x; i < nbytes; i += kEncThreads) dst[i] = stage[i];
+    } else {
+        for (int i = threadIdx.x; i < nbytes; i += kEncThreads) dst[i] = stage[i];
+    }
+}
+
+// Any GS (multiple of 16): two passes over the group (norm, then codes); the
+// second pass re-reads the group through the caches.
+template <int WDT>
+__global__ __launch_bounds__(kEncThreads) void encode_kernel_any(
+    const void* __restrict__ w, int64_t numel, int64_t ngroups, int64_t gs, float root,
+    uint8_t* __restrict__ packed, uint16_t* __restrict__ scales) {
+#pragma clang fp contract(off)
+    const int64_t g = (int64_t)blockIdx.x * kEncThreads + threadIdx.x;
+    if (g >= ngroups) return;
+    const int64_t base = g * gs;
+    float acc[8];
+    for (int t = 0; t < gs / 8; ++t) {
+        float x[8];
+        load8<WDT>(w, base + 8 * t, numel, false, x);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = (t == 0) ? x[j] * x[j] : __builtin_fmaf(x[j], x[j], acc[j]);
+    }
+    float sum = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) sum = sum + acc[j];
+    float s = __builtin_sqrtf(sum) / root;
+    s = s + 1e-8f;
+    uint8_t* dst = packed + base * 3 / 16;
+    for (int p = 0; p < gs / 16; ++p) {
+        float x[16];
+        load8<WDT>(w, base + 16 * p, numel, false, x);
+        load8<WDT>(w, base + 16 * p + 8, numel, false, x + 8);
+        uint32_t c0 = quantize8(x, s);
+        uint32_t c1 = quantize8(x + 8, s);
+        dst[3 * p + 0] = (uint8_t)(c0 & 0xFFu);
+        dst[3 * p + 1] = (uint8_t)(((c0 >> 8) & 0x0Fu) | ((c1 & 0x0Fu) << 4));
+        dst[3 * p + 2] = (uint8_t)((c1 >> 4) & 0xFFu);
+    }
+    scales[g] = (uint16_t)f32_to_f16_bits(s);
+}
+
+template <int WDT>
+static hipError_t launch_encode_t(const void* w, int64_t numel, int64_t gs, uint8_t* packed,
+                                  uint16_t* scales, hipStream_t stream) {
+    const int64_t padded = numel + (gs - numel % gs) % gs;
+    const int64_t ngroups = padded / gs;
+    const float root = (float)__builtin_sqrt((double)gs);
+    const int64_t blocks = (ngroups + kEncThreads - 1) / kEncThreads;
+    const bool vec_ok = (((uintptr_t)w) & 15u) == 0;
+    if (gs == 16)
+        hipLaunchKernelGGL((encode_kernel<WDT, 16>), dim3((unsigned)blocks), dim3(kEncThreads), 0,
+                           stream, w, numel, ngroups, root, vec_ok, packed, scales);
+    else if (gs == 32)
+        hipLaunchKernelGGL((encode_kernel<WDT, 32>), dim3((unsigned)blocks), dim3(kEncThreads), 0,
+                           stream, w, numel, ngroups, root, vec_ok, packed, scales);
+    else if (gs == 64)
+        hipLaunchKernelGGL((encode_kernel<WDT, 64>), dim3((unsigned)blocks), dim3(kEncThreads), 0,
+                           stream, w, numel, ngroups, root, vec_ok, packed, scales);
+    else
+        hipLaunchKernelGGL((encode_kernel_any<WDT>), dim3((unsigned)blocks), dim3(kEncThreads), 0,
+                           stream, w, numel, ngroups, gs, root, packed, scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_encode(const void* w, int wdt, int64_t numel, int64_t gs, uint8_t* packed,
+                         uint16_t* scales, hipStream_t stream) {
+    switch (wdt) {
+        case kF32: return launch_encode_t<kF32>(w, numel, gs, packed, scales, stream);
+        case kF16: return launch_encode_t<kF16>(w, numel, gs, packed, scales, stream);
+        default: return launch_encode_t<kBF16>(w, numel, gs, packed, scales, stream);
+    }
+}
+
+// ---------------------------------------------------------------- decoder
+
+constexpr int kDecThreads = 256;
+
+template <int ODT>
+__global__ __launch_bounds__(kDecThreads) void decode_kernel(
+    const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales, int64_t numel,
+    int64_t gs, bool vec_ok, void* __restrict__ out) {
+    const int64_t p = (int64_t)blockIdx.x * kDecThreads + threadIdx.x;  // code pair
+    const int64_t e0 = p * 16;
+    if (e0 >= numel) return;
+    const uint32_t b0 = packed[3 * p], b1 = packed[3 * p + 1], b2 = packed[3 * p + 2];
+    uint32_t raw0 = 2u * (b0 | ((b1 & 0x0Fu) << 8));
+    uint32_t raw1 = 2u * ((b1 >> 4) | (b2 << 4));
+    const float s = scale_for<ODT>(scales[e0 / gs]);  // gs % 16 == 0: one group per pair
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[i] = (float)((int)(raw0 % 3u) - 1) * s;
+        v[8 + i] = (float)((int)(raw1 % 3u) - 1) * s;
+        raw0 /= 3u;
+        raw1 /= 3u;
+    }
+    if (vec_ok && e0 + 16 <= numel) {
+        if constexpr (ODT == kF32) {
+            float4* o = reinterpret_cast<float4*>((float*)out + e0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        } else {
+            uint32_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                uint32_t lo, hi;
+                if constexpr (ODT == kF16) { lo = f32_to_f16_bits(v[2 * i]); hi = f32_to_f16_bits(v[2 * i + 1]); }
+                else { lo = f32_to_bf16_bits(v[2 * i]); hi = f32_to_bf16_bits(v[2 * i + 1]); }
+                h[i] = lo | (hi << 16);
+            }
+            uint4* o = reinterpret_cast<uint4*>((uint16_t*)out + e0);
+            o[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (e0 + i < numel) store_from_f32<ODT>(out, e0 + i, v[i]);
+    }
+}
+
+hipError_t launch_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel, int64_t gs,
+                         int odt, void* out, hipStream_t stream) {
+    const int64_t pairs = (numel + 15) / 16;
+    const int64_t blocks = (pairs + kDecThreads - 1) / kDecThreads;
+    const bool vec_ok = (((uintptr_t)out) & 15u) == 0;
+    switch (odt) {
+        case kF32:
+            hipLaunchKernelGGL((decode_kernel<kF32>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, packed, scales, numel, gs, vec_ok, out);
+            break;
+        case kF16:
+            hipLaunchKernelGGL((decode_kernel<kF16>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, packed, scales, numel, gs, vec_ok, out);
+            break;
+        default:
+            hipLaunchKernelGGL((decode_kernel<kBF16>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, packed, scales, numel, gs, vec_ok, out);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace ojx

@@ -1,0 +1,75 @@
+// e8t_device.h -- device helpers shared by the ternary-E8 kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ojx {
+
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+    return __uint_as_float(b << 16);
+}
+
+// fp32 -> bf16 bits, round-nearest-even, NaN -> 0x7FC0 (torch's c10::BFloat16 rule).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// fp32 -> fp16 bits, round-nearest-even (v_cvt_f16_f32), subnormals kept.
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <int DT> struct Elem;
+template <> struct Elem<kF32> { using T = float; };
+template <> struct Elem<kF16> { using T = uint16_t; };
+template <> struct Elem<kBF16> { using T = uint16_t; };
+
+template <int DT> __device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
+    if constexpr (DT == kF32) return ((const float*)p)[i];
+    else if constexpr (DT == kF16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+    else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+template <int DT> __device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v) {
+    if constexpr (DT == kF32) ((float*)p)[i] = v;
+    else if constexpr (DT == kF16) ((uint16_t*)p)[i] = (uint16_t)f32_to_f16_bits(v);
+    else ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+// Scale value the reference multiplies decoded coordinates by for activations of
+// dtype DT (lattice.py:414-418: scales.to(dtype)): fp32 and fp16 keep the fp16
+// value exactly, bf16 rounds it to bf16.
+template <int DT> __device__ __forceinline__ float scale_for(uint32_t s16) {
+    float s = f16_bits_to_f32(s16);
+    if constexpr (DT == kBF16) s = bf16_bits_to_f32(f32_to_bf16_bits(s));
+    return s;
+}
+
+// ---------------------------------------------------------------- packed codes
+
+// 12-bit code t of the packed stream (lattice.py:397-405).
+__device__ __forceinline__ uint32_t load_code(const uint8_t* __restrict__ packed, int64_t t) {
+    const uint8_t* b = packed + 3 * (t >> 1);
+    if (t & 1) return ((uint32_t)b[1] >> 4) | ((uint32_t)b[2] << 4);
+    return (uint32_t)b[0] | (((uint32_t)b[1] & 0x0Fu) << 8);
+}
+
+// Coordinate i (0..7, in {-1,0,1}) of codeword `code`: base-3 digit i of raw = 2*code.
+__device__ __forceinline__ int code_coord(uint32_t code, int i) {
+    const uint32_t pow3[8] = {1, 3, 9, 27, 81, 243, 729, 2187};
+    return (int)(((2u * code) / pow3[i]) % 3u) - 1;
+}
+
+}  // namespace ojx

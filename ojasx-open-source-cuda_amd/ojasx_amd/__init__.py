@@ -1,0 +1,31 @@
+"""ojasx_amd -- MI355X-native ternary-E8 (1.5 bit/weight) quantized-weight path.
+
+Drop-in for the E8 names of ``ojasx3.lattice``: the packer, the fused linear and
+the layer keep the reference's signatures and buffer layout, and every array
+operation runs in hand-written HIP kernels for gfx950 (libojasx_e8t.so, C ABI in
+include/ojasx_e8t.h) registered as ``torch.ops.ojasx_e8t.*``.
+"""
+
+from . import ops
+from .lattice import (
+    E8LatticeLinear,
+    TernaryE8LatticePacker,
+    _FusedE8GEMMFunction,
+    _get_ternary_e8_luts,
+    fwht_block32,
+    pack_model_e8,
+)
+from .streaming import pack_weight_rowwise
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "ops",
+    "E8LatticeLinear",
+    "TernaryE8LatticePacker",
+    "_FusedE8GEMMFunction",
+    "_get_ternary_e8_luts",
+    "fwht_block32",
+    "pack_model_e8",
+    "pack_weight_rowwise",
+]

@@ -1,0 +1,277 @@
+"""Ternary-E8 (1.5 bit/weight) lattice quantization on MI355X.
+
+Mirrors the ternary part of ``ojasx3.lattice`` / ``ojasx2.math.lattice`` -- same
+names, arguments, buffers, coercions and errors -- with every array operation
+on the path running in the HIP kernels behind ``ojasx_amd.ops``:
+
+=================================  ==========================================
+this module                         reference (ojasx2/math/lattice.py)
+=================================  ==========================================
+``fwht_block32``                    :91-102
+``_get_ternary_e8_luts``            :292-332
+``TernaryE8LatticePacker.pack``     :338-384   -> ops.encode (one HIP kernel)
+``TernaryE8LatticePacker.unpack``   :386-419   -> ops.decode
+``_FusedE8GEMMFunction``            :548-717   -> ops.e8t_linear / _bwd_dx
+``E8LatticeLinear``                 :724-846
+``pack_model_e8``                   :901-945
+=================================  ==========================================
+
+Only bitrate 1.5 is implemented here; 2.0 and 1.0 raise ``NotImplementedError``.
+CPU tensors given to ``pack`` / ``unpack`` are processed on the current GPU and
+the result is returned on the CPU; the fused forward requires GPU tensors.
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+from typing import Dict, Optional, Tuple, Union
+
+import torch
+import torch.nn as nn
+
+from . import ops
+
+__all__ = [
+    "fwht_block32",
+    "TernaryE8LatticePacker",
+    "_FusedE8GEMMFunction",
+    "E8LatticeLinear",
+    "pack_model_e8",
+]
+
+_HADAMARD_NORM = 0.1767766952966369  # 1/sqrt(32), as a python float (lattice.py:101)
+
+
+def fwht_block32(x: torch.Tensor) -> torch.Tensor:
+    """Normalised 32-point Walsh-Hadamard transform along the last dim (lattice.py:91-102).
+
+    Radix-2 butterflies at distances 1, 2, 4, 8, 16 (sum to the lower index,
+    difference to the upper), then one multiply by 1/sqrt(32): the same sequence
+    of rounded operations as the reference, so packed codes of a Hadamard layer
+    match bit for bit.  Returns ``x`` unchanged if the last dim is not a
+    positive multiple of 32."""
+    shape = x.shape
+    if shape[-1] == 0 or shape[-1] % 32 != 0:
+        return x
+    h = x.reshape(-1, 32)
+    for dist in (1, 2, 4, 8, 16):
+        v = h.reshape(-1, 32 // (2 * dist), 2, dist)
+        a, b = v[:, :, 0, :], v[:, :, 1, :]
+        h = torch.stack([a + b, a - b], dim=2).reshape(-1, 32)
+    return (h * _HADAMARD_NORM).reshape(shape)
+
+
+_DEVICE_TERNARY_LUTS: Dict[Tuple[str, Optional[int]], Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
+
+
+def _get_ternary_e8_luts(device: Optional[torch.device] = None
+                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(rank_to_coords int8 [3281, 8], raw_to_rank int64 [6561], powers int64 [8]).
+
+    Same tables as lattice.py:292-332, built from the closed form raw = 2 * rank
+    (the enumeration keeps even digit sums, and 3^i is odd).  The HIP kernels do
+    not use them; they are provided for callers of the reference API."""
+    if device is None:
+        key = ("cpu", None)
+    else:
+        device = torch.device(device)
+        key = (device.type, device.index)
+    if key not in _DEVICE_TERNARY_LUTS:
+        raw = torch.arange(3281, dtype=torch.int64) * 2
+        digits = []
+        r = raw.clone()
+        for _ in range(8):
+            digits.append(r % 3 - 1)
+            r = r // 3
+        rank_to_coords = torch.stack(digits, dim=1).to(torch.int8)
+        raw_to_rank = torch.zeros(6561, dtype=torch.int64)
+        raw_to_rank[raw] = torch.arange(3281, dtype=torch.int64)
+        powers = torch.tensor([3 ** i for i in range(8)], dtype=torch.int64)
+        dev = torch.device(key[0], key[1]) if key[1] is not None else torch.device(key[0])
+        _DEVICE_TERNARY_LUTS[key] = (rank_to_coords.to(dev), raw_to_rank.to(dev), powers.to(dev))
+    return _DEVICE_TERNARY_LUTS[key]
+
+
+def _on_gpu(t: torch.Tensor) -> torch.Tensor:
+    if t.device.type == "cuda":
+        return t
+    if not torch.cuda.is_available():
+        raise RuntimeError("ojasx_amd needs a ROCm GPU; no device is available")
+    return t.to("cuda")
+
+
+class TernaryE8LatticePacker:
+    """Packs weight matrices into 1.50 bits/weight using D8 cap {-1, 0, +1}^8 (3,281 points)."""
+
+    @staticmethod
+    def pack(w: torch.Tensor, group_size: int = 32
+             ) -> Tuple[torch.Tensor, torch.Tensor, Tuple[int, int]]:
+        m, n = w.shape
+        if group_size <= 0 or group_size % 16 != 0:
+            group_size = 16  # silent coercion, lattice.py:346-347
+        packed, scales = ops.encode(_on_gpu(w), group_size)
+        if w.device.type != "cuda":
+            packed, scales = packed.to(w.device), scales.to(w.device)
+        return packed, scales, (m, n)
+
+    @staticmethod
+    def unpack(packed_codes: torch.Tensor, scales: torch.Tensor, shape: Tuple[int, int],
+               dtype: torch.dtype = torch.float32, use_workspace: bool = False) -> torch.Tensor:
+        # use_workspace selected a shared scratch buffer in the reference
+        # (lattice.py:62-84); here every call returns a fresh tensor.
+        del use_workspace
+        total = shape[0] * shape[1]
+        padded = (packed_codes.numel() // 3) * 16
+        group_size = padded // max(1, scales.numel())  # inferred as in lattice.py:407-409
+        out = ops.decode(_on_gpu(packed_codes), _on_gpu(scales), total, group_size, dtype)
+        if packed_codes.device.type != "cuda":
+            out = out.to(packed_codes.device)
+        return out.view(shape)
+
+
+def _require_ternary(bitrate: float) -> None:
+    if float(bitrate) != 1.5:
+        raise NotImplementedError(
+            f"ojasx_amd implements the ternary (bitrate 1.5) E8 path; bitrate {bitrate} "
+            "is not available")
+
+
+class _FusedE8GEMMFunction(torch.autograd.Function):
+    """Fused decode-in-register E8 linear (lattice.py:548-717), one HIP route.
+
+    Same ``apply`` arguments as the reference: (x, packed_weight, block_scales,
+    bias, out_features, in_features, group_size, bitrate, use_hadamard).  Saves
+    only the packed buffers for backward; returns grads for x and bias."""
+
+    MAX_EPHEMERAL_ELEMENTS: int = 67_108_864  # kept for API parity; no workspace is used
+
+    @staticmethod
+    def forward(ctx, x, packed_weight, block_scales, bias, out_features, in_features,
+                group_size, bitrate, use_hadamard=False):
+        _require_ternary(bitrate)
+        x_rot = fwht_block32(x) if (use_hadamard and in_features % 32 == 0) else x
+        ctx.save_for_backward(packed_weight, block_scales)
+        ctx.dims = (out_features, in_features, group_size)
+        ctx.x_shape = x_rot.shape
+        ctx.has_bias = bias is not None
+        ctx.use_hadamard = use_hadamard
+        return ops.e8t_linear(x_rot, packed_weight, block_scales, bias, out_features,
+                              in_features, group_size)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        packed_weight, block_scales = ctx.saved_tensors
+        out_features, in_features, group_size = ctx.dims
+        grad_x = ops.e8t_linear_bwd_dx(grad_y.contiguous(), packed_weight, block_scales,
+                                       out_features, in_features, group_size)
+        grad_x = grad_x.reshape(ctx.x_shape)
+        if ctx.use_hadamard and in_features % 32 == 0:
+            grad_x = fwht_block32(grad_x)
+        grad_bias = grad_y.reshape(-1, out_features).sum(dim=0) if ctx.has_bias else None
+        return grad_x, None, None, grad_bias, None, None, None, None, None
+
+
+class E8LatticeLinear(nn.Module):
+    """Linear layer with base weights packed into the 8D E8 lattice (lattice.py:724-846).
+
+    Buffers ``packed_weight`` (uint8 [padded*3/16]) and ``block_scales`` (fp16
+    [padded/group]) have the reference's names, shapes and layout, so its
+    state_dicts load unchanged.  LoRA adapters as in the reference."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, rank: int = 0,
+                 lora_alpha: float = 16.0, group_size: int = 8, bitrate: float = 2.0,
+                 use_hadamard: bool = False, device: Optional[torch.device] = None,
+                 dtype: Optional[torch.dtype] = None) -> None:
+        super().__init__()
+        _require_ternary(bitrate)
+        self.in_features = in_features
+        self.out_features = out_features
+        self.rank = rank
+        self.lora_alpha = lora_alpha
+        self.scaling = (lora_alpha / rank) if rank > 0 else 0.0
+        self.bitrate = float(bitrate)
+        self.use_hadamard = bool(use_hadamard and (in_features % 32 == 0))
+
+        total = out_features * in_features
+        eff_group = group_size if (group_size >= 16 and group_size % 16 == 0) else 16
+        padded = total + ((-total) % eff_group)
+        self.group_size = eff_group
+        self.register_buffer("packed_weight",
+                             torch.zeros((padded * 3) // 16, dtype=torch.uint8, device=device))
+        self.register_buffer("block_scales",
+                             torch.ones(padded // eff_group, dtype=torch.float16, device=device))
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype, device=device))
+        else:
+            self.register_parameter("bias", None)
+        if rank > 0:
+            self.lora_A = nn.Parameter(torch.zeros(in_features, rank, dtype=dtype, device=device))
+            self.lora_B = nn.Parameter(torch.zeros(rank, out_features, dtype=dtype, device=device))
+            nn.init.kaiming_uniform_(self.lora_A, a=math.sqrt(5))
+            nn.init.zeros_(self.lora_B)
+        else:
+            self.register_parameter("lora_A", None)
+            self.register_parameter("lora_B", None)
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, rank: int = 0, lora_alpha: float = 16.0,
+                    group_size: int = 8, bitrate: float = 2.0,
+                    use_hadamard: bool = False) -> "E8LatticeLinear":
+        _require_ternary(bitrate)
+        eff_gs = max(16, group_size)  # lattice.py:793
+        m = cls(linear.in_features, linear.out_features, bias=(linear.bias is not None),
+                rank=rank, lora_alpha=lora_alpha, group_size=eff_gs, bitrate=bitrate,
+                use_hadamard=use_hadamard, device=linear.weight.device,
+                dtype=linear.weight.dtype)
+        with torch.no_grad():
+            w = fwht_block32(linear.weight) if m.use_hadamard else linear.weight
+            packed, scales, _ = TernaryE8LatticePacker.pack(w, group_size=m.group_size)
+            m.packed_weight.copy_(packed)
+            m.block_scales.copy_(scales)
+            if linear.bias is not None:
+                m.bias.copy_(linear.bias)
+        return m
+
+    def unpack_weights(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        w = TernaryE8LatticePacker.unpack(self.packed_weight, self.block_scales,
+                                          (self.out_features, self.in_features), dtype=dtype)
+        return fwht_block32(w) if self.use_hadamard else w
+
+    def forward_fused(self, x: torch.Tensor) -> torch.Tensor:
+        out = _FusedE8GEMMFunction.apply(x, self.packed_weight, self.block_scales, self.bias,
+                                         self.out_features, self.in_features, self.group_size,
+                                         self.bitrate, self.use_hadamard)
+        if self.rank > 0 and self.lora_A is not None and self.lora_B is not None:
+            lora_a = self.lora_A.to(x.dtype) if self.lora_A.dtype != x.dtype else self.lora_A
+            lora_b = self.lora_B.to(x.dtype) if self.lora_B.dtype != x.dtype else self.lora_B
+            out = out + self.scaling * ((x @ lora_a) @ lora_b)
+        return out
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.forward_fused(x)
+
+
+def pack_model_e8(model: nn.Module, rank: int = 0, lora_alpha: float = 16.0,
+                  group_size: int = 32, bitrate: float = 2.0, use_hadamard: bool = False,
+                  target_modules: Optional[Union[list, tuple, str]] = None,
+                  exclude_modules: Optional[Union[list, tuple]] = None,
+                  inplace: bool = True) -> nn.Module:
+    """Recursively replaces nn.Linear modules by E8LatticeLinear (lattice.py:901-945)."""
+    target = model if inplace else copy.deepcopy(model)
+    if isinstance(target_modules, str):
+        target_modules = [target_modules]
+    for name, module in target.named_children():
+        if exclude_modules is not None and any(ex in name for ex in exclude_modules):
+            continue
+        targeted = True if target_modules is None else any(t in name for t in target_modules)
+        if isinstance(module, nn.Linear) and targeted:
+            setattr(target, name, E8LatticeLinear.from_linear(
+                module, rank=rank, lora_alpha=lora_alpha, group_size=group_size,
+                bitrate=bitrate, use_hadamard=use_hadamard))
+        else:
+            pack_model_e8(module, rank=rank, lora_alpha=lora_alpha, group_size=group_size,
+                          bitrate=bitrate, use_hadamard=use_hadamard,
+                          target_modules=target_modules, exclude_modules=exclude_modules,
+                          inplace=True)
+    return target

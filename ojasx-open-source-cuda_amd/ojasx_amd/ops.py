@@ -1,0 +1,263 @@
+"""``torch.library`` custom ops (namespace ``ojasx_e8t``) over the C ABI.
+
+Ops and the reference interfaces they replace:
+
+* ``encode(w, group_size) -> (packed, scales)``
+    TernaryE8LatticePacker.pack (ojasx2/math/lattice.py:338-384)
+* ``decode(packed, scales, numel, group_size, dtype) -> W``
+    TernaryE8LatticePacker.unpack (lattice.py:386-419)
+* ``e8t_linear(x, packed_weight, block_scales, bias, out_features, in_features,
+  group_size) -> y``  (autograd registered; saves only packed and scales, as
+  lattice.py:569 does)
+    the routing of _FusedE8GEMMFunction.forward/backward (lattice.py:552-717)
+    with the TileLang / native / portable backends replaced by one HIP path
+* ``fused_ternary_e8_gemm_fwd`` / ``fused_ternary_e8_gemm_bwd_dx``
+    the reference's native op schemas (ojasx_math_bindings.cpp:593-594) with the
+    binding's layout checks (:17-34, :414-433), for callers that bind the op by name.
+
+Every op runs on the current HIP stream of the input's device, allocates its
+outputs through torch's caching allocator and raises ``RuntimeError`` for
+unsupported layouts or non-ROCm tensors; nothing silently declines or falls back.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _native as N
+
+_NS = "ojasx_e8t"
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    try:
+        return N.DTYPE_CODE[dt]
+    except KeyError:
+        raise RuntimeError(f"ojasx_e8t supports float32, float16 and bfloat16 (got {dt})")
+
+
+def _padded(numel: int, gs: int) -> int:
+    return numel + ((-numel) % gs)
+
+
+def _check_gs(gs: int) -> None:
+    if gs <= 0 or gs % 16 != 0:
+        raise RuntimeError(f"group_size must be a positive multiple of 16 (got {gs})")
+
+
+# ----------------------------------------------------------------------------- encode
+
+@torch.library.custom_op(f"{_NS}::encode", mutates_args=())
+def encode(w: torch.Tensor, group_size: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    dev = N.require_device(w)
+    _check_gs(group_size)
+    if w.dtype not in N.DTYPE_CODE:
+        w = w.to(torch.float32)  # the reference widens to fp32 first (lattice.py:350)
+    w = w.contiguous()
+    numel = w.numel()
+    padded = _padded(numel, group_size)
+    packed = torch.empty(padded * 3 // 16, dtype=torch.uint8, device=dev)
+    scales = torch.empty(padded // group_size, dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8t_encode(N.ptr(w), _dtype_code(w.dtype), numel, group_size,
+                                       N.ptr(packed), N.ptr(scales), N.stream_handle(dev)),
+                "encode")
+    return packed, scales
+
+
+@encode.register_fake
+def _(w, group_size):
+    padded = _padded(w.numel(), group_size)
+    return (w.new_empty(padded * 3 // 16, dtype=torch.uint8),
+            w.new_empty(padded // group_size, dtype=torch.float16))
+
+
+# ----------------------------------------------------------------------------- decode
+
+@torch.library.custom_op(f"{_NS}::decode", mutates_args=())
+def decode(packed: torch.Tensor, scales: torch.Tensor, numel: int, group_size: int,
+           dtype: torch.dtype) -> torch.Tensor:
+    dev = N.require_device(packed, scales)
+    _check_gs(group_size)
+    if packed.dtype != torch.uint8 or scales.dtype != torch.float16:
+        raise RuntimeError("decode expects uint8 packed codes and float16 scales")
+    padded = _padded(numel, group_size)
+    if packed.numel() < padded * 3 // 16 or scales.numel() < padded // group_size:
+        raise RuntimeError(
+            f"packed/scales too small for {numel} weights at group_size {group_size}")
+    packed = packed.contiguous()
+    scales = scales.contiguous()
+    out = torch.empty(numel, dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8t_decode(N.ptr(packed), N.ptr(scales), numel, group_size,
+                                       _dtype_code(dtype), N.ptr(out), N.stream_handle(dev)),
+                "decode")
+    return out
+
+
+@decode.register_fake
+def _(packed, scales, numel, group_size, dtype):
+    return packed.new_empty(numel, dtype=dtype)
+
+
+# ----------------------------------------------------------------------------- linear
+
+def _check_layer_buffers(packed: torch.Tensor, scales: torch.Tensor, out_features: int,
+                         in_features: int, group_size: int) -> None:
+    if packed.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if scales.dtype != torch.float16:
+        raise RuntimeError("block_scales must be float16")
+    padded = _padded(out_features * in_features, group_size)
+    if packed.numel() < padded * 3 // 16:
+        raise RuntimeError(
+            f"packed_weight holds {packed.numel()} bytes; {out_features}x{in_features} at "
+            f"group_size {group_size} needs {padded * 3 // 16}")
+    if scales.numel() < padded // group_size:
+        raise RuntimeError(
+            f"block_scales holds {scales.numel()} values; needs {padded // group_size}")
+
+
+@torch.library.custom_op(f"{_NS}::e8t_linear", mutates_args=())
+def e8t_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+               bias: Optional[torch.Tensor], out_features: int, in_features: int,
+               group_size: int) -> torch.Tensor:
+    dev = N.require_device(x, packed_weight, block_scales, bias)
+    _check_gs(group_size)
+    if x.shape[-1] != in_features:
+        raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    _check_layer_buffers(packed_weight, block_scales, out_features, in_features, group_size)
+    dt = _dtype_code(x.dtype)
+    x2 = x.reshape(-1, in_features).contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, out_features), dtype=x.dtype, device=dev)
+    b = None
+    if bias is not None:
+        if bias.numel() != out_features:
+            raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
+        b = bias.to(x.dtype).contiguous()  # the reference casts bias to x's dtype
+    packed_weight = packed_weight.contiguous()
+    block_scales = block_scales.contiguous()
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8t_gemm_fwd(N.ptr(x2), N.ptr(packed_weight), N.ptr(block_scales),
+                                         N.ptr(b), N.ptr(y), M, out_features, in_features,
+                                         group_size, dt, N.stream_handle(dev)),
+                "gemm_fwd")
+    return y.reshape(*x.shape[:-1], out_features)
+
+
+@e8t_linear.register_fake
+def _(x, packed_weight, block_scales, bias, out_features, in_features, group_size):
+    return x.new_empty((*x.shape[:-1], out_features))
+
+
+@torch.library.custom_op(f"{_NS}::e8t_linear_bwd_dx", mutates_args=())
+def e8t_linear_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
+                      block_scales: torch.Tensor, out_features: int, in_features: int,
+                      group_size: int) -> torch.Tensor:
+    dev = N.require_device(grad_y, packed_weight, block_scales)
+    _check_gs(group_size)
+    if grad_y.shape[-1] != out_features:
+        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
+    _check_layer_buffers(packed_weight, block_scales, out_features, in_features, group_size)
+    dt = _dtype_code(grad_y.dtype)
+    gy = grad_y.reshape(-1, out_features).contiguous()
+    M = gy.shape[0]
+    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8t_gemm_bwd_dx(N.ptr(gy), N.ptr(packed_weight.contiguous()),
+                                            N.ptr(block_scales.contiguous()), N.ptr(gx), M,
+                                            out_features, in_features, group_size, dt,
+                                            N.stream_handle(dev)),
+                "gemm_bwd_dx")
+    return gx.reshape(*grad_y.shape[:-1], in_features)
+
+
+@e8t_linear_bwd_dx.register_fake
+def _(grad_y, packed_weight, block_scales, out_features, in_features, group_size):
+    return grad_y.new_empty((*grad_y.shape[:-1], in_features))
+
+
+def _linear_setup_context(ctx, inputs, output):
+    x, packed_weight, block_scales, bias, out_features, in_features, group_size = inputs
+    ctx.save_for_backward(packed_weight, block_scales)
+    ctx.dims = (out_features, in_features, group_size)
+    ctx.has_bias = bias is not None
+
+
+def _linear_backward(ctx, grad_y):
+    packed_weight, block_scales = ctx.saved_tensors
+    out_features, in_features, group_size = ctx.dims
+    grad_x = None
+    if ctx.needs_input_grad[0]:
+        grad_x = e8t_linear_bwd_dx(grad_y, packed_weight, block_scales, out_features,
+                                   in_features, group_size)
+    grad_bias = grad_y.reshape(-1, out_features).sum(dim=0) if ctx.has_bias else None
+    return grad_x, None, None, grad_bias, None, None, None
+
+
+e8t_linear.register_autograd(_linear_backward, setup_context=_linear_setup_context)
+
+
+# ------------------------------------------------------- reference native op schemas
+
+@torch.library.custom_op(f"{_NS}::fused_ternary_e8_gemm_fwd", mutates_args=())
+def fused_ternary_e8_gemm_fwd(x: torch.Tensor, packed_weight: torch.Tensor,
+                              block_scales: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                              group_size: int = 32) -> torch.Tensor:
+    """Same schema and checks as the reference's native op (ojasx_math_bindings.cpp:407-433)."""
+    if packed_weight.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if group_size <= 0 or group_size % 16 != 0:
+        raise RuntimeError("group_size must be a positive multiple of 16")
+    if x.dim() < 1:
+        raise RuntimeError("input must have a feature axis")
+    K = x.shape[-1]
+    if packed_weight.dim() != 2:
+        raise RuntimeError("packed_weight must be a 2D matrix")
+    if K <= 0 or K % 16 != 0 or K % group_size != 0:
+        raise RuntimeError("feature count must be divisible by the packing unit and group_size")
+    Nf = packed_weight.shape[0]
+    if block_scales.numel() != Nf * (K // group_size):
+        raise RuntimeError("block_scales must contain exactly N * (K / group_size) elements")
+    if packed_weight.shape[1] != (K * 3) // 16:
+        raise RuntimeError("packed_weight dim 1 must match (in_features * 3) / 16")
+    return e8t_linear(x, packed_weight.reshape(-1), block_scales.reshape(-1).to(torch.float16),
+                      bias, Nf, K, group_size)
+
+
+@fused_ternary_e8_gemm_fwd.register_fake
+def _(x, packed_weight, block_scales, bias=None, group_size=32):
+    return x.new_empty((*x.shape[:-1], packed_weight.shape[0]))
+
+
+@torch.library.custom_op(f"{_NS}::fused_ternary_e8_gemm_bwd_dx", mutates_args=())
+def fused_ternary_e8_gemm_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
+                                 block_scales: torch.Tensor, in_features: int,
+                                 group_size: int = 32) -> torch.Tensor:
+    """Same schema and checks as the reference's native op (ojasx_math_bindings.cpp:479-500)."""
+    if packed_weight.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if packed_weight.dim() != 2:
+        raise RuntimeError("packed_weight must be 2D [N, (K * 3) / 16]")
+    if packed_weight.shape[1] != (in_features * 3) // 16:
+        raise RuntimeError("packed_weight dim 1 must match (in_features * 3) / 16")
+    if group_size <= 0 or group_size % 16 != 0:
+        raise RuntimeError("group_size must be a positive multiple of 16")
+    K = in_features
+    if K <= 0 or K % 16 != 0 or K % group_size != 0:
+        raise RuntimeError("feature count must be divisible by the packing unit and group_size")
+    Nf = packed_weight.shape[0]
+    if block_scales.numel() != Nf * (K // group_size):
+        raise RuntimeError("block_scales must contain exactly N * (K / group_size) elements")
+    if grad_y.shape[-1] != Nf:
+        raise RuntimeError("Last dimension of grad_y must match N")
+    return e8t_linear_bwd_dx(grad_y, packed_weight.reshape(-1),
+                             block_scales.reshape(-1).to(torch.float16), Nf, K, group_size)
+
+
+@fused_ternary_e8_gemm_bwd_dx.register_fake
+def _(grad_y, packed_weight, block_scales, in_features, group_size=32):
+    return grad_y.new_empty((*grad_y.shape[:-1], in_features))

@@ -1,0 +1,150 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+declared symbol, argument validation rejects bad calls before any launch, and
+the Python layer keeps the reference's shapes, coercions and errors."""
+
+import ctypes
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import ojasx_amd
+from ojasx_amd import _native as N
+from ojasx_amd import lattice as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ojasx_e8t.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(ojx_e8t_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_exports():
+    assert _declared_symbols() == sorted(N.EXPORTS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = N.lib()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.ojx_e8t_version() >= 100
+
+
+def test_library_has_gfx950_code_object():
+    # the HIP fat binary embeds the target id; the library must carry gfx950 code
+    with open(N.LIB_PATH, "rb") as f:
+        blob = f.read()
+    assert b"gfx950" in blob
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    lib = N.lib()
+    # negative sizes, unknown dtype and bad group size fail without touching a GPU
+    assert lib.ojx_e8t_encode(None, 0, -1, 32, None, None, None) == -1
+    assert lib.ojx_e8t_encode(None, 7, 16, 32, None, None, None) == -3
+    assert lib.ojx_e8t_encode(None, 0, 16, 24, None, None, None) == -2
+    assert b"multiple of 16" in lib.ojx_e8t_last_error()
+    assert lib.ojx_e8t_decode(None, None, 16, 0, 0, None, None) == -2
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, -1, 4, 4, 32, 0, None) == -1
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 1, 4, 4, 32, 9, None) == -3
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 1, 4, 32, 32, 0, None) == -1
+    assert lib.ojx_e8t_gemm_bwd_dx(None, None, None, None, 1, 4, 32, 20, 2, None) == -2
+    # empty work is a no-op success
+    assert lib.ojx_e8t_encode(None, 0, 0, 32, None, None, None) == 0
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, None) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        ojasx_amd.ops.encode(torch.randn(4, 32), 32)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        ojasx_amd.ops.e8t_linear(torch.randn(2, 32), torch.zeros(6, dtype=torch.uint8),
+                                 torch.ones(2, dtype=torch.float16), None, 2, 32, 32)
+
+
+@pytest.mark.parametrize("gs,eff", [(8, 16), (24, 16), (16, 16), (32, 32), (64, 64)])
+def test_layer_buffer_shapes_and_group_coercion(gs, eff):
+    # lattice.py:748-767 (bitrate 1.5 branch)
+    layer = ojasx_amd.E8LatticeLinear(128, 96, rank=4, group_size=gs, bitrate=1.5)
+    assert layer.group_size == eff
+    total = 128 * 96
+    padded = total + ((-total) % eff)
+    assert layer.packed_weight.shape == (padded * 3 // 16,)
+    assert layer.packed_weight.dtype == torch.uint8
+    assert layer.block_scales.shape == (padded // eff,)
+    assert layer.block_scales.dtype == torch.float16
+    assert layer.lora_A.shape == (128, 4) and layer.lora_B.shape == (4, 96)
+    assert layer.scaling == 16.0 / 4
+
+
+def test_layer_state_dict_keys_match_reference():
+    layer = ojasx_amd.E8LatticeLinear(64, 32, bias=True, rank=2, group_size=32, bitrate=1.5)
+    assert set(layer.state_dict()) == {"packed_weight", "block_scales", "bias", "lora_A", "lora_B"}
+
+
+def test_non_ternary_bitrates_raise():
+    with pytest.raises(NotImplementedError):
+        ojasx_amd.E8LatticeLinear(64, 32, bitrate=2.0)
+    with pytest.raises(NotImplementedError):
+        ojasx_amd.E8LatticeLinear.from_linear(nn.Linear(32, 32), bitrate=1.0)
+
+
+def test_rowwise_layout_validation_messages():
+    # streaming_e8.py:90-109 (reference tests/test_streaming_e8.py:42-47)
+    with pytest.raises(ValueError, match="not divisible"):
+        ojasx_amd.pack_weight_rowwise(torch.randn(2, 30), group_size=32)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ojasx_amd.pack_weight_rowwise(torch.randn(2, 48), group_size=24)
+    with pytest.raises(ValueError, match="rank-2"):
+        ojasx_amd.pack_weight_rowwise(torch.randn(2, 4, 32))
+
+
+def test_ternary_luts_closed_form():
+    r2c, raw2rank, powers = ojasx_amd._get_ternary_e8_luts()
+    assert r2c.shape == (3281, 8) and r2c.dtype == torch.int8
+    raw = ((r2c.long() + 1) * powers).sum(dim=1)
+    assert torch.equal(raw, 2 * torch.arange(3281))
+    assert torch.equal(raw2rank[raw], torch.arange(3281))
+
+
+def test_fwht_block32_is_normalised_hadamard_and_involution():
+    from scipy.linalg import hadamard
+
+    x = torch.randn(7, 96, dtype=torch.float64)
+    H = torch.from_numpy(hadamard(32).astype(np.float64)) / math.sqrt(32)
+    ref = (x.view(7, 3, 32) @ H.T).view(7, 96)
+    assert torch.allclose(L.fwht_block32(x), ref, atol=1e-12)
+    assert torch.allclose(L.fwht_block32(L.fwht_block32(x)), x, atol=1e-12)
+    y = torch.randn(3, 30)
+    assert L.fwht_block32(y) is y  # not a multiple of 32: unchanged
+
+
+def test_fwht_block32_matches_stagewise_butterflies_bitwise():
+    # lattice.py:95-101 combines pairs at distance 1, then 2, 4, 8, 16 with the sum
+    # in the lower slot; the same rounded ops in another order change low bits.
+    x = torch.randn(64, 32)
+    h = x.clone()
+    for d in (1, 2, 4, 8, 16):
+        out = h.clone()
+        for i in range(32):
+            if (i // d) % 2 == 0:
+                out[:, i] = h[:, i] + h[:, i + d]
+                out[:, i + d] = h[:, i] - h[:, i + d]
+        h = out
+    ref = h * 0.1767766952966369
+    assert torch.equal(L.fwht_block32(x), ref)
+
+
+def test_ctypes_signatures_match_header_arity():
+    text = open(HEADER).read()
+    lib = N.lib()
+    for name in N.EXPORTS:
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(getattr(lib, name).argtypes) == len(params), name
