@@ -1,0 +1,421 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X ternary-E8 hot path; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
+
+Workload (the metric's headline): decode GEMV
+y[M,N] = x[M,K] . Wq[N,K]^T on a stack of L (default 32) Llama-3-8B-shaped
+decoder layers, each with seven E8-packed linears q 4096x4096, k/v 1024x4096,
+o 4096x4096, gate/up 14336x4096, down 4096x14336 (ternary-E8 codes, group-32
+fp16 scales, 1,751,252,992 bytes at L=32), at batch M in {1, 4, 16} with bf16
+activations.  Weights are drawn N(0, 0.02) in fp32 on the GPU (seeded) and
+encoded by this library's encoder; activations are bf16 N(0, 1).
+
+One step = one GEMV over every linear of the stack at each M (3 x 7 x L
+launches, replayed from one hipGraph per M).  The stack is far larger than the
+GPU's last-level (MALL) cache, so every step streams the weights from HBM.
+
+value   = effective weight bandwidth: packed-code + scale bytes of the stack x 3
+          passes / measured step time (GB/s), as the metric defines it.
+roofline= HBM-bound: ALGORITHMIC bytes of every GEMV launch in the timed region
+          (codes + scales + x + y) / the region's duration (HIP events on the
+          replay stream), against 8 TB/s.
+
+Also reported (not the headline): prefill GEMM TFLOP/s on the four shapes at
+M in {512, 2048, 8192}, encoder throughput on one layer of fp16
+weights with 0.1% +-8 sigma outliers, and the CPU baseline: this
+repo's torch restatement of the reference's portable decode-then-matmul path
+(configs[0]) timed on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "ojasx-open-source-cuda_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+GS = 32
+
+# (name, N, K) per decoder layer, Llama-3-8B
+LAYER_SHAPES = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+                ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+PREFILL_SHAPES = [("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
+                  ("down", 4096, 14336)]
+DECODE_M = (1, 4, 16)
+PREFILL_M = (512, 2048, 8192)
+
+
+def weight_bytes(N: int, K: int) -> int:
+    return N * K * 3 // 16 + (N * K // GS) * 2
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--prefill-m", type=str, default=",".join(map(str, PREFILL_M)))
+    ap.add_argument("--prefill-time", type=float, default=0.15,
+                    help="target seconds of timed work per prefill case")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bounded CPU-baseline sample length")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-encode", action="store_true")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------------- setup
+
+def build_stack(torch, ops, layers: int, dev):
+    """Encode `layers` x 7 weight matrices on the GPU; returns list of dicts."""
+    stack = []
+    t0 = time.time()
+    for layer in range(layers):
+        for j, (name, N, K) in enumerate(LAYER_SHAPES):
+            g = torch.Generator(device=dev).manual_seed(8200 + 7 * layer + j)
+            w = torch.randn(N, K, generator=g, device=dev, dtype=torch.float32) * 0.02
+            packed, scales = ops.encode(w, GS)
+            del w
+            stack.append(dict(layer=layer, name=name, N=N, K=K, packed=packed, scales=scales))
+    torch.cuda.synchronize()
+    log(f"encoded {len(stack)} linears ({sum(weight_bytes(s['N'], s['K']) for s in stack) / 1e9:.3f}"
+        f" GB packed) in {time.time() - t0:.1f} s")
+    return stack
+
+
+def check_decode_outputs(torch, ops, stack, xs, ys, dev) -> float:
+    """Max relative error of sampled GEMV outputs against a torch fp32 matmul of
+    the decoded (bf16-rule) weights; a sanity check of what was timed."""
+    worst = 0.0
+    for M in DECODE_M:
+        for idx in (0, 4, 6):  # q, gate, down of layer 0
+            s = stack[idx]
+            w = ops.decode(s["packed"], s["scales"], s["N"] * s["K"], GS, torch.bfloat16)
+            ref = xs[(M, s["K"])].float() @ w.view(s["N"], s["K"]).float().t()
+            y = ys[(M, idx)].float()
+            err = (y - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+            worst = max(worst, err)
+    return worst
+
+
+# --------------------------------------------------------------------------- decode GEMV
+
+def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
+    lib = N_.lib()
+    xs, ys = {}, {}
+    for M in DECODE_M:
+        for K in (4096, 14336):
+            g = torch.Generator(device=dev).manual_seed(8300 + M + K)
+            xs[(M, K)] = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        for i, s in enumerate(stack):
+            ys[(M, i)] = torch.empty(M, s["N"], dtype=torch.bfloat16, device=dev)
+
+    def launch_all(M, stream_handle):
+        for i, s in enumerate(stack):
+            st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
+                                      s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
+                                      s["N"], s["K"], GS, N_.BF16, stream_handle)
+            N_.check(st, "gemm_fwd")
+
+    # eager warm-up (also caches the device check) before capture
+    for M in DECODE_M:
+        launch_all(M, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+
+    graphs = {}
+    cap_stream = torch.cuda.Stream()
+    for M in DECODE_M:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap_stream):
+            launch_all(M, torch.cuda.current_stream().cuda_stream)
+        graphs[M] = g
+    torch.cuda.synchronize()
+
+    for _ in range(warmup):
+        for M in DECODE_M:
+            graphs[M].replay()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    ev = {M: [] for M in DECODE_M}
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()  # barrier + sync (N=1: no other ranks)
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for _ in range(steps):
+        for M in DECODE_M:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            graphs[M].replay()
+            b.record(stream)
+            ev[M].append((a, b))
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_time(t_end)
+
+    wbytes = sum(weight_bytes(s["N"], s["K"]) for s in stack)
+    per_m = {}
+    alg_bytes_region = 0
+    kernel_ms_region = 0.0
+    for M in DECODE_M:
+        ms = sum(a.elapsed_time(b) for a, b in ev[M]) / steps
+        act = sum(M * s["K"] * 2 + M * s["N"] * 2 for s in stack)
+        per_m[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
+                             frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                             launches=len(stack))
+        alg_bytes_region += (wbytes + act) * steps
+        kernel_ms_region += ms * steps
+    err = check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys, dev)
+    return dict(total_ms=total_ms, wall_s=wall, wbytes=wbytes, per_m=per_m,
+                alg_bytes=alg_bytes_region, kernel_ms=kernel_ms_region,
+                launches=len(stack) * len(DECODE_M) * steps, max_rel_err=err)
+
+
+# --------------------------------------------------------------------------- prefill GEMM
+
+def bench_prefill(torch, N_, stack, Ms, target_s: float, dev):
+    lib = N_.lib()
+    by_name = {}
+    for s in stack[:7]:
+        by_name.setdefault((s["N"], s["K"]), s)
+    results = {}
+    tot_flop = 0.0
+    tot_ms = 0.0
+    stream = torch.cuda.current_stream()
+    for M in Ms:
+        for name, N, K in PREFILL_SHAPES:
+            s = by_name[(N, K)]
+            g = torch.Generator(device=dev).manual_seed(8400 + M)
+            x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+            y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+            def run():
+                N_.check(lib.ojx_e8t_gemm_fwd(x.data_ptr(), s["packed"].data_ptr(),
+                                              s["scales"].data_ptr(), None, y.data_ptr(), M, N,
+                                              K, GS, N_.BF16, stream.cuda_stream), "gemm_fwd")
+
+            run()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            run()
+            b.record(stream)
+            torch.cuda.synchronize()
+            one = max(a.elapsed_time(b), 1e-3)
+            iters = max(1, min(200, int(target_s * 1e3 / one)))
+            a.record(stream)
+            for _ in range(iters):
+                run()
+            b.record(stream)
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / iters
+            flop = 2.0 * M * N * K
+            tf = flop / ms / 1e9
+            results[f"{name}_M{M}"] = dict(ms=round(ms, 4), TFLOPs=round(tf, 1),
+                                           frac_mfma=round(tf / BF16_MFMA_PEAK_TFLOPS, 4))
+            tot_flop += flop
+            tot_ms += ms
+            del x, y
+    agg = tot_flop / tot_ms / 1e9 if tot_ms > 0 else 0.0
+    return dict(cases=results, TFLOPs=round(agg, 1),
+                frac_mfma=round(agg / BF16_MFMA_PEAK_TFLOPS, 4))
+
+
+# --------------------------------------------------------------------------- encoder
+
+def bench_encode(torch, ops, dev, target_s: float = 0.1):
+    """configs[3] per layer: fp16 N(0, 0.02) weights with 0.1% +-8 sigma outliers."""
+    out = {}
+    tot_w = 0
+    tot_ms = 0.0
+    stream = torch.cuda.current_stream()
+    for j, (name, N, K) in enumerate(LAYER_SHAPES):
+        g = torch.Generator(device=dev).manual_seed(9000 + j)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+        idx = torch.randperm(w.numel(), generator=g, device=dev)[: w.numel() // 1000]
+        sign = torch.where(torch.rand(idx.numel(), generator=g, device=dev) < 0.5, -1.0, 1.0)
+        w.view(-1)[idx] = (0.16 * sign).half()
+        ops.encode(w, GS)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        iters = 5
+        a.record(stream)
+        for _ in range(iters):
+            ops.encode(w, GS)
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / iters
+        numel = N * K
+        out[name] = dict(ms=round(ms, 4), Gweights_s=round(numel / ms / 1e6, 2),
+                         GBs=round(numel * 2.25 / ms / 1e6, 1))
+        tot_w += numel
+        tot_ms += ms
+    return dict(layers=out, Gweights_s=round(tot_w / tot_ms / 1e6, 2),
+                GBs=round(tot_w * 2.25 / tot_ms / 1e6, 1),
+                frac_hbm=round(tot_w * 2.25 / tot_ms / 1e6 / HBM_PEAK_GBS, 4))
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(seconds: float):
+    """the reference's Linux CPU path (unpack into the workspace, then
+    F.linear), restated in oracle/portable.py, on one 4096x4096 layer at M=1 fp32."""
+    import platform
+
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+    from oracle import portable
+
+    cores = len(os.sched_getaffinity(0))
+    cores = max(1, min(cores, 16))  # the GPU box's CPU share
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(8101)
+    w = torch.randn(4096, 4096, generator=g) * 0.02
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(8102))
+    packed, s16, _ = O.encode(w.numpy(), GS)
+    packed_t = torch.from_numpy(packed)
+    scales_t = torch.from_numpy(s16.view(np.float16).copy())
+    portable.linear(x, packed_t, scales_t, None, 4096, 4096)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        portable.linear(x, packed_t, scales_t, None, 4096, 4096)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / n
+    wb = weight_bytes(4096, 4096)
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(value=round(wb / per / 1e9, 3), unit="GB/s", cores=cores, kind="port",
+                sample=(f"configs[0]: 4096x4096 ternary-E8 layer (seed 8101), x[1,4096] fp32 "
+                        f"(seed 8102); unpack(use_workspace)+F.linear restated in "
+                        f"oracle/portable.py; {n} calls in {el:.1f} s = {per * 1e3:.2f} ms/call; "
+                        f"{cpu_model}"))
+
+
+# --------------------------------------------------------------------------- main
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the E8 path is benchmarked on a "
+              "single MI355X; multi-GPU sharding is a design note, not a measured path). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    import ojasx_amd
+    from ojasx_amd import _native as N_
+    from ojasx_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    stack = build_stack(torch, ops, args.layers, dev)
+    log("decode GEMV timing")
+    dec = bench_decode(torch, N_, stack, args.steps, args.warmup, dev)
+    ms_per_step = dec["total_ms"] / args.steps
+    value = dec["wbytes"] * len(DECODE_M) / ms_per_step / 1e6  # GB/s
+    achieved = dec["alg_bytes"] / dec["kernel_ms"] / 1e6
+    log(f"decode: {ms_per_step:.3f} ms/step, {value:.1f} GB/s weights, "
+        f"rel err {dec['max_rel_err']:.2e}")
+
+    result = {
+        "metric": "E8 GEMV effective GB/s (% HBM peak) + prefill TFLOP/s (% MFMA), 8B shapes",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"decode GEMV over a {args.layers}-layer Llama-3-8B-shaped ternary-E8 "
+                         "stack (q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down "
+                         "4096x14336; group-32 fp16 scales), batch M in {1,4,16}, bf16 "
+                         "activations, fp32 accumulation; one hipGraph of per-linear launches "
+                         "per M"),
+            "layers": args.layers,
+            "decode_M": list(DECODE_M),
+            "group_size": GS,
+            "stack_weight_bytes": dec["wbytes"],
+            "parallelism": "single GPU",
+        },
+        "decode": dict(per_M=dec["per_m"], max_rel_err=dec["max_rel_err"],
+                       launches_per_step=len(stack) * len(DECODE_M)),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "ojx e8t decode GEMV",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+
+    if not args.no_prefill:
+        Ms = [int(m) for m in args.prefill_m.split(",") if m]
+        log(f"prefill timing M={Ms}")
+        result["prefill"] = bench_prefill(torch, N_, stack, Ms, args.prefill_time, dev)
+        log(f"prefill: {result['prefill']['TFLOPs']} TFLOP/s")
+    if not args.no_encode:
+        del stack
+        torch.cuda.empty_cache()
+        log("encode timing")
+        result["encode"] = bench_encode(torch, ops, dev)
+        log(f"encode: {result['encode']['Gweights_s']} Gweights/s")
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s sample)")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
