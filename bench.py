@@ -11,15 +11,17 @@ fp16 scales, 1,751,252,992 bytes at L=32), at batch M in {1, 4, 16} with bf16
 activations.  Weights are drawn N(0, 0.02) in fp32 on the GPU (seeded) and
 encoded by this library's encoder; activations are bf16 N(0, 1).
 
-One step = one GEMV over every linear of the stack at each M (3 x 7 x L
-launches, replayed from one hipGraph per M).  The stack is far larger than the
-GPU's last-level (MALL) cache, so every step streams the weights from HBM.
+One step = one GEMV over every linear of the stack at each M: one grouped launch
+per M (the job table covers all 7 x L linears).  The stack is far larger than the
+GPU's last-level (MALL) cache, so every step streams the weights from HBM.  The
+same GEMVs issued as one launch per linear (replayed from a hipGraph) are timed
+after the headline region and reported beside it.
 
 value   = effective weight bandwidth: packed-code + scale bytes of the stack x 3
           passes / measured step time (GB/s), as the metric defines it.
-roofline= HBM-bound: ALGORITHMIC bytes of every GEMV launch in the timed region
-          (codes + scales + x + y) / the region's duration (HIP events on the
-          replay stream), against 8 TB/s.
+roofline= HBM-bound: ALGORITHMIC bytes of the grouped GEMV launches in the timed
+          region (codes + scales + x + y) / their summed durations (HIP events
+          around each launch, on its stream), against 8 TB/s.
 
 Also reported (not the headline): prefill GEMM TFLOP/s on the four shapes at
 M in {512, 2048, 8192}, encoder throughput on one layer of fp16
@@ -117,6 +119,11 @@ def check_decode_outputs(torch, ops, stack, xs, ys, dev) -> float:
 # --------------------------------------------------------------------------- decode GEMV
 
 def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
+    """Headline: one grouped launch per M over every linear of the stack.  Also timed
+    (reported beside it): the same GEMVs as one launch per linear, replayed from a
+    hipGraph per M."""
+    from ojasx_amd.grouped import GroupedGemv, stack_jobs
+
     lib = N_.lib()
     xs, ys = {}, {}
     for M in DECODE_M:
@@ -126,33 +133,20 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
         for i, s in enumerate(stack):
             ys[(M, i)] = torch.empty(M, s["N"], dtype=torch.bfloat16, device=dev)
 
-    def launch_all(M, stream_handle):
-        for i, s in enumerate(stack):
-            st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
-                                      s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
-                                      s["N"], s["K"], GS, N_.BF16, stream_handle)
-            N_.check(st, "gemm_fwd")
-
-    # eager warm-up (also caches the device check) before capture
+    plans = {}
     for M in DECODE_M:
-        launch_all(M, torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
-
-    graphs = {}
-    cap_stream = torch.cuda.Stream()
-    for M in DECODE_M:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cap_stream):
-            launch_all(M, torch.cuda.current_stream().cuda_stream)
-        graphs[M] = g
-    torch.cuda.synchronize()
-
-    for _ in range(warmup):
-        for M in DECODE_M:
-            graphs[M].replay()
-    torch.cuda.synchronize()
+        xk = {K: xs[(M, K)] for K in (4096, 14336)}
+        yl = [ys[(M, i)] for i in range(len(stack))]
+        plans[M] = GroupedGemv(stack_jobs(stack, xk, yl), M, torch.bfloat16, dev,
+                               keep=list(xk.values()) + yl)
 
     stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        for M in DECODE_M:
+            plans[M]()
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly `steps` steps, synchronised on both sides
     ev = {M: [] for M in DECODE_M}
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
@@ -164,7 +158,7 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            graphs[M].replay()
+            plans[M]()
             b.record(stream)
             ev[M].append((a, b))
     t_end.record(stream)
@@ -181,13 +175,49 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
         act = sum(M * s["K"] * 2 + M * s["N"] * 2 for s in stack)
         per_m[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
                              frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-                             launches=len(stack))
+                             grid=plans[M].grid)
         alg_bytes_region += (wbytes + act) * steps
         kernel_ms_region += ms * steps
     err = check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys, dev)
+
+    # ---- beside it: one launch per linear, replayed from one hipGraph per M
+    def launch_all(M, stream_handle):
+        for i, s in enumerate(stack):
+            st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
+                                      s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
+                                      s["N"], s["K"], GS, N_.BF16, stream_handle)
+            N_.check(st, "gemm_fwd")
+
+    for M in DECODE_M:
+        launch_all(M, stream.cuda_stream)
+    torch.cuda.synchronize()
+    graphs = {}
+    cap_stream = torch.cuda.Stream()
+    for M in DECODE_M:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap_stream):
+            launch_all(M, torch.cuda.current_stream().cuda_stream)
+        graphs[M] = g
+    for M in DECODE_M:
+        graphs[M].replay()
+    torch.cuda.synchronize()
+    per_linear = {}
+    for M in DECODE_M:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            graphs[M].replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / steps
+        per_linear[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
+                                  frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                  launches=len(stack))
+    err = max(err, check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys, dev))
     return dict(total_ms=total_ms, wall_s=wall, wbytes=wbytes, per_m=per_m,
-                alg_bytes=alg_bytes_region, kernel_ms=kernel_ms_region,
-                launches=len(stack) * len(DECODE_M) * steps, max_rel_err=err)
+                per_linear=per_linear, alg_bytes=alg_bytes_region, kernel_ms=kernel_ms_region,
+                launches=len(DECODE_M) * steps, max_rel_err=err)
 
 
 # --------------------------------------------------------------------------- prefill GEMM
@@ -376,16 +406,17 @@ def main() -> int:
             "workload": (f"decode GEMV over a {args.layers}-layer Llama-3-8B-shaped ternary-E8 "
                          "stack (q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down "
                          "4096x14336; group-32 fp16 scales), batch M in {1,4,16}, bf16 "
-                         "activations, fp32 accumulation; one hipGraph of per-linear launches "
-                         "per M"),
+                         "activations, fp32 accumulation; one grouped GEMV launch per M "
+                         "covering every linear of the stack (per-linear launches from a "
+                         "hipGraph are reported under decode.per_linear)"),
             "layers": args.layers,
             "decode_M": list(DECODE_M),
             "group_size": GS,
             "stack_weight_bytes": dec["wbytes"],
             "parallelism": "single GPU",
         },
-        "decode": dict(per_M=dec["per_m"], max_rel_err=dec["max_rel_err"],
-                       launches_per_step=len(stack) * len(DECODE_M)),
+        "decode": dict(per_M=dec["per_m"], per_linear=dec["per_linear"],
+                       max_rel_err=dec["max_rel_err"], launches_per_step=len(DECODE_M)),
         "roofline": {
             "bound": "hbm",
             "kernel": "ojx e8t decode GEMV",

@@ -75,8 +75,8 @@ int ojx_e8t_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel,
  * schema at :594) and dispatch_tilelang_e8_gemm (ojasx2/tilelang_kernels.py:370-419);
  * called from _FusedE8GEMMFunction.forward (lattice.py:584-608).
  *   x, y, bias in `dtype`; bias may be NULL.  Wdeq follows the decoder's rule for `dtype`.
- *   Any K >= 1 (flat layout); the MFMA kernels run when K % 256 == 0 and gs == 32 for
- *   F16/BF16, other shapes and F32 use a general tiled kernel.  Never declines. */
+ *   Any K >= 1 (flat layout).  F16/BF16 with K % 256 == 0, gs == 32 and M <= 16 run the
+ *   MFMA decode GEMV; other shapes and F32 use a general tiled kernel.  Never declines. */
 int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                      int dtype, void* stream);
@@ -87,6 +87,41 @@ int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scale
 int ojx_e8t_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_t* scales,
                         void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
                         void* stream);
+
+/* ---------------------------------------------------------------- grouped decode GEMV
+ *
+ * One launch runs the decode GEMV (batch M <= 16) of several independent linears: a
+ * decoder layer's q/k/v (or gate/up) projections sharing one x and writing one
+ * concatenated output, or any table of linears (e.g. a whole layer stack).  This has no
+ * single counterpart in the reference, whose decode path runs one unpack + GEMM per
+ * linear (_FusedE8GEMMFunction.forward, lattice.py:610-624); the per-linear semantics of
+ * each job are exactly those of ojx_e8t_gemm_fwd.
+ *
+ * Requirements per job: K % 256 == 0, group size 32, dtype F16 or BF16, 1 <= M <= 16,
+ * x 16-byte aligned, packed and scales 4-byte aligned, y_ld >= y_col + N. */
+typedef struct ojx_e8t_gemv_job {
+    const void* x;          /* [M, K] activations; NULL = the launch's x          */
+    const uint8_t* packed;  /* [N*K*3/16] codes of W[N, K]                        */
+    const uint16_t* scales; /* [N*K/32] fp16 scale bits                           */
+    const void* bias;       /* [N] in dtype, or NULL                              */
+    void* y;                /* output base; NULL = the launch's y                  */
+    int64_t N, K;
+    int64_t y_col;          /* y[m, y_col + n] receives output n of row m          */
+    int64_t y_ld;           /* row stride of y in elements (0 means N)             */
+    int64_t wg_begin;       /* written by ojx_e8t_gemv_grouped_plan                */
+} ojx_e8t_gemv_job;
+
+/* Validates `jobs` (host array) for batch M and dtype, fills each wg_begin (and y_ld
+ * when 0) and returns the launch grid in *grid.  A planned array may be copied to
+ * device memory once and reused for every launch with the same M. */
+int ojx_e8t_gemv_grouped_plan(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype,
+                              int64_t* grid);
+
+/* Launches a planned group.  `jobs` is the planned host array; `jobs_dev` is NULL (then
+ * njobs <= 4 and the jobs travel in the kernel arguments) or a device copy of `jobs`.
+ * `x` and `y` are the defaults for jobs whose x / y are NULL. */
+int ojx_e8t_gemv_grouped(const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev,
+                         int njobs, const void* x, void* y, int64_t M, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@ LIB = os.path.join(HERE, "lib", "libojasx_e8t.so")
 SOURCES = [
     "e8t_codec.hip",
     "e8t_gemm_generic.hip",
+    "e8t_gemv.hip",
     "e8t_capi.cpp",
 ]
 

@@ -10,6 +10,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstddef>
 #include <cstring>
 
 #include "../../include/ojasx_e8t.h"
@@ -130,8 +131,104 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
     hipStream_t s = (hipStream_t)stream;
+    if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, K, gs, dtype)) {
+        ojx::GemvLaunch a{};
+        ojx::GemvJob& j = a.inl[0];
+        j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
+        j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
+        a.njobs = 1;
+        a.M = (int)M;
+        int R = 1, S = 1;
+        ojx::gemv_pick((N + 15) / 16, &R, &S);
+        return done(ojx::launch_gemv(a, R, S, ojx::gemv_wgs_for(N, R, S), dtype, s),
+                    "e8t gemv launch");
+    }
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                 "e8t gemm_fwd launch");
+}
+
+static_assert(sizeof(ojx_e8t_gemv_job) == sizeof(ojx::GemvJob), "job layout");
+static_assert(offsetof(ojx_e8t_gemv_job, wg_begin) == offsetof(ojx::GemvJob, wg_begin),
+              "job layout");
+
+static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, int64_t* grid,
+                     int* R, int* S, bool fill) {
+    if (njobs <= 0 || !jobs) return fail(OJX_EINVAL, "empty job list");
+    if (dtype != OJX_BF16 && dtype != OJX_F16)
+        return fail(OJX_EDTYPE, "grouped GEMV takes F16 or BF16 activations (got %d)", dtype);
+    if (M < 1 || M > 16) return fail(OJX_ELAYOUT, "grouped GEMV needs 1 <= M <= 16 (got %lld)",
+                                     (long long)M);
+    int64_t tiles = 0;
+    for (int i = 0; i < njobs; ++i) {
+        const ojx_e8t_gemv_job& j = jobs[i];
+        if (j.N < 1 || j.K < 256 || j.K % 256 != 0)
+            return fail(OJX_ELAYOUT, "job %d: needs N >= 1 and K %% 256 == 0 (N=%lld K=%lld)", i,
+                        (long long)j.N, (long long)j.K);
+        if (!j.packed || !j.scales) return fail(OJX_EINVAL, "job %d: null weight pointer", i);
+        if (((uintptr_t)j.packed & 3u) || ((uintptr_t)j.scales & 3u) || ((uintptr_t)j.x & 15u) ||
+            ((uintptr_t)j.y & 1u) || ((uintptr_t)j.bias & 1u))
+            return fail(OJX_ELAYOUT, "job %d: misaligned pointer", i);
+        const int64_t ld = j.y_ld ? j.y_ld : j.N;
+        if (j.y_col < 0 || ld < j.y_col + j.N)
+            return fail(OJX_ELAYOUT, "job %d: y_ld %lld < y_col %lld + N %lld", i, (long long)ld,
+                        (long long)j.y_col, (long long)j.N);
+        tiles += (j.N + 15) / 16;
+    }
+    ojx::gemv_pick(tiles, R, S);
+    int64_t wg = 0;
+    for (int i = 0; i < njobs; ++i) {
+        if (fill) {
+            jobs[i].wg_begin = wg;
+            if (jobs[i].y_ld == 0) jobs[i].y_ld = jobs[i].N;
+        } else if (jobs[i].wg_begin != wg || jobs[i].y_ld == 0) {
+            return fail(OJX_EINVAL, "job %d: the job array was not planned for this M", i);
+        }
+        wg += ojx::gemv_wgs_for(jobs[i].N, *R, *S);
+    }
+    if (wg > 0x7FFFFFFF) return fail(OJX_ELAYOUT, "grouped GEMV grid too large");
+    *grid = wg;
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8t_gemv_grouped_plan(ojx_e8t_gemv_job* jobs,
+                                                                     int njobs, int64_t M,
+                                                                     int dtype, int64_t* grid) {
+    int64_t g = 0;
+    int R = 1, S = 1;
+    if (int r = plan_jobs(jobs, njobs, M, dtype, &g, &R, &S, true)) return r;
+    if (grid) *grid = g;
+    g_last_error[0] = '\0';
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
+    const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev, int njobs, const void* x,
+    void* y, int64_t M, int dtype, void* stream) {
+    int64_t grid = 0;
+    int R = 1, S = 1;
+    if (int r = plan_jobs(const_cast<ojx_e8t_gemv_job*>(jobs), njobs, M, dtype, &grid, &R, &S,
+                          false))
+        return r;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 1u))
+        return fail(OJX_ELAYOUT, "misaligned default x / y");
+    for (int i = 0; i < njobs; ++i) {
+        if (!jobs[i].x && !x) return fail(OJX_EINVAL, "job %d has no activations", i);
+        if (!jobs[i].y && !y) return fail(OJX_EINVAL, "job %d has no output", i);
+    }
+    if (!jobs_dev && njobs > ojx::kGemvInlineJobs)
+        return fail(OJX_EINVAL, "more than %d jobs need a device job table",
+                    ojx::kGemvInlineJobs);
+    if (int r = check_device()) return r;
+    ojx::GemvLaunch a{};
+    if (!jobs_dev)
+        for (int i = 0; i < njobs; ++i) std::memcpy(&a.inl[i], &jobs[i], sizeof(ojx::GemvJob));
+    a.jobs = reinterpret_cast<const ojx::GemvJob*>(jobs_dev);
+    a.x = x;
+    a.y = y;
+    a.njobs = njobs;
+    a.M = (int)M;
+    return done(ojx::launch_gemv(a, R, S, grid, dtype, (hipStream_t)stream),
+                "e8t grouped gemv launch");
 }
 
 __attribute__((visibility("default"))) int ojx_e8t_gemm_bwd_dx(const void* grad_y,

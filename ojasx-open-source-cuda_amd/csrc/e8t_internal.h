@@ -21,3 +21,40 @@ hipError_t launch_gemm_generic_bwd(const void* gy, const uint8_t* packed, const 
                                    hipStream_t stream);
 
 }  // namespace ojx
+
+namespace ojx {
+
+// One linear of a (possibly grouped) decode-GEMV launch; same field order and types as
+// ojx_e8t_gemv_job in include/ojasx_e8t.h.  Device pointers; flat layout with
+// K % 256 == 0 and group size 32.
+struct GemvJob {
+    const void* x;            // [M, K] activations, or nullptr: the launch's x
+    const uint8_t* packed;    // [N * K * 3 / 16]
+    const uint16_t* scales;   // [N * K / 32] fp16 bits
+    const void* bias;         // [N] or nullptr
+    void* y;                  // output base, or nullptr: the launch's y
+    int64_t N;
+    int64_t K;
+    int64_t y_col;            // first output column of this job in y
+    int64_t y_ld;             // row stride of y in elements
+    int64_t wg_begin;         // first workgroup of this job in the launch grid
+};
+
+constexpr int kGemvInlineJobs = 4;
+
+struct GemvLaunch {
+    GemvJob inl[kGemvInlineJobs];  // used when jobs == nullptr
+    const GemvJob* jobs;           // device array of njobs jobs, sorted by wg_begin
+    const void* x;                 // default activations
+    void* y;                       // default output
+    int njobs;
+    int M;
+};
+
+bool gemv_supported(const void* x, const uint8_t* packed, const uint16_t* scales, const void* y,
+                    int64_t M, int64_t K, int64_t gs, int dt);
+void gemv_pick(int64_t total_tiles, int* R, int* S);
+int64_t gemv_wgs_for(int64_t N, int R, int S);
+hipError_t launch_gemv(const GemvLaunch& a, int R, int S, int64_t wgs, int dt, hipStream_t stream);
+
+}  // namespace ojx

@@ -6,7 +6,7 @@ operation runs in hand-written HIP kernels for gfx950 (libojasx_e8t.so, C ABI in
 include/ojasx_e8t.h) registered as ``torch.ops.ojasx_e8t.*``.
 """
 
-from . import ops
+from . import grouped, ops
 from .lattice import (
     E8LatticeLinear,
     TernaryE8LatticePacker,
@@ -20,6 +20,7 @@ from .streaming import pack_weight_rowwise
 __version__ = "0.1.0"
 
 __all__ = [
+    "grouped",
     "ops",
     "E8LatticeLinear",
     "TernaryE8LatticePacker",

@@ -26,7 +26,26 @@ EXPORTS = (
     "ojx_e8t_decode",
     "ojx_e8t_gemm_fwd",
     "ojx_e8t_gemm_bwd_dx",
+    "ojx_e8t_gemv_grouped_plan",
+    "ojx_e8t_gemv_grouped",
 )
+
+
+class GemvJob(ctypes.Structure):
+    """ojx_e8t_gemv_job of include/ojasx_e8t.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("packed", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("N", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("y_col", ctypes.c_int64),
+        ("y_ld", ctypes.c_int64),
+        ("wg_begin", ctypes.c_int64),
+    ]
 
 _lib = None
 _lock = threading.Lock()
@@ -60,6 +79,10 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8t_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
             L.ojx_e8t_gemm_bwd_dx.restype = _INT
             L.ojx_e8t_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8t_gemv_grouped_plan.restype = _INT
+            L.ojx_e8t_gemv_grouped_plan.argtypes = [_P, _INT, _I64, _INT, _P]
+            L.ojx_e8t_gemv_grouped.restype = _INT
+            L.ojx_e8t_gemv_grouped.argtypes = [_P, _P, _INT, _P, _P, _I64, _INT, _P]
             _lib = L
     return _lib
 

@@ -1,0 +1,106 @@
+"""Grouped decode GEMV: several E8-packed linears in one HIP launch.
+
+The decode path of a decoder layer runs q/k/v (and gate/up) on the same
+activations; the reference runs one unpack + dense GEMM per linear
+(``_FusedE8GEMMFunction.forward``, ``ojasx2/math/lattice.py:610-624``).
+``GroupedGemv`` plans a table of linears once (``ojx_e8t_gemv_grouped_plan``)
+and launches them together (``ojx_e8t_gemv_grouped``).  Each job computes
+exactly what ``ops.e8t_linear`` computes for it.
+
+Typical uses:
+
+* fused projections -- ``GroupedGemv.fused(layers, M, dtype)``: the outputs of
+  the layers are concatenated along the last dim of one ``[M, sum(N)]`` tensor
+  and every job reads the launch's ``x`` (at most 4 jobs travel in the kernel
+  arguments, no device table);
+* a fixed table -- explicit ``x`` / ``y`` per job, uploaded once to the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _native as N
+
+
+def _job(packed: torch.Tensor, scales: torch.Tensor, bias: Optional[torch.Tensor], n: int,
+         k: int, x: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
+         y_col: int = 0, y_ld: int = 0) -> N.GemvJob:
+    j = N.GemvJob()
+    j.x = N.ptr(x)
+    j.packed = packed.data_ptr()
+    j.scales = scales.data_ptr()
+    j.bias = N.ptr(bias)
+    j.y = N.ptr(y)
+    j.N, j.K, j.y_col, j.y_ld, j.wg_begin = n, k, y_col, y_ld, 0
+    return j
+
+
+class GroupedGemv:
+    """A planned group of decode-GEMV jobs for batch ``M`` and activation ``dtype``."""
+
+    def __init__(self, jobs: Sequence[N.GemvJob], M: int, dtype: torch.dtype,
+                 device: torch.device, keep: Sequence[torch.Tensor] = ()) -> None:
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise RuntimeError("grouped GEMV takes bfloat16 or float16 activations")
+        self.M = int(M)
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.n = len(jobs)
+        self._arr = (N.GemvJob * self.n)(*jobs)
+        grid = ctypes.c_int64(0)
+        N.check(N.lib().ojx_e8t_gemv_grouped_plan(ctypes.addressof(self._arr), self.n, self.M,
+                                                  N.DTYPE_CODE[dtype], ctypes.byref(grid)),
+                "gemv_grouped_plan")
+        self.grid = grid.value
+        self._keep = list(keep)  # tensors the job pointers refer to
+        self._dev = None
+        if self.n > 4:
+            raw = bytes(ctypes.string_at(ctypes.addressof(self._arr), ctypes.sizeof(self._arr)))
+            self._dev = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
+
+    @classmethod
+    def fused(cls, layers: Sequence[torch.nn.Module], M: int, dtype: torch.dtype
+              ) -> "GroupedGemv":
+        """Jobs for E8LatticeLinear-like layers (packed_weight, block_scales, bias,
+        out_features, in_features) whose outputs are concatenated along dim -1."""
+        n_total = sum(int(l.out_features) for l in layers)
+        jobs, col, keep = [], 0, []
+        for l in layers:
+            if int(l.group_size) != 32:
+                raise RuntimeError("grouped GEMV needs group_size 32")
+            bias = l.bias.detach().to(dtype).contiguous() if l.bias is not None else None
+            if bias is not None:
+                keep.append(bias)
+            jobs.append(_job(l.packed_weight, l.block_scales, bias, int(l.out_features),
+                             int(l.in_features), y_col=col, y_ld=n_total))
+            keep += [l.packed_weight, l.block_scales]
+            col += int(l.out_features)
+        g = cls(jobs, M, dtype, layers[0].packed_weight.device, keep)
+        g.n_total = n_total
+        return g
+
+    def __call__(self, x: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
+                 stream: Optional[torch.cuda.Stream] = None) -> Optional[torch.Tensor]:
+        if x is not None:
+            if x.dtype != self.dtype or not x.is_contiguous():
+                raise RuntimeError("x must be contiguous and of the planned dtype")
+            if x.numel() // x.shape[-1] != self.M:
+                raise RuntimeError(f"x has {x.numel() // x.shape[-1]} rows, planned for {self.M}")
+        if y is None and hasattr(self, "n_total") and x is not None:
+            y = torch.empty((*x.shape[:-1], self.n_total), dtype=self.dtype, device=self.device)
+        s = stream.cuda_stream if stream is not None else N.stream_handle(self.device)
+        N.check(N.lib().ojx_e8t_gemv_grouped(ctypes.addressof(self._arr),
+                                             N.ptr(self._dev), self.n, N.ptr(x), N.ptr(y),
+                                             self.M, N.DTYPE_CODE[self.dtype], s),
+                "gemv_grouped")
+        return y
+
+
+def stack_jobs(linears: Sequence[dict], xs: dict, ys: List[torch.Tensor]) -> List[N.GemvJob]:
+    """Jobs with explicit x and y for a table of {packed, scales, N, K} dicts."""
+    return [_job(l["packed"], l["scales"], None, l["N"], l["K"], x=xs[l["K"]], y=y)
+            for l, y in zip(linears, ys)]

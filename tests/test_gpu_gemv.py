@@ -1,0 +1,153 @@
+"""GPU parity of the MFMA decode GEMV (M <= 16) and of grouped launches.
+
+Bar (north star): max|y - y_ref| / max|y_ref| <= 1e-2 against the fp64
+dequantize-then-matmul oracle with the reference's bf16/fp16 weight rule
+(coord * scales.to(dtype), lattice.py:414-418).  Every kernel variant (tiles per
+wave R, in-workgroup K split S) is reached through the size of the launch."""
+
+import numpy as np
+import pytest
+import torch
+
+import ojasx_amd
+from ojasx_amd import _native as NAT
+from ojasx_amd import ops
+from ojasx_amd.grouped import GroupedGemv, _job
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+REL_TOL = 1e-2
+DT_CODE = {torch.float16: O.DT_F16, torch.bfloat16: O.DT_BF16}
+
+
+def _encoded(N, K, seed, scale=0.02):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * scale
+    packed, s16, _ = O.encode(w.numpy(), 32)
+    return (torch.from_numpy(packed).to(DEV), torch.from_numpy(s16.view(np.float16).copy()).to(DEV),
+            packed, s16)
+
+
+def _x(M, K, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).to(dtype)
+
+
+def _rel(y, ref):
+    y = y.detach().float().cpu().numpy()
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 13, 16])
+@pytest.mark.parametrize("N,K", [(256, 512), (100, 768), (16, 256), (1024, 4096)])
+def test_gemv_matches_oracle(dtype, M, N, K):
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=N * 7 + K)
+    x = _x(M, K, seed=M + K, dtype=dtype)
+    bias = _x(1, N, seed=N, dtype=dtype).reshape(N)
+    print(f"gemv M={M} N={N} K={K} {dtype}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, DT_CODE[dtype])
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("N", [16 * 512, 16 * 1024, 16 * 2048, 16 * 8192 + 48])
+def test_gemv_every_variant(N):
+    # tiles = N/16 selects (R, S): <512 -> (1,4), 512 -> (1,2), 1024 -> (1,1),
+    # 2048 -> (2,1), 8192+ -> (4,1); the last size also has a ragged final tile
+    K, M = 256, 16
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=N)
+    x = _x(M, K, seed=3, dtype=torch.bfloat16)
+    print(f"gemv variant N={N}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+
+
+def test_gemv_llama_down_shape_all_m():
+    N, K = 4096, 14336
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=8206)
+    for M in (1, 4, 16):
+        x = _x(M, K, seed=8300 + M, dtype=torch.bfloat16)
+        print(f"gemv down M={M}", flush=True)
+        y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+        torch.cuda.synchronize()
+        ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
+        assert _rel(y, ref) <= REL_TOL
+
+
+def test_gemv_misaligned_input_uses_general_kernel():
+    N, K, M = 64, 512, 3
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=5)
+    xb = _x(M * K + 1, 1, seed=6, dtype=torch.bfloat16).reshape(-1).to(DEV)
+    x = xb[1:].view(M, K)  # 2-byte offset: not 16-byte aligned
+    y = ops.e8t_linear(x, pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().cpu().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+
+
+class _L:  # minimal layer record for GroupedGemv.fused
+    def __init__(self, N, K, seed, bias=None):
+        self.packed_weight, self.block_scales, self.pk_np, self.sc_np = _encoded(N, K, seed)
+        self.out_features, self.in_features, self.group_size = N, K, 32
+        self.bias = bias
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_grouped_fused_qkv_matches_separate_linears(M):
+    K = 1024
+    b = _x(1, 128, seed=9, dtype=torch.bfloat16).reshape(128).to(DEV)
+    layers = [_L(512, K, 11), _L(128, K, 12, bias=b), _L(128, K, 13), _L(256, K, 14)]
+    x = _x(M, K, seed=M, dtype=torch.bfloat16).to(DEV)
+    g = GroupedGemv.fused(layers, M, torch.bfloat16)
+    print(f"grouped fused M={M} grid={g.grid}", flush=True)
+    y = g(x)
+    torch.cuda.synchronize()
+    assert y.shape == (M, 1024)
+    col = 0
+    for l in layers:
+        ref = O.gemm_f64(x.float().cpu().numpy(), l.pk_np, l.sc_np,
+                         None if l.bias is None else l.bias.float().cpu().numpy(),
+                         l.out_features, K, 32, O.DT_BF16)
+        assert _rel(y[:, col:col + l.out_features], ref) <= REL_TOL
+        sep = ops.e8t_linear(x, l.packed_weight, l.block_scales, l.bias, l.out_features, K, 32)
+        assert _rel(y[:, col:col + l.out_features], sep.float().cpu().numpy().astype(np.float64)) <= REL_TOL
+        col += l.out_features
+
+
+def test_grouped_device_table_with_explicit_x_and_y():
+    M = 4
+    shapes = [(256, 512), (64, 1024), (300, 512), (128, 256), (512, 512), (32, 2048)]
+    layers = [_L(n, k, 100 + i) for i, (n, k) in enumerate(shapes)]
+    xs = {k: _x(M, k, seed=k, dtype=torch.float16).to(DEV) for k in {k for _, k in shapes}}
+    ys = [torch.full((M, n), float("nan"), dtype=torch.float16, device=DEV) for n, _ in shapes]
+    jobs = [_job(l.packed_weight, l.block_scales, None, l.out_features, l.in_features,
+                 x=xs[l.in_features], y=y) for l, y in zip(layers, ys)]
+    g = GroupedGemv(jobs, M, torch.float16, DEV, keep=list(xs.values()) + ys)
+    print(f"grouped table jobs={g.n} grid={g.grid}", flush=True)
+    for _ in range(2):  # replaying a planned table is idempotent
+        g()
+        torch.cuda.synchronize()
+        for l, y in zip(layers, ys):
+            ref = O.gemm_f64(xs[l.in_features].float().cpu().numpy(), l.pk_np, l.sc_np, None,
+                             l.out_features, l.in_features, 32, O.DT_F16)
+            assert _rel(y, ref) <= REL_TOL
+
+
+def test_grouped_plan_rejects_bad_jobs():
+    l = _L(64, 512, 1)
+    bad_k = _job(l.packed_weight, l.block_scales, None, 64, 500)
+    with pytest.raises(RuntimeError, match="K % 256"):
+        GroupedGemv([bad_k], 4, torch.bfloat16, DEV)
+    ok = _job(l.packed_weight, l.block_scales, None, 64, 512)
+    with pytest.raises(RuntimeError, match="1 <= M <= 16"):
+        GroupedGemv([ok], 17, torch.bfloat16, DEV)
+    g = GroupedGemv([ok], 2, torch.bfloat16, DEV, keep=[l.packed_weight, l.block_scales])
+    with pytest.raises(RuntimeError, match="no activations"):
+        g()
