@@ -131,16 +131,15 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
     hipStream_t s = (hipStream_t)stream;
-    if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, K, gs, dtype)) {
+    if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, N, K, gs, dtype)) {
         ojx::GemvLaunch a{};
         ojx::GemvJob& j = a.inl[0];
         j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
         j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
         a.njobs = 1;
         a.M = (int)M;
-        int R = 1, S = 1;
-        ojx::gemv_pick((N + 15) / 16, &R, &S);
-        return done(ojx::launch_gemv(a, R, S, ojx::gemv_wgs_for(N, R, S), dtype, s),
+        const ojx::GemvPlan plan = ojx::gemv_pick((N + 15) / 16, M);
+        return done(ojx::launch_gemv(a, plan, ojx::gemv_wgs_for(N, plan), dtype, s),
                     "e8t gemv launch");
     }
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
@@ -152,7 +151,7 @@ static_assert(offsetof(ojx_e8t_gemv_job, wg_begin) == offsetof(ojx::GemvJob, wg_
               "job layout");
 
 static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, int64_t* grid,
-                     int* R, int* S, bool fill) {
+                     ojx::GemvPlan* plan, bool fill) {
     if (njobs <= 0 || !jobs) return fail(OJX_EINVAL, "empty job list");
     if (dtype != OJX_BF16 && dtype != OJX_F16)
         return fail(OJX_EDTYPE, "grouped GEMV takes F16 or BF16 activations (got %d)", dtype);
@@ -164,6 +163,8 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
         if (j.N < 1 || j.K < 256 || j.K % 256 != 0)
             return fail(OJX_ELAYOUT, "job %d: needs N >= 1 and K %% 256 == 0 (N=%lld K=%lld)", i,
                         (long long)j.N, (long long)j.K);
+        if (!ojx::gemv_shape_ok(j.N, j.K))
+            return fail(OJX_ELAYOUT, "job %d: layer too large for 32-bit offsets", i);
         if (!j.packed || !j.scales) return fail(OJX_EINVAL, "job %d: null weight pointer", i);
         if (((uintptr_t)j.packed & 3u) || ((uintptr_t)j.scales & 3u) || ((uintptr_t)j.x & 15u) ||
             ((uintptr_t)j.y & 1u) || ((uintptr_t)j.bias & 1u))
@@ -174,7 +175,7 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
                         (long long)j.y_col, (long long)j.N);
         tiles += (j.N + 15) / 16;
     }
-    ojx::gemv_pick(tiles, R, S);
+    *plan = ojx::gemv_pick(tiles, M);
     int64_t wg = 0;
     for (int i = 0; i < njobs; ++i) {
         if (fill) {
@@ -183,7 +184,7 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
         } else if (jobs[i].wg_begin != wg || jobs[i].y_ld == 0) {
             return fail(OJX_EINVAL, "job %d: the job array was not planned for this M", i);
         }
-        wg += ojx::gemv_wgs_for(jobs[i].N, *R, *S);
+        wg += ojx::gemv_wgs_for(jobs[i].N, *plan);
     }
     if (wg > 0x7FFFFFFF) return fail(OJX_ELAYOUT, "grouped GEMV grid too large");
     *grid = wg;
@@ -194,8 +195,8 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped_plan(ojx_e8t_gem
                                                                      int njobs, int64_t M,
                                                                      int dtype, int64_t* grid) {
     int64_t g = 0;
-    int R = 1, S = 1;
-    if (int r = plan_jobs(jobs, njobs, M, dtype, &g, &R, &S, true)) return r;
+    ojx::GemvPlan plan{};
+    if (int r = plan_jobs(jobs, njobs, M, dtype, &g, &plan, true)) return r;
     if (grid) *grid = g;
     g_last_error[0] = '\0';
     return OJX_OK;
@@ -205,8 +206,8 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
     const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev, int njobs, const void* x,
     void* y, int64_t M, int dtype, void* stream) {
     int64_t grid = 0;
-    int R = 1, S = 1;
-    if (int r = plan_jobs(const_cast<ojx_e8t_gemv_job*>(jobs), njobs, M, dtype, &grid, &R, &S,
+    ojx::GemvPlan plan{};
+    if (int r = plan_jobs(const_cast<ojx_e8t_gemv_job*>(jobs), njobs, M, dtype, &grid, &plan,
                           false))
         return r;
     if (((uintptr_t)x & 15u) || ((uintptr_t)y & 1u))
@@ -227,7 +228,7 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
     a.y = y;
     a.njobs = njobs;
     a.M = (int)M;
-    return done(ojx::launch_gemv(a, R, S, grid, dtype, (hipStream_t)stream),
+    return done(ojx::launch_gemv(a, plan, grid, dtype, (hipStream_t)stream),
                 "e8t grouped gemv launch");
 }
 

@@ -32,70 +32,85 @@
 #include "e8t_device.h"
 #include "e8t_internal.h"
 
+#include <cstdlib>
+#include <utility>
+
 namespace ojx {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(3))) uint32_t u32x3;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
 constexpr int kGemvThreads = 256;           // 4 waves
 constexpr int kLutEntries = 102;            // 81 valid + slack so that any 12-bit code stays in bounds
-constexpr int kLutSlots = 16;               // bank slices (one per lane of a ds_read_b64 phase)
-constexpr uint32_t kHiMagic = 414253u;      // floor((256c + b) * kHiMagic / 2^32) == floor(2c / 81)
+constexpr int kLutSlots = 32;               // bank slices: lane l reads slice l % 32
+constexpr uint32_t kLutStride = kLutSlots * 8;  // bytes per table entry (all slices)
+constexpr uint32_t kHiMagic = 207127u;      // floor((512c + b) * kHiMagic / 2^32) == floor(2c / 81), b < 256
 constexpr int kChunk = 256;                 // K per chunk: 32 codes per row = 48 bytes
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
 
 __device__ __forceinline__ uint32_t lut_mask_half(int digit) {
     return digit == 0 ? 0xFFFFu : (digit == 1 ? 0x0000u : 0x7FFFu);
 }
 
-// Fills the bank-sliced table: entry e, slot c at byte offset e*128 + c*8.
-__device__ __forceinline__ void fill_lut(uint2* lut) {
-    for (int i = threadIdx.x; i < kLutEntries * kLutSlots; i += blockDim.x) {
-        const int e = i / kLutSlots;
+// Fills the bank-sliced table: entry e, slice c at byte offset (e + 1) * kLutStride + c * 8
+// of the storage; entry -1 is a zero guard (with kHiMagic, the lo address of an invalid
+// code >= 3281 can reach 8 bytes below entry 0; valid codes never do).
+__device__ __forceinline__ void fill_lut(uint2* storage) {
+    for (int i = threadIdx.x; i < (kLutEntries + 1) * kLutSlots; i += blockDim.x) {
+        const int e = i / kLutSlots - 1;
+        if (e < 0) {
+            storage[i] = make_uint2(0u, 0u);
+            continue;
+        }
         const int d0 = e % 3, d1 = (e / 3) % 3, d2 = (e / 9) % 3, d3 = (e / 27) % 3;
-        lut[i] = make_uint2(lut_mask_half(d0) | (lut_mask_half(d1) << 16),
-                            lut_mask_half(d2) | (lut_mask_half(d3) << 16));
+        storage[i] = make_uint2(lut_mask_half(d0) | (lut_mask_half(d1) << 16),
+                                lut_mask_half(d2) | (lut_mask_half(d3) << 16));
     }
 }
 
-// Z = 256 * code_j + slot_byte for code j (0..7) of the 12-byte, 8-code group (d0,d1,d2):
+// Z = (code_j << 9) | slot for code j (0..7) of the 12-byte, 8-code group (d0, d1, d2):
 // code j occupies bits [12j, 12j+12) of the little-endian stream (lattice.py:375-383).
 template <int J>
-__device__ __forceinline__ uint32_t code_z(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t slot) {
+__device__ __forceinline__ uint32_t code_z(const uint32_t (&d)[3], uint32_t slot) {
     uint32_t t;
-    if constexpr (J == 0) t = d0 << 8;
-    else if constexpr (J == 1) t = d0 >> 4;
-    else if constexpr (J == 2) t = __builtin_amdgcn_alignbit(d1, d0, 16);
-    else if constexpr (J == 3) t = d1 << 4;
-    else if constexpr (J == 4) t = d1 >> 8;
-    else if constexpr (J == 5) t = __builtin_amdgcn_alignbit(d2, d1, 20);
-    else if constexpr (J == 6) t = d2;
-    else t = d2 >> 12;
-    return (t & 0xFFF00u) | slot;
+    if constexpr (J == 0) t = d[0] << 9;
+    else if constexpr (J == 1) t = d[0] >> 3;
+    else if constexpr (J == 2) t = __builtin_amdgcn_alignbit(d[1], d[0], 15);
+    else if constexpr (J == 3) t = d[1] << 5;
+    else if constexpr (J == 4) t = d[1] >> 7;
+    else if constexpr (J == 5) t = __builtin_amdgcn_alignbit(d[2], d[1], 19);
+    else if constexpr (J == 6) t = d[2] << 1;
+    else t = d[2] >> 11;
+    return (t & 0x1FFE00u) | slot;
 }
 
-// Packs the bf16 (DT=bf16) or fp16 bits of one group scale as s | s<<16 | 0x80008000.
-template <int DT>
-__device__ __forceinline__ uint32_t scale_word(uint32_t s16) {
-    uint32_t b;
-    if constexpr (DT == kBF16) b = f32_to_bf16_bits(f16_bits_to_f32(s16));
-    else b = s16;
-    return (b * 0x10001u) | 0x80008000u;
-}
-
-// z - 10368 * h as one full-rate 24-bit multiply-add (the compiler otherwise picks a
-// 64-bit v_mad_u64_u32 for this pattern).
-__device__ __forceinline__ uint32_t mad_i24(uint32_t h, uint32_t z) {
+// lo address = Z - 81 * kLutStride * hi = (2c - 81 hi) * kLutStride + slot, as one
+// full-rate 24-bit multiply-add (the compiler otherwise picks a 64-bit v_mad_u64_u32).
+__device__ __forceinline__ uint32_t lo_addr_of(uint32_t h, uint32_t z) {
     uint32_t r;
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(h), "s"(-10368), "v"(z));
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(h), "s"(-81 * (int)kLutStride), "v"(z));
     return r;
 }
 
-struct GemvLane {
-    uint32_t slot;   // byte offset of this lane's bank slice
-    int g;           // lane group (0..3)
-    int i16;         // lane % 16
-};
+// Two group scales (fp16 bits, packed) -> the AND words s | s<<16 | 0x80008000 in the
+// activation dtype (bf16: bf16_rne(float(s16)), lattice.py:414-418; fp16: exact).
+template <int DT>
+__device__ __forceinline__ void scale_words(uint32_t sc, uint32_t& w0, uint32_t& w1) {
+    uint32_t p;
+    if constexpr (DT == kBF16) {
+        const __bf16 b0 = (__bf16)f16_bits_to_f32(sc & 0xFFFFu);  // v_cvt_pk_bf16_f32 (RNE)
+        const __bf16 b1 = (__bf16)f16_bits_to_f32(sc >> 16);
+        p = (uint32_t)__builtin_bit_cast(uint16_t, b0) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, b1) << 16);
+    } else {
+        p = sc;
+    }
+    w0 = __builtin_amdgcn_perm(p, p, 0x01000100u) | 0x80008000u;
+    w1 = __builtin_amdgcn_perm(p, p, 0x03020302u) | 0x80008000u;
+}
 
 template <int DT>
 __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f32x4& c) {
@@ -107,67 +122,106 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f3
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-template <int DT, int R>
-struct Chunk {
-    uint32_t cd[R][3];   // 8 codes of each of the wave's R rows-for-this-lane
-    uint32_t sc[R];      // two fp16 scales
-    uint4 xa[8];         // A fragments for the 8 steps
+template <int R>
+struct Codes {
+    uint32_t cd[R][3];   // 8 codes (12 bytes) of each of this lane's R rows
+    uint32_t sc[R];      // the two fp16 scales covering them
 };
 
-// Loads are unconditional: rows past N and activation rows past M read a clamped, valid
-// row; the MFMA outputs they produce are never stored.
-template <int DT, int R>
-__device__ __forceinline__ void load_chunk(Chunk<DT, R>& ch, int64_t c, const GemvLane& L,
-                                           const uint8_t* const (&prow)[R],
-                                           const uint16_t* const (&srow)[R],
-                                           const uint16_t* xrow) {
+// Per-wave streaming state: buffer resources and lane offsets, fixed for the wave.
+template <int R>
+struct Stream {
+    __amdgpu_buffer_rsrc_t packed, scales, x;
+    uint32_t vo_code[R], vo_scale[R];
+    uint32_t vo_x;
+    bool x_live;         // this lane's activation row is < M
+    uint32_t slot;       // byte offset of this lane's table slice
+};
+
+// Loads beyond the end of a weight buffer (rows >= N) return 0 (raw buffer bounds
+// check); the outputs they feed are never stored.
+template <int R>
+__device__ __forceinline__ void load_codes(Codes<R>& ch, int64_t c, const Stream<R>& st) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(prow[r] + c * 48 + 12 * L.g);
-        ch.cd[r][0] = p[0];
-        ch.cd[r][1] = p[1];
-        ch.cd[r][2] = p[2];
-        ch.sc[r] = *reinterpret_cast<const uint32_t*>(srow[r] + c * 8 + 2 * L.g);
+        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(st.packed, st.vo_code[r],
+                                                             (int)(c * 48), 0);
+        ch.cd[r][0] = v.x;
+        ch.cd[r][1] = v.y;
+        ch.cd[r][2] = v.z;
+        ch.sc[r] = __builtin_amdgcn_raw_buffer_load_b32(st.scales, st.vo_scale[r],
+                                                        (int)(c * 16), 0);
     }
-    const uint4* xp = reinterpret_cast<const uint4*>(xrow + c * kChunk + 64 * L.g);
+}
+
+template <int R>
+__device__ __forceinline__ void load_x(uint4& xa, int64_t c, int j, const Stream<R>& st) {
+    if (st.x_live) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(st.x, st.vo_x + 16u * j,
+                                                              (int)(c * (kChunk * 2)), 0);
+        xa = make_uint4(v.x, v.y, v.z, v.w);
+    }
+}
+
+template <int R, int J>
+__device__ __forceinline__ void lut_reads(const Codes<R>& ch, const char* lut, uint32_t slot,
+                                          uint2 (&ml)[R], uint2 (&mh)[R]) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ch.xa[j] = xp[j];
+    for (int r = 0; r < R; ++r) {
+        const uint32_t z = code_z<J>(ch.cd[r], slot);
+        const uint32_t h = __umulhi(z, kHiMagic);
+        ml[r] = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+        mh[r] = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+    }
 }
 
 template <int DT, int R, int J>
-__device__ __forceinline__ void step(const Chunk<DT, R>& ch, const uint32_t (&sw)[R][2],
-                                     const char* lut, const GemvLane& L, f32x4 (&acc)[R]) {
+__device__ __forceinline__ void mfma_step(const uint2 (&ml)[R], const uint2 (&mh)[R],
+                                          const uint32_t (&sw)[R][2], const uint4& xa,
+                                          f32x4 (&acc)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t z = code_z<J>(ch.cd[r][0], ch.cd[r][1], ch.cd[r][2], L.slot);
-        const uint32_t h = __umulhi(z, kHiMagic);
-        const uint32_t lo_addr = mad_i24(h, z);
-        const uint32_t hi_addr = h * 128u + L.slot;
-        const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr);
-        const uint2 mh = *reinterpret_cast<const uint2*>(lut + hi_addr);
         const uint32_t s = sw[r][J >> 2];
-        const uint4 b = make_uint4(ml.x & s, ml.y & s, mh.x & s, mh.y & s);
-        acc[r] = mfma16<DT>(ch.xa[J], b, acc[r]);
+        const uint4 b = make_uint4(ml[r].x & s, ml[r].y & s, mh[r].x & s, mh[r].y & s);
+        acc[r] = mfma16<DT>(xa, b, acc[r]);
     }
 }
 
+// One 256-wide K chunk: 8 MFMA steps per row tile.  The table reads of step j+1 are
+// issued before the MFMAs of step j; x fragment j is refilled with chunk `cn`'s
+// fragment j as soon as step j has consumed it (cn < 0: no next chunk).
 template <int DT, int R>
-__device__ __forceinline__ void compute_chunk(const Chunk<DT, R>& ch, const char* lut,
-                                              const GemvLane& L, f32x4 (&acc)[R]) {
+__device__ __forceinline__ void compute_chunk(const Codes<R>& ch, uint4 (&xa)[8], int64_t cn,
+                                              const char* lut, const Stream<R>& st,
+                                              f32x4 (&acc)[R]) {
     uint32_t sw[R][2];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        sw[r][0] = scale_word<DT>(ch.sc[r] & 0xFFFFu);
-        sw[r][1] = scale_word<DT>(ch.sc[r] >> 16);
-    }
-    step<DT, R, 0>(ch, sw, lut, L, acc);
-    step<DT, R, 1>(ch, sw, lut, L, acc);
-    step<DT, R, 2>(ch, sw, lut, L, acc);
-    step<DT, R, 3>(ch, sw, lut, L, acc);
-    step<DT, R, 4>(ch, sw, lut, L, acc);
-    step<DT, R, 5>(ch, sw, lut, L, acc);
-    step<DT, R, 6>(ch, sw, lut, L, acc);
-    step<DT, R, 7>(ch, sw, lut, L, acc);
+    for (int r = 0; r < R; ++r) scale_words<DT>(ch.sc[r], sw[r][0], sw[r][1]);
+    uint2 l0[R], h0[R], l1[R], h1[R];
+    lut_reads<R, 0>(ch, lut, st.slot, l0, h0);
+    lut_reads<R, 1>(ch, lut, st.slot, l1, h1);
+    mfma_step<DT, R, 0>(l0, h0, sw, xa[0], acc);
+    if (cn >= 0) load_x(xa[0], cn, 0, st);
+    lut_reads<R, 2>(ch, lut, st.slot, l0, h0);
+    mfma_step<DT, R, 1>(l1, h1, sw, xa[1], acc);
+    if (cn >= 0) load_x(xa[1], cn, 1, st);
+    lut_reads<R, 3>(ch, lut, st.slot, l1, h1);
+    mfma_step<DT, R, 2>(l0, h0, sw, xa[2], acc);
+    if (cn >= 0) load_x(xa[2], cn, 2, st);
+    lut_reads<R, 4>(ch, lut, st.slot, l0, h0);
+    mfma_step<DT, R, 3>(l1, h1, sw, xa[3], acc);
+    if (cn >= 0) load_x(xa[3], cn, 3, st);
+    lut_reads<R, 5>(ch, lut, st.slot, l1, h1);
+    mfma_step<DT, R, 4>(l0, h0, sw, xa[4], acc);
+    if (cn >= 0) load_x(xa[4], cn, 4, st);
+    lut_reads<R, 6>(ch, lut, st.slot, l0, h0);
+    mfma_step<DT, R, 5>(l1, h1, sw, xa[5], acc);
+    if (cn >= 0) load_x(xa[5], cn, 5, st);
+    lut_reads<R, 7>(ch, lut, st.slot, l1, h1);
+    mfma_step<DT, R, 6>(l0, h0, sw, xa[6], acc);
+    if (cn >= 0) load_x(xa[6], cn, 6, st);
+    mfma_step<DT, R, 7>(l1, h1, sw, xa[7], acc);
+    if (cn >= 0) load_x(xa[7], cn, 7, st);
 }
 
 __device__ __forceinline__ int find_job(const GemvJob* jobs, int njobs, int64_t wg) {
@@ -184,7 +238,7 @@ __device__ __forceinline__ int find_job(const GemvJob* jobs, int njobs, int64_t 
 // the workgroup's 4 waves are (4/S) tile sets x S K ranges, reduced through LDS.
 template <int DT, int R, int S>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
-    __shared__ uint2 lut_storage[kLutEntries * kLutSlots];
+    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
     __shared__ f32x4 red[(S > 1) ? (kGemvThreads / 64) * R * 64 : 1];
 
     fill_lut(lut_storage);
@@ -207,28 +261,31 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ks = wave % S;          // K range of this wave
     const int ts = wave / S;          // tile set of this wave
-    GemvLane L;
-    L.g = lane >> 4;
-    L.i16 = lane & 15;
-    L.slot = (uint32_t)L.i16 * 8u;
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
 
     const int64_t N = job.N, K = job.K;
     const int M = args.M;
-    const int64_t rowbytes = K * 3 / 16;
-    const int64_t srowlen = K / 32;
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
+    const uint32_t srowbytes = (uint32_t)(K / 16);
     const int64_t tile0 = (wg * (4 / S) + ts) * R;
 
-    const uint8_t* prow[R];
-    const uint16_t* srow[R];
+    Stream<R> st;
+    st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
+                                                  (int)(N * rowbytes), kRsrcWord3);
+    st.scales = __builtin_amdgcn_make_buffer_rsrc((void*)job.scales, (short)0,
+                                                  (int)(N * srowbytes), kRsrcWord3);
+    st.x = __builtin_amdgcn_make_buffer_rsrc((void*)xbase, (short)0, (int)(M * K * 2),
+                                             kRsrcWord3);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        int64_t row = (tile0 + r) * 16 + L.i16;
-        row = row < N ? row : N - 1;
-        prow[r] = job.packed + row * rowbytes;
-        srow[r] = job.scales + row * srowlen;
+        const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
+        st.vo_code[r] = row * rowbytes + 12u * g;
+        st.vo_scale[r] = row * srowbytes + 4u * g;
     }
-    const int xr = L.i16 < M ? L.i16 : M - 1;
-    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(xbase) + (int64_t)xr * K;
+    st.vo_x = (uint32_t)(i16 * K * 2 + 128 * g);
+    st.x_live = i16 < M;
+    st.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
 
     const int64_t nch = K / kChunk;
     const int64_t c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
@@ -236,21 +293,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
     f32x4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 xa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xa[j] = make_uint4(0u, 0u, 0u, 0u);
 
-    __syncthreads();  // LUT ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage);
-
-    Chunk<DT, R> A, B;
-    int64_t c = c0;
-    if (c < c1) load_chunk<DT, R>(A, c, L, prow, srow, xrow);
-    while (c + 1 < c1) {
-        load_chunk<DT, R>(B, c + 1, L, prow, srow, xrow);
-        compute_chunk<DT, R>(A, lut, L, acc);
-        if (c + 2 < c1) load_chunk<DT, R>(A, c + 2, L, prow, srow, xrow);
-        compute_chunk<DT, R>(B, lut, L, acc);
-        c += 2;
+    Codes<R> A, B;
+    if (c0 < c1) {
+        load_codes<R>(A, c0, st);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) load_x(xa[j], c0, j, st);
     }
-    if (c < c1) compute_chunk<DT, R>(A, lut, L, acc);
+    __syncthreads();  // LUT ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+
+    for (int64_t c = c0; c < c1; c += 2) {
+        const bool has1 = c + 1 < c1, has2 = c + 2 < c1;
+        if (has1) load_codes<R>(B, c + 1, st);
+        compute_chunk<DT, R>(A, xa, has1 ? c + 1 : -1, lut, st, acc);
+        if (!has1) break;
+        if (has2) load_codes<R>(A, c + 2, st);
+        compute_chunk<DT, R>(B, xa, has2 ? c + 2 : -1, lut, st, acc);
+    }
 
     if constexpr (S > 1) {
 #pragma unroll
@@ -270,12 +333,247 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
     // lane (g, n) holds rows m = 4g + q of column n (MFMA 16x16 output layout)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int64_t row = (tile0 + r) * 16 + L.i16;
+        const int64_t row = (tile0 + r) * 16 + i16;
         if (row >= N) continue;
         const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int m = 4 * L.g + q;
+            const int m = 4 * g + q;
+            if (m < M) store_from_f32<DT>(ybase, (int64_t)m * job.y_ld + job.y_col + row,
+                                          acc[r][q] + bv);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------- wide kernel
+//
+// Streaming-optimised variant for launches with many row tiles (grouped launches, large
+// N).  A "round" covers 1024 k: lane (g, n) loads 48 contiguous bytes of row n (the 32
+// codes of chunk g of the round, three 16-byte loads) plus their 8 scales, so each row
+// is read in 192-byte contiguous spans -- the access pattern the memory system streams
+// at near-peak rate.  Step j of the round contracts code j of every lane: lane group g
+// covers k = 1024u + 256g + 8j.  The activations of the round (M rows x 1024) are staged
+// in LDS by buffer->LDS loads issued one round ahead (padded rows: conflict-free reads),
+// and each MFMA step reads its A fragment with one ds_read_b128.  Codes are double
+// buffered in registers one round ahead; one workgroup barrier per round.
+
+constexpr int kRound = 1024;                      // K per round
+constexpr uint32_t kXRow = kRound * 2 + 16;       // bytes per padded activation row in LDS
+
+template <int R>
+struct WideCodes {
+    uint32_t cd[R][12];  // 48 bytes = 32 codes of one row
+    uint32_t sc[R][4];   // the 8 group scales covering them
+};
+
+template <int R>
+struct WideStream {
+    __amdgpu_buffer_rsrc_t packed, scales, x;
+    uint32_t vo_code[R], vo_scale[R];
+    uint32_t slot;
+    int64_t K;
+    int g;
+};
+
+template <int R>
+__device__ __forceinline__ void load_wide(WideCodes<R>& w, int64_t u, const WideStream<R>& st) {
+    // lane groups past K in a partial last round read the next row's bytes: zero their
+    // scales so those codes contribute exactly zero
+    const bool live = u * kRound + 256 * st.g < st.K;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                st.packed, st.vo_code[r] + 16u * t, (int)(u * 192), 0);
+            w.cd[r][4 * t + 0] = v.x;
+            w.cd[r][4 * t + 1] = v.y;
+            w.cd[r][4 * t + 2] = v.z;
+            w.cd[r][4 * t + 3] = v.w;
+        }
+        const u32x4 s = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r],
+                                                              (int)(u * 64), 0);
+        w.sc[r][0] = live ? s.x : 0u;
+        w.sc[r][1] = live ? s.y : 0u;
+        w.sc[r][2] = live ? s.z : 0u;
+        w.sc[r][3] = live ? s.w : 0u;
+    }
+}
+
+// Stages x[m][1024u .. 1024u + 1024) for m < M into LDS buffer `xs` (row stride kXRow):
+// 2M wave-level loads of 1 KB each, spread over the workgroup's 4 waves.
+__device__ __forceinline__ void stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int64_t u, int M,
+                                        int64_t K, int wave, int lane) {
+    for (int q = wave; q < 2 * M; q += 4) {
+        const int m = q >> 1, half = q & 1;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            x, (__attribute__((address_space(3))) void*)(xs + m * kXRow + half * 1024),
+            16, (uint32_t)(m * K * 2 + half * 1024 + lane * 16), (int)(u * kRound * 2), 0, 0);
+    }
+}
+
+template <int R, int J>
+__device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut, uint32_t slot,
+                                         uint2 (&ml)[R], uint2 (&mh)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t d[3] = {w.cd[r][3 * (J / 8)], w.cd[r][3 * (J / 8) + 1],
+                               w.cd[r][3 * (J / 8) + 2]};
+        const uint32_t z = code_z<J % 8>(d, slot);
+        const uint32_t h = __umulhi(z, kHiMagic);
+        ml[r] = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+        mh[r] = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+    }
+}
+
+template <int DT, int R, int J>
+__device__ __forceinline__ void wide_step(const WideCodes<R>& w, const char* lut,
+                                          const char* xa_base, uint32_t slot, uint4& xa_cur,
+                                          uint2 (&ml)[R], uint2 (&mh)[R], uint32_t (&sw)[R],
+                                          f32x4 (&acc)[R]) {
+    if constexpr (J % 4 == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t w0, w1;
+            scale_words<DT>(w.sc[r][J / 8], w0, w1);
+            sw[r] = (J % 8 == 0) ? w0 : w1;
+        }
+    }
+    uint4 xa_nxt;
+    uint2 ml_n[R], mh_n[R];
+    if constexpr (J + 1 < 32) {
+        xa_nxt = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + 1));
+        wide_lut<R, J + 1>(w, lut, slot, ml_n, mh_n);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t s = sw[r];
+        const uint4 b = make_uint4(ml[r].x & s, ml[r].y & s, mh[r].x & s, mh[r].y & s);
+        acc[r] = mfma16<DT>(xa_cur, b, acc[r]);
+    }
+    if constexpr (J + 1 < 32) {
+        xa_cur = xa_nxt;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ml[r] = ml_n[r];
+            mh[r] = mh_n[r];
+        }
+    }
+}
+
+template <int DT, int R, int... J>
+__device__ __forceinline__ void wide_steps(const WideCodes<R>& w, const char* lut,
+                                           const char* xa_base, uint32_t slot, uint4& xa,
+                                           uint2 (&ml)[R], uint2 (&mh)[R], uint32_t (&sw)[R],
+                                           f32x4 (&acc)[R],
+                                           std::integer_sequence<int, J...>) {
+    (wide_step<DT, R, J>(w, lut, xa_base, slot, xa, ml, mh, sw, acc), ...);
+}
+
+template <int DT, int R>
+__device__ __forceinline__ void wide_round(const WideCodes<R>& w, const char* lut,
+                                           const char* xa_base, uint32_t slot, f32x4 (&acc)[R]) {
+    uint4 xa = *reinterpret_cast<const uint4*>(xa_base);
+    uint2 ml[R], mh[R];
+    uint32_t sw[R];
+    wide_lut<R, 0>(w, lut, slot, ml, mh);
+    wide_steps<DT, R>(w, lut, xa_base, slot, xa, ml, mh, sw, acc,
+                      std::make_integer_sequence<int, 32>{});
+}
+
+__device__ __forceinline__ void vm_wait_all() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
+}
+
+// R: n-tiles (16 rows) per wave; MMAX: activation rows staged (4 or 16; M <= MMAX).
+template <int DT, int R, int MMAX>
+__global__ __launch_bounds__(kGemvThreads) void gemv_wide_kernel(GemvLaunch args) {
+    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ __attribute__((aligned(16))) char xs_storage[2][MMAX * kXRow];
+
+    fill_lut(lut_storage);
+
+    int64_t wg = blockIdx.x;
+    GemvJob job;
+    if (args.jobs != nullptr) {
+        job = args.jobs[find_job(args.jobs, args.njobs, wg)];
+    } else {
+        job = args.inl[0];
+#pragma unroll
+        for (int i = 1; i < kGemvInlineJobs; ++i)
+            if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
+    }
+    wg -= job.wg_begin;
+    const void* xbase = job.x ? job.x : args.x;
+    void* ybase = job.y ? job.y : args.y;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
+    const int64_t N = job.N, K = job.K;
+    const int M = args.M;
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
+    const uint32_t srowbytes = (uint32_t)(K / 16);
+    const int64_t tile0 = (wg * 4 + wave) * R;
+
+    WideStream<R> st;
+    st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
+                                                  (int)(N * rowbytes), kRsrcWord3);
+    st.scales = __builtin_amdgcn_make_buffer_rsrc((void*)job.scales, (short)0,
+                                                  (int)(N * srowbytes), kRsrcWord3);
+    st.x = __builtin_amdgcn_make_buffer_rsrc((void*)xbase, (short)0, (int)(M * K * 2),
+                                             kRsrcWord3);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
+        st.vo_code[r] = row * rowbytes + 48u * g;
+        st.vo_scale[r] = row * srowbytes + 16u * g;
+    }
+    st.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+    st.K = K;
+    st.g = g;
+    const int mrow = i16 < M ? i16 : M - 1;
+    const uint32_t xa_off = (uint32_t)(mrow * kXRow + 512 * g);
+
+    const int64_t T = (K + kRound - 1) / kRound;
+    f32x4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    WideCodes<R> CA, CB;
+    load_wide<R>(CA, 0, st);
+    stage_x(xs_storage[0], st.x, 0, M, K, wave, lane);
+    vm_wait_all();
+    __syncthreads();  // LUT and round-0 activations ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+
+    for (int64_t t = 0; t < T; t += 2) {
+        if (t + 1 < T) {
+            load_wide<R>(CB, t + 1, st);
+            stage_x(xs_storage[1], st.x, t + 1, M, K, wave, lane);
+        }
+        wide_round<DT, R>(CA, lut, xs_storage[0] + xa_off, st.slot, acc);
+        vm_wait_all();
+        __syncthreads();
+        if (t + 1 >= T) break;
+        if (t + 2 < T) {
+            load_wide<R>(CA, t + 2, st);
+            stage_x(xs_storage[0], st.x, t + 2, M, K, wave, lane);
+        }
+        wide_round<DT, R>(CB, lut, xs_storage[1] + xa_off, st.slot, acc);
+        vm_wait_all();
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = (tile0 + r) * 16 + i16;
+        if (row >= N) continue;
+        const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = 4 * g + q;
             if (m < M) store_from_f32<DT>(ybase, (int64_t)m * job.y_ld + job.y_col + row,
                                           acc[r][q] + bv);
         }
@@ -284,29 +582,49 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
 
 // ------------------------------------------------------------------------- host side
 
+bool gemv_shape_ok(int64_t N, int64_t K) {
+    // buffer offsets and record counts are 32-bit: every byte offset of the layer (plus
+    // the row padding of the last tile set) must stay below 2^31
+    return N >= 1 && K >= kChunk && K % kChunk == 0 && (N + 64) * (K * 3 / 16) < (1ll << 31) &&
+           16 * K * 2 < (1ll << 31);
+}
+
 bool gemv_supported(const void* x, const uint8_t* packed, const uint16_t* scales, const void* y,
-                    int64_t M, int64_t K, int64_t gs, int dt) {
+                    int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
     if (dt != kBF16 && dt != kF16) return false;
-    if (gs != 32 || M < 1 || M > 16 || K <= 0 || K % kChunk != 0) return false;
+    if (gs != 32 || M < 1 || M > 16 || !gemv_shape_ok(N, K)) return false;
     if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 3u) || ((uintptr_t)scales & 3u) ||
         ((uintptr_t)y & 1u))
         return false;
     return true;
 }
 
-void gemv_pick(int64_t total_tiles, int* R, int* S) {
-    // Enough waves to fill 256 CUs (>= 4 per CU) first, then reuse of the x fragments
-    // (R tiles per wave) -- larger R cuts the activation re-reads per weight byte.
-    if (total_tiles >= 8192) { *R = 4; *S = 1; }
-    else if (total_tiles >= 2048) { *R = 2; *S = 1; }
-    else if (total_tiles >= 1024) { *R = 1; *S = 1; }
-    else if (total_tiles >= 512) { *R = 1; *S = 2; }
-    else { *R = 1; *S = 4; }
+GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
+    GemvPlan p;
+    if (total_tiles >= 1024) {
+        // enough row tiles to fill the GPU with one tile set per wave: streaming kernel
+        p.wide = true;
+        p.R = 2;
+        p.S = 1;
+        p.mmax = M <= 4 ? 4 : 16;
+    } else {
+        // small layers: split K inside the workgroup to get enough waves
+        p.wide = false;
+        p.R = 1;
+        p.S = total_tiles >= 512 ? 2 : 4;
+        p.mmax = 16;
+    }
+    if (const char* e = getenv("OJX_TUNE_GEMV_RS")) {  // TEMPORARY tuning override
+        p.wide = e[2] == 'w';
+        p.R = e[0] - '0';
+        p.S = e[1] - '0';
+    }
+    return p;
 }
 
-int64_t gemv_wgs_for(int64_t N, int R, int S) {
+int64_t gemv_wgs_for(int64_t N, const GemvPlan& p) {
     const int64_t tiles = (N + 15) / 16;
-    const int64_t per_wg = (int64_t)(4 / S) * R;
+    const int64_t per_wg = p.wide ? 4 * p.R : (int64_t)(4 / p.S) * p.R;
     return (tiles + per_wg - 1) / per_wg;
 }
 
@@ -317,22 +635,37 @@ static hipError_t launch_rs(const GemvLaunch& a, int64_t wgs, hipStream_t stream
     return hipGetLastError();
 }
 
+template <int DT, int R, int MMAX>
+static hipError_t launch_wide(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
+    hipLaunchKernelGGL((gemv_wide_kernel<DT, R, MMAX>), dim3((unsigned)wgs), dim3(kGemvThreads),
+                       0, stream, a);
+    return hipGetLastError();
+}
+
 template <int DT>
-static hipError_t launch_dt(const GemvLaunch& a, int R, int S, int64_t wgs, hipStream_t stream) {
-    if (R == 4 && S == 1) return launch_rs<DT, 4, 1>(a, wgs, stream);
-    if (R == 2 && S == 1) return launch_rs<DT, 2, 1>(a, wgs, stream);
-    if (R == 1 && S == 1) return launch_rs<DT, 1, 1>(a, wgs, stream);
-    if (R == 1 && S == 2) return launch_rs<DT, 1, 2>(a, wgs, stream);
-    if (R == 1 && S == 4) return launch_rs<DT, 1, 4>(a, wgs, stream);
+static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
+                            hipStream_t stream) {
+    if (p.wide) {
+        if (p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4>(a, wgs, stream);
+        if (p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16>(a, wgs, stream);
+        if (p.R == 1 && p.mmax == 4) return launch_wide<DT, 1, 4>(a, wgs, stream);
+        if (p.R == 1 && p.mmax == 16) return launch_wide<DT, 1, 16>(a, wgs, stream);
+        return hipErrorInvalidValue;
+    }
+    if (p.R == 4 && p.S == 1) return launch_rs<DT, 4, 1>(a, wgs, stream);
+    if (p.R == 2 && p.S == 1) return launch_rs<DT, 2, 1>(a, wgs, stream);
+    if (p.R == 1 && p.S == 1) return launch_rs<DT, 1, 1>(a, wgs, stream);
+    if (p.R == 1 && p.S == 2) return launch_rs<DT, 1, 2>(a, wgs, stream);
+    if (p.R == 1 && p.S == 4) return launch_rs<DT, 1, 4>(a, wgs, stream);
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(const GemvLaunch& a, int R, int S, int64_t wgs, int dt,
+hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream) {
     if (wgs <= 0) return hipSuccess;
     if (wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
-    return dt == kBF16 ? launch_dt<kBF16>(a, R, S, wgs, stream)
-                       : launch_dt<kF16>(a, R, S, wgs, stream);
+    return dt == kBF16 ? launch_dt<kBF16>(a, p, wgs, stream)
+                       : launch_dt<kF16>(a, p, wgs, stream);
 }
 
 }  // namespace ojx

@@ -51,10 +51,19 @@ struct GemvLaunch {
     int M;
 };
 
+bool gemv_shape_ok(int64_t N, int64_t K);
 bool gemv_supported(const void* x, const uint8_t* packed, const uint16_t* scales, const void* y,
-                    int64_t M, int64_t K, int64_t gs, int dt);
-void gemv_pick(int64_t total_tiles, int* R, int* S);
-int64_t gemv_wgs_for(int64_t N, int R, int S);
-hipError_t launch_gemv(const GemvLaunch& a, int R, int S, int64_t wgs, int dt, hipStream_t stream);
+                    int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+// Kernel variant of a decode-GEMV launch.
+struct GemvPlan {
+    bool wide;   // streaming kernel (one tile set per wave, full K) vs in-workgroup K split
+    int R;       // 16-row tiles per wave
+    int S;       // K split ways inside the workgroup (non-wide only)
+    int mmax;    // activation rows staged in LDS (wide only): 4 or 16
+};
+GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
+int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
+hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
+                       hipStream_t stream);
 
 }  // namespace ojx

@@ -151,3 +151,31 @@ def test_grouped_plan_rejects_bad_jobs():
     g = GroupedGemv([ok], 2, torch.bfloat16, DEV, keep=[l.packed_weight, l.block_scales])
     with pytest.raises(RuntimeError, match="no activations"):
         g()
+
+
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 16])
+@pytest.mark.parametrize("K", [1280, 4096])
+def test_wide_kernel_partial_rounds_and_ragged_rows(M, K):
+    # >= 1024 row tiles selects the streaming kernel; K = 1280 leaves a partial
+    # second round (one live chunk of four), N = 16424 a ragged last tile
+    N = 16 * 1024 + 40
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=K + M)
+    x = _x(M, K, seed=M * 3, dtype=torch.bfloat16)
+    bias = _x(1, N, seed=4, dtype=torch.bfloat16).reshape(N)
+    print(f"wide M={M} K={K}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+
+
+def test_wide_kernel_fp16_and_subnormal_scales():
+    # tiny weights give fp16-subnormal group scales; fp16 activations keep them exactly
+    N, K, M = 16 * 1024, 512, 4
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=77, scale=2e-6)
+    assert (np.abs(sc_np.view(np.float16).astype(np.float32)) < 6.1e-5).mean() > 0.5
+    x = _x(M, K, seed=78, dtype=torch.float16)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_F16)
+    assert _rel(y, ref) <= REL_TOL
