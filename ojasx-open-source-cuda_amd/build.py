@@ -23,6 +23,7 @@ SOURCES = [
     "e8t_codec.hip",
     "e8t_gemm_generic.hip",
     "e8t_gemv.hip",
+    "e8t_gemm_mfma.hip",
     "e8t_capi.cpp",
 ]
 

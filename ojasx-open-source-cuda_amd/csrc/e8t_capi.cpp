@@ -142,6 +142,9 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
         return done(ojx::launch_gemv(a, plan, ojx::gemv_wgs_for(N, plan), dtype, s),
                     "e8t gemv launch");
     }
+    if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype))
+        return done(ojx::launch_gemm_mfma(x, packed, scales, bias, y, M, N, K, dtype, s),
+                    "e8t gemm_mfma launch");
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                 "e8t gemm_fwd launch");
 }

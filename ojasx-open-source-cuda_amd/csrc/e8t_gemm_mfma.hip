@@ -1,0 +1,337 @@
+// e8t_gemm_mfma.hip -- prefill fused ternary-E8 GEMM for gfx950 (batch M > 16).
+//
+// Y[M,N] = X[M,K] . Wq[N,K]^T (+ bias), Wq[n,k] = coord(code) * scale(n, k/32) in the
+// activation dtype (bf16: coord * bf16_rne(s16), lattice.py:414-418), fp32 accumulation.
+// Replaces the reference's TileLang ternary GEMM (tilelang_kernels.py:277-363, 64x64x64
+// tiles, LUT gathered from global memory) and its unpack + dense-GEMM fallback
+// (lattice.py:610-640): the weight tile is decoded once per workgroup into LDS and fed
+// to bf16 MFMA, so no dense weight ever reaches HBM.
+//
+// Tiling.  256x256 output tile per workgroup, K step 64, 8 waves in a 2x4 grid, each
+// wave 128x64 = 8x4 v_mfma_f32_16x16x32 tiles (128 fp32 accumulators per lane), so two
+// waves fit on each SIMD and cover each other's LDS and barrier waits.
+//   * X tile (256 x 64 bf16 = 32 KB) arrives by buffer->LDS loads, one K step ahead.
+//   * W tile: each pair of threads owns one of the 256 weight rows of the tile, loads
+//     its 8 codes (12 bytes) and 2 scales two K steps ahead, and each thread expands 4
+//     of them through the bank-sliced LDS table (e8t_lut.h) one step ahead, writing 64
+//     bytes of bf16 weights.
+//   * Both tiles are double buffered; rows are stored as 8 pieces of 16 bytes with piece
+//     p of row r at position p ^ ((r >> 1) & 7), which makes the 16-lane fragment reads
+//     and the row writes bank-conflict free.  One barrier per K step.
+// Workgroup order: consecutive workgroup ids land on different XCDs (round robin); the
+// tile index is remapped so that each XCD walks a contiguous, M-grouped range of tiles
+// and its L2 serves the X rows and weight columns that its concurrent workgroups share.
+
+#include "e8t_device.h"
+#include "e8t_internal.h"
+#include "e8t_lut.h"
+
+namespace ojx {
+
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kWaves = 8;                  // 2 (M) x 4 (N) waves, 128 x 64 each
+constexpr int kGemmThreads = 64 * kWaves;
+constexpr int kWM = 128, kWN = 64;         // wave tile
+constexpr int kTM = kWM / 16, kTN = kWN / 16;  // 8 x 4 MFMA tiles per wave
+constexpr int kTileBytes = kBM * kBK * 2;  // 32 KB per operand tile
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t piece) {
+    return row * 128u + 16u * (piece ^ ((row >> 1) & 7u));
+}
+
+// X tile rows [m0, m0+256) x k [k0, k0+64) -> LDS tile (swizzled); each of the 8 waves
+// issues 4 1-KB loads (8 rows each).  Rows >= M read past the buffer's end: zeros.
+__device__ __forceinline__ void load_x_tile(char* tile, __amdgpu_buffer_rsrc_t x, int64_t m0,
+                                            int64_t k0, int64_t K, int wave, int lane) {
+    const uint32_t r_in = (uint32_t)lane >> 3, q = (uint32_t)lane & 7u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = 32u * wave + 8u * i + r_in;
+        const uint32_t p = q ^ ((row >> 1) & 7u);
+        const uint32_t voff = (uint32_t)((m0 + row) * K * 2 + 16u * p);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            x, (__attribute__((address_space(3))) void*)(tile + (32 * wave + 8 * i) * 128), 16,
+            voff, uniform_offset(k0 * 2), 0, 0);
+    }
+}
+
+struct RowCodes {
+    uint32_t d[3];  // 8 codes of this thread's weight row for one K step
+    uint32_t s;     // its two group scales (fp16 bits)
+};
+
+__device__ __forceinline__ void load_codes_row(RowCodes& rc, __amdgpu_buffer_rsrc_t packed,
+                                               __amdgpu_buffer_rsrc_t scales, uint32_t vo_code,
+                                               uint32_t vo_scale, int64_t k0) {
+    const u32x3 v =
+        __builtin_amdgcn_raw_buffer_load_b96(packed, vo_code, uniform_offset(k0 * 3 / 16), 0);
+    rc.d[0] = v.x;
+    rc.d[1] = v.y;
+    rc.d[2] = v.z;
+    rc.s = __builtin_amdgcn_raw_buffer_load_b32(scales, vo_scale, uniform_offset(k0 / 16), 0);
+}
+
+template <int J>
+__device__ __forceinline__ void decode_piece(const RowCodes& rc, const char* lut, uint32_t slot,
+                                             uint32_t sw, char* tile, uint32_t row) {
+    const uint32_t z = code_z<J>(rc.d, slot);
+    const uint32_t h = __umulhi(z, kHiMagic);
+    const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+    const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+    *reinterpret_cast<uint4*>(tile + swz(row, J)) =
+        make_uint4(ml.x & sw, ml.y & sw, mh.x & sw, mh.y & sw);
+}
+
+// Expands codes 4h .. 4h+3 of this thread's weight row (32 weights; h = half) into the
+// LDS tile.
+template <int DT>
+__device__ __forceinline__ void decode_half(const RowCodes& rc, const char* lut, uint32_t slot,
+                                            char* tile, uint32_t row, int half) {
+    uint32_t w0, w1;
+    scale_words<DT>(rc.s, w0, w1);
+    if (half == 0) {
+        decode_piece<0>(rc, lut, slot, w0, tile, row);
+        decode_piece<1>(rc, lut, slot, w0, tile, row);
+        decode_piece<2>(rc, lut, slot, w0, tile, row);
+        decode_piece<3>(rc, lut, slot, w0, tile, row);
+    } else {
+        decode_piece<4>(rc, lut, slot, w1, tile, row);
+        decode_piece<5>(rc, lut, slot, w1, tile, row);
+        decode_piece<6>(rc, lut, slot, w1, tile, row);
+        decode_piece<7>(rc, lut, slot, w1, tile, row);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void mma_row(const uint4& a, const uint4 (&b)[kTN], f32x4 (&acc)[kTN]) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) acc[j] = mfma16<DT>(a, b[j], acc[j]);
+}
+
+// Fragment addresses.  Rows of a wave's A (B) fragments are arow0 + 16i + i16 (brow0 +
+// 16j + i16) with arow0, brow0 multiples of 64, so the swizzle term (row >> 1) & 7 is
+// (i16 >> 1) & 7 for every fragment of a lane: each fragment is a per-lane base plus the
+// compile-time offset 2048*i (one ds_read_b128 with an immediate offset).
+struct FragLane {
+    uint32_t a[2], b[2];  // byte offsets within a tile for K sub-step 0 / 1
+};
+
+__device__ __forceinline__ FragLane frag_lane(uint32_t arow0, uint32_t brow0, int g, int i16) {
+    const uint32_t c = ((uint32_t)i16 >> 1) & 7u;
+    FragLane f;
+    f.a[0] = (arow0 + i16) * 128u + 16u * ((uint32_t)g ^ c);
+    f.a[1] = (arow0 + i16) * 128u + 16u * ((4u + g) ^ c);
+    f.b[0] = (brow0 + i16) * 128u + 16u * ((uint32_t)g ^ c);
+    f.b[1] = (brow0 + i16) * 128u + 16u * ((4u + g) ^ c);
+    return f;
+}
+
+__device__ __forceinline__ void load_frags(const char* xt, const char* wt, const FragLane& f,
+                                           int sub, uint4 (&a)[kTM], uint4 (&b)[kTN]) {
+    const char* pa = xt + f.a[sub];
+    const char* pb = wt + f.b[sub];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) a[i] = *reinterpret_cast<const uint4*>(pa + 2048 * i);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) b[j] = *reinterpret_cast<const uint4*>(pb + 2048 * j);
+}
+
+// Table reads of code j (0..7) of this thread's row (two 8-byte masks).
+template <int J>
+__device__ __forceinline__ void lut_read(const RowCodes& rc, const char* lut, uint32_t slot,
+                                         uint2& ml, uint2& mh) {
+    const uint32_t z = code_z<J>(rc.d, slot);
+    const uint32_t h = __umulhi(z, kHiMagic);
+    ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+    mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+}
+
+// Table reads for codes 4*half .. 4*half+3 of this thread's row.
+__device__ __forceinline__ void lut_reads_half(const RowCodes& rc, const char* lut,
+                                               uint32_t slot, int half, uint2 (&ml)[4],
+                                               uint2 (&mh)[4]) {
+    if (half == 0) {
+        lut_read<0>(rc, lut, slot, ml[0], mh[0]);
+        lut_read<1>(rc, lut, slot, ml[1], mh[1]);
+        lut_read<2>(rc, lut, slot, ml[2], mh[2]);
+        lut_read<3>(rc, lut, slot, ml[3], mh[3]);
+    } else {
+        lut_read<4>(rc, lut, slot, ml[0], mh[0]);
+        lut_read<5>(rc, lut, slot, ml[1], mh[1]);
+        lut_read<6>(rc, lut, slot, ml[2], mh[2]);
+        lut_read<7>(rc, lut, slot, ml[3], mh[3]);
+    }
+}
+
+// One K step (64) of the wave's 128x64 block.
+//   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read;
+//   2. table reads for this thread's 4 codes of the NEXT step's weight row (their codes
+//      arrived a full step ago), then `rc` is re-armed with the codes of the step after;
+//   3. sub-step 1; in its second half the masked weight pairs of the next step are
+//      written to the other LDS buffer (the table reads were issued 4 MFMA rows earlier).
+template <int DT>
+__device__ __forceinline__ void kstep(const char* xt, const char* wt, const FragLane& fl,
+                                      uint4 (&a0)[kTM], uint4 (&b0)[kTN], uint4 (&a1)[kTM],
+                                      uint4 (&b1)[kTN], RowCodes& rc, const char* lut,
+                                      uint32_t slot, char* wt_next, uint32_t wrow, int half,
+                                      f32x4 (&acc)[kTM][kTN], __amdgpu_buffer_rsrc_t pr,
+                                      __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
+                                      uint32_t vo_scale, int64_t k_reload) {
+    const char* pa1 = xt + fl.a[1];
+    const char* pb1 = wt + fl.b[1];
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) b1[j] = *reinterpret_cast<const uint4*>(pb1 + 2048 * j);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+        mma_row<DT>(a0[i], b0, acc[i]);
+        a1[i] = *reinterpret_cast<const uint4*>(pa1 + 2048 * i);
+    }
+    uint2 ml[4], mh[4];
+    lut_reads_half(rc, lut, slot, half, ml, mh);
+    uint32_t w0, w1;
+    scale_words<DT>(rc.s, w0, w1);
+    const uint32_t sw = half ? w1 : w0;
+    load_codes_row(rc, pr, sr, vo_code, vo_scale, k_reload);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+        mma_row<DT>(a1[i], b1, acc[i]);
+        if (i >= 4) {  // the table reads were issued 4 MFMA rows ago
+            *reinterpret_cast<uint4*>(wt_next + swz(wrow, 4u * half + (i - 4))) = make_uint4(
+                ml[i - 4].x & sw, ml[i - 4].y & sw, mh[i - 4].x & sw, mh[i - 4].y & sw);
+        }
+    }
+}
+
+__device__ __forceinline__ void vm_wait_le2() {
+    __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): all but the two newest loads (gfx9)
+}
+
+template <int DT>
+__global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
+    const void* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
+    int64_t M, int64_t N, int64_t K) {
+    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ __attribute__((aligned(16))) char xs[2][kTileBytes];
+    __shared__ __attribute__((aligned(16))) char ws[2][kTileBytes];
+
+    fill_lut(lut_storage);
+
+    // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
+    const int64_t tm_n = (M + kBM - 1) / kBM, tn_n = (N + kBN - 1) / kBN;
+    const int64_t tiles = tm_n * tn_n;
+    const int64_t bid = blockIdx.x;
+    const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+    const int64_t xcd = bid % kXcds, slot_in = bid / kXcds;
+    int64_t t = xcd * per_xcd + slot_in;
+    if (per_xcd * kXcds != tiles) {
+        // grid not a multiple of the XCD count: fall back to the plain order
+        t = bid;
+    }
+    if (t >= tiles) return;
+    const int64_t group = t / (kGroupM * tn_n);
+    const int64_t first_m = group * kGroupM;
+    const int64_t gsize = (tm_n - first_m) < kGroupM ? (tm_n - first_m) : kGroupM;
+    const int64_t tm = first_m + (t % (kGroupM * tn_n)) % gsize;
+    const int64_t tn = (t % (kGroupM * tn_n)) / gsize;
+    const int64_t m0 = tm * kBM, n0 = tn * kBN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const uint32_t arow0 = (uint32_t)kWM * (uint32_t)(wave >> 2);
+    const uint32_t brow0 = (uint32_t)kWN * (uint32_t)(wave & 3);
+
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16), srowbytes = (uint32_t)(K / 16);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const uint32_t wrow = (uint32_t)tid >> 1;  // this thread's weight row in the tile
+    const int half = tid & 1;                   // ... and which 4 of its 8 codes
+    const uint32_t vo_code = (uint32_t)(n0 + wrow) * rowbytes;
+    const uint32_t vo_scale = (uint32_t)(n0 + wrow) * srowbytes;
+    const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+
+    f32x4 acc[kTM][kTN];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t steps = K / kBK;
+    // Codes run one K step ahead of the weight tile being decoded, which runs one step
+    // ahead of the MFMAs.  Branch-free body: loads past the last step fetch bytes past the
+    // operands (zeros, or the next row's data) into buffers that are never read.
+    RowCodes rc;
+    load_x_tile(xs[0], xr, m0, 0, K, wave, lane);
+    load_codes_row(rc, pr, sr, vo_code, vo_scale, 0);
+    __syncthreads();  // table ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+    decode_half<DT>(rc, lut, slot, ws[0], wrow, half);
+    load_codes_row(rc, pr, sr, vo_code, vo_scale, kBK);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+
+    const FragLane fl = frag_lane(arow0, brow0, g, i16);
+    uint4 a0[kTM], b0[kTN], a1[kTM], b1[kTN];
+    load_frags(xs[0], ws[0], fl, 0, a0, b0);
+    for (int64_t s = 0; s < steps; ++s) {
+        const int cur = (int)(s & 1), nxt = cur ^ 1;
+        load_x_tile(xs[nxt], xr, m0, (s + 1) * kBK, K, wave, lane);
+        kstep<DT>(xs[cur], ws[cur], fl, a0, b0, a1, b1, rc, lut, slot, ws[nxt], wrow, half, acc,
+                  pr, sr, vo_code, vo_scale, (s + 2) * kBK);
+        vm_wait_le2();  // the X tile of step s+1 has landed; the code loads may still fly
+        __syncthreads();
+        load_frags(xs[nxt], ws[nxt], fl, 0, a0, b0);
+    }
+
+    // ---- epilogue: lane (g, i16) holds rows 4g+q of column i16 of each 16x16 tile
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+        const int64_t col = n0 + brow0 + 16 * j + i16;
+        if (col >= N) continue;
+        const float bv = bias ? load_as_f32<DT>(bias, col) : 0.f;
+#pragma unroll
+        for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t row = m0 + arow0 + 16 * i + 4 * g + q;
+                if (row < M) store_from_f32<DT>(y, row * N + col, acc[i][j][q] + bv);
+            }
+        }
+    }
+}
+
+bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+    if (dt != kBF16 && dt != kF16) return false;
+    if (gs != 32 || M < 1 || N < 1 || K < kBK || K % kBK != 0) return false;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 3u) || ((uintptr_t)scales & 3u))
+        return false;
+    // 32-bit buffer offsets: the activation matrix and the weight buffers (plus one tile
+    // of padding rows) must stay below 2^31 bytes
+    if ((M + kBM) * K * 2 >= (1ll << 31) || (N + kBN) * (K * 3 / 16) >= (1ll << 31)) return false;
+    return true;
+}
+
+hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
+                            const void* bias, void* y, int64_t M, int64_t N, int64_t K, int dt,
+                            hipStream_t stream) {
+    const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+    if (dt == kBF16)
+        hipLaunchKernelGGL((gemm_mfma_kernel<kBF16>), dim3((unsigned)tiles), dim3(kGemmThreads), 0,
+                           stream, x, packed, scales, bias, y, M, N, K);
+    else
+        hipLaunchKernelGGL((gemm_mfma_kernel<kF16>), dim3((unsigned)tiles), dim3(kGemmThreads), 0,
+                           stream, x, packed, scales, bias, y, M, N, K);
+    return hipGetLastError();
+}
+
+}  // namespace ojx

@@ -31,96 +31,15 @@
 
 #include "e8t_device.h"
 #include "e8t_internal.h"
+#include "e8t_lut.h"
 
 #include <cstdlib>
 #include <utility>
 
 namespace ojx {
 
-typedef __attribute__((ext_vector_type(4))) float f32x4;
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-typedef __attribute__((ext_vector_type(3))) uint32_t u32x3;
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-
 constexpr int kGemvThreads = 256;           // 4 waves
-constexpr int kLutEntries = 102;            // 81 valid + slack so that any 12-bit code stays in bounds
-constexpr int kLutSlots = 32;               // bank slices: lane l reads slice l % 32
-constexpr uint32_t kLutStride = kLutSlots * 8;  // bytes per table entry (all slices)
-constexpr uint32_t kHiMagic = 207127u;      // floor((512c + b) * kHiMagic / 2^32) == floor(2c / 81), b < 256
 constexpr int kChunk = 256;                 // K per chunk: 32 codes per row = 48 bytes
-constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
-
-__device__ __forceinline__ uint32_t lut_mask_half(int digit) {
-    return digit == 0 ? 0xFFFFu : (digit == 1 ? 0x0000u : 0x7FFFu);
-}
-
-// Fills the bank-sliced table: entry e, slice c at byte offset (e + 1) * kLutStride + c * 8
-// of the storage; entry -1 is a zero guard (with kHiMagic, the lo address of an invalid
-// code >= 3281 can reach 8 bytes below entry 0; valid codes never do).
-__device__ __forceinline__ void fill_lut(uint2* storage) {
-    for (int i = threadIdx.x; i < (kLutEntries + 1) * kLutSlots; i += blockDim.x) {
-        const int e = i / kLutSlots - 1;
-        if (e < 0) {
-            storage[i] = make_uint2(0u, 0u);
-            continue;
-        }
-        const int d0 = e % 3, d1 = (e / 3) % 3, d2 = (e / 9) % 3, d3 = (e / 27) % 3;
-        storage[i] = make_uint2(lut_mask_half(d0) | (lut_mask_half(d1) << 16),
-                                lut_mask_half(d2) | (lut_mask_half(d3) << 16));
-    }
-}
-
-// Z = (code_j << 9) | slot for code j (0..7) of the 12-byte, 8-code group (d0, d1, d2):
-// code j occupies bits [12j, 12j+12) of the little-endian stream (lattice.py:375-383).
-template <int J>
-__device__ __forceinline__ uint32_t code_z(const uint32_t (&d)[3], uint32_t slot) {
-    uint32_t t;
-    if constexpr (J == 0) t = d[0] << 9;
-    else if constexpr (J == 1) t = d[0] >> 3;
-    else if constexpr (J == 2) t = __builtin_amdgcn_alignbit(d[1], d[0], 15);
-    else if constexpr (J == 3) t = d[1] << 5;
-    else if constexpr (J == 4) t = d[1] >> 7;
-    else if constexpr (J == 5) t = __builtin_amdgcn_alignbit(d[2], d[1], 19);
-    else if constexpr (J == 6) t = d[2] << 1;
-    else t = d[2] >> 11;
-    return (t & 0x1FFE00u) | slot;
-}
-
-// lo address = Z - 81 * kLutStride * hi = (2c - 81 hi) * kLutStride + slot, as one
-// full-rate 24-bit multiply-add (the compiler otherwise picks a 64-bit v_mad_u64_u32).
-__device__ __forceinline__ uint32_t lo_addr_of(uint32_t h, uint32_t z) {
-    uint32_t r;
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(h), "s"(-81 * (int)kLutStride), "v"(z));
-    return r;
-}
-
-// Two group scales (fp16 bits, packed) -> the AND words s | s<<16 | 0x80008000 in the
-// activation dtype (bf16: bf16_rne(float(s16)), lattice.py:414-418; fp16: exact).
-template <int DT>
-__device__ __forceinline__ void scale_words(uint32_t sc, uint32_t& w0, uint32_t& w1) {
-    uint32_t p;
-    if constexpr (DT == kBF16) {
-        const __bf16 b0 = (__bf16)f16_bits_to_f32(sc & 0xFFFFu);  // v_cvt_pk_bf16_f32 (RNE)
-        const __bf16 b1 = (__bf16)f16_bits_to_f32(sc >> 16);
-        p = (uint32_t)__builtin_bit_cast(uint16_t, b0) |
-            ((uint32_t)__builtin_bit_cast(uint16_t, b1) << 16);
-    } else {
-        p = sc;
-    }
-    w0 = __builtin_amdgcn_perm(p, p, 0x01000100u) | 0x80008000u;
-    w1 = __builtin_amdgcn_perm(p, p, 0x03020302u) | 0x80008000u;
-}
-
-template <int DT>
-__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f32x4& c) {
-    if constexpr (DT == kBF16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
 
 template <int R>
 struct Codes {
@@ -145,12 +64,12 @@ __device__ __forceinline__ void load_codes(Codes<R>& ch, int64_t c, const Stream
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(st.packed, st.vo_code[r],
-                                                             (int)(c * 48), 0);
+                                                             uniform_offset(c * 48), 0);
         ch.cd[r][0] = v.x;
         ch.cd[r][1] = v.y;
         ch.cd[r][2] = v.z;
         ch.sc[r] = __builtin_amdgcn_raw_buffer_load_b32(st.scales, st.vo_scale[r],
-                                                        (int)(c * 16), 0);
+                                                        uniform_offset(c * 16), 0);
     }
 }
 
@@ -158,7 +77,7 @@ template <int R>
 __device__ __forceinline__ void load_x(uint4& xa, int64_t c, int j, const Stream<R>& st) {
     if (st.x_live) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(st.x, st.vo_x + 16u * j,
-                                                              (int)(c * (kChunk * 2)), 0);
+                                                              uniform_offset(c * (kChunk * 2)), 0);
         xa = make_uint4(v.x, v.y, v.z, v.w);
     }
 }
@@ -385,14 +304,14 @@ __device__ __forceinline__ void load_wide(WideCodes<R>& w, int64_t u, const Wide
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                st.packed, st.vo_code[r] + 16u * t, (int)(u * 192), 0);
+                st.packed, st.vo_code[r] + 16u * t, uniform_offset(u * 192), 0);
             w.cd[r][4 * t + 0] = v.x;
             w.cd[r][4 * t + 1] = v.y;
             w.cd[r][4 * t + 2] = v.z;
             w.cd[r][4 * t + 3] = v.w;
         }
         const u32x4 s = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r],
-                                                              (int)(u * 64), 0);
+                                                              uniform_offset(u * 64), 0);
         w.sc[r][0] = live ? s.x : 0u;
         w.sc[r][1] = live ? s.y : 0u;
         w.sc[r][2] = live ? s.z : 0u;
@@ -401,14 +320,15 @@ __device__ __forceinline__ void load_wide(WideCodes<R>& w, int64_t u, const Wide
 }
 
 // Stages x[m][1024u .. 1024u + 1024) for m < M into LDS buffer `xs` (row stride kXRow):
-// 2M wave-level loads of 1 KB each, spread over the workgroup's 4 waves.
+// 2M wave-level loads of 1 KB each, spread over the workgroup's `waves` waves.
 __device__ __forceinline__ void stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int64_t u, int M,
-                                        int64_t K, int wave, int lane) {
-    for (int q = wave; q < 2 * M; q += 4) {
+                                        int64_t K, int wave, int lane, int waves) {
+    for (int q = wave; q < 2 * M; q += waves) {
         const int m = q >> 1, half = q & 1;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             x, (__attribute__((address_space(3))) void*)(xs + m * kXRow + half * 1024),
-            16, (uint32_t)(m * K * 2 + half * 1024 + lane * 16), (int)(u * kRound * 2), 0, 0);
+            16, (uint32_t)(m * K * 2 + half * 1024 + lane * 16), uniform_offset(u * kRound * 2), 0,
+            0);
     }
 }
 
@@ -485,9 +405,10 @@ __device__ __forceinline__ void vm_wait_all() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
 }
 
-// R: n-tiles (16 rows) per wave; MMAX: activation rows staged (4 or 16; M <= MMAX).
-template <int DT, int R, int MMAX>
-__global__ __launch_bounds__(kGemvThreads) void gemv_wide_kernel(GemvLaunch args) {
+// R: n-tiles (16 rows) per wave; MMAX: activation rows staged (4 or 16; M <= MMAX);
+// W: waves per workgroup (they share the table and the activation stage).
+template <int DT, int R, int MMAX, int W>
+__global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
     __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
     __shared__ __attribute__((aligned(16))) char xs_storage[2][MMAX * kXRow];
 
@@ -515,7 +436,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_wide_kernel(GemvLaunch args
     const int M = args.M;
     const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
     const uint32_t srowbytes = (uint32_t)(K / 16);
-    const int64_t tile0 = (wg * 4 + wave) * R;
+    const int64_t tile0 = (wg * W + wave) * R;
 
     WideStream<R> st;
     st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
@@ -543,7 +464,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_wide_kernel(GemvLaunch args
 
     WideCodes<R> CA, CB;
     load_wide<R>(CA, 0, st);
-    stage_x(xs_storage[0], st.x, 0, M, K, wave, lane);
+    stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // LUT and round-0 activations ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
@@ -551,7 +472,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_wide_kernel(GemvLaunch args
     for (int64_t t = 0; t < T; t += 2) {
         if (t + 1 < T) {
             load_wide<R>(CB, t + 1, st);
-            stage_x(xs_storage[1], st.x, t + 1, M, K, wave, lane);
+            stage_x(xs_storage[1], st.x, t + 1, M, K, wave, lane, W);
         }
         wide_round<DT, R>(CA, lut, xs_storage[0] + xa_off, st.slot, acc);
         vm_wait_all();
@@ -559,7 +480,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_wide_kernel(GemvLaunch args
         if (t + 1 >= T) break;
         if (t + 2 < T) {
             load_wide<R>(CA, t + 2, st);
-            stage_x(xs_storage[0], st.x, t + 2, M, K, wave, lane);
+            stage_x(xs_storage[0], st.x, t + 2, M, K, wave, lane, W);
         }
         wide_round<DT, R>(CB, lut, xs_storage[1] + xa_off, st.slot, acc);
         vm_wait_all();
@@ -607,24 +528,27 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.R = 2;
         p.S = 1;
         p.mmax = M <= 4 ? 4 : 16;
+        p.W = p.mmax == 16 ? 8 : 4;  // the 16-row activation stage is shared by 8 waves
     } else {
         // small layers: split K inside the workgroup to get enough waves
         p.wide = false;
         p.R = 1;
         p.S = total_tiles >= 512 ? 2 : 4;
+        p.W = 4;
         p.mmax = 16;
     }
     if (const char* e = getenv("OJX_TUNE_GEMV_RS")) {  // TEMPORARY tuning override
         p.wide = e[2] == 'w';
         p.R = e[0] - '0';
         p.S = e[1] - '0';
+        if (p.wide) p.W = e[3] - '0';
     }
     return p;
 }
 
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p) {
     const int64_t tiles = (N + 15) / 16;
-    const int64_t per_wg = p.wide ? 4 * p.R : (int64_t)(4 / p.S) * p.R;
+    const int64_t per_wg = p.wide ? (int64_t)p.W * p.R : (int64_t)(4 / p.S) * p.R;
     return (tiles + per_wg - 1) / per_wg;
 }
 
@@ -635,10 +559,10 @@ static hipError_t launch_rs(const GemvLaunch& a, int64_t wgs, hipStream_t stream
     return hipGetLastError();
 }
 
-template <int DT, int R, int MMAX>
+template <int DT, int R, int MMAX, int W>
 static hipError_t launch_wide(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_wide_kernel<DT, R, MMAX>), dim3((unsigned)wgs), dim3(kGemvThreads),
-                       0, stream, a);
+    hipLaunchKernelGGL((gemv_wide_kernel<DT, R, MMAX, W>), dim3((unsigned)wgs), dim3(64 * W), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
@@ -646,10 +570,12 @@ template <int DT>
 static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                             hipStream_t stream) {
     if (p.wide) {
-        if (p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4>(a, wgs, stream);
-        if (p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16>(a, wgs, stream);
-        if (p.R == 1 && p.mmax == 4) return launch_wide<DT, 1, 4>(a, wgs, stream);
-        if (p.R == 1 && p.mmax == 16) return launch_wide<DT, 1, 16>(a, wgs, stream);
+        if (p.W == 4 && p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4, 4>(a, wgs, stream);
+        if (p.W == 4 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 4>(a, wgs, stream);
+        if (p.W == 8 && p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4, 8>(a, wgs, stream);
+        if (p.W == 8 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 8>(a, wgs, stream);
+        if (p.W == 8 && p.R == 1 && p.mmax == 4) return launch_wide<DT, 1, 4, 8>(a, wgs, stream);
+        if (p.W == 8 && p.R == 1 && p.mmax == 16) return launch_wide<DT, 1, 16, 8>(a, wgs, stream);
         return hipErrorInvalidValue;
     }
     if (p.R == 4 && p.S == 1) return launch_rs<DT, 4, 1>(a, wgs, stream);

@@ -59,11 +59,19 @@ struct GemvPlan {
     bool wide;   // streaming kernel (one tile set per wave, full K) vs in-workgroup K split
     int R;       // 16-row tiles per wave
     int S;       // K split ways inside the workgroup (non-wide only)
+    int W;       // waves per workgroup (wide only)
     int mmax;    // activation rows staged in LDS (wide only): 4 or 16
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream);
+
+// Prefill MFMA GEMM (M > 16): F16/BF16, K % 64 == 0, group size 32.
+bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
+                            const void* bias, void* y, int64_t M, int64_t N, int64_t K, int dt,
+                            hipStream_t stream);
 
 }  // namespace ojx
