@@ -33,7 +33,6 @@
 #include "e8t_internal.h"
 #include "e8t_lut.h"
 
-#include <cstdlib>
 #include <utility>
 
 namespace ojx {
@@ -536,12 +535,6 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.S = total_tiles >= 512 ? 2 : 4;
         p.W = 4;
         p.mmax = 16;
-    }
-    if (const char* e = getenv("OJX_TUNE_GEMV_RS")) {  // TEMPORARY tuning override
-        p.wide = e[2] == 'w';
-        p.R = e[0] - '0';
-        p.S = e[1] - '0';
-        if (p.wide) p.W = e[3] - '0';
     }
     return p;
 }
