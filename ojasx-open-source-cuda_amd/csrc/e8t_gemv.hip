@@ -281,7 +281,11 @@ constexpr uint32_t kXRow = kRound * 2 + 16;       // bytes per padded activation
 template <int R>
 struct WideCodes {
     uint32_t cd[R][12];  // 48 bytes = 32 codes of one row
-    uint32_t sc[R][4];   // the 8 group scales covering them
+};
+
+template <int R>
+struct WideScales {
+    uint32_t sc[R][4];   // the 8 group scales covering the 32 codes
 };
 
 template <int R>
@@ -293,22 +297,28 @@ struct WideStream {
     int g;
 };
 
+// Piece t (bytes 16t .. 16t+15) of each row's 48 code bytes of round u.
 template <int R>
-__device__ __forceinline__ void load_wide(WideCodes<R>& w, int64_t u, const WideStream<R>& st) {
+__device__ __forceinline__ void load_code_piece(WideCodes<R>& w, int t, int64_t u,
+                                                const WideStream<R>& st) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+            st.packed, st.vo_code[r] + 16u * t, uniform_offset(u * 192), 0);
+        w.cd[r][4 * t + 0] = v.x;
+        w.cd[r][4 * t + 1] = v.y;
+        w.cd[r][4 * t + 2] = v.z;
+        w.cd[r][4 * t + 3] = v.w;
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void load_scales(WideScales<R>& w, int64_t u, const WideStream<R>& st) {
     // lane groups past K in a partial last round read the next row's bytes: zero their
     // scales so those codes contribute exactly zero
     const bool live = u * kRound + 256 * st.g < st.K;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                st.packed, st.vo_code[r] + 16u * t, uniform_offset(u * 192), 0);
-            w.cd[r][4 * t + 0] = v.x;
-            w.cd[r][4 * t + 1] = v.y;
-            w.cd[r][4 * t + 2] = v.z;
-            w.cd[r][4 * t + 3] = v.w;
-        }
         const u32x4 s = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r],
                                                               uniform_offset(u * 64), 0);
         w.sc[r][0] = live ? s.x : 0u;
@@ -345,16 +355,24 @@ __device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut,
     }
 }
 
+// Step J of a round.  Code piece 0 (dwords 0-3) is last read by the table lookahead of
+// step 9 (code 10), piece 1 by that of step 20 (code 21), piece 2 by that of step 30
+// (code 31): each is refilled with the next round's bytes right after steps 10, 21 and
+// 31, and is next needed 21 steps later.  The next round's scales are fetched at step 0.
 template <int DT, int R, int J>
-__device__ __forceinline__ void wide_step(const WideCodes<R>& w, const char* lut,
-                                          const char* xa_base, uint32_t slot, uint4& xa_cur,
-                                          uint2 (&ml)[R], uint2 (&mh)[R], uint32_t (&sw)[R],
-                                          f32x4 (&acc)[R]) {
+__device__ __forceinline__ void wide_step(WideCodes<R>& w, const WideScales<R>& sc,
+                                          WideScales<R>& sc_next, int64_t u_next,
+                                          const WideStream<R>& st, const char* lut,
+                                          const char* xa_base, uint4& xa_cur, uint2 (&ml)[R],
+                                          uint2 (&mh)[R], uint32_t (&sw)[R], f32x4 (&acc)[R]) {
+    if constexpr (J == 0) {
+        if (u_next >= 0) load_scales<R>(sc_next, u_next, st);
+    }
     if constexpr (J % 4 == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             uint32_t w0, w1;
-            scale_words<DT>(w.sc[r][J / 8], w0, w1);
+            scale_words<DT>(sc.sc[r][J / 8], w0, w1);
             sw[r] = (J % 8 == 0) ? w0 : w1;
         }
     }
@@ -362,13 +380,16 @@ __device__ __forceinline__ void wide_step(const WideCodes<R>& w, const char* lut
     uint2 ml_n[R], mh_n[R];
     if constexpr (J + 1 < 32) {
         xa_nxt = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + 1));
-        wide_lut<R, J + 1>(w, lut, slot, ml_n, mh_n);
+        wide_lut<R, J + 1>(w, lut, st.slot, ml_n, mh_n);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t s = sw[r];
         const uint4 b = make_uint4(ml[r].x & s, ml[r].y & s, mh[r].x & s, mh[r].y & s);
         acc[r] = mfma16<DT>(xa_cur, b, acc[r]);
+    }
+    if constexpr (J == 10 || J == 21 || J == 31) {
+        if (u_next >= 0) load_code_piece<R>(w, J == 10 ? 0 : (J == 21 ? 1 : 2), u_next, st);
     }
     if constexpr (J + 1 < 32) {
         xa_cur = xa_nxt;
@@ -381,27 +402,38 @@ __device__ __forceinline__ void wide_step(const WideCodes<R>& w, const char* lut
 }
 
 template <int DT, int R, int... J>
-__device__ __forceinline__ void wide_steps(const WideCodes<R>& w, const char* lut,
-                                           const char* xa_base, uint32_t slot, uint4& xa,
-                                           uint2 (&ml)[R], uint2 (&mh)[R], uint32_t (&sw)[R],
-                                           f32x4 (&acc)[R],
+__device__ __forceinline__ void wide_steps(WideCodes<R>& w, const WideScales<R>& sc,
+                                           WideScales<R>& sc_next, int64_t u_next,
+                                           const WideStream<R>& st, const char* lut,
+                                           const char* xa_base, uint4& xa, uint2 (&ml)[R],
+                                           uint2 (&mh)[R], uint32_t (&sw)[R], f32x4 (&acc)[R],
                                            std::integer_sequence<int, J...>) {
-    (wide_step<DT, R, J>(w, lut, xa_base, slot, xa, ml, mh, sw, acc), ...);
+    (wide_step<DT, R, J>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sw, acc), ...);
 }
 
+// One round on the codes in `w` (refilled in place with round u_next's, if >= 0).
 template <int DT, int R>
-__device__ __forceinline__ void wide_round(const WideCodes<R>& w, const char* lut,
-                                           const char* xa_base, uint32_t slot, f32x4 (&acc)[R]) {
+__device__ __forceinline__ void wide_round(WideCodes<R>& w, const WideScales<R>& sc,
+                                           WideScales<R>& sc_next, int64_t u_next,
+                                           const WideStream<R>& st, const char* lut,
+                                           const char* xa_base, f32x4 (&acc)[R]) {
     uint4 xa = *reinterpret_cast<const uint4*>(xa_base);
     uint2 ml[R], mh[R];
     uint32_t sw[R];
-    wide_lut<R, 0>(w, lut, slot, ml, mh);
-    wide_steps<DT, R>(w, lut, xa_base, slot, xa, ml, mh, sw, acc,
+    wide_lut<R, 0>(w, lut, st.slot, ml, mh);
+    wide_steps<DT, R>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sw, acc,
                       std::make_integer_sequence<int, 32>{});
 }
 
 __device__ __forceinline__ void vm_wait_all() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
+}
+
+// vmcnt(N) (N < 16): all but this wave's N most recent vector-memory loads have landed.
+template <int N>
+__device__ __forceinline__ void vm_wait_le() {
+    static_assert(N >= 0 && N < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
 // R: n-tiles (16 rows) per wave; MMAX: activation rows staged (4 or 16; M <= MMAX);
@@ -461,28 +493,33 @@ __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    WideCodes<R> CA, CB;
-    load_wide<R>(CA, 0, st);
+    // One register set of codes (refilled piece by piece during each round), two of
+    // scales.  At a round's end, this wave's only loads newer than its activation-stage
+    // loads are the 4R code/scale loads of the next round: vmcnt(4R) waits exactly for
+    // the stage.
+    WideCodes<R> w;
+    WideScales<R> scA, scB;
+    load_code_piece<R>(w, 0, 0, st);
+    load_code_piece<R>(w, 1, 0, st);
+    load_code_piece<R>(w, 2, 0, st);
+    load_scales<R>(scA, 0, st);
     stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // LUT and round-0 activations ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
 
     for (int64_t t = 0; t < T; t += 2) {
-        if (t + 1 < T) {
-            load_wide<R>(CB, t + 1, st);
-            stage_x(xs_storage[1], st.x, t + 1, M, K, wave, lane, W);
-        }
-        wide_round<DT, R>(CA, lut, xs_storage[0] + xa_off, st.slot, acc);
-        vm_wait_all();
+        const bool has1 = t + 1 < T, has2 = t + 2 < T;
+        if (has1) stage_x(xs_storage[1], st.x, t + 1, M, K, wave, lane, W);
+        wide_round<DT, R>(w, scA, scB, has1 ? t + 1 : -1, st, lut, xs_storage[0] + xa_off, acc);
+        if (has1) vm_wait_le<4 * R>();
+        else vm_wait_all();
         __syncthreads();
-        if (t + 1 >= T) break;
-        if (t + 2 < T) {
-            load_wide<R>(CA, t + 2, st);
-            stage_x(xs_storage[0], st.x, t + 2, M, K, wave, lane, W);
-        }
-        wide_round<DT, R>(CB, lut, xs_storage[1] + xa_off, st.slot, acc);
-        vm_wait_all();
+        if (!has1) break;
+        if (has2) stage_x(xs_storage[0], st.x, t + 2, M, K, wave, lane, W);
+        wide_round<DT, R>(w, scB, scA, has2 ? t + 2 : -1, st, lut, xs_storage[1] + xa_off, acc);
+        if (has2) vm_wait_le<4 * R>();
+        else vm_wait_all();
         __syncthreads();
     }
 
@@ -527,7 +564,8 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.R = 2;
         p.S = 1;
         p.mmax = M <= 4 ? 4 : 16;
-        p.W = p.mmax == 16 ? 8 : 4;  // the 16-row activation stage is shared by 8 waves
+        // waves sharing one table copy and one activation stage (measured best on MI355X)
+        p.W = p.mmax == 16 ? 16 : 4;
     } else {
         // small layers: split K inside the workgroup to get enough waves
         p.wide = false;
@@ -564,16 +602,9 @@ static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                             hipStream_t stream) {
     if (p.wide) {
         if (p.W == 4 && p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4, 4>(a, wgs, stream);
-        if (p.W == 4 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 4>(a, wgs, stream);
-        if (p.W == 8 && p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4, 8>(a, wgs, stream);
-        if (p.W == 8 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 8>(a, wgs, stream);
-        if (p.W == 8 && p.R == 1 && p.mmax == 4) return launch_wide<DT, 1, 4, 8>(a, wgs, stream);
-        if (p.W == 8 && p.R == 1 && p.mmax == 16) return launch_wide<DT, 1, 16, 8>(a, wgs, stream);
+        if (p.W == 16 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 16>(a, wgs, stream);
         return hipErrorInvalidValue;
     }
-    if (p.R == 4 && p.S == 1) return launch_rs<DT, 4, 1>(a, wgs, stream);
-    if (p.R == 2 && p.S == 1) return launch_rs<DT, 2, 1>(a, wgs, stream);
-    if (p.R == 1 && p.S == 1) return launch_rs<DT, 1, 1>(a, wgs, stream);
     if (p.R == 1 && p.S == 2) return launch_rs<DT, 1, 2>(a, wgs, stream);
     if (p.R == 1 && p.S == 4) return launch_rs<DT, 1, 4>(a, wgs, stream);
     return hipErrorInvalidValue;

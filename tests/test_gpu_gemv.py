@@ -55,10 +55,10 @@ def test_gemv_matches_oracle(dtype, M, N, K):
     assert _rel(y, ref) <= REL_TOL
 
 
-@pytest.mark.parametrize("N", [16 * 512, 16 * 1024, 16 * 2048, 16 * 8192 + 48])
+@pytest.mark.parametrize("N", [16 * 256, 16 * 512, 16 * 1024, 16 * 2048, 16 * 8192 + 48])
 def test_gemv_every_variant(N):
-    # tiles = N/16 selects (R, S): <512 -> (1,4), 512 -> (1,2), 1024 -> (1,1),
-    # 2048 -> (2,1), 8192+ -> (4,1); the last size also has a ragged final tile
+    # tiles = N/16 selects the kernel: < 512 -> K split 4 ways, < 1024 -> K split 2 ways,
+    # >= 1024 -> the streaming (wide) kernel; the last size also has a ragged final tile
     K, M = 256, 16
     pk, sc, pk_np, sc_np = _encoded(N, K, seed=N)
     x = _x(M, K, seed=3, dtype=torch.bfloat16)
