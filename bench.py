@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -79,6 +80,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-encode", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--e2e-layers", type=int, default=32)
     return ap.parse_args()
 
 
@@ -306,6 +309,273 @@ def bench_encode(torch, ops, dev, target_s: float = 0.1):
                 frac_hbm=round(tot_w * 2.25 / tot_ms / 1e6 / HBM_PEAK_GBS, 4))
 
 
+# --------------------------------------------------------------------------- end-to-end decoder
+
+E2E = dict(layers=32, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
+           batch=4, prompt=512, gen=128, lora_rank=8, lora_alpha=16.0, rope_theta=500000.0,
+           eps=1e-5)
+
+
+class E8Decoder:
+    """random-init Llama-3-8B-shaped decoder, every linear (and lm_head)
+    ternary-E8 packed (group 32), rank-8 bf16 LoRA on q/v, RMSNorm and RoPE in bf16.
+    Attention (not part of the E8 path) is computed in fp32 with a pre-transposed K
+    cache; decode steps run the E8 linears as grouped GEMVs (fused q/k/v and gate/up)."""
+
+    def __init__(self, torch, dev, cfg, layers, seed=9500):
+        import ojasx_amd
+        from ojasx_amd.grouped import GroupedGemv
+
+        self.t, self.dev, self.c = torch, dev, cfg
+        self.L = layers
+        H, F_, V = cfg["hidden"], cfg["ffn"], cfg["vocab"]
+        kvd = cfg["kv_heads"] * cfg["head_dim"]
+        bf = torch.bfloat16
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def lin(n_out, n_in, rank=0):
+            m = ojasx_amd.E8LatticeLinear(n_in, n_out, bias=False, rank=rank,
+                                          lora_alpha=cfg["lora_alpha"], group_size=32,
+                                          bitrate=1.5, device=dev, dtype=bf)
+            w = torch.randn(n_out, n_in, generator=g, device=dev) * 0.02
+            pk, sc = ojasx_amd.ops.encode(w, 32)
+            del w
+            m.packed_weight.copy_(pk)
+            m.block_scales.copy_(sc)
+            if rank:
+                with torch.no_grad():
+                    m.lora_A.copy_((torch.randn(n_in, rank, generator=g, device=dev) * 0.02).to(bf))
+                    m.lora_B.copy_((torch.randn(rank, n_out, generator=g, device=dev) * 0.02).to(bf))
+            m.requires_grad_(False)
+            return m
+
+        self.emb = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(bf)
+        self.layers = []
+        for _ in range(layers):
+            self.layers.append(dict(
+                q=lin(H, H, cfg["lora_rank"]), k=lin(kvd, H), v=lin(kvd, H, cfg["lora_rank"]),
+                o=lin(H, H), gate=lin(F_, H), up=lin(F_, H), down=lin(H, F_),
+                n1=torch.ones(H, dtype=bf, device=dev), n2=torch.ones(H, dtype=bf, device=dev)))
+        self.norm = torch.ones(H, dtype=bf, device=dev)
+        self.lm_head = lin(V, H)
+        B = cfg["batch"]
+        for ly in self.layers:  # decode-time grouped launches (planned once for M = batch)
+            ly["qkv_g"] = GroupedGemv.fused([ly["q"], ly["k"], ly["v"]], B, bf)
+            ly["gu_g"] = GroupedGemv.fused([ly["gate"], ly["up"]], B, bf)
+        hd = cfg["head_dim"]
+        Lmax = cfg["prompt"] + cfg["gen"]
+        inv = 1.0 / (cfg["rope_theta"] ** (torch.arange(0, hd, 2, device=dev).float() / hd))
+        ang = torch.arange(Lmax, device=dev).float()[:, None] * inv[None, :]
+        self.cos, self.sin = ang.cos(), ang.sin()  # [Lmax, hd/2] fp32
+        self.Lmax = Lmax
+        self.kt = [torch.zeros(B, cfg["kv_heads"], hd, Lmax, device=dev) for _ in range(layers)]
+        self.vc = [torch.zeros(B, cfg["kv_heads"], Lmax, hd, device=dev) for _ in range(layers)]
+
+    def rms(self, x, w):
+        t = self.t
+        xf = x.float()
+        y = xf * t.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.c["eps"])
+        return y.to(x.dtype) * w
+
+    def rope(self, x, cos, sin):
+        # x [..., heads, hd] (rotate-half form); cos/sin broadcast over heads
+        h = x.shape[-1] // 2
+        xf = x.float()
+        x1, x2 = xf[..., :h], xf[..., h:]
+        return self.t.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
+
+    def lora(self, m, h):
+        return m.scaling * ((h @ m.lora_A) @ m.lora_B)
+
+    # ---- prefill: M = batch * prompt rows through the prefill MFMA GEMM
+    def prefill(self, ids, e8_events=None):
+        t, c = self.t, self.c
+        B, S = ids.shape
+        nh, nkv, hd = c["heads"], c["kv_heads"], c["head_dim"]
+        x = self.emb[ids]  # [B, S, H]
+        cos, sin = self.cos[:S][None, :, None, :], self.sin[:S][None, :, None, :]
+        causal = t.full((S, S), float("-inf"), device=self.dev).triu(1)
+
+        def e8(m, h):
+            if e8_events is None:
+                return m(h)
+            a = t.cuda.Event(enable_timing=True)
+            b = t.cuda.Event(enable_timing=True)
+            a.record()
+            y = m(h)
+            b.record()
+            e8_events.append((a, b))
+            return y
+
+        for li, ly in enumerate(self.layers):
+            h = self.rms(x, ly["n1"])
+            q = e8(ly["q"], h).view(B, S, nh, hd)
+            k = e8(ly["k"], h).view(B, S, nkv, hd)
+            v = e8(ly["v"], h).view(B, S, nkv, hd)
+            q = self.rope(q, cos, sin).permute(0, 2, 1, 3)          # [B, nh, S, hd] fp32
+            k = self.rope(k, cos, sin).permute(0, 2, 1, 3)          # [B, nkv, S, hd]
+            vf = v.float().permute(0, 2, 1, 3)                       # [B, nkv, S, hd]
+            self.kt[li][:, :, :, :S] = k.transpose(-1, -2)
+            self.vc[li][:, :, :S, :] = vf
+            qg = q.reshape(B, nkv, (nh // nkv) * S, hd)               # heads grouped per kv head
+            sc = t.matmul(qg, self.kt[li][:, :, :, :S].contiguous()) / math.sqrt(hd)
+            sc = sc.view(B, nkv, nh // nkv, S, S) + causal
+            o = t.matmul(sc.softmax(-1).view(B, nkv, (nh // nkv) * S, S), vf)
+            o = o.view(B, nh, S, hd).permute(0, 2, 1, 3).reshape(B, S, nh * hd).to(x.dtype)
+            x = x + e8(ly["o"], o)
+            h2 = self.rms(x, ly["n2"])
+            a = t.nn.functional.silu(e8(ly["gate"], h2)) * e8(ly["up"], h2)
+            x = x + e8(ly["down"], a)
+        hl = self.rms(x[:, -1, :], self.norm)
+        return e8(self.lm_head, hl).argmax(-1)
+
+    # ---- the E8 linears of one decode step alone (same shapes; no positions touched)
+    def decode_step_e8_only(self, x):
+        c = self.c
+        for ly in self.layers:
+            ly["qkv_g"](x)
+            a = ly["gu_g"](x)
+            x = x + ly["o"].forward_fused(x) + ly["down"].forward_fused(a[:, : c["ffn"]])
+        return self.lm_head.forward_fused(x)
+
+    # ---- one decode step (M = batch) on static buffers; graph-capturable.  The caller
+    # keeps pos < Lmax (the RoPE tables and the KV cache hold Lmax positions).
+    def decode_step(self, ids, pos):
+        t, c = self.t, self.c
+        B = ids.shape[0]
+        nh, nkv, hd, H = c["heads"], c["kv_heads"], c["head_dim"], c["hidden"]
+        kvd = nkv * hd
+        x = self.emb[ids]  # [B, H]
+        cos = self.cos.index_select(0, pos)[:, None, :]  # [1, 1, hd/2]
+        sin = self.sin.index_select(0, pos)[:, None, :]
+        ar = t.arange(self.Lmax, device=self.dev)
+        mask = t.where(ar <= pos, 0.0, float("-inf"))  # [Lmax]
+        for li, ly in enumerate(self.layers):
+            h = self.rms(x, ly["n1"])
+            qkv = ly["qkv_g"](h)
+            q = qkv[:, :H] + self.lora(ly["q"], h)
+            k = qkv[:, H:H + kvd]
+            v = qkv[:, H + kvd:] + self.lora(ly["v"], h)
+            q = self.rope(q.view(B, nh, hd), cos, sin)            # fp32 [B, nh, hd]
+            k = self.rope(k.view(B, nkv, hd), cos, sin)
+            self.kt[li].index_copy_(3, pos, k.unsqueeze(-1))
+            self.vc[li].index_copy_(2, pos, v.float().view(B, nkv, 1, hd))
+            qg = q.view(B, nkv, nh // nkv, hd)
+            sc = t.matmul(qg, self.kt[li]) / math.sqrt(hd) + mask  # [B, nkv, g, Lmax]
+            o = t.matmul(sc.softmax(-1), self.vc[li]).reshape(B, H).to(x.dtype)
+            x = x + ly["o"].forward_fused(o)
+            h2 = self.rms(x, ly["n2"])
+            gu = ly["gu_g"](h2)
+            a = t.nn.functional.silu(gu[:, : c["ffn"]]) * gu[:, c["ffn"]:]
+            x = x + ly["down"].forward_fused(a)
+        logits = self.lm_head.forward_fused(self.rms(x, self.norm))
+        nxt = logits.argmax(-1)
+        ids.copy_(nxt)
+        pos.add_(1)
+        return nxt
+
+
+def bench_e2e(torch, dev, layers: int):
+    """batch 4, 512 random prompt tokens, 128 greedy steps.  Decode steps are
+    replayed from one captured hipGraph; the E8 linears of a decode step are also timed
+    alone (a second graph holding only them, on the same buffers)."""
+    c = E2E
+    t0 = time.time()
+    model = E8Decoder(torch, dev, c, layers)
+    torch.cuda.synchronize()
+    build_s = time.time() - t0
+    g = torch.Generator(device=dev).manual_seed(9501)
+    B, S, G = c["batch"], c["prompt"], c["gen"]
+    prompt = torch.randint(0, c["vocab"], (B, S), generator=g, device=dev)
+    stream = torch.cuda.current_stream()
+
+    # warm-up prefill (also first token), then the timed prefill
+    model.prefill(prompt)
+    torch.cuda.synchronize()
+    ev = []
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    first = model.prefill(prompt, e8_events=ev)
+    b.record(stream)
+    torch.cuda.synchronize()
+    prefill_ms = a.elapsed_time(b)
+    prefill_e8_ms = sum(x.elapsed_time(y) for x, y in ev)
+
+    if S + G > model.Lmax:
+        raise RuntimeError("prompt + generated tokens exceed the KV cache")
+    ids = first.clone()
+    pos = torch.full((1,), S, dtype=torch.long, device=dev)
+    # eager reference of the first 4 decode steps (for the graph check)
+    eager = []
+    for _ in range(4):
+        eager.append(model.decode_step(ids, pos).clone())
+    torch.cuda.synchronize()
+
+    cap = torch.cuda.Stream()
+    ids.copy_(first)
+    pos.fill_(S)
+    with torch.cuda.stream(cap):  # warm-up on the capture stream
+        model.decode_step(ids, pos)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    ids.copy_(first)
+    pos.fill_(S)
+    with torch.cuda.graph(graph, stream=cap):
+        model.decode_step(ids, pos)
+    torch.cuda.synchronize()
+
+    # graph replays must reproduce the eager tokens (the KV cache rows are rewritten)
+    ids.copy_(first)
+    pos.fill_(S)
+    graph_tokens = []
+    for _ in range(4):
+        graph.replay()
+        graph_tokens.append(ids.clone())
+    torch.cuda.synchronize()
+    match = all(bool((x == y).all()) for x, y in zip(eager, graph_tokens))
+
+    ids.copy_(first)
+    pos.fill_(S)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(G):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    decode_ms = a.elapsed_time(b)
+
+    # the E8 linears of one decode step, alone, on a static [batch, hidden] input
+    xin = (torch.randn(B, c["hidden"], generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    with torch.cuda.stream(cap):
+        model.decode_step_e8_only(xin)
+    torch.cuda.synchronize()
+    g_e8 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_e8, stream=cap):
+        model.decode_step_e8_only(xin)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(G):
+        g_e8.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    decode_e8_ms = a.elapsed_time(b)
+    wbytes = sum(weight_bytes(m.out_features, m.in_features) for ly in model.layers
+                 for m in (ly["q"], ly["k"], ly["v"], ly["o"], ly["gate"], ly["up"], ly["down"]))
+    wbytes += weight_bytes(model.lm_head.out_features, model.lm_head.in_features)
+    return dict(
+        layers=layers, batch=B, prompt=S, generated=G, build_s=round(build_s, 1),
+        prefill_ms=round(prefill_ms, 2), prefill_tokens_s=round(B * S / prefill_ms * 1e3, 1),
+        prefill_e8_linear_ms=round(prefill_e8_ms, 2),
+        decode_ms=round(decode_ms, 2), decode_tokens_s=round(B * G / decode_ms * 1e3, 1),
+        decode_ms_per_step=round(decode_ms / G, 3),
+        decode_e8_linear_ms=round(decode_e8_ms, 2),
+        decode_e8_weight_GBs=round(wbytes * G / decode_e8_ms / 1e6, 1),
+        total_tokens_s=round(B * (S + G) / (prefill_ms + decode_ms) * 1e3, 1),
+        graph_replay_matches_eager=match,
+        lm_head="E8-packed (128256 x 4096)", attention="fp32 math, pre-transposed K cache")
+
+
 # --------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(seconds: float):
@@ -439,6 +709,12 @@ def main() -> int:
         log("encode timing")
         result["encode"] = bench_encode(torch, ops, dev)
         log(f"encode: {result['encode']['Gweights_s']} Gweights/s")
+    if not args.no_e2e:
+        torch.cuda.empty_cache()
+        log(f"end-to-end decoder ({args.e2e_layers} layers)")
+        result["e2e"] = bench_e2e(torch, dev, args.e2e_layers)
+        log(f"e2e: decode {result['e2e']['decode_tokens_s']} tok/s, prefill "
+            f"{result['e2e']['prefill_tokens_s']} tok/s")
     if not args.no_cpu_baseline:
         log(f"cpu baseline ({args.cpu_seconds:.0f} s sample)")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
