@@ -37,9 +37,17 @@ COMMON = ["-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
           "-fvisibility=hidden", "-Wall", "-Wno-unused-function"] + DEVICE_FLAGS
 
 
+# Per-file code generation options.  The decode GEMV keeps its MFMA results in ordinary
+# VGPRs: its post-scaled kernel reads every result with VALU FMAs, and the accumulator
+# register form would add a v_accvgpr_read per read and raise the register total.
+EXTRA = {
+    "e8t_gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC] + COMMON + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC] + COMMON + EXTRA.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

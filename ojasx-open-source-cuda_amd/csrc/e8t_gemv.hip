@@ -276,6 +276,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
 // buffered in registers one round ahead; one workgroup barrier per round.
 
 constexpr int kRound = 1024;                      // K per round
+// Post-scaled kernel: tile groups per workgroup.  Measured on MI355X (32-layer decode
+// stack, M = 1): 1 -> 3.7-3.8 TB/s, 2 -> 3.5, 4 -> 3.3, 8 -> 2.9; longer workgroups save
+// table fills and prologue latency but leave a longer tail of partly idle CUs.
+constexpr int kPsChunk = 1;
 constexpr uint32_t kXRow = kRound * 2 + 16;       // bytes per padded activation row in LDS
 
 template <int R>
@@ -537,6 +541,278 @@ __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
     }
 }
 
+// ------------------------------------------------------------------------- post-scaled kernel
+//
+// Streaming kernel for M <= 4 (token-by-token decode).  Same rounds, code and scale
+// streams as the wide kernel, but the table holds the coordinates themselves (+-1, 0 in
+// the activation dtype) and the group scale multiplies fp32 partial sums instead of every
+// decoded weight:
+//
+//   A row a = 4*g' + m carries activation row m, but only in the k slots of lane group
+//   g' (lanes whose A row does not match their lane group read a zero block), so
+//   D[4g' + m][n] = sum over lane group g''s 8 k of one step = the contribution of ONE
+//   scale group (lane group g' at step j covers k = 1024u + 256g' + 8j, group 8g' + j/4).
+//   In the MFMA output layout lane (g', n) holds D rows 4g' + q, i.e. exactly the partials
+//   of its own codes for activation rows q = 0..3.  Four steps (one scale group) accumulate
+//   into D; then acc[q] += s(n, group) * D[q], with the scale this lane already holds.
+//
+// The sum over the four lane groups of a row is formed once, at the end.  Per code this
+// removes the four mask ANDs and the scale-word packing of the wide kernel; the weights are
+// still coord * scale in the activation dtype's rule (bf16: bf16_rne(s16)), applied in fp32.
+
+// Keeps all four result registers of an MFMA allocated up to this point.  With M == 1 only
+// result 0 is read; the compiler would otherwise hand the other three registers to VALU
+// code right after the MFMA issues, while the MFMA may still write them back (observed:
+// corrupted code registers and wrong outputs on gfx950).  The empty asm takes the
+// post-scale FMA's result as well, so it sits after the FMA that reads the MFMA result:
+// by then the write-back has landed and the registers may be reused.
+__device__ __forceinline__ void keep_mfma_result(const f32x4& d, float& consumer) {
+    asm volatile("" : "+v"(consumer) : "v"(d));
+}
+
+// Step J of a post-scaled round; d[r] accumulates the current scale group of tile r.
+template <int DT, int R, int MM, int J>
+__device__ __forceinline__ void ps_step(WideCodes<R>& w, const WideScales<R>& sc,
+                                        WideScales<R>& sc_next, int64_t u_next,
+                                        const WideStream<R>& st, const char* lut,
+                                        const char* xa_base, uint4& xa_cur, uint2 (&ml)[R],
+                                        uint2 (&mh)[R], float (&sf)[R][2], f32x4 (&d)[R],
+                                        float (&acc)[R][MM]) {
+    if constexpr (J == 0) {
+        if (u_next >= 0) load_scales<R>(sc_next, u_next, st);
+    }
+    if constexpr (J % 4 == 0 && J > 0) {
+        // scale group J/4 - 1 is complete in d
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int q = 0; q < MM; ++q)
+                acc[r][q] = __builtin_fmaf(d[r][q], sf[r][(J / 4 - 1) & 1], acc[r][q]);
+            keep_mfma_result(d[r], acc[r][0]);
+        }
+    }
+    if constexpr (J % 8 == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) scale_pair_f32<DT>(sc.sc[r][J / 8], sf[r][0], sf[r][1]);
+    }
+    uint4 xa_nxt;
+    uint2 ml_n[R], mh_n[R];
+    if constexpr (J + 1 < 32) {
+        xa_nxt = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + 1));
+        wide_lut<R, J + 1>(w, lut, st.slot, ml_n, mh_n);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint4 b = make_uint4(ml[r].x, ml[r].y, mh[r].x, mh[r].y);
+        d[r] = mfma16<DT>(xa_cur, b, J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[r]);
+    }
+    if constexpr (J == 10 || J == 21 || J == 31) {
+        if (u_next >= 0) load_code_piece<R>(w, J == 10 ? 0 : (J == 21 ? 1 : 2), u_next, st);
+    }
+    if constexpr (J + 1 < 32) {
+        xa_cur = xa_nxt;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ml[r] = ml_n[r];
+            mh[r] = mh_n[r];
+        }
+    }
+    if constexpr (J == 31) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int q = 0; q < MM; ++q)
+                acc[r][q] = __builtin_fmaf(d[r][q], sf[r][1], acc[r][q]);
+            keep_mfma_result(d[r], acc[r][0]);
+        }
+    }
+}
+
+template <int DT, int R, int MM, int... J>
+__device__ __forceinline__ void ps_steps(WideCodes<R>& w, const WideScales<R>& sc,
+                                         WideScales<R>& sc_next, int64_t u_next,
+                                         const WideStream<R>& st, const char* lut,
+                                         const char* xa_base, uint4& xa, uint2 (&ml)[R],
+                                         uint2 (&mh)[R], float (&sf)[R][2], f32x4 (&d)[R],
+                                         float (&acc)[R][MM], std::integer_sequence<int, J...>) {
+    (ps_step<DT, R, MM, J>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sf, d, acc),
+     ...);
+}
+
+template <int DT, int R, int MM>
+__device__ __forceinline__ void ps_round(WideCodes<R>& w, const WideScales<R>& sc,
+                                         WideScales<R>& sc_next, int64_t u_next,
+                                         const WideStream<R>& st, const char* lut,
+                                         const char* xa_base, float (&acc)[R][MM]) {
+    uint4 xa = *reinterpret_cast<const uint4*>(xa_base);
+    uint2 ml[R], mh[R];
+    float sf[R][2];
+    f32x4 d[R];
+    wide_lut<R, 0>(w, lut, st.slot, ml, mh);
+    ps_steps<DT, R, MM>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sf, d, acc,
+                        std::make_integer_sequence<int, 32>{});
+}
+
+// Moves a stream `rows` rows further down its weight buffers (a later tile group).
+template <int R>
+__device__ __forceinline__ void ps_shift(WideStream<R>& st, int64_t rows, uint32_t rowbytes,
+                                         uint32_t srowbytes) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        st.vo_code[r] += (uint32_t)rows * rowbytes;
+        st.vo_scale[r] += (uint32_t)rows * srowbytes;
+    }
+}
+
+// Sums the four lane groups of each row and stores one tile group's outputs (lane group q
+// stores activation row q); clears the accumulators.
+template <int DT, int R, int MM>
+__device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M, int64_t tile0,
+                                         int lane, float (&acc)[R][MM]) {
+    const int g = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = (tile0 + r) * 16 + i16;
+        float out = 0.f;
+#pragma unroll
+        for (int q = 0; q < MM; ++q) {
+            float v = acc[r][q];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (q == g) out = v;
+            acc[r][q] = 0.f;
+        }
+        if (row < job.N && g < M) {
+            const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
+            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out + bv);
+        }
+    }
+}
+
+// MM: activation rows handled (1 or 4; M <= MM); W: waves per workgroup.  A workgroup
+// runs args.chunk consecutive tile groups (W * R row tiles each) of one job, one
+// code/scale/activation prefetch pipeline across the tile-group boundaries, and fills its
+// table once.  Tile group c of the workgroup reads rows 16 W R c further down the same
+// buffers: the shift is a wave-uniform offset.
+template <int DT, int R, int MM, int W>
+__global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
+    static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
+    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ __attribute__((aligned(16))) char xs_storage[2][MM * kXRow];
+    __shared__ __attribute__((aligned(16))) uint4 xzero[32];  // A rows outside a lane's group
+
+    fill_lut(lut_storage, LutValues<DT>());
+    if (threadIdx.x < 32) xzero[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+
+    int64_t wg = blockIdx.x;
+    GemvJob job;
+    if (args.jobs != nullptr) {
+        job = args.jobs[find_job(args.jobs, args.njobs, wg)];
+    } else {
+        job = args.inl[0];
+#pragma unroll
+        for (int i = 1; i < kGemvInlineJobs; ++i)
+            if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
+    }
+    wg -= job.wg_begin;
+    const void* xbase = job.x ? job.x : args.x;
+    void* ybase = job.y ? job.y : args.y;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
+    const int64_t N = job.N, K = job.K;
+    const int M = args.M;
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
+    const uint32_t srowbytes = (uint32_t)(K / 16);
+    constexpr int64_t kGroupRows = 16 * W * R;
+    // tile groups of this workgroup: [c0, c1) of the job
+    const int64_t groups = (N + kGroupRows - 1) / kGroupRows;
+    const int64_t c0 = wg * args.chunk;
+    const int64_t c1 = c0 + args.chunk < groups ? c0 + args.chunk : groups;
+    const int64_t tile0 = (c0 * W + wave) * R;  // first row tile, tile group c0
+
+    WideStream<R> st;
+    st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
+                                                  (int)(N * rowbytes), kRsrcWord3);
+    st.scales = __builtin_amdgcn_make_buffer_rsrc((void*)job.scales, (short)0,
+                                                  (int)(N * srowbytes), kRsrcWord3);
+    st.x = __builtin_amdgcn_make_buffer_rsrc((void*)xbase, (short)0, (int)(M * K * 2),
+                                             kRsrcWord3);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
+        st.vo_code[r] = row * rowbytes + 48u * g;
+        st.vo_scale[r] = row * srowbytes + 16u * g;
+    }
+    st.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+    st.K = K;
+    st.g = g;
+    // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
+    const int am = i16 & 3;
+    const bool a_live = (i16 >> 2) == g && am < M;
+    const char* xa0 = a_live ? xs_storage[0] + am * kXRow + 512 * g
+                             : reinterpret_cast<const char*>(xzero);
+    const char* xa1 = a_live ? xs_storage[1] + am * kXRow + 512 * g
+                             : reinterpret_cast<const char*>(xzero);
+
+    // Items are (tile group c0 + c, round u), c-major; item (c, u) is processed while the
+    // next item's codes, scales and activations are fetched.
+    const int T = (int)((K + kRound - 1) / kRound);
+    const int ngroups = (int)(c1 - c0);
+    float acc[R][MM];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < MM; ++q) acc[r][q] = 0.f;
+
+    WideCodes<R> w;
+    WideScales<R> scA, scB;
+    load_code_piece<R>(w, 0, 0, st);
+    load_code_piece<R>(w, 1, 0, st);
+    load_code_piece<R>(w, 2, 0, st);
+    load_scales<R>(scA, 0, st);
+    stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
+    vm_wait_all();
+    __syncthreads();  // table, zero block and round-0 activations ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+
+    int c = 0, u = 0;
+    for (;;) {
+        {
+            const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
+            const bool has = cn < ngroups;
+            WideStream<R> sn = st;
+            ps_shift<R>(sn, (int64_t)cn * kGroupRows, rowbytes, srowbytes);
+            if (has) stage_x(xs_storage[1], st.x, un, M, K, wave, lane, W);
+            ps_round<DT, R, MM>(w, scA, scB, has ? un : -1, sn, lut, xa0, acc);
+            if (has) vm_wait_le<4 * R>();
+            else vm_wait_all();
+            __syncthreads();
+            if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0 + (int64_t)c * W * R, lane, acc);
+            if (!has) break;
+            c = cn;
+            u = un;
+        }
+        {
+            const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
+            const bool has = cn < ngroups;
+            WideStream<R> sn = st;
+            ps_shift<R>(sn, (int64_t)cn * kGroupRows, rowbytes, srowbytes);
+            if (has) stage_x(xs_storage[0], st.x, un, M, K, wave, lane, W);
+            ps_round<DT, R, MM>(w, scB, scA, has ? un : -1, sn, lut, xa1, acc);
+            if (has) vm_wait_le<4 * R>();
+            else vm_wait_all();
+            __syncthreads();
+            if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0 + (int64_t)c * W * R, lane, acc);
+            if (!has) break;
+            c = cn;
+            u = un;
+        }
+    }
+}
+
 // ------------------------------------------------------------------------- host side
 
 bool gemv_shape_ok(int64_t N, int64_t K) {
@@ -561,14 +837,18 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
     if (total_tiles >= 1024) {
         // enough row tiles to fill the GPU with one tile set per wave: streaming kernel
         p.wide = true;
-        p.R = 2;
         p.S = 1;
-        p.mmax = M <= 4 ? 4 : 16;
+        // M <= 4: post-scaled kernel (mmax 1 or 4); otherwise the mask kernel
+        p.mmax = M == 1 ? 1 : (M <= 4 ? 4 : 16);
+        p.R = 2;
+        // post-scaled kernel: consecutive tile groups per workgroup
+        p.C = p.mmax == 16 ? 1 : kPsChunk;
         // waves sharing one table copy and one activation stage (measured best on MI355X)
         p.W = p.mmax == 16 ? 16 : 4;
     } else {
         // small layers: split K inside the workgroup to get enough waves
         p.wide = false;
+        p.C = 1;
         p.R = 1;
         p.S = total_tiles >= 512 ? 2 : 4;
         p.W = 4;
@@ -579,7 +859,7 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
 
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p) {
     const int64_t tiles = (N + 15) / 16;
-    const int64_t per_wg = p.wide ? (int64_t)p.W * p.R : (int64_t)(4 / p.S) * p.R;
+    const int64_t per_wg = p.wide ? (int64_t)p.W * p.R * p.C : (int64_t)(4 / p.S) * p.R;
     return (tiles + per_wg - 1) / per_wg;
 }
 
@@ -597,11 +877,22 @@ static hipError_t launch_wide(const GemvLaunch& a, int64_t wgs, hipStream_t stre
     return hipGetLastError();
 }
 
+template <int DT, int R, int MM, int W>
+static hipError_t launch_ps(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
+                            hipStream_t stream) {
+    GemvLaunch l = a;
+    l.chunk = p.C;
+    hipLaunchKernelGGL((gemv_ps_kernel<DT, R, MM, W>), dim3((unsigned)wgs), dim3(64 * W), 0,
+                       stream, l);
+    return hipGetLastError();
+}
+
 template <int DT>
 static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                             hipStream_t stream) {
     if (p.wide) {
-        if (p.W == 4 && p.R == 2 && p.mmax == 4) return launch_wide<DT, 2, 4, 4>(a, wgs, stream);
+        if (p.W == 4 && p.R == 2 && p.mmax == 1) return launch_ps<DT, 2, 1, 4>(a, p, wgs, stream);
+        if (p.W == 4 && p.R == 2 && p.mmax == 4) return launch_ps<DT, 2, 4, 4>(a, p, wgs, stream);
         if (p.W == 16 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 16>(a, wgs, stream);
         return hipErrorInvalidValue;
     }

@@ -49,6 +49,7 @@ struct GemvLaunch {
     void* y;                       // default output
     int njobs;
     int M;
+    int chunk;                     // post-scaled kernel: tile groups per workgroup
 };
 
 bool gemv_shape_ok(int64_t N, int64_t K);
@@ -60,7 +61,8 @@ struct GemvPlan {
     int R;       // 16-row tiles per wave
     int S;       // K split ways inside the workgroup (non-wide only)
     int W;       // waves per workgroup (wide only)
-    int mmax;    // activation rows staged in LDS (wide only): 4 or 16
+    int mmax;    // activation rows staged in LDS (wide only): 1, 4 (post-scaled) or 16
+    int C;       // consecutive tile groups per workgroup (post-scaled kernel; else 1)
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);

@@ -33,14 +33,28 @@ __device__ __forceinline__ int uniform_offset(int64_t v) {
     return __builtin_amdgcn_readfirstlane((int)v);
 }
 
-__device__ __forceinline__ uint32_t lut_mask_half(int digit) {
-    return digit == 0 ? 0xFFFFu : (digit == 1 ? 0x0000u : 0x7FFFu);
-}
+// Mask table half-word of base-3 digit d (coord d - 1).
+struct LutMasks {
+    __device__ uint32_t operator()(int d) const {
+        return d == 0 ? 0xFFFFu : (d == 1 ? 0x0000u : 0x7FFFu);
+    }
+};
+
+// Value table half-word: coord d - 1 itself in the activation dtype (+-1.0 or 0), for
+// kernels that apply the group scale to fp32 partial sums after the MFMA.
+template <int DT>
+struct LutValues {
+    __device__ uint32_t operator()(int d) const {
+        const uint32_t one = DT == kBF16 ? 0x3F80u : 0x3C00u;
+        return d == 0 ? (one | 0x8000u) : (d == 1 ? 0x0000u : one);
+    }
+};
 
 // Fills the bank-sliced table: entry e, slice c at byte offset (e + 1) * kLutStride + c * 8
 // of the storage; entry -1 is a zero guard (with kHiMagic, the lo address of an invalid
 // code >= 3281 can reach 8 bytes below entry 0; valid codes never do).
-__device__ __forceinline__ void fill_lut(uint2* storage) {
+template <typename Half = LutMasks>
+__device__ __forceinline__ void fill_lut(uint2* storage, Half half = Half()) {
     for (int i = threadIdx.x; i < (kLutEntries + 1) * kLutSlots; i += blockDim.x) {
         const int e = i / kLutSlots - 1;
         if (e < 0) {
@@ -48,8 +62,7 @@ __device__ __forceinline__ void fill_lut(uint2* storage) {
             continue;
         }
         const int d0 = e % 3, d1 = (e / 3) % 3, d2 = (e / 9) % 3, d3 = (e / 27) % 3;
-        storage[i] = make_uint2(lut_mask_half(d0) | (lut_mask_half(d1) << 16),
-                                lut_mask_half(d2) | (lut_mask_half(d3) << 16));
+        storage[i] = make_uint2(half(d0) | (half(d1) << 16), half(d2) | (half(d3) << 16));
     }
 }
 
@@ -92,6 +105,22 @@ __device__ __forceinline__ void scale_words(uint32_t sc, uint32_t& w0, uint32_t&
     }
     w0 = __builtin_amdgcn_perm(p, p, 0x01000100u) | 0x80008000u;
     w1 = __builtin_amdgcn_perm(p, p, 0x03020302u) | 0x80008000u;
+}
+
+// Two group scales (fp16 bits, packed) as fp32 multipliers in the activation dtype's
+// rule (bf16: bf16_rne(float(s16)), lattice.py:414-418; fp16: exact).
+template <int DT>
+__device__ __forceinline__ void scale_pair_f32(uint32_t sc, float& s0, float& s1) {
+    const float f0 = f16_bits_to_f32(sc & 0xFFFFu), f1 = f16_bits_to_f32(sc >> 16);
+    if constexpr (DT == kBF16) {
+        const uint32_t p = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f0) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f1) << 16);
+        s0 = __uint_as_float(p << 16);
+        s1 = __uint_as_float(p & 0xFFFF0000u);
+    } else {
+        s0 = f0;
+        s1 = f1;
+    }
 }
 
 template <int DT>
