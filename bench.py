@@ -82,6 +82,13 @@ def parse_args():
     ap.add_argument("--no-encode", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-layers", type=int, default=32)
+    ap.add_argument("--decode-m", type=str, default=",".join(map(str, DECODE_M)),
+                    help="decode batch sizes of the headline step (profiling runs pick one)")
+    ap.add_argument("--no-per-linear", action="store_true",
+                    help="skip the per-linear hipGraph timing beside the headline")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run three device-to-device copies of this many MiB (the "
+                         "known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
@@ -104,11 +111,11 @@ def build_stack(torch, ops, layers: int, dev):
     return stack
 
 
-def check_decode_outputs(torch, ops, stack, xs, ys, dev) -> float:
+def check_decode_outputs(torch, ops, stack, xs, ys, dev, Ms) -> float:
     """Max relative error of sampled GEMV outputs against a torch fp32 matmul of
     the decoded (bf16-rule) weights; a sanity check of what was timed."""
     worst = 0.0
-    for M in DECODE_M:
+    for M in Ms:
         for idx in (0, 4, 6):  # q, gate, down of layer 0
             s = stack[idx]
             w = ops.decode(s["packed"], s["scales"], s["N"] * s["K"], GS, torch.bfloat16)
@@ -121,7 +128,48 @@ def check_decode_outputs(torch, ops, stack, xs, ys, dev) -> float:
 
 # --------------------------------------------------------------------------- decode GEMV
 
-def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
+def _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes):
+    """The stack's GEMVs as one launch per linear, replayed from one hipGraph per M."""
+    stream = torch.cuda.current_stream()
+
+    def launch_all(M, stream_handle):
+        for i, s in enumerate(stack):
+            st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
+                                      s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
+                                      s["N"], s["K"], GS, N_.BF16, stream_handle)
+            N_.check(st, "gemm_fwd")
+
+    for M in Ms:
+        launch_all(M, stream.cuda_stream)
+    torch.cuda.synchronize()
+    graphs = {}
+    cap_stream = torch.cuda.Stream()
+    for M in Ms:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap_stream):
+            launch_all(M, torch.cuda.current_stream().cuda_stream)
+        graphs[M] = g
+    for M in Ms:
+        graphs[M].replay()
+    torch.cuda.synchronize()
+    per_linear = {}
+    for M in Ms:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            graphs[M].replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / steps
+        per_linear[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
+                                  frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                  launches=len(stack))
+    return per_linear
+
+
+def bench_decode(torch, N_, stack, steps: int, warmup: int, dev, Ms=DECODE_M,
+                 per_linear_too: bool = True):
     """Headline: one grouped launch per M over every linear of the stack.  Also timed
     (reported beside it): the same GEMVs as one launch per linear, replayed from a
     hipGraph per M."""
@@ -129,7 +177,7 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
 
     lib = N_.lib()
     xs, ys = {}, {}
-    for M in DECODE_M:
+    for M in Ms:
         for K in (4096, 14336):
             g = torch.Generator(device=dev).manual_seed(8300 + M + K)
             xs[(M, K)] = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
@@ -137,7 +185,7 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
             ys[(M, i)] = torch.empty(M, s["N"], dtype=torch.bfloat16, device=dev)
 
     plans = {}
-    for M in DECODE_M:
+    for M in Ms:
         xk = {K: xs[(M, K)] for K in (4096, 14336)}
         yl = [ys[(M, i)] for i in range(len(stack))]
         plans[M] = GroupedGemv(stack_jobs(stack, xk, yl), M, torch.bfloat16, dev,
@@ -145,19 +193,19 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
 
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
-        for M in DECODE_M:
+        for M in Ms:
             plans[M]()
     torch.cuda.synchronize()
 
     # ---- timed region: exactly `steps` steps, synchronised on both sides
-    ev = {M: [] for M in DECODE_M}
+    ev = {M: [] for M in Ms}
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()  # barrier + sync (N=1: no other ranks)
     wall0 = time.perf_counter()
     t_start.record(stream)
     for _ in range(steps):
-        for M in DECODE_M:
+        for M in Ms:
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
@@ -173,7 +221,7 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
     per_m = {}
     alg_bytes_region = 0
     kernel_ms_region = 0.0
-    for M in DECODE_M:
+    for M in Ms:
         ms = sum(a.elapsed_time(b) for a, b in ev[M]) / steps
         act = sum(M * s["K"] * 2 + M * s["N"] * 2 for s in stack)
         per_m[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
@@ -181,46 +229,16 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev):
                              grid=plans[M].grid)
         alg_bytes_region += (wbytes + act) * steps
         kernel_ms_region += ms * steps
-    err = check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys, dev)
+    err = check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys, dev, Ms)
 
-    # ---- beside it: one launch per linear, replayed from one hipGraph per M
-    def launch_all(M, stream_handle):
-        for i, s in enumerate(stack):
-            st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
-                                      s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
-                                      s["N"], s["K"], GS, N_.BF16, stream_handle)
-            N_.check(st, "gemm_fwd")
-
-    for M in DECODE_M:
-        launch_all(M, stream.cuda_stream)
-    torch.cuda.synchronize()
-    graphs = {}
-    cap_stream = torch.cuda.Stream()
-    for M in DECODE_M:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cap_stream):
-            launch_all(M, torch.cuda.current_stream().cuda_stream)
-        graphs[M] = g
-    for M in DECODE_M:
-        graphs[M].replay()
-    torch.cuda.synchronize()
     per_linear = {}
-    for M in DECODE_M:
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(steps):
-            graphs[M].replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / steps
-        per_linear[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
-                                  frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-                                  launches=len(stack))
-    err = max(err, check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys, dev))
+    if per_linear_too:
+        per_linear = _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes)
+        err = max(err, check_decode_outputs(torch, __import__("ojasx_amd").ops, stack, xs, ys,
+                                            dev, Ms))
     return dict(total_ms=total_ms, wall_s=wall, wbytes=wbytes, per_m=per_m,
                 per_linear=per_linear, alg_bytes=alg_bytes_region, kernel_ms=kernel_ms_region,
-                launches=len(DECODE_M) * steps, max_rel_err=err)
+                launches=len(Ms) * steps, max_rel_err=err)
 
 
 # --------------------------------------------------------------------------- prefill GEMM
@@ -647,14 +665,27 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe_mib > 0:
+        # reads n bytes and writes n bytes per launch: torch's elementwise negation
+        n = args.copy_probe_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n,
+                          "launches": 3, "kernel": "torch.neg (elementwise) fp32"}), flush=True)
+        return 0
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
 
     stack = build_stack(torch, ops, args.layers, dev)
     log("decode GEMV timing")
-    dec = bench_decode(torch, N_, stack, args.steps, args.warmup, dev)
+    decode_mlist = tuple(int(m) for m in args.decode_m.split(",") if m)
+    dec = bench_decode(torch, N_, stack, args.steps, args.warmup, dev, decode_mlist,
+                       per_linear_too=not args.no_per_linear)
     ms_per_step = dec["total_ms"] / args.steps
-    value = dec["wbytes"] * len(DECODE_M) / ms_per_step / 1e6  # GB/s
+    value = dec["wbytes"] * len(decode_mlist) / ms_per_step / 1e6  # GB/s
     achieved = dec["alg_bytes"] / dec["kernel_ms"] / 1e6
     log(f"decode: {ms_per_step:.3f} ms/step, {value:.1f} GB/s weights, "
         f"rel err {dec['max_rel_err']:.2e}")
@@ -680,13 +711,13 @@ def main() -> int:
                          "covering every linear of the stack (per-linear launches from a "
                          "hipGraph are reported under decode.per_linear)"),
             "layers": args.layers,
-            "decode_M": list(DECODE_M),
+            "decode_M": list(decode_mlist),
             "group_size": GS,
             "stack_weight_bytes": dec["wbytes"],
             "parallelism": "single GPU",
         },
         "decode": dict(per_M=dec["per_m"], per_linear=dec["per_linear"],
-                       max_rel_err=dec["max_rel_err"], launches_per_step=len(DECODE_M)),
+                       max_rel_err=dec["max_rel_err"], launches_per_step=len(decode_mlist)),
         "roofline": {
             "bound": "hbm",
             "kernel": "ojx e8t decode GEMV",

@@ -213,11 +213,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     int64_t M, int64_t N, int64_t K) {
-    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ uint4 lut_storage[kLutStorageU4];
     __shared__ __attribute__((aligned(16))) char xs[2][kTileBytes];
     __shared__ __attribute__((aligned(16))) char ws[2][kTileBytes];
 
-    fill_lut(lut_storage);
+    fill_lut<kGemmThreads>(lut_storage, kLutMasks);
 
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
     const int64_t tm_n = (M + kBM - 1) / kBM, tn_n = (N + kBN - 1) / kBN;
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
     load_x_tile(xs[0], xr, m0, 0, K, wave, lane);
     load_codes_row(rc, pr, sr, vo_code, vo_scale, 0);
     __syncthreads();  // table ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
     decode_half<DT>(rc, lut, slot, ws[0], wrow, half);
     load_codes_row(rc, pr, sr, vo_code, vo_scale, kBK);
     __builtin_amdgcn_s_waitcnt(0x0F70);

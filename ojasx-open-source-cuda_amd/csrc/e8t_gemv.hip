@@ -21,9 +21,9 @@
 // halves, each looked up in an 81-entry LDS table of 4 masks (8 bytes: 0xFFFF for
 // -1, 0x0000 for 0, 0x7FFF for +1 per half-word).  AND-ing a mask word with
 // (s | s<<16 | 0x80008000) yields the bf16 (or fp16) pair coord*s exactly, since
-// s >= 0.  hi = floor(2c/81) is one mul_hi (exact for every 12-bit input, checked
-// exhaustively).  The table is "bank sliced": 16 copies, copy c occupying only
-// bank pair c, so the 16 lanes of each ds_read_b64 phase never conflict.
+// s >= 0.  hi = floor(2c/81) is one mul_hi (exact for every valid code, checked
+// exhaustively).  The table is "bank sliced" (e8t_lut.h): lane l reads copy
+// l % kLutSlots, which occupies only its own bank pair.
 //
 // Grouped launches: one launch may run many independent linears (a job table in
 // device memory), e.g. a decoder's q/k/v projections that share x, or a whole
@@ -156,10 +156,10 @@ __device__ __forceinline__ int find_job(const GemvJob* jobs, int njobs, int64_t 
 // the workgroup's 4 waves are (4/S) tile sets x S K ranges, reduced through LDS.
 template <int DT, int R, int S>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
-    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ uint4 lut_storage[kLutStorageU4];
     __shared__ f32x4 red[(S > 1) ? (kGemvThreads / 64) * R * 64 : 1];
 
-    fill_lut(lut_storage);
+    fill_lut<kGemvThreads>(lut_storage, kLutMasks);
 
     int64_t wg = blockIdx.x;
     GemvJob job;
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
         for (int j = 0; j < 8; ++j) load_x(xa[j], c0, j, st);
     }
     __syncthreads();  // LUT ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
 
     for (int64_t c = c0; c < c1; c += 2) {
         const bool has1 = c + 1 < c1, has2 = c + 2 < c1;
@@ -279,7 +279,26 @@ constexpr int kRound = 1024;                      // K per round
 // Post-scaled kernel: tile groups per workgroup.  Measured on MI355X (32-layer decode
 // stack, M = 1): 1 -> 3.7-3.8 TB/s, 2 -> 3.5, 4 -> 3.3, 8 -> 2.9; longer workgroups save
 // table fills and prologue latency but leave a longer tail of partly idle CUs.
-constexpr int kPsChunk = 1;
+#ifndef OJX_PS_CHUNK
+#define OJX_PS_CHUNK 1
+#endif
+constexpr int kPsChunk = OJX_PS_CHUNK;
+// Waves per workgroup of the post-scaled kernel.
+#ifndef OJX_PS_WAVES
+#define OJX_PS_WAVES 4
+#endif
+constexpr int kPsWaves = OJX_PS_WAVES;
+// Row tiles (16 rows) per wave of the post-scaled kernel.
+#ifndef OJX_PS_TILES
+#define OJX_PS_TILES 2
+#endif
+constexpr int kPsTiles = OJX_PS_TILES;
+// Optional occupancy request for the post-scaled kernel (waves per SIMD), e.g. 5.
+#ifdef OJX_PS_MIN_WAVES
+#define OJX_PS_OCC __attribute__((amdgpu_waves_per_eu(OJX_PS_MIN_WAVES)))
+#else
+#define OJX_PS_OCC
+#endif
 constexpr uint32_t kXRow = kRound * 2 + 16;       // bytes per padded activation row in LDS
 
 template <int R>
@@ -444,10 +463,10 @@ __device__ __forceinline__ void vm_wait_le() {
 // W: waves per workgroup (they share the table and the activation stage).
 template <int DT, int R, int MMAX, int W>
 __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
-    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ uint4 lut_storage[kLutStorageU4];
     __shared__ __attribute__((aligned(16))) char xs_storage[2][MMAX * kXRow];
 
-    fill_lut(lut_storage);
+    fill_lut<64 * W>(lut_storage, kLutMasks);
 
     int64_t wg = blockIdx.x;
     GemvJob job;
@@ -510,7 +529,7 @@ __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
     stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // LUT and round-0 activations ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
 
     for (int64_t t = 0; t < T; t += 2) {
         const bool has1 = t + 1 < T, has2 = t + 2 < T;
@@ -543,10 +562,9 @@ __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
 
 // ------------------------------------------------------------------------- post-scaled kernel
 //
-// Streaming kernel for M <= 4 (token-by-token decode).  Same rounds, code and scale
-// streams as the wide kernel, but the table holds the coordinates themselves (+-1, 0 in
-// the activation dtype) and the group scale multiplies fp32 partial sums instead of every
-// decoded weight:
+// Streaming kernel for M <= 4 (token-by-token decode).  Same rounds as the wide kernel, but
+// the table holds the coordinates themselves (+-1, 0 in the activation dtype) and the group
+// scale multiplies fp32 partial sums instead of every decoded weight:
 //
 //   A row a = 4*g' + m carries activation row m, but only in the k slots of lane group
 //   g' (lanes whose A row does not match their lane group read a zero block), so
@@ -559,6 +577,94 @@ __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
 // The sum over the four lane groups of a row is formed once, at the end.  Per code this
 // removes the four mask ANDs and the scale-word packing of the wide kernel; the weights are
 // still coord * scale in the activation dtype's rule (bf16: bf16_rne(s16)), applied in fp32.
+//
+// Weight stream.  In round u the R row tiles of a wave need 16R rows x 192 bytes of codes
+// (bytes 192u .. 192u+191 of each row: 128 codes) and 16R rows x 64 bytes of scales.  They
+// are fetched by 16-byte buffer->LDS loads in which the 64 lanes of a load read consecutive
+// 16-byte pieces of whole row segments -- each load covers complete 192-byte (64-byte) runs,
+// the pattern that streams at the HBM ceiling -- into a per-wave LDS stage.  At the start of
+// the round every lane reads back its own blocks in the MFMA layout: lane (g, n) takes the
+// 48 code bytes 48g .. 48g+47 (codes 32g .. 32g+31) and the 16 scale bytes 16g .. 16g+15 of
+// row n of each tile.  Within a row the four lane-group blocks are rotated: block g sits at
+// position (g + tau(n)) mod 4, tau(n) = (n + n/4) mod 4, so the read-backs of the 16 rows
+// hit distinct LDS banks.  The next round's loads are issued right after the read-back and
+// have the whole round's compute to land.
+
+__device__ __forceinline__ uint32_t ps_tau(uint32_t n) { return (n + (n >> 2)) & 3u; }
+
+// One round of one wave's codes, in LDS.
+template <int R>
+struct PsStage {
+    uint4 codes[3 * R][64];   // tile r row n block position q piece t: slot 192r + 12n + 3q + t
+};
+
+template <int R>
+struct PsStream {
+    __amdgpu_buffer_rsrc_t packed, scales, x;
+    uint32_t ld_code[3 * R];  // byte offset of the code piece this lane fetches per load
+    uint32_t vo_scale[R];     // byte offset of this lane's 8 scales (tile group c0, round 0)
+    uint32_t rd_code;         // byte offset of this lane's code block in a stage tile
+};
+
+// LDS destination operand of a buffer->LDS load (kept out of templates: the host pass of
+// a template instantiation rejects the address-space cast of a dependent expression).
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(void* p) {
+    return (__attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ void lds_wait_all() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Issues the code loads of round u of the tile group whose rows start `code_shift` bytes
+// after tile group c0's into the stage at `stg` (a PsStage of `tiles` tiles).  Loads past
+// the buffer's end read zeros.  (Not a template: the host pass rejects this builtin inside
+// a function template instantiated from a kernel template.)
+__device__ __forceinline__ void ps_issue(char* stg, __amdgpu_buffer_rsrc_t packed,
+                                         const uint32_t* ld_code, int tiles, int64_t code_shift,
+                                         int u) {
+    const int so = uniform_offset(code_shift + (int64_t)u * 192);
+#pragma unroll
+    for (int i = 0; i < 3 * tiles; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16, ld_code[i],
+                                                 so, 0, 0);
+}
+
+// The 8 scales of this lane's codes in round u (16 contiguous bytes per lane: every load
+// covers whole 64-byte row segments).  Lane groups past K in a partial last round read the
+// next row's codes: their scales are zeroed so those codes contribute exactly zero.
+template <int R>
+__device__ __forceinline__ void ps_load_scales(WideScales<R>& sc, const PsStream<R>& st,
+                                               int64_t scale_shift, int u, int64_t K, int g) {
+    const bool live = (int64_t)u * kRound + 256 * g < K;
+    const int so = uniform_offset(scale_shift + (int64_t)u * 64);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r], so, 0);
+        sc.sc[r][0] = live ? v.x : 0u;
+        sc.sc[r][1] = live ? v.y : 0u;
+        sc.sc[r][2] = live ? v.z : 0u;
+        sc.sc[r][3] = live ? v.w : 0u;
+    }
+}
+
+// This lane's codes of the staged round (MFMA layout).
+template <int R>
+__device__ __forceinline__ void ps_readback(const PsStage<R>& stg, const PsStream<R>& st,
+                                            WideCodes<R>& w) {
+    const char* cb = reinterpret_cast<const char*>(&stg.codes[0][0]) + st.rd_code;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const uint4 v = *reinterpret_cast<const uint4*>(cb + 3072 * r + 16 * t);
+            w.cd[r][4 * t + 0] = v.x;
+            w.cd[r][4 * t + 1] = v.y;
+            w.cd[r][4 * t + 2] = v.z;
+            w.cd[r][4 * t + 3] = v.w;
+        }
+    }
+}
 
 // Keeps all four result registers of an MFMA allocated up to this point.  With M == 1 only
 // result 0 is read; the compiler would otherwise hand the other three registers to VALU
@@ -572,15 +678,10 @@ __device__ __forceinline__ void keep_mfma_result(const f32x4& d, float& consumer
 
 // Step J of a post-scaled round; d[r] accumulates the current scale group of tile r.
 template <int DT, int R, int MM, int J>
-__device__ __forceinline__ void ps_step(WideCodes<R>& w, const WideScales<R>& sc,
-                                        WideScales<R>& sc_next, int64_t u_next,
-                                        const WideStream<R>& st, const char* lut,
-                                        const char* xa_base, uint4& xa_cur, uint2 (&ml)[R],
-                                        uint2 (&mh)[R], float (&sf)[R][2], f32x4 (&d)[R],
-                                        float (&acc)[R][MM]) {
-    if constexpr (J == 0) {
-        if (u_next >= 0) load_scales<R>(sc_next, u_next, st);
-    }
+__device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<R>& sc,
+                                        const char* lut, uint32_t slot, const char* xa_base,
+                                        uint4& xa_cur, uint2 (&ml)[R], uint2 (&mh)[R],
+                                        float (&sf)[R][2], f32x4 (&d)[R], float (&acc)[R][MM]) {
     if constexpr (J % 4 == 0 && J > 0) {
         // scale group J/4 - 1 is complete in d
 #pragma unroll
@@ -599,15 +700,12 @@ __device__ __forceinline__ void ps_step(WideCodes<R>& w, const WideScales<R>& sc
     uint2 ml_n[R], mh_n[R];
     if constexpr (J + 1 < 32) {
         xa_nxt = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + 1));
-        wide_lut<R, J + 1>(w, lut, st.slot, ml_n, mh_n);
+        wide_lut<R, J + 1>(w, lut, slot, ml_n, mh_n);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint4 b = make_uint4(ml[r].x, ml[r].y, mh[r].x, mh[r].y);
         d[r] = mfma16<DT>(xa_cur, b, J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[r]);
-    }
-    if constexpr (J == 10 || J == 21 || J == 31) {
-        if (u_next >= 0) load_code_piece<R>(w, J == 10 ? 0 : (J == 21 ? 1 : 2), u_next, st);
     }
     if constexpr (J + 1 < 32) {
         xa_cur = xa_nxt;
@@ -629,39 +727,25 @@ __device__ __forceinline__ void ps_step(WideCodes<R>& w, const WideScales<R>& sc
 }
 
 template <int DT, int R, int MM, int... J>
-__device__ __forceinline__ void ps_steps(WideCodes<R>& w, const WideScales<R>& sc,
-                                         WideScales<R>& sc_next, int64_t u_next,
-                                         const WideStream<R>& st, const char* lut,
-                                         const char* xa_base, uint4& xa, uint2 (&ml)[R],
-                                         uint2 (&mh)[R], float (&sf)[R][2], f32x4 (&d)[R],
-                                         float (&acc)[R][MM], std::integer_sequence<int, J...>) {
-    (ps_step<DT, R, MM, J>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sf, d, acc),
-     ...);
+__device__ __forceinline__ void ps_steps(const WideCodes<R>& w, const WideScales<R>& sc,
+                                         const char* lut, uint32_t slot, const char* xa_base,
+                                         uint4& xa, uint2 (&ml)[R], uint2 (&mh)[R],
+                                         float (&sf)[R][2], f32x4 (&d)[R], float (&acc)[R][MM],
+                                         std::integer_sequence<int, J...>) {
+    (ps_step<DT, R, MM, J>(w, sc, lut, slot, xa_base, xa, ml, mh, sf, d, acc), ...);
 }
 
 template <int DT, int R, int MM>
-__device__ __forceinline__ void ps_round(WideCodes<R>& w, const WideScales<R>& sc,
-                                         WideScales<R>& sc_next, int64_t u_next,
-                                         const WideStream<R>& st, const char* lut,
-                                         const char* xa_base, float (&acc)[R][MM]) {
+__device__ __forceinline__ void ps_round(const WideCodes<R>& w, const WideScales<R>& sc,
+                                         const char* lut, uint32_t slot, const char* xa_base,
+                                         float (&acc)[R][MM]) {
     uint4 xa = *reinterpret_cast<const uint4*>(xa_base);
     uint2 ml[R], mh[R];
     float sf[R][2];
     f32x4 d[R];
-    wide_lut<R, 0>(w, lut, st.slot, ml, mh);
-    ps_steps<DT, R, MM>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sf, d, acc,
+    wide_lut<R, 0>(w, lut, slot, ml, mh);
+    ps_steps<DT, R, MM>(w, sc, lut, slot, xa_base, xa, ml, mh, sf, d, acc,
                         std::make_integer_sequence<int, 32>{});
-}
-
-// Moves a stream `rows` rows further down its weight buffers (a later tile group).
-template <int R>
-__device__ __forceinline__ void ps_shift(WideStream<R>& st, int64_t rows, uint32_t rowbytes,
-                                         uint32_t srowbytes) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        st.vo_code[r] += (uint32_t)rows * rowbytes;
-        st.vo_scale[r] += (uint32_t)rows * srowbytes;
-    }
 }
 
 // Sums the four lane groups of each row and stores one tile group's outputs (lane group q
@@ -691,17 +775,18 @@ __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M,
 
 // MM: activation rows handled (1 or 4; M <= MM); W: waves per workgroup.  A workgroup
 // runs args.chunk consecutive tile groups (W * R row tiles each) of one job, one
-// code/scale/activation prefetch pipeline across the tile-group boundaries, and fills its
+// weight/activation prefetch pipeline across the tile-group boundaries, and fills its
 // table once.  Tile group c of the workgroup reads rows 16 W R c further down the same
 // buffers: the shift is a wave-uniform offset.
 template <int DT, int R, int MM, int W>
-__global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
+__global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch args) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
-    __shared__ uint2 lut_storage[(kLutEntries + 1) * kLutSlots];
+    __shared__ uint4 lut_storage[kLutValidStorageU4];
     __shared__ __attribute__((aligned(16))) char xs_storage[2][MM * kXRow];
     __shared__ __attribute__((aligned(16))) uint4 xzero[32];  // A rows outside a lane's group
+    __shared__ PsStage<R> stage[W];
 
-    fill_lut(lut_storage, LutValues<DT>());
+    fill_lut<64 * W, kLutValidEntries>(lut_storage, lut_values_kind<DT>());
     if (threadIdx.x < 32) xzero[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
 
     int64_t wg = blockIdx.x;
@@ -733,22 +818,28 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     const int64_t c1 = c0 + args.chunk < groups ? c0 + args.chunk : groups;
     const int64_t tile0 = (c0 * W + wave) * R;  // first row tile, tile group c0
 
-    WideStream<R> st;
+    PsStream<R> st;
     st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
                                                   (int)(N * rowbytes), kRsrcWord3);
     st.scales = __builtin_amdgcn_make_buffer_rsrc((void*)job.scales, (short)0,
                                                   (int)(N * srowbytes), kRsrcWord3);
     st.x = __builtin_amdgcn_make_buffer_rsrc((void*)xbase, (short)0, (int)(M * K * 2),
                                              kRsrcWord3);
+    const uint32_t row0 = (uint32_t)(tile0 * 16);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
-        st.vo_code[r] = row * rowbytes + 48u * g;
-        st.vo_scale[r] = row * srowbytes + 16u * g;
+    for (int i = 0; i < 3 * R; ++i) {
+        // stage slot s = 64 i + lane: tile s / 192, row n, block position q, piece t
+        const uint32_t s = 64u * i + lane, r = s / 192u, w192 = s % 192u;
+        const uint32_t n = w192 / 12u, pos = w192 % 12u, q = pos / 3u, t = pos % 3u;
+        const uint32_t gg = (q - ps_tau(n)) & 3u;
+        st.ld_code[i] = (row0 + 16u * r + n) * rowbytes + 16u * (3u * gg + t);
     }
-    st.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
-    st.K = K;
-    st.g = g;
+#pragma unroll
+    for (int r = 0; r < R; ++r) st.vo_scale[r] = (row0 + 16u * r + i16) * srowbytes + 16u * g;
+    const uint32_t q_me = ((uint32_t)g + ps_tau((uint32_t)i16)) & 3u;
+    st.rd_code = (12u * i16 + 3u * q_me) * 16u;
+    const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+
     // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
     const int am = i16 & 3;
     const bool a_live = (i16 >> 2) == g && am < M;
@@ -761,55 +852,45 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     // next item's codes, scales and activations are fetched.
     const int T = (int)((K + kRound - 1) / kRound);
     const int ngroups = (int)(c1 - c0);
+    const int64_t code_gshift = kGroupRows * (int64_t)rowbytes;
+    const int64_t scale_gshift = kGroupRows * (int64_t)srowbytes;
     float acc[R][MM];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int q = 0; q < MM; ++q) acc[r][q] = 0.f;
 
+    const PsStage<R>& stg = stage[wave];
+    char* const stg_bytes = reinterpret_cast<char*>(&stage[wave]);
     WideCodes<R> w;
-    WideScales<R> scA, scB;
-    load_code_piece<R>(w, 0, 0, st);
-    load_code_piece<R>(w, 1, 0, st);
-    load_code_piece<R>(w, 2, 0, st);
-    load_scales<R>(scA, 0, st);
+    WideScales<R> sc, sc_next;
+    ps_issue(stg_bytes, st.packed, st.ld_code, R, 0, 0);
+    ps_load_scales<R>(sc, st, 0, 0, K, g);
     stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
-    __syncthreads();  // table, zero block and round-0 activations ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutStride;
+    __syncthreads();  // table, zero block, round-0 weights and activations ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
 
-    int c = 0, u = 0;
+    int c = 0, u = 0, buf = 0;
     for (;;) {
-        {
-            const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
-            const bool has = cn < ngroups;
-            WideStream<R> sn = st;
-            ps_shift<R>(sn, (int64_t)cn * kGroupRows, rowbytes, srowbytes);
-            if (has) stage_x(xs_storage[1], st.x, un, M, K, wave, lane, W);
-            ps_round<DT, R, MM>(w, scA, scB, has ? un : -1, sn, lut, xa0, acc);
-            if (has) vm_wait_le<4 * R>();
-            else vm_wait_all();
-            __syncthreads();
-            if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0 + (int64_t)c * W * R, lane, acc);
-            if (!has) break;
-            c = cn;
-            u = un;
+        ps_readback<R>(stg, st, w);
+        lds_wait_all();  // the read-back has landed: the stage may be refilled
+        const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
+        const bool has = cn < ngroups;  // uniform over the workgroup
+        if (has) {
+            ps_issue(stg_bytes, st.packed, st.ld_code, R, cn * code_gshift, un);
+            ps_load_scales<R>(sc_next, st, cn * scale_gshift, un, K, g);
+            stage_x(xs_storage[buf ^ 1], st.x, un, M, K, wave, lane, W);
         }
-        {
-            const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
-            const bool has = cn < ngroups;
-            WideStream<R> sn = st;
-            ps_shift<R>(sn, (int64_t)cn * kGroupRows, rowbytes, srowbytes);
-            if (has) stage_x(xs_storage[0], st.x, un, M, K, wave, lane, W);
-            ps_round<DT, R, MM>(w, scB, scA, has ? un : -1, sn, lut, xa1, acc);
-            if (has) vm_wait_le<4 * R>();
-            else vm_wait_all();
-            __syncthreads();
-            if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0 + (int64_t)c * W * R, lane, acc);
-            if (!has) break;
-            c = cn;
-            u = un;
-        }
+        ps_round<DT, R, MM>(w, sc, lut, slot, buf ? xa1 : xa0, acc);
+        if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0 + (int64_t)c * W * R, lane, acc);
+        if (!has) break;
+        vm_wait_all();
+        __syncthreads();  // next item's codes (own stage) and activations (shared) ready
+        sc = sc_next;
+        c = cn;
+        u = un;
+        buf ^= 1;
     }
 }
 
@@ -840,11 +921,11 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.S = 1;
         // M <= 4: post-scaled kernel (mmax 1 or 4); otherwise the mask kernel
         p.mmax = M == 1 ? 1 : (M <= 4 ? 4 : 16);
-        p.R = 2;
+        p.R = p.mmax == 16 ? 2 : kPsTiles;
         // post-scaled kernel: consecutive tile groups per workgroup
         p.C = p.mmax == 16 ? 1 : kPsChunk;
         // waves sharing one table copy and one activation stage (measured best on MI355X)
-        p.W = p.mmax == 16 ? 16 : 4;
+        p.W = p.mmax == 16 ? 16 : kPsWaves;
     } else {
         // small layers: split K inside the workgroup to get enough waves
         p.wide = false;
@@ -891,8 +972,10 @@ template <int DT>
 static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                             hipStream_t stream) {
     if (p.wide) {
-        if (p.W == 4 && p.R == 2 && p.mmax == 1) return launch_ps<DT, 2, 1, 4>(a, p, wgs, stream);
-        if (p.W == 4 && p.R == 2 && p.mmax == 4) return launch_ps<DT, 2, 4, 4>(a, p, wgs, stream);
+        if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 1)
+            return launch_ps<DT, kPsTiles, 1, kPsWaves>(a, p, wgs, stream);
+        if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 4)
+            return launch_ps<DT, kPsTiles, 4, kPsWaves>(a, p, wgs, stream);
         if (p.W == 16 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 16>(a, wgs, stream);
         return hipErrorInvalidValue;
     }

@@ -7,7 +7,10 @@
 // coord*s exactly, since group scales are >= 0.  hi = floor(2c/81) is one mul_hi
 // (exact for every valid code, checked exhaustively).  The table is "bank sliced":
 // kLutSlots copies, lane l reading copy l % kLutSlots, which occupies only its own bank
-// pair -- the lanes of a ds_read_b64 phase never conflict.
+// pair.  16 copies (13 KB) measured as fast as 32 (26 KB) on MI355X and leave LDS for the
+// kernels' staging buffers; 8 copies lose more to bank conflicts than they gain.  The
+// table is filled from a constant base table in device memory (one 8-byte load per
+// thread-item), not recomputed per entry.
 #pragma once
 
 #include "e8t_device.h"
@@ -20,10 +23,23 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(3))) uint32_t u32x3;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
+#ifndef OJX_LUT_SLOTS
+#define OJX_LUT_SLOTS 16
+#endif
+
 constexpr int kLutEntries = 102;            // 81 valid + slack so that any 12-bit code stays in bounds
-constexpr int kLutSlots = 32;               // bank slices: lane l reads slice l % 32
+constexpr int kLutSlots = OJX_LUT_SLOTS;    // bank slices: lane l reads slice l % kLutSlots
+static_assert(kLutSlots == 8 || kLutSlots == 16 || kLutSlots == 32, "8, 16 or 32 table slices");
 constexpr uint32_t kLutStride = kLutSlots * 8;  // bytes per table entry (all slices)
-constexpr uint32_t kHiMagic = 207127u;      // floor((512c + b) * kHiMagic / 2^32) == floor(2c / 81), b < 256
+// Z = 2 * code * kLutStride + slot = (code << kCodeShift) | slot; kHiMagic makes
+// floor(Z * kHiMagic / 2^32) == floor(2c / 81) for every valid code c < 3281 and every slot
+// offset (checked exhaustively); for invalid codes the two table addresses stay within the
+// table and its zero guard entry.
+constexpr int kCodeShift = kLutSlots == 32 ? 9 : (kLutSlots == 16 ? 8 : 7);
+constexpr uint32_t kHiMagic = kLutSlots == 32 ? 207127u : (kLutSlots == 16 ? 414253u : 828505u);
+// With 32 slices the lo address of an invalid code can fall 8 bytes below entry 0: a zero
+// guard entry precedes the table.  With 8 or 16 slices every address is >= 0.
+constexpr int kLutGuard = kLutSlots == 32 ? 1 : 0;
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
 
 // Scalar (SOFFSET) operand of a buffer instruction: the value is wave-uniform by
@@ -33,53 +49,86 @@ __device__ __forceinline__ int uniform_offset(int64_t v) {
     return __builtin_amdgcn_readfirstlane((int)v);
 }
 
-// Mask table half-word of base-3 digit d (coord d - 1).
-struct LutMasks {
-    __device__ uint32_t operator()(int d) const {
-        return d == 0 ? 0xFFFFu : (d == 1 ? 0x0000u : 0x7FFFu);
-    }
-};
+// Table kinds.  Masks: half-word 0xFFFF for coordinate -1, 0x0000 for 0, 0x7FFF for +1
+// (AND-ed with the scale word).  Values: the coordinate itself in the activation dtype
+// (+-1.0 or 0), for kernels that apply the group scale to fp32 partial sums.
+enum : int { kLutMasks = 0, kLutValuesBF16 = 1, kLutValuesF16 = 2 };
 
-// Value table half-word: coord d - 1 itself in the activation dtype (+-1.0 or 0), for
-// kernels that apply the group scale to fp32 partial sums after the MFMA.
 template <int DT>
-struct LutValues {
-    __device__ uint32_t operator()(int d) const {
-        const uint32_t one = DT == kBF16 ? 0x3F80u : 0x3C00u;
-        return d == 0 ? (one | 0x8000u) : (d == 1 ? 0x0000u : one);
-    }
+constexpr int lut_values_kind() { return DT == kBF16 ? kLutValuesBF16 : kLutValuesF16; }
+
+constexpr uint32_t lut_half(int kind, int d) {  // base-3 digit d = coordinate + 1
+    return kind == kLutMasks ? (d == 0 ? 0xFFFFu : (d == 1 ? 0x0000u : 0x7FFFu))
+         : kind == kLutValuesBF16 ? (d == 0 ? 0xBF80u : (d == 1 ? 0x0000u : 0x3F80u))
+                                  : (d == 0 ? 0xBC00u : (d == 1 ? 0x0000u : 0x3C00u));
+}
+
+// Base table: word pair i + 1 holds entry i (4 digits of i, two per word, digit 0 in the
+// low half-word); word pair 0 is the zero guard entry.
+struct alignas(16) LutBase {
+    uint32_t w[2 * (kLutEntries + 1)];
 };
 
-// Fills the bank-sliced table: entry e, slice c at byte offset (e + 1) * kLutStride + c * 8
-// of the storage; entry -1 is a zero guard (with kHiMagic, the lo address of an invalid
-// code >= 3281 can reach 8 bytes below entry 0; valid codes never do).
-template <typename Half = LutMasks>
-__device__ __forceinline__ void fill_lut(uint2* storage, Half half = Half()) {
-    for (int i = threadIdx.x; i < (kLutEntries + 1) * kLutSlots; i += blockDim.x) {
-        const int e = i / kLutSlots - 1;
-        if (e < 0) {
-            storage[i] = make_uint2(0u, 0u);
-            continue;
-        }
+constexpr LutBase make_lut_base(int kind) {
+    LutBase t{};
+    for (int e = 0; e < kLutEntries; ++e) {
         const int d0 = e % 3, d1 = (e / 3) % 3, d2 = (e / 9) % 3, d3 = (e / 27) % 3;
-        storage[i] = make_uint2(half(d0) | (half(d1) << 16), half(d2) | (half(d3) << 16));
+        t.w[2 * (e + 1)] = lut_half(kind, d0) | (lut_half(kind, d1) << 16);
+        t.w[2 * (e + 1) + 1] = lut_half(kind, d2) | (lut_half(kind, d3) << 16);
+    }
+    return t;
+}
+
+static __device__ const LutBase kLutBaseTab[3] = {
+    make_lut_base(kLutMasks), make_lut_base(kLutValuesBF16), make_lut_base(kLutValuesF16)};
+
+// Fills the bank-sliced table from the base table in device memory: entry e (-1 = guard),
+// slice c at byte offset (e + kLutGuard) * kLutStride + c * 8 of the storage.  Each thread writes
+// 16-byte items (two slices of one entry); its base-table loads are all issued before its
+// first write.  NT: threads of the workgroup.
+template <int NT, int ENTRIES = kLutEntries>
+__device__ __forceinline__ void fill_lut(uint4* storage, int kind) {
+    constexpr int kPairs = kLutSlots / 2;
+    constexpr int kItems = (ENTRIES + kLutGuard) * kPairs;
+    constexpr int kPer = (kItems + NT - 1) / NT;
+    const uint2* tab = reinterpret_cast<const uint2*>(kLutBaseTab[kind].w);
+    uint2 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        v[k] = i < kItems ? tab[i / kPairs + 1 - kLutGuard] : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        if (i < kItems) storage[i] = make_uint4(v[k].x, v[k].y, v[k].x, v[k].y);
     }
 }
 
-// Z = (code_j << 9) | slot for code j (0..7) of the 12-byte, 8-code group (d0, d1, d2):
-// code j occupies bits [12j, 12j+12) of the little-endian stream (lattice.py:375-383).
+// LDS words of the table (16-byte aligned, for the 16-byte fill writes).
+constexpr int kLutStorageU4 = (kLutEntries + kLutGuard) * kLutSlots / 2;
+// A table of the 81 entries that valid codes (< 3281) reach.  An invalid code then reads
+// neighbouring LDS words of the same workgroup (or zeros past its allocation): a garbage
+// result for garbage input, never an access outside the workgroup's LDS.
+constexpr int kLutValidEntries = 81;
+constexpr int kLutValidStorageU4 = (kLutValidEntries + kLutGuard) * kLutSlots / 2;
+// Byte offset of entry 0 in the storage.
+constexpr uint32_t kLutBaseOffset = kLutGuard * kLutStride;
+
+// Z = (code_j << kCodeShift) | slot for code j (0..7) of the 12-byte, 8-code group
+// (d0, d1, d2): code j occupies bits [12j, 12j+12) of the little-endian stream
+// (lattice.py:375-383).
 template <int J>
 __device__ __forceinline__ uint32_t code_z(const uint32_t (&d)[3], uint32_t slot) {
+    constexpr int p = 12 * J, w = p / 32, o = p % 32;
     uint32_t t;
-    if constexpr (J == 0) t = d[0] << 9;
-    else if constexpr (J == 1) t = d[0] >> 3;
-    else if constexpr (J == 2) t = __builtin_amdgcn_alignbit(d[1], d[0], 15);
-    else if constexpr (J == 3) t = d[1] << 5;
-    else if constexpr (J == 4) t = d[1] >> 7;
-    else if constexpr (J == 5) t = __builtin_amdgcn_alignbit(d[2], d[1], 19);
-    else if constexpr (J == 6) t = d[2] << 1;
-    else t = d[2] >> 11;
-    return (t & 0x1FFE00u) | slot;
+    if constexpr (o + 12 <= 32) {
+        if constexpr (o <= kCodeShift) t = d[w] << (kCodeShift - o);
+        else t = d[w] >> (o - kCodeShift);
+    } else {
+        t = __builtin_amdgcn_alignbit(d[w + 1], d[w], o - kCodeShift);
+    }
+    return (t & (0xFFFu << kCodeShift)) | slot;
 }
 
 // lo address = Z - 81 * kLutStride * hi = (2c - 81 hi) * kLutStride + slot, as one
