@@ -263,17 +263,19 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
     }
 }
 
-// ------------------------------------------------------------------------- wide kernel
+// ------------------------------------------------------------------------- streaming kernels
 //
-// Streaming-optimised variant for launches with many row tiles (grouped launches, large
-// N).  A "round" covers 1024 k: lane (g, n) loads 48 contiguous bytes of row n (the 32
-// codes of chunk g of the round, three 16-byte loads) plus their 8 scales, so each row
-// is read in 192-byte contiguous spans -- the access pattern the memory system streams
-// at near-peak rate.  Step j of the round contracts code j of every lane: lane group g
-// covers k = 1024u + 256g + 8j.  The activations of the round (M rows x 1024) are staged
-// in LDS by buffer->LDS loads issued one round ahead (padded rows: conflict-free reads),
-// and each MFMA step reads its A fragment with one ds_read_b128.  Codes are double
-// buffered in registers one round ahead; one workgroup barrier per round.
+// Two streaming kernels cover launches with many row tiles (grouped launches, large N):
+// the post-scaled kernel (M <= 4, 1024-k rounds) and the mask kernel (M <= 16, 512-k
+// rounds).  In both, a wave owns R = 2 tiles of 16 rows; per round, its code bytes (and the
+// mask kernel's scales) are fetched by 16-byte buffer->LDS loads in which consecutive lanes
+// read consecutive pieces of whole row segments, into a per-wave LDS stage, then read back
+// in the MFMA layout (lane (g, n): the codes of lane group g of row n).  Loads that cover
+// whole row segments stream near the HBM ceiling on MI355X (about 6.3 TB/s measured),
+// while one lane reading its own 48 bytes of each of 16 rows per load instruction -- the
+// MFMA layout fetched directly -- stays near 4.5 TB/s.  The round's activations are staged
+// in LDS by buffer->LDS loads issued one round ahead (padded rows: conflict-free reads);
+// one workgroup barrier per round.
 
 constexpr int kRound = 1024;                      // K per round
 // Post-scaled kernel: tile groups per workgroup.  Measured on MI355X (32-layer decode
@@ -311,44 +313,10 @@ struct WideScales {
     uint32_t sc[R][4];   // the 8 group scales covering the 32 codes
 };
 
-template <int R>
-struct WideStream {
-    __amdgpu_buffer_rsrc_t packed, scales, x;
-    uint32_t vo_code[R], vo_scale[R];
-    uint32_t slot;
-    int64_t K;
-    int g;
-};
-
-// Piece t (bytes 16t .. 16t+15) of each row's 48 code bytes of round u.
-template <int R>
-__device__ __forceinline__ void load_code_piece(WideCodes<R>& w, int t, int64_t u,
-                                                const WideStream<R>& st) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-            st.packed, st.vo_code[r] + 16u * t, uniform_offset(u * 192), 0);
-        w.cd[r][4 * t + 0] = v.x;
-        w.cd[r][4 * t + 1] = v.y;
-        w.cd[r][4 * t + 2] = v.z;
-        w.cd[r][4 * t + 3] = v.w;
-    }
-}
-
-template <int R>
-__device__ __forceinline__ void load_scales(WideScales<R>& w, int64_t u, const WideStream<R>& st) {
-    // lane groups past K in a partial last round read the next row's bytes: zero their
-    // scales so those codes contribute exactly zero
-    const bool live = u * kRound + 256 * st.g < st.K;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const u32x4 s = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r],
-                                                              uniform_offset(u * 64), 0);
-        w.sc[r][0] = live ? s.x : 0u;
-        w.sc[r][1] = live ? s.y : 0u;
-        w.sc[r][2] = live ? s.z : 0u;
-        w.sc[r][3] = live ? s.w : 0u;
-    }
+// LDS destination operand of a buffer->LDS load (kept out of templates: the host pass of
+// a template instantiation rejects the address-space cast of a dependent expression).
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(void* p) {
+    return (__attribute__((address_space(3))) void*)p;
 }
 
 // Stages x[m][1024u .. 1024u + 1024) for m < M into LDS buffer `xs` (row stride kXRow):
@@ -358,19 +326,20 @@ __device__ __forceinline__ void stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int6
     for (int q = wave; q < 2 * M; q += waves) {
         const int m = q >> 1, half = q & 1;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            x, (__attribute__((address_space(3))) void*)(xs + m * kXRow + half * 1024),
-            16, (uint32_t)(m * K * 2 + half * 1024 + lane * 16), uniform_offset(u * kRound * 2), 0,
+            x, lds_ptr(xs + m * kXRow + half * 1024), 16,
+            (uint32_t)(m * K * 2 + half * 1024 + lane * 16), uniform_offset(u * kRound * 2), 0,
             0);
     }
 }
 
-template <int R, int J>
-__device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut, uint32_t slot,
-                                         uint2 (&ml)[R], uint2 (&mh)[R]) {
+// Table reads of code J of each tile's code words (NW words = 8 codes per 3 words).
+template <int R, int NW, int J>
+__device__ __forceinline__ void codes_lut(const uint32_t (&cd)[R][NW], const char* lut,
+                                          uint32_t slot, uint2 (&ml)[R], uint2 (&mh)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t d[3] = {w.cd[r][3 * (J / 8)], w.cd[r][3 * (J / 8) + 1],
-                               w.cd[r][3 * (J / 8) + 2]};
+        const uint32_t d[3] = {cd[r][3 * (J / 8)], cd[r][3 * (J / 8) + 1],
+                               cd[r][3 * (J / 8) + 2]};
         const uint32_t z = code_z<J % 8>(d, slot);
         const uint32_t h = __umulhi(z, kHiMagic);
         ml[r] = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
@@ -378,95 +347,164 @@ __device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut,
     }
 }
 
-// Step J of a round.  Code piece 0 (dwords 0-3) is last read by the table lookahead of
-// step 9 (code 10), piece 1 by that of step 20 (code 21), piece 2 by that of step 30
-// (code 31): each is refilled with the next round's bytes right after steps 10, 21 and
-// 31, and is next needed 21 steps later.  The next round's scales are fetched at step 0.
-template <int DT, int R, int J>
-__device__ __forceinline__ void wide_step(WideCodes<R>& w, const WideScales<R>& sc,
-                                          WideScales<R>& sc_next, int64_t u_next,
-                                          const WideStream<R>& st, const char* lut,
-                                          const char* xa_base, uint4& xa_cur, uint2 (&ml)[R],
-                                          uint2 (&mh)[R], uint32_t (&sw)[R], f32x4 (&acc)[R]) {
-    if constexpr (J == 0) {
-        if (u_next >= 0) load_scales<R>(sc_next, u_next, st);
-    }
-    if constexpr (J % 4 == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            uint32_t w0, w1;
-            scale_words<DT>(sc.sc[r][J / 8], w0, w1);
-            sw[r] = (J % 8 == 0) ? w0 : w1;
-        }
-    }
-    uint4 xa_nxt;
-    uint2 ml_n[R], mh_n[R];
-    if constexpr (J + 1 < 32) {
-        xa_nxt = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + 1));
-        wide_lut<R, J + 1>(w, lut, st.slot, ml_n, mh_n);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t s = sw[r];
-        const uint4 b = make_uint4(ml[r].x & s, ml[r].y & s, mh[r].x & s, mh[r].y & s);
-        acc[r] = mfma16<DT>(xa_cur, b, acc[r]);
-    }
-    if constexpr (J == 10 || J == 21 || J == 31) {
-        if (u_next >= 0) load_code_piece<R>(w, J == 10 ? 0 : (J == 21 ? 1 : 2), u_next, st);
-    }
-    if constexpr (J + 1 < 32) {
-        xa_cur = xa_nxt;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ml[r] = ml_n[r];
-            mh[r] = mh_n[r];
-        }
-    }
+template <int R, int J>
+__device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut, uint32_t slot,
+                                         uint2 (&ml)[R], uint2 (&mh)[R]) {
+    codes_lut<R, 12, J>(w.cd, lut, slot, ml, mh);
 }
 
-template <int DT, int R, int... J>
-__device__ __forceinline__ void wide_steps(WideCodes<R>& w, const WideScales<R>& sc,
-                                           WideScales<R>& sc_next, int64_t u_next,
-                                           const WideStream<R>& st, const char* lut,
-                                           const char* xa_base, uint4& xa, uint2 (&ml)[R],
-                                           uint2 (&mh)[R], uint32_t (&sw)[R], f32x4 (&acc)[R],
-                                           std::integer_sequence<int, J...>) {
-    (wide_step<DT, R, J>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sw, acc), ...);
-}
-
-// One round on the codes in `w` (refilled in place with round u_next's, if >= 0).
-template <int DT, int R>
-__device__ __forceinline__ void wide_round(WideCodes<R>& w, const WideScales<R>& sc,
-                                           WideScales<R>& sc_next, int64_t u_next,
-                                           const WideStream<R>& st, const char* lut,
-                                           const char* xa_base, f32x4 (&acc)[R]) {
-    uint4 xa = *reinterpret_cast<const uint4*>(xa_base);
+// The same table reads, as one 4-word B operand per tile (lo words, hi words).
+template <int R, int NW, int J>
+__device__ __forceinline__ void codes_lut4(const uint32_t (&cd)[R][NW], const char* lut,
+                                           uint32_t slot, uint4 (&b)[R]) {
     uint2 ml[R], mh[R];
-    uint32_t sw[R];
-    wide_lut<R, 0>(w, lut, st.slot, ml, mh);
-    wide_steps<DT, R>(w, sc, sc_next, u_next, st, lut, xa_base, xa, ml, mh, sw, acc,
-                      std::make_integer_sequence<int, 32>{});
+    codes_lut<R, NW, J>(cd, lut, slot, ml, mh);
+#pragma unroll
+    for (int r = 0; r < R; ++r) b[r] = make_uint4(ml[r].x, ml[r].y, mh[r].x, mh[r].y);
+}
+
+// Operands (A fragment and table words) of the next kLookahead steps of a round, read
+// ahead so that the table reads of a step have kLookahead steps of other work to land.
+#ifndef OJX_LOOKAHEAD
+#define OJX_LOOKAHEAD 2
+#endif
+constexpr int kLookahead = OJX_LOOKAHEAD;
+static_assert(kLookahead == 1 || kLookahead == 2, "read-ahead depth 1 or 2");
+
+template <int R>
+struct Ahead {
+    uint4 xa[kLookahead];
+    uint4 b[kLookahead][R];   // table words of each tile: lo half, hi half
+};
+
+// Drops step J's operands and appends the fresh ones (for step J + kLookahead).
+template <int R>
+__device__ __forceinline__ void ahead_shift(Ahead<R>& ah, const uint4& xa_n, const uint4 (&b_n)[R],
+                                            bool fresh) {
+#pragma unroll
+    for (int i = 0; i + 1 < kLookahead; ++i) {
+        ah.xa[i] = ah.xa[i + 1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) ah.b[i][r] = ah.b[i + 1][r];
+    }
+    if (fresh) {
+        ah.xa[kLookahead - 1] = xa_n;
+#pragma unroll
+        for (int r = 0; r < R; ++r) ah.b[kLookahead - 1][r] = b_n[r];
+    }
+}
+
+// Reads the operands of steps 0 .. kLookahead-1 of a round.
+template <int R, int NW>
+__device__ __forceinline__ void ahead_fill(Ahead<R>& ah, const uint32_t (&cd)[R][NW],
+                                           const char* lut, uint32_t slot, const char* xa_base) {
+    ah.xa[0] = *reinterpret_cast<const uint4*>(xa_base);
+    codes_lut4<R, NW, 0>(cd, lut, slot, ah.b[0]);
+    if constexpr (kLookahead > 1) {
+        ah.xa[1] = *reinterpret_cast<const uint4*>(xa_base + 16);
+        codes_lut4<R, NW, 1>(cd, lut, slot, ah.b[1]);
+    }
 }
 
 __device__ __forceinline__ void vm_wait_all() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
 }
 
-// vmcnt(N) (N < 16): all but this wave's N most recent vector-memory loads have landed.
-template <int N>
-__device__ __forceinline__ void vm_wait_le() {
-    static_assert(N >= 0 && N < 16, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+__device__ __forceinline__ void lds_wait_all() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// R: n-tiles (16 rows) per wave; MMAX: activation rows staged (4 or 16; M <= MMAX);
-// W: waves per workgroup (they share the table and the activation stage).
-template <int DT, int R, int MMAX, int W>
-__global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
-    __shared__ uint4 lut_storage[kLutStorageU4];
-    __shared__ __attribute__((aligned(16))) char xs_storage[2][MMAX * kXRow];
+// ------------------------------------------------------------------------- mask kernel
+//
+// M <= 16.  Rounds of 512 k: lane group g covers k = 512u + 128g + 8j, j = 0..15, i.e. 16
+// codes (24 bytes) and 4 group scales (8 bytes) of each of its rows.  A wave's round is 32
+// rows x 96 code bytes + 32 rows x 32 scale bytes = 4 KB, fetched into its stage by four
+// 1-KB loads.  Step j decodes code j of every lane into 8 weights (table masks AND-ed with
+// the group scale word) and runs one v_mfma_f32_16x16x32 per tile with the 16 activation
+// rows as A.  Stage rows are rotated to spread the read-backs over the LDS banks: piece p
+// (16 bytes) of code row n sits at position (p + n/4) mod 6, scale piece p at
+// p ^ ((n/4 + n/8) & 1).
 
-    fill_lut<64 * W>(lut_storage, kLutMasks);
+constexpr int kMRound = 512;                      // K per round of the mask kernel
+#ifndef OJX_MASK_WAVES
+#define OJX_MASK_WAVES 8
+#endif
+constexpr int kMaskWaves = OJX_MASK_WAVES;        // waves per workgroup
+constexpr uint32_t kMXRow = kMRound * 2 + 16;     // bytes per padded activation row in LDS
+constexpr uint32_t kMStageBytes = 4096;           // codes 3 KB + scales 1 KB (two tiles)
+
+__device__ __forceinline__ uint32_t mk_rot(uint32_t n) { return n >> 2; }
+__device__ __forceinline__ uint32_t mk_rot_s(uint32_t n) { return ((n >> 2) + (n >> 3)) & 1u; }
+
+// Issues round u's four stage loads (three of codes, one of scales) of the tile group
+// whose rows start `code_shift` / `scale_shift` bytes after this wave's first rows.
+__device__ __forceinline__ void mk_issue(char* stg, __amdgpu_buffer_rsrc_t packed,
+                                         __amdgpu_buffer_rsrc_t scales, const uint32_t* ld_code,
+                                         uint32_t ld_scale, int64_t code_shift,
+                                         int64_t scale_shift, int u) {
+    const int so_c = uniform_offset(code_shift + (int64_t)u * 96);
+    const int so_s = uniform_offset(scale_shift + (int64_t)u * 32);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16, ld_code[i],
+                                                 so_c, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(scales, lds_ptr(stg + 3072), 16, ld_scale, so_s,
+                                             0, 0);
+}
+
+// Stages x[m][512u .. 512u + 512) for m < M into `xs` (row stride kMXRow): one 1-KB load
+// per activation row, spread over the workgroup's waves.
+__device__ __forceinline__ void mk_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int64_t u, int M,
+                                           int64_t K, int wave, int lane, int waves) {
+    for (int m = wave; m < M; m += waves)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x, lds_ptr(xs + m * kMXRow), 16,
+                                                 (uint32_t)(m * K * 2 + lane * 16),
+                                                 uniform_offset(u * kMRound * 2), 0, 0);
+}
+
+// Step J (0..15) of a mask-kernel round.
+template <int DT, int J>
+__device__ __forceinline__ void mk_step(const uint32_t (&cd)[2][6], const uint32_t (&sc)[2][2],
+                                        const char* lut, uint32_t slot, const char* xa_base,
+                                        Ahead<2>& ah, uint32_t (&sw)[2][2], f32x4 (&acc)[2]) {
+    if constexpr (J % 8 == 0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) scale_words<DT>(sc[r][J / 8], sw[r][0], sw[r][1]);
+    }
+    constexpr bool kFresh = J + kLookahead < 16;
+    uint4 xa_n, b_n[2];
+    if constexpr (kFresh) {
+        xa_n = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + kLookahead));
+        codes_lut4<2, 6, (kFresh ? J + kLookahead : 0)>(cd, lut, slot, b_n);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t s = sw[r][(J / 4) & 1];
+        const uint4 m = ah.b[0][r];
+        const uint4 b = make_uint4(m.x & s, m.y & s, m.z & s, m.w & s);
+        acc[r] = mfma16<DT>(ah.xa[0], b, acc[r]);
+    }
+    if constexpr (J + 1 < 16) ahead_shift<2>(ah, xa_n, b_n, kFresh);
+}
+
+template <int DT, int... J>
+__device__ __forceinline__ void mk_steps(const uint32_t (&cd)[2][6], const uint32_t (&sc)[2][2],
+                                         const char* lut, uint32_t slot, const char* xa_base,
+                                         Ahead<2>& ah, uint32_t (&sw)[2][2], f32x4 (&acc)[2],
+                                         std::integer_sequence<int, J...>) {
+    (mk_step<DT, J>(cd, sc, lut, slot, xa_base, ah, sw, acc), ...);
+}
+
+// MMAX: activation rows staged (M <= MMAX); W: waves per workgroup (they share the table
+// and the activation stage).  One tile group (W x 2 row tiles) per workgroup.
+template <int DT, int MMAX, int W>
+__global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
+    constexpr int R = 2;
+    __shared__ uint4 lut_storage[kLutValidStorageU4];
+    __shared__ __attribute__((aligned(16))) char xs_storage[2][MMAX * kMXRow];
+    __shared__ __attribute__((aligned(16))) char stage[W][kMStageBytes];
+
+    fill_lut<64 * W, kLutValidEntries>(lut_storage, kLutMasks);
 
     int64_t wg = blockIdx.x;
     GemvJob job;
@@ -491,61 +529,89 @@ __global__ __launch_bounds__(64 * W) void gemv_wide_kernel(GemvLaunch args) {
     const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
     const uint32_t srowbytes = (uint32_t)(K / 16);
     const int64_t tile0 = (wg * W + wave) * R;
+    const uint32_t row0 = (uint32_t)(tile0 * 16);
 
-    WideStream<R> st;
-    st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
-                                                  (int)(N * rowbytes), kRsrcWord3);
-    st.scales = __builtin_amdgcn_make_buffer_rsrc((void*)job.scales, (short)0,
-                                                  (int)(N * srowbytes), kRsrcWord3);
-    st.x = __builtin_amdgcn_make_buffer_rsrc((void*)xbase, (short)0, (int)(M * K * 2),
-                                             kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t packed = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t scales = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)xbase, (short)0, (int)(M * K * 2), kRsrcWord3);
+
+    // stage slot s (16 bytes) of load i holds piece p of row n of tile r
+    uint32_t ld_code[3];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
-        st.vo_code[r] = row * rowbytes + 48u * g;
-        st.vo_scale[r] = row * srowbytes + 16u * g;
+    for (int i = 0; i < 3; ++i) {
+        const uint32_t s = 64u * i + lane, r = s / 96u, w96 = s % 96u;
+        const uint32_t n = w96 / 6u, pos = w96 % 6u;
+        const uint32_t p = (pos + 6u - mk_rot(n)) % 6u;
+        ld_code[i] = (row0 + 16u * r + n) * rowbytes + 16u * p;
     }
-    st.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
-    st.K = K;
-    st.g = g;
+    uint32_t ld_scale;
+    {
+        const uint32_t r = (uint32_t)lane >> 5, w32 = (uint32_t)lane & 31u;
+        const uint32_t n = w32 >> 1, p = (w32 & 1u) ^ mk_rot_s(n);
+        ld_scale = (row0 + 16u * r + n) * srowbytes + 16u * p;
+    }
+    // read-back offsets of this lane's 8-byte words (codes: words 3g .. 3g+2 of its row)
+    uint32_t rd_code[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const uint32_t wd = 3u * g + t, p = wd >> 1;
+        rd_code[t] = 96u * i16 + 16u * ((p + mk_rot(i16)) % 6u) + 8u * (wd & 1u);
+    }
+    const uint32_t rd_scale =
+        3072u + 32u * i16 + 16u * (((uint32_t)g >> 1) ^ mk_rot_s(i16)) + 8u * (g & 1);
+    const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
     const int mrow = i16 < M ? i16 : M - 1;
-    const uint32_t xa_off = (uint32_t)(mrow * kXRow + 512 * g);
+    const uint32_t xa_off = (uint32_t)(mrow * kMXRow + 256 * g);
 
-    const int64_t T = (K + kRound - 1) / kRound;
+    const int T = (int)((K + kMRound - 1) / kMRound);
     f32x4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // One register set of codes (refilled piece by piece during each round), two of
-    // scales.  At a round's end, this wave's only loads newer than its activation-stage
-    // loads are the 4R code/scale loads of the next round: vmcnt(4R) waits exactly for
-    // the stage.
-    WideCodes<R> w;
-    WideScales<R> scA, scB;
-    load_code_piece<R>(w, 0, 0, st);
-    load_code_piece<R>(w, 1, 0, st);
-    load_code_piece<R>(w, 2, 0, st);
-    load_scales<R>(scA, 0, st);
-    stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
+    char* const stg = stage[wave];
+    mk_issue(stg, packed, scales, ld_code, ld_scale, 0, 0, 0);
+    mk_stage_x(xs_storage[0], xr, 0, M, K, wave, lane, W);
     vm_wait_all();
-    __syncthreads();  // LUT and round-0 activations ready
+    __syncthreads();  // table, round-0 weights and activations ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
 
-    for (int64_t t = 0; t < T; t += 2) {
-        const bool has1 = t + 1 < T, has2 = t + 2 < T;
-        if (has1) stage_x(xs_storage[1], st.x, t + 1, M, K, wave, lane, W);
-        wide_round<DT, R>(w, scA, scB, has1 ? t + 1 : -1, st, lut, xs_storage[0] + xa_off, acc);
-        if (has1) vm_wait_le<4 * R>();
-        else vm_wait_all();
-        __syncthreads();
-        if (!has1) break;
-        if (has2) stage_x(xs_storage[0], st.x, t + 2, M, K, wave, lane, W);
-        wide_round<DT, R>(w, scB, scA, has2 ? t + 2 : -1, st, lut, xs_storage[1] + xa_off, acc);
-        if (has2) vm_wait_le<4 * R>();
-        else vm_wait_all();
-        __syncthreads();
+    for (int u = 0; u < T; ++u) {
+        uint32_t cd[R][6], sc[R][2];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                const uint2 v = *reinterpret_cast<const uint2*>(stg + 1536 * r + rd_code[t]);
+                cd[r][2 * t] = v.x;
+                cd[r][2 * t + 1] = v.y;
+            }
+            const uint2 v = *reinterpret_cast<const uint2*>(stg + 512 * r + rd_scale);
+            // lane groups past K in a partial last round hold the next row's codes
+            const bool live = (int64_t)u * kMRound + 128 * g < K;
+            sc[r][0] = live ? v.x : 0u;
+            sc[r][1] = live ? v.y : 0u;
+        }
+        lds_wait_all();  // the read-back has landed: the stage may be refilled
+        const bool has = u + 1 < T;  // uniform over the workgroup
+        if (has) {
+            mk_issue(stg, packed, scales, ld_code, ld_scale, 0, 0, u + 1);
+            mk_stage_x(xs_storage[(u + 1) & 1], xr, u + 1, M, K, wave, lane, W);
+        }
+        const char* xa_base = xs_storage[u & 1] + xa_off;
+        Ahead<R> ah;
+        uint32_t sw[R][2];
+        ahead_fill<R, 6>(ah, cd, lut, slot, xa_base);
+        mk_steps<DT>(cd, sc, lut, slot, xa_base, ah, sw, acc,
+                     std::make_integer_sequence<int, 16>{});
+        if (!has) break;
+        vm_wait_all();
+        __syncthreads();  // next round's stage (own) and activations (shared) ready
     }
 
+    // lane (g, n) holds rows m = 4g + q of column n (MFMA 16x16 output layout)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t row = (tile0 + r) * 16 + i16;
@@ -606,15 +672,6 @@ struct PsStream {
     uint32_t rd_code;         // byte offset of this lane's code block in a stage tile
 };
 
-// LDS destination operand of a buffer->LDS load (kept out of templates: the host pass of
-// a template instantiation rejects the address-space cast of a dependent expression).
-__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(void* p) {
-    return (__attribute__((address_space(3))) void*)p;
-}
-
-__device__ __forceinline__ void lds_wait_all() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-}
 
 // Issues the code loads of round u of the tile group whose rows start `code_shift` bytes
 // after tile group c0's into the stage at `stg` (a PsStage of `tiles` tiles).  Loads past
@@ -680,8 +737,8 @@ __device__ __forceinline__ void keep_mfma_result(const f32x4& d, float& consumer
 template <int DT, int R, int MM, int J>
 __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<R>& sc,
                                         const char* lut, uint32_t slot, const char* xa_base,
-                                        uint4& xa_cur, uint2 (&ml)[R], uint2 (&mh)[R],
-                                        float (&sf)[R][2], f32x4 (&d)[R], float (&acc)[R][MM]) {
+                                        Ahead<R>& ah, float (&sf)[R][2], f32x4 (&d)[R],
+                                        float (&acc)[R][MM]) {
     if constexpr (J % 4 == 0 && J > 0) {
         // scale group J/4 - 1 is complete in d
 #pragma unroll
@@ -696,25 +753,16 @@ __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<
 #pragma unroll
         for (int r = 0; r < R; ++r) scale_pair_f32<DT>(sc.sc[r][J / 8], sf[r][0], sf[r][1]);
     }
-    uint4 xa_nxt;
-    uint2 ml_n[R], mh_n[R];
-    if constexpr (J + 1 < 32) {
-        xa_nxt = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + 1));
-        wide_lut<R, J + 1>(w, lut, slot, ml_n, mh_n);
+    constexpr bool kFresh = J + kLookahead < 32;
+    uint4 xa_n, b_n[R];
+    if constexpr (kFresh) {
+        xa_n = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + kLookahead));
+        codes_lut4<R, 12, (kFresh ? J + kLookahead : 0)>(w.cd, lut, slot, b_n);
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint4 b = make_uint4(ml[r].x, ml[r].y, mh[r].x, mh[r].y);
-        d[r] = mfma16<DT>(xa_cur, b, J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[r]);
-    }
-    if constexpr (J + 1 < 32) {
-        xa_cur = xa_nxt;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ml[r] = ml_n[r];
-            mh[r] = mh_n[r];
-        }
-    }
+    for (int r = 0; r < R; ++r)
+        d[r] = mfma16<DT>(ah.xa[0], ah.b[0][r], J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[r]);
+    if constexpr (J + 1 < 32) ahead_shift<R>(ah, xa_n, b_n, kFresh);
     if constexpr (J == 31) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -729,22 +777,20 @@ __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<
 template <int DT, int R, int MM, int... J>
 __device__ __forceinline__ void ps_steps(const WideCodes<R>& w, const WideScales<R>& sc,
                                          const char* lut, uint32_t slot, const char* xa_base,
-                                         uint4& xa, uint2 (&ml)[R], uint2 (&mh)[R],
-                                         float (&sf)[R][2], f32x4 (&d)[R], float (&acc)[R][MM],
-                                         std::integer_sequence<int, J...>) {
-    (ps_step<DT, R, MM, J>(w, sc, lut, slot, xa_base, xa, ml, mh, sf, d, acc), ...);
+                                         Ahead<R>& ah, float (&sf)[R][2], f32x4 (&d)[R],
+                                         float (&acc)[R][MM], std::integer_sequence<int, J...>) {
+    (ps_step<DT, R, MM, J>(w, sc, lut, slot, xa_base, ah, sf, d, acc), ...);
 }
 
 template <int DT, int R, int MM>
 __device__ __forceinline__ void ps_round(const WideCodes<R>& w, const WideScales<R>& sc,
                                          const char* lut, uint32_t slot, const char* xa_base,
                                          float (&acc)[R][MM]) {
-    uint4 xa = *reinterpret_cast<const uint4*>(xa_base);
-    uint2 ml[R], mh[R];
+    Ahead<R> ah;
     float sf[R][2];
     f32x4 d[R];
-    wide_lut<R, 0>(w, lut, slot, ml, mh);
-    ps_steps<DT, R, MM>(w, sc, lut, slot, xa_base, xa, ml, mh, sf, d, acc,
+    ahead_fill<R, 12>(ah, w.cd, lut, slot, xa_base);
+    ps_steps<DT, R, MM>(w, sc, lut, slot, xa_base, ah, sf, d, acc,
                         std::make_integer_sequence<int, 32>{});
 }
 
@@ -899,7 +945,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
 bool gemv_shape_ok(int64_t N, int64_t K) {
     // buffer offsets and record counts are 32-bit: every byte offset of the layer (plus
     // the row padding of the last tile set) must stay below 2^31
-    return N >= 1 && K >= kChunk && K % kChunk == 0 && (N + 64) * (K * 3 / 16) < (1ll << 31) &&
+    return N >= 1 && K >= kChunk && K % kChunk == 0 && (N + 512) * (K * 3 / 16) < (1ll << 31) &&
            16 * K * 2 < (1ll << 31);
 }
 
@@ -924,8 +970,8 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.R = p.mmax == 16 ? 2 : kPsTiles;
         // post-scaled kernel: consecutive tile groups per workgroup
         p.C = p.mmax == 16 ? 1 : kPsChunk;
-        // waves sharing one table copy and one activation stage (measured best on MI355X)
-        p.W = p.mmax == 16 ? 16 : kPsWaves;
+        // waves sharing one table copy and one activation stage
+        p.W = p.mmax == 16 ? kMaskWaves : kPsWaves;
     } else {
         // small layers: split K inside the workgroup to get enough waves
         p.wide = false;
@@ -951,9 +997,9 @@ static hipError_t launch_rs(const GemvLaunch& a, int64_t wgs, hipStream_t stream
     return hipGetLastError();
 }
 
-template <int DT, int R, int MMAX, int W>
-static hipError_t launch_wide(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_wide_kernel<DT, R, MMAX, W>), dim3((unsigned)wgs), dim3(64 * W), 0,
+template <int DT, int MMAX, int W>
+static hipError_t launch_mask(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
+    hipLaunchKernelGGL((gemv_mask_kernel<DT, MMAX, W>), dim3((unsigned)wgs), dim3(64 * W), 0,
                        stream, a);
     return hipGetLastError();
 }
@@ -976,7 +1022,8 @@ static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
             return launch_ps<DT, kPsTiles, 1, kPsWaves>(a, p, wgs, stream);
         if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 4)
             return launch_ps<DT, kPsTiles, 4, kPsWaves>(a, p, wgs, stream);
-        if (p.W == 16 && p.R == 2 && p.mmax == 16) return launch_wide<DT, 2, 16, 16>(a, wgs, stream);
+        if (p.W == kMaskWaves && p.R == 2 && p.mmax == 16)
+            return launch_mask<DT, 16, kMaskWaves>(a, wgs, stream);
         return hipErrorInvalidValue;
     }
     if (p.R == 1 && p.S == 2) return launch_rs<DT, 1, 2>(a, wgs, stream);

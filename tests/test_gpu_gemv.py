@@ -169,9 +169,11 @@ def test_wide_kernel_partial_rounds_and_ragged_rows(M, K):
     assert _rel(y, ref) <= REL_TOL
 
 
-def test_wide_kernel_fp16_and_subnormal_scales():
+@pytest.mark.parametrize("M", [4, 12])
+def test_wide_kernel_fp16_and_subnormal_scales(M):
     # tiny weights give fp16-subnormal group scales; fp16 activations keep them exactly
-    N, K, M = 16 * 1024, 512, 4
+    # (M = 4: post-scaled kernel, M = 12: mask kernel)
+    N, K = 16 * 1024, 512
     pk, sc, pk_np, sc_np = _encoded(N, K, seed=77, scale=2e-6)
     assert (np.abs(sc_np.view(np.float16).astype(np.float32)) < 6.1e-5).mean() > 0.5
     x = _x(M, K, seed=78, dtype=torch.float16)
