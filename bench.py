@@ -58,6 +58,20 @@ DECODE_M = (1, 4, 16)
 PREFILL_M = (512, 2048, 8192)
 
 
+def measured_traffic():
+    """HBM bytes per grouped decode-GEMV launch (mean over M = 1, 4, 16) from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary, calibrated against a copy kernel of known
+    size; None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_gemv_traffic.md")
+    try:
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        data = json.loads(block)
+        return int(data["traffic_bytes_per_launch"]), data
+    except (OSError, IndexError, KeyError, ValueError):
+        return None, None
+
+
 def weight_bytes(N: int, K: int) -> int:
     return N * K * 3 // 16 + (N * K // GS) * 2
 
@@ -725,7 +739,11 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic()[0],
+            "traffic_note": ("HBM bytes per launch (mean over the M = 1, 4, 16 launches) from "
+                             "rocprofv3 FETCH_SIZE/WRITE_SIZE scaled by a copy-kernel "
+                             "calibration: profiles/decode_gemv_traffic.md; algorithmic bytes "
+                             "per launch (mean) = " + str(int(dec["alg_bytes"] / dec["launches"]))),
         },
     }
 
