@@ -28,32 +28,47 @@
 
 namespace ojx {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kWaves = 8;                  // 2 (M) x 4 (N) waves, 128 x 64 each
-constexpr int kGemmThreads = 64 * kWaves;
-constexpr int kWM = 128, kWN = 64;         // wave tile
-constexpr int kTM = kWM / 16, kTN = kWN / 16;  // 8 x 4 MFMA tiles per wave
-constexpr int kTileBytes = kBM * kBK * 2;  // 32 KB per operand tile
+constexpr int kBK = 64;
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
+
+// Tile configuration: BM x BN output tile per workgroup, WAVES_M x WAVES_N waves of
+// (BM / WAVES_M) x (BN / WAVES_N) each.  Two threads decode each weight row of the tile.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_>
+struct GemmCfg {
+    static constexpr int BM = BM_, BN = BN_;
+    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, WAVES = WAVES_M_ * WAVES_N_;
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
+    static constexpr int TM = WM / 16, TN = WN / 16;            // MFMA tiles per wave
+    static constexpr int XTILE = BM * kBK * 2, WTILE = BN * kBK * 2;  // bytes per operand tile
+    static constexpr int XLOADS = BM / (8 * WAVES);             // 1-KB X loads per wave
+    static_assert(THREADS == 2 * BN, "two threads per weight row");
+    static_assert(XLOADS * 8 * WAVES == BM, "X tile rows split evenly over the waves");
+    static_assert(TM >= 4, "decode writes are spread over the last four MFMA rows");
+};
+using CfgLarge = GemmCfg<256, 256, 2, 4>;  // 8 waves of 128 x 64: large grids
+using CfgSmall = GemmCfg<128, 128, 2, 2>;  // 4 waves of 64 x 64: grids under one wave
 
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t piece) {
     return row * 128u + 16u * (piece ^ ((row >> 1) & 7u));
 }
 
-// X tile rows [m0, m0+256) x k [k0, k0+64) -> LDS tile (swizzled); each of the 8 waves
-// issues 4 1-KB loads (8 rows each).  Rows >= M read past the buffer's end: zeros.
+// X tile rows [m0, m0+BM) x k [k0, k0+64) -> LDS tile (swizzled); each wave issues
+// `loads` 1-KB loads (8 rows each).  Rows >= M read past the buffer's end: zeros.
 __device__ __forceinline__ void load_x_tile(char* tile, __amdgpu_buffer_rsrc_t x, int64_t m0,
-                                            int64_t k0, int64_t K, int wave, int lane) {
+                                            int64_t k0, int64_t K, int wave, int lane,
+                                            int loads) {
     const uint32_t r_in = (uint32_t)lane >> 3, q = (uint32_t)lane & 7u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t row = 32u * wave + 8u * i + r_in;
+    for (int i = 0; i < loads; ++i) {
+        const uint32_t row0 = 8u * (uint32_t)(loads * wave + i);
+        const uint32_t row = row0 + r_in;
         const uint32_t p = q ^ ((row >> 1) & 7u);
         const uint32_t voff = (uint32_t)((m0 + row) * K * 2 + 16u * p);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            x, (__attribute__((address_space(3))) void*)(tile + (32 * wave + 8 * i) * 128), 16,
-            voff, uniform_offset(k0 * 2), 0, 0);
+            x, (__attribute__((address_space(3))) void*)(tile + row0 * 128), 16, voff,
+            uniform_offset(k0 * 2), 0, 0);
     }
 }
 
@@ -104,10 +119,10 @@ __device__ __forceinline__ void decode_half(const RowCodes& rc, const char* lut,
     }
 }
 
-template <int DT>
-__device__ __forceinline__ void mma_row(const uint4& a, const uint4 (&b)[kTN], f32x4 (&acc)[kTN]) {
+template <int DT, int TN>
+__device__ __forceinline__ void mma_row(const uint4& a, const uint4 (&b)[TN], f32x4 (&acc)[TN]) {
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) acc[j] = mfma16<DT>(a, b[j], acc[j]);
+    for (int j = 0; j < TN; ++j) acc[j] = mfma16<DT>(a, b[j], acc[j]);
 }
 
 // Fragment addresses.  Rows of a wave's A (B) fragments are arow0 + 16i + i16 (brow0 +
@@ -128,14 +143,15 @@ __device__ __forceinline__ FragLane frag_lane(uint32_t arow0, uint32_t brow0, in
     return f;
 }
 
+template <int TM, int TN>
 __device__ __forceinline__ void load_frags(const char* xt, const char* wt, const FragLane& f,
-                                           int sub, uint4 (&a)[kTM], uint4 (&b)[kTN]) {
+                                           int sub, uint4 (&a)[TM], uint4 (&b)[TN]) {
     const char* pa = xt + f.a[sub];
     const char* pb = wt + f.b[sub];
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) a[i] = *reinterpret_cast<const uint4*>(pa + 2048 * i);
+    for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const uint4*>(pa + 2048 * i);
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) b[j] = *reinterpret_cast<const uint4*>(pb + 2048 * j);
+    for (int j = 0; j < TN; ++j) b[j] = *reinterpret_cast<const uint4*>(pb + 2048 * j);
 }
 
 // Table reads of code j (0..7) of this thread's row (two 8-byte masks).
@@ -165,27 +181,27 @@ __device__ __forceinline__ void lut_reads_half(const RowCodes& rc, const char* l
     }
 }
 
-// One K step (64) of the wave's 128x64 block.
+// One K step (64) of the wave's block.
 //   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read;
 //   2. table reads for this thread's 4 codes of the NEXT step's weight row (their codes
 //      arrived a full step ago), then `rc` is re-armed with the codes of the step after;
-//   3. sub-step 1; in its second half the masked weight pairs of the next step are
-//      written to the other LDS buffer (the table reads were issued 4 MFMA rows earlier).
-template <int DT>
+//   3. sub-step 1; in its last four MFMA rows the masked weight pairs of the next step are
+//      written to the other LDS buffer.
+template <int DT, int TM, int TN>
 __device__ __forceinline__ void kstep(const char* xt, const char* wt, const FragLane& fl,
-                                      uint4 (&a0)[kTM], uint4 (&b0)[kTN], uint4 (&a1)[kTM],
-                                      uint4 (&b1)[kTN], RowCodes& rc, const char* lut,
+                                      uint4 (&a0)[TM], uint4 (&b0)[TN], uint4 (&a1)[TM],
+                                      uint4 (&b1)[TN], RowCodes& rc, const char* lut,
                                       uint32_t slot, char* wt_next, uint32_t wrow, int half,
-                                      f32x4 (&acc)[kTM][kTN], __amdgpu_buffer_rsrc_t pr,
+                                      f32x4 (&acc)[TM][TN], __amdgpu_buffer_rsrc_t pr,
                                       __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
                                       uint32_t vo_scale, int64_t k_reload) {
     const char* pa1 = xt + fl.a[1];
     const char* pb1 = wt + fl.b[1];
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) b1[j] = *reinterpret_cast<const uint4*>(pb1 + 2048 * j);
+    for (int j = 0; j < TN; ++j) b1[j] = *reinterpret_cast<const uint4*>(pb1 + 2048 * j);
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-        mma_row<DT>(a0[i], b0, acc[i]);
+    for (int i = 0; i < TM; ++i) {
+        mma_row<DT, TN>(a0[i], b0, acc[i]);
         a1[i] = *reinterpret_cast<const uint4*>(pa1 + 2048 * i);
     }
     uint2 ml[4], mh[4];
@@ -195,11 +211,12 @@ __device__ __forceinline__ void kstep(const char* xt, const char* wt, const Frag
     const uint32_t sw = half ? w1 : w0;
     load_codes_row(rc, pr, sr, vo_code, vo_scale, k_reload);
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-        mma_row<DT>(a1[i], b1, acc[i]);
-        if (i >= 4) {  // the table reads were issued 4 MFMA rows ago
-            *reinterpret_cast<uint4*>(wt_next + swz(wrow, 4u * half + (i - 4))) = make_uint4(
-                ml[i - 4].x & sw, ml[i - 4].y & sw, mh[i - 4].x & sw, mh[i - 4].y & sw);
+    for (int i = 0; i < TM; ++i) {
+        mma_row<DT, TN>(a1[i], b1, acc[i]);
+        if (i >= TM - 4) {  // the table reads were issued TM - 4 MFMA rows earlier
+            const int p = i - (TM - 4);
+            *reinterpret_cast<uint4*>(wt_next + swz(wrow, 4u * half + p)) = make_uint4(
+                ml[p].x & sw, ml[p].y & sw, mh[p].x & sw, mh[p].y & sw);
         }
     }
 }
@@ -208,19 +225,20 @@ __device__ __forceinline__ void vm_wait_le2() {
     __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): all but the two newest loads (gfx9)
 }
 
-template <int DT>
-__global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
+template <int DT, typename C>
+__global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     int64_t M, int64_t N, int64_t K) {
     __shared__ uint4 lut_storage[kLutStorageU4];
-    __shared__ __attribute__((aligned(16))) char xs[2][kTileBytes];
-    __shared__ __attribute__((aligned(16))) char ws[2][kTileBytes];
+    __shared__ __attribute__((aligned(16))) char xs[2][C::XTILE];
+    __shared__ __attribute__((aligned(16))) char ws[2][C::WTILE];
+    constexpr int kTM = C::TM, kTN = C::TN;
 
-    fill_lut<kGemmThreads>(lut_storage, kLutMasks);
+    fill_lut<C::THREADS>(lut_storage, kLutMasks);
 
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
-    const int64_t tm_n = (M + kBM - 1) / kBM, tn_n = (N + kBN - 1) / kBN;
+    const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (N + C::BN - 1) / C::BN;
     const int64_t tiles = tm_n * tn_n;
     const int64_t bid = blockIdx.x;
     const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
@@ -236,14 +254,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
     const int64_t gsize = (tm_n - first_m) < kGroupM ? (tm_n - first_m) : kGroupM;
     const int64_t tm = first_m + (t % (kGroupM * tn_n)) % gsize;
     const int64_t tn = (t % (kGroupM * tn_n)) / gsize;
-    const int64_t m0 = tm * kBM, n0 = tn * kBN;
+    const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, i16 = lane & 15;
-    const uint32_t arow0 = (uint32_t)kWM * (uint32_t)(wave >> 2);
-    const uint32_t brow0 = (uint32_t)kWN * (uint32_t)(wave & 3);
+    const uint32_t arow0 = (uint32_t)C::WM * (uint32_t)(wave / C::WAVES_N);
+    const uint32_t brow0 = (uint32_t)C::WN * (uint32_t)(wave % C::WAVES_N);
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
@@ -269,7 +287,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
     // ahead of the MFMAs.  Branch-free body: loads past the last step fetch bytes past the
     // operands (zeros, or the next row's data) into buffers that are never read.
     RowCodes rc;
-    load_x_tile(xs[0], xr, m0, 0, K, wave, lane);
+    load_x_tile(xs[0], xr, m0, 0, K, wave, lane, C::XLOADS);
     load_codes_row(rc, pr, sr, vo_code, vo_scale, 0);
     __syncthreads();  // table ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
@@ -283,9 +301,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(
     load_frags(xs[0], ws[0], fl, 0, a0, b0);
     for (int64_t s = 0; s < steps; ++s) {
         const int cur = (int)(s & 1), nxt = cur ^ 1;
-        load_x_tile(xs[nxt], xr, m0, (s + 1) * kBK, K, wave, lane);
-        kstep<DT>(xs[cur], ws[cur], fl, a0, b0, a1, b1, rc, lut, slot, ws[nxt], wrow, half, acc,
-                  pr, sr, vo_code, vo_scale, (s + 2) * kBK);
+        load_x_tile(xs[nxt], xr, m0, (s + 1) * kBK, K, wave, lane, C::XLOADS);
+        kstep<DT, kTM, kTN>(xs[cur], ws[cur], fl, a0, b0, a1, b1, rc, lut, slot, ws[nxt], wrow,
+                            half, acc, pr, sr, vo_code, vo_scale, (s + 2) * kBK);
         vm_wait_le2();  // the X tile of step s+1 has landed; the code loads may still fly
         __syncthreads();
         load_frags(xs[nxt], ws[nxt], fl, 0, a0, b0);
@@ -316,22 +334,40 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
         return false;
     // 32-bit buffer offsets: the activation matrix and the weight buffers (plus one tile
     // of padding rows) must stay below 2^31 bytes
-    if ((M + kBM) * K * 2 >= (1ll << 31) || (N + kBN) * (K * 3 / 16) >= (1ll << 31)) return false;
+    if ((M + CfgLarge::BM) * K * 2 >= (1ll << 31) ||
+        (N + CfgLarge::BN) * (K * 3 / 16) >= (1ll << 31))
+        return false;
     return true;
+}
+
+// Grids of large tiles that leave CUs idle (under about one workgroup per CU) run the
+// small-tile configuration, which has four times the tiles and two workgroups per CU.
+#ifndef OJX_GEMM_SMALL_BELOW
+#define OJX_GEMM_SMALL_BELOW 192
+#endif
+
+template <int DT, typename C>
+static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_t* scales,
+                             const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                             hipStream_t stream) {
+    const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
+    if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C>), dim3((unsigned)tiles), dim3(C::THREADS), 0,
+                       stream, x, packed, scales, bias, y, M, N, K);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, int64_t M, int64_t N, int64_t K, int dt,
                             hipStream_t stream) {
-    const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-    if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const int64_t large = ((M + CfgLarge::BM - 1) / CfgLarge::BM) *
+                          ((N + CfgLarge::BN - 1) / CfgLarge::BN);
+    const bool small = large < OJX_GEMM_SMALL_BELOW;
     if (dt == kBF16)
-        hipLaunchKernelGGL((gemm_mfma_kernel<kBF16>), dim3((unsigned)tiles), dim3(kGemmThreads), 0,
-                           stream, x, packed, scales, bias, y, M, N, K);
-    else
-        hipLaunchKernelGGL((gemm_mfma_kernel<kF16>), dim3((unsigned)tiles), dim3(kGemmThreads), 0,
-                           stream, x, packed, scales, bias, y, M, N, K);
-    return hipGetLastError();
+        return small ? launch_cfg<kBF16, CfgSmall>(x, packed, scales, bias, y, M, N, K, stream)
+                     : launch_cfg<kBF16, CfgLarge>(x, packed, scales, bias, y, M, N, K, stream);
+    return small ? launch_cfg<kF16, CfgSmall>(x, packed, scales, bias, y, M, N, K, stream)
+                 : launch_cfg<kF16, CfgLarge>(x, packed, scales, bias, y, M, N, K, stream);
 }
 
 }  // namespace ojx
