@@ -940,6 +940,112 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     }
 }
 
+// ------------------------------------------------------------------------- small-layer kernel
+//
+// Post-scaled kernel for launches with few row tiles and M <= 4 (per-linear decode of
+// q/k/v/o/down-sized layers): one 16-row tile per workgroup, whose W waves take the 1024-k
+// rounds u = w, w + W, ... of that tile.  Each wave stages its own round's codes (coalesced,
+// as above) and activations in LDS and waits only for its own loads; the waves' partial sums
+// are added through LDS at the end.  A layer's weights are thus requested almost at once:
+// a q/o-sized layer (256 tiles) occupies 256 workgroups for about one memory round trip,
+// instead of a chain of dependent activation loads per chunk.
+
+template <int DT, int MM, int W>
+__global__ __launch_bounds__(64 * W) void gemv_psk_kernel(GemvLaunch args) {
+    static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
+    constexpr int R = 1;
+    __shared__ uint4 lut_storage[kLutValidStorageU4];
+    __shared__ __attribute__((aligned(16))) char stage[W][3072];
+    __shared__ __attribute__((aligned(16))) char xs[W][MM * kXRow];
+    __shared__ __attribute__((aligned(16))) uint4 xzero[32];
+    __shared__ float red[W][MM][64];
+
+    fill_lut<64 * W, kLutValidEntries>(lut_storage, lut_values_kind<DT>());
+    if (threadIdx.x < 32) xzero[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+
+    int64_t wg = blockIdx.x;
+    GemvJob job;
+    if (args.jobs != nullptr) {
+        job = args.jobs[find_job(args.jobs, args.njobs, wg)];
+    } else {
+        job = args.inl[0];
+#pragma unroll
+        for (int i = 1; i < kGemvInlineJobs; ++i)
+            if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
+    }
+    wg -= job.wg_begin;
+    const void* xbase = job.x ? job.x : args.x;
+    void* ybase = job.y ? job.y : args.y;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
+    const int64_t N = job.N, K = job.K;
+    const int M = args.M;
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
+    const uint32_t srowbytes = (uint32_t)(K / 16);
+    const int64_t tile0 = wg;
+    const uint32_t row0 = (uint32_t)(tile0 * 16);
+
+    PsStream<R> st;
+    st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
+                                                  (int)(N * rowbytes), kRsrcWord3);
+    st.scales = __builtin_amdgcn_make_buffer_rsrc((void*)job.scales, (short)0,
+                                                  (int)(N * srowbytes), kRsrcWord3);
+    st.x = __builtin_amdgcn_make_buffer_rsrc((void*)xbase, (short)0, (int)(M * K * 2),
+                                             kRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const uint32_t s = 64u * i + lane;  // stage slot: row n, block position q, piece t
+        const uint32_t n = s / 12u, pos = s % 12u, q = pos / 3u, t = pos % 3u;
+        const uint32_t gg = (q - ps_tau(n)) & 3u;
+        st.ld_code[i] = (row0 + n) * rowbytes + 16u * (3u * gg + t);
+    }
+    st.vo_scale[0] = (row0 + i16) * srowbytes + 16u * g;
+    const uint32_t q_me = ((uint32_t)g + ps_tau((uint32_t)i16)) & 3u;
+    st.rd_code = (12u * i16 + 3u * q_me) * 16u;
+    const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+
+    // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
+    const int am = i16 & 3;
+    const bool a_live = (i16 >> 2) == g && am < M;
+    const char* xa = a_live ? xs[wave] + am * kXRow + 512 * g
+                            : reinterpret_cast<const char*>(xzero);
+
+    const int T = (int)((K + kRound - 1) / kRound);
+    float acc[R][MM];
+#pragma unroll
+    for (int q = 0; q < MM; ++q) acc[0][q] = 0.f;
+
+    __syncthreads();  // table and zero block ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
+    char* const stg_bytes = stage[wave];
+    const PsStage<R>& stg = *reinterpret_cast<const PsStage<R>*>(stage[wave]);
+
+    for (int u = wave; u < T; u += W) {  // uniform within the wave
+        lds_wait_all();  // the previous round's reads of the stage and x buffer have landed
+        ps_issue(stg_bytes, st.packed, st.ld_code, R, 0, u);
+        WideScales<R> sc;
+        ps_load_scales<R>(sc, st, 0, u, K, g);
+        stage_x(xs[wave], st.x, u, M, K, 0, lane, 1);
+        vm_wait_all();
+        WideCodes<R> w;
+        ps_readback<R>(stg, st, w);
+        ps_round<DT, R, MM>(w, sc, lut, slot, xa, acc);
+    }
+
+#pragma unroll
+    for (int q = 0; q < MM; ++q) red[wave][q][lane] = acc[0][q];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w2 = 1; w2 < W; ++w2)
+#pragma unroll
+        for (int q = 0; q < MM; ++q) acc[0][q] += red[w2][q][lane];
+    ps_store<DT, R, MM>(job, ybase, M, tile0, lane, acc);
+}
+
 // ------------------------------------------------------------------------- host side
 
 bool gemv_shape_ok(int64_t N, int64_t K) {
@@ -960,7 +1066,7 @@ bool gemv_supported(const void* x, const uint8_t* packed, const uint16_t* scales
 }
 
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
-    GemvPlan p;
+    GemvPlan p{};
     if (total_tiles >= 1024) {
         // enough row tiles to fill the GPU with one tile set per wave: streaming kernel
         p.wide = true;
@@ -972,6 +1078,15 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.C = p.mmax == 16 ? 1 : kPsChunk;
         // waves sharing one table copy and one activation stage
         p.W = p.mmax == 16 ? kMaskWaves : kPsWaves;
+    } else if (M <= 4) {
+        // small layers, M <= 4: one tile per workgroup, rounds split over its waves
+        p.wide = false;
+        p.split_ps = true;
+        p.C = 1;
+        p.R = 1;
+        p.S = 1;
+        p.W = 4;
+        p.mmax = M == 1 ? 1 : 4;
     } else {
         // small layers: split K inside the workgroup to get enough waves
         p.wide = false;
@@ -986,7 +1101,9 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
 
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p) {
     const int64_t tiles = (N + 15) / 16;
-    const int64_t per_wg = p.wide ? (int64_t)p.W * p.R * p.C : (int64_t)(4 / p.S) * p.R;
+    const int64_t per_wg = p.split_ps ? 1
+                           : p.wide   ? (int64_t)p.W * p.R * p.C
+                                      : (int64_t)(4 / p.S) * p.R;
     return (tiles + per_wg - 1) / per_wg;
 }
 
@@ -1014,9 +1131,20 @@ static hipError_t launch_ps(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
     return hipGetLastError();
 }
 
+template <int DT, int MM>
+static hipError_t launch_psk(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
+    hipLaunchKernelGGL((gemv_psk_kernel<DT, MM, 4>), dim3((unsigned)wgs), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <int DT>
 static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                             hipStream_t stream) {
+    if (p.split_ps) {
+        if (p.mmax == 1) return launch_psk<DT, 1>(a, wgs, stream);
+        if (p.mmax == 4) return launch_psk<DT, 4>(a, wgs, stream);
+        return hipErrorInvalidValue;
+    }
     if (p.wide) {
         if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 1)
             return launch_ps<DT, kPsTiles, 1, kPsWaves>(a, p, wgs, stream);

@@ -63,6 +63,7 @@ struct GemvPlan {
     int W;       // waves per workgroup (wide only)
     int mmax;    // activation rows staged in LDS (wide only): 1, 4 (post-scaled) or 16
     int C;       // consecutive tile groups per workgroup (post-scaled kernel; else 1)
+    bool split_ps;  // small-layer post-scaled kernel: one tile per workgroup, K split over waves
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
