@@ -96,6 +96,7 @@ def parse_args():
     ap.add_argument("--no-encode", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-layers", type=int, default=32)
+    ap.add_argument("--encode-layers", type=int, default=32)
     ap.add_argument("--decode-m", type=str, default=",".join(map(str, DECODE_M)),
                     help="decode batch sizes of the headline step (profiling runs pick one)")
     ap.add_argument("--no-per-linear", action="store_true",
@@ -308,37 +309,84 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev):
 
 # --------------------------------------------------------------------------- encoder
 
-def bench_encode(torch, ops, dev, target_s: float = 0.1):
-    """configs[3] per layer: fp16 N(0, 0.02) weights with 0.1% +-8 sigma outliers."""
-    out = {}
-    tot_w = 0
-    tot_ms = 0.0
+def bench_encode(torch, N_, dev, layers: int, reps: int = 3, check_rows: int = 64):
+    """encode a `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights
+    with 0.1% of entries set to +-8 sigma (seed 9000 + 7*layer + j), layer by layer: one
+    encode launch per linear, the whole stack replayed from one hipGraph.  One layer of each
+    shape is checked bit for bit against the CPU oracle on its first `check_rows` rows, and
+    the oracle's own encode rate on one q-shaped layer is reported beside it."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    lib = N_.lib()
+    t0 = time.time()
+    items = []
+    for layer in range(layers):
+        for j, (name, N, K) in enumerate(LAYER_SHAPES):
+            g = torch.Generator(device=dev).manual_seed(9000 + 7 * layer + j)
+            w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+            nout = w.numel() // 1000
+            idx = torch.randperm(w.numel(), generator=g, device=dev)[:nout]
+            sign = torch.where(torch.rand(nout, generator=g, device=dev) < 0.5, -1.0, 1.0)
+            w.view(-1)[idx] = (0.16 * sign).half()
+            del idx, sign
+            packed = torch.empty(N * K * 3 // 16, dtype=torch.uint8, device=dev)
+            scales = torch.empty(N * K // GS, dtype=torch.float16, device=dev)
+            items.append((w, packed, scales, name, N, K))
+    torch.cuda.synchronize()
+    gen_s = time.time() - t0
+    numel = sum(it[4] * it[5] for it in items)
+
+    def launch_all(h):
+        for w, pk, sc, _, _, _ in items:
+            N_.check(lib.ojx_e8t_encode(w.data_ptr(), N_.F16, w.numel(), GS, pk.data_ptr(),
+                                        sc.data_ptr(), h), "encode")
+
     stream = torch.cuda.current_stream()
-    for j, (name, N, K) in enumerate(LAYER_SHAPES):
-        g = torch.Generator(device=dev).manual_seed(9000 + j)
-        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
-        idx = torch.randperm(w.numel(), generator=g, device=dev)[: w.numel() // 1000]
-        sign = torch.where(torch.rand(idx.numel(), generator=g, device=dev) < 0.5, -1.0, 1.0)
-        w.view(-1)[idx] = (0.16 * sign).half()
-        ops.encode(w, GS)
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        iters = 5
-        a.record(stream)
-        for _ in range(iters):
-            ops.encode(w, GS)
-        b.record(stream)
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / iters
-        numel = N * K
-        out[name] = dict(ms=round(ms, 4), Gweights_s=round(numel / ms / 1e6, 2),
-                         GBs=round(numel * 2.25 / ms / 1e6, 1))
-        tot_w += numel
-        tot_ms += ms
-    return dict(layers=out, Gweights_s=round(tot_w / tot_ms / 1e6, 2),
-                GBs=round(tot_w * 2.25 / tot_ms / 1e6, 1),
-                frac_hbm=round(tot_w * 2.25 / tot_ms / 1e6 / HBM_PEAK_GBS, 4))
+    launch_all(stream.cuda_stream)
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        launch_all(torch.cuda.current_stream().cuda_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+
+    # bit-exactness sample: the first check_rows rows of layer 0 of each shape
+    exact = True
+    for w, pk, sc, name, N, K in items[:7]:
+        rows = min(check_rows, N)
+        ref_pk, ref_sc, _ = O.encode(w[:rows].float().cpu().numpy(), GS)
+        got_pk = pk[: rows * K * 3 // 16].cpu().numpy()
+        got_sc = sc[: rows * K // GS].cpu().view(torch.int16).numpy().view(np.uint16)
+        exact = exact and np.array_equal(got_pk, ref_pk) and np.array_equal(got_sc, ref_sc)
+
+    # the CPU oracle's encode rate (host cores) on one q-shaped layer of the stack
+    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+    wq = items[0][0].float().cpu().numpy()
+    O.encode(wq[:64], GS, cores)
+    t1 = time.perf_counter()
+    O.encode(wq, GS, cores)
+    cpu_s = time.perf_counter() - t1
+    del items
+    torch.cuda.empty_cache()
+    return dict(layers=layers, linears=7 * layers, weights=numel, ms=round(ms, 3),
+                Gweights_s=round(numel / ms / 1e6, 1), GBs=round(numel * 2.25 / ms / 1e6, 1),
+                frac_hbm=round(numel * 2.25 / ms / 1e6 / HBM_PEAK_GBS, 4),
+                bytes_per_weight=2.25, bit_exact_sample=exact,
+                sample=f"first {check_rows} rows of layer 0 of each shape vs oracle/e8t_oracle.c",
+                generate_s=round(gen_s, 1),
+                cpu_oracle=dict(Gweights_s=round(wq.size / cpu_s / 1e9, 3), cores=cores,
+                                sample="one 4096x4096 layer, oracle/e8t_oracle.c (OpenMP)"))
 
 
 # --------------------------------------------------------------------------- end-to-end decoder
@@ -755,9 +803,10 @@ def main() -> int:
     if not args.no_encode:
         del stack
         torch.cuda.empty_cache()
-        log("encode timing")
-        result["encode"] = bench_encode(torch, ops, dev)
-        log(f"encode: {result['encode']['Gweights_s']} Gweights/s")
+        log(f"encode timing ({args.encode_layers}-layer stack)")
+        result["encode"] = bench_encode(torch, N_, dev, args.encode_layers)
+        log(f"encode: {result['encode']['Gweights_s']} Gweights/s, "
+            f"bit-exact sample {result['encode']['bit_exact_sample']}")
     if not args.no_e2e:
         torch.cuda.empty_cache()
         log(f"end-to-end decoder ({args.e2e_layers} layers)")

@@ -86,23 +86,43 @@ static __device__ const LutBase kLutBaseTab[3] = {
 // slice c at byte offset (e + kLutGuard) * kLutStride + c * 8 of the storage.  Each thread writes
 // 16-byte items (two slices of one entry); its base-table loads are all issued before its
 // first write.  NT: threads of the workgroup.
+// Items (16-byte words, two slices of one entry) each thread of an NT-thread workgroup
+// writes for a table of ENTRIES entries.
+template <int NT, int ENTRIES>
+struct LutFill {
+    static constexpr int kPairs = kLutSlots / 2;
+    static constexpr int kItems = (ENTRIES + kLutGuard) * kPairs;
+    static constexpr int kPer = (kItems + NT - 1) / NT;
+    uint2 v[kPer];
+
+    // Issues this thread's base-table loads (device memory; an L2 hit after the first
+    // workgroup).  Kernels issue their first weight loads between load() and store(), so
+    // the two latencies overlap.
+    __device__ __forceinline__ void load(int kind) {
+        const uint2* tab = reinterpret_cast<const uint2*>(kLutBaseTab[kind].w);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = (int)threadIdx.x + k * NT;
+            v[k] = tab[(i < kItems ? i : 0) / kPairs + 1 - kLutGuard];
+        }
+    }
+    __device__ __forceinline__ void store(uint4* storage) const {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = (int)threadIdx.x + k * NT;
+            if (i < kItems) storage[i] = make_uint4(v[k].x, v[k].y, v[k].x, v[k].y);
+        }
+    }
+};
+
+// Fills the bank-sliced table from the base table in device memory: entry e (-1 = guard),
+// slice c at byte offset (e + kLutGuard) * kLutStride + c * 8 of the storage.  NT: threads
+// of the workgroup.
 template <int NT, int ENTRIES = kLutEntries>
 __device__ __forceinline__ void fill_lut(uint4* storage, int kind) {
-    constexpr int kPairs = kLutSlots / 2;
-    constexpr int kItems = (ENTRIES + kLutGuard) * kPairs;
-    constexpr int kPer = (kItems + NT - 1) / NT;
-    const uint2* tab = reinterpret_cast<const uint2*>(kLutBaseTab[kind].w);
-    uint2 v[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int i = (int)threadIdx.x + k * NT;
-        v[k] = i < kItems ? tab[i / kPairs + 1 - kLutGuard] : make_uint2(0u, 0u);
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int i = (int)threadIdx.x + k * NT;
-        if (i < kItems) storage[i] = make_uint4(v[k].x, v[k].y, v[k].x, v[k].y);
-    }
+    LutFill<NT, ENTRIES> f;
+    f.load(kind);
+    f.store(storage);
 }
 
 // LDS words of the table (16-byte aligned, for the 16-byte fill writes).
