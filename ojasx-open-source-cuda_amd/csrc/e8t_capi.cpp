@@ -1,9 +1,10 @@
 // e8t_capi.cpp -- extern "C" entry points of libojasx_e8t.so (declared in
 // include/ojasx_e8t.h).  Validates arguments the way the reference's native
 // binding does (ojasx_math_bindings.cpp:17-34, 414-433), checks the device,
-// picks a kernel and enqueues it on the caller's stream.  No allocation, no
-// locks on the launch path, no mutable state other than a per-device arch
-// cache and a thread-local error message.
+// picks a kernel and enqueues it on the caller's stream.  The only mutable state
+// is a per-device arch cache, a thread-local error message and the prefill GEMM's
+// K-split scratch (e8t_workspace.cpp: allocated only when a stream's buffer must
+// grow, never during graph capture).
 
 #include <hip/hip_runtime.h>
 
@@ -142,9 +143,18 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
         return done(ojx::launch_gemv(a, plan, ojx::gemv_wgs_for(N, plan), dtype, s),
                     "e8t gemv launch");
     }
-    if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype))
-        return done(ojx::launch_gemm_mfma(x, packed, scales, bias, y, M, N, K, dtype, s),
+    if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype)) {
+        int splits = ojx::gemm_mfma_splits(M, N, K);
+        float* part = nullptr;
+        if (splits > 1) {
+            part = static_cast<float*>(ojx::stream_workspace(
+                s, (size_t)splits * (size_t)ojx::split_stride(M, N) * sizeof(float)));
+            if (!part) splits = 1;  // capturing, or no memory: the unsplit kernel
+        }
+        return done(ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, splits, M, N, K,
+                                          dtype, s),
                     "e8t gemm_mfma launch");
+    }
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                 "e8t gemm_fwd launch");
 }

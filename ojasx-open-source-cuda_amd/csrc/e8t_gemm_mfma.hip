@@ -182,19 +182,21 @@ __device__ __forceinline__ void lut_reads_half(const RowCodes& rc, const char* l
 }
 
 // One K step (64) of the wave's block.
-//   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read;
+//   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read,
+//      then the next step's X tile load is issued (issue_x);
 //   2. table reads for this thread's 4 codes of the NEXT step's weight row (their codes
 //      arrived a full step ago), then `rc` is re-armed with the codes of the step after;
 //   3. sub-step 1; in its last four MFMA rows the masked weight pairs of the next step are
 //      written to the other LDS buffer.
-template <int DT, int TM, int TN>
+template <int DT, int TM, int TN, typename IssueX>
 __device__ __forceinline__ void kstep(const char* xt, const char* wt, const FragLane& fl,
                                       uint4 (&a0)[TM], uint4 (&b0)[TN], uint4 (&a1)[TM],
                                       uint4 (&b1)[TN], RowCodes& rc, const char* lut,
                                       uint32_t slot, char* wt_next, uint32_t wrow, int half,
                                       f32x4 (&acc)[TM][TN], __amdgpu_buffer_rsrc_t pr,
                                       __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
-                                      uint32_t vo_scale, int64_t k_reload) {
+                                      uint32_t vo_scale, int64_t k_reload,
+                                      const IssueX& issue_x) {
     const char* pa1 = xt + fl.a[1];
     const char* pb1 = wt + fl.b[1];
 #pragma unroll
@@ -204,6 +206,9 @@ __device__ __forceinline__ void kstep(const char* xt, const char* wt, const Frag
         mma_row<DT, TN>(a0[i], b0, acc[i]);
         a1[i] = *reinterpret_cast<const uint4*>(pa1 + 2048 * i);
     }
+    // every read of this step's X tile is issued: the next X tile may now be loaded into
+    // the other buffer without the compiler holding a later read of this one behind it
+    issue_x();
     uint2 ml[4], mh[4];
     lut_reads_half(rc, lut, slot, half, ml, mh);
     uint32_t w0, w1;
@@ -229,7 +234,7 @@ template <int DT, typename C>
 __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int64_t M, int64_t N, int64_t K) {
+    float* __restrict__ part, int splits, int64_t M, int64_t N, int64_t K) {
     __shared__ uint4 lut_storage[kLutStorageU4];
     __shared__ __attribute__((aligned(16))) char xs[2][C::XTILE];
     __shared__ __attribute__((aligned(16))) char ws[2][C::WTILE];
@@ -240,7 +245,9 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
     const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (N + C::BN - 1) / C::BN;
     const int64_t tiles = tm_n * tn_n;
-    const int64_t bid = blockIdx.x;
+    // K split: workgroup blockIdx.x runs K steps [s_begin, s_end) of tile blockIdx.x % tiles
+    const int split = (int)(blockIdx.x / (uint32_t)tiles);
+    const int64_t bid = blockIdx.x - (int64_t)split * tiles;
     const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
     const int64_t xcd = bid % kXcds, slot_in = bid / kXcds;
     int64_t t = xcd * per_xcd + slot_in;
@@ -283,33 +290,57 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int64_t steps = K / kBK;
+    const int64_t s_begin = steps * split / splits, s_end = steps * (split + 1) / splits;
+    const int64_t k_begin = s_begin * kBK;
     // Codes run one K step ahead of the weight tile being decoded, which runs one step
     // ahead of the MFMAs.  Branch-free body: loads past the last step fetch bytes past the
     // operands (zeros, or the next row's data) into buffers that are never read.
     RowCodes rc;
-    load_x_tile(xs[0], xr, m0, 0, K, wave, lane, C::XLOADS);
-    load_codes_row(rc, pr, sr, vo_code, vo_scale, 0);
+    load_x_tile(xs[0], xr, m0, k_begin, K, wave, lane, C::XLOADS);
+    load_codes_row(rc, pr, sr, vo_code, vo_scale, k_begin);
     __syncthreads();  // table ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
     decode_half<DT>(rc, lut, slot, ws[0], wrow, half);
-    load_codes_row(rc, pr, sr, vo_code, vo_scale, kBK);
+    load_codes_row(rc, pr, sr, vo_code, vo_scale, k_begin + kBK);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
 
     const FragLane fl = frag_lane(arow0, brow0, g, i16);
     uint4 a0[kTM], b0[kTN], a1[kTM], b1[kTN];
     load_frags(xs[0], ws[0], fl, 0, a0, b0);
-    for (int64_t s = 0; s < steps; ++s) {
-        const int cur = (int)(s & 1), nxt = cur ^ 1;
-        load_x_tile(xs[nxt], xr, m0, (s + 1) * kBK, K, wave, lane, C::XLOADS);
+    for (int64_t s = s_begin; s < s_end; ++s) {
+        const int cur = (int)((s - s_begin) & 1), nxt = cur ^ 1;
+        char* xn = xs[nxt];
+        const int64_t kx = (s + 1) * kBK;
         kstep<DT, kTM, kTN>(xs[cur], ws[cur], fl, a0, b0, a1, b1, rc, lut, slot, ws[nxt], wrow,
-                            half, acc, pr, sr, vo_code, vo_scale, (s + 2) * kBK);
+                            half, acc, pr, sr, vo_code, vo_scale, (s + 2) * kBK,
+                            [&] { load_x_tile(xn, xr, m0, kx, K, wave, lane, C::XLOADS); });
         vm_wait_le2();  // the X tile of step s+1 has landed; the code loads may still fly
         __syncthreads();
         load_frags(xs[nxt], ws[nxt], fl, 0, a0, b0);
+        // all of the step's first fragment reads go out before its first MFMA (left to
+        // itself the scheduler sinks each A read to its MFMA row and exposes its latency)
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- epilogue: lane (g, i16) holds rows 4g+q of column i16 of each 16x16 tile
+    if (splits > 1) {  // fp32 partial sums of this K range: part[split][row][col]
+        float* pp = part + (int64_t)split * split_stride(M, N);
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) {
+            const int64_t col = n0 + brow0 + 16 * j + i16;
+            if (col >= N) continue;
+#pragma unroll
+            for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t row = m0 + arow0 + 16 * i + 4 * g + q;
+                    if (row < M) pp[row * N + col] = acc[i][j][q];
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
         const int64_t col = n0 + brow0 + 16 * j + i16;
@@ -322,6 +353,36 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
                 const int64_t row = m0 + arow0 + 16 * i + 4 * g + q;
                 if (row < M) store_from_f32<DT>(y, row * N + col, acc[i][j][q] + bv);
             }
+        }
+    }
+}
+
+// y[m, n] = sum over the K splits of part[s][m][n] (+ bias[n]), rounded once to dtype.
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
+    const float* __restrict__ part, int splits, const void* __restrict__ bias,
+    void* __restrict__ y, int64_t M, int64_t N) {
+    const int64_t MN = M * N, stride = split_stride(M, N);
+    const int64_t i4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i4 >= MN) return;
+    if (i4 + 4 <= MN) {
+        float4 a = *reinterpret_cast<const float4*>(part + i4);
+        for (int s = 1; s < splits; ++s) {
+            const float4 b = *reinterpret_cast<const float4*>(part + (int64_t)s * stride + i4);
+            a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+        const float v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float bv = bias ? load_as_f32<DT>(bias, (i4 + e) % N) : 0.f;
+            store_from_f32<DT>(y, i4 + e, v[e] + bv);
+        }
+    } else {
+        for (int64_t i = i4; i < MN; ++i) {
+            float a = 0.f;
+            for (int s = 0; s < splits; ++s) a += part[(int64_t)s * stride + i];
+            const float bv = bias ? load_as_f32<DT>(bias, i % N) : 0.f;
+            store_from_f32<DT>(y, i, a + bv);
         }
     }
 }
@@ -348,26 +409,59 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
 
 template <int DT, typename C>
 static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_t* scales,
-                             const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                             hipStream_t stream) {
+                             const void* bias, void* y, float* part, int splits, int64_t M,
+                             int64_t N, int64_t K, hipStream_t stream) {
     const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
-    if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C>), dim3((unsigned)tiles), dim3(C::THREADS), 0,
-                       stream, x, packed, scales, bias, y, M, N, K);
+    if (tiles * splits > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C>), dim3((unsigned)(tiles * splits)),
+                       dim3(C::THREADS), 0, stream, x, packed, scales, bias, y, part, splits, M,
+                       N, K);
+    if (splits == 1) return hipGetLastError();
+    const int64_t groups = (M * N + 1023) / 1024;
+    hipLaunchKernelGGL((gemm_split_reduce_kernel<DT>), dim3((unsigned)groups), dim3(256), 0,
+                       stream, part, splits, bias, y, M, N);
     return hipGetLastError();
 }
 
+// K split of small grids: the small-tile grid is split over K until it holds about two
+// workgroups per CU (the small configuration's residency), keeping at least kMinSplitSteps
+// K steps per split and the fp32 partial sums under kSplitBytesMax.
+#ifndef OJX_SPLIT_TARGET_WGS
+#define OJX_SPLIT_TARGET_WGS 512
+#endif
+constexpr int kMaxSplits = 16;
+constexpr int64_t kMinSplitSteps = 4;
+constexpr int64_t kSplitBytesMax = 256ll << 20;
+
+int gemm_mfma_splits(int64_t M, int64_t N, int64_t K) {
+    const int64_t large = ((M + CfgLarge::BM - 1) / CfgLarge::BM) *
+                          ((N + CfgLarge::BN - 1) / CfgLarge::BN);
+    if (large >= OJX_GEMM_SMALL_BELOW) return 1;
+    const int64_t tiles = ((M + CfgSmall::BM - 1) / CfgSmall::BM) *
+                          ((N + CfgSmall::BN - 1) / CfgSmall::BN);
+    int64_t s = (OJX_SPLIT_TARGET_WGS + tiles / 2) / tiles;
+    if (s > kMaxSplits) s = kMaxSplits;
+    if (s > (K / kBK) / kMinSplitSteps) s = (K / kBK) / kMinSplitSteps;
+    while (s > 1 && s * split_stride(M, N) * 4 > kSplitBytesMax) --s;
+    return s < 1 ? 1 : (int)s;
+}
+
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
-                            const void* bias, void* y, int64_t M, int64_t N, int64_t K, int dt,
-                            hipStream_t stream) {
+                            const void* bias, void* y, float* part, int splits, int64_t M,
+                            int64_t N, int64_t K, int dt, hipStream_t stream) {
     const int64_t large = ((M + CfgLarge::BM - 1) / CfgLarge::BM) *
                           ((N + CfgLarge::BN - 1) / CfgLarge::BN);
     const bool small = large < OJX_GEMM_SMALL_BELOW;
+    if (splits < 1 || (splits > 1 && (!small || !part))) return hipErrorInvalidValue;
     if (dt == kBF16)
-        return small ? launch_cfg<kBF16, CfgSmall>(x, packed, scales, bias, y, M, N, K, stream)
-                     : launch_cfg<kBF16, CfgLarge>(x, packed, scales, bias, y, M, N, K, stream);
-    return small ? launch_cfg<kF16, CfgSmall>(x, packed, scales, bias, y, M, N, K, stream)
-                 : launch_cfg<kF16, CfgLarge>(x, packed, scales, bias, y, M, N, K, stream);
+        return small ? launch_cfg<kBF16, CfgSmall>(x, packed, scales, bias, y, part, splits, M, N,
+                                                   K, stream)
+                     : launch_cfg<kBF16, CfgLarge>(x, packed, scales, bias, y, part, 1, M, N, K,
+                                                   stream);
+    return small ? launch_cfg<kF16, CfgSmall>(x, packed, scales, bias, y, part, splits, M, N, K,
+                                              stream)
+                 : launch_cfg<kF16, CfgLarge>(x, packed, scales, bias, y, part, 1, M, N, K,
+                                              stream);
 }
 
 }  // namespace ojx

@@ -89,3 +89,64 @@ def test_prefill_unaligned_input_falls_back():
     torch.cuda.synchronize()
     ref = O.gemm_f64(x.float().cpu().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
     assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(201, 301, 1344), (40, 1024, 4096), (129, 640, 2048)])
+def test_prefill_k_split_uneven_steps_and_ragged_tail(dtype, M, N, K):
+    # small grids run split over K: 21 K steps over 5 splits (uneven), up to 16 splits, and
+    # M*N not a multiple of 4 (the reduction's scalar tail)
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=M * 3 + N + K)
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"prefill split M={M} N={N} K={K} {dtype}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32,
+                     DT_CODE[dtype])
+    assert _rel(y, ref) <= REL_TOL
+
+
+def test_prefill_k_split_scratch_growth_and_reuse():
+    # the K-split scratch grows with the request and is reused by smaller ones afterwards
+    cases = [(64, 256, 1024), (512, 1024, 4096), (96, 512, 2048), (600, 2048, 4096),
+             (64, 256, 1024)]
+    for i, (M, N, K) in enumerate(cases):
+        pk, sc, pk_np, sc_np = _encoded(N, K, seed=40 + i)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(i)).to(torch.bfloat16)
+        print(f"prefill scratch case {i} M={M} N={N} K={K}", flush=True)
+        y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+        torch.cuda.synchronize()
+        rows = list(range(0, M, max(1, M // 16))) + [M - 1]
+        ref = O.gemm_f64(x[rows].float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
+        assert _rel(y[rows], ref) <= REL_TOL
+
+
+def test_prefill_graph_capture_runs_unsplit_and_matches_eager():
+    # inside graph capture no scratch is allocated: the captured launch is the unsplit
+    # kernel; every replay (with eager work in between) matches the eager split result
+    M, N, K = 512, 1024, 4096
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=77)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV)
+    y_eager = ops.e8t_linear(x, pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.e8t_linear(x, pk, sc, None, N, K, 32)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_graph = ops.e8t_linear(x, pk, sc, None, N, K, 32)
+    rows = [0, 1, 255, 511]
+    ref = O.gemm_f64(x[rows].float().cpu().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
+    assert _rel(y_eager[rows], ref) <= REL_TOL
+    for rep in range(3):
+        y_graph.fill_(float("nan"))
+        ops.e8t_linear(x, pk, sc, None, N, K, 32)  # eager (split) work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert _rel(y_graph[rows], ref) <= REL_TOL, rep
+        assert _rel(y_graph, y_eager.double()) <= 1e-2, rep
