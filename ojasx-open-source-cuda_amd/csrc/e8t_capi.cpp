@@ -144,15 +144,14 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
                     "e8t gemv launch");
     }
     if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype)) {
-        int splits = ojx::gemm_mfma_splits(M, N, K);
+        ojx::GemmChoice c = ojx::gemm_mfma_choice(M, N, K);
         float* part = nullptr;
-        if (splits > 1) {
+        if (c.splits > 1) {
             part = static_cast<float*>(ojx::stream_workspace(
-                s, (size_t)splits * (size_t)ojx::split_stride(M, N) * sizeof(float)));
-            if (!part) splits = 1;  // capturing, or no memory: the unsplit kernel
+                s, (size_t)c.splits * (size_t)ojx::split_stride(M, N) * sizeof(float)));
+            if (!part) c.splits = 1;  // capturing, or no memory: the unsplit kernel
         }
-        return done(ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, splits, M, N, K,
-                                          dtype, s),
+        return done(ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s),
                     "e8t gemm_mfma launch");
     }
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),

@@ -423,45 +423,58 @@ static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_
     return hipGetLastError();
 }
 
-// K split of small grids: the small-tile grid is split over K until it holds about two
-// workgroups per CU (the small configuration's residency), keeping at least kMinSplitSteps
-// K steps per split and the fp32 partial sums under kSplitBytesMax.
+// Tile configuration and K split of a launch.
+//  * Grids of at least OJX_GEMM_SMALL_BELOW large tiles: large tiles, unsplit.
+//  * Smaller grids: large tiles split over K towards one workgroup per CU, if every split
+//    keeps at least kMinLargeSplitSteps K steps and the split grid still covers three
+//    quarters of the CUs;
+//  * otherwise small tiles, split over K towards two workgroups per CU (the small
+//    configuration's residency), at least kMinSplitSteps K steps per split.
+// The fp32 partial sums of a split stay under kSplitBytesMax.
 #ifndef OJX_SPLIT_TARGET_WGS
 #define OJX_SPLIT_TARGET_WGS 512
 #endif
 constexpr int kMaxSplits = 16;
 constexpr int64_t kMinSplitSteps = 4;
+constexpr int64_t kMinLargeSplitSteps = 16;
 constexpr int64_t kSplitBytesMax = 256ll << 20;
+constexpr int64_t kLargeTargetWgs = 256;
+constexpr int64_t kLargeMinWgs = 192;
 
-int gemm_mfma_splits(int64_t M, int64_t N, int64_t K) {
+static int64_t splits_for(int64_t tiles, int64_t target, int64_t min_steps, int64_t M,
+                          int64_t N, int64_t K) {
+    int64_t s = (target + tiles / 2) / tiles;
+    if (s > kMaxSplits) s = kMaxSplits;
+    if (s > (K / kBK) / min_steps) s = (K / kBK) / min_steps;
+    while (s > 1 && s * split_stride(M, N) * 4 > kSplitBytesMax) --s;
+    return s < 1 ? 1 : s;
+}
+
+GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K) {
     const int64_t large = ((M + CfgLarge::BM - 1) / CfgLarge::BM) *
                           ((N + CfgLarge::BN - 1) / CfgLarge::BN);
-    if (large >= OJX_GEMM_SMALL_BELOW) return 1;
+    if (large >= OJX_GEMM_SMALL_BELOW) return GemmChoice{false, 1};
+    const int64_t sl = splits_for(large, kLargeTargetWgs, kMinLargeSplitSteps, M, N, K);
+    if (large * sl >= kLargeMinWgs) return GemmChoice{false, (int)sl};
     const int64_t tiles = ((M + CfgSmall::BM - 1) / CfgSmall::BM) *
                           ((N + CfgSmall::BN - 1) / CfgSmall::BN);
-    int64_t s = (OJX_SPLIT_TARGET_WGS + tiles / 2) / tiles;
-    if (s > kMaxSplits) s = kMaxSplits;
-    if (s > (K / kBK) / kMinSplitSteps) s = (K / kBK) / kMinSplitSteps;
-    while (s > 1 && s * split_stride(M, N) * 4 > kSplitBytesMax) --s;
-    return s < 1 ? 1 : (int)s;
+    return GemmChoice{true,
+                      (int)splits_for(tiles, OJX_SPLIT_TARGET_WGS, kMinSplitSteps, M, N, K)};
 }
 
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
-                            const void* bias, void* y, float* part, int splits, int64_t M,
+                            const void* bias, void* y, float* part, GemmChoice c, int64_t M,
                             int64_t N, int64_t K, int dt, hipStream_t stream) {
-    const int64_t large = ((M + CfgLarge::BM - 1) / CfgLarge::BM) *
-                          ((N + CfgLarge::BN - 1) / CfgLarge::BN);
-    const bool small = large < OJX_GEMM_SMALL_BELOW;
-    if (splits < 1 || (splits > 1 && (!small || !part))) return hipErrorInvalidValue;
+    if (c.splits < 1 || (c.splits > 1 && !part)) return hipErrorInvalidValue;
     if (dt == kBF16)
-        return small ? launch_cfg<kBF16, CfgSmall>(x, packed, scales, bias, y, part, splits, M, N,
-                                                   K, stream)
-                     : launch_cfg<kBF16, CfgLarge>(x, packed, scales, bias, y, part, 1, M, N, K,
-                                                   stream);
-    return small ? launch_cfg<kF16, CfgSmall>(x, packed, scales, bias, y, part, splits, M, N, K,
-                                              stream)
-                 : launch_cfg<kF16, CfgLarge>(x, packed, scales, bias, y, part, 1, M, N, K,
-                                              stream);
+        return c.small ? launch_cfg<kBF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits,
+                                                     M, N, K, stream)
+                       : launch_cfg<kBF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits,
+                                                     M, N, K, stream);
+    return c.small ? launch_cfg<kF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits, M, N,
+                                                K, stream)
+                   : launch_cfg<kF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits, M, N,
+                                                K, stream);
 }
 
 }  // namespace ojx

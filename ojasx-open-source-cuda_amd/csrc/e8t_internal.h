@@ -73,14 +73,18 @@ hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int 
 // Prefill MFMA GEMM (M > 16): F16/BF16, K % 64 == 0, group size 32.
 bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                          int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
-// K splits the prefill GEMM uses for this shape (1 = none).  With splits > 1 the launch
-// needs `part`, fp32 scratch of splits * split_stride(M, N) floats.
-int gemm_mfma_splits(int64_t M, int64_t N, int64_t K);
+// Tile configuration and K splits of the prefill GEMM for a shape (splits 1 = none).  With
+// splits > 1 the launch needs `part`, fp32 scratch of splits * split_stride(M, N) floats.
+struct GemmChoice {
+    bool small;  // 128 x 128 tiles (else 256 x 256)
+    int splits;
+};
+GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K);
 __host__ __device__ inline int64_t split_stride(int64_t M, int64_t N) {
     return (M * N + 3) & ~(int64_t)3;  // 16-byte aligned per split
 }
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
-                            const void* bias, void* y, float* part, int splits, int64_t M,
+                            const void* bias, void* y, float* part, GemmChoice c, int64_t M,
                             int64_t N, int64_t K, int dt, hipStream_t stream);
 
 // Scratch device memory owned by the library, one buffer per (device, stream), grown on

@@ -150,3 +150,25 @@ def test_prefill_graph_capture_runs_unsplit_and_matches_eager():
         torch.cuda.synchronize()
         assert _rel(y_graph[rows], ref) <= REL_TOL, rep
         assert _rel(y_graph, y_eager.double()) <= 1e-2, rep
+
+
+def test_prefill_large_tile_k_split_uneven_and_ragged():
+    # 4 x 24 large tiles split 3 ways over 65 K steps (21/22/22), ragged M and N, bias
+    M, N, K = 1000, 6100, 4160
+    gw = torch.Generator(device=DEV).manual_seed(4242)
+    w = torch.randn(N, K, generator=gw, device=DEV) * 0.02
+    pk, sc = ops.encode(w, 32)
+    del w
+    x = torch.randn(M, K, generator=gw, device=DEV).to(torch.bfloat16)
+    bias = torch.randn(N, generator=gw, device=DEV).to(torch.bfloat16)
+    print(f"prefill large split M={M} N={N} K={K}", flush=True)
+    y = ops.e8t_linear(x, pk, sc, bias, N, K, 32)
+    wdq = ops.decode(pk, sc, N * K, 32, torch.bfloat16).view(N, K).float()
+    ref = x.float() @ wdq.t().contiguous() + bias.float()
+    torch.cuda.synchronize()
+    assert _rel(y, ref) <= REL_TOL
+    rows = [0, 255, 256, 511, 999]
+    ref64 = O.gemm_f64(x[rows].float().cpu().numpy(), pk.cpu().numpy(),
+                       sc.cpu().view(torch.int16).numpy().view(np.uint16),
+                       bias.float().cpu().numpy(), N, K, 32, O.DT_BF16)
+    assert _rel(y[rows], ref64) <= REL_TOL
