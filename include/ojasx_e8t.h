@@ -5,9 +5,14 @@
  *
  * Plain pointers and sizes only.  Every pointer argument except `stream` is a
  * device pointer (HBM) on the current HIP device.  `stream` is a hipStream_t
- * (NULL = the null stream).  No entry point allocates device memory, takes a
- * lock or keeps mutable global state; each one enqueues its kernels on `stream`
- * and returns without synchronising.  Results are ready when the stream is.
+ * (NULL = the null stream).  Each entry point enqueues its kernels on `stream`
+ * and returns without synchronising; results are ready when the stream is.  The
+ * only device memory the library allocates is the prefill GEMM's K-split scratch
+ * (ojx_e8t_gemm_fwd, M > 16, small grids): one buffer per (device, stream), grown
+ * under a lock when a launch needs more (the stream is synchronised before an old
+ * buffer is freed), never while the stream is capturing a graph (the launch then
+ * runs unsplit), kept until the process ends.  No other mutable global state beyond
+ * a per-device architecture check and a thread-local error message.
  *
  * Data layout (identical to the reference's buffers, so existing state_dicts load):
  *   packed  uint8 [padded * 3 / 16]   two 12-bit codes per 3 bytes, little-endian bit
@@ -76,7 +81,9 @@ int ojx_e8t_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel,
  * called from _FusedE8GEMMFunction.forward (lattice.py:584-608).
  *   x, y, bias in `dtype`; bias may be NULL.  Wdeq follows the decoder's rule for `dtype`.
  *   Any K >= 1 (flat layout).  F16/BF16 with K % 256 == 0, gs == 32 and M <= 16 run the
- *   MFMA decode GEMV; other shapes and F32 use a general tiled kernel.  Never declines. */
+ *   MFMA decode GEMV; F16/BF16 with K % 64 == 0, gs == 32 and M > 16 the MFMA prefill
+ *   GEMM (split over K for small grids, with the scratch described above); other shapes
+ *   and F32 use a general tiled kernel.  Never declines. */
 int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                      int dtype, void* stream);
