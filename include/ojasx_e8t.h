@@ -95,6 +95,36 @@ int ojx_e8t_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_
                         void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
                         void* stream);
 
+/* ---------------------------------------------------------------- 2-bit E8
+ *
+ * E8LatticePacker (2.0 bit/weight, ojasx2/math/lattice.py:209-279): four 2-bit codes per
+ * byte (code j of a byte in bits [2j, 2j+2), the flat weight order), one fp16 scale per
+ * flat group of gs weights; weight = (code - 1.5) * scale.
+ *   packed  uint8 [padded / 4];  scales uint16 [padded / gs];  padded as above. */
+
+/* Encoder, bit-exact with E8LatticePacker.pack (lattice.py:213-249).  gs a positive
+ * multiple of 8 (the packer's ValueError, :220-221, is OJX_ELAYOUT here). */
+int ojx_e8_encode(const void* w, int w_dtype, int64_t numel, int64_t gs, uint8_t* packed,
+                  uint16_t* scales, void* stream);
+
+/* Decoder, bit-exact with E8LatticePacker.unpack (lattice.py:252-279): out[i] =
+ * (code - 1.5) * scales.to(dtype), the product rounded once to dtype.  gs a positive
+ * multiple of 8. */
+int ojx_e8_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel, int64_t gs,
+                  int out_dtype, void* out, void* stream);
+
+/* Fused forward and backward dX over 2-bit weights, with the decoder's weight rule and
+ * fp32 accumulation.  Replace fused_e8_gemm_fwd / fused_e8_gemm_bwd_dx
+ * (ojasx_math_bindings.cpp:274-404, schemas :591-592) and the 2-bit portable path of
+ * _FusedE8GEMMFunction (lattice.py:610-640, 684-717).  gs a positive multiple of 4 (the
+ * native op's rule, bindings.cpp:285).  Any M, N, K (flat layout). */
+int ojx_e8_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
+                    const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                    int dtype, void* stream);
+int ojx_e8_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_t* scales,
+                       void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
+                       void* stream);
+
 /* ---------------------------------------------------------------- grouped decode GEMV
  *
  * One launch runs the decode GEMV (batch M <= 16) of several independent linears: a

@@ -15,6 +15,7 @@
 #include <cstring>
 
 #include "../../include/ojasx_e8t.h"
+#include "e8t_device.h"
 #include "e8t_internal.h"
 
 namespace {
@@ -256,6 +257,84 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_bwd_dx(const void* grad_
     hipStream_t s = (hipStream_t)stream;
     return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype, s),
                 "e8t gemm_bwd_dx launch");
+}
+
+// ------------------------------------------------------------------ 2-bit E8
+
+static int check_gs_multiple(int64_t gs, int64_t unit) {
+    if (gs <= 0 || gs % unit != 0)
+        return fail(OJX_ELAYOUT, "group_size must be a positive multiple of %lld (got %lld)",
+                    (long long)unit, (long long)gs);
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8_encode(const void* w, int w_dtype,
+                                                         int64_t numel, int64_t gs,
+                                                         uint8_t* packed, uint16_t* scales,
+                                                         void* stream) {
+    if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);
+    if (!valid_dtype(w_dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", w_dtype);
+    if (int r = check_gs_multiple(gs, 8)) return r;
+    if (numel == 0) return OJX_OK;
+    if (!w || !packed || !scales) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_encode2(w, w_dtype, numel, gs, packed, scales, (hipStream_t)stream),
+                "e8 encode launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8_decode(const uint8_t* packed,
+                                                         const uint16_t* scales, int64_t numel,
+                                                         int64_t gs, int out_dtype, void* out,
+                                                         void* stream) {
+    if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);
+    if (!valid_dtype(out_dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", out_dtype);
+    if (int r = check_gs_multiple(gs, 8)) return r;
+    if (numel == 0) return OJX_OK;
+    if (!packed || !scales || !out) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_decode2(packed, scales, numel, gs, out_dtype, out, (hipStream_t)stream),
+                "e8 decode launch");
+}
+
+static int check_gemm2_args(const void* a, const uint8_t* packed, const uint16_t* scales,
+                            const void* out, int64_t M, int64_t N, int64_t K, int64_t gs,
+                            int dtype) {
+    if (M < 0 || N < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld N=%lld K=%lld",
+                                             (long long)M, (long long)N, (long long)K);
+    if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
+    if (int r = check_gs_multiple(gs, 4)) return r;
+    if (M > 0 && N > 0) {
+        if (!out) return fail(OJX_EINVAL, "null output pointer");
+        if (K > 0 && (!a || !packed || !scales)) return fail(OJX_EINVAL, "null input pointer");
+    }
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemm_fwd(const void* x, const uint8_t* packed,
+                                                           const uint16_t* scales,
+                                                           const void* bias, void* y, int64_t M,
+                                                           int64_t N, int64_t K, int64_t gs,
+                                                           int dtype, void* stream) {
+    if (int r = check_gemm2_args(x, packed, scales, y, M, N, K, gs, dtype)) return r;
+    if (M == 0 || N == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype,
+                                             (hipStream_t)stream, ojx::kFmt2Bit),
+                "e8 gemm_fwd launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemm_bwd_dx(const void* grad_y,
+                                                              const uint8_t* packed,
+                                                              const uint16_t* scales,
+                                                              void* grad_x, int64_t M, int64_t N,
+                                                              int64_t K, int64_t gs, int dtype,
+                                                              void* stream) {
+    if (int r = check_gemm2_args(grad_y, packed, scales, grad_x, M, K, N, gs, dtype)) return r;
+    if (M == 0 || K == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype,
+                                             (hipStream_t)stream, ojx::kFmt2Bit),
+                "e8 gemm_bwd_dx launch");
 }
 
 }  // extern "C"

@@ -1,4 +1,5 @@
-// e8t_codec.hip -- ternary-E8 encoder and decoder kernels for gfx950.
+// e8t_codec.hip -- E8 encoder and decoder kernels for gfx950: ternary 1.5-bit
+// (TernaryE8LatticePacker) and 2-bit (E8LatticePacker, at the end of the file).
 //
 // Encoder: bit-exact restatement of TernaryE8LatticePacker.pack
 // (ojasx2/math/lattice.py:338-384) as one fused pass: each weight is read once
@@ -286,6 +287,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(
     for (int i = 0; i < 8; ++i) {
         v[i] = (float)((int)(raw0 % 3u) - 1) * s;
         v[8 + i] = (float)((int)(raw1 % 3u) - 1) * s;
+        keep_f32(v[i]);  // -1 * 0 stays -0 (see keep_f32)
+        keep_f32(v[8 + i]);
         raw0 /= 3u;
         raw1 /= 3u;
     }
@@ -331,6 +334,252 @@ hipError_t launch_decode(const uint8_t* packed, const uint16_t* scales, int64_t 
         default:
             hipLaunchKernelGGL((decode_kernel<kBF16>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
                                stream, packed, scales, numel, gs, vec_ok, out);
+            break;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- 2-bit encoder
+//
+// E8LatticePacker.pack (lattice.py:213-249), bit-exact: the same scale (torch's norm
+// order, correctly rounded quotients) and per 8-vector
+//   xs = w/s - 0.5; f2 = clamp(rint(xs), -2, 1)
+//   alt = xs >= f2 ? clamp(f2 + 1, -2, 1) : clamp(f2 - 1, -2, 1)
+//   pen = (alt - xs)^2 - (f2 - xs)^2 (rounded ops, never contracted)
+//   odd sum(f2): f2[first argmin pen] = alt;  code_i = f2_i + 2
+// A clamped coordinate has alt == f2 and pen 0; as the first minimum its "flip" is a no-op
+// and the vector keeps its odd sum, exactly as in the reference.  Returns the 8 codes as
+// 16 bits (two packed bytes, code i in bits [2i, 2i+2)).
+
+template <bool EXACT>
+__device__ __forceinline__ uint32_t quantize8_2bit(const float* __restrict__ w,
+                                                   const GroupRecip& g) {
+#pragma clang fp contract(off)
+    const float pow4[8] = {1.f, 4.f, 16.f, 64.f, 256.f, 1024.f, 4096.f, 16384.f};
+    float xs[8], f2[8];
+    float fsum = 0.f;
+    float codes = 0.f;  // sum (f2_i + 2) 4^i: exact in fp32
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float v = EXACT ? w[i] / g.s : div_rn(w[i], g);
+        xs[i] = v - 0.5f;
+        float r = __builtin_rintf(xs[i]);
+        r = fmaxf(r, -2.f);
+        r = fminf(r, 1.f);
+        f2[i] = r;
+        fsum = fsum + r;
+        codes = __builtin_fmaf(r + 2.f, pow4[i], codes);
+    }
+    float best_pen = 0.f, best_delta = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float up = fminf(f2[i] + 1.f, 1.f), dn = fmaxf(f2[i] - 1.f, -2.f);
+        const float alt = xs[i] >= f2[i] ? up : dn;
+        const float a = alt - xs[i];
+        const float b = f2[i] - xs[i];
+        const float a2 = a * a;
+        const float b2 = b * b;
+        const float pen = a2 - b2;
+        const float delta = (alt - f2[i]) * pow4[i];
+        if (i == 0 || pen < best_pen) {
+            best_pen = pen;
+            best_delta = delta;
+        }
+    }
+    const int odd = ((int)fsum) & 1;  // sum(f2) is an integer in [-16, 8]
+    codes = odd ? codes + best_delta : codes;
+    return (uint32_t)codes;
+}
+
+// GS in {8, 16, 32, 64}: the group stays in registers; bytes staged in LDS and written
+// coalesced.
+template <int WDT, int GS>
+__global__ __launch_bounds__(kEncThreads) void encode2_kernel(
+    const void* __restrict__ w, int64_t numel, int64_t ngroups, float root, bool vec_ok,
+    uint8_t* __restrict__ packed, uint16_t* __restrict__ scales) {
+    constexpr int NV = GS / 8;
+    constexpr int BYTES = GS / 4;
+    __shared__ uint8_t stage[kEncThreads * BYTES];
+    const int64_t g0 = (int64_t)blockIdx.x * kEncThreads;
+    const int64_t g = g0 + threadIdx.x;
+    if (g < ngroups) {
+        float x[GS];
+#pragma unroll
+        for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+        const float s = group_scale<GS>(x, root);
+        const GroupRecip gr = group_recip(s);
+        uint8_t* st = stage + threadIdx.x * BYTES;
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+            const uint32_t c = gr.exact ? quantize8_2bit<true>(x + 8 * t, gr)
+                                        : quantize8_2bit<false>(x + 8 * t, gr);
+            st[2 * t] = (uint8_t)(c & 0xFFu);
+            st[2 * t + 1] = (uint8_t)(c >> 8);
+        }
+        scales[g] = (uint16_t)f32_to_f16_bits(s);
+    }
+    __syncthreads();
+    const int64_t ng = (ngroups - g0) < kEncThreads ? (ngroups - g0) : kEncThreads;
+    const int nbytes = (int)ng * BYTES;
+    uint8_t* dst = packed + g0 * BYTES;
+    if ((((uintptr_t)dst) & 3u) == 0) {
+        const int nwords = nbytes >> 2;
+        const uint32_t* src32 = reinterpret_cast<const uint32_t*>(stage);
+        uint32_t* dst32 = reinterpret_cast<uint32_t*>(dst);
+        for (int i = threadIdx.x; i < nwords; i += kEncThreads) dst32[i] = src32[i];
+        for (int i = (nwords << 2) + threadIdx.x; i < nbytes; i += kEncThreads) dst[i] = stage[i];
+    } else {
+        for (int i = threadIdx.x; i < nbytes; i += kEncThreads) dst[i] = stage[i];
+    }
+}
+
+// Any GS (multiple of 8): norm pass, then the codes, re-reading the group.
+template <int WDT>
+__global__ __launch_bounds__(kEncThreads) void encode2_kernel_any(
+    const void* __restrict__ w, int64_t numel, int64_t ngroups, int64_t gs, float root,
+    uint8_t* __restrict__ packed, uint16_t* __restrict__ scales) {
+#pragma clang fp contract(off)
+    const int64_t g = (int64_t)blockIdx.x * kEncThreads + threadIdx.x;
+    if (g >= ngroups) return;
+    const int64_t base = g * gs;
+    float acc[8];
+    for (int t = 0; t < gs / 8; ++t) {
+        float x[8];
+        load8<WDT>(w, base + 8 * t, numel, false, x);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = (t == 0) ? x[j] * x[j] : __builtin_fmaf(x[j], x[j], acc[j]);
+    }
+    float sum = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) sum = sum + acc[j];
+    float s = __builtin_sqrtf(sum) / root;
+    s = s + 1e-8f;
+    uint8_t* dst = packed + base / 4;
+    const GroupRecip gr = group_recip(s);
+    for (int t = 0; t < gs / 8; ++t) {
+        float x[8];
+        load8<WDT>(w, base + 8 * t, numel, false, x);
+        const uint32_t c = gr.exact ? quantize8_2bit<true>(x, gr) : quantize8_2bit<false>(x, gr);
+        dst[2 * t] = (uint8_t)(c & 0xFFu);
+        dst[2 * t + 1] = (uint8_t)(c >> 8);
+    }
+    scales[g] = (uint16_t)f32_to_f16_bits(s);
+}
+
+template <int WDT>
+static hipError_t launch_encode2_t(const void* w, int64_t numel, int64_t gs, uint8_t* packed,
+                                   uint16_t* scales, hipStream_t stream) {
+    const int64_t padded = numel + (gs - numel % gs) % gs;
+    const int64_t ngroups = padded / gs;
+    const float root = (float)__builtin_sqrt((double)gs);
+    const int64_t blocks = (ngroups + kEncThreads - 1) / kEncThreads;
+    const bool vec_ok = (((uintptr_t)w) & 15u) == 0;
+    switch (gs) {
+        case 8:
+            hipLaunchKernelGGL((encode2_kernel<WDT, 8>), dim3((unsigned)blocks), dim3(kEncThreads),
+                               0, stream, w, numel, ngroups, root, vec_ok, packed, scales);
+            break;
+        case 16:
+            hipLaunchKernelGGL((encode2_kernel<WDT, 16>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, root, vec_ok,
+                               packed, scales);
+            break;
+        case 32:
+            hipLaunchKernelGGL((encode2_kernel<WDT, 32>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, root, vec_ok,
+                               packed, scales);
+            break;
+        case 64:
+            hipLaunchKernelGGL((encode2_kernel<WDT, 64>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, root, vec_ok,
+                               packed, scales);
+            break;
+        default:
+            hipLaunchKernelGGL((encode2_kernel_any<WDT>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, gs, root, packed,
+                               scales);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_encode2(const void* w, int wdt, int64_t numel, int64_t gs, uint8_t* packed,
+                          uint16_t* scales, hipStream_t stream) {
+    switch (wdt) {
+        case kF32: return launch_encode2_t<kF32>(w, numel, gs, packed, scales, stream);
+        case kF16: return launch_encode2_t<kF16>(w, numel, gs, packed, scales, stream);
+        default: return launch_encode2_t<kBF16>(w, numel, gs, packed, scales, stream);
+    }
+}
+
+// ---------------------------------------------------------------- 2-bit decoder
+//
+// E8LatticePacker.unpack (lattice.py:252-279): one lane per 16 weights (4 bytes), each
+// (code - 1.5) * scales.to(dtype) rounded once to dtype.
+
+template <int ODT>
+__global__ __launch_bounds__(kDecThreads) void decode2_kernel(
+    const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales, int64_t numel,
+    int64_t padded, int64_t gs, bool vec_ok, void* __restrict__ out) {
+    const int64_t p = (int64_t)blockIdx.x * kDecThreads + threadIdx.x;
+    const int64_t e0 = p * 16;
+    if (e0 >= numel) return;
+    uint32_t word;
+    if (e0 + 16 <= padded && (((uintptr_t)packed) & 3u) == 0) {
+        word = *reinterpret_cast<const uint32_t*>(packed + e0 / 4);
+    } else {
+        word = 0;
+        for (int b = 0; b < 4 && e0 + 4 * b < padded; ++b)
+            word |= (uint32_t)packed[e0 / 4 + b] << (8 * b);
+    }
+    const uint32_t s0 = scales[e0 / gs];  // gs % 8 == 0: each run of 8 is one group
+    const uint32_t s1 = (e0 + 8 < padded) ? scales[(e0 + 8) / gs] : s0;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = deq2_value<ODT>((word >> (2 * i)) & 3u, i < 8 ? s0 : s1);
+    if (vec_ok && e0 + 16 <= numel) {
+        if constexpr (ODT == kF32) {
+            float4* o = reinterpret_cast<float4*>((float*)out + e0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        } else {
+            uint32_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                uint32_t lo, hi;
+                if constexpr (ODT == kF16) { lo = f32_to_f16_bits(v[2 * i]); hi = f32_to_f16_bits(v[2 * i + 1]); }
+                else { lo = f32_to_bf16_bits(v[2 * i]); hi = f32_to_bf16_bits(v[2 * i + 1]); }
+                h[i] = lo | (hi << 16);
+            }
+            uint4* o = reinterpret_cast<uint4*>((uint16_t*)out + e0);
+            o[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (e0 + i < numel) store_from_f32<ODT>(out, e0 + i, v[i]);
+    }
+}
+
+hipError_t launch_decode2(const uint8_t* packed, const uint16_t* scales, int64_t numel,
+                          int64_t gs, int odt, void* out, hipStream_t stream) {
+    const int64_t padded = numel + (gs - numel % gs) % gs;
+    const int64_t quads = (numel + 15) / 16;
+    const int64_t blocks = (quads + kDecThreads - 1) / kDecThreads;
+    const bool vec_ok = (((uintptr_t)out) & 15u) == 0;
+    switch (odt) {
+        case kF32:
+            hipLaunchKernelGGL((decode2_kernel<kF32>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, packed, scales, numel, padded, gs, vec_ok, out);
+            break;
+        case kF16:
+            hipLaunchKernelGGL((decode2_kernel<kF16>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, packed, scales, numel, padded, gs, vec_ok, out);
+            break;
+        default:
+            hipLaunchKernelGGL((decode2_kernel<kBF16>), dim3((unsigned)blocks), dim3(kDecThreads),
+                               0, stream, packed, scales, numel, padded, gs, vec_ok, out);
             break;
     }
     return hipGetLastError();

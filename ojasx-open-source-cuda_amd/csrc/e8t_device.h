@@ -1,4 +1,5 @@
-// e8t_device.h -- device helpers shared by the ternary-E8 kernels (gfx950).
+// e8t_device.h -- device helpers shared by the E8 kernels (gfx950): ternary 1.5-bit and
+// 2-bit codes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -48,6 +49,11 @@ template <int DT> __device__ __forceinline__ void store_from_f32(void* p, int64_
     else ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(v);
 }
 
+// Keeps v a rounded fp32 value in a register.  Left alone, the compiler fuses a product
+// that is then narrowed to fp16 into v_fma_mixlo_f16 with a +0 addend, which turns a -0
+// product (a negative coefficient times a zero scale) into +0; the reference keeps -0.
+__device__ __forceinline__ void keep_f32(float& v) { asm volatile("" : "+v"(v)); }
+
 // Scale value the reference multiplies decoded coordinates by for activations of
 // dtype DT (lattice.py:414-418: scales.to(dtype)): fp32 and fp16 keep the fp16
 // value exactly, bf16 rounds it to bf16.
@@ -70,6 +76,28 @@ __device__ __forceinline__ uint32_t load_code(const uint8_t* __restrict__ packed
 __device__ __forceinline__ int code_coord(uint32_t code, int i) {
     const uint32_t pow3[8] = {1, 3, 9, 27, 81, 243, 729, 2187};
     return (int)(((2u * code) / pow3[i]) % 3u) - 1;
+}
+
+// ---------------------------------------------------------------- 2-bit E8 codes
+
+// Code formats of the packed weight buffers.
+enum : int { kFmtTernary = 0, kFmt2Bit = 1 };
+
+// 2-bit code f of the flat stream (E8LatticePacker): four per byte, code j of a byte in
+// bits [2j, 2j+2) (lattice.py:242-247).
+__device__ __forceinline__ uint32_t load_code2(const uint8_t* __restrict__ packed, int64_t f) {
+    return ((uint32_t)packed[f >> 2] >> (2 * (f & 3))) & 3u;
+}
+
+// Decoded 2-bit weight under the reference's dtype rule (lattice.py:274-276):
+// (code - 1.5) * scales.to(dtype), the product computed in fp32 (exact) and rounded once
+// to dtype; returned as its fp32 value.
+template <int DT> __device__ __forceinline__ float deq2_value(uint32_t code, uint32_t s16) {
+    float p = ((float)code - 1.5f) * scale_for<DT>(s16);
+    keep_f32(p);
+    if constexpr (DT == kF16) return f16_bits_to_f32(f32_to_f16_bits(p));
+    else if constexpr (DT == kBF16) return bf16_bits_to_f32(f32_to_bf16_bits(p));
+    else return p;
 }
 
 }  // namespace ojx

@@ -1,4 +1,5 @@
-// e8t_gemm_generic.hip -- general LDS-tiled SIMT kernels for the fused E8 linear.
+// e8t_gemm_generic.hip -- general LDS-tiled SIMT kernels for the fused E8 linear
+// (ternary 1.5-bit and 2-bit codes).
 //
 // These cover every shape and dtype the op accepts (fp32 activations, K not a
 // multiple of the MFMA chunk, flat layouts whose groups cross rows, as the
@@ -15,16 +16,19 @@ namespace ojx {
 constexpr int kTile = 64;  // output tile edge
 constexpr int kChunk = 32; // contraction chunk
 
-template <int DT>
+// Weight at flat index f under the reference's dtype rule: ternary coord * scale
+// (lattice.py:412-419), or 2-bit (code - 1.5) * scale rounded to dtype (lattice.py:274-276).
+template <int FMT, int DT>
 __device__ __forceinline__ float deq_flat(const uint8_t* __restrict__ packed,
                                           const uint16_t* __restrict__ scales, int64_t f,
                                           int64_t gs) {
+    if constexpr (FMT == kFmt2Bit) return deq2_value<DT>(load_code2(packed, f), scales[f / gs]);
     const uint32_t code = load_code(packed, f >> 3);
     return (float)code_coord(code, (int)(f & 7)) * scale_for<DT>(scales[f / gs]);
 }
 
 // y[M,N] = x[M,K] . W[N,K]^T + bias
-template <int DT>
+template <int FMT, int DT>
 __global__ __launch_bounds__(256) void gemm_generic_fwd(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
@@ -43,7 +47,7 @@ __global__ __launch_bounds__(256) void gemm_generic_fwd(
             const int64_t gk = k0 + kk;
             const int64_t gm = m0 + row, gn = n0 + row;
             xs[kk][row] = (gm < M && gk < K) ? load_as_f32<DT>(x, gm * K + gk) : 0.f;
-            ws[kk][row] = (gn < N && gk < K) ? deq_flat<DT>(packed, scales, gn * K + gk, gs) : 0.f;
+            ws[kk][row] = (gn < N && gk < K) ? deq_flat<FMT, DT>(packed, scales, gn * K + gk, gs) : 0.f;
         }
         __syncthreads();
 #pragma unroll 8
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(256) void gemm_generic_fwd(
 }
 
 // gx[M,K] = gy[M,N] . W[N,K]
-template <int DT>
+template <int FMT, int DT>
 __global__ __launch_bounds__(256) void gemm_generic_bwd(
     const void* __restrict__ gy, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, void* __restrict__ gx, int64_t M, int64_t N, int64_t K,
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(256) void gemm_generic_bwd(
             {
                 const int nn = idx / kTile, kk = idx % kTile;
                 const int64_t gn = n0 + nn, gk = k0 + kk;
-                ws[nn][kk] = (gn < N && gk < K) ? deq_flat<DT>(packed, scales, gn * K + gk, gs) : 0.f;
+                ws[nn][kk] = (gn < N && gk < K) ? deq_flat<FMT, DT>(packed, scales, gn * K + gk, gs) : 0.f;
             }
         }
         __syncthreads();
@@ -127,43 +131,61 @@ __global__ __launch_bounds__(256) void gemm_generic_bwd(
     }
 }
 
-template <int DT>
+template <int FMT, int DT>
 static hipError_t fwd_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                         hipStream_t stream) {
     dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
-    hipLaunchKernelGGL((gemm_generic_fwd<DT>), grid, dim3(256), 0, stream, x, packed, scales, bias,
-                       y, M, N, K, gs);
+    hipLaunchKernelGGL((gemm_generic_fwd<FMT, DT>), grid, dim3(256), 0, stream, x, packed, scales,
+                       bias, y, M, N, K, gs);
     return hipGetLastError();
 }
 
-template <int DT>
+template <int FMT, int DT>
 static hipError_t bwd_t(const void* gy, const uint8_t* packed, const uint16_t* scales, void* gx,
                         int64_t M, int64_t N, int64_t K, int64_t gs, hipStream_t stream) {
     dim3 grid((unsigned)((K + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
-    hipLaunchKernelGGL((gemm_generic_bwd<DT>), grid, dim3(256), 0, stream, gy, packed, scales, gx,
-                       M, N, K, gs);
+    hipLaunchKernelGGL((gemm_generic_bwd<FMT, DT>), grid, dim3(256), 0, stream, gy, packed, scales,
+                       gx, M, N, K, gs);
     return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t fwd_fmt(const void* x, const uint8_t* packed, const uint16_t* scales,
+                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                          int dt, hipStream_t stream) {
+    switch (dt) {
+        case kF32: return fwd_t<FMT, kF32>(x, packed, scales, bias, y, M, N, K, gs, stream);
+        case kF16: return fwd_t<FMT, kF16>(x, packed, scales, bias, y, M, N, K, gs, stream);
+        default: return fwd_t<FMT, kBF16>(x, packed, scales, bias, y, M, N, K, gs, stream);
+    }
+}
+
+template <int FMT>
+static hipError_t bwd_fmt(const void* gy, const uint8_t* packed, const uint16_t* scales, void* gx,
+                          int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
+                          hipStream_t stream) {
+    switch (dt) {
+        case kF32: return bwd_t<FMT, kF32>(gy, packed, scales, gx, M, N, K, gs, stream);
+        case kF16: return bwd_t<FMT, kF16>(gy, packed, scales, gx, M, N, K, gs, stream);
+        default: return bwd_t<FMT, kBF16>(gy, packed, scales, gx, M, N, K, gs, stream);
+    }
 }
 
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                                   int64_t gs, int dt, hipStream_t stream) {
-    switch (dt) {
-        case kF32: return fwd_t<kF32>(x, packed, scales, bias, y, M, N, K, gs, stream);
-        case kF16: return fwd_t<kF16>(x, packed, scales, bias, y, M, N, K, gs, stream);
-        default: return fwd_t<kBF16>(x, packed, scales, bias, y, M, N, K, gs, stream);
-    }
+                                   int64_t gs, int dt, hipStream_t stream, int fmt) {
+    return fmt == kFmt2Bit
+               ? fwd_fmt<kFmt2Bit>(x, packed, scales, bias, y, M, N, K, gs, dt, stream)
+               : fwd_fmt<kFmtTernary>(x, packed, scales, bias, y, M, N, K, gs, dt, stream);
 }
 
 hipError_t launch_gemm_generic_bwd(const void* gy, const uint8_t* packed, const uint16_t* scales,
                                    void* gx, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
-                                   hipStream_t stream) {
-    switch (dt) {
-        case kF32: return bwd_t<kF32>(gy, packed, scales, gx, M, N, K, gs, stream);
-        case kF16: return bwd_t<kF16>(gy, packed, scales, gx, M, N, K, gs, stream);
-        default: return bwd_t<kBF16>(gy, packed, scales, gx, M, N, K, gs, stream);
-    }
+                                   hipStream_t stream, int fmt) {
+    return fmt == kFmt2Bit
+               ? bwd_fmt<kFmt2Bit>(gy, packed, scales, gx, M, N, K, gs, dt, stream)
+               : bwd_fmt<kFmtTernary>(gy, packed, scales, gx, M, N, K, gs, dt, stream);
 }
 
 }  // namespace ojx

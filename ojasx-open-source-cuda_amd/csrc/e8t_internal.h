@@ -12,13 +12,20 @@ hipError_t launch_encode(const void* w, int wdt, int64_t numel, int64_t gs, uint
 hipError_t launch_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel, int64_t gs,
                          int odt, void* out, hipStream_t stream);
 
-// General tiled kernels: any M, N, K >= 1 (flat layout), any dtype.
+// 2-bit E8 codec (E8LatticePacker): gs a positive multiple of 8.
+hipError_t launch_encode2(const void* w, int wdt, int64_t numel, int64_t gs, uint8_t* packed,
+                          uint16_t* scales, hipStream_t stream);
+hipError_t launch_decode2(const uint8_t* packed, const uint16_t* scales, int64_t numel,
+                          int64_t gs, int odt, void* out, hipStream_t stream);
+
+// General tiled kernels: any M, N, K >= 1 (flat layout), any dtype; fmt selects the code
+// format (0 ternary, 1 2-bit).
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                                   int64_t gs, int dt, hipStream_t stream);
+                                   int64_t gs, int dt, hipStream_t stream, int fmt = 0);
 hipError_t launch_gemm_generic_bwd(const void* gy, const uint8_t* packed, const uint16_t* scales,
                                    void* gx, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
-                                   hipStream_t stream);
+                                   hipStream_t stream, int fmt = 0);
 
 }  // namespace ojx
 

@@ -1,4 +1,5 @@
-"""ojasx_amd -- MI355X-native ternary-E8 (1.5 bit/weight) quantized-weight path.
+"""ojasx_amd -- MI355X-native E8 quantized-weight path: ternary 1.5 bit/weight and
+2 bit/weight.
 
 Drop-in for the E8 names of ``ojasx3.lattice``: the packer, the fused linear and
 the layer keep the reference's signatures and buffer layout, and every array
@@ -9,7 +10,9 @@ include/ojasx_e8t.h) registered as ``torch.ops.ojasx_e8t.*``.
 from . import grouped, ops
 from .lattice import (
     E8LatticeLinear,
+    E8LatticePacker,
     TernaryE8LatticePacker,
+    _get_packer_for_bitrate,
     _FusedE8GEMMFunction,
     _get_ternary_e8_luts,
     fwht_block32,
@@ -23,7 +26,9 @@ __all__ = [
     "grouped",
     "ops",
     "E8LatticeLinear",
+    "E8LatticePacker",
     "TernaryE8LatticePacker",
+    "_get_packer_for_bitrate",
     "_FusedE8GEMMFunction",
     "_get_ternary_e8_luts",
     "fwht_block32",

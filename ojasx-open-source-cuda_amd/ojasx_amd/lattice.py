@@ -1,8 +1,8 @@
-"""Ternary-E8 (1.5 bit/weight) lattice quantization on MI355X.
+"""E8 lattice quantization (ternary 1.5 bit/weight and 2 bit/weight) on MI355X.
 
-Mirrors the ternary part of ``ojasx3.lattice`` / ``ojasx2.math.lattice`` -- same
-names, arguments, buffers, coercions and errors -- with every array operation
-on the path running in the HIP kernels behind ``ojasx_amd.ops``:
+Mirrors the ternary and 2-bit parts of ``ojasx3.lattice`` / ``ojasx2.math.lattice``
+-- same names, arguments, buffers, coercions and errors -- with every array
+operation on the path running in the HIP kernels behind ``ojasx_amd.ops``:
 
 =================================  ==========================================
 this module                         reference (ojasx2/math/lattice.py)
@@ -11,12 +11,17 @@ this module                         reference (ojasx2/math/lattice.py)
 ``_get_ternary_e8_luts``            :292-332
 ``TernaryE8LatticePacker.pack``     :338-384   -> ops.encode (one HIP kernel)
 ``TernaryE8LatticePacker.unpack``   :386-419   -> ops.decode
-``_FusedE8GEMMFunction``            :548-717   -> ops.e8t_linear / _bwd_dx
+``E8LatticePacker.pack``            :213-249   -> ops.encode2 (2-bit)
+``E8LatticePacker.unpack``          :252-279   -> ops.decode2
+``_get_packer_for_bitrate``         :536-541
+``_FusedE8GEMMFunction``            :548-717   -> ops.e8t_linear / ops.e8_linear
 ``E8LatticeLinear``                 :724-846
 ``pack_model_e8``                   :901-945
 =================================  ==========================================
 
-Only bitrate 1.5 is implemented here; 2.0 and 1.0 raise ``NotImplementedError``.
+Bitrates 1.5 (ternary) and 2.0 (2-bit, the reference's default for any bitrate
+other than 1.0 and 1.5) are implemented; 1.0 (RootE8LatticePacker) raises
+``NotImplementedError``.
 CPU tensors given to ``pack`` / ``unpack`` are processed on the current GPU and
 the result is returned on the CPU; the fused forward requires GPU tensors.
 """
@@ -35,6 +40,7 @@ from . import ops
 __all__ = [
     "fwht_block32",
     "TernaryE8LatticePacker",
+    "E8LatticePacker",
     "_FusedE8GEMMFunction",
     "E8LatticeLinear",
     "pack_model_e8",
@@ -130,11 +136,47 @@ class TernaryE8LatticePacker:
         return out.view(shape)
 
 
-def _require_ternary(bitrate: float) -> None:
-    if float(bitrate) != 1.5:
+class E8LatticePacker:
+    """Packs weight matrices into 2.0 bits/weight (4 weights per uint8 byte) with auto-padding."""
+
+    @staticmethod
+    def pack(w: torch.Tensor, group_size: int = 8
+             ) -> Tuple[torch.Tensor, torch.Tensor, Tuple[int, int]]:
+        m, n = w.shape
+        if group_size <= 0 or group_size % 8 != 0:
+            raise ValueError(f"group_size ({group_size}) must be a positive multiple of 8.")
+        packed, scales = ops.encode2(_on_gpu(w), group_size)
+        if w.device.type != "cuda":
+            packed, scales = packed.to(w.device), scales.to(w.device)
+        return packed, scales, (m, n)
+
+    @staticmethod
+    def unpack(packed_codes: torch.Tensor, scales: torch.Tensor, shape: Tuple[int, int],
+               dtype: torch.dtype = torch.float32, use_workspace: bool = False) -> torch.Tensor:
+        del use_workspace  # a shared scratch buffer in the reference; a fresh tensor here
+        total = shape[0] * shape[1]
+        padded = packed_codes.numel() * 4
+        group_size = padded // max(1, scales.numel())  # inferred as in lattice.py:264-266
+        out = ops.decode2(_on_gpu(packed_codes), _on_gpu(scales), total, group_size, dtype)
+        if packed_codes.device.type != "cuda":
+            out = out.to(packed_codes.device)
+        return out.view(shape)
+
+
+def _get_packer_for_bitrate(bitrate: float):
+    """lattice.py:536-541: 1.0 -> RootE8LatticePacker (not implemented here), 1.5 ->
+    TernaryE8LatticePacker, anything else -> E8LatticePacker."""
+    if bitrate == 1.0:
         raise NotImplementedError(
-            f"ojasx_amd implements the ternary (bitrate 1.5) E8 path; bitrate {bitrate} "
-            "is not available")
+            "ojasx_amd implements the ternary (1.5) and 2-bit E8 paths; bitrate 1.0 "
+            "(RootE8LatticePacker) is not available")
+    if bitrate == 1.5:
+        return TernaryE8LatticePacker
+    return E8LatticePacker
+
+
+def _require_supported(bitrate: float) -> None:
+    _get_packer_for_bitrate(float(bitrate))
 
 
 class _FusedE8GEMMFunction(torch.autograd.Function):
@@ -149,22 +191,25 @@ class _FusedE8GEMMFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, packed_weight, block_scales, bias, out_features, in_features,
                 group_size, bitrate, use_hadamard=False):
-        _require_ternary(bitrate)
+        _require_supported(bitrate)
         x_rot = fwht_block32(x) if (use_hadamard and in_features % 32 == 0) else x
         ctx.save_for_backward(packed_weight, block_scales)
         ctx.dims = (out_features, in_features, group_size)
+        ctx.ternary = float(bitrate) == 1.5
         ctx.x_shape = x_rot.shape
         ctx.has_bias = bias is not None
         ctx.use_hadamard = use_hadamard
-        return ops.e8t_linear(x_rot, packed_weight, block_scales, bias, out_features,
-                              in_features, group_size)
+        linear = ops.e8t_linear if ctx.ternary else ops.e8_linear
+        return linear(x_rot, packed_weight, block_scales, bias, out_features, in_features,
+                      group_size)
 
     @staticmethod
     def backward(ctx, grad_y):
         packed_weight, block_scales = ctx.saved_tensors
         out_features, in_features, group_size = ctx.dims
-        grad_x = ops.e8t_linear_bwd_dx(grad_y.contiguous(), packed_weight, block_scales,
-                                       out_features, in_features, group_size)
+        bwd = ops.e8t_linear_bwd_dx if ctx.ternary else ops.e8_linear_bwd_dx
+        grad_x = bwd(grad_y.contiguous(), packed_weight, block_scales, out_features,
+                     in_features, group_size)
         grad_x = grad_x.reshape(ctx.x_shape)
         if ctx.use_hadamard and in_features % 32 == 0:
             grad_x = fwht_block32(grad_x)
@@ -175,16 +220,16 @@ class _FusedE8GEMMFunction(torch.autograd.Function):
 class E8LatticeLinear(nn.Module):
     """Linear layer with base weights packed into the 8D E8 lattice (lattice.py:724-846).
 
-    Buffers ``packed_weight`` (uint8 [padded*3/16]) and ``block_scales`` (fp16
-    [padded/group]) have the reference's names, shapes and layout, so its
-    state_dicts load unchanged.  LoRA adapters as in the reference."""
+    Buffers ``packed_weight`` (uint8 [padded*3/16] at bitrate 1.5, [padded/4] at 2.0)
+    and ``block_scales`` (fp16 [padded/group]) have the reference's names, shapes and
+    layout, so its state_dicts load unchanged.  LoRA adapters as in the reference."""
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True, rank: int = 0,
                  lora_alpha: float = 16.0, group_size: int = 8, bitrate: float = 2.0,
                  use_hadamard: bool = False, device: Optional[torch.device] = None,
                  dtype: Optional[torch.dtype] = None) -> None:
         super().__init__()
-        _require_ternary(bitrate)
+        _require_supported(bitrate)
         self.in_features = in_features
         self.out_features = out_features
         self.rank = rank
@@ -194,11 +239,17 @@ class E8LatticeLinear(nn.Module):
         self.use_hadamard = bool(use_hadamard and (in_features % 32 == 0))
 
         total = out_features * in_features
-        eff_group = group_size if (group_size >= 16 and group_size % 16 == 0) else 16
-        padded = total + ((-total) % eff_group)
+        if self.bitrate == 1.5:  # lattice.py:752-766
+            eff_group = group_size if (group_size >= 16 and group_size % 16 == 0) else 16
+            padded = total + ((-total) % eff_group)
+            num_bytes = (padded * 3) // 16
+        else:
+            eff_group = group_size if (group_size >= 8 and group_size % 8 == 0) else 8
+            padded = total + ((-total) % eff_group)
+            num_bytes = padded // 4
         self.group_size = eff_group
         self.register_buffer("packed_weight",
-                             torch.zeros((padded * 3) // 16, dtype=torch.uint8, device=device))
+                             torch.zeros(num_bytes, dtype=torch.uint8, device=device))
         self.register_buffer("block_scales",
                              torch.ones(padded // eff_group, dtype=torch.float16, device=device))
         if bias:
@@ -218,15 +269,16 @@ class E8LatticeLinear(nn.Module):
     def from_linear(cls, linear: nn.Linear, rank: int = 0, lora_alpha: float = 16.0,
                     group_size: int = 8, bitrate: float = 2.0,
                     use_hadamard: bool = False) -> "E8LatticeLinear":
-        _require_ternary(bitrate)
-        eff_gs = max(16, group_size)  # lattice.py:793
+        _require_supported(bitrate)
+        eff_gs = max(16, group_size) if bitrate == 1.5 else group_size  # lattice.py:793
         m = cls(linear.in_features, linear.out_features, bias=(linear.bias is not None),
                 rank=rank, lora_alpha=lora_alpha, group_size=eff_gs, bitrate=bitrate,
                 use_hadamard=use_hadamard, device=linear.weight.device,
                 dtype=linear.weight.dtype)
         with torch.no_grad():
             w = fwht_block32(linear.weight) if m.use_hadamard else linear.weight
-            packed, scales, _ = TernaryE8LatticePacker.pack(w, group_size=m.group_size)
+            packer = _get_packer_for_bitrate(bitrate)
+            packed, scales, _ = packer.pack(w, group_size=m.group_size)
             m.packed_weight.copy_(packed)
             m.block_scales.copy_(scales)
             if linear.bias is not None:
@@ -234,8 +286,9 @@ class E8LatticeLinear(nn.Module):
         return m
 
     def unpack_weights(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
-        w = TernaryE8LatticePacker.unpack(self.packed_weight, self.block_scales,
-                                          (self.out_features, self.in_features), dtype=dtype)
+        packer = _get_packer_for_bitrate(self.bitrate)
+        w = packer.unpack(self.packed_weight, self.block_scales,
+                          (self.out_features, self.in_features), dtype=dtype)
         return fwht_block32(w) if self.use_hadamard else w
 
     def forward_fused(self, x: torch.Tensor) -> torch.Tensor:

@@ -14,6 +14,9 @@ Ops and the reference interfaces they replace:
 * ``fused_ternary_e8_gemm_fwd`` / ``fused_ternary_e8_gemm_bwd_dx``
     the reference's native op schemas (ojasx_math_bindings.cpp:593-594) with the
     binding's layout checks (:17-34, :414-433), for callers that bind the op by name.
+* 2-bit E8 (E8LatticePacker, lattice.py:209-279): ``encode2`` / ``decode2``,
+  ``e8_linear`` (autograd) / ``e8_linear_bwd_dx``, and the native schemas
+  ``fused_e8_gemm_fwd`` / ``fused_e8_gemm_bwd_dx`` (ojasx_math_bindings.cpp:591-592).
 
 Every op runs on the current HIP stream of the input's device, allocates its
 outputs through torch's caching allocator and raises ``RuntimeError`` for
@@ -259,5 +262,213 @@ def fused_ternary_e8_gemm_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tens
 
 
 @fused_ternary_e8_gemm_bwd_dx.register_fake
+def _(grad_y, packed_weight, block_scales, in_features, group_size=32):
+    return grad_y.new_empty((*grad_y.shape[:-1], in_features))
+
+
+# ----------------------------------------------------------------------------- 2-bit E8
+
+def _check_gs2(gs: int, unit: int) -> None:
+    if gs <= 0 or gs % unit != 0:
+        raise RuntimeError(f"group_size must be a positive multiple of {unit} (got {gs})")
+
+
+@torch.library.custom_op(f"{_NS}::encode2", mutates_args=())
+def encode2(w: torch.Tensor, group_size: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """E8LatticePacker.pack (lattice.py:213-249): (packed uint8 [padded/4], fp16 scales)."""
+    dev = N.require_device(w)
+    _check_gs2(group_size, 8)
+    if w.dtype not in N.DTYPE_CODE:
+        w = w.to(torch.float32)  # the reference widens to fp32 first (lattice.py:222)
+    w = w.contiguous()
+    numel = w.numel()
+    padded = _padded(numel, group_size)
+    packed = torch.empty(padded // 4, dtype=torch.uint8, device=dev)
+    scales = torch.empty(padded // group_size, dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8_encode(N.ptr(w), _dtype_code(w.dtype), numel, group_size,
+                                      N.ptr(packed), N.ptr(scales), N.stream_handle(dev)),
+                "e8 encode")
+    return packed, scales
+
+
+@encode2.register_fake
+def _(w, group_size):
+    padded = _padded(w.numel(), group_size)
+    return (w.new_empty(padded // 4, dtype=torch.uint8),
+            w.new_empty(padded // group_size, dtype=torch.float16))
+
+
+@torch.library.custom_op(f"{_NS}::decode2", mutates_args=())
+def decode2(packed: torch.Tensor, scales: torch.Tensor, numel: int, group_size: int,
+            dtype: torch.dtype) -> torch.Tensor:
+    """E8LatticePacker.unpack (lattice.py:252-279), flat, first ``numel`` weights."""
+    dev = N.require_device(packed, scales)
+    _check_gs2(group_size, 8)
+    if packed.dtype != torch.uint8 or scales.dtype != torch.float16:
+        raise RuntimeError("decode2 expects uint8 packed codes and float16 scales")
+    padded = _padded(numel, group_size)
+    if packed.numel() < padded // 4 or scales.numel() < padded // group_size:
+        raise RuntimeError(
+            f"packed/scales too small for {numel} weights at group_size {group_size}")
+    out = torch.empty(numel, dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8_decode(N.ptr(packed.contiguous()), N.ptr(scales.contiguous()),
+                                      numel, group_size, _dtype_code(dtype), N.ptr(out),
+                                      N.stream_handle(dev)),
+                "e8 decode")
+    return out
+
+
+@decode2.register_fake
+def _(packed, scales, numel, group_size, dtype):
+    return packed.new_empty(numel, dtype=dtype)
+
+
+def _check_layer_buffers2(packed: torch.Tensor, scales: torch.Tensor, out_features: int,
+                          in_features: int, group_size: int) -> None:
+    if packed.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if scales.dtype != torch.float16:
+        raise RuntimeError("block_scales must be float16")
+    padded = _padded(out_features * in_features, group_size)
+    if packed.numel() < padded // 4:
+        raise RuntimeError(
+            f"packed_weight holds {packed.numel()} bytes; {out_features}x{in_features} at "
+            f"group_size {group_size} needs {padded // 4}")
+    if scales.numel() < padded // group_size:
+        raise RuntimeError(
+            f"block_scales holds {scales.numel()} values; needs {padded // group_size}")
+
+
+@torch.library.custom_op(f"{_NS}::e8_linear", mutates_args=())
+def e8_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+              bias: Optional[torch.Tensor], out_features: int, in_features: int,
+              group_size: int) -> torch.Tensor:
+    """2-bit fused linear: x . Wdeq^T + bias, Wdeq = (code - 1.5) * scale in x's dtype."""
+    dev = N.require_device(x, packed_weight, block_scales, bias)
+    _check_gs2(group_size, 4)
+    if x.shape[-1] != in_features:
+        raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    _check_layer_buffers2(packed_weight, block_scales, out_features, in_features, group_size)
+    dt = _dtype_code(x.dtype)
+    x2 = x.reshape(-1, in_features).contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, out_features), dtype=x.dtype, device=dev)
+    b = None
+    if bias is not None:
+        if bias.numel() != out_features:
+            raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
+        b = bias.to(x.dtype).contiguous()
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8_gemm_fwd(N.ptr(x2), N.ptr(packed_weight.contiguous()),
+                                        N.ptr(block_scales.contiguous()), N.ptr(b), N.ptr(y), M,
+                                        out_features, in_features, group_size, dt,
+                                        N.stream_handle(dev)),
+                "e8 gemm_fwd")
+    return y.reshape(*x.shape[:-1], out_features)
+
+
+@e8_linear.register_fake
+def _(x, packed_weight, block_scales, bias, out_features, in_features, group_size):
+    return x.new_empty((*x.shape[:-1], out_features))
+
+
+@torch.library.custom_op(f"{_NS}::e8_linear_bwd_dx", mutates_args=())
+def e8_linear_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
+                     block_scales: torch.Tensor, out_features: int, in_features: int,
+                     group_size: int) -> torch.Tensor:
+    dev = N.require_device(grad_y, packed_weight, block_scales)
+    _check_gs2(group_size, 4)
+    if grad_y.shape[-1] != out_features:
+        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
+    _check_layer_buffers2(packed_weight, block_scales, out_features, in_features, group_size)
+    dt = _dtype_code(grad_y.dtype)
+    gy = grad_y.reshape(-1, out_features).contiguous()
+    M = gy.shape[0]
+    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8_gemm_bwd_dx(N.ptr(gy), N.ptr(packed_weight.contiguous()),
+                                           N.ptr(block_scales.contiguous()), N.ptr(gx), M,
+                                           out_features, in_features, group_size, dt,
+                                           N.stream_handle(dev)),
+                "e8 gemm_bwd_dx")
+    return gx.reshape(*grad_y.shape[:-1], in_features)
+
+
+@e8_linear_bwd_dx.register_fake
+def _(grad_y, packed_weight, block_scales, out_features, in_features, group_size):
+    return grad_y.new_empty((*grad_y.shape[:-1], in_features))
+
+
+def _linear2_backward(ctx, grad_y):
+    packed_weight, block_scales = ctx.saved_tensors
+    out_features, in_features, group_size = ctx.dims
+    grad_x = None
+    if ctx.needs_input_grad[0]:
+        grad_x = e8_linear_bwd_dx(grad_y, packed_weight, block_scales, out_features,
+                                  in_features, group_size)
+    grad_bias = grad_y.reshape(-1, out_features).sum(dim=0) if ctx.has_bias else None
+    return grad_x, None, None, grad_bias, None, None, None
+
+
+e8_linear.register_autograd(_linear2_backward, setup_context=_linear_setup_context)
+
+
+@torch.library.custom_op(f"{_NS}::fused_e8_gemm_fwd", mutates_args=())
+def fused_e8_gemm_fwd(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+                      bias: Optional[torch.Tensor] = None, group_size: int = 32) -> torch.Tensor:
+    """Same schema and checks as the reference's native op (ojasx_math_bindings.cpp:274-292)."""
+    if packed_weight.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if group_size <= 0 or group_size % 4 != 0:
+        raise RuntimeError("group_size must be a positive multiple of 4")
+    if x.dim() < 1:
+        raise RuntimeError("input must have a feature axis")
+    K = x.shape[-1]
+    if packed_weight.dim() != 2:
+        raise RuntimeError("packed_weight must be a 2D matrix")
+    if K <= 0 or K % 4 != 0 or K % group_size != 0:
+        raise RuntimeError("feature count must be divisible by the packing unit and group_size")
+    Nf = packed_weight.shape[0]
+    if block_scales.numel() != Nf * (K // group_size):
+        raise RuntimeError("block_scales must contain exactly N * (K / group_size) elements")
+    if packed_weight.shape[1] != K // 4:
+        raise RuntimeError("packed_weight dim 1 must match in_features / 4")
+    return e8_linear(x, packed_weight.reshape(-1), block_scales.reshape(-1).to(torch.float16),
+                     bias, Nf, K, group_size)
+
+
+@fused_e8_gemm_fwd.register_fake
+def _(x, packed_weight, block_scales, bias=None, group_size=32):
+    return x.new_empty((*x.shape[:-1], packed_weight.shape[0]))
+
+
+@torch.library.custom_op(f"{_NS}::fused_e8_gemm_bwd_dx", mutates_args=())
+def fused_e8_gemm_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
+                         block_scales: torch.Tensor, in_features: int,
+                         group_size: int = 32) -> torch.Tensor:
+    """Same schema and checks as the reference's native op (ojasx_math_bindings.cpp:346-366)."""
+    if packed_weight.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if packed_weight.dim() != 2:
+        raise RuntimeError("packed_weight must be 2D [N, K / 4]")
+    if packed_weight.shape[1] != in_features // 4:
+        raise RuntimeError("packed_weight dim 1 must match in_features / 4")
+    if group_size <= 0 or group_size % 4 != 0:
+        raise RuntimeError("group_size must be a positive multiple of 4")
+    K = in_features
+    if K <= 0 or K % 4 != 0 or K % group_size != 0:
+        raise RuntimeError("feature count must be divisible by the packing unit and group_size")
+    Nf = packed_weight.shape[0]
+    if block_scales.numel() != Nf * (K // group_size):
+        raise RuntimeError("block_scales must contain exactly N * (K / group_size) elements")
+    if grad_y.shape[-1] != Nf:
+        raise RuntimeError("Last dimension of grad_y must match N")
+    return e8_linear_bwd_dx(grad_y, packed_weight.reshape(-1),
+                            block_scales.reshape(-1).to(torch.float16), Nf, K, group_size)
+
+
+@fused_e8_gemm_bwd_dx.register_fake
 def _(grad_y, packed_weight, block_scales, in_features, group_size=32):
     return grad_y.new_empty((*grad_y.shape[:-1], in_features))

@@ -12,7 +12,7 @@ from typing import List, Tuple
 
 import torch
 
-from .lattice import TernaryE8LatticePacker, _require_ternary, fwht_block32
+from .lattice import _get_packer_for_bitrate, fwht_block32
 
 _SUPPORTED_BITRATES = {1.0, 1.5, 2.0}
 
@@ -23,7 +23,7 @@ def _validate_row_layout(out_features: int, in_features: int, bitrate: float,
     if float(bitrate) not in _SUPPORTED_BITRATES:
         raise ValueError(f"Unsupported E8 bitrate {bitrate!r}; expected one of "
                          f"{sorted(_SUPPORTED_BITRATES)}")
-    _require_ternary(bitrate)
+    _get_packer_for_bitrate(float(bitrate))  # 1.0 (Root E8) is not implemented
     if out_features <= 0 or in_features <= 0:
         raise ValueError("Streaming E8 requires non-empty two-dimensional weights")
     if group_size <= 0 or group_size % 32 != 0:
@@ -40,7 +40,8 @@ def _pack_row_block(block: torch.Tensor, bitrate: float, group_size: int,
                     use_hadamard: bool) -> Tuple[torch.Tensor, torch.Tensor]:
     """streaming_e8.py:112-123: the Hadamard pair is part of the layer transform."""
     source = fwht_block32(block) if use_hadamard else block
-    packed, scales, _ = TernaryE8LatticePacker.pack(source, group_size=group_size)
+    packer = _get_packer_for_bitrate(float(bitrate))
+    packed, scales, _ = packer.pack(source, group_size=group_size)
     return packed, scales
 
 

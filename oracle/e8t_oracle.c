@@ -18,6 +18,9 @@
  *   decoder             lattice.py:386-419
  *   portable forward    lattice.py:610-624  (unpack + F.linear)
  *
+ * The 2-bit E8 codec (E8LatticePacker, lattice.py:209-279) and its dequantize-then-
+ * matmul follow in the section "2-bit E8" below (ojo_e8b_*).
+ *
  * Pinning of each function (tests/test_oracle_*.py):
  *   ojo_f32_to_f16 / ojo_f32_to_bf16   vs numpy / torch conversions (library)
  *   ojo_e8t_group_scale                vs torch.norm(...)/math.sqrt(gs)+1e-8 (library)
@@ -27,6 +30,14 @@
  *   ojo_e8t_encode / _decode           byte layout closed form, the reference tests'
  *                                      invariants (size, cos > 0.7, row-wise == whole)
  *   ojo_e8t_gemm_f64                   vs the reference's C++ fused GEMV (oracle/_ref)
+ *   ojo_e8b_quantize8                  vs exhaustive nearest-point search over the even-
+ *                                      parity half-integer codewords for unclamped vectors,
+ *                                      plus hand-derived clamp / tie cases
+ *                                      (tests/golden/known_answers_e8b.json)
+ *   ojo_e8b_encode / _decode           byte layout closed form, the reference tests'
+ *                                      invariants, torch's own dtype products
+ *   ojo_e8b_gemm_f64 / _bwd_f64        vs the reference's C++ 2-bit fused GEMM and
+ *                                      backward (ojasx_math_core.hpp:440-534, oracle/_ref)
  */
 #include <math.h>
 #include <stdint.h>
@@ -356,4 +367,172 @@ OJO_API void ojo_e8t_group_scale_array(const float* w, int64_t ngroups, int64_t 
 }
 OJO_API void ojo_e8t_quantize8_array(const float* v, int64_t nvec, int32_t* codes) {
     for (int64_t t = 0; t < nvec; ++t) codes[t] = ojo_e8t_quantize8(v + 8 * t, 0);
+}
+
+/* ------------------------------------------------------------------------- */
+/* 2-bit E8 (E8LatticePacker, lattice.py:209-279)                             */
+/* ------------------------------------------------------------------------- */
+
+/* Group size rule of E8LatticePacker.pack (lattice.py:220-221): a positive multiple of 8,
+ * otherwise ValueError (the caller checks; -1 here). */
+OJO_API int64_t ojo_e8b_check_gs(int64_t gs) { return (gs <= 0 || gs % 8 != 0) ? -1 : gs; }
+
+/* One 8-vector v (already divided by the scale), lattice.py:229-238 step by step:
+ *   xs  = v - 0.5
+ *   f2  = clamp(round_half_even(xs), -2, 1)
+ *   alt = (xs >= f2) ? clamp(f2 + 1, -2, 1) : clamp(f2 - 1, -2, 1)
+ *   pen = (alt - xs)^2 - (f2 - xs)^2          (five separately rounded fp32 ops)
+ *   if sum(f2) is odd: f2[first argmin pen] = alt[...]
+ *   code_i = f2_i + 2                          (= clamp(round(f2 + 0.5 + 1.5), 0, 3))
+ * A coordinate clamped at -2 or 1 has alt == f2 and pen == 0: when it is the first
+ * minimum, the "flip" changes nothing and the vector keeps an odd sum, as the
+ * reference's does.  Writes the 8 codes (0..3) to codes[]. */
+OJO_API void ojo_e8b_quantize8(const float v[8], uint8_t codes[8]) {
+    float xs[8], f2[8], alt[8], pen[8];
+    float sum = 0.0f;
+    for (int i = 0; i < 8; ++i) {
+        xs[i] = v[i] - 0.5f;
+        float r = rintf(xs[i]);
+        if (r < -2.0f) r = -2.0f;
+        if (r > 1.0f) r = 1.0f;
+        f2[i] = r;
+        sum += r; /* small integers: exact */
+    }
+    for (int i = 0; i < 8; ++i) {
+        float up = f2[i] + 1.0f, dn = f2[i] - 1.0f;
+        if (up > 1.0f) up = 1.0f;
+        if (dn < -2.0f) dn = -2.0f;
+        alt[i] = (xs[i] >= f2[i]) ? up : dn;
+        float a = alt[i] - xs[i];
+        float b = f2[i] - xs[i];
+        float a2 = a * a;
+        float b2 = b * b;
+        pen[i] = a2 - b2;
+    }
+    if (((int)sum) & 1) {
+        int best = 0;
+        for (int i = 1; i < 8; ++i)
+            if (pen[i] < pen[best]) best = i;
+        f2[best] = alt[best];
+    }
+    for (int i = 0; i < 8; ++i) codes[i] = (uint8_t)((int)f2[i] + 2);
+}
+
+/* Encode one flat group of gs fp32 weights: scale as the ternary packer's
+ * (lattice.py:227 is the same expression), codes 4 per byte, code j of a byte in
+ * bits [2j, 2j+2) (lattice.py:242-247). */
+static void e8b_encode_group(const float* w, int64_t gs, uint8_t* packed, uint16_t* scale16,
+                             float* scale32) {
+    float s = ojo_e8t_group_scale(w, gs);
+    for (int64_t t = 0; t < gs / 8; ++t) {
+        float v[8];
+        uint8_t c[8];
+        for (int i = 0; i < 8; ++i) v[i] = w[8 * t + i] / s;
+        ojo_e8b_quantize8(v, c);
+        packed[2 * t] = (uint8_t)(c[0] | (c[1] << 2) | (c[2] << 4) | (c[3] << 6));
+        packed[2 * t + 1] = (uint8_t)(c[4] | (c[5] << 2) | (c[6] << 4) | (c[7] << 6));
+    }
+    *scale16 = ojo_f32_to_f16(s);
+    if (scale32) *scale32 = s;
+}
+
+/* E8LatticePacker.pack on a flat fp32 array of numel values (gs a positive multiple
+ * of 8).  packed: padded/4 bytes; scales: padded/gs fp16 bits; scales32 optional. */
+OJO_API void ojo_e8b_encode(const float* w, int64_t numel, int64_t gs, uint8_t* packed,
+                            uint16_t* scales, float* scales32, int nthreads) {
+    int64_t padded = ojo_e8t_padded(numel, gs);
+    int64_t ngroups = padded / gs;
+    int64_t full = numel / gs;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t g = 0; g < full; ++g)
+        e8b_encode_group(w + g * gs, gs, packed + g * gs / 4, scales + g,
+                         scales32 ? scales32 + g : 0);
+    (void)nthreads;
+    if (full < ngroups) { /* tail group, zero padded (F.pad, lattice.py:223-225) */
+        float buf[4096];
+        if (gs > 4096) return; /* not reachable from the tests */
+        int64_t rem = numel - full * gs;
+        for (int64_t i = 0; i < gs; ++i) buf[i] = i < rem ? w[full * gs + i] : 0.0f;
+        e8b_encode_group(buf, gs, packed + full * gs / 4, scales + full,
+                         scales32 ? scales32 + full : 0);
+    }
+}
+
+/* Decoded weight as E8LatticePacker.unpack produces it for out dtype
+ * (lattice.py:274-276): (codes.to(dtype) - 1.5) * scales.to(dtype), the product
+ * rounded to dtype (torch computes it in fp32 and rounds once).
+ *   dtype 0 (fp32): (c - 1.5) * float(s16)                exact
+ *   dtype 1 (fp16): fp16_rne((c - 1.5) * float(s16))
+ *   dtype 2 (bf16): bf16_rne((c - 1.5) * bf16_rne(float(s16))) */
+static inline float e8b_deq_value(int code, uint16_t s16, int dtype) {
+    float s = ojo_f16_to_f32(s16);
+    if (dtype == 2) s = ojo_bf16_to_f32(ojo_f32_to_bf16(s));
+    float p = ((float)code - 1.5f) * s; /* exact in fp32 */
+    if (dtype == 1) return ojo_f16_to_f32(ojo_f32_to_f16(p));
+    if (dtype == 2) return ojo_bf16_to_f32(ojo_f32_to_bf16(p));
+    return p;
+}
+
+static inline int e8b_code(const uint8_t* packed, int64_t f) {
+    return (packed[f >> 2] >> (2 * (f & 3))) & 3;
+}
+
+/* Unpack into numel values; gs = padded / numel(scales) as the reference infers it
+ * (lattice.py:264-266).  out_dtype: 0 f32, 1 f16 bits, 2 bf16 bits. */
+OJO_API void ojo_e8b_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel,
+                            int64_t gs, int out_dtype, void* out) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t f = 0; f < numel; ++f) {
+        float v = e8b_deq_value(e8b_code(packed, f), scales[f / gs], out_dtype);
+        if (out_dtype == 0) ((float*)out)[f] = v;
+        else if (out_dtype == 1) ((uint16_t*)out)[f] = ojo_f32_to_f16(v);
+        else ((uint16_t*)out)[f] = ojo_f32_to_bf16(v);
+    }
+}
+
+/* y = x . Wdeq^T + bias in fp64, Wdeq by the dtype rule above (the portable path,
+ * lattice.py:618-623).  Flat layout: element (n, k) is flat index n*K + k. */
+OJO_API void ojo_e8b_gemm_f64(const float* x, const uint8_t* packed, const uint16_t* scales,
+                              const float* bias, double* y, int64_t M, int64_t N, int64_t K,
+                              int64_t gs, int w_dtype) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t n = 0; n < N; ++n) {
+        double wrow_buf[16384];
+        double* wrow = wrow_buf;
+        if (K > 16384) continue; /* not reachable from the tests */
+        for (int64_t k = 0; k < K; ++k) {
+            int64_t f = n * K + k;
+            wrow[k] = (double)e8b_deq_value(e8b_code(packed, f), scales[f / gs], w_dtype);
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            double acc = bias ? (double)bias[n] : 0.0;
+            const float* xr = x + m * K;
+            for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * wrow[k];
+            y[m * N + n] = acc;
+        }
+    }
+}
+
+/* grad_x = gy . Wdeq in fp64 (lattice.py:686-696 with the 2-bit unpack). */
+OJO_API void ojo_e8b_gemm_bwd_f64(const float* gy, const uint8_t* packed, const uint16_t* scales,
+                                  double* gx, int64_t M, int64_t N, int64_t K, int64_t gs,
+                                  int w_dtype) {
+    memset(gx, 0, sizeof(double) * (size_t)(M * K));
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t k = 0; k < K; ++k) {
+            int64_t f = n * K + k;
+            double wv = (double)e8b_deq_value(e8b_code(packed, f), scales[f / gs], w_dtype);
+            for (int64_t m = 0; m < M; ++m) gx[m * K + k] += (double)gy[m * N + n] * wv;
+        }
+}
+
+OJO_API void ojo_e8b_quantize8_array(const float* v, int64_t nvec, uint8_t* codes) {
+    for (int64_t t = 0; t < nvec; ++t) ojo_e8b_quantize8(v + 8 * t, codes + 8 * t);
 }

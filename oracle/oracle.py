@@ -1,4 +1,5 @@
-"""CPU oracle for the ternary-E8 path -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for the E8 quantized-weight paths (ternary 1.5-bit and 2-bit) -- TEST
+INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
 leg import this module, and only as the checker.  The product package never
@@ -79,6 +80,20 @@ def lib() -> ctypes.CDLL:
         L.ojo_e8t_group_scale_array.argtypes = [_P, _I64, _I64, _P]
         L.ojo_e8t_quantize8_array.restype = None
         L.ojo_e8t_quantize8_array.argtypes = [_P, _I64, _P]
+        L.ojo_e8b_check_gs.restype = _I64
+        L.ojo_e8b_check_gs.argtypes = [_I64]
+        L.ojo_e8b_quantize8.restype = None
+        L.ojo_e8b_quantize8.argtypes = [_P, _P]
+        L.ojo_e8b_quantize8_array.restype = None
+        L.ojo_e8b_quantize8_array.argtypes = [_P, _I64, _P]
+        L.ojo_e8b_encode.restype = None
+        L.ojo_e8b_encode.argtypes = [_P, _I64, _I64, _P, _P, _P, ctypes.c_int]
+        L.ojo_e8b_decode.restype = None
+        L.ojo_e8b_decode.argtypes = [_P, _P, _I64, _I64, ctypes.c_int, _P]
+        L.ojo_e8b_gemm_f64.restype = None
+        L.ojo_e8b_gemm_f64.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
+        L.ojo_e8b_gemm_bwd_f64.restype = None
+        L.ojo_e8b_gemm_bwd_f64.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -97,6 +112,10 @@ def ref() -> ctypes.CDLL:
         R.ojr_ternary_fwd_f32.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]
         R.ojr_ternary_bwd_dx_f32.restype = None
         R.ojr_ternary_bwd_dx_f32.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64]
+        R.ojr_e8_fwd_f32.restype = None
+        R.ojr_e8_fwd_f32.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]
+        R.ojr_e8_bwd_dx_f32.restype = None
+        R.ojr_e8_bwd_dx_f32.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64]
         _ref = R
     return _ref
 
@@ -263,4 +282,97 @@ def ref_fused_bwd_dx(gy: np.ndarray, packed: np.ndarray, scales_f32: np.ndarray,
     s = np.ascontiguousarray(scales_f32, dtype=np.float32)
     ref().ojr_ternary_bwd_dx_f32(_ptr(gy), _ptr(np.ascontiguousarray(packed)), _ptr(s),
                                  _ptr(gx), M, K, N, int(group_size))
+    return gx
+
+
+# --------------------------------------------------------------------------
+# 2-bit E8 (E8LatticePacker, lattice.py:209-279)
+# --------------------------------------------------------------------------
+
+def e8b_quantize8_many(v: np.ndarray) -> np.ndarray:
+    """Codes (0..3) of n 8-vectors v [n, 8] (already divided by their scale)."""
+    v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1, 8)
+    codes = np.empty(v.shape, dtype=np.uint8)
+    lib().ojo_e8b_quantize8_array(_ptr(v), v.shape[0], _ptr(codes))
+    return codes
+
+
+def e8b_encode(w: np.ndarray, group_size: int = 8, nthreads: int = 0
+               ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """E8LatticePacker.pack on the flattened fp32 values of ``w``.
+
+    Returns (packed uint8 [padded/4], scales fp16 bits uint16 [padded/gs],
+    scales32 fp32 [padded/gs]).  A group size that is not a positive multiple of 8
+    raises ValueError, as lattice.py:220-221 does."""
+    if lib().ojo_e8b_check_gs(int(group_size)) < 0:
+        raise ValueError(f"group_size ({group_size}) must be a positive multiple of 8.")
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    p = padded(w.size, group_size)
+    packed = np.empty(p // 4, dtype=np.uint8)
+    scales = np.empty(p // group_size, dtype=np.uint16)
+    scales32 = np.empty(p // group_size, dtype=np.float32)
+    lib().ojo_e8b_encode(_ptr(w), w.size, int(group_size), _ptr(packed), _ptr(scales),
+                         _ptr(scales32), int(nthreads))
+    return packed, scales, scales32
+
+
+def e8b_decode(packed: np.ndarray, scales: np.ndarray, numel: int, group_size: int,
+               dtype: int = DT_F32) -> np.ndarray:
+    """E8LatticePacker.unpack: fp32 values, or fp16 / bf16 bit patterns."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint16)
+    out = np.empty(numel, dtype=np.float32 if dtype == DT_F32 else np.uint16)
+    lib().ojo_e8b_decode(_ptr(packed), _ptr(scales), numel, int(group_size), int(dtype),
+                         _ptr(out))
+    return out
+
+
+def e8b_gemm_f64(x: np.ndarray, packed: np.ndarray, scales: np.ndarray,
+                 bias: Optional[np.ndarray], N: int, K: int, group_size: int,
+                 w_dtype: int = DT_F32) -> np.ndarray:
+    """fp64-accumulated x @ Wdeq^T + bias, Wdeq by the 2-bit dtype rule."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
+    M = x.shape[0]
+    y = np.empty((M, N), dtype=np.float64)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().ojo_e8b_gemm_f64(_ptr(x), _ptr(np.ascontiguousarray(packed)),
+                           _ptr(np.ascontiguousarray(scales, dtype=np.uint16)),
+                           None if b is None else _ptr(b), _ptr(y), M, N, K,
+                           int(group_size), int(w_dtype))
+    return y
+
+
+def e8b_gemm_bwd_f64(gy: np.ndarray, packed: np.ndarray, scales: np.ndarray, N: int, K: int,
+                     group_size: int, w_dtype: int = DT_F32) -> np.ndarray:
+    gy = np.ascontiguousarray(gy, dtype=np.float32).reshape(-1, N)
+    M = gy.shape[0]
+    gx = np.empty((M, K), dtype=np.float64)
+    lib().ojo_e8b_gemm_bwd_f64(_ptr(gy), _ptr(np.ascontiguousarray(packed)),
+                               _ptr(np.ascontiguousarray(scales, dtype=np.uint16)), _ptr(gx),
+                               M, N, K, int(group_size), int(w_dtype))
+    return gx
+
+
+def ref_e8_fused_fwd(x: np.ndarray, packed: np.ndarray, scales_f32: np.ndarray,
+                     bias: Optional[np.ndarray], N: int, K: int, group_size: int) -> np.ndarray:
+    """The reference's C++ 2-bit fused forward (ojasx_math_core.hpp:440-483)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
+    M = x.shape[0]
+    y = np.empty((M, N), dtype=np.float32)
+    s = np.ascontiguousarray(scales_f32, dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    ref().ojr_e8_fwd_f32(_ptr(x), _ptr(np.ascontiguousarray(packed)), _ptr(s),
+                         None if b is None else _ptr(b), _ptr(y), M, K, N, int(group_size))
+    return y
+
+
+def ref_e8_fused_bwd_dx(gy: np.ndarray, packed: np.ndarray, scales_f32: np.ndarray, N: int,
+                        K: int, group_size: int) -> np.ndarray:
+    """The reference's C++ 2-bit fused backward dX (ojasx_math_core.hpp:490-534)."""
+    gy = np.ascontiguousarray(gy, dtype=np.float32).reshape(-1, N)
+    M = gy.shape[0]
+    gx = np.empty((M, K), dtype=np.float32)
+    s = np.ascontiguousarray(scales_f32, dtype=np.float32)
+    ref().ojr_e8_bwd_dx_f32(_ptr(gy), _ptr(np.ascontiguousarray(packed)), _ptr(s), _ptr(gx),
+                            M, K, N, int(group_size))
     return gx

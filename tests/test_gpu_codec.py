@@ -212,3 +212,22 @@ def test_encode_does_not_call_cpu_on_device_tensors():
         packed, scales, shape = ojasx_amd.TernaryE8LatticePacker.pack(w, group_size=32)
         rec = ojasx_amd.TernaryE8LatticePacker.unpack(packed, scales, shape)
         assert rec.is_cuda
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_negative_zero_of_zero_scales(dtype):
+    # arbitrary valid codes with zero scales: coord -1 times scale 0 is -0 in the reference
+    # (coords.to(dtype) * scales.to(dtype), lattice.py:414-418)
+    rng = np.random.default_rng(77)
+    n, gs = 64 * 128, 32
+    codes = rng.integers(0, 3281, n // 8)
+    c0, c1 = codes[0::2], codes[1::2]
+    packed = np.stack([c0 & 0xFF, ((c0 >> 8) & 0xF) | ((c1 & 0xF) << 4), (c1 >> 4) & 0xFF],
+                      axis=1).astype(np.uint8).reshape(-1)
+    s = (np.abs(rng.standard_normal(n // gs)) * 0.02).astype(np.float16)
+    s[::3] = 0
+    out = ops.decode(torch.from_numpy(packed).to(DEV), torch.from_numpy(s).to(DEV), n, gs, dtype)
+    ref = O.decode(packed, s.view(np.uint16), n, gs,
+                   O.DT_F16 if dtype == torch.float16 else O.DT_BF16)
+    assert (ref == 0x8000).any()
+    assert np.array_equal(_u16(out), ref)

@@ -22,7 +22,7 @@ HEADER = os.path.join(ROOT, "include", "ojasx_e8t.h")
 
 def _declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(ojx_e8t_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ojx_e8t?_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_exports():
@@ -58,6 +58,17 @@ def test_abi_rejects_bad_arguments_before_launch():
     # empty work is a no-op success
     assert lib.ojx_e8t_encode(None, 0, 0, 32, None, None, None) == 0
     assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, None) == 0
+    # 2-bit: the packer's group rule (multiple of 8), the native op's (multiple of 4)
+    assert lib.ojx_e8_encode(None, 0, 64, 12, None, None, None) == -2
+    assert b"multiple of 8" in lib.ojx_e8t_last_error()
+    assert lib.ojx_e8_encode(None, 0, -1, 8, None, None, None) == -1
+    assert lib.ojx_e8_decode(None, None, 16, 4, 0, None, None) == -2
+    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 1, 4, 8, 6, 0, None) == -2
+    assert b"multiple of 4" in lib.ojx_e8t_last_error()
+    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 1, 4, 8, 4, 9, None) == -3
+    assert lib.ojx_e8_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None) == -1
+    assert lib.ojx_e8_encode(None, 0, 0, 8, None, None, None) == 0
+    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -88,11 +99,33 @@ def test_layer_state_dict_keys_match_reference():
     assert set(layer.state_dict()) == {"packed_weight", "block_scales", "bias", "lora_A", "lora_B"}
 
 
-def test_non_ternary_bitrates_raise():
+def test_root_e8_bitrate_raises():
+    # bitrate 1.0 (RootE8LatticePacker) is not implemented; every other bitrate but 1.5
+    # selects the 2-bit packer, as lattice.py:536-541 does
     with pytest.raises(NotImplementedError):
-        ojasx_amd.E8LatticeLinear(64, 32, bitrate=2.0)
+        ojasx_amd.E8LatticeLinear(64, 32, bitrate=1.0)
     with pytest.raises(NotImplementedError):
         ojasx_amd.E8LatticeLinear.from_linear(nn.Linear(32, 32), bitrate=1.0)
+    assert ojasx_amd._get_packer_for_bitrate(2.0) is ojasx_amd.E8LatticePacker
+    assert ojasx_amd._get_packer_for_bitrate(3.0) is ojasx_amd.E8LatticePacker
+    assert ojasx_amd._get_packer_for_bitrate(1.5) is ojasx_amd.TernaryE8LatticePacker
+
+
+@pytest.mark.parametrize("gs,eff", [(8, 8), (4, 8), (12, 8), (16, 16), (32, 32), (24, 24)])
+def test_2bit_layer_buffer_shapes_and_group_coercion(gs, eff):
+    # lattice.py:756-767 (2-bit branch): group >= 8 and a multiple of 8, else 8
+    layer = ojasx_amd.E8LatticeLinear(128, 96, rank=2, group_size=gs, bitrate=2.0)
+    assert layer.group_size == eff
+    total = 128 * 96
+    padded = total + ((-total) % eff)
+    assert layer.packed_weight.shape == (padded // 4,)
+    assert layer.block_scales.shape == (padded // eff,)
+
+
+def test_2bit_packer_group_size_error():
+    # lattice.py:220-221: ValueError, not a coercion
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ojasx_amd.E8LatticePacker.pack(torch.randn(4, 32), group_size=12)
 
 
 def test_rowwise_layout_validation_messages():
