@@ -318,6 +318,10 @@ __attribute__((visibility("default"))) int ojx_e8_gemm_fwd(const void* x, const 
     if (int r = check_gemm2_args(x, packed, scales, y, M, N, K, gs, dtype)) return r;
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
+    if (ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
+        return done(ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype,
+                                      (hipStream_t)stream),
+                    "e8 gemv launch");
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype,
                                              (hipStream_t)stream, ojx::kFmt2Bit),
                 "e8 gemm_fwd launch");

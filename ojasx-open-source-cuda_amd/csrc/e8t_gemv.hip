@@ -311,6 +311,7 @@ struct WideCodes {
 template <int R>
 struct WideScales {
     uint32_t sc[R][4];   // the 8 group scales covering the 32 codes
+    bool live;           // false: the lane group's k range is past K (its scales count as 0)
 };
 
 // LDS destination operand of a buffer->LDS load (kept out of templates: the host pass of
@@ -689,19 +690,22 @@ __device__ __forceinline__ void ps_issue(char* stg, __amdgpu_buffer_rsrc_t packe
 
 // The 8 scales of this lane's codes in round u (16 contiguous bytes per lane: every load
 // covers whole 64-byte row segments).  Lane groups past K in a partial last round read the
-// next row's codes: their scales are zeroed so those codes contribute exactly zero.
+// next row's codes: sc.live is false and their scales count as zero where they are used,
+// so those codes contribute exactly zero.  (Zeroing the loaded words here would make the
+// compiler wait for the load, and with it for every load issued before it, right away.)
 template <int R>
 __device__ __forceinline__ void ps_load_scales(WideScales<R>& sc, const PsStream<R>& st,
                                                int64_t scale_shift, int u, int64_t K, int g) {
     const bool live = (int64_t)u * kRound + 256 * g < K;
     const int so = uniform_offset(scale_shift + (int64_t)u * 64);
+    sc.live = live;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r], so, 0);
-        sc.sc[r][0] = live ? v.x : 0u;
-        sc.sc[r][1] = live ? v.y : 0u;
-        sc.sc[r][2] = live ? v.z : 0u;
-        sc.sc[r][3] = live ? v.w : 0u;
+        sc.sc[r][0] = v.x;
+        sc.sc[r][1] = v.y;
+        sc.sc[r][2] = v.z;
+        sc.sc[r][3] = v.w;
     }
 }
 
@@ -751,7 +755,8 @@ __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<
     }
     if constexpr (J % 8 == 0) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) scale_pair_f32<DT>(sc.sc[r][J / 8], sf[r][0], sf[r][1]);
+        for (int r = 0; r < R; ++r)
+            scale_pair_f32<DT>(sc.live ? sc.sc[r][J / 8] : 0u, sf[r][0], sf[r][1]);
     }
     constexpr bool kFresh = J + kLookahead < 32;
     uint4 xa_n, b_n[R];
@@ -794,11 +799,41 @@ __device__ __forceinline__ void ps_round(const WideCodes<R>& w, const WideScales
                         std::make_integer_sequence<int, 32>{});
 }
 
+// Bias bits of this lane's rows of one tile group (0 without bias; rows past N read row
+// N - 1 and are never stored).  Unconditional loads whose conversion waits until the
+// store, so that issuing them costs no wait.
+template <int DT, int R>
+__device__ __forceinline__ void ps_load_bias(const GemvJob& job, int64_t tile0, int lane,
+                                             uint32_t (&bv)[R]) {
+    const int i16 = lane & 15;
+#pragma unroll
+    for (int r = 0; r < R; ++r) bv[r] = 0u;
+    if (!job.bias) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int64_t row = (tile0 + r) * 16 + i16;
+        row = row < job.N ? row : job.N - 1;
+        // global (not flat) loads: a wait for a flat load is a wait for every load
+        if constexpr (DT == kF32)
+            bv[r] = ((const __attribute__((address_space(1))) uint32_t*)job.bias)[row];
+        else
+            bv[r] = ((const __attribute__((address_space(1))) uint16_t*)job.bias)[row];
+    }
+}
+
+template <int DT> __device__ __forceinline__ float bias_bits_to_f32(uint32_t b) {
+    if constexpr (DT == kF32) return __uint_as_float(b);
+    else if constexpr (DT == kF16) return f16_bits_to_f32(b);
+    else return bf16_bits_to_f32(b);
+}
+
 // Sums the four lane groups of each row and stores one tile group's outputs (lane group q
-// stores activation row q); clears the accumulators.
+// stores activation row q) with the bias values bv (ps_load_bias, loaded before the next
+// item's prefetch so that waiting for them does not wait for the prefetch); clears the
+// accumulators.
 template <int DT, int R, int MM>
 __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M, int64_t tile0,
-                                         int lane, float (&acc)[R][MM]) {
+                                         int lane, float (&acc)[R][MM], const uint32_t (&bv)[R]) {
     const int g = lane >> 4, i16 = lane & 15;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -812,10 +847,8 @@ __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M,
             if (q == g) out = v;
             acc[r][q] = 0.f;
         }
-        if (row < job.N && g < M) {
-            const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
-            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out + bv);
-        }
+        if (row < job.N && g < M)
+            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out + bias_bits_to_f32<DT>(bv[r]));
     }
 }
 
@@ -828,12 +861,20 @@ template <int DT, int R, int MM, int W>
 __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch args) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
     __shared__ uint4 lut_storage[kLutValidStorageU4];
-    __shared__ __attribute__((aligned(16))) char xs_storage[2][MM * kXRow];
-    __shared__ __attribute__((aligned(16))) uint4 xzero[32];  // A rows outside a lane's group
+    // Two activation buffers, separate LDS objects, each ending in 512 zero bytes (the A rows
+    // outside a lane's group): every activation read then points into one known buffer, so
+    // the compiler does not hold it behind the pending buffer->LDS loads into the other one
+    // (or into the code stage).
+    constexpr int kXBytes = MM * kXRow;
+    __shared__ __attribute__((aligned(16))) char xsa[kXBytes + 512];
+    __shared__ __attribute__((aligned(16))) char xsb[kXBytes + 512];
     __shared__ PsStage<R> stage[W];
 
     fill_lut<64 * W, kLutValidEntries>(lut_storage, lut_values_kind<DT>());
-    if (threadIdx.x < 32) xzero[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    if (threadIdx.x < 32) {
+        reinterpret_cast<uint4*>(xsa + kXBytes)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+        reinterpret_cast<uint4*>(xsb + kXBytes)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    }
 
     int64_t wg = blockIdx.x;
     GemvJob job;
@@ -889,13 +930,13 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
     const int am = i16 & 3;
     const bool a_live = (i16 >> 2) == g && am < M;
-    const char* xa0 = a_live ? xs_storage[0] + am * kXRow + 512 * g
-                             : reinterpret_cast<const char*>(xzero);
-    const char* xa1 = a_live ? xs_storage[1] + am * kXRow + 512 * g
-                             : reinterpret_cast<const char*>(xzero);
+    const char* xa0 = xsa + (a_live ? am * kXRow + 512 * g : kXBytes);
+    const char* xa1 = xsb + (a_live ? am * kXRow + 512 * g : kXBytes);
 
     // Items are (tile group c0 + c, round u), c-major; item (c, u) is processed while the
-    // next item's codes, scales and activations are fetched.
+    // next item's codes, scales and activations are fetched.  Items alternate between the
+    // activation buffers xsa and xsb (the loop is unrolled by two so that each buffer is a
+    // compile-time choice).
     const int T = (int)((K + kRound - 1) / kRound);
     const int ngroups = (int)(c1 - c0);
     const int64_t code_gshift = kGroupRows * (int64_t)rowbytes;
@@ -912,31 +953,40 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     WideScales<R> sc, sc_next;
     ps_issue(stg_bytes, st.packed, st.ld_code, R, 0, 0);
     ps_load_scales<R>(sc, st, 0, 0, K, g);
-    stage_x(xs_storage[0], st.x, 0, M, K, wave, lane, W);
+    stage_x(xsa, st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
-    __syncthreads();  // table, zero block, round-0 weights and activations ready
+    __syncthreads();  // table, zero blocks, round-0 weights and activations ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
 
-    int c = 0, u = 0, buf = 0;
-    for (;;) {
+    int c = 0, u = 0;
+    // one item: computes from the activation buffer behind xa_cur, fetches the next item
+    // into xs_next; false when there is no next item
+    auto item = [&](const char* xa_cur, char* xs_next) -> bool {
         ps_readback<R>(stg, st, w);
+        const int64_t tg = tile0 + (int64_t)c * W * R;
+        uint32_t bv[R];
+        if (u == T - 1) ps_load_bias<DT, R>(job, tg, lane, bv);
         lds_wait_all();  // the read-back has landed: the stage may be refilled
         const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
         const bool has = cn < ngroups;  // uniform over the workgroup
         if (has) {
             ps_issue(stg_bytes, st.packed, st.ld_code, R, cn * code_gshift, un);
             ps_load_scales<R>(sc_next, st, cn * scale_gshift, un, K, g);
-            stage_x(xs_storage[buf ^ 1], st.x, un, M, K, wave, lane, W);
+            stage_x(xs_next, st.x, un, M, K, wave, lane, W);
         }
-        ps_round<DT, R, MM>(w, sc, lut, slot, buf ? xa1 : xa0, acc);
-        if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0 + (int64_t)c * W * R, lane, acc);
-        if (!has) break;
+        ps_round<DT, R, MM>(w, sc, lut, slot, xa_cur, acc);
+        if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tg, lane, acc, bv);
+        if (!has) return false;
         vm_wait_all();
         __syncthreads();  // next item's codes (own stage) and activations (shared) ready
         sc = sc_next;
         c = cn;
         u = un;
-        buf ^= 1;
+        return true;
+    };
+    for (;;) {
+        if (!item(xa0, xsb)) break;
+        if (!item(xa1, xsa)) break;
     }
 }
 
@@ -1043,7 +1093,297 @@ __global__ __launch_bounds__(64 * W) void gemv_psk_kernel(GemvLaunch args) {
     for (int w2 = 1; w2 < W; ++w2)
 #pragma unroll
         for (int q = 0; q < MM; ++q) acc[0][q] += red[w2][q][lane];
-    ps_store<DT, R, MM>(job, ybase, M, tile0, lane, acc);
+    uint32_t bv[R];
+    ps_load_bias<DT, R>(job, tile0, lane, bv);
+    ps_store<DT, R, MM>(job, ybase, M, tile0, lane, acc, bv);
+}
+
+// ------------------------------------------------------------------------- 2-bit GEMV
+//
+// Decode GEMV (M <= 4) over 2-bit E8 weights (E8LatticePacker: four 2-bit codes per byte,
+// one fp16 scale per gs weights): y = x . ((code - 1.5) * s)^T, fp32 accumulation, the
+// group scale (in the activation dtype, as the native binding casts it,
+// ojasx_math_bindings.cpp:286) applied to fp32 partial sums per group, as the reference's
+// own 2-bit fused kernel does (ojasx_math_core.hpp:454-479: acc += group_acc * scale).
+//
+// Each wave owns one 16-row tile and walks K in 1024-k rounds.  A round of a row is 256
+// code bytes (16 pieces of 16 bytes, 64 weights each) and 2048/gs scale bytes.  Lane (g, n)
+// takes pieces g, 4 + g, 8 + g and 12 + g of row n: load t of the wave reads piece 4t + g of
+// all 16 rows, so the four lane groups read 64 contiguous bytes of each row per
+// instruction; scales use the same mapping (128/gs bytes per piece).  The next round's
+// pieces are loaded into a second register set while the current round computes.
+//
+// Step J (0..31) of a round takes the 8 codes of half-word J % 8 of piece J / 8, k = 64 (4t +
+// g) + 8 (J % 8).  Every 4-bit nibble (two codes) indexes a 16-entry table of weight pairs
+// (code - 1.5 in the activation dtype, exact) with 32 copies: one conflict-free b32 read per
+// pair of weights.  A row 4g' + m carries activation row m only in lane group g''s k slots
+// (a zero block elsewhere), so the MFMA output of lane (g', n) is the partial sum of its own
+// k slots and its group scale can multiply it every gs/8 steps; the four lane groups are
+// added at the end.
+
+constexpr int kB2Waves = 4;
+constexpr int kB2LutU4 = 16 * 32 * 4 / 16;  // 16 entries x 32 copies x 4 bytes
+constexpr int kB2ZeroBytes = 2048;          // covers the largest A-fragment offset of a round
+
+template <int DT>
+__device__ __forceinline__ uint32_t b2_half(int c) {  // code c -> (c - 1.5) in dtype bits
+    if constexpr (DT == kBF16) return c == 0 ? 0xBFC0u : c == 1 ? 0xBF00u : c == 2 ? 0x3F00u : 0x3FC0u;
+    else return c == 0 ? 0xBE00u : c == 1 ? 0xB800u : c == 2 ? 0x3800u : 0x3E00u;
+}
+
+template <int DT, int NT>
+__device__ __forceinline__ void fill_b2lut(uint4* lut) {
+    for (int i = (int)threadIdx.x; i < kB2LutU4; i += NT) {
+        const int e = i >> 3;  // 8 items (32 copies x 4 bytes) per entry
+        const uint32_t w = b2_half<DT>(e & 3) | (b2_half<DT>(e >> 2) << 16);
+        lut[i] = make_uint4(w, w, w, w);
+    }
+}
+
+// B operand of the 8 codes in half-word H of dword dw: four table reads.
+template <int H>
+__device__ __forceinline__ uint4 b2_operand(uint32_t dw, const char* lut, uint32_t slot) {
+    uint32_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * H + 4 * i, 4) << 7) | slot;
+        v[i] = *reinterpret_cast<const uint32_t*>(lut + a);
+    }
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Scale (fp16 bits) of step J for group size GS from this lane's scale pieces of the round.
+template <int GS, int J>
+__device__ __forceinline__ uint32_t b2_scale(const uint4 (&sp)[4]) {
+    constexpr int t = J / 8, j = J % 8;           // piece, 8-weight unit within it
+    constexpr int idx = (j * 8) / GS;             // scale within the piece
+    constexpr int word = idx / 2, half = idx % 2;
+    const uint32_t w = word == 0 ? sp[t].x : word == 1 ? sp[t].y : word == 2 ? sp[t].z : sp[t].w;
+    return half ? (w >> 16) : (w & 0xFFFFu);
+}
+
+template <int DT, int MM, int GS>
+struct B2Round {
+    // one round of one wave: steps 0..31 with the table reads and A fragment of step J + 1
+    // issued before the MFMA of step J, the scale of a finished group applied after the
+    // next group's first MFMA has been issued
+    static constexpr int kSpg = GS / 8;  // steps per scale group
+    template <int J>
+    __device__ __forceinline__ static void step(const uint4 (&cp)[4], const uint4 (&sp)[4],
+                                                const char* lut, uint32_t slot,
+                                                const char* xa, uint4& a_cur, uint4& b_cur,
+                                                f32x4 (&d)[2], float& sf_prev,
+                                                float (&acc)[MM]) {
+        uint4 a_n, b_n;
+        if constexpr (J + 1 < 32) {
+            constexpr int t = (J + 1) / 8, hw = (J + 1) % 8;
+            a_n = *reinterpret_cast<const uint4*>(xa + 512 * t + 16 * hw);
+            const uint32_t dw = (hw / 2) == 0 ? cp[t].x : (hw / 2) == 1 ? cp[t].y
+                              : (hw / 2) == 2 ? cp[t].z : cp[t].w;
+            b_n = b2_operand<(hw % 2)>(dw, lut, slot);
+        }
+        constexpr int grp = J / kSpg, slot_d = grp & 1;
+        constexpr bool first = (J % kSpg) == 0;
+        d[slot_d] = mfma16<DT>(a_cur, b_cur, first ? f32x4{0.f, 0.f, 0.f, 0.f} : d[slot_d]);
+        if constexpr (first && J > 0) {
+            // group grp - 1 is complete in the other accumulator
+#pragma unroll
+            for (int q = 0; q < MM; ++q)
+                acc[q] = __builtin_fmaf(d[slot_d ^ 1][q], sf_prev, acc[q]);
+            keep_mfma_result(d[slot_d ^ 1], acc[0]);
+        }
+        if constexpr (first) sf_prev = scale_for<DT>(b2_scale<GS, J>(sp));
+        if constexpr (J == 31) {
+#pragma unroll
+            for (int q = 0; q < MM; ++q) acc[q] = __builtin_fmaf(d[slot_d][q], sf_prev, acc[q]);
+            keep_mfma_result(d[slot_d], acc[0]);
+        }
+        if constexpr (J + 1 < 32) {
+            a_cur = a_n;
+            b_cur = b_n;
+        }
+    }
+    template <int... J>
+    __device__ __forceinline__ static void steps(const uint4 (&cp)[4], const uint4 (&sp)[4],
+                                                 const char* lut, uint32_t slot, const char* xa,
+                                                 uint4& a, uint4& b, f32x4 (&d)[2], float& sf,
+                                                 float (&acc)[MM], std::integer_sequence<int, J...>) {
+        (step<J>(cp, sp, lut, slot, xa, a, b, d, sf, acc), ...);
+    }
+    __device__ __forceinline__ static void run(const uint4 (&cp)[4], const uint4 (&sp)[4],
+                                               const char* lut, uint32_t slot, const char* xa,
+                                               float (&acc)[MM]) {
+        uint4 a = *reinterpret_cast<const uint4*>(xa);
+        uint4 b = b2_operand<0>(cp[0].x, lut, slot);
+        f32x4 d[2];
+        float sf = 0.f;
+        steps(cp, sp, lut, slot, xa, a, b, d, sf, acc, std::make_integer_sequence<int, 32>{});
+    }
+};
+
+// Stages round u of the MM activation rows into one wave's buffer: always 2 * MM DMA
+// loads (rows m >= M re-read row M - 1 into slots no lane reads), so that every round
+// issues the same number of loads.
+template <int MM>
+__device__ __forceinline__ void b2_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int64_t u, int M,
+                                           int64_t K, int lane) {
+#pragma unroll
+    for (int q = 0; q < 2 * MM; ++q) {
+        const int m = q >> 1, half = q & 1;
+        const int msrc = m < M ? m : M - 1;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            x, lds_ptr(xs + m * kXRow + half * 1024), 16,
+            (uint32_t)(msrc * K * 2 + half * 1024 + lane * 16), uniform_offset(u * kRound * 2),
+            0, 0);
+    }
+}
+
+// Waits until the older of the two rounds in flight has landed.  A round issues 4 code
+// loads, 4 scale loads (8 for GS 16) and 2 * MM activation loads; loads complete in issue
+// order for vmcnt, so at most that many outstanding means every load of the older round
+// is done.  s_waitcnt fields: vmcnt[3:0] and [15:14], expcnt[6:4] = 7 and lgkmcnt[11:8]
+// = 15 (no wait).
+template <int GS, int MM>
+__device__ __forceinline__ void vm_wait_le_round() {
+    constexpr int n = 4 + (GS == 16 ? 8 : 4) + 2 * MM;
+    static_assert(n < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
+}
+
+// This lane's code and scale pieces of round u (t = 0..3: piece 4t + g).
+template <int GS>
+__device__ __forceinline__ void b2_load(uint4 (&cp)[4], uint4 (&sp)[4],
+                                        __amdgpu_buffer_rsrc_t pr, __amdgpu_buffer_rsrc_t sr,
+                                        uint32_t vo_code, uint32_t vo_scale, int u) {
+    const int so_c = uniform_offset((int64_t)u * 256), so_s = uniform_offset((int64_t)u * 2048 / GS);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code + 64u * t, so_c, 0);
+        cp[t] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        constexpr uint32_t kPiece = 128 / GS;  // scale bytes per code piece
+        const uint32_t o = vo_scale + 4u * kPiece * t;
+        if constexpr (kPiece == 16) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(sr, o, so_s, 0);
+            sp[t] = make_uint4(v.x, v.y, v.z, v.w);
+        } else if constexpr (kPiece == 8) {
+            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(sr, o, so_s, 0);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(sr, o + 4, so_s, 0);
+            sp[t] = make_uint4(lo, hi, 0u, 0u);
+        } else if constexpr (kPiece == 4) {
+            sp[t] = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(sr, o, so_s, 0), 0u, 0u, 0u);
+        } else {
+            sp[t] = make_uint4(__builtin_amdgcn_raw_buffer_load_b16(sr, o, so_s, 0), 0u, 0u, 0u);
+        }
+    }
+}
+
+template <int DT, int MM, int GS>
+__global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
+    const void* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
+    int M, int64_t N, int64_t K) {
+    static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
+    __shared__ uint4 lut_storage[kB2LutU4];
+    // Two activation buffers per wave, each its own LDS object ending in a zero block, so
+    // that the compiler can tell the reads of one from the DMA into the other (it waits for
+    // every outstanding load before an LDS read that may alias a pending DMA target).
+    constexpr int kXsBytes = kB2Waves * MM * (int)kXRow;
+    __shared__ __attribute__((aligned(16))) char xs0[kXsBytes + kB2ZeroBytes];
+    __shared__ __attribute__((aligned(16))) char xs1[kXsBytes + kB2ZeroBytes];
+    __shared__ float red[kB2Waves][MM][64];
+
+    fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
+    for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * kB2Waves) {
+        reinterpret_cast<uint4*>(xs0 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
+        reinterpret_cast<uint4*>(xs1 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t tile = blockIdx.x;
+    const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+    const uint32_t row = (uint32_t)(tile * 16 + i16);
+    const uint32_t vo_code = row * rowbytes + 16u * g;
+    const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
+    const uint32_t slot = (uint32_t)(lane & 31) * 4u;
+
+    // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
+    const int am = i16 & 3;
+    const bool a_live = (i16 >> 2) == g && am < M;
+    const int xoff = wave * MM * (int)kXRow;
+    char* const xw0 = xs0 + xoff;
+    char* const xw1 = xs1 + xoff;
+    const int aoff = a_live ? xoff + am * (int)kXRow + 128 * g : kXsBytes;
+    const char* xa0 = xs0 + aoff;
+    const char* xa1 = xs1 + aoff;
+
+    // wave w takes rounds w, w + W, ...: its own register sets and activation buffers, so
+    // the waves never wait for each other inside the loop
+    const int T = (int)(K / kRound);
+    float acc[MM];
+#pragma unroll
+    for (int q = 0; q < MM; ++q) acc[q] = 0.f;
+    uint4 cp[2][4], sp[2][4];
+    int u = wave;
+    if (u < T) {
+        b2_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u);
+        b2_stage_x<MM>(xw0, xr, u, M, K, lane);
+    }
+    __syncthreads();  // table and zero block ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage);
+    while (u < T) {  // uniform within the wave
+        if (u + kB2Waves < T) {
+            b2_load<GS>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
+            b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
+            vm_wait_le_round<GS, MM>();  // round u's codes, scales and activations have landed
+        } else {
+            vm_wait_all();
+        }
+        B2Round<DT, MM, GS>::run(cp[0], sp[0], lut, slot, xa0, acc);
+        u += kB2Waves;
+        if (u >= T) break;
+        lds_wait_all();  // round u - W's activation reads are done: buffer 0 may be refilled
+        if (u + kB2Waves < T) {
+            b2_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u + kB2Waves);
+            b2_stage_x<MM>(xw0, xr, u + kB2Waves, M, K, lane);
+            vm_wait_le_round<GS, MM>();
+        } else {
+            vm_wait_all();
+        }
+        B2Round<DT, MM, GS>::run(cp[1], sp[1], lut, slot, xa1, acc);
+        u += kB2Waves;
+        lds_wait_all();
+    }
+
+    // add the waves' partial sums, then the four lane groups; lane group q stores row q
+#pragma unroll
+    for (int q = 0; q < MM; ++q) red[wave][q][lane] = acc[q];
+    __syncthreads();
+    if (wave != 0) return;
+    float out = 0.f;
+#pragma unroll
+    for (int q = 0; q < MM; ++q) {
+        float v = red[0][q][lane];
+#pragma unroll
+        for (int w2 = 1; w2 < kB2Waves; ++w2) v += red[w2][q][lane];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (q == g) out = v;
+    }
+    if ((int64_t)row < N && g < M) {
+        const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
+        store_from_f32<DT>(y, (int64_t)g * N + row, out + bv);
+    }
 }
 
 // ------------------------------------------------------------------------- host side
@@ -1165,6 +1505,54 @@ hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int 
     if (wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
     return dt == kBF16 ? launch_dt<kBF16>(a, p, wgs, stream)
                        : launch_dt<kF16>(a, p, wgs, stream);
+}
+
+bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                     const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+    if (dt != kBF16 && dt != kF16) return false;
+    if (M < 1 || M > 4 || N < 1 || K < kRound || K % kRound != 0) return false;
+    if (gs != 8 && gs != 16 && gs != 32 && gs != 64) return false;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 15u) || ((uintptr_t)scales & 15u) ||
+        ((uintptr_t)y & 1u))
+        return false;
+    // 32-bit buffer offsets (codes, scales, activations, with one tile of row padding)
+    if ((N + 64) * (K / 4) >= (1ll << 31) || (N + 64) * (K * 2 / gs) >= (1ll << 31) ||
+        M * K * 2 >= (1ll << 31))
+        return false;
+    return true;
+}
+
+template <int DT, int MM, int GS>
+static hipError_t launch_gemv2_t(const void* x, const uint8_t* packed, const uint16_t* scales,
+                                 const void* bias, void* y, int M, int64_t N, int64_t K,
+                                 hipStream_t stream) {
+    const int64_t wgs = (N + 15) / 16;  // one 16-row tile per workgroup
+    hipLaunchKernelGGL((gemv2_kernel<DT, MM, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
+                       stream, x, packed, scales, bias, y, M, N, K);
+    return hipGetLastError();
+}
+
+template <int DT, int MM>
+static hipError_t launch_gemv2_gs(const void* x, const uint8_t* packed, const uint16_t* scales,
+                                  const void* bias, void* y, int M, int64_t N, int64_t K,
+                                  int64_t gs, hipStream_t stream) {
+    switch (gs) {
+        case 8: return launch_gemv2_t<DT, MM, 8>(x, packed, scales, bias, y, M, N, K, stream);
+        case 16: return launch_gemv2_t<DT, MM, 16>(x, packed, scales, bias, y, M, N, K, stream);
+        case 32: return launch_gemv2_t<DT, MM, 32>(x, packed, scales, bias, y, M, N, K, stream);
+        default: return launch_gemv2_t<DT, MM, 64>(x, packed, scales, bias, y, M, N, K, stream);
+    }
+}
+
+hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,
+                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        int dt, hipStream_t stream) {
+    const int m = (int)M;
+    if (dt == kBF16)
+        return M == 1 ? launch_gemv2_gs<kBF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream)
+                      : launch_gemv2_gs<kBF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream);
+    return M == 1 ? launch_gemv2_gs<kF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream)
+                  : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream);
 }
 
 }  // namespace ojx

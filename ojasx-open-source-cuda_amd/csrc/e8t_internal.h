@@ -18,6 +18,14 @@ hipError_t launch_encode2(const void* w, int wdt, int64_t numel, int64_t gs, uin
 hipError_t launch_decode2(const uint8_t* packed, const uint16_t* scales, int64_t numel,
                           int64_t gs, int odt, void* out, hipStream_t stream);
 
+// 2-bit decode GEMV (M <= 4, bf16/fp16, K % 1024 == 0, gs in {8, 16, 32, 64}, 16-byte
+// aligned buffers).
+bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                     const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,
+                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        int dt, hipStream_t stream);
+
 // General tiled kernels: any M, N, K >= 1 (flat layout), any dtype; fmt selects the code
 // format (0 ternary, 1 2-bit).
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,

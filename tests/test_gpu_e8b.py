@@ -208,3 +208,25 @@ def test_e8b_native_schema_ops_and_rowwise_packing():
         ops.fused_e8_gemm_fwd(x, whole[:96].to(DEV).view(12, 8), ws.to(DEV), None, 32)
     with pytest.raises(RuntimeError, match="block_scales"):
         ops.fused_e8_gemm_fwd(x, whole.to(DEV).view(12, 16), ws[:20].to(DEV), None, 32)
+
+
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (1, 4100, 3072, 8, torch.bfloat16),    # odd round count, ragged last tile
+    (2, 1000, 1024, 16, torch.float16),    # one round
+    (3, 777, 2048, 32, torch.bfloat16),
+    (4, 64, 5120, 64, torch.bfloat16),     # five rounds, one workgroup
+    (4, 4096, 14336, 8, torch.bfloat16),   # down-projection shape
+    (1, 16, 1024, 8, torch.float16),
+])
+def test_e8b_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
+    # M <= 4, K % 1024 == 0 and gs in {8, 16, 32, 64} select the 2-bit MFMA decode GEMV
+    pk, sc, pk_np, sc_np = _layer2(N, K, seed=N + K + gs, gs=gs)
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"e8b gemv M={M} N={N} K={K} gs={gs} {dtype}", flush=True)
+    y = ops.e8_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, gs)
+    torch.cuda.synchronize()
+    ref = O.e8b_gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, gs,
+                         DT_CODE[dtype])
+    assert _rel_err(y, ref) <= REL_TOL
