@@ -25,7 +25,8 @@ roofline= HBM-bound: ALGORITHMIC bytes of the grouped GEMV launches in the timed
 
 Also reported (not the headline): prefill GEMM TFLOP/s on the four shapes at
 M in {512, 2048, 8192}, encoder throughput on one layer of fp16
-weights with 0.1% +-8 sigma outliers, and the CPU baseline: this
+weights with 0.1% +-8 sigma outliers, the 2-bit E8 format (encoder, decode
+GEMV and prefill per linear on an 8-layer stack), and the CPU baseline: this
 repo's torch restatement of the reference's portable decode-then-matmul path
 (configs[0]) timed on the host cores.
 """
@@ -97,6 +98,8 @@ def parse_args():
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-layers", type=int, default=32)
     ap.add_argument("--encode-layers", type=int, default=32)
+    ap.add_argument("--e8b-layers", type=int, default=8,
+                    help="layers of the 2-bit E8 stack (0: skip that leg)")
     ap.add_argument("--decode-m", type=str, default=",".join(map(str, DECODE_M)),
                     help="decode batch sizes of the headline step (profiling runs pick one)")
     ap.add_argument("--no-per-linear", action="store_true",
@@ -387,6 +390,123 @@ def bench_encode(torch, N_, dev, layers: int, reps: int = 3, check_rows: int = 6
                 generate_s=round(gen_s, 1),
                 cpu_oracle=dict(Gweights_s=round(wq.size / cpu_s / 1e9, 3), cores=cores,
                                 sample="one 4096x4096 layer, oracle/e8t_oracle.c (OpenMP)"))
+
+
+# --------------------------------------------------------------------------- 2-bit E8
+
+E8B_GS = 32  # pack_model_e8's default group size (reference lattice.py:905)
+
+
+def e8b_weight_bytes(N: int, K: int, gs: int = E8B_GS) -> int:
+    return N * K // 4 + N * K // gs * 2
+
+
+def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m: int = 512,
+              check_rows: int = 32):
+    """2-bit E8 (E8LatticePacker, the default bitrate of E8LatticeLinear/pack_model_e8): a
+    `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights (seed 9700 + 7*layer +
+    j), group size 32.  Encoder: the stack's encode launches replayed from one hipGraph,
+    layer 0 of each shape checked bit for bit against the CPU oracle on its first
+    `check_rows` rows.  Decode: one ojx_e8_gemm_fwd launch per linear at each M, replayed
+    from a hipGraph; outputs of layer 0 checked against an fp32 matmul of the decoded
+    weights.  Prefill: the same at M = `prefill_m`."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    lib = N_.lib()
+    items = []
+    for layer in range(layers):
+        for j, (name, N, K) in enumerate(LAYER_SHAPES):
+            g = torch.Generator(device=dev).manual_seed(9700 + 7 * layer + j)
+            w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+            packed = torch.empty(N * K // 4, dtype=torch.uint8, device=dev)
+            scales = torch.empty(N * K // E8B_GS, dtype=torch.float16, device=dev)
+            items.append(dict(w=w, packed=packed, scales=scales, name=name, N=N, K=K))
+    numel = sum(it["N"] * it["K"] for it in items)
+    wbytes = sum(e8b_weight_bytes(it["N"], it["K"]) for it in items)
+    stream = torch.cuda.current_stream()
+
+    def replay_ms(launch_all, reps):
+        launch_all(stream.cuda_stream)
+        torch.cuda.synchronize()
+        cap = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            launch_all(torch.cuda.current_stream().cuda_stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def encode_all(h):
+        for it in items:
+            N_.check(lib.ojx_e8_encode(it["w"].data_ptr(), N_.F16, it["w"].numel(), E8B_GS,
+                                       it["packed"].data_ptr(), it["scales"].data_ptr(), h),
+                     "e8 encode")
+
+    enc_ms = replay_ms(encode_all, 3)
+    exact = True
+    for it in items[:7]:
+        rows, K = min(check_rows, it["N"]), it["K"]
+        ref_pk, ref_sc, _ = O.e8b_encode(it["w"][:rows].float().cpu().numpy(), E8B_GS)
+        got_pk = it["packed"][: rows * K // 4].cpu().numpy()
+        got_sc = it["scales"][: rows * K // E8B_GS].cpu().view(torch.int16).numpy().view(np.uint16)
+        exact = exact and np.array_equal(got_pk, ref_pk) and np.array_equal(got_sc, ref_sc)
+    for it in items:
+        del it["w"]
+    torch.cuda.empty_cache()
+
+    def gemm_leg(M):
+        xs = {K: torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(9800 + M + K),
+                             device=dev).to(torch.bfloat16) for K in (4096, 14336)}
+        ys = [torch.empty(M, it["N"], dtype=torch.bfloat16, device=dev) for it in items]
+
+        def launch_all(h):
+            for it, y in zip(items, ys):
+                N_.check(lib.ojx_e8_gemm_fwd(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
+                                             it["scales"].data_ptr(), None, y.data_ptr(), M,
+                                             it["N"], it["K"], E8B_GS, N_.BF16, h), "e8 gemm")
+
+        ms = replay_ms(launch_all, steps)
+        worst = 0.0
+        from ojasx_amd import ops
+        for idx in (0, 4, 6):  # q, gate, down of layer 0
+            it = items[idx]
+            wd = ops.decode2(it["packed"], it["scales"], it["N"] * it["K"], E8B_GS,
+                             torch.bfloat16).view(it["N"], it["K"]).float()
+            ref = xs[it["K"]].float() @ wd.t().contiguous()
+            err = (ys[idx].float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+            worst = max(worst, err)
+        return ms, worst
+
+    decode, worst = {}, 0.0
+    for M in Ms:
+        ms, err = gemm_leg(M)
+        worst = max(worst, err)
+        decode[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
+                              frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                              launches=len(items))
+    ms, err = gemm_leg(prefill_m)
+    worst = max(worst, err)
+    flops = 2.0 * prefill_m * numel
+    prefill = dict(M=prefill_m, ms=round(ms, 3), TFLOPs=round(flops / ms / 1e9, 1),
+                   frac_mfma=round(flops / ms / 1e9 / BF16_MFMA_PEAK_TFLOPS, 4))
+    del items
+    torch.cuda.empty_cache()
+    return dict(layers=layers, linears=7 * layers, group_size=E8B_GS, weights=numel,
+                stack_weight_bytes=wbytes,
+                encode=dict(ms=round(enc_ms, 3), Gweights_s=round(numel / enc_ms / 1e6, 1),
+                            bit_exact_sample=exact,
+                            sample=f"first {check_rows} rows of layer 0 of each shape vs "
+                                   "oracle/e8t_oracle.c"),
+                decode_per_linear=decode, prefill_per_linear=prefill, max_rel_err=worst)
 
 
 # --------------------------------------------------------------------------- end-to-end decoder
@@ -807,6 +927,12 @@ def main() -> int:
         result["encode"] = bench_encode(torch, N_, dev, args.encode_layers)
         log(f"encode: {result['encode']['Gweights_s']} Gweights/s, "
             f"bit-exact sample {result['encode']['bit_exact_sample']}")
+    if args.e8b_layers > 0:
+        torch.cuda.empty_cache()
+        log(f"2-bit E8 ({args.e8b_layers}-layer stack)")
+        result["e8_2bit"] = bench_e8b(torch, N_, dev, args.e8b_layers, args.steps)
+        log(f"2-bit: decode M=1 {result['e8_2bit']['decode_per_linear']['1']['weight_GBs']} GB/s, "
+            f"encode {result['e8_2bit']['encode']['Gweights_s']} Gweights/s")
     if not args.no_e2e:
         torch.cuda.empty_cache()
         log(f"end-to-end decoder ({args.e2e_layers} layers)")

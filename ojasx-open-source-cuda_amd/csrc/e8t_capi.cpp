@@ -124,6 +124,21 @@ __attribute__((visibility("default"))) int ojx_e8t_decode(const uint8_t* packed,
                 "e8t decode launch");
 }
 
+// The prefill MFMA GEMM with its tile configuration and K split; the split's fp32 partial
+// sums live in the per-stream workspace (none while the stream is captured: unsplit).
+static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
+                              const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                              int64_t gs, int dtype, hipStream_t s, int fmt) {
+    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, N, K);
+    float* part = nullptr;
+    if (c.splits > 1) {
+        part = static_cast<float*>(ojx::stream_workspace(
+            s, (size_t)c.splits * (size_t)ojx::split_stride(M, N) * sizeof(float)));
+        if (!part) c.splits = 1;  // capturing, or no memory: the unsplit kernel
+    }
+    return ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s, gs, fmt);
+}
+
 __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed,
                                                             const uint16_t* scales,
                                                             const void* bias, void* y, int64_t M,
@@ -144,17 +159,10 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
         return done(ojx::launch_gemv(a, plan, ojx::gemv_wgs_for(N, plan), dtype, s),
                     "e8t gemv launch");
     }
-    if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype)) {
-        ojx::GemmChoice c = ojx::gemm_mfma_choice(M, N, K);
-        float* part = nullptr;
-        if (c.splits > 1) {
-            part = static_cast<float*>(ojx::stream_workspace(
-                s, (size_t)c.splits * (size_t)ojx::split_stride(M, N) * sizeof(float)));
-            if (!part) c.splits = 1;  // capturing, or no memory: the unsplit kernel
-        }
-        return done(ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s),
+    if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype))
+        return done(launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
+                                ojx::kFmtTernary),
                     "e8t gemm_mfma launch");
-    }
     return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                 "e8t gemm_fwd launch");
 }
@@ -318,12 +326,15 @@ __attribute__((visibility("default"))) int ojx_e8_gemm_fwd(const void* x, const 
     if (int r = check_gemm2_args(x, packed, scales, y, M, N, K, gs, dtype)) return r;
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
+    hipStream_t s = (hipStream_t)stream;
     if (ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
-        return done(ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype,
-                                      (hipStream_t)stream),
+        return done(ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                     "e8 gemv launch");
-    return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype,
-                                             (hipStream_t)stream, ojx::kFmt2Bit),
+    if (ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, ojx::kFmt2Bit))
+        return done(launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmt2Bit),
+                    "e8 gemm_mfma launch");
+    return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
+                                             ojx::kFmt2Bit),
                 "e8 gemm_fwd launch");
 }
 

@@ -22,6 +22,8 @@
 // tile index is remapped so that each XCD walks a contiguous, M-grouped range of tiles
 // and its L2 serves the X rows and weight columns that its concurrent workgroups share.
 
+#include <type_traits>
+
 #include "e8t_device.h"
 #include "e8t_internal.h"
 #include "e8t_lut.h"
@@ -88,37 +90,6 @@ __device__ __forceinline__ void load_codes_row(RowCodes& rc, __amdgpu_buffer_rsr
     rc.s = __builtin_amdgcn_raw_buffer_load_b32(scales, vo_scale, uniform_offset(k0 / 16), 0);
 }
 
-template <int J>
-__device__ __forceinline__ void decode_piece(const RowCodes& rc, const char* lut, uint32_t slot,
-                                             uint32_t sw, char* tile, uint32_t row) {
-    const uint32_t z = code_z<J>(rc.d, slot);
-    const uint32_t h = __umulhi(z, kHiMagic);
-    const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
-    const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
-    *reinterpret_cast<uint4*>(tile + swz(row, J)) =
-        make_uint4(ml.x & sw, ml.y & sw, mh.x & sw, mh.y & sw);
-}
-
-// Expands codes 4h .. 4h+3 of this thread's weight row (32 weights; h = half) into the
-// LDS tile.
-template <int DT>
-__device__ __forceinline__ void decode_half(const RowCodes& rc, const char* lut, uint32_t slot,
-                                            char* tile, uint32_t row, int half) {
-    uint32_t w0, w1;
-    scale_words<DT>(rc.s, w0, w1);
-    if (half == 0) {
-        decode_piece<0>(rc, lut, slot, w0, tile, row);
-        decode_piece<1>(rc, lut, slot, w0, tile, row);
-        decode_piece<2>(rc, lut, slot, w0, tile, row);
-        decode_piece<3>(rc, lut, slot, w0, tile, row);
-    } else {
-        decode_piece<4>(rc, lut, slot, w1, tile, row);
-        decode_piece<5>(rc, lut, slot, w1, tile, row);
-        decode_piece<6>(rc, lut, slot, w1, tile, row);
-        decode_piece<7>(rc, lut, slot, w1, tile, row);
-    }
-}
-
 template <int DT, int TN>
 __device__ __forceinline__ void mma_row(const uint4& a, const uint4 (&b)[TN], f32x4 (&acc)[TN]) {
 #pragma unroll
@@ -181,21 +152,139 @@ __device__ __forceinline__ void lut_reads_half(const RowCodes& rc, const char* l
     }
 }
 
+// ---- weight-row decoders: each thread owns half of one weight row of the tile (32 k of a
+// 64-k step) and produces its four 16-byte pieces of activation-dtype weights.
+//   load(k0)  issue the loads of the codes/scales of K step k0 (two steps ahead);
+//   prep()    table reads and scale words for the codes loaded earlier (one step ahead);
+//   piece(p)  the p-th 16-byte piece (8 weights) from what prep() read.
+
+// Ternary E8: 8 codes (12 bytes) of the whole row per step; the thread expands 4 of them.
+template <int DT>
+struct TernaryRowDecoder {
+    RowCodes rc;
+    uint2 ml[4], mh[4];
+    uint32_t sw;
+    const char* lut;
+    uint32_t slot, vo_code, vo_scale;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    int half;
+    __device__ __forceinline__ void load(int64_t k0) {
+        load_codes_row(rc, pr, sr, vo_code, vo_scale, k0);
+    }
+    __device__ __forceinline__ void prep() {
+        lut_reads_half(rc, lut, slot, half, ml, mh);
+        uint32_t w0, w1;
+        scale_words<DT>(rc.s, w0, w1);
+        sw = half ? w1 : w0;
+    }
+    __device__ __forceinline__ uint4 piece(int p) const {
+        return make_uint4(ml[p].x & sw, ml[p].y & sw, mh[p].x & sw, mh[p].y & sw);
+    }
+};
+
+// 2-bit E8 (E8LatticePacker, lattice.py:252-279): code c in {0..3} is the weight
+// (c - 1.5) * s, rounded once to the activation dtype (s = scales.to(dtype)).  Per scale
+// group the four possible weights are -B, -A, +A, +B with A = rnd(0.5 s), B = rnd(1.5 s)
+// (the products are exact in fp32; -rnd(x) = rnd(-x)); they form the 8-byte table
+// {S0 = A | B << 16, S1 = -B | -A << 16} whose byte pair 2c, 2c + 1 is the weight of code
+// c.  One v_perm_b32 then yields two weights from a selector word; the selector words of a
+// code byte (4 codes) come from a 256-entry LDS table (2 KB, `kSel2Entries`).
+constexpr int kSel2Entries = 256;
+
+__device__ __forceinline__ void fill_sel2(uint2* tab, int nthreads) {
+    for (int e = (int)threadIdx.x; e < kSel2Entries; e += nthreads) {
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t c0 = ((uint32_t)e >> (4 * h)) & 3u, c1 = ((uint32_t)e >> (4 * h + 2)) & 3u;
+            w[h] = (2u * c0) | ((2u * c0 + 1u) << 8) | ((2u * c1) << 16) | ((2u * c1 + 1u) << 24);
+        }
+        tab[e] = make_uint2(w[0], w[1]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t rnd_bits(float v) {
+    keep_f32(v);
+    if constexpr (DT == kF16) return f32_to_f16_bits(v);
+    else return f32_to_bf16_bits(v);
+}
+
+// Value words {S0, S1} of one scale group (fp16 bits s16).
+template <int DT>
+__device__ __forceinline__ uint2 values2(uint32_t s16) {
+    const float s = scale_for<DT>(s16 & 0xFFFFu);
+    const uint32_t a = rnd_bits<DT>(0.5f * s), b = rnd_bits<DT>(1.5f * s);
+    return make_uint2(a | (b << 16), (b ^ 0x8000u) | ((a ^ 0x8000u) << 16));
+}
+
+template <int DT, int GS>
+struct Bit2RowDecoder {
+    static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "2-bit group size 8..64");
+    uint2 c;          // the half-row's 32 codes (8 bytes)
+    uint2 sc;         // its scales: GS 8: four, GS 16: two, GS 32/64: one (fp16 bits)
+    uint2 sel[4][2];  // selector words of pieces 0..3
+    uint2 val[4];     // value words of pieces 0..3
+    const char* tab;
+    uint32_t vo_code, vo_scale;  // this thread's half-row (codes) and scale bytes
+    __amdgpu_buffer_rsrc_t pr, sr;
+    __device__ __forceinline__ void load(int64_t k0) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(pr, vo_code, uniform_offset(k0 / 4), 0);
+        c = make_uint2(v[0], v[1]);
+        const int so = uniform_offset(k0 * 2 / GS);
+        if constexpr (GS == 8) {
+            const auto u = __builtin_amdgcn_raw_buffer_load_b64(sr, vo_scale, so, 0);
+            sc = make_uint2(u[0], u[1]);
+        } else if constexpr (GS == 16) {
+            sc = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(sr, vo_scale, so, 0), 0u);
+        } else {
+            sc = make_uint2(__builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale, so, 0), 0u);
+        }
+    }
+    __device__ __forceinline__ void prep() {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t w = p < 2 ? c.x : c.y;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t byte = (w >> (16 * (p & 1) + 8 * h)) & 0xFFu;
+                sel[p][h] = *reinterpret_cast<const uint2*>(tab + 8u * byte);
+            }
+        }
+        if constexpr (GS == 8) {
+            val[0] = values2<DT>(sc.x);
+            val[1] = values2<DT>(sc.x >> 16);
+            val[2] = values2<DT>(sc.y);
+            val[3] = values2<DT>(sc.y >> 16);
+        } else if constexpr (GS == 16) {
+            val[0] = val[1] = values2<DT>(sc.x);
+            val[2] = val[3] = values2<DT>(sc.x >> 16);
+        } else {
+            val[0] = val[1] = val[2] = val[3] = values2<DT>(sc.x);
+        }
+    }
+    __device__ __forceinline__ uint4 piece(int p) const {
+        const uint32_t s0 = val[p].x, s1 = val[p].y;
+        return make_uint4(__builtin_amdgcn_perm(s0, s1, sel[p][0].x),
+                          __builtin_amdgcn_perm(s0, s1, sel[p][0].y),
+                          __builtin_amdgcn_perm(s0, s1, sel[p][1].x),
+                          __builtin_amdgcn_perm(s0, s1, sel[p][1].y));
+    }
+};
+
 // One K step (64) of the wave's block.
 //   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read,
 //      then the next step's X tile load is issued (issue_x);
-//   2. table reads for this thread's 4 codes of the NEXT step's weight row (their codes
-//      arrived a full step ago), then `rc` is re-armed with the codes of the step after;
-//   3. sub-step 1; in its last four MFMA rows the masked weight pairs of the next step are
-//      written to the other LDS buffer.
-template <int DT, int TM, int TN, typename IssueX>
+//   2. the decoder's table reads for this thread's half row of the NEXT step's weights
+//      (their codes arrived a full step ago), then its codes are re-armed with those of the
+//      step after;
+//   3. sub-step 1; in its last four MFMA rows the next step's weight pieces are written to
+//      the other LDS buffer.
+template <int DT, int TM, int TN, typename Dec, typename IssueX>
 __device__ __forceinline__ void kstep(const char* xt, const char* wt, const FragLane& fl,
                                       uint4 (&a0)[TM], uint4 (&b0)[TN], uint4 (&a1)[TM],
-                                      uint4 (&b1)[TN], RowCodes& rc, const char* lut,
-                                      uint32_t slot, char* wt_next, uint32_t wrow, int half,
-                                      f32x4 (&acc)[TM][TN], __amdgpu_buffer_rsrc_t pr,
-                                      __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
-                                      uint32_t vo_scale, int64_t k_reload,
+                                      uint4 (&b1)[TN], Dec& dec, char* wt_next, uint32_t wrow,
+                                      int half, f32x4 (&acc)[TM][TN], int64_t k_reload,
                                       const IssueX& issue_x) {
     const char* pa1 = xt + fl.a[1];
     const char* pb1 = wt + fl.b[1];
@@ -209,19 +298,14 @@ __device__ __forceinline__ void kstep(const char* xt, const char* wt, const Frag
     // every read of this step's X tile is issued: the next X tile may now be loaded into
     // the other buffer without the compiler holding a later read of this one behind it
     issue_x();
-    uint2 ml[4], mh[4];
-    lut_reads_half(rc, lut, slot, half, ml, mh);
-    uint32_t w0, w1;
-    scale_words<DT>(rc.s, w0, w1);
-    const uint32_t sw = half ? w1 : w0;
-    load_codes_row(rc, pr, sr, vo_code, vo_scale, k_reload);
+    dec.prep();
+    dec.load(k_reload);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         mma_row<DT, TN>(a1[i], b1, acc[i]);
         if (i >= TM - 4) {  // the table reads were issued TM - 4 MFMA rows earlier
             const int p = i - (TM - 4);
-            *reinterpret_cast<uint4*>(wt_next + swz(wrow, 4u * half + p)) = make_uint4(
-                ml[p].x & sw, ml[p].y & sw, mh[p].x & sw, mh[p].y & sw);
+            *reinterpret_cast<uint4*>(wt_next + swz(wrow, 4u * half + p)) = dec.piece(p);
         }
     }
 }
@@ -230,17 +314,20 @@ __device__ __forceinline__ void vm_wait_le2() {
     __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): all but the two newest loads (gfx9)
 }
 
-template <int DT, typename C>
+// FMT: kFmtTernary (group size 32) or kFmt2Bit (group size GS2).
+template <int DT, typename C, int FMT, int GS2>
 __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     float* __restrict__ part, int splits, int64_t M, int64_t N, int64_t K) {
-    __shared__ uint4 lut_storage[kLutStorageU4];
+    constexpr bool kTernary = FMT == kFmtTernary;
+    __shared__ uint4 lut_storage[kTernary ? kLutStorageU4 : kSel2Entries / 2];
     __shared__ __attribute__((aligned(16))) char xs[2][C::XTILE];
     __shared__ __attribute__((aligned(16))) char ws[2][C::WTILE];
     constexpr int kTM = C::TM, kTN = C::TN;
 
-    fill_lut<C::THREADS>(lut_storage, kLutMasks);
+    if constexpr (kTernary) fill_lut<C::THREADS>(lut_storage, kLutMasks);
+    else fill_sel2(reinterpret_cast<uint2*>(lut_storage), C::THREADS);
 
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
     const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (N + C::BN - 1) / C::BN;
@@ -272,16 +359,33 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
-    const uint32_t rowbytes = (uint32_t)(K * 3 / 16), srowbytes = (uint32_t)(K / 16);
+    const uint32_t rowbytes = kTernary ? (uint32_t)(K * 3 / 16) : (uint32_t)(K / 4);
+    const uint32_t srowbytes = kTernary ? (uint32_t)(K / 16) : (uint32_t)(K * 2 / GS2);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
     const uint32_t wrow = (uint32_t)tid >> 1;  // this thread's weight row in the tile
-    const int half = tid & 1;                   // ... and which 4 of its 8 codes
+    const int half = tid & 1;                   // ... and which half of its K step
     const uint32_t vo_code = (uint32_t)(n0 + wrow) * rowbytes;
     const uint32_t vo_scale = (uint32_t)(n0 + wrow) * srowbytes;
-    const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + (kTernary ? kLutBaseOffset : 0);
+    using Dec = std::conditional_t<kTernary, TernaryRowDecoder<DT>, Bit2RowDecoder<DT, GS2>>;
+    Dec dec;
+    dec.pr = pr;
+    dec.sr = sr;
+    if constexpr (kTernary) {
+        dec.lut = lut;
+        dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+        dec.vo_code = vo_code;
+        dec.vo_scale = vo_scale;
+        dec.half = half;
+    } else {
+        dec.tab = lut;
+        dec.vo_code = vo_code + 8u * (uint32_t)half;
+        // scale bytes of the half row: GS 8: 4 scales, 16: 2, 32: 1; GS 64: the step's one
+        dec.vo_scale = vo_scale + (GS2 < 64 ? (uint32_t)half * (64u / GS2) : 0u);
+    }
 
     f32x4 acc[kTM][kTN];
 #pragma unroll
@@ -295,13 +399,14 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     // Codes run one K step ahead of the weight tile being decoded, which runs one step
     // ahead of the MFMAs.  Branch-free body: loads past the last step fetch bytes past the
     // operands (zeros, or the next row's data) into buffers that are never read.
-    RowCodes rc;
     load_x_tile(xs[0], xr, m0, k_begin, K, wave, lane, C::XLOADS);
-    load_codes_row(rc, pr, sr, vo_code, vo_scale, k_begin);
+    dec.load(k_begin);
     __syncthreads();  // table ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
-    decode_half<DT>(rc, lut, slot, ws[0], wrow, half);
-    load_codes_row(rc, pr, sr, vo_code, vo_scale, k_begin + kBK);
+    dec.prep();
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+        *reinterpret_cast<uint4*>(ws[0] + swz(wrow, 4u * half + p)) = dec.piece(p);
+    dec.load(k_begin + kBK);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
 
@@ -312,8 +417,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         const int cur = (int)((s - s_begin) & 1), nxt = cur ^ 1;
         char* xn = xs[nxt];
         const int64_t kx = (s + 1) * kBK;
-        kstep<DT, kTM, kTN>(xs[cur], ws[cur], fl, a0, b0, a1, b1, rc, lut, slot, ws[nxt], wrow,
-                            half, acc, pr, sr, vo_code, vo_scale, (s + 2) * kBK,
+        kstep<DT, kTM, kTN>(xs[cur], ws[cur], fl, a0, b0, a1, b1, dec, ws[nxt], wrow, half,
+                            acc, (s + 2) * kBK,
                             [&] { load_x_tile(xn, xr, m0, kx, K, wave, lane, C::XLOADS); });
         vm_wait_le2();  // the X tile of step s+1 has landed; the code loads may still fly
         __syncthreads();
@@ -388,15 +493,19 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
 }
 
 bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt) {
     if (dt != kBF16 && dt != kF16) return false;
-    if (gs != 32 || M < 1 || N < 1 || K < kBK || K % kBK != 0) return false;
-    if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 3u) || ((uintptr_t)scales & 3u))
+    if (M < 1 || N < 1 || K < kBK || K % kBK != 0) return false;
+    if (fmt == kFmtTernary ? gs != 32 : (gs != 8 && gs != 16 && gs != 32 && gs != 64))
+        return false;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 7u) || ((uintptr_t)scales & 7u))
         return false;
     // 32-bit buffer offsets: the activation matrix and the weight buffers (plus one tile
     // of padding rows) must stay below 2^31 bytes
-    if ((M + CfgLarge::BM) * K * 2 >= (1ll << 31) ||
-        (N + CfgLarge::BN) * (K * 3 / 16) >= (1ll << 31))
+    const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : K / 4;
+    const int64_t srowbytes = fmt == kFmtTernary ? K / 16 : K * 2 / gs;
+    if ((M + CfgLarge::BM) * K * 2 >= (1ll << 31) || (N + CfgLarge::BN) * rowbytes >= (1ll << 31) ||
+        (N + CfgLarge::BN) * srowbytes >= (1ll << 31))
         return false;
     return true;
 }
@@ -407,13 +516,13 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
 #define OJX_GEMM_SMALL_BELOW 192
 #endif
 
-template <int DT, typename C>
+template <int DT, typename C, int FMT, int GS2>
 static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_t* scales,
                              const void* bias, void* y, float* part, int splits, int64_t M,
                              int64_t N, int64_t K, hipStream_t stream) {
     const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
     if (tiles * splits > 0x7FFFFFFF) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C>), dim3((unsigned)(tiles * splits)),
+    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C, FMT, GS2>), dim3((unsigned)(tiles * splits)),
                        dim3(C::THREADS), 0, stream, x, packed, scales, bias, y, part, splits, M,
                        N, K);
     if (splits == 1) return hipGetLastError();
@@ -462,19 +571,45 @@ GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K) {
                       (int)splits_for(tiles, OJX_SPLIT_TARGET_WGS, kMinSplitSteps, M, N, K)};
 }
 
+template <int DT, typename C>
+static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_t* scales,
+                             const void* bias, void* y, float* part, int splits, int64_t M,
+                             int64_t N, int64_t K, int64_t gs, int fmt, hipStream_t stream) {
+    if (fmt == kFmtTernary)
+        return launch_cfg<DT, C, kFmtTernary, 32>(x, packed, scales, bias, y, part, splits, M, N,
+                                                  K, stream);
+    switch (gs) {
+    case 8:
+        return launch_cfg<DT, C, kFmt2Bit, 8>(x, packed, scales, bias, y, part, splits, M, N, K,
+                                              stream);
+    case 16:
+        return launch_cfg<DT, C, kFmt2Bit, 16>(x, packed, scales, bias, y, part, splits, M, N, K,
+                                               stream);
+    case 32:
+        return launch_cfg<DT, C, kFmt2Bit, 32>(x, packed, scales, bias, y, part, splits, M, N, K,
+                                               stream);
+    case 64:
+        return launch_cfg<DT, C, kFmt2Bit, 64>(x, packed, scales, bias, y, part, splits, M, N, K,
+                                               stream);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, float* part, GemmChoice c, int64_t M,
-                            int64_t N, int64_t K, int dt, hipStream_t stream) {
+                            int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs,
+                            int fmt) {
     if (c.splits < 1 || (c.splits > 1 && !part)) return hipErrorInvalidValue;
     if (dt == kBF16)
-        return c.small ? launch_cfg<kBF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits,
-                                                     M, N, K, stream)
-                       : launch_cfg<kBF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits,
-                                                     M, N, K, stream);
-    return c.small ? launch_cfg<kF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits, M, N,
-                                                K, stream)
-                   : launch_cfg<kF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits, M, N,
-                                                K, stream);
+        return c.small ? launch_fmt<kBF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits,
+                                                     M, N, K, gs, fmt, stream)
+                       : launch_fmt<kBF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits,
+                                                     M, N, K, gs, fmt, stream);
+    return c.small ? launch_fmt<kF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits, M, N,
+                                                K, gs, fmt, stream)
+                   : launch_fmt<kF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits, M, N,
+                                                K, gs, fmt, stream);
 }
 
 }  // namespace ojx

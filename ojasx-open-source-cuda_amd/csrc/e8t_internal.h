@@ -85,9 +85,10 @@ int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream);
 
-// Prefill MFMA GEMM (M > 16): F16/BF16, K % 64 == 0, group size 32.
+// Prefill MFMA GEMM: F16/BF16, K % 64 == 0; fmt 0 (ternary, group size 32) or 1 (2-bit,
+// group size 8, 16, 32 or 64).
 bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt = 0);
 // Tile configuration and K splits of the prefill GEMM for a shape (splits 1 = none).  With
 // splits > 1 the launch needs `part`, fp32 scratch of splits * split_stride(M, N) floats.
 struct GemmChoice {
@@ -100,7 +101,8 @@ __host__ __device__ inline int64_t split_stride(int64_t M, int64_t N) {
 }
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, float* part, GemmChoice c, int64_t M,
-                            int64_t N, int64_t K, int dt, hipStream_t stream);
+                            int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs = 32,
+                            int fmt = 0);
 
 // Scratch device memory owned by the library, one buffer per (device, stream), grown on
 // demand and kept until the process ends.  Returns nullptr (and allocates nothing) while

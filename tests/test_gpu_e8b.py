@@ -230,3 +230,55 @@ def test_e8b_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
     ref = O.e8b_gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, gs,
                          DT_CODE[dtype])
     assert _rel_err(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (17, 256, 512, 8, torch.bfloat16),
+    (100, 1000, 256, 16, torch.float16),
+    (256, 256, 1024, 32, torch.bfloat16),
+    (300, 520, 512, 64, torch.float16),
+    (513, 96, 128, 8, torch.bfloat16),
+    (64, 4096, 64, 32, torch.bfloat16),
+    (40, 1024, 4096, 8, torch.bfloat16),   # small grid: K split over 16 steps per split
+    (201, 301, 1344, 16, torch.float16),   # 21 K steps over uneven splits, ragged M and N
+    (8, 2048, 2048, 64, torch.float16),    # decode-sized batch on the MFMA kernel
+])
+def test_e8b_prefill_mfma_matches_oracle(M, N, K, gs, dtype):
+    # K % 64 == 0, gs in {8, 16, 32, 64} and M > 4 (or K % 1024 != 0) select the MFMA GEMM
+    # with the 2-bit weight decoder
+    pk, sc, pk_np, sc_np = _layer2(N, K, seed=M + N + K + gs, gs=gs)
+    g = torch.Generator().manual_seed(M * 3 + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"e8b prefill M={M} N={N} K={K} gs={gs} {dtype}", flush=True)
+    y = ops.e8_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, gs)
+    torch.cuda.synchronize()
+    ref = O.e8b_gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, gs,
+                         DT_CODE[dtype])
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel_err(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("gs", [8, 32])
+@pytest.mark.parametrize("M,name,N,K", [(512, "gate_up", 14336, 4096), (2048, "down", 4096, 14336),
+                                        (512, "q_o", 4096, 4096)])
+def test_e8b_prefill_llama8b_shapes(M, name, N, K, gs):
+    # every element against an fp32 matmul of the decoded weights (the decoder is pinned
+    # bit-exact above), plus a row sample against the fp64 oracle
+    gw = torch.Generator(device=DEV).manual_seed(9100 + N + gs)
+    w = torch.randn(N, K, generator=gw, device=DEV) * 0.02
+    pk, sc = ops.encode2(w, gs)
+    del w
+    x = torch.randn(M, K, generator=gw, device=DEV).to(torch.bfloat16)
+    print(f"e8b prefill {name} M={M} gs={gs}", flush=True)
+    y = ops.e8_linear(x, pk, sc, None, N, K, gs)
+    wdq = ops.decode2(pk, sc, N * K, gs, torch.bfloat16).view(N, K).float()
+    ref = x.float() @ wdq.t().contiguous()
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    err = ((y.float() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= REL_TOL
+    rows = [0, 1, 255, 256, M - 1]
+    ref64 = O.e8b_gemm_f64(x[rows].float().cpu().numpy(), pk.cpu().numpy(), _u16(sc), None, N, K,
+                           gs, O.DT_BF16)
+    assert _rel_err(y[rows], ref64) <= REL_TOL
