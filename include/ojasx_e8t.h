@@ -125,6 +125,36 @@ int ojx_e8_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_t
                        void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
                        void* stream);
 
+/* ---------------------------------------------------------------- 1-bit Root E8
+ *
+ * RootE8LatticePacker (1.0 bit/weight, ojasx2/math/lattice.py:426-533): one code byte per
+ * flat 8-vector (an index into the reference's 256-entry table, :436-456), one fp16 scale
+ * per flat group of gs weights; weight = table[code][k] * scale.
+ *   codes  uint8 [padded / 8];  scales uint16 [padded / gs];  padded as above. */
+
+/* Encoder, bit-exact with RootE8LatticePacker.pack (lattice.py:473-509): codes by the
+ * argmax of v . u/|u| over the table rows (torch's CPU matmul order, first maximum), MMSE
+ * scales sum(w q) / sum(q q) in torch's CPU sum order.  gs a positive multiple of 8 (the
+ * packer coerces other values to 8, :485-486; that coercion is the caller's). */
+int ojx_e8r_encode(const void* w, int w_dtype, int64_t numel, int64_t gs, uint8_t* codes,
+                   uint16_t* scales, void* stream);
+
+/* Decoder, bit-exact with RootE8LatticePacker.unpack (lattice.py:519-533): out[i] =
+ * table[code][i % 8] * scales.to(dtype), rounded to dtype.  gs a positive multiple of 8. */
+int ojx_e8r_decode(const uint8_t* codes, const uint16_t* scales, int64_t numel, int64_t gs,
+                   int out_dtype, void* out, void* stream);
+
+/* Fused forward and backward dX over 1-bit weights with the decoder's weight rule and
+ * fp32 accumulation.  Replace the 1-bit portable path of _FusedE8GEMMFunction (unpack +
+ * F.linear, lattice.py:610-640; backward :684-717).  gs a positive multiple of 8.  Any
+ * M, N, K (flat layout). */
+int ojx_e8r_gemm_fwd(const void* x, const uint8_t* codes, const uint16_t* scales,
+                     const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                     int dtype, void* stream);
+int ojx_e8r_gemm_bwd_dx(const void* grad_y, const uint8_t* codes, const uint16_t* scales,
+                        void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
+                        void* stream);
+
 /* ---------------------------------------------------------------- grouped decode GEMV
  *
  * One launch runs the decode GEMV (batch M <= 16) of several independent linears: a

@@ -352,4 +352,79 @@ __attribute__((visibility("default"))) int ojx_e8_gemm_bwd_dx(const void* grad_y
                 "e8 gemm_bwd_dx launch");
 }
 
+// ---------------------------------------------------------------- 1-bit Root E8
+
+__attribute__((visibility("default"))) int ojx_e8r_encode(const void* w, int w_dtype,
+                                                          int64_t numel, int64_t gs,
+                                                          uint8_t* codes, uint16_t* scales,
+                                                          void* stream) {
+    if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);
+    if (!valid_dtype(w_dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", w_dtype);
+    if (int r = check_gs_multiple(gs, 8)) return r;
+    if (numel == 0) return OJX_OK;
+    if (!w || !codes || !scales) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_encode1(w, w_dtype, numel, gs, codes, scales, (hipStream_t)stream),
+                "e8r encode launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_decode(const uint8_t* codes,
+                                                          const uint16_t* scales, int64_t numel,
+                                                          int64_t gs, int out_dtype, void* out,
+                                                          void* stream) {
+    if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);
+    if (!valid_dtype(out_dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", out_dtype);
+    if (int r = check_gs_multiple(gs, 8)) return r;
+    if (numel == 0) return OJX_OK;
+    if (!codes || !scales || !out) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_decode1(codes, scales, numel, gs, out_dtype, out, (hipStream_t)stream),
+                "e8r decode launch");
+}
+
+static int check_gemm1_args(const void* a, const uint8_t* codes, const uint16_t* scales,
+                            const void* out, int64_t M, int64_t N, int64_t K, int64_t gs,
+                            int dtype) {
+    if (M < 0 || N < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld N=%lld K=%lld",
+                                             (long long)M, (long long)N, (long long)K);
+    if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
+    if (int r = check_gs_multiple(gs, 8)) return r;
+    if (M > 0 && N > 0) {
+        if (!out) return fail(OJX_EINVAL, "null output pointer");
+        if (K > 0 && (!a || !codes || !scales)) return fail(OJX_EINVAL, "null input pointer");
+    }
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemm_fwd(const void* x, const uint8_t* codes,
+                                                            const uint16_t* scales,
+                                                            const void* bias, void* y, int64_t M,
+                                                            int64_t N, int64_t K, int64_t gs,
+                                                            int dtype, void* stream) {
+    if (int r = check_gemm1_args(x, codes, scales, y, M, N, K, gs, dtype)) return r;
+    if (M == 0 || N == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    hipStream_t s = (hipStream_t)stream;
+    if (ojx::gemm_mfma_supported(x, codes, scales, M, N, K, gs, dtype, ojx::kFmtRoot))
+        return done(launch_mfma(x, codes, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmtRoot),
+                    "e8r gemm_mfma launch");
+    return done(ojx::launch_gemm_generic_fwd(x, codes, scales, bias, y, M, N, K, gs, dtype, s,
+                                             ojx::kFmtRoot),
+                "e8r gemm_fwd launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemm_bwd_dx(const void* grad_y,
+                                                               const uint8_t* codes,
+                                                               const uint16_t* scales,
+                                                               void* grad_x, int64_t M, int64_t N,
+                                                               int64_t K, int64_t gs, int dtype,
+                                                               void* stream) {
+    if (int r = check_gemm1_args(grad_y, codes, scales, grad_x, M, K, N, gs, dtype)) return r;
+    if (M == 0 || K == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    return done(ojx::launch_gemm_generic_bwd(grad_y, codes, scales, grad_x, M, N, K, gs, dtype,
+                                             (hipStream_t)stream, ojx::kFmtRoot),
+                "e8r gemm_bwd_dx launch");
+}
+
 }  // extern "C"

@@ -19,6 +19,7 @@
 
 #include "e8t_device.h"
 #include "e8t_internal.h"
+#include "e8t_root.h"
 
 namespace ojx {
 
@@ -580,6 +581,263 @@ hipError_t launch_decode2(const uint8_t* packed, const uint16_t* scales, int64_t
         default:
             hipLaunchKernelGGL((decode2_kernel<kBF16>), dim3((unsigned)blocks), dim3(kDecThreads),
                                0, stream, packed, scales, numel, padded, gs, vec_ok, out);
+            break;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- 1-bit Root-E8 encoder
+//
+// RootE8LatticePacker.pack (lattice.py:473-509), per flat group of gs weights:
+//   s = torch.norm(w)/sqrt(gs) + 1e-8 (the CPU norm order, as the other packers);
+//   v = w / s; code = argmax over the 256 table rows u of v . u/|u| (first maximal index);
+//   scale = sum(w * q) / max(sum(q * q), 1e-8) for q = table[code], stored as fp16.
+// The code search is root_code (e8t_root.h).  Both sums run in torch's CPU order for a
+// contiguous last dim: four
+// 8-lane accumulators over the 8-blocks of each 32-block, later 8-blocks into the first
+// accumulator, accumulators added in order, then the 8 lanes left to right.
+
+// torch's CPU row-sum order (see above), fed one 8-block at a time.
+struct TorchRowSum {
+    float acc[4][8];
+    int block;
+    int main_blocks;  // 8-blocks inside whole 32-blocks
+    __device__ __forceinline__ void init(int64_t n) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[a][j] = 0.f;
+        block = 0;
+        main_blocks = (int)((n / 8) / 4 * 4);
+    }
+    __device__ __forceinline__ void add8(const float (&x)[8]) {
+#pragma clang fp contract(off)
+        const int a = block < main_blocks ? (block & 3) : 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (q == a)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[q][j] = acc[q][j] + x[j];
+        ++block;
+    }
+    __device__ __forceinline__ float result() const {
+#pragma clang fp contract(off)
+        float lane[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lane[j] = ((acc[0][j] + acc[1][j]) + acc[2][j]) + acc[3][j];
+        float s = lane[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) s = s + lane[j];
+        return s;
+    }
+};
+
+// Codes of one group whose weights are read 8 at a time by `get(t, x)`; accumulates the
+// MMSE sums; returns the fp16 scale bits.
+template <typename Get>
+__device__ __forceinline__ uint32_t root_group(const Get& get, int64_t gs, float s,
+                                               uint8_t* codes_out) {
+#pragma clang fp contract(off)
+    const GroupRecip gr = group_recip(s);
+    TorchRowSum num, den;
+    num.init(gs);
+    den.init(gs);
+    for (int64_t t = 0; t < gs / 8; ++t) {
+        float x[8], v[8];
+        get(t, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = gr.exact ? x[i] / s : div_rn(x[i], gr);
+        const uint32_t c = root_code(v);
+        codes_out[t] = (uint8_t)c;
+        float wq[8], qq[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float q = (float)kRootTable.c[c][i];
+            wq[i] = x[i] * q;
+            qq[i] = q * q;
+        }
+        num.add8(wq);
+        den.add8(qq);
+    }
+    float d = den.result();
+    d = d < 1e-8f ? 1e-8f : d;
+    return f32_to_f16_bits(num.result() / d);
+}
+
+// GS in {8, 16, 32, 64}: the group stays in registers; code bytes staged in LDS and written
+// coalesced.
+template <int WDT, int GS>
+__global__ __launch_bounds__(kEncThreads) void encode1_kernel(
+    const void* __restrict__ w, int64_t numel, int64_t ngroups, float root, bool vec_ok,
+    uint8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+    constexpr int NV = GS / 8;
+    __shared__ uint8_t stage[kEncThreads * NV];
+    const int64_t g0 = (int64_t)blockIdx.x * kEncThreads;
+    const int64_t g = g0 + threadIdx.x;
+    if (g < ngroups) {
+        float x[GS];
+#pragma unroll
+        for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+        const float s = group_scale<GS>(x, root);
+        auto get = [&](int64_t t, float (&o)[8]) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = x[8 * t + i];
+        };
+        scales[g] = (uint16_t)root_group(get, GS, s, stage + threadIdx.x * NV);
+    }
+    __syncthreads();
+    const int64_t ng = (ngroups - g0) < kEncThreads ? (ngroups - g0) : kEncThreads;
+    const int nbytes = (int)ng * NV;
+    uint8_t* dst = codes + g0 * NV;
+    if ((((uintptr_t)dst) & 3u) == 0) {
+        const int nwords = nbytes >> 2;
+        const uint32_t* src32 = reinterpret_cast<const uint32_t*>(stage);
+        uint32_t* dst32 = reinterpret_cast<uint32_t*>(dst);
+        for (int i = threadIdx.x; i < nwords; i += kEncThreads) dst32[i] = src32[i];
+        for (int i = (nwords << 2) + threadIdx.x; i < nbytes; i += kEncThreads) dst[i] = stage[i];
+    } else {
+        for (int i = threadIdx.x; i < nbytes; i += kEncThreads) dst[i] = stage[i];
+    }
+}
+
+// Any gs (multiple of 8): norm pass, then the codes, re-reading the group.
+template <int WDT>
+__global__ __launch_bounds__(kEncThreads) void encode1_kernel_any(
+    const void* __restrict__ w, int64_t numel, int64_t ngroups, int64_t gs, float root,
+    uint8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+#pragma clang fp contract(off)
+    const int64_t g = (int64_t)blockIdx.x * kEncThreads + threadIdx.x;
+    if (g >= ngroups) return;
+    const int64_t base = g * gs;
+    float acc[8];
+    for (int t = 0; t < gs / 8; ++t) {
+        float x[8];
+        load8<WDT>(w, base + 8 * t, numel, false, x);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = (t == 0) ? x[j] * x[j] : __builtin_fmaf(x[j], x[j], acc[j]);
+    }
+    float sum = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) sum = sum + acc[j];
+    float s = __builtin_sqrtf(sum) / root;
+    s = s + 1e-8f;
+    auto get = [&](int64_t t, float (&o)[8]) { load8<WDT>(w, base + 8 * t, numel, false, o); };
+    scales[g] = (uint16_t)root_group(get, gs, s, codes + base / 8);
+}
+
+template <int WDT>
+static hipError_t launch_encode1_t(const void* w, int64_t numel, int64_t gs, uint8_t* codes,
+                                   uint16_t* scales, hipStream_t stream) {
+    const int64_t padded = numel + (gs - numel % gs) % gs;
+    const int64_t ngroups = padded / gs;
+    const float root = (float)__builtin_sqrt((double)gs);
+    const int64_t blocks = (ngroups + kEncThreads - 1) / kEncThreads;
+    const bool vec_ok = (((uintptr_t)w) & 15u) == 0;
+    switch (gs) {
+        case 8:
+            hipLaunchKernelGGL((encode1_kernel<WDT, 8>), dim3((unsigned)blocks), dim3(kEncThreads),
+                               0, stream, w, numel, ngroups, root, vec_ok, codes, scales);
+            break;
+        case 16:
+            hipLaunchKernelGGL((encode1_kernel<WDT, 16>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, root, vec_ok,
+                               codes, scales);
+            break;
+        case 32:
+            hipLaunchKernelGGL((encode1_kernel<WDT, 32>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, root, vec_ok,
+                               codes, scales);
+            break;
+        case 64:
+            hipLaunchKernelGGL((encode1_kernel<WDT, 64>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, root, vec_ok,
+                               codes, scales);
+            break;
+        default:
+            hipLaunchKernelGGL((encode1_kernel_any<WDT>), dim3((unsigned)blocks),
+                               dim3(kEncThreads), 0, stream, w, numel, ngroups, gs, root, codes,
+                               scales);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_encode1(const void* w, int wdt, int64_t numel, int64_t gs, uint8_t* codes,
+                          uint16_t* scales, hipStream_t stream) {
+    switch (wdt) {
+        case kF32: return launch_encode1_t<kF32>(w, numel, gs, codes, scales, stream);
+        case kF16: return launch_encode1_t<kF16>(w, numel, gs, codes, scales, stream);
+        default: return launch_encode1_t<kBF16>(w, numel, gs, codes, scales, stream);
+    }
+}
+
+// ---------------------------------------------------------------- 1-bit decoder
+//
+// RootE8LatticePacker.unpack (lattice.py:519-533): one lane per 16 weights (two codes),
+// table[code][k] * scales.to(dtype) rounded to dtype (the fp32 product is exact).
+
+template <int ODT>
+__global__ __launch_bounds__(kDecThreads) void decode1_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales, int64_t numel,
+    int64_t padded, int64_t gs, bool vec_ok, void* __restrict__ out) {
+    const int64_t p = (int64_t)blockIdx.x * kDecThreads + threadIdx.x;
+    const int64_t e0 = p * 16;
+    if (e0 >= numel) return;
+    const uint32_t c0 = codes[e0 / 8];
+    const uint32_t c1 = (e0 + 8 < padded) ? codes[e0 / 8 + 1] : 0u;
+    const uint32_t s0 = scales[e0 / gs];
+    const uint32_t s1 = (e0 + 8 < padded) ? scales[(e0 + 8) / gs] : s0;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float q = (float)kRootTable.c[i < 8 ? c0 : c1][i & 7];
+        float prod = q * scale_for<ODT>(i < 8 ? s0 : s1);
+        keep_f32(prod);
+        v[i] = prod;
+    }
+    if (vec_ok && e0 + 16 <= numel) {
+        if constexpr (ODT == kF32) {
+            float4* o = reinterpret_cast<float4*>((float*)out + e0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        } else {
+            uint32_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                uint32_t lo, hi;
+                if constexpr (ODT == kF16) { lo = f32_to_f16_bits(v[2 * i]); hi = f32_to_f16_bits(v[2 * i + 1]); }
+                else { lo = f32_to_bf16_bits(v[2 * i]); hi = f32_to_bf16_bits(v[2 * i + 1]); }
+                h[i] = lo | (hi << 16);
+            }
+            uint4* o = reinterpret_cast<uint4*>((uint16_t*)out + e0);
+            o[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (e0 + i < numel) store_from_f32<ODT>(out, e0 + i, v[i]);
+    }
+}
+
+hipError_t launch_decode1(const uint8_t* codes, const uint16_t* scales, int64_t numel,
+                          int64_t gs, int odt, void* out, hipStream_t stream) {
+    const int64_t padded = numel + (gs - numel % gs) % gs;
+    const int64_t pairs = (numel + 15) / 16;
+    const int64_t blocks = (pairs + kDecThreads - 1) / kDecThreads;
+    const bool vec_ok = (((uintptr_t)out) & 15u) == 0;
+    switch (odt) {
+        case kF32:
+            hipLaunchKernelGGL((decode1_kernel<kF32>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, codes, scales, numel, padded, gs, vec_ok, out);
+            break;
+        case kF16:
+            hipLaunchKernelGGL((decode1_kernel<kF16>), dim3((unsigned)blocks), dim3(kDecThreads), 0,
+                               stream, codes, scales, numel, padded, gs, vec_ok, out);
+            break;
+        default:
+            hipLaunchKernelGGL((decode1_kernel<kBF16>), dim3((unsigned)blocks), dim3(kDecThreads),
+                               0, stream, codes, scales, numel, padded, gs, vec_ok, out);
             break;
     }
     return hipGetLastError();

@@ -81,7 +81,7 @@ __device__ __forceinline__ int code_coord(uint32_t code, int i) {
 // ---------------------------------------------------------------- 2-bit E8 codes
 
 // Code formats of the packed weight buffers.
-enum : int { kFmtTernary = 0, kFmt2Bit = 1 };
+enum : int { kFmtTernary = 0, kFmt2Bit = 1, kFmtRoot = 2 };
 
 // 2-bit code f of the flat stream (E8LatticePacker): four per byte, code j of a byte in
 // bits [2j, 2j+2) (lattice.py:242-247).

@@ -10,6 +10,7 @@
 
 #include "e8t_device.h"
 #include "e8t_internal.h"
+#include "e8t_root.h"
 
 namespace ojx {
 
@@ -23,6 +24,7 @@ __device__ __forceinline__ float deq_flat(const uint8_t* __restrict__ packed,
                                           const uint16_t* __restrict__ scales, int64_t f,
                                           int64_t gs) {
     if constexpr (FMT == kFmt2Bit) return deq2_value<DT>(load_code2(packed, f), scales[f / gs]);
+    if constexpr (FMT == kFmtRoot) return deq1_value<DT>(packed[f >> 3], (int)(f & 7), scales[f / gs]);
     const uint32_t code = load_code(packed, f >> 3);
     return (float)code_coord(code, (int)(f & 7)) * scale_for<DT>(scales[f / gs]);
 }
@@ -175,6 +177,7 @@ static hipError_t bwd_fmt(const void* gy, const uint8_t* packed, const uint16_t*
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int64_t M, int64_t N, int64_t K,
                                    int64_t gs, int dt, hipStream_t stream, int fmt) {
+    if (fmt == kFmtRoot) return fwd_fmt<kFmtRoot>(x, packed, scales, bias, y, M, N, K, gs, dt, stream);
     return fmt == kFmt2Bit
                ? fwd_fmt<kFmt2Bit>(x, packed, scales, bias, y, M, N, K, gs, dt, stream)
                : fwd_fmt<kFmtTernary>(x, packed, scales, bias, y, M, N, K, gs, dt, stream);
@@ -183,6 +186,7 @@ hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const u
 hipError_t launch_gemm_generic_bwd(const void* gy, const uint8_t* packed, const uint16_t* scales,
                                    void* gx, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
                                    hipStream_t stream, int fmt) {
+    if (fmt == kFmtRoot) return bwd_fmt<kFmtRoot>(gy, packed, scales, gx, M, N, K, gs, dt, stream);
     return fmt == kFmt2Bit
                ? bwd_fmt<kFmt2Bit>(gy, packed, scales, gx, M, N, K, gs, dt, stream)
                : bwd_fmt<kFmtTernary>(gy, packed, scales, gx, M, N, K, gs, dt, stream);

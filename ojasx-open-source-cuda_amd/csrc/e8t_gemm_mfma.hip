@@ -27,6 +27,7 @@
 #include "e8t_device.h"
 #include "e8t_internal.h"
 #include "e8t_lut.h"
+#include "e8t_root.h"
 
 namespace ojx {
 
@@ -272,6 +273,78 @@ struct Bit2RowDecoder {
     }
 };
 
+// 1-bit Root E8 (RootE8LatticePacker, lattice.py:426-533): one code byte per 8 weights,
+// coordinates 0, +-1, +-2 times the group scale, rounded to the activation dtype (exact
+// except an fp16 overflow of 2 s).  Per scale group the table {S0 = s | rnd(2s) << 16,
+// S1 = -s | -rnd(2s) << 16}; a 256-entry LDS table (4 KB, `kSel1Entries`) maps a code to
+// four v_perm_b32 selector words (selector byte 12 gives the zero bytes).
+constexpr int kSel1Entries = 256;
+
+__device__ __forceinline__ void fill_sel1(uint4* tab, int nthreads) {
+    for (int e = (int)threadIdx.x; e < kSel1Entries; e += nthreads) {
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            w[h] = root_sel_pair(kRootTable.c[e][2 * h]) |
+                   (root_sel_pair(kRootTable.c[e][2 * h + 1]) << 16);
+        tab[e] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint2 values1(uint32_t s16) {
+    const float s = scale_for<DT>(s16 & 0xFFFFu);
+    const uint32_t a = rnd_bits<DT>(s), b = rnd_bits<DT>(2.0f * s);
+    return make_uint2(a | (b << 16), (a ^ 0x8000u) | ((b ^ 0x8000u) << 16));
+}
+
+template <int DT, int GS>
+struct RootRowDecoder {
+    static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "1-bit group size 8..64");
+    uint32_t c;       // the half-row's 4 codes (32 weights)
+    uint2 sc;         // its scales, as Bit2RowDecoder
+    uint4 sel[4];     // selector words of pieces 0..3
+    uint2 val[4];     // value words of pieces 0..3
+    const char* tab;
+    uint32_t vo_code, vo_scale;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    __device__ __forceinline__ void load(int64_t k0) {
+        c = __builtin_amdgcn_raw_buffer_load_b32(pr, vo_code, uniform_offset(k0 / 8), 0);
+        const int so = uniform_offset(k0 * 2 / GS);
+        if constexpr (GS == 8) {
+            const auto u = __builtin_amdgcn_raw_buffer_load_b64(sr, vo_scale, so, 0);
+            sc = make_uint2(u[0], u[1]);
+        } else if constexpr (GS == 16) {
+            sc = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(sr, vo_scale, so, 0), 0u);
+        } else {
+            sc = make_uint2(__builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale, so, 0), 0u);
+        }
+    }
+    __device__ __forceinline__ void prep() {
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            sel[p] = *reinterpret_cast<const uint4*>(tab + 16u * ((c >> (8 * p)) & 0xFFu));
+        if constexpr (GS == 8) {
+            val[0] = values1<DT>(sc.x);
+            val[1] = values1<DT>(sc.x >> 16);
+            val[2] = values1<DT>(sc.y);
+            val[3] = values1<DT>(sc.y >> 16);
+        } else if constexpr (GS == 16) {
+            val[0] = val[1] = values1<DT>(sc.x);
+            val[2] = val[3] = values1<DT>(sc.x >> 16);
+        } else {
+            val[0] = val[1] = val[2] = val[3] = values1<DT>(sc.x);
+        }
+    }
+    __device__ __forceinline__ uint4 piece(int p) const {
+        const uint32_t s0 = val[p].x, s1 = val[p].y;
+        return make_uint4(__builtin_amdgcn_perm(s0, s1, sel[p].x),
+                          __builtin_amdgcn_perm(s0, s1, sel[p].y),
+                          __builtin_amdgcn_perm(s0, s1, sel[p].z),
+                          __builtin_amdgcn_perm(s0, s1, sel[p].w));
+    }
+};
+
 // One K step (64) of the wave's block.
 //   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read,
 //      then the next step's X tile load is issued (issue_x);
@@ -314,20 +387,22 @@ __device__ __forceinline__ void vm_wait_le2() {
     __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): all but the two newest loads (gfx9)
 }
 
-// FMT: kFmtTernary (group size 32) or kFmt2Bit (group size GS2).
+// FMT: kFmtTernary (group size 32), kFmt2Bit or kFmtRoot (group size GS2).
 template <int DT, typename C, int FMT, int GS2>
 __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     float* __restrict__ part, int splits, int64_t M, int64_t N, int64_t K) {
     constexpr bool kTernary = FMT == kFmtTernary;
-    __shared__ uint4 lut_storage[kTernary ? kLutStorageU4 : kSel2Entries / 2];
+    __shared__ uint4 lut_storage[kTernary ? kLutStorageU4
+                                          : (FMT == kFmt2Bit ? kSel2Entries / 2 : kSel1Entries)];
     __shared__ __attribute__((aligned(16))) char xs[2][C::XTILE];
     __shared__ __attribute__((aligned(16))) char ws[2][C::WTILE];
     constexpr int kTM = C::TM, kTN = C::TN;
 
     if constexpr (kTernary) fill_lut<C::THREADS>(lut_storage, kLutMasks);
-    else fill_sel2(reinterpret_cast<uint2*>(lut_storage), C::THREADS);
+    else if constexpr (FMT == kFmt2Bit) fill_sel2(reinterpret_cast<uint2*>(lut_storage), C::THREADS);
+    else fill_sel1(lut_storage, C::THREADS);
 
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
     const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (N + C::BN - 1) / C::BN;
@@ -359,7 +434,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
-    const uint32_t rowbytes = kTernary ? (uint32_t)(K * 3 / 16) : (uint32_t)(K / 4);
+    const uint32_t rowbytes = kTernary ? (uint32_t)(K * 3 / 16)
+                                       : (FMT == kFmt2Bit ? (uint32_t)(K / 4) : (uint32_t)(K / 8));
     const uint32_t srowbytes = kTernary ? (uint32_t)(K / 16) : (uint32_t)(K * 2 / GS2);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
@@ -370,7 +446,9 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const uint32_t vo_code = (uint32_t)(n0 + wrow) * rowbytes;
     const uint32_t vo_scale = (uint32_t)(n0 + wrow) * srowbytes;
     const char* lut = reinterpret_cast<const char*>(lut_storage) + (kTernary ? kLutBaseOffset : 0);
-    using Dec = std::conditional_t<kTernary, TernaryRowDecoder<DT>, Bit2RowDecoder<DT, GS2>>;
+    using Dec = std::conditional_t<
+        kTernary, TernaryRowDecoder<DT>,
+        std::conditional_t<FMT == kFmt2Bit, Bit2RowDecoder<DT, GS2>, RootRowDecoder<DT, GS2>>>;
     Dec dec;
     dec.pr = pr;
     dec.sr = sr;
@@ -382,7 +460,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         dec.half = half;
     } else {
         dec.tab = lut;
-        dec.vo_code = vo_code + 8u * (uint32_t)half;
+        dec.vo_code = vo_code + (FMT == kFmt2Bit ? 8u : 4u) * (uint32_t)half;
         // scale bytes of the half row: GS 8: 4 scales, 16: 2, 32: 1; GS 64: the step's one
         dec.vo_scale = vo_scale + (GS2 < 64 ? (uint32_t)half * (64u / GS2) : 0u);
     }
@@ -498,11 +576,12 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
     if (M < 1 || N < 1 || K < kBK || K % kBK != 0) return false;
     if (fmt == kFmtTernary ? gs != 32 : (gs != 8 && gs != 16 && gs != 32 && gs != 64))
         return false;
+    if (fmt != kFmtTernary && fmt != kFmt2Bit && fmt != kFmtRoot) return false;
     if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 7u) || ((uintptr_t)scales & 7u))
         return false;
     // 32-bit buffer offsets: the activation matrix and the weight buffers (plus one tile
     // of padding rows) must stay below 2^31 bytes
-    const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : K / 4;
+    const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : (fmt == kFmt2Bit ? K / 4 : K / 8);
     const int64_t srowbytes = fmt == kFmtTernary ? K / 16 : K * 2 / gs;
     if ((M + CfgLarge::BM) * K * 2 >= (1ll << 31) || (N + CfgLarge::BN) * rowbytes >= (1ll << 31) ||
         (N + CfgLarge::BN) * srowbytes >= (1ll << 31))
@@ -578,6 +657,24 @@ static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_
     if (fmt == kFmtTernary)
         return launch_cfg<DT, C, kFmtTernary, 32>(x, packed, scales, bias, y, part, splits, M, N,
                                                   K, stream);
+    if (fmt == kFmtRoot) {
+        switch (gs) {
+        case 8:
+            return launch_cfg<DT, C, kFmtRoot, 8>(x, packed, scales, bias, y, part, splits, M, N,
+                                                  K, stream);
+        case 16:
+            return launch_cfg<DT, C, kFmtRoot, 16>(x, packed, scales, bias, y, part, splits, M, N,
+                                                   K, stream);
+        case 32:
+            return launch_cfg<DT, C, kFmtRoot, 32>(x, packed, scales, bias, y, part, splits, M, N,
+                                                   K, stream);
+        case 64:
+            return launch_cfg<DT, C, kFmtRoot, 64>(x, packed, scales, bias, y, part, splits, M, N,
+                                                   K, stream);
+        default:
+            return hipErrorInvalidValue;
+        }
+    }
     switch (gs) {
     case 8:
         return launch_cfg<DT, C, kFmt2Bit, 8>(x, packed, scales, bias, y, part, splits, M, N, K,

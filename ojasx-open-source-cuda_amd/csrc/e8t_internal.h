@@ -18,6 +18,12 @@ hipError_t launch_encode2(const void* w, int wdt, int64_t numel, int64_t gs, uin
 hipError_t launch_decode2(const uint8_t* packed, const uint16_t* scales, int64_t numel,
                           int64_t gs, int odt, void* out, hipStream_t stream);
 
+// 1-bit Root-E8 codec (RootE8LatticePacker): gs a positive multiple of 8.
+hipError_t launch_encode1(const void* w, int wdt, int64_t numel, int64_t gs, uint8_t* codes,
+                          uint16_t* scales, hipStream_t stream);
+hipError_t launch_decode1(const uint8_t* codes, const uint16_t* scales, int64_t numel,
+                          int64_t gs, int odt, void* out, hipStream_t stream);
+
 // 2-bit decode GEMV (M <= 4, bf16/fp16, K % 1024 == 0, gs in {8, 16, 32, 64}, 16-byte
 // aligned buffers).
 bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
@@ -27,7 +33,7 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
                         int dt, hipStream_t stream);
 
 // General tiled kernels: any M, N, K >= 1 (flat layout), any dtype; fmt selects the code
-// format (0 ternary, 1 2-bit).
+// format (0 ternary, 1 2-bit, 2 1-bit Root E8).
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int64_t M, int64_t N, int64_t K,
                                    int64_t gs, int dt, hipStream_t stream, int fmt = 0);
@@ -85,8 +91,8 @@ int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream);
 
-// Prefill MFMA GEMM: F16/BF16, K % 64 == 0; fmt 0 (ternary, group size 32) or 1 (2-bit,
-// group size 8, 16, 32 or 64).
+// Prefill MFMA GEMM: F16/BF16, K % 64 == 0; fmt 0 (ternary, group size 32), 1 (2-bit) or 2
+// (1-bit Root E8), the last two with group size 8, 16, 32 or 64.
 bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                          int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt = 0);
 // Tile configuration and K splits of the prefill GEMM for a shape (splits 1 = none).  With

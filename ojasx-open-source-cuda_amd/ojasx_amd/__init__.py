@@ -1,5 +1,5 @@
-"""ojasx_amd -- MI355X-native E8 quantized-weight path: ternary 1.5 bit/weight and
-2 bit/weight.
+"""ojasx_amd -- MI355X-native E8 quantized-weight path: ternary 1.5 bit/weight,
+2 bit/weight and 1 bit/weight (Root E8).
 
 Drop-in for the E8 names of ``ojasx3.lattice``: the packer, the fused linear and
 the layer keep the reference's signatures and buffer layout, and every array
@@ -11,8 +11,10 @@ from . import grouped, ops
 from .lattice import (
     E8LatticeLinear,
     E8LatticePacker,
+    RootE8LatticePacker,
     TernaryE8LatticePacker,
     _get_packer_for_bitrate,
+    _get_root_e8_lut,
     _FusedE8GEMMFunction,
     _get_ternary_e8_luts,
     fwht_block32,
@@ -27,8 +29,10 @@ __all__ = [
     "ops",
     "E8LatticeLinear",
     "E8LatticePacker",
+    "RootE8LatticePacker",
     "TernaryE8LatticePacker",
     "_get_packer_for_bitrate",
+    "_get_root_e8_lut",
     "_FusedE8GEMMFunction",
     "_get_ternary_e8_luts",
     "fwht_block32",

@@ -32,6 +32,10 @@ EXPORTS = (
     "ojx_e8_decode",
     "ojx_e8_gemm_fwd",
     "ojx_e8_gemm_bwd_dx",
+    "ojx_e8r_encode",
+    "ojx_e8r_decode",
+    "ojx_e8r_gemm_fwd",
+    "ojx_e8r_gemm_bwd_dx",
 )
 
 
@@ -95,6 +99,14 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
             L.ojx_e8_gemm_bwd_dx.restype = _INT
             L.ojx_e8_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8r_encode.restype = _INT
+            L.ojx_e8r_encode.argtypes = [_P, _INT, _I64, _I64, _P, _P, _P]
+            L.ojx_e8r_decode.restype = _INT
+            L.ojx_e8r_decode.argtypes = [_P, _P, _I64, _I64, _INT, _P, _P]
+            L.ojx_e8r_gemm_fwd.restype = _INT
+            L.ojx_e8r_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8r_gemm_bwd_dx.restype = _INT
+            L.ojx_e8r_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
             _lib = L
     return _lib
 

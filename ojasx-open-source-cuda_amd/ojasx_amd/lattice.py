@@ -1,6 +1,6 @@
-"""E8 lattice quantization (ternary 1.5 bit/weight and 2 bit/weight) on MI355X.
+"""E8 lattice quantization (ternary 1.5, 2 and 1 bit/weight) on MI355X.
 
-Mirrors the ternary and 2-bit parts of ``ojasx3.lattice`` / ``ojasx2.math.lattice``
+Mirrors the E8 parts of ``ojasx3.lattice`` / ``ojasx2.math.lattice``
 -- same names, arguments, buffers, coercions and errors -- with every array
 operation on the path running in the HIP kernels behind ``ojasx_amd.ops``:
 
@@ -13,15 +13,17 @@ this module                         reference (ojasx2/math/lattice.py)
 ``TernaryE8LatticePacker.unpack``   :386-419   -> ops.decode
 ``E8LatticePacker.pack``            :213-249   -> ops.encode2 (2-bit)
 ``E8LatticePacker.unpack``          :252-279   -> ops.decode2
+``_get_root_e8_lut``                :428-466
+``RootE8LatticePacker.pack``        :473-509   -> ops.encode1 (1-bit)
+``RootE8LatticePacker.unpack``      :512-533   -> ops.decode1
 ``_get_packer_for_bitrate``         :536-541
 ``_FusedE8GEMMFunction``            :548-717   -> ops.e8t_linear / ops.e8_linear
 ``E8LatticeLinear``                 :724-846
 ``pack_model_e8``                   :901-945
 =================================  ==========================================
 
-Bitrates 1.5 (ternary) and 2.0 (2-bit, the reference's default for any bitrate
-other than 1.0 and 1.5) are implemented; 1.0 (RootE8LatticePacker) raises
-``NotImplementedError``.
+Bitrates 1.5 (ternary), 2.0 (2-bit, the reference's default for any bitrate other
+than 1.0 and 1.5) and 1.0 (RootE8LatticePacker) are implemented.
 CPU tensors given to ``pack`` / ``unpack`` are processed on the current GPU and
 the result is returned on the CPU; the fused forward requires GPU tensors.
 """
@@ -41,6 +43,7 @@ __all__ = [
     "fwht_block32",
     "TernaryE8LatticePacker",
     "E8LatticePacker",
+    "RootE8LatticePacker",
     "_FusedE8GEMMFunction",
     "E8LatticeLinear",
     "pack_model_e8",
@@ -163,13 +166,75 @@ class E8LatticePacker:
         return out.view(shape)
 
 
+_DEVICE_ROOT_E8_LUTS: Dict[Tuple[str, Optional[int]], torch.Tensor] = {}
+
+
+def _get_root_e8_lut(device: Optional[torch.device] = None) -> torch.Tensor:
+    """The 256 x 8 fp32 table of lattice.py:428-466 (scaled by 2): the 112 rows with +-2 at
+    two coordinates, the 128 rows (+-1)^8 with an even number of -1 (itertools.product
+    order), the 16 rows with +-2 at one coordinate.  The HIP kernels carry the same table
+    (csrc/e8t_root.h); this copy is for callers of the reference API."""
+    if device is None:
+        key = ("cpu", None)
+    else:
+        device = torch.device(device)
+        key = (device.type, device.index)
+    if key not in _DEVICE_ROOT_E8_LUTS:
+        rows = []
+        for i in range(8):
+            for j in range(i + 1, 8):
+                for s1 in (-1.0, 1.0):
+                    for s2 in (-1.0, 1.0):
+                        r = [0.0] * 8
+                        r[i], r[j] = s1, s2
+                        rows.append(r)
+        for p in range(256):
+            signs = [0.5 if (p >> (7 - k)) & 1 else -0.5 for k in range(8)]
+            if sum(1 for v in signs if v < 0) % 2 == 0:
+                rows.append(signs)
+        for i in range(8):
+            for s in (-1.0, 1.0):
+                r = [0.0] * 8
+                r[i] = s
+                rows.append(r)
+        lut = torch.tensor(rows, dtype=torch.float32) * 2.0
+        dev = torch.device(key[0], key[1]) if key[1] is not None else torch.device(key[0])
+        _DEVICE_ROOT_E8_LUTS[key] = lut.to(dev)
+    return _DEVICE_ROOT_E8_LUTS[key]
+
+
+class RootE8LatticePacker:
+    """Packs weight matrices into 1.00 bit/weight (1 byte per 8D vector) using the 240 E8 roots."""
+
+    @staticmethod
+    def pack(w: torch.Tensor, group_size: int = 32
+             ) -> Tuple[torch.Tensor, torch.Tensor, Tuple[int, int]]:
+        m, n = w.shape
+        if group_size <= 0 or group_size % 8 != 0:
+            group_size = 8  # silent coercion, lattice.py:485-486
+        codes, scales = ops.encode1(_on_gpu(w), group_size)
+        if w.device.type != "cuda":
+            codes, scales = codes.to(w.device), scales.to(w.device)
+        return codes, scales, (m, n)
+
+    @staticmethod
+    def unpack(packed_codes: torch.Tensor, scales: torch.Tensor, shape: Tuple[int, int],
+               dtype: torch.dtype = torch.float32, use_workspace: bool = False) -> torch.Tensor:
+        del use_workspace  # a shared scratch buffer in the reference; a fresh tensor here
+        total = shape[0] * shape[1]
+        padded = packed_codes.numel() * 8
+        group_size = padded // max(1, scales.numel())  # inferred as in lattice.py:524-525
+        out = ops.decode1(_on_gpu(packed_codes), _on_gpu(scales), total, group_size, dtype)
+        if packed_codes.device.type != "cuda":
+            out = out.to(packed_codes.device)
+        return out.view(shape)
+
+
 def _get_packer_for_bitrate(bitrate: float):
-    """lattice.py:536-541: 1.0 -> RootE8LatticePacker (not implemented here), 1.5 ->
-    TernaryE8LatticePacker, anything else -> E8LatticePacker."""
+    """lattice.py:536-541: 1.0 -> RootE8LatticePacker, 1.5 -> TernaryE8LatticePacker,
+    anything else -> E8LatticePacker."""
     if bitrate == 1.0:
-        raise NotImplementedError(
-            "ojasx_amd implements the ternary (1.5) and 2-bit E8 paths; bitrate 1.0 "
-            "(RootE8LatticePacker) is not available")
+        return RootE8LatticePacker
     if bitrate == 1.5:
         return TernaryE8LatticePacker
     return E8LatticePacker
@@ -195,11 +260,11 @@ class _FusedE8GEMMFunction(torch.autograd.Function):
         x_rot = fwht_block32(x) if (use_hadamard and in_features % 32 == 0) else x
         ctx.save_for_backward(packed_weight, block_scales)
         ctx.dims = (out_features, in_features, group_size)
-        ctx.ternary = float(bitrate) == 1.5
+        ctx.bitrate = float(bitrate)
         ctx.x_shape = x_rot.shape
         ctx.has_bias = bias is not None
         ctx.use_hadamard = use_hadamard
-        linear = ops.e8t_linear if ctx.ternary else ops.e8_linear
+        linear = {1.5: ops.e8t_linear, 1.0: ops.e8r_linear}.get(ctx.bitrate, ops.e8_linear)
         return linear(x_rot, packed_weight, block_scales, bias, out_features, in_features,
                       group_size)
 
@@ -207,7 +272,8 @@ class _FusedE8GEMMFunction(torch.autograd.Function):
     def backward(ctx, grad_y):
         packed_weight, block_scales = ctx.saved_tensors
         out_features, in_features, group_size = ctx.dims
-        bwd = ops.e8t_linear_bwd_dx if ctx.ternary else ops.e8_linear_bwd_dx
+        bwd = {1.5: ops.e8t_linear_bwd_dx, 1.0: ops.e8r_linear_bwd_dx}.get(
+            ctx.bitrate, ops.e8_linear_bwd_dx)
         grad_x = bwd(grad_y.contiguous(), packed_weight, block_scales, out_features,
                      in_features, group_size)
         grad_x = grad_x.reshape(ctx.x_shape)
@@ -220,7 +286,8 @@ class _FusedE8GEMMFunction(torch.autograd.Function):
 class E8LatticeLinear(nn.Module):
     """Linear layer with base weights packed into the 8D E8 lattice (lattice.py:724-846).
 
-    Buffers ``packed_weight`` (uint8 [padded*3/16] at bitrate 1.5, [padded/4] at 2.0)
+    Buffers ``packed_weight`` (uint8 [padded*3/16] at bitrate 1.5, [padded/4] at 2.0,
+    [padded/8] at 1.0)
     and ``block_scales`` (fp16 [padded/group]) have the reference's names, shapes and
     layout, so its state_dicts load unchanged.  LoRA adapters as in the reference."""
 
@@ -243,6 +310,10 @@ class E8LatticeLinear(nn.Module):
             eff_group = group_size if (group_size >= 16 and group_size % 16 == 0) else 16
             padded = total + ((-total) % eff_group)
             num_bytes = (padded * 3) // 16
+        elif self.bitrate == 1.0:
+            eff_group = group_size if (group_size >= 8 and group_size % 8 == 0) else 8
+            padded = total + ((-total) % eff_group)
+            num_bytes = padded // 8
         else:
             eff_group = group_size if (group_size >= 8 and group_size % 8 == 0) else 8
             padded = total + ((-total) % eff_group)

@@ -472,3 +472,148 @@ def fused_e8_gemm_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
 @fused_e8_gemm_bwd_dx.register_fake
 def _(grad_y, packed_weight, block_scales, in_features, group_size=32):
     return grad_y.new_empty((*grad_y.shape[:-1], in_features))
+
+
+# --------------------------------------------------------------------------- 1-bit Root E8
+
+@torch.library.custom_op(f"{_NS}::encode1", mutates_args=())
+def encode1(w: torch.Tensor, group_size: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """RootE8LatticePacker.pack (lattice.py:473-509): (codes uint8 [padded/8], fp16 scales).
+    group_size must already be coerced (a positive multiple of 8)."""
+    dev = N.require_device(w)
+    _check_gs2(group_size, 8)
+    if w.dtype not in N.DTYPE_CODE:
+        w = w.to(torch.float32)  # the reference widens to fp32 first (lattice.py:489)
+    w = w.contiguous()
+    numel = w.numel()
+    padded = _padded(numel, group_size)
+    codes = torch.empty(padded // 8, dtype=torch.uint8, device=dev)
+    scales = torch.empty(padded // group_size, dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8r_encode(N.ptr(w), _dtype_code(w.dtype), numel, group_size,
+                                       N.ptr(codes), N.ptr(scales), N.stream_handle(dev)),
+                "e8r encode")
+    return codes, scales
+
+
+@encode1.register_fake
+def _(w, group_size):
+    padded = _padded(w.numel(), group_size)
+    return (w.new_empty(padded // 8, dtype=torch.uint8),
+            w.new_empty(padded // group_size, dtype=torch.float16))
+
+
+@torch.library.custom_op(f"{_NS}::decode1", mutates_args=())
+def decode1(codes: torch.Tensor, scales: torch.Tensor, numel: int, group_size: int,
+            dtype: torch.dtype) -> torch.Tensor:
+    """RootE8LatticePacker.unpack (lattice.py:519-533), flat, first ``numel`` weights."""
+    dev = N.require_device(codes, scales)
+    _check_gs2(group_size, 8)
+    if codes.dtype != torch.uint8 or scales.dtype != torch.float16:
+        raise RuntimeError("decode1 expects uint8 codes and float16 scales")
+    padded = _padded(numel, group_size)
+    if codes.numel() < padded // 8 or scales.numel() < padded // group_size:
+        raise RuntimeError(
+            f"codes/scales too small for {numel} weights at group_size {group_size}")
+    out = torch.empty(numel, dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8r_decode(N.ptr(codes.contiguous()), N.ptr(scales.contiguous()),
+                                       numel, group_size, _dtype_code(dtype), N.ptr(out),
+                                       N.stream_handle(dev)),
+                "e8r decode")
+    return out
+
+
+@decode1.register_fake
+def _(codes, scales, numel, group_size, dtype):
+    return codes.new_empty(numel, dtype=dtype)
+
+
+def _check_layer_buffers1(codes: torch.Tensor, scales: torch.Tensor, out_features: int,
+                          in_features: int, group_size: int) -> None:
+    if codes.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if scales.dtype != torch.float16:
+        raise RuntimeError("block_scales must be float16")
+    padded = _padded(out_features * in_features, group_size)
+    if codes.numel() < padded // 8:
+        raise RuntimeError(
+            f"packed_weight holds {codes.numel()} bytes; {out_features}x{in_features} at "
+            f"group_size {group_size} needs {padded // 8}")
+    if scales.numel() < padded // group_size:
+        raise RuntimeError(
+            f"block_scales holds {scales.numel()} values; needs {padded // group_size}")
+
+
+@torch.library.custom_op(f"{_NS}::e8r_linear", mutates_args=())
+def e8r_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+               bias: Optional[torch.Tensor], out_features: int, in_features: int,
+               group_size: int) -> torch.Tensor:
+    """1-bit fused linear: x . Wdeq^T + bias, Wdeq = table[code] * scale in x's dtype."""
+    dev = N.require_device(x, packed_weight, block_scales, bias)
+    _check_gs2(group_size, 8)
+    if x.shape[-1] != in_features:
+        raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    _check_layer_buffers1(packed_weight, block_scales, out_features, in_features, group_size)
+    dt = _dtype_code(x.dtype)
+    x2 = x.reshape(-1, in_features).contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, out_features), dtype=x.dtype, device=dev)
+    b = None
+    if bias is not None:
+        if bias.numel() != out_features:
+            raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
+        b = bias.to(x.dtype).contiguous()
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8r_gemm_fwd(N.ptr(x2), N.ptr(packed_weight.contiguous()),
+                                         N.ptr(block_scales.contiguous()), N.ptr(b), N.ptr(y), M,
+                                         out_features, in_features, group_size, dt,
+                                         N.stream_handle(dev)),
+                "e8r gemm_fwd")
+    return y.reshape(*x.shape[:-1], out_features)
+
+
+@e8r_linear.register_fake
+def _(x, packed_weight, block_scales, bias, out_features, in_features, group_size):
+    return x.new_empty((*x.shape[:-1], out_features))
+
+
+@torch.library.custom_op(f"{_NS}::e8r_linear_bwd_dx", mutates_args=())
+def e8r_linear_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
+                      block_scales: torch.Tensor, out_features: int, in_features: int,
+                      group_size: int) -> torch.Tensor:
+    dev = N.require_device(grad_y, packed_weight, block_scales)
+    _check_gs2(group_size, 8)
+    if grad_y.shape[-1] != out_features:
+        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
+    _check_layer_buffers1(packed_weight, block_scales, out_features, in_features, group_size)
+    dt = _dtype_code(grad_y.dtype)
+    gy = grad_y.reshape(-1, out_features).contiguous()
+    M = gy.shape[0]
+    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8r_gemm_bwd_dx(N.ptr(gy), N.ptr(packed_weight.contiguous()),
+                                            N.ptr(block_scales.contiguous()), N.ptr(gx), M,
+                                            out_features, in_features, group_size, dt,
+                                            N.stream_handle(dev)),
+                "e8r gemm_bwd_dx")
+    return gx.reshape(*grad_y.shape[:-1], in_features)
+
+
+@e8r_linear_bwd_dx.register_fake
+def _(grad_y, packed_weight, block_scales, out_features, in_features, group_size):
+    return grad_y.new_empty((*grad_y.shape[:-1], in_features))
+
+
+def _linear1_backward(ctx, grad_y):
+    packed_weight, block_scales = ctx.saved_tensors
+    out_features, in_features, group_size = ctx.dims
+    grad_x = None
+    if ctx.needs_input_grad[0]:
+        grad_x = e8r_linear_bwd_dx(grad_y, packed_weight, block_scales, out_features,
+                                   in_features, group_size)
+    grad_bias = grad_y.reshape(-1, out_features).sum(dim=0) if ctx.has_bias else None
+    return grad_x, None, None, grad_bias, None, None, None
+
+
+e8r_linear.register_autograd(_linear1_backward, setup_context=_linear_setup_context)

@@ -23,7 +23,7 @@ def _validate_row_layout(out_features: int, in_features: int, bitrate: float,
     if float(bitrate) not in _SUPPORTED_BITRATES:
         raise ValueError(f"Unsupported E8 bitrate {bitrate!r}; expected one of "
                          f"{sorted(_SUPPORTED_BITRATES)}")
-    _get_packer_for_bitrate(float(bitrate))  # 1.0 (Root E8) is not implemented
+    _get_packer_for_bitrate(float(bitrate))
     if out_features <= 0 or in_features <= 0:
         raise ValueError("Streaming E8 requires non-empty two-dimensional weights")
     if group_size <= 0 or group_size % 32 != 0:

@@ -536,3 +536,229 @@ OJO_API void ojo_e8b_gemm_bwd_f64(const float* gy, const uint8_t* packed, const 
 OJO_API void ojo_e8b_quantize8_array(const float* v, int64_t nvec, uint8_t* codes) {
     for (int64_t t = 0; t < nvec; ++t) ojo_e8b_quantize8(v + 8 * t, codes + 8 * t);
 }
+
+/* ------------------------------------------------------------------------- */
+/* 1-bit Root E8 (RootE8LatticePacker, lattice.py:426-533)                      */
+/* ------------------------------------------------------------------------- */
+
+/* The 256-entry table of lattice.py:436-456, scaled by 2 as the reference scales it:
+ *   0..111   (+-2 at i, +-2 at j), i < j, loops i, j, s1 in (-1, +1), s2 in (-1, +1)
+ *   112..239 (+-1)^8 with an even number of -1, in itertools.product order over
+ *            (-0.5, +0.5) (first coordinate slowest), scaled
+ *   240..255 (+-2 at i), loops i, s in (-1, +1) */
+OJO_API void ojo_e8r_lut(float out[256 * 8]) {
+    int e = 0;
+    memset(out, 0, 256 * 8 * sizeof(float));
+    for (int i = 0; i < 8; ++i)
+        for (int j = i + 1; j < 8; ++j)
+            for (int a = 0; a < 2; ++a)
+                for (int b = 0; b < 2; ++b) {
+                    out[8 * e + i] = a ? 2.0f : -2.0f;
+                    out[8 * e + j] = b ? 2.0f : -2.0f;
+                    ++e;
+                }
+    for (int p = 0; p < 256; ++p) {
+        int neg = 0;
+        for (int k = 0; k < 8; ++k) neg += !((p >> (7 - k)) & 1);
+        if (neg & 1) continue;
+        for (int k = 0; k < 8; ++k) out[8 * e + k] = ((p >> (7 - k)) & 1) ? 1.0f : -1.0f;
+        ++e;
+    }
+    for (int i = 0; i < 8; ++i)
+        for (int s = 0; s < 2; ++s) {
+            out[8 * e + i] = s ? 2.0f : -2.0f;
+            ++e;
+        }
+}
+
+/* Code of one 8-vector v (already divided by the group's initial scale), as
+ * argmax(v . normalize(lut)^T) (lattice.py:497-500): each dot product is the
+ * sequential FMA chain acc = fmaf(v[k], u[k], acc) from acc = +0 over k = 0..7 (the
+ * order of torch's CPU matmul for these shapes, checked against torch), u the table
+ * row divided by its norm in fp32; the first maximal index wins (torch.argmax). */
+OJO_API int32_t ojo_e8r_quantize8(const float v[8]) {
+    static float unorm[256 * 8];
+    static int ready = 0;
+    if (!ready) { /* not thread-safe on first use: callers warm it up (ojo_e8r_prepare) */
+        float lut[256 * 8];
+        ojo_e8r_lut(lut);
+        for (int e = 0; e < 256; ++e) {
+            float ss = 0.0f;
+            for (int k = 0; k < 8; ++k) ss = ss + lut[8 * e + k] * lut[8 * e + k];
+            float n = sqrtf(ss);
+            if (n < 1e-12f) n = 1e-12f;
+            for (int k = 0; k < 8; ++k) unorm[8 * e + k] = lut[8 * e + k] / n;
+        }
+        ready = 1;
+    }
+    int best = 0;
+    float best_dot = 0.0f;
+    for (int e = 0; e < 256; ++e) {
+        float acc = 0.0f;
+        for (int k = 0; k < 8; ++k) acc = fmaf(v[k], unorm[8 * e + k], acc);
+        if (e == 0 || acc > best_dot) {
+            best = e;
+            best_dot = acc;
+        }
+    }
+    return best;
+}
+
+OJO_API void ojo_e8r_prepare(void) {
+    float v[8] = {0};
+    (void)ojo_e8r_quantize8(v);
+}
+
+/* Sum over a group of gs values in the order of torch's CPU sum along a contiguous last
+ * dim (checked against torch for every multiple of 8 up to 256): four 8-lane
+ * accumulators take the 8-blocks of each 32-block in turn, 8-blocks after the last full
+ * 32-block go to the first accumulator, the four accumulators are added in order and
+ * then their 8 lanes left to right. */
+static float torch_row_sum(const float* x, int64_t n) {
+    float acc[4][8];
+    memset(acc, 0, sizeof(acc));
+    int64_t nch = n / 8, main = (nch / 4) * 4;
+    for (int64_t c = 0; c < nch; ++c) {
+        int a = c < main ? (int)(c % 4) : 0;
+        for (int j = 0; j < 8; ++j) acc[a][j] = acc[a][j] + x[8 * c + j];
+    }
+    float lane[8];
+    for (int j = 0; j < 8; ++j) lane[j] = ((acc[0][j] + acc[1][j]) + acc[2][j]) + acc[3][j];
+    float s = lane[0];
+    for (int j = 1; j < 8; ++j) s = s + lane[j];
+    return s;
+}
+
+OJO_API float ojo_e8r_row_sum(const float* x, int64_t n) { return torch_row_sum(x, n); }
+
+/* One flat group (lattice.py:486-509): initial scale as the other packers', codes by
+ * ojo_e8r_quantize8 of w / s, then the MMSE scale
+ *   sum(w * q) / clamp(sum(q * q), 1e-8)  with q = lut[code] (the x2 table),
+ * both sums in torch's order; stored as fp16. */
+static void e8r_encode_group(const float* w, int64_t gs, const float* lut, uint8_t* codes,
+                             uint16_t* scale16, float* scale32) {
+    float s = ojo_e8t_group_scale(w, gs);
+    float prod[4096], qq[4096];
+    for (int64_t t = 0; t < gs / 8; ++t) {
+        float v[8];
+        for (int i = 0; i < 8; ++i) v[i] = w[8 * t + i] / s;
+        int32_t c = ojo_e8r_quantize8(v);
+        codes[t] = (uint8_t)c;
+        for (int i = 0; i < 8; ++i) {
+            float q = lut[8 * c + i];
+            prod[8 * t + i] = w[8 * t + i] * q;
+            qq[8 * t + i] = q * q;
+        }
+    }
+    float num = torch_row_sum(prod, gs);
+    float den = torch_row_sum(qq, gs);
+    if (den < 1e-8f) den = 1e-8f;
+    float mm = num / den;
+    *scale16 = ojo_f32_to_f16(mm);
+    if (scale32) *scale32 = mm;
+}
+
+/* RootE8LatticePacker.pack on a flat fp32 array (gs a positive multiple of 8, at most
+ * 4096; the caller applies the reference's coercion of other values to 8).
+ * codes: padded/8 bytes; scales: padded/gs fp16 bits; scales32 optional. */
+OJO_API void ojo_e8r_encode(const float* w, int64_t numel, int64_t gs, uint8_t* codes,
+                            uint16_t* scales, float* scales32, int nthreads) {
+    float lut[256 * 8];
+    ojo_e8r_lut(lut);
+    ojo_e8r_prepare();
+    int64_t padded = ojo_e8t_padded(numel, gs);
+    int64_t ngroups = padded / gs;
+    int64_t full = numel / gs;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t g = 0; g < full; ++g)
+        e8r_encode_group(w + g * gs, gs, lut, codes + g * gs / 8, scales + g,
+                         scales32 ? scales32 + g : 0);
+    (void)nthreads;
+    if (full < ngroups) { /* tail group, zero padded (F.pad, lattice.py:490-492) */
+        float buf[4096];
+        if (gs > 4096) return;
+        int64_t rem = numel - full * gs;
+        for (int64_t i = 0; i < gs; ++i) buf[i] = i < rem ? w[full * gs + i] : 0.0f;
+        e8r_encode_group(buf, gs, lut, codes + full * gs / 8, scales + full,
+                         scales32 ? scales32 + full : 0);
+    }
+}
+
+/* Decoded weight as RootE8LatticePacker.unpack produces it (lattice.py:519-533):
+ * lut.to(dtype)[code] * scales.to(dtype), the product rounded to dtype (coordinates
+ * are 0, +-1, +-2: the fp32 product is exact).  gs = padded / numel(scales). */
+OJO_API void ojo_e8r_decode(const uint8_t* codes, const uint16_t* scales, int64_t numel,
+                            int64_t gs, int out_dtype, void* out) {
+    float lut[256 * 8];
+    ojo_e8r_lut(lut);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t f = 0; f < numel; ++f) {
+        float s = ojo_f16_to_f32(scales[f / gs]);
+        if (out_dtype == 2) s = ojo_bf16_to_f32(ojo_f32_to_bf16(s));
+        float p = lut[8 * codes[f >> 3] + (f & 7)] * s;
+        if (out_dtype == 0) ((float*)out)[f] = p;
+        else if (out_dtype == 1) ((uint16_t*)out)[f] = ojo_f32_to_f16(p);
+        else ((uint16_t*)out)[f] = ojo_f32_to_bf16(p);
+    }
+}
+
+static inline double e8r_deq(const float* lut, const uint8_t* codes, const uint16_t* scales,
+                             int64_t f, int64_t gs, int w_dtype) {
+    float s = ojo_f16_to_f32(scales[f / gs]);
+    if (w_dtype == 2) s = ojo_bf16_to_f32(ojo_f32_to_bf16(s));
+    float p = lut[8 * codes[f >> 3] + (f & 7)] * s;
+    if (w_dtype == 1) p = ojo_f16_to_f32(ojo_f32_to_f16(p));
+    else if (w_dtype == 2) p = ojo_bf16_to_f32(ojo_f32_to_bf16(p));
+    return (double)p;
+}
+
+/* y = x . Wdeq^T + bias in fp64 (the reference's 1-bit forward: unpack + F.linear,
+ * lattice.py:614-624).  Flat layout: element (n, k) is flat index n*K + k. */
+OJO_API void ojo_e8r_gemm_f64(const float* x, const uint8_t* codes, const uint16_t* scales,
+                              const float* bias, double* y, int64_t M, int64_t N, int64_t K,
+                              int64_t gs, int w_dtype) {
+    float lut[256 * 8];
+    ojo_e8r_lut(lut);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t m = 0; m < M; ++m) {
+            double acc = bias ? (double)bias[n] : 0.0;
+            for (int64_t k = 0; k < K; ++k)
+                acc += (double)x[m * K + k] * e8r_deq(lut, codes, scales, n * K + k, gs, w_dtype);
+            y[m * N + n] = acc;
+        }
+    }
+}
+
+/* grad_x = grad_y . Wdeq in fp64 (the portable backward, lattice.py:684-717). */
+OJO_API void ojo_e8r_gemm_bwd_f64(const float* gy, const uint8_t* codes, const uint16_t* scales,
+                                  double* gx, int64_t M, int64_t N, int64_t K, int64_t gs,
+                                  int w_dtype) {
+    float lut[256 * 8];
+    ojo_e8r_lut(lut);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t k = 0; k < K; ++k) {
+            double acc = 0.0;
+            for (int64_t n = 0; n < N; ++n)
+                acc += (double)gy[m * N + n] * e8r_deq(lut, codes, scales, n * K + k, gs, w_dtype);
+            gx[m * K + k] = acc;
+        }
+}
+
+OJO_API void ojo_e8r_quantize8_array(const float* v, int64_t nvec, int32_t* codes) {
+    ojo_e8r_prepare();
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t i = 0; i < nvec; ++i) codes[i] = ojo_e8r_quantize8(v + 8 * i);
+}

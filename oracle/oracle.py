@@ -94,6 +94,22 @@ def lib() -> ctypes.CDLL:
         L.ojo_e8b_gemm_f64.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
         L.ojo_e8b_gemm_bwd_f64.restype = None
         L.ojo_e8b_gemm_bwd_f64.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
+        L.ojo_e8r_lut.restype = None
+        L.ojo_e8r_lut.argtypes = [_P]
+        L.ojo_e8r_quantize8.restype = ctypes.c_int32
+        L.ojo_e8r_quantize8.argtypes = [_P]
+        L.ojo_e8r_quantize8_array.restype = None
+        L.ojo_e8r_quantize8_array.argtypes = [_P, _I64, _P]
+        L.ojo_e8r_row_sum.restype = ctypes.c_float
+        L.ojo_e8r_row_sum.argtypes = [_P, _I64]
+        L.ojo_e8r_encode.restype = None
+        L.ojo_e8r_encode.argtypes = [_P, _I64, _I64, _P, _P, _P, ctypes.c_int]
+        L.ojo_e8r_decode.restype = None
+        L.ojo_e8r_decode.argtypes = [_P, _P, _I64, _I64, ctypes.c_int, _P]
+        L.ojo_e8r_gemm_f64.restype = None
+        L.ojo_e8r_gemm_f64.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
+        L.ojo_e8r_gemm_bwd_f64.restype = None
+        L.ojo_e8r_gemm_bwd_f64.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -375,4 +391,86 @@ def ref_e8_fused_bwd_dx(gy: np.ndarray, packed: np.ndarray, scales_f32: np.ndarr
     s = np.ascontiguousarray(scales_f32, dtype=np.float32)
     ref().ojr_e8_bwd_dx_f32(_ptr(gy), _ptr(np.ascontiguousarray(packed)), _ptr(s), _ptr(gx),
                             M, K, N, int(group_size))
+    return gx
+
+
+# --------------------------------------------------------------------------- 1-bit Root E8
+
+def e8r_effective_gs(gs: int) -> int:
+    """RootE8LatticePacker.pack's silent coercion (lattice.py:485-486)."""
+    return 8 if (gs <= 0 or gs % 8 != 0) else int(gs)
+
+
+def e8r_lut() -> np.ndarray:
+    """The 256 x 8 table of lattice.py:436-456 (x2), fp32."""
+    out = np.empty(256 * 8, dtype=np.float32)
+    lib().ojo_e8r_lut(_ptr(out))
+    return out.reshape(256, 8)
+
+
+def e8r_quantize8_many(v: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1, 8)
+    codes = np.empty(v.shape[0], dtype=np.int32)
+    lib().ojo_e8r_quantize8_array(_ptr(v), v.shape[0], _ptr(codes))
+    return codes
+
+
+def e8r_row_sum(x: np.ndarray) -> float:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    return float(lib().ojo_e8r_row_sum(_ptr(x), x.size))
+
+
+def e8r_encode(w: np.ndarray, group_size: int = 32, nthreads: int = 0
+               ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """RootE8LatticePacker.pack on the flattened fp32 values of ``w``.
+
+    Returns (codes uint8 [padded/8], scales fp16 bits uint16 [padded/gs], scales32 fp32
+    [padded/gs]) with gs coerced as the reference coerces it."""
+    gs = e8r_effective_gs(group_size)
+    if gs > 4096:
+        raise ValueError("oracle group size limit is 4096")
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    p = padded(w.size, gs)
+    codes = np.empty(p // 8, dtype=np.uint8)
+    scales = np.empty(p // gs, dtype=np.uint16)
+    scales32 = np.empty(p // gs, dtype=np.float32)
+    lib().ojo_e8r_encode(_ptr(w), w.size, gs, _ptr(codes), _ptr(scales), _ptr(scales32),
+                         int(nthreads))
+    return codes, scales, scales32
+
+
+def e8r_decode(codes: np.ndarray, scales: np.ndarray, numel: int, group_size: int,
+               dtype: int = DT_F32) -> np.ndarray:
+    """RootE8LatticePacker.unpack: fp32 values, or fp16 / bf16 bit patterns."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint16)
+    out = np.empty(numel, dtype=np.float32 if dtype == DT_F32 else np.uint16)
+    lib().ojo_e8r_decode(_ptr(codes), _ptr(scales), numel, int(group_size), int(dtype),
+                         _ptr(out))
+    return out
+
+
+def e8r_gemm_f64(x: np.ndarray, codes: np.ndarray, scales: np.ndarray,
+                 bias: Optional[np.ndarray], N: int, K: int, group_size: int,
+                 w_dtype: int = DT_F32) -> np.ndarray:
+    """fp64-accumulated x @ Wdeq^T + bias, Wdeq by the 1-bit dtype rule."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
+    M = x.shape[0]
+    y = np.empty((M, N), dtype=np.float64)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().ojo_e8r_gemm_f64(_ptr(x), _ptr(np.ascontiguousarray(codes)),
+                           _ptr(np.ascontiguousarray(scales, dtype=np.uint16)),
+                           None if b is None else _ptr(b), _ptr(y), M, N, K,
+                           int(group_size), int(w_dtype))
+    return y
+
+
+def e8r_gemm_bwd_f64(gy: np.ndarray, codes: np.ndarray, scales: np.ndarray, N: int, K: int,
+                     group_size: int, w_dtype: int = DT_F32) -> np.ndarray:
+    gy = np.ascontiguousarray(gy, dtype=np.float32).reshape(-1, N)
+    M = gy.shape[0]
+    gx = np.empty((M, K), dtype=np.float64)
+    lib().ojo_e8r_gemm_bwd_f64(_ptr(gy), _ptr(np.ascontiguousarray(codes)),
+                               _ptr(np.ascontiguousarray(scales, dtype=np.uint16)), _ptr(gx),
+                               M, N, K, int(group_size), int(w_dtype))
     return gx

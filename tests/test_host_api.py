@@ -22,7 +22,7 @@ HEADER = os.path.join(ROOT, "include", "ojasx_e8t.h")
 
 def _declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(ojx_e8t?_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ojx_e8[tr]?_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_exports():
@@ -69,6 +69,16 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert lib.ojx_e8_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None) == -1
     assert lib.ojx_e8_encode(None, 0, 0, 8, None, None, None) == 0
     assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None) == 0
+    # 1-bit Root E8: group sizes are multiples of 8 everywhere (the packer coerces first)
+    assert lib.ojx_e8r_encode(None, 0, 64, 12, None, None, None) == -2
+    assert b"multiple of 8" in lib.ojx_e8t_last_error()
+    assert lib.ojx_e8r_encode(None, 0, -1, 8, None, None, None) == -1
+    assert lib.ojx_e8r_decode(None, None, 16, 4, 0, None, None) == -2
+    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 1, 4, 8, 4, 0, None) == -2
+    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 1, 4, 8, 8, 9, None) == -3
+    assert lib.ojx_e8r_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None) == -1
+    assert lib.ojx_e8r_encode(None, 0, 0, 8, None, None, None) == 0
+    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -99,16 +109,46 @@ def test_layer_state_dict_keys_match_reference():
     assert set(layer.state_dict()) == {"packed_weight", "block_scales", "bias", "lora_A", "lora_B"}
 
 
-def test_root_e8_bitrate_raises():
-    # bitrate 1.0 (RootE8LatticePacker) is not implemented; every other bitrate but 1.5
-    # selects the 2-bit packer, as lattice.py:536-541 does
-    with pytest.raises(NotImplementedError):
-        ojasx_amd.E8LatticeLinear(64, 32, bitrate=1.0)
-    with pytest.raises(NotImplementedError):
-        ojasx_amd.E8LatticeLinear.from_linear(nn.Linear(32, 32), bitrate=1.0)
+def test_bitrate_routing():
+    # lattice.py:536-541: 1.0 -> RootE8LatticePacker, 1.5 -> ternary, anything else -> 2-bit
+    assert ojasx_amd._get_packer_for_bitrate(1.0) is ojasx_amd.RootE8LatticePacker
     assert ojasx_amd._get_packer_for_bitrate(2.0) is ojasx_amd.E8LatticePacker
     assert ojasx_amd._get_packer_for_bitrate(3.0) is ojasx_amd.E8LatticePacker
     assert ojasx_amd._get_packer_for_bitrate(1.5) is ojasx_amd.TernaryE8LatticePacker
+
+
+@pytest.mark.parametrize("gs,eff", [(8, 8), (4, 8), (12, 8), (16, 16), (32, 32), (40, 40)])
+def test_1bit_layer_buffer_shapes_and_group_coercion(gs, eff):
+    # lattice.py:756-767 (1.0 branch): group >= 8 and a multiple of 8, else 8; 1 byte / 8
+    layer = ojasx_amd.E8LatticeLinear(128, 96, rank=2, group_size=gs, bitrate=1.0)
+    assert layer.group_size == eff
+    total = 128 * 96
+    padded = total + ((-total) % eff)
+    assert layer.packed_weight.shape == (padded // 8,)
+    assert layer.block_scales.shape == (padded // eff,)
+
+
+def test_root_e8_lut_matches_reference_construction():
+    # the table as lattice.py:436-456 builds it (loops and itertools.product), scaled by 2
+    import itertools
+    pts = []
+    for i in range(8):
+        for j in range(i + 1, 8):
+            for s1 in (-1.0, 1.0):
+                for s2 in (-1.0, 1.0):
+                    vec = [0.0] * 8
+                    vec[i], vec[j] = s1, s2
+                    pts.append(vec)
+    for signs in itertools.product((-0.5, 0.5), repeat=8):
+        if sum(1 for s in signs if s < 0) % 2 == 0:
+            pts.append(list(signs))
+    for i in range(8):
+        for s in (-1.0, 1.0):
+            vec = [0.0] * 8
+            vec[i] = s
+            pts.append(vec)
+    ref = torch.tensor(pts, dtype=torch.float32) * 2.0
+    assert torch.equal(ojasx_amd._get_root_e8_lut(), ref)
 
 
 @pytest.mark.parametrize("gs,eff", [(8, 8), (4, 8), (12, 8), (16, 16), (32, 32), (24, 24)])
