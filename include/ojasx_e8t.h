@@ -155,6 +155,19 @@ int ojx_e8r_gemm_bwd_dx(const void* grad_y, const uint8_t* codes, const uint16_t
                         void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
                         void* stream);
 
+/* ---------------------------------------------------------------- QAT helpers
+ *
+ * Conway-Sloane nearest point of the E8 lattice for nvec contiguous 8-vectors, as
+ * conway_sloane_e8_project's torch path computes it (ojasx2/math/lattice.py:162-203;
+ * the reference's native CPU kernel, ojasx_math_core.hpp:385-425, rounds halves away from
+ * zero instead).  x and out are fp32 (f64 = 0) or fp64 (f64 = 1). */
+int ojx_e8_cs_project(const void* x, int f64, int64_t nvec, void* out, void* stream);
+
+/* Forward of the QAT straight-through quantizer _E8STEFunction (lattice.py:853-865) on fp32
+ * weights: per flat 8-vector (zero padded) s = torch.norm/sqrt(8) + 1e-8, out =
+ * project(w / s) * s. */
+int ojx_e8_ste_quantize(const float* w, int64_t numel, float* out, void* stream);
+
 /* ---------------------------------------------------------------- grouped decode GEMV
  *
  * One launch runs the decode GEMV (batch M <= 16) of several independent linears: a

@@ -427,4 +427,27 @@ __attribute__((visibility("default"))) int ojx_e8r_gemm_bwd_dx(const void* grad_
                 "e8r gemm_bwd_dx launch");
 }
 
+// ---------------------------------------------------------------- QAT helpers
+
+__attribute__((visibility("default"))) int ojx_e8_cs_project(const void* x, int f64,
+                                                             int64_t nvec, void* out,
+                                                             void* stream) {
+    if (nvec < 0) return fail(OJX_EINVAL, "negative vector count %lld", (long long)nvec);
+    if (nvec == 0) return OJX_OK;
+    if (!x || !out) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_cs_project(x, f64 != 0, nvec, out, (hipStream_t)stream),
+                "e8 cs_project launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8_ste_quantize(const float* w, int64_t numel,
+                                                               float* out, void* stream) {
+    if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);
+    if (numel == 0) return OJX_OK;
+    if (!w || !out) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_ste_quantize(w, numel, out, (hipStream_t)stream),
+                "e8 ste_quantize launch");
+}
+
 }  // extern "C"

@@ -24,6 +24,12 @@ hipError_t launch_encode1(const void* w, int wdt, int64_t numel, int64_t gs, uin
 hipError_t launch_decode1(const uint8_t* codes, const uint16_t* scales, int64_t numel,
                           int64_t gs, int odt, void* out, hipStream_t stream);
 
+// Conway-Sloane E8 projection (fp32 or fp64, nvec 8-vectors) and the QAT straight-through
+// quantizer (fp32 weights).
+hipError_t launch_cs_project(const void* x, bool f64, int64_t nvec, void* out,
+                             hipStream_t stream);
+hipError_t launch_ste_quantize(const float* w, int64_t numel, float* out, hipStream_t stream);
+
 // 2-bit decode GEMV (M <= 4, bf16/fp16, K % 1024 == 0, gs in {8, 16, 32, 64}, 16-byte
 // aligned buffers).
 bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scales,

@@ -10,6 +10,9 @@ include/ojasx_e8t.h) registered as ``torch.ops.ojasx_e8t.*``.
 from . import grouped, ops
 from .lattice import (
     E8LatticeLinear,
+    E8QuantizationAwareLinear,
+    _E8STEFunction,
+    conway_sloane_e8_project,
     E8LatticePacker,
     RootE8LatticePacker,
     TernaryE8LatticePacker,
@@ -28,6 +31,9 @@ __all__ = [
     "grouped",
     "ops",
     "E8LatticeLinear",
+    "E8QuantizationAwareLinear",
+    "_E8STEFunction",
+    "conway_sloane_e8_project",
     "E8LatticePacker",
     "RootE8LatticePacker",
     "TernaryE8LatticePacker",

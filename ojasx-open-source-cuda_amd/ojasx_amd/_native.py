@@ -36,6 +36,8 @@ EXPORTS = (
     "ojx_e8r_decode",
     "ojx_e8r_gemm_fwd",
     "ojx_e8r_gemm_bwd_dx",
+    "ojx_e8_cs_project",
+    "ojx_e8_ste_quantize",
 )
 
 
@@ -107,6 +109,10 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8r_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
             L.ojx_e8r_gemm_bwd_dx.restype = _INT
             L.ojx_e8r_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8_cs_project.restype = _INT
+            L.ojx_e8_cs_project.argtypes = [_P, _INT, _I64, _P, _P]
+            L.ojx_e8_ste_quantize.restype = _INT
+            L.ojx_e8_ste_quantize.argtypes = [_P, _I64, _P, _P]
             _lib = L
     return _lib
 

@@ -8,6 +8,9 @@ operation on the path running in the HIP kernels behind ``ojasx_amd.ops``:
 this module                         reference (ojasx2/math/lattice.py)
 =================================  ==========================================
 ``fwht_block32``                    :91-102
+``conway_sloane_e8_project``        :162-203   -> ops.cs_project
+``_E8STEFunction``                  :853-869   -> ops.ste_quantize
+``E8QuantizationAwareLinear``       :872-898
 ``_get_ternary_e8_luts``            :292-332
 ``TernaryE8LatticePacker.pack``     :338-384   -> ops.encode (one HIP kernel)
 ``TernaryE8LatticePacker.unpack``   :386-419   -> ops.decode
@@ -36,6 +39,7 @@ from typing import Dict, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import ops
 
@@ -45,6 +49,9 @@ __all__ = [
     "E8LatticePacker",
     "RootE8LatticePacker",
     "_FusedE8GEMMFunction",
+    "conway_sloane_e8_project",
+    "_E8STEFunction",
+    "E8QuantizationAwareLinear",
     "E8LatticeLinear",
     "pack_model_e8",
 ]
@@ -69,6 +76,68 @@ def fwht_block32(x: torch.Tensor) -> torch.Tensor:
         a, b = v[:, :, 0, :], v[:, :, 1, :]
         h = torch.stack([a + b, a - b], dim=2).reshape(-1, 32)
     return (h * _HADAMARD_NORM).reshape(shape)
+
+
+def conway_sloane_e8_project(x: torch.Tensor, prefer_native: bool = True) -> torch.Tensor:
+    """Snaps every 8-vector of x to the nearest point of E8 = D8 U (D8 + 1/2) (lattice.py:162-203).
+
+    One HIP kernel, with the arithmetic of the reference's torch path (round half to even;
+    an odd sum moves the first coordinate with the largest rounding error towards x; D8
+    wins ties of the squared distances).  ``prefer_native`` selected the reference's CPU
+    kernel, which rounds halves away from zero; it is accepted and ignored.  fp32 and fp64
+    tensors; CPU tensors are processed on the current GPU and returned on the CPU."""
+    del prefer_native
+    if x.shape[-1] != 8:
+        raise ValueError(f"Last dimension must be 8 for E8 lattice (got {x.shape[-1]}).")
+    if x.numel() == 0:
+        return x.clone()
+    out = ops.cs_project(_on_gpu(x))
+    return out.to(x.device) if x.device.type != "cuda" else out
+
+
+class _E8STEFunction(torch.autograd.Function):
+    """Straight-through E8 weight quantizer (lattice.py:853-869): the forward snaps each flat
+    8-vector, scaled by its norm / sqrt(8) + 1e-8, to E8 (one HIP kernel, fp32 weights);
+    the backward passes the gradient through unchanged."""
+
+    @staticmethod
+    def forward(ctx, w: torch.Tensor) -> torch.Tensor:
+        out = ops.ste_quantize(_on_gpu(w))
+        return out.to(w.device) if w.device.type != "cuda" else out
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor) -> torch.Tensor:
+        return grad_output
+
+
+class E8QuantizationAwareLinear(nn.Module):
+    """nn.Linear whose weight passes through the E8 straight-through quantizer in every
+    forward (lattice.py:872-898)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 device: Optional[torch.device] = None, dtype: Optional[torch.dtype] = None
+                 ) -> None:
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, device=device,
+                                               dtype=dtype))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, device=device, dtype=dtype))
+        else:
+            self.register_parameter("bias", None)
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if self.bias is not None:
+            fan_in, _ = nn.init._calculate_fan_in_and_fan_out(self.weight)
+            bound = 1 / math.sqrt(fan_in) if fan_in > 0 else 0
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        w_q = _E8STEFunction.apply(self.weight)
+        return F.linear(x, w_q, self.bias)
 
 
 _DEVICE_TERNARY_LUTS: Dict[Tuple[str, Optional[int]], Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}

@@ -617,3 +617,48 @@ def _linear1_backward(ctx, grad_y):
 
 
 e8r_linear.register_autograd(_linear1_backward, setup_context=_linear_setup_context)
+
+
+# --------------------------------------------------------------------------- QAT helpers
+
+@torch.library.custom_op(f"{_NS}::cs_project", mutates_args=())
+def cs_project(x: torch.Tensor) -> torch.Tensor:
+    """Conway-Sloane nearest E8 point of every 8-vector of x (fp32 or fp64, last dim 8),
+    as conway_sloane_e8_project's torch path computes it (lattice.py:180-203)."""
+    dev = N.require_device(x)
+    if x.dtype not in (torch.float32, torch.float64):
+        raise RuntimeError(f"cs_project supports float32 and float64 tensors (got {x.dtype})")
+    if x.shape[-1] != 8:
+        raise RuntimeError(f"last dimension must be 8 (got {x.shape[-1]})")
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8_cs_project(N.ptr(xc), int(x.dtype == torch.float64),
+                                          xc.numel() // 8, N.ptr(out), N.stream_handle(dev)),
+                "e8 cs_project")
+    return out
+
+
+@cs_project.register_fake
+def _(x):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op(f"{_NS}::ste_quantize", mutates_args=())
+def ste_quantize(w: torch.Tensor) -> torch.Tensor:
+    """Forward of _E8STEFunction (lattice.py:853-865) on fp32 weights."""
+    dev = N.require_device(w)
+    if w.dtype != torch.float32:
+        raise RuntimeError(f"ste_quantize supports float32 weights (got {w.dtype})")
+    wc = w.contiguous()
+    out = torch.empty_like(wc)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_e8_ste_quantize(N.ptr(wc), wc.numel(), N.ptr(out),
+                                            N.stream_handle(dev)),
+                "e8 ste_quantize")
+    return out
+
+
+@ste_quantize.register_fake
+def _(w):
+    return torch.empty_like(w)

@@ -762,3 +762,68 @@ OJO_API void ojo_e8r_quantize8_array(const float* v, int64_t nvec, int32_t* code
 #endif
     for (int64_t i = 0; i < nvec; ++i) codes[i] = ojo_e8r_quantize8(v + 8 * i);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Conway-Sloane E8 projection and the QAT straight-through quantizer           */
+/* ------------------------------------------------------------------------- */
+
+/* conway_sloane_e8_project as its torch path computes it (lattice.py:180-203), for one
+ * 8-vector, in fp32 (OJO_CS_T float) and fp64: the nearest point of D8 (round half to
+ * even, parity fixed at the first largest rounding error, towards x) and of D8 + 1/2
+ * (the same on x - 1/2, plus 1/2), the closer one by the sequential sum of squared
+ * differences, D8 on ties. */
+#define OJO_CS_DEFINE(NAME, T, RINT, FABS)                                              \
+    static void NAME##_candidate(const T* x, T shift, T out[8]) {                       \
+        T f[8], xs[8];                                                                  \
+        long sum = 0;                                                                   \
+        int worst = 0;                                                                  \
+        T werr = 0;                                                                     \
+        for (int i = 0; i < 8; ++i) {                                                   \
+            xs[i] = x[i] - shift;                                                       \
+            f[i] = RINT(xs[i]);                                                         \
+            sum += (long)f[i];                                                          \
+            T err = FABS(xs[i] - f[i]);                                                 \
+            if (i == 0 || err > werr) { werr = err; worst = i; }                        \
+        }                                                                               \
+        if (sum % 2 != 0) {                                                             \
+            T d = xs[worst] - f[worst];                                                 \
+            f[worst] = f[worst] + ((d < 0) ? (T)-1 : (T)1);                             \
+        }                                                                               \
+        for (int i = 0; i < 8; ++i) out[i] = f[i] + shift;                              \
+    }                                                                                   \
+    OJO_API void NAME(const T* x, T* out, int64_t nvec) {                               \
+        for (int64_t b = 0; b < nvec; ++b) {                                            \
+            const T* v = x + 8 * b;                                                     \
+            T c1[8], c2[8];                                                             \
+            NAME##_candidate(v, (T)0, c1);                                              \
+            NAME##_candidate(v, (T)0.5, c2);                                            \
+            T d1 = 0, d2 = 0;                                                           \
+            for (int i = 0; i < 8; ++i) {                                               \
+                T a = v[i] - c1[i], b2 = v[i] - c2[i];                                  \
+                T a2 = a * a, bb = b2 * b2;                                             \
+                d1 = d1 + a2;                                                           \
+                d2 = d2 + bb;                                                           \
+            }                                                                           \
+            const T* ch = (d1 <= d2) ? c1 : c2;                                         \
+            for (int i = 0; i < 8; ++i) out[8 * b + i] = ch[i];                         \
+        }                                                                               \
+    }
+
+OJO_CS_DEFINE(ojo_e8_cs_project_f32, float, rintf, fabsf)
+OJO_CS_DEFINE(ojo_e8_cs_project_f64, double, rint, fabs)
+
+/* _E8STEFunction.forward (lattice.py:853-865) on fp32 weights: flat, zero padded to a
+ * multiple of 8; per 8-vector s = torch.norm(w8)/sqrt(8) + 1e-8 (the CPU norm order),
+ * out = project(w8 / s) * s; the first numel values. */
+OJO_API void ojo_e8_ste_quantize_f32(const float* w, int64_t numel, float* out) {
+    int64_t nvec = (numel + 7) / 8;
+    for (int64_t b = 0; b < nvec; ++b) {
+        float x[8], v[8], p[8];
+        for (int i = 0; i < 8; ++i) x[i] = (8 * b + i < numel) ? w[8 * b + i] : 0.0f;
+        float s = ojo_e8t_group_scale(x, 8);
+        for (int i = 0; i < 8; ++i) v[i] = x[i] / s;
+        ojo_e8_cs_project_f32(v, p, 1);
+        for (int i = 0; i < 8; ++i)
+            if (8 * b + i < numel) out[8 * b + i] = p[i] * s;
+    }
+}

@@ -110,6 +110,12 @@ def lib() -> ctypes.CDLL:
         L.ojo_e8r_gemm_f64.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
         L.ojo_e8r_gemm_bwd_f64.restype = None
         L.ojo_e8r_gemm_bwd_f64.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int]
+        L.ojo_e8_cs_project_f32.restype = None
+        L.ojo_e8_cs_project_f32.argtypes = [_P, _P, _I64]
+        L.ojo_e8_cs_project_f64.restype = None
+        L.ojo_e8_cs_project_f64.argtypes = [_P, _P, _I64]
+        L.ojo_e8_ste_quantize_f32.restype = None
+        L.ojo_e8_ste_quantize_f32.argtypes = [_P, _I64, _P]
         _lib = L
     return _lib
 
@@ -474,3 +480,26 @@ def e8r_gemm_bwd_f64(gy: np.ndarray, codes: np.ndarray, scales: np.ndarray, N: i
                                _ptr(np.ascontiguousarray(scales, dtype=np.uint16)), _ptr(gx),
                                M, N, K, int(group_size), int(w_dtype))
     return gx
+
+
+# --------------------------------------------------------------------------- Conway-Sloane / STE
+
+def cs_project(x: np.ndarray) -> np.ndarray:
+    """conway_sloane_e8_project's torch path (lattice.py:180-203) over [..., 8], fp32 or fp64."""
+    if x.dtype == np.float64:
+        a = np.ascontiguousarray(x)
+        out = np.empty_like(a)
+        lib().ojo_e8_cs_project_f64(_ptr(a), _ptr(out), a.size // 8)
+    else:
+        a = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty_like(a)
+        lib().ojo_e8_cs_project_f32(_ptr(a), _ptr(out), a.size // 8)
+    return out
+
+
+def ste_quantize(w: np.ndarray) -> np.ndarray:
+    """_E8STEFunction.forward (lattice.py:853-865) on fp32 weights."""
+    a = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().ojo_e8_ste_quantize_f32(_ptr(a), a.size, _ptr(out))
+    return out
