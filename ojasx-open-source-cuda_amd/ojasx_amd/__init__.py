@@ -23,7 +23,7 @@ from .lattice import (
     fwht_block32,
     pack_model_e8,
 )
-from .streaming import pack_weight_rowwise
+from .streaming import StreamingE8LoadReport, load_hf_checkpoint_e8, pack_weight_rowwise
 
 __version__ = "0.1.0"
 
@@ -44,4 +44,6 @@ __all__ = [
     "fwht_block32",
     "pack_model_e8",
     "pack_weight_rowwise",
+    "load_hf_checkpoint_e8",
+    "StreamingE8LoadReport",
 ]

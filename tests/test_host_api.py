@@ -221,3 +221,17 @@ def test_ctypes_signatures_match_header_arity():
         m = re.search(name + r"\s*\(([^)]*)\)", text)
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(getattr(lib, name).argtypes) == len(params), name
+
+
+def test_checkpoint_loader_argument_errors(tmp_path):
+    # streaming_e8.py:286-298: argument checks come before any file or device access
+    with pytest.raises(ValueError, match="row_block must be positive"):
+        ojasx_amd.load_hf_checkpoint_e8(str(tmp_path), row_block=0)
+    with pytest.raises(ValueError, match="lora_rank must be non-negative"):
+        ojasx_amd.load_hf_checkpoint_e8(str(tmp_path), lora_rank=-1)
+    with pytest.raises(ValueError, match="Unsupported E8 bitrate"):
+        ojasx_amd.load_hf_checkpoint_e8(str(tmp_path), bitrate=3.0)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ojasx_amd.load_hf_checkpoint_e8(str(tmp_path), group_size=48)
+    with pytest.raises(NotADirectoryError):
+        ojasx_amd.load_hf_checkpoint_e8(str(tmp_path / "absent"))
