@@ -126,17 +126,20 @@ __attribute__((visibility("default"))) int ojx_e8t_decode(const uint8_t* packed,
 
 // The prefill MFMA GEMM with its tile configuration and K split; the split's fp32 partial
 // sums live in the per-stream workspace (none while the stream is captured: unsplit).
+// bwd: the backward dX (output [M, K], reduction over N).
 static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                               const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                              int64_t gs, int dtype, hipStream_t s, int fmt) {
-    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, N, K);
+                              int64_t gs, int dtype, hipStream_t s, int fmt, bool bwd = false) {
+    const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
+    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, out_cols, red);
     float* part = nullptr;
     if (c.splits > 1) {
         part = static_cast<float*>(ojx::stream_workspace(
-            s, (size_t)c.splits * (size_t)ojx::split_stride(M, N) * sizeof(float)));
+            s, (size_t)c.splits * (size_t)ojx::split_stride(M, out_cols) * sizeof(float)));
         if (!part) c.splits = 1;  // capturing, or no memory: the unsplit kernel
     }
-    return ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s, gs, fmt);
+    return ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s, gs, fmt,
+                                 bwd);
 }
 
 __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed,
@@ -263,6 +266,11 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_bwd_dx(const void* grad_
     if (M == 0 || K == 0) return OJX_OK;
     if (int r = check_device()) return r;
     hipStream_t s = (hipStream_t)stream;
+    if (N > 0 && ojx::gemm_mfma_supported(grad_y, packed, scales, M, N, K, gs, dtype,
+                                          ojx::kFmtTernary, true))
+        return done(launch_mfma(grad_y, packed, scales, nullptr, grad_x, M, N, K, gs, dtype, s,
+                                ojx::kFmtTernary, true),
+                    "e8t gemm_mfma bwd launch");
     return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype, s),
                 "e8t gemm_bwd_dx launch");
 }
@@ -347,8 +355,14 @@ __attribute__((visibility("default"))) int ojx_e8_gemm_bwd_dx(const void* grad_y
     if (int r = check_gemm2_args(grad_y, packed, scales, grad_x, M, K, N, gs, dtype)) return r;
     if (M == 0 || K == 0) return OJX_OK;
     if (int r = check_device()) return r;
-    return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype,
-                                             (hipStream_t)stream, ojx::kFmt2Bit),
+    hipStream_t s = (hipStream_t)stream;
+    if (N > 0 && ojx::gemm_mfma_supported(grad_y, packed, scales, M, N, K, gs, dtype,
+                                          ojx::kFmt2Bit, true))
+        return done(launch_mfma(grad_y, packed, scales, nullptr, grad_x, M, N, K, gs, dtype, s,
+                                ojx::kFmt2Bit, true),
+                    "e8 gemm_mfma bwd launch");
+    return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype, s,
+                                             ojx::kFmt2Bit),
                 "e8 gemm_bwd_dx launch");
 }
 
@@ -422,8 +436,14 @@ __attribute__((visibility("default"))) int ojx_e8r_gemm_bwd_dx(const void* grad_
     if (int r = check_gemm1_args(grad_y, codes, scales, grad_x, M, K, N, gs, dtype)) return r;
     if (M == 0 || K == 0) return OJX_OK;
     if (int r = check_device()) return r;
-    return done(ojx::launch_gemm_generic_bwd(grad_y, codes, scales, grad_x, M, N, K, gs, dtype,
-                                             (hipStream_t)stream, ojx::kFmtRoot),
+    hipStream_t s = (hipStream_t)stream;
+    if (N > 0 && ojx::gemm_mfma_supported(grad_y, codes, scales, M, N, K, gs, dtype,
+                                          ojx::kFmtRoot, true))
+        return done(launch_mfma(grad_y, codes, scales, nullptr, grad_x, M, N, K, gs, dtype, s,
+                                ojx::kFmtRoot, true),
+                    "e8r gemm_mfma bwd launch");
+    return done(ojx::launch_gemm_generic_bwd(grad_y, codes, scales, grad_x, M, N, K, gs, dtype, s,
+                                             ojx::kFmtRoot),
                 "e8r gemm_bwd_dx launch");
 }
 

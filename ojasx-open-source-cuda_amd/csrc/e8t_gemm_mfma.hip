@@ -162,6 +162,7 @@ __device__ __forceinline__ void lut_reads_half(const RowCodes& rc, const char* l
 // Ternary E8: 8 codes (12 bytes) of the whole row per step; the thread expands 4 of them.
 template <int DT>
 struct TernaryRowDecoder {
+    static constexpr int kLoads = 2;  // loads issued by load()
     RowCodes rc;
     uint2 ml[4], mh[4];
     uint32_t sw;
@@ -180,6 +181,9 @@ struct TernaryRowDecoder {
     }
     __device__ __forceinline__ uint4 piece(int p) const {
         return make_uint4(ml[p].x & sw, ml[p].y & sw, mh[p].x & sw, mh[p].y & sw);
+    }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t wrow, int hf) const {
+        *reinterpret_cast<uint4*>(tile + swz(wrow, 4u * hf + p)) = piece(p);
     }
 };
 
@@ -222,6 +226,7 @@ __device__ __forceinline__ uint2 values2(uint32_t s16) {
 template <int DT, int GS>
 struct Bit2RowDecoder {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "2-bit group size 8..64");
+    static constexpr int kLoads = 2;
     uint2 c;          // the half-row's 32 codes (8 bytes)
     uint2 sc;         // its scales: GS 8: four, GS 16: two, GS 32/64: one (fp16 bits)
     uint2 sel[4][2];  // selector words of pieces 0..3
@@ -271,6 +276,9 @@ struct Bit2RowDecoder {
                           __builtin_amdgcn_perm(s0, s1, sel[p][1].x),
                           __builtin_amdgcn_perm(s0, s1, sel[p][1].y));
     }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t wrow, int hf) const {
+        *reinterpret_cast<uint4*>(tile + swz(wrow, 4u * hf + p)) = piece(p);
+    }
 };
 
 // 1-bit Root E8 (RootE8LatticePacker, lattice.py:426-533): one code byte per 8 weights,
@@ -301,6 +309,7 @@ __device__ __forceinline__ uint2 values1(uint32_t s16) {
 template <int DT, int GS>
 struct RootRowDecoder {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "1-bit group size 8..64");
+    static constexpr int kLoads = 2;
     uint32_t c;       // the half-row's 4 codes (32 weights)
     uint2 sc;         // its scales, as Bit2RowDecoder
     uint4 sel[4];     // selector words of pieces 0..3
@@ -343,6 +352,164 @@ struct RootRowDecoder {
                           __builtin_amdgcn_perm(s0, s1, sel[p].z),
                           __builtin_amdgcn_perm(s0, s1, sel[p].w));
     }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t wrow, int hf) const {
+        *reinterpret_cast<uint4*>(tile + swz(wrow, 4u * hf + p)) = piece(p);
+    }
+};
+
+// ---- backward-dX decoders: gx[M, K] = gy[M, N] . W[N, K] runs the same MFMA loop with the
+// weight tile transposed: tile row = output column k, piece = 8 consecutive reduction rows
+// n.  Thread pair (2b, 2b + 1) owns the 8 x 8 block b of the step's 64 x BN slice: rows
+// n = 8 (b % 8) + 4 h .. + 3 (h = the thread's parity), columns k = 8 (b / 8) .. + 7.  Each
+// thread expands the code of its 4 rows into 4 rows of 8 weights (dwords of k pairs), then
+// v_perm_b32 transposes them into 8 columns of 4 weights (dwords of n pairs) written as
+// 8-byte halves of the tile's pieces.
+
+struct BwdBlock {
+    uint32_t rows;   // 8 (b % 8) + 4 h: first of the thread's 4 weight rows in the step
+    uint32_t col;    // 8 (b / 8): first tile column (output k) of the block
+    uint32_t piece;  // b % 8
+    uint32_t hoff;   // 8 h: byte offset inside the piece
+};
+
+__device__ __forceinline__ BwdBlock bwd_block(int tid) {
+    const uint32_t b = (uint32_t)tid >> 1;
+    BwdBlock k;
+    k.piece = b & 7u;
+    k.rows = 8u * k.piece + 4u * ((uint32_t)tid & 1u);
+    k.col = 8u * (b >> 3);
+    k.hoff = 8u * ((uint32_t)tid & 1u);
+    return k;
+}
+
+// Writes columns 2p and 2p + 1 of a thread's 4 x 8 block (r[row][dword of k pairs]) as
+// dwords of n pairs.
+__device__ __forceinline__ void bwd_store_cols(const uint32_t (&r)[4][4], int p, char* tile,
+                                               const BwdBlock& bk) {
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+        const int c = 2 * p + c2;
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t d0 = __builtin_amdgcn_perm(r[1][c >> 1], r[0][c >> 1], sel);
+        const uint32_t d1 = __builtin_amdgcn_perm(r[3][c >> 1], r[2][c >> 1], sel);
+        *reinterpret_cast<uint2*>(tile + swz(bk.col + (uint32_t)c, bk.piece) + bk.hoff) =
+            make_uint2(d0, d1);
+    }
+}
+
+// One scale in the activation dtype as the AND word s | s << 16 | 0x80008000 (ternary masks).
+template <int DT>
+__device__ __forceinline__ uint32_t scale_word1(uint32_t s16) {
+    uint32_t p;
+    if constexpr (DT == kBF16) p = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f16_bits_to_f32(s16 & 0xFFFFu));
+    else p = s16 & 0xFFFFu;
+    return (p | (p << 16)) | 0x80008000u;
+}
+
+template <int DT>
+struct TernaryBwdDecoder {
+    static constexpr int kLoads = 12;
+    uint32_t lo[4], hi[4], sc[4];  // the code's two bytes and the scale of each row
+    uint32_t r[4][4];
+    const char* lut;
+    uint32_t slot, odd;            // odd: the code is the second of its 3-byte pair
+    uint32_t vo_code[4], vo_scale[4], rowbytes, srowbytes;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    BwdBlock bk;
+    __device__ __forceinline__ void load(int64_t n0) {
+        const int so = uniform_offset(n0 * rowbytes), ss = uniform_offset(n0 * srowbytes);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            lo[q] = __builtin_amdgcn_raw_buffer_load_b8(pr, vo_code[q], so, 0);
+            hi[q] = __builtin_amdgcn_raw_buffer_load_b8(pr, vo_code[q] + 1u, so, 0);
+            sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
+        }
+    }
+    __device__ __forceinline__ void prep() {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t code = odd ? ((lo[q] >> 4) | (hi[q] << 4)) : (lo[q] | ((hi[q] & 0xFu) << 8));
+            const uint32_t z = (code << kCodeShift) | slot;
+            const uint32_t h = __umulhi(z, kHiMagic);
+            const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+            const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+            const uint32_t sw = scale_word1<DT>(sc[q]);
+            r[q][0] = ml.x & sw;
+            r[q][1] = ml.y & sw;
+            r[q][2] = mh.x & sw;
+            r[q][3] = mh.y & sw;
+        }
+    }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
+        bwd_store_cols(r, p, tile, bk);
+    }
+};
+
+template <int DT, int GS>
+struct Bit2BwdDecoder {
+    static constexpr int kLoads = 8;
+    uint32_t cw[4], sc[4];  // each row's two code bytes (8 weights) and scale
+    uint32_t r[4][4];
+    const char* tab;
+    uint32_t vo_code[4], vo_scale[4], rowbytes, srowbytes;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    BwdBlock bk;
+    __device__ __forceinline__ void load(int64_t n0) {
+        const int so = uniform_offset(n0 * rowbytes), ss = uniform_offset(n0 * srowbytes);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cw[q] = __builtin_amdgcn_raw_buffer_load_b16(pr, vo_code[q], so, 0);
+            sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
+        }
+    }
+    __device__ __forceinline__ void prep() {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint2 v = values2<DT>(sc[q]);
+            const uint2 a = *reinterpret_cast<const uint2*>(tab + 8u * (cw[q] & 0xFFu));
+            const uint2 b = *reinterpret_cast<const uint2*>(tab + 8u * ((cw[q] >> 8) & 0xFFu));
+            r[q][0] = __builtin_amdgcn_perm(v.x, v.y, a.x);
+            r[q][1] = __builtin_amdgcn_perm(v.x, v.y, a.y);
+            r[q][2] = __builtin_amdgcn_perm(v.x, v.y, b.x);
+            r[q][3] = __builtin_amdgcn_perm(v.x, v.y, b.y);
+        }
+    }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
+        bwd_store_cols(r, p, tile, bk);
+    }
+};
+
+template <int DT, int GS>
+struct RootBwdDecoder {
+    static constexpr int kLoads = 8;
+    uint32_t cd[4], sc[4];  // each row's code byte (8 weights) and scale
+    uint32_t r[4][4];
+    const char* tab;
+    uint32_t vo_code[4], vo_scale[4], rowbytes, srowbytes;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    BwdBlock bk;
+    __device__ __forceinline__ void load(int64_t n0) {
+        const int so = uniform_offset(n0 * rowbytes), ss = uniform_offset(n0 * srowbytes);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cd[q] = __builtin_amdgcn_raw_buffer_load_b8(pr, vo_code[q], so, 0);
+            sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
+        }
+    }
+    __device__ __forceinline__ void prep() {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint2 v = values1<DT>(sc[q]);
+            const uint4 sl = *reinterpret_cast<const uint4*>(tab + 16u * (cd[q] & 0xFFu));
+            r[q][0] = __builtin_amdgcn_perm(v.x, v.y, sl.x);
+            r[q][1] = __builtin_amdgcn_perm(v.x, v.y, sl.y);
+            r[q][2] = __builtin_amdgcn_perm(v.x, v.y, sl.z);
+            r[q][3] = __builtin_amdgcn_perm(v.x, v.y, sl.w);
+        }
+    }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
+        bwd_store_cols(r, p, tile, bk);
+    }
 };
 
 // One K step (64) of the wave's block.
@@ -378,22 +545,30 @@ __device__ __forceinline__ void kstep(const char* xt, const char* wt, const Frag
         mma_row<DT, TN>(a1[i], b1, acc[i]);
         if (i >= TM - 4) {  // the table reads were issued TM - 4 MFMA rows earlier
             const int p = i - (TM - 4);
-            *reinterpret_cast<uint4*>(wt_next + swz(wrow, 4u * half + p)) = dec.piece(p);
+            dec.store(p, wt_next, wrow, half);
         }
     }
 }
 
-__device__ __forceinline__ void vm_wait_le2() {
-    __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): all but the two newest loads (gfx9)
+// s_waitcnt vmcnt(N) (fields vmcnt[3:0] and [15:14]; expcnt and lgkmcnt left alone):
+// all but the N newest loads have completed.
+template <int N>
+__device__ __forceinline__ void vm_wait_le() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-// FMT: kFmtTernary (group size 32), kFmt2Bit or kFmtRoot (group size GS2).
-template <int DT, typename C, int FMT, int GS2>
+// FMT: kFmtTernary (group size 32), kFmt2Bit or kFmtRoot (group size GS2).  BWD = false:
+// y[M, N] = x[M, K] . W[N, K]^T + bias; BWD = true: y[M, K] = x[M, N] . W[N, K] (backward
+// dX; x is grad_y, bias unused).  The weight matrix is W[N, K] in both.
+template <int DT, typename C, int FMT, int GS2, bool BWD>
 __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     float* __restrict__ part, int splits, int64_t M, int64_t N, int64_t K) {
     constexpr bool kTernary = FMT == kFmtTernary;
+    const int64_t NO = BWD ? K : N;  // output columns
+    const int64_t R = BWD ? N : K;   // reduction length (row length of x)
     __shared__ uint4 lut_storage[kTernary ? kLutStorageU4
                                           : (FMT == kFmt2Bit ? kSel2Entries / 2 : kSel1Entries)];
     __shared__ __attribute__((aligned(16))) char xs[2][C::XTILE];
@@ -405,7 +580,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     else fill_sel1(lut_storage, C::THREADS);
 
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
-    const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (N + C::BN - 1) / C::BN;
+    const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (NO + C::BN - 1) / C::BN;
     const int64_t tiles = tm_n * tn_n;
     // K split: workgroup blockIdx.x runs K steps [s_begin, s_end) of tile blockIdx.x % tiles
     const int split = (int)(blockIdx.x / (uint32_t)tiles);
@@ -433,7 +608,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const uint32_t brow0 = (uint32_t)C::WN * (uint32_t)(wave % C::WAVES_N);
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+        (void*)x, (short)0, (int)(M * R * 2), kRsrcWord3);
     const uint32_t rowbytes = kTernary ? (uint32_t)(K * 3 / 16)
                                        : (FMT == kFmt2Bit ? (uint32_t)(K / 4) : (uint32_t)(K / 8));
     const uint32_t srowbytes = kTernary ? (uint32_t)(K / 16) : (uint32_t)(K * 2 / GS2);
@@ -446,13 +621,42 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const uint32_t vo_code = (uint32_t)(n0 + wrow) * rowbytes;
     const uint32_t vo_scale = (uint32_t)(n0 + wrow) * srowbytes;
     const char* lut = reinterpret_cast<const char*>(lut_storage) + (kTernary ? kLutBaseOffset : 0);
-    using Dec = std::conditional_t<
+    using FwdDec = std::conditional_t<
         kTernary, TernaryRowDecoder<DT>,
         std::conditional_t<FMT == kFmt2Bit, Bit2RowDecoder<DT, GS2>, RootRowDecoder<DT, GS2>>>;
+    using BwdDec = std::conditional_t<
+        kTernary, TernaryBwdDecoder<DT>,
+        std::conditional_t<FMT == kFmt2Bit, Bit2BwdDecoder<DT, GS2>, RootBwdDecoder<DT, GS2>>>;
+    using Dec = std::conditional_t<BWD, BwdDec, FwdDec>;
     Dec dec;
     dec.pr = pr;
     dec.sr = sr;
-    if constexpr (kTernary) {
+    if constexpr (BWD) {
+        // block rows n (per step) and output columns k = n0 + bk.col .. + 7 (n0 is the
+        // tile's first output column here)
+        dec.bk = bwd_block(tid);
+        dec.rowbytes = rowbytes;
+        dec.srowbytes = srowbytes;
+        const uint32_t kcol = (uint32_t)n0 + dec.bk.col;
+        uint32_t cbyte, sbyte;
+        if constexpr (kTernary) {
+            dec.lut = lut;
+            dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+            const uint32_t j = kcol / 8u;  // code index in the row
+            dec.odd = j & 1u;
+            cbyte = 3u * (j >> 1) + (j & 1u);
+            sbyte = 2u * (kcol / 32u);
+        } else {
+            dec.tab = lut;
+            cbyte = FMT == kFmt2Bit ? kcol / 4u : kcol / 8u;
+            sbyte = 2u * (kcol / (uint32_t)GS2);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            dec.vo_code[q] = (dec.bk.rows + (uint32_t)q) * rowbytes + cbyte;
+            dec.vo_scale[q] = (dec.bk.rows + (uint32_t)q) * srowbytes + sbyte;
+        }
+    } else if constexpr (kTernary) {
         dec.lut = lut;
         dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
         dec.vo_code = vo_code;
@@ -471,19 +675,18 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 #pragma unroll
         for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t steps = K / kBK;
+    const int64_t steps = R / kBK;
     const int64_t s_begin = steps * split / splits, s_end = steps * (split + 1) / splits;
     const int64_t k_begin = s_begin * kBK;
     // Codes run one K step ahead of the weight tile being decoded, which runs one step
     // ahead of the MFMAs.  Branch-free body: loads past the last step fetch bytes past the
     // operands (zeros, or the next row's data) into buffers that are never read.
-    load_x_tile(xs[0], xr, m0, k_begin, K, wave, lane, C::XLOADS);
+    load_x_tile(xs[0], xr, m0, k_begin, R, wave, lane, C::XLOADS);
     dec.load(k_begin);
     __syncthreads();  // table ready
     dec.prep();
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
-        *reinterpret_cast<uint4*>(ws[0] + swz(wrow, 4u * half + p)) = dec.piece(p);
+    for (int p = 0; p < 4; ++p) dec.store(p, ws[0], wrow, half);
     dec.load(k_begin + kBK);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
@@ -497,8 +700,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         const int64_t kx = (s + 1) * kBK;
         kstep<DT, kTM, kTN>(xs[cur], ws[cur], fl, a0, b0, a1, b1, dec, ws[nxt], wrow, half,
                             acc, (s + 2) * kBK,
-                            [&] { load_x_tile(xn, xr, m0, kx, K, wave, lane, C::XLOADS); });
-        vm_wait_le2();  // the X tile of step s+1 has landed; the code loads may still fly
+                            [&] { load_x_tile(xn, xr, m0, kx, R, wave, lane, C::XLOADS); });
+        vm_wait_le<Dec::kLoads>();  // the X tile of step s+1 has landed; code loads may fly
         __syncthreads();
         load_frags(xs[nxt], ws[nxt], fl, 0, a0, b0);
         // all of the step's first fragment reads go out before its first MFMA (left to
@@ -508,17 +711,17 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 
     // ---- epilogue: lane (g, i16) holds rows 4g+q of column i16 of each 16x16 tile
     if (splits > 1) {  // fp32 partial sums of this K range: part[split][row][col]
-        float* pp = part + (int64_t)split * split_stride(M, N);
+        float* pp = part + (int64_t)split * split_stride(M, NO);
 #pragma unroll
         for (int j = 0; j < kTN; ++j) {
             const int64_t col = n0 + brow0 + 16 * j + i16;
-            if (col >= N) continue;
+            if (col >= NO) continue;
 #pragma unroll
             for (int i = 0; i < kTM; ++i) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int64_t row = m0 + arow0 + 16 * i + 4 * g + q;
-                    if (row < M) pp[row * N + col] = acc[i][j][q];
+                    if (row < M) pp[row * NO + col] = acc[i][j][q];
                 }
             }
         }
@@ -527,14 +730,14 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
         const int64_t col = n0 + brow0 + 16 * j + i16;
-        if (col >= N) continue;
-        const float bv = bias ? load_as_f32<DT>(bias, col) : 0.f;
+        if (col >= NO) continue;
+        const float bv = (!BWD && bias) ? load_as_f32<DT>(bias, col) : 0.f;
 #pragma unroll
         for (int i = 0; i < kTM; ++i) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t row = m0 + arow0 + 16 * i + 4 * g + q;
-                if (row < M) store_from_f32<DT>(y, row * N + col, acc[i][j][q] + bv);
+                if (row < M) store_from_f32<DT>(y, row * NO + col, acc[i][j][q] + bv);
             }
         }
     }
@@ -571,9 +774,12 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
 }
 
 bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt) {
+                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt,
+                         bool bwd) {
     if (dt != kBF16 && dt != kF16) return false;
     if (M < 1 || N < 1 || K < kBK || K % kBK != 0) return false;
+    if (bwd && N % kBK != 0) return false;  // the backward reduces over N
+    const int64_t R = bwd ? N : K;
     if (fmt == kFmtTernary ? gs != 32 : (gs != 8 && gs != 16 && gs != 32 && gs != 64))
         return false;
     if (fmt != kFmtTernary && fmt != kFmt2Bit && fmt != kFmtRoot) return false;
@@ -583,7 +789,7 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
     // of padding rows) must stay below 2^31 bytes
     const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : (fmt == kFmt2Bit ? K / 4 : K / 8);
     const int64_t srowbytes = fmt == kFmtTernary ? K / 16 : K * 2 / gs;
-    if ((M + CfgLarge::BM) * K * 2 >= (1ll << 31) || (N + CfgLarge::BN) * rowbytes >= (1ll << 31) ||
+    if ((M + CfgLarge::BM) * R * 2 >= (1ll << 31) || (N + CfgLarge::BN) * rowbytes >= (1ll << 31) ||
         (N + CfgLarge::BN) * srowbytes >= (1ll << 31))
         return false;
     return true;
@@ -595,19 +801,20 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
 #define OJX_GEMM_SMALL_BELOW 192
 #endif
 
-template <int DT, typename C, int FMT, int GS2>
+template <int DT, typename C, int FMT, int GS2, bool BWD>
 static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_t* scales,
                              const void* bias, void* y, float* part, int splits, int64_t M,
                              int64_t N, int64_t K, hipStream_t stream) {
-    const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
+    const int64_t NO = BWD ? K : N;
+    const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((NO + C::BN - 1) / C::BN);
     if (tiles * splits > 0x7FFFFFFF) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C, FMT, GS2>), dim3((unsigned)(tiles * splits)),
+    hipLaunchKernelGGL((gemm_mfma_kernel<DT, C, FMT, GS2, BWD>), dim3((unsigned)(tiles * splits)),
                        dim3(C::THREADS), 0, stream, x, packed, scales, bias, y, part, splits, M,
                        N, K);
     if (splits == 1) return hipGetLastError();
-    const int64_t groups = (M * N + 1023) / 1024;
+    const int64_t groups = (M * NO + 1023) / 1024;
     hipLaunchKernelGGL((gemm_split_reduce_kernel<DT>), dim3((unsigned)groups), dim3(256), 0,
-                       stream, part, splits, bias, y, M, N);
+                       stream, part, splits, BWD ? nullptr : bias, y, M, NO);
     return hipGetLastError();
 }
 
@@ -650,26 +857,26 @@ GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K) {
                       (int)splits_for(tiles, OJX_SPLIT_TARGET_WGS, kMinSplitSteps, M, N, K)};
 }
 
-template <int DT, typename C>
+template <int DT, typename C, bool BWD>
 static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_t* scales,
                              const void* bias, void* y, float* part, int splits, int64_t M,
                              int64_t N, int64_t K, int64_t gs, int fmt, hipStream_t stream) {
     if (fmt == kFmtTernary)
-        return launch_cfg<DT, C, kFmtTernary, 32>(x, packed, scales, bias, y, part, splits, M, N,
+        return launch_cfg<DT, C, kFmtTernary, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N,
                                                   K, stream);
     if (fmt == kFmtRoot) {
         switch (gs) {
         case 8:
-            return launch_cfg<DT, C, kFmtRoot, 8>(x, packed, scales, bias, y, part, splits, M, N,
+            return launch_cfg<DT, C, kFmtRoot, 8, BWD>(x, packed, scales, bias, y, part, splits, M, N,
                                                   K, stream);
         case 16:
-            return launch_cfg<DT, C, kFmtRoot, 16>(x, packed, scales, bias, y, part, splits, M, N,
+            return launch_cfg<DT, C, kFmtRoot, 16, BWD>(x, packed, scales, bias, y, part, splits, M, N,
                                                    K, stream);
         case 32:
-            return launch_cfg<DT, C, kFmtRoot, 32>(x, packed, scales, bias, y, part, splits, M, N,
+            return launch_cfg<DT, C, kFmtRoot, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N,
                                                    K, stream);
         case 64:
-            return launch_cfg<DT, C, kFmtRoot, 64>(x, packed, scales, bias, y, part, splits, M, N,
+            return launch_cfg<DT, C, kFmtRoot, 64, BWD>(x, packed, scales, bias, y, part, splits, M, N,
                                                    K, stream);
         default:
             return hipErrorInvalidValue;
@@ -677,16 +884,16 @@ static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_
     }
     switch (gs) {
     case 8:
-        return launch_cfg<DT, C, kFmt2Bit, 8>(x, packed, scales, bias, y, part, splits, M, N, K,
+        return launch_cfg<DT, C, kFmt2Bit, 8, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
                                               stream);
     case 16:
-        return launch_cfg<DT, C, kFmt2Bit, 16>(x, packed, scales, bias, y, part, splits, M, N, K,
+        return launch_cfg<DT, C, kFmt2Bit, 16, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
                                                stream);
     case 32:
-        return launch_cfg<DT, C, kFmt2Bit, 32>(x, packed, scales, bias, y, part, splits, M, N, K,
+        return launch_cfg<DT, C, kFmt2Bit, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
                                                stream);
     case 64:
-        return launch_cfg<DT, C, kFmt2Bit, 64>(x, packed, scales, bias, y, part, splits, M, N, K,
+        return launch_cfg<DT, C, kFmt2Bit, 64, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
                                                stream);
     default:
         return hipErrorInvalidValue;
@@ -696,17 +903,28 @@ static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, float* part, GemmChoice c, int64_t M,
                             int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs,
-                            int fmt) {
+                            int fmt, bool bwd) {
     if (c.splits < 1 || (c.splits > 1 && !part)) return hipErrorInvalidValue;
+    if (bwd) {
+        if (dt == kBF16)
+            return c.small ? launch_fmt<kBF16, CfgSmall, true>(x, packed, scales, bias, y, part,
+                                                               c.splits, M, N, K, gs, fmt, stream)
+                           : launch_fmt<kBF16, CfgLarge, true>(x, packed, scales, bias, y, part,
+                                                               c.splits, M, N, K, gs, fmt, stream);
+        return c.small ? launch_fmt<kF16, CfgSmall, true>(x, packed, scales, bias, y, part,
+                                                          c.splits, M, N, K, gs, fmt, stream)
+                       : launch_fmt<kF16, CfgLarge, true>(x, packed, scales, bias, y, part,
+                                                          c.splits, M, N, K, gs, fmt, stream);
+    }
     if (dt == kBF16)
-        return c.small ? launch_fmt<kBF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits,
-                                                     M, N, K, gs, fmt, stream)
-                       : launch_fmt<kBF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits,
-                                                     M, N, K, gs, fmt, stream);
-    return c.small ? launch_fmt<kF16, CfgSmall>(x, packed, scales, bias, y, part, c.splits, M, N,
-                                                K, gs, fmt, stream)
-                   : launch_fmt<kF16, CfgLarge>(x, packed, scales, bias, y, part, c.splits, M, N,
-                                                K, gs, fmt, stream);
+        return c.small ? launch_fmt<kBF16, CfgSmall, false>(x, packed, scales, bias, y, part,
+                                                            c.splits, M, N, K, gs, fmt, stream)
+                       : launch_fmt<kBF16, CfgLarge, false>(x, packed, scales, bias, y, part,
+                                                            c.splits, M, N, K, gs, fmt, stream);
+    return c.small ? launch_fmt<kF16, CfgSmall, false>(x, packed, scales, bias, y, part, c.splits,
+                                                       M, N, K, gs, fmt, stream)
+                   : launch_fmt<kF16, CfgLarge, false>(x, packed, scales, bias, y, part, c.splits,
+                                                       M, N, K, gs, fmt, stream);
 }
 
 }  // namespace ojx

@@ -99,8 +99,10 @@ hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int 
 
 // Prefill MFMA GEMM: F16/BF16, K % 64 == 0; fmt 0 (ternary, group size 32), 1 (2-bit) or 2
 // (1-bit Root E8), the last two with group size 8, 16, 32 or 64.
+// bwd: the backward dX y[M, K] = x[M, N] . W[N, K] (also needs N % 64 == 0).
 bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt = 0);
+                         int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt = 0,
+                         bool bwd = false);
 // Tile configuration and K splits of the prefill GEMM for a shape (splits 1 = none).  With
 // splits > 1 the launch needs `part`, fp32 scratch of splits * split_stride(M, N) floats.
 struct GemmChoice {
@@ -114,7 +116,7 @@ __host__ __device__ inline int64_t split_stride(int64_t M, int64_t N) {
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, float* part, GemmChoice c, int64_t M,
                             int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs = 32,
-                            int fmt = 0);
+                            int fmt = 0, bool bwd = false);
 
 // Scratch device memory owned by the library, one buffer per (device, stream), grown on
 // demand and kept until the process ends.  Returns nullptr (and allocates nothing) while
