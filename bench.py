@@ -24,7 +24,8 @@ roofline= HBM-bound: ALGORITHMIC bytes of the grouped GEMV launches in the timed
           around each launch, on its stream), against 8 TB/s.
 
 Also reported (not the headline): prefill GEMM TFLOP/s on the four shapes at
-M in {512, 2048, 8192}, encoder throughput on one layer of fp16
+M in {512, 2048, 8192} and the backward dX of the same layers, encoder
+throughput on one layer of fp16
 weights with 0.1% +-8 sigma outliers, the 2-bit E8 format (encoder, decode
 GEMV and prefill per linear on an 8-layer stack), and the CPU baseline: this
 repo's torch restatement of the reference's portable decode-then-matmul path
@@ -261,7 +262,9 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev, Ms=DECODE_M,
 
 # --------------------------------------------------------------------------- prefill GEMM
 
-def bench_prefill(torch, N_, stack, Ms, target_s: float, dev):
+def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = False):
+    """Prefill GEMM per shape and M; with backward=True the backward dX of the same layers
+    (grad_x[M, K] = grad_y[M, N] . W[N, K], ojx_e8t_gemm_bwd_dx)."""
     lib = N_.lib()
     by_name = {}
     for s in stack[:7]:
@@ -274,13 +277,24 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev):
         for name, N, K in PREFILL_SHAPES:
             s = by_name[(N, K)]
             g = torch.Generator(device=dev).manual_seed(8400 + M)
-            x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
-            y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            if backward:
+                x = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+                y = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
 
-            def run():
-                N_.check(lib.ojx_e8t_gemm_fwd(x.data_ptr(), s["packed"].data_ptr(),
-                                              s["scales"].data_ptr(), None, y.data_ptr(), M, N,
-                                              K, GS, N_.BF16, stream.cuda_stream), "gemm_fwd")
+                def run():
+                    N_.check(lib.ojx_e8t_gemm_bwd_dx(x.data_ptr(), s["packed"].data_ptr(),
+                                                     s["scales"].data_ptr(), y.data_ptr(), M, N,
+                                                     K, GS, N_.BF16, stream.cuda_stream),
+                             "gemm_bwd_dx")
+            else:
+                x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+                y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+                def run():
+                    N_.check(lib.ojx_e8t_gemm_fwd(x.data_ptr(), s["packed"].data_ptr(),
+                                                  s["scales"].data_ptr(), None, y.data_ptr(), M,
+                                                  N, K, GS, N_.BF16, stream.cuda_stream),
+                             "gemm_fwd")
 
             run()
             torch.cuda.synchronize()
@@ -407,9 +421,10 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights (seed 9700 + 7*layer +
     j), group size 32.  Encoder: the stack's encode launches replayed from one hipGraph,
     layer 0 of each shape checked bit for bit against the CPU oracle on its first
-    `check_rows` rows.  Decode: one ojx_e8_gemm_fwd launch per linear at each M, replayed
-    from a hipGraph; outputs of layer 0 checked against an fp32 matmul of the decoded
-    weights.  Prefill: the same at M = `prefill_m`."""
+    `check_rows` rows.  Decode: one ojx_e8_gemm_fwd launch per linear at each M (replayed
+    from a hipGraph for M <= 4, the GEMV; issued eagerly above, where the MFMA GEMM splits
+    over K); outputs of layer 0 checked against an fp32 matmul of the decoded weights.
+    Prefill: the same at M = `prefill_m`."""
     import numpy as np
 
     from oracle import oracle as O
@@ -426,6 +441,20 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     numel = sum(it["N"] * it["K"] for it in items)
     wbytes = sum(e8b_weight_bytes(it["N"], it["K"]) for it in items)
     stream = torch.cuda.current_stream()
+
+    def eager_ms(launch_all, reps):
+        # launches outside graph capture (the GEMM's K split needs the library's stream
+        # scratch, which is never handed out while a stream is capturing)
+        launch_all(stream.cuda_stream)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            launch_all(stream.cuda_stream)
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
 
     def replay_ms(launch_all, reps):
         launch_all(stream.cuda_stream)
@@ -474,7 +503,7 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
                                              it["scales"].data_ptr(), None, y.data_ptr(), M,
                                              it["N"], it["K"], E8B_GS, N_.BF16, h), "e8 gemm")
 
-        ms = replay_ms(launch_all, steps)
+        ms = replay_ms(launch_all, steps) if M <= 4 else eager_ms(launch_all, steps)
         worst = 0.0
         from ojasx_amd import ops
         for idx in (0, 4, 6):  # q, gate, down of layer 0
@@ -920,6 +949,10 @@ def main() -> int:
         log(f"prefill timing M={Ms}")
         result["prefill"] = bench_prefill(torch, N_, stack, Ms, args.prefill_time, dev)
         log(f"prefill: {result['prefill']['TFLOPs']} TFLOP/s")
+        log(f"backward dX timing M={Ms}")
+        result["backward_dx"] = bench_prefill(torch, N_, stack, Ms, args.prefill_time, dev,
+                                              backward=True)
+        log(f"backward dX: {result['backward_dx']['TFLOPs']} TFLOP/s")
     if not args.no_encode:
         del stack
         torch.cuda.empty_cache()
