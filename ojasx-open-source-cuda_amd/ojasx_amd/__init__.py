@@ -13,6 +13,8 @@ from .lattice import (
     E8QuantizationAwareLinear,
     _E8STEFunction,
     conway_sloane_e8_project,
+    fast_walsh_hadamard_transform,
+    randomized_hadamard_transform,
     E8LatticePacker,
     RootE8LatticePacker,
     TernaryE8LatticePacker,
@@ -35,6 +37,8 @@ __all__ = [
     "E8QuantizationAwareLinear",
     "_E8STEFunction",
     "conway_sloane_e8_project",
+    "fast_walsh_hadamard_transform",
+    "randomized_hadamard_transform",
     "E8LatticePacker",
     "RootE8LatticePacker",
     "TernaryE8LatticePacker",

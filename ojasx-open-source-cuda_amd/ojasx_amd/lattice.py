@@ -8,6 +8,8 @@ operation on the path running in the HIP kernels behind ``ojasx_amd.ops``:
 this module                         reference (ojasx2/math/lattice.py)
 =================================  ==========================================
 ``fwht_block32``                    :91-102
+``fast_walsh_hadamard_transform``   :104-122
+``randomized_hadamard_transform``   :125-155
 ``conway_sloane_e8_project``        :162-203   -> ops.cs_project
 ``_E8STEFunction``                  :853-869   -> ops.ste_quantize
 ``E8QuantizationAwareLinear``       :872-898
@@ -45,6 +47,8 @@ from . import ops
 
 __all__ = [
     "fwht_block32",
+    "fast_walsh_hadamard_transform",
+    "randomized_hadamard_transform",
     "TernaryE8LatticePacker",
     "E8LatticePacker",
     "RootE8LatticePacker",
@@ -138,6 +142,49 @@ class E8QuantizationAwareLinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         w_q = _E8STEFunction.apply(self.weight)
         return F.linear(x, w_q, self.bias)
+
+
+def fast_walsh_hadamard_transform(x: torch.Tensor) -> torch.Tensor:
+    """Normalised Walsh-Hadamard transform along a power-of-two last dim (lattice.py:104-122).
+
+    fwht_block32 for n = 32; otherwise butterflies at distances 1, 2, 4, ... (sum to the
+    lower index, difference to the upper) and one true division by sqrt(n): the reference's
+    sequence of rounded operations, on the tensor's own device."""
+    n = x.shape[-1]
+    if n <= 0 or (n & (n - 1)) != 0:
+        raise ValueError(f"Last dimension ({n}) must be a positive power of 2 for FWHT.")
+    if n == 32:
+        return fwht_block32(x)
+    h, d = x.reshape(-1, n), 1
+    while d < n:
+        v = h.reshape(-1, n // (2 * d), 2, d)
+        h = torch.stack([v[:, :, 0, :] + v[:, :, 1, :], v[:, :, 0, :] - v[:, :, 1, :]], dim=2)
+        d *= 2
+    return h.reshape(x.shape) / math.sqrt(n)
+
+
+def randomized_hadamard_transform(w: torch.Tensor, seed: Optional[int] = 42
+                                  ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Randomised Hadamard rotation of a weight matrix (lattice.py:125-155): random row and
+    column signs s1, s2 drawn from a generator on w's device seeded with ``seed`` (the same
+    draws as the reference on the same device), then the two-sided transform when both
+    dims are powers of two, else fwht_block32 along rows of a multiple-of-32 width.
+    Returns (w_rot, s1, s2)."""
+    m, n = w.shape
+    rng = torch.Generator(device=w.device)
+    if seed is not None:
+        rng.manual_seed(seed)
+    s1 = torch.randint(0, 2, (m,), generator=rng, device=w.device, dtype=w.dtype) * 2 - 1
+    s2 = torch.randint(0, 2, (n,), generator=rng, device=w.device, dtype=w.dtype) * 2 - 1
+    signed = (w * s2.unsqueeze(0)) * s1.unsqueeze(1)
+    if m & (m - 1) == 0 and n & (n - 1) == 0:
+        rot = fast_walsh_hadamard_transform(signed)
+        rot = fast_walsh_hadamard_transform(rot.transpose(0, 1)).transpose(0, 1)
+    elif n % 32 == 0:
+        rot = fwht_block32(signed)
+    else:
+        rot = signed
+    return rot, s1, s2
 
 
 _DEVICE_TERNARY_LUTS: Dict[Tuple[str, Optional[int]], Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}

@@ -235,3 +235,53 @@ def test_checkpoint_loader_argument_errors(tmp_path):
         ojasx_amd.load_hf_checkpoint_e8(str(tmp_path), group_size=48)
     with pytest.raises(NotADirectoryError):
         ojasx_amd.load_hf_checkpoint_e8(str(tmp_path / "absent"))
+
+
+def _fwht_stagewise(x):
+    # the reference's loop (lattice.py:112-122): in-place halves at distance h, then / sqrt(n)
+    n = x.shape[-1]
+    out = x.clone()
+    h = 1
+    while h < n:
+        out = out.view(-1, n // (2 * h), 2, h)
+        a = out[:, :, 0, :].clone()
+        b = out[:, :, 1, :].clone()
+        out[:, :, 0, :] = a + b
+        out[:, :, 1, :] = a - b
+        h *= 2
+    return out.view(x.shape) / math.sqrt(n)
+
+
+@pytest.mark.parametrize("n", [1, 2, 8, 64, 256, 1024])
+def test_fast_walsh_hadamard_transform_bitwise_and_orthonormal(n):
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(3, 5, n, generator=g)
+    y = ojasx_amd.fast_walsh_hadamard_transform(x)
+    assert torch.equal(y, _fwht_stagewise(x))
+    assert torch.allclose(ojasx_amd.fast_walsh_hadamard_transform(y), x, atol=1e-5)
+    assert torch.allclose(y.norm(dim=-1), x.norm(dim=-1), rtol=1e-5)
+    with pytest.raises(ValueError, match="power of 2"):
+        ojasx_amd.fast_walsh_hadamard_transform(torch.zeros(2, 12))
+    assert torch.equal(ojasx_amd.fast_walsh_hadamard_transform(x[..., :32] if n >= 32 else
+                                                                torch.zeros(1, 32)),
+                       ojasx_amd.fwht_block32(x[..., :32] if n >= 32 else torch.zeros(1, 32)))
+
+
+def test_randomized_hadamard_transform_matches_reference_steps():
+    w = torch.randn(64, 128, generator=torch.Generator().manual_seed(1))
+    rot, s1, s2 = ojasx_amd.randomized_hadamard_transform(w, seed=42)
+    rng = torch.Generator().manual_seed(42)
+    e1 = torch.randint(0, 2, (64,), generator=rng, dtype=w.dtype) * 2 - 1
+    e2 = torch.randint(0, 2, (128,), generator=rng, dtype=w.dtype) * 2 - 1
+    assert torch.equal(s1, e1) and torch.equal(s2, e2)
+    signed = (w * e2.unsqueeze(0)) * e1.unsqueeze(1)
+    ref = _fwht_stagewise(_fwht_stagewise(signed).transpose(0, 1)).transpose(0, 1)
+    assert torch.equal(rot, ref)
+    # non-power-of-two rows with a multiple-of-32 width: fwht_block32 along rows
+    w2 = torch.randn(48, 96, generator=torch.Generator().manual_seed(2))
+    rot2, a1, a2 = ojasx_amd.randomized_hadamard_transform(w2, seed=7)
+    assert torch.equal(rot2, ojasx_amd.fwht_block32((w2 * a2.unsqueeze(0)) * a1.unsqueeze(1)))
+    # neither: signs only
+    w3 = torch.randn(5, 7)
+    rot3, b1, b2 = ojasx_amd.randomized_hadamard_transform(w3, seed=None)
+    assert torch.equal(rot3, (w3 * b2.unsqueeze(0)) * b1.unsqueeze(1))
