@@ -7,7 +7,7 @@ operation runs in hand-written HIP kernels for gfx950 (libojasx_e8t.so, C ABI in
 include/ojasx_e8t.h) registered as ``torch.ops.ojasx_e8t.*``.
 """
 
-from . import grouped, ops, optim_state
+from . import grouped, hardware, ops, optim_state
 from .lattice import (
     E8LatticeLinear,
     E8QuantizationAwareLinear,
@@ -31,6 +31,7 @@ __version__ = "0.1.0"
 
 __all__ = [
     "grouped",
+    "hardware",
     "ops",
     "optim_state",
     "E8LatticeLinear",
