@@ -338,6 +338,9 @@ __attribute__((visibility("default"))) int ojx_e8_gemm_fwd(const void* x, const 
     if (ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
         return done(ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                     "e8 gemv launch");
+    if (ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype))
+        return done(ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
+                    "e8 gemv launch");
     if (ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, ojx::kFmt2Bit))
         return done(launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmt2Bit),
                     "e8 gemm_mfma launch");

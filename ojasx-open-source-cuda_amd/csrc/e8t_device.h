@@ -100,4 +100,23 @@ template <int DT> __device__ __forceinline__ float deq2_value(uint32_t code, uin
     else return p;
 }
 
+// v rounded once to the activation dtype DT (fp16 or bf16), as bits.
+template <int DT>
+__device__ __forceinline__ uint32_t rnd_bits(float v) {
+    keep_f32(v);
+    if constexpr (DT == kF16) return f32_to_f16_bits(v);
+    else return f32_to_bf16_bits(v);
+}
+
+// Value words {S0, S1} of one 2-bit scale group (fp16 bits s16): the four weights -B, -A,
+// +A, +B (A = rnd(0.5 s), B = rnd(1.5 s), s = scales.to(dtype)) as S1 = -B | -A << 16,
+// S0 = A | B << 16, so that byte pair 2c, 2c + 1 of v_perm_b32's {S0, S1} is the weight of
+// code c (products exact in fp32; -rnd(x) = rnd(-x)).
+template <int DT>
+__device__ __forceinline__ uint2 values2(uint32_t s16) {
+    const float s = scale_for<DT>(s16 & 0xFFFFu);
+    const uint32_t a = rnd_bits<DT>(0.5f * s), b = rnd_bits<DT>(1.5f * s);
+    return make_uint2(a | (b << 16), (b ^ 0x8000u) | ((a ^ 0x8000u) << 16));
+}
+
 }  // namespace ojx

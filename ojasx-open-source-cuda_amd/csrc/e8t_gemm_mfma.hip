@@ -208,21 +208,6 @@ __device__ __forceinline__ void fill_sel2(uint2* tab, int nthreads) {
     }
 }
 
-template <int DT>
-__device__ __forceinline__ uint32_t rnd_bits(float v) {
-    keep_f32(v);
-    if constexpr (DT == kF16) return f32_to_f16_bits(v);
-    else return f32_to_bf16_bits(v);
-}
-
-// Value words {S0, S1} of one scale group (fp16 bits s16).
-template <int DT>
-__device__ __forceinline__ uint2 values2(uint32_t s16) {
-    const float s = scale_for<DT>(s16 & 0xFFFFu);
-    const uint32_t a = rnd_bits<DT>(0.5f * s), b = rnd_bits<DT>(1.5f * s);
-    return make_uint2(a | (b << 16), (b ^ 0x8000u) | ((a ^ 0x8000u) << 16));
-}
-
 template <int DT, int GS>
 struct Bit2RowDecoder {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "2-bit group size 8..64");

@@ -1341,29 +1341,28 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     }
     __syncthreads();  // table and zero block ready
     const char* lut = reinterpret_cast<const char*>(lut_storage);
-    while (u < T) {  // uniform within the wave
-        if (u + kB2Waves < T) {
-            b2_load<GS>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
-            b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
-            vm_wait_le_round<GS, MM>();  // round u's codes, scales and activations have landed
-        } else {
-            vm_wait_all();
-        }
+    // Rounds in pairs (u, u + W), each prefetching the next: the loop body has no branch
+    // between the two halves, so the compiler neither sinks the prefetch of the second
+    // half's codes below the first half's compute nor loses track of which activation
+    // buffer a pending DMA writes (either would make it wait for the prefetch).  The
+    // second half's prefetch of round u + 2W re-fetches round T - 1 (an L2 hit, never
+    // read) when there is none.
+    while (u + kB2Waves < T) {  // uniform within the wave
+        b2_load<GS>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
+        vm_wait_le_round<GS, MM>();  // round u's codes, scales and activations have landed
         B2Round<DT, MM, GS>::run(cp[0], sp[0], lut, slot, xa0, acc);
-        u += kB2Waves;
-        if (u >= T) break;
-        lds_wait_all();  // round u - W's activation reads are done: buffer 0 may be refilled
-        if (u + kB2Waves < T) {
-            b2_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u + kB2Waves);
-            b2_stage_x<MM>(xw0, xr, u + kB2Waves, M, K, lane);
-            vm_wait_le_round<GS, MM>();
-        } else {
-            vm_wait_all();
-        }
+        lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
+        const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
+        b2_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, un);
+        b2_stage_x<MM>(xw0, xr, un, M, K, lane);
+        vm_wait_le_round<GS, MM>();
         B2Round<DT, MM, GS>::run(cp[1], sp[1], lut, slot, xa1, acc);
-        u += kB2Waves;
         lds_wait_all();
+        u += 2 * kB2Waves;
     }
+    vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
+    if (u < T) B2Round<DT, MM, GS>::run(cp[0], sp[0], lut, slot, xa0, acc);
 
     // add the waves' partial sums, then the four lane groups; lane group q stores row q
 #pragma unroll
@@ -1383,6 +1382,247 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     if ((int64_t)row < N && g < M) {
         const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
         store_from_f32<DT>(y, (int64_t)g * N + row, out + bv);
+    }
+}
+
+// ------------------------------------------------------------------------- 2-bit GEMV, 4 < M <= 16
+//
+// With up to 16 activation rows every A row of the MFMA is live, so the group scale can no
+// longer multiply per-lane partial sums: the B operand carries the weights themselves,
+// rnd_dt((c - 1.5) * s_dt) (lattice.py:274-276; the native binding's dtype rule,
+// ojasx_math_bindings.cpp:286).  Per scale group a lane forms the two value words of
+// `values2`; each pair of codes (one nibble) then becomes one dword of two weights by
+// v_perm_b32, its selector read from a 16-entry nibble table (32 copies: one conflict-free
+// b32 read per pair of weights).
+//
+// Each workgroup owns one 16-row tile; its 4 waves take the 256-k rounds u = w, w + 4, ...
+// (their own registers and activation buffers, so they never wait for each other until the
+// final reduction).  A round of a row is 64 code bytes and 512/gs scale bytes: lane (g, n)
+// takes code bytes 16g .. 16g+15 of row n (one 16-byte load per lane; the four lane groups
+// read 64 contiguous bytes of each row per instruction) and the 64/gs scales of those
+// weights.  The 16 activation rows of the round (8 KB) are staged into the wave's LDS
+// buffer by eight 1-KB loads.  Step h (0..7) takes the 8 codes of half-word h of the lane's
+// piece, k = 256u + 64g + 8h, and runs one v_mfma_f32_16x16x32 with activation row i16 as
+// A row i16 (rows past M re-read row M - 1; their outputs are not stored).
+
+constexpr int kB2mRound = 256;                      // K per round
+constexpr int kB2mXBytes = 16 * kB2mRound * 2;      // one wave's activation buffer (8 KB)
+
+template <int NT>
+__device__ __forceinline__ void fill_b2sel(uint4* lut) {
+    for (int i = (int)threadIdx.x; i < kB2LutU4; i += NT) {
+        const uint32_t e = (uint32_t)i >> 3;  // nibble: code c0 in bits 0-1, c1 in bits 2-3
+        const uint32_t c0 = e & 3u, c1 = e >> 2;
+        const uint32_t w = (2u * c0) | ((2u * c0 + 1u) << 8) | ((2u * c1) << 16) |
+                           ((2u * c1 + 1u) << 24);
+        lut[i] = make_uint4(w, w, w, w);
+    }
+}
+
+// B operand (8 weights) of half-word H of this lane's 16-byte code piece.
+template <int H>
+__device__ __forceinline__ uint4 b2m_operand(const uint4& cp, const uint2& val, const char* lut,
+                                             uint32_t slot) {
+    const uint32_t dw = (H / 2) == 0 ? cp.x : (H / 2) == 1 ? cp.y : (H / 2) == 2 ? cp.z : cp.w;
+    uint32_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * (H % 2) + 4 * i, 4) << 7) | slot;
+        const uint32_t sel = *reinterpret_cast<const uint32_t*>(lut + a);
+        v[i] = __builtin_amdgcn_perm(val.x, val.y, sel);
+    }
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Scale (fp16 bits) of step H from this lane's scales of the round (64/GS of them).
+template <int GS, int H>
+__device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
+    constexpr int idx = (8 * H) / GS, word = idx / 2;
+    const uint32_t w = word == 0 ? sp.x : word == 1 ? sp.y : word == 2 ? sp.z : sp.w;
+    return (idx % 2) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+// Step h's A fragment: with the lane's offset xo = 8192 w + 512 i16 + 16 ((8g & 16) |
+// ((8g & 8) ^ (i16 & 8)) | (i16 & 7)) (bits 4..6 equal to i16 & 7), piece 8g + h of row
+// i16 sits at xs + (xo ^ 16 h).
+template <int DT, int GS>
+struct B2mRound {
+    // step H: the A fragment and B operand of step H + 1 are formed before the MFMA of
+    // step H is issued
+    template <int H>
+    __device__ __forceinline__ static void step(const uint4& cp, const uint4& sp,
+                                                const char* lut, uint32_t slot, const char* xs,
+                                                uint32_t xo, uint4& a_cur, uint4& b_cur, uint2& val,
+                                                f32x4& acc) {
+        uint4 a_n, b_n;
+        if constexpr (H + 1 < 8) {
+            if constexpr ((8 * (H + 1)) % GS == 0) val = values2<DT>(b2m_scale<GS, H + 1>(sp));
+            a_n = *reinterpret_cast<const uint4*>(xs + (xo ^ (16u * (H + 1))));
+            b_n = b2m_operand<H + 1>(cp, val, lut, slot);
+        }
+        acc = mfma16<DT>(a_cur, b_cur, acc);
+        if constexpr (H + 1 < 8) {
+            a_cur = a_n;
+            b_cur = b_n;
+        }
+    }
+    template <int... H>
+    __device__ __forceinline__ static void steps(const uint4& cp, const uint4& sp,
+                                                 const char* lut, uint32_t slot, const char* xs,
+                                                 uint32_t xo, uint4& a, uint4& b, uint2& val,
+                                                 f32x4& acc,
+                                                 std::integer_sequence<int, H...>) {
+        (step<H>(cp, sp, lut, slot, xs, xo, a, b, val, acc), ...);
+    }
+    __device__ __forceinline__ static void run(const uint4& cp, const uint4& sp, const char* lut,
+                                               uint32_t slot, const char* xs, uint32_t xo,
+                                               f32x4& acc) {
+        uint2 val = values2<DT>(b2m_scale<GS, 0>(sp));
+        uint4 a = *reinterpret_cast<const uint4*>(xs + xo);
+        uint4 b = b2m_operand<0>(cp, val, lut, slot);
+        steps(cp, sp, lut, slot, xs, xo, a, b, val, acc, std::make_integer_sequence<int, 8>{});
+    }
+};
+
+// Activation buffer layout: row m (512 bytes) at 512 m; its 16-byte piece p (k = 8p ..
+// 8p + 7 of the round) at position (p & 16) | ((p & 15) ^ m), so that the 16 rows' reads of
+// one piece fall on distinct banks.  The DMA writes 64 consecutive 16-byte slots per load
+// (rows 2q and 2q + 1), so lane l of load q fetches the piece that belongs at its slot.
+// Global byte offset (without the round) of lane l's piece in load q (rows >= M re-read row
+// M - 1; no lane reads their outputs).
+__device__ __forceinline__ uint32_t b2m_x_offset(int q, int lane, int M, int64_t K) {
+    const uint32_t m = 2u * (uint32_t)q + ((uint32_t)lane >> 5), pos = (uint32_t)lane & 31u;
+    const uint32_t p = (pos & 16u) | ((pos & 15u) ^ m);
+    const uint32_t msrc = (int)m < M ? m : (uint32_t)(M - 1);
+    return msrc * (uint32_t)(K * 2) + 16u * p;
+}
+
+// Stages round u of the 16 activation rows into one wave's buffer: eight 1-KB loads, the
+// same count every round.
+__device__ __forceinline__ void b2m_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int64_t u,
+                                            const uint32_t (&xo)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x, lds_ptr(xs + 1024 * q), 16, xo[q],
+                                                 uniform_offset(u * kB2mRound * 2), 0, 0);
+}
+
+// Waits until the older of the two rounds in flight has landed: a round issues one code
+// load, one scale load and eight activation loads (in-order vmcnt).
+__device__ __forceinline__ void b2m_wait_round() {
+    constexpr int n = 10;
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
+}
+
+// This lane's code piece and scales of round u.
+template <int GS>
+__device__ __forceinline__ void b2m_load(uint4& cp, uint4& sp, __amdgpu_buffer_rsrc_t pr,
+                                         __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
+                                         uint32_t vo_scale, int u) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code,
+                                                          uniform_offset((int64_t)u * 64), 0);
+    cp = make_uint4(v.x, v.y, v.z, v.w);
+    const int so = uniform_offset((int64_t)u * (2 * kB2mRound / GS));
+    if constexpr (GS == 8) {
+        const u32x4 s = __builtin_amdgcn_raw_buffer_load_b128(sr, vo_scale, so, 0);
+        sp = make_uint4(s.x, s.y, s.z, s.w);
+    } else if constexpr (GS == 16) {
+        const auto s = __builtin_amdgcn_raw_buffer_load_b64(sr, vo_scale, so, 0);
+        sp = make_uint4(s[0], s[1], 0u, 0u);
+    } else if constexpr (GS == 32) {
+        sp = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(sr, vo_scale, so, 0), 0u, 0u, 0u);
+    } else {
+        sp = make_uint4(__builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale, so, 0), 0u, 0u, 0u);
+    }
+}
+
+template <int DT, int GS>
+__global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
+    const void* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
+    int M, int64_t N, int64_t K) {
+    static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "2-bit group size 8..64");
+    __shared__ uint4 lut_storage[kB2LutU4];
+    // two activation buffers per wave, separate LDS objects (see gemv2_kernel)
+    __shared__ __attribute__((aligned(128))) char xs0[kB2Waves * kB2mXBytes];
+    __shared__ __attribute__((aligned(128))) char xs1[kB2Waves * kB2mXBytes];
+    __shared__ f32x4 red[kB2Waves][64];
+
+    fill_b2sel<64 * kB2Waves>(lut_storage);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t tile = blockIdx.x;
+    const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+    // rows past N read zeros (buffer bound) and are never stored
+    const uint32_t row = (uint32_t)(tile * 16 + i16);
+    const uint32_t vo_code = row * rowbytes + 16u * g;
+    const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
+    const uint32_t slot = (uint32_t)(lane & 31) * 4u;
+    uint32_t xo_ld[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xo_ld[q] = b2m_x_offset(q, lane, M, K);
+    const uint32_t gu = (uint32_t)g, iu = (uint32_t)i16;
+    const uint32_t xo = (uint32_t)wave * kB2mXBytes + 512u * iu +
+                        16u * ((8u * gu & 16u) | ((8u * gu & 8u) ^ (iu & 8u)) | (iu & 7u));
+    char* const xw0 = xs0 + wave * kB2mXBytes;
+    char* const xw1 = xs1 + wave * kB2mXBytes;
+
+    // wave w takes rounds w, w + W, ...; round u + W is fetched while round u computes
+    const int T = (int)(K / kB2mRound);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    uint4 cp[2], sp[2];
+    int u = wave;
+    if (u < T) {
+        b2m_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u);
+        b2m_stage_x(xw0, xr, u, xo_ld);
+    }
+    __syncthreads();  // selector table ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage);
+    // rounds in pairs, as in gemv2_kernel
+    while (u + kB2Waves < T) {  // uniform within the wave
+        b2m_load<GS>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        b2m_stage_x(xw1, xr, u + kB2Waves, xo_ld);
+        b2m_wait_round();  // round u's codes, scales and activations have landed
+        B2mRound<DT, GS>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+        lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
+        const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
+        b2m_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, un);
+        b2m_stage_x(xw0, xr, un, xo_ld);
+        b2m_wait_round();
+        B2mRound<DT, GS>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
+        lds_wait_all();
+        u += 2 * kB2Waves;
+    }
+    vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
+    if (u < T) B2mRound<DT, GS>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+
+    // add the waves' partial sums; lane (g, n) holds rows m = 4g + q of column n
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w2 = 1; w2 < kB2Waves; ++w2) {
+        const f32x4 o = red[w2][lane];
+        acc[0] += o[0];
+        acc[1] += o[1];
+        acc[2] += o[2];
+        acc[3] += o[3];
+    }
+    if ((int64_t)row < N) {
+        const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = 4 * g + q;
+            if (m < M) store_from_f32<DT>(y, (int64_t)m * N + row, acc[q] + bv);
+        }
     }
 }
 
@@ -1542,6 +1782,49 @@ static hipError_t launch_gemv2_gs(const void* x, const uint8_t* packed, const ui
         case 32: return launch_gemv2_t<DT, MM, 32>(x, packed, scales, bias, y, M, N, K, stream);
         default: return launch_gemv2_t<DT, MM, 64>(x, packed, scales, bias, y, M, N, K, stream);
     }
+}
+
+bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                      const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+    if (dt != kBF16 && dt != kF16) return false;
+    if (M < 1 || M > 16 || N < 1 || K < kB2mRound || K % kB2mRound != 0) return false;
+    if (gs != 8 && gs != 16 && gs != 32 && gs != 64) return false;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 15u) || ((uintptr_t)scales & 15u) ||
+        ((uintptr_t)y & 1u))
+        return false;
+    if ((N + 16) * (K / 4) >= (1ll << 31) || (N + 16) * (K * 2 / gs) >= (1ll << 31) ||
+        M * K * 2 >= (1ll << 31))
+        return false;
+    return true;
+}
+
+template <int DT, int GS>
+static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const uint16_t* scales,
+                                  const void* bias, void* y, int M, int64_t N, int64_t K,
+                                  hipStream_t stream) {
+    const int64_t wgs = (N + 15) / 16;  // one 16-row tile per workgroup
+    hipLaunchKernelGGL((gemv2m_kernel<DT, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
+                       stream, x, packed, scales, bias, y, M, N, K);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_gemv2m_gs(const void* x, const uint8_t* packed, const uint16_t* scales,
+                                   const void* bias, void* y, int M, int64_t N, int64_t K,
+                                   int64_t gs, hipStream_t stream) {
+    switch (gs) {
+        case 8: return launch_gemv2m_t<DT, 8>(x, packed, scales, bias, y, M, N, K, stream);
+        case 16: return launch_gemv2m_t<DT, 16>(x, packed, scales, bias, y, M, N, K, stream);
+        case 32: return launch_gemv2m_t<DT, 32>(x, packed, scales, bias, y, M, N, K, stream);
+        default: return launch_gemv2m_t<DT, 64>(x, packed, scales, bias, y, M, N, K, stream);
+    }
+}
+
+hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* scales,
+                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                         int dt, hipStream_t stream) {
+    return dt == kBF16 ? launch_gemv2m_gs<kBF16>(x, packed, scales, bias, y, (int)M, N, K, gs, stream)
+                       : launch_gemv2m_gs<kF16>(x, packed, scales, bias, y, (int)M, N, K, gs, stream);
 }
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,

@@ -233,6 +233,35 @@ def test_e8b_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
 
 
 @pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (5, 4100, 1024, 8, torch.bfloat16),    # ragged last tile, one round per wave
+    (8, 1000, 768, 16, torch.float16),     # three rounds: one wave idle
+    (16, 777, 2048, 32, torch.bfloat16),   # one round pair per wave
+    (16, 64, 5120, 64, torch.bfloat16),    # five rounds per wave: pairs and a tail round
+    (12, 4096, 14336, 8, torch.bfloat16),  # down-projection shape
+    (2, 300, 256, 32, torch.float16),      # M <= 4 with K % 1024 != 0; a single round
+    (16, 16, 256, 8, torch.float16),
+    (9, 4096, 4096, 32, torch.bfloat16),
+])
+def test_e8b_gemv16_kernel_matches_oracle(M, N, K, gs, dtype):
+    # M <= 16 (above 4, or K % 1024 != 0), K % 256 == 0 and gs in {8, 16, 32, 64} select
+    # the 2-bit GEMV with the weights in the B operand
+    pk, sc, pk_np, sc_np = _layer2(N, K, seed=3 * N + K + gs, gs=gs)
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"e8b gemv16 M={M} N={N} K={K} gs={gs} {dtype}", flush=True)
+    y = ops.e8_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, gs)
+    y_nb = ops.e8_linear(x.to(DEV), pk, sc, None, N, K, gs)
+    torch.cuda.synchronize()
+    ref = O.e8b_gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, gs,
+                         DT_CODE[dtype])
+    ref_nb = O.e8b_gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, gs, DT_CODE[dtype])
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel_err(y, ref) <= REL_TOL
+    assert _rel_err(y_nb, ref_nb) <= REL_TOL
+
+
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
     (17, 256, 512, 8, torch.bfloat16),
     (100, 1000, 256, 16, torch.float16),
     (256, 256, 1024, 32, torch.bfloat16),
@@ -241,10 +270,10 @@ def test_e8b_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
     (64, 4096, 64, 32, torch.bfloat16),
     (40, 1024, 4096, 8, torch.bfloat16),   # small grid: K split over 16 steps per split
     (201, 301, 1344, 16, torch.float16),   # 21 K steps over uneven splits, ragged M and N
-    (8, 2048, 2048, 64, torch.float16),    # decode-sized batch on the MFMA kernel
+    (20, 2048, 2048, 64, torch.float16),   # small batch just above the GEMV range
 ])
 def test_e8b_prefill_mfma_matches_oracle(M, N, K, gs, dtype):
-    # K % 64 == 0, gs in {8, 16, 32, 64} and M > 4 (or K % 1024 != 0) select the MFMA GEMM
+    # K % 64 == 0, gs in {8, 16, 32, 64} and M > 16 (or K % 256 != 0) select the MFMA GEMM
     # with the 2-bit weight decoder
     pk, sc, pk_np, sc_np = _layer2(N, K, seed=M + N + K + gs, gs=gs)
     g = torch.Generator().manual_seed(M * 3 + K)
