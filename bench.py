@@ -100,7 +100,7 @@ def parse_args():
     ap.add_argument("--e2e-layers", type=int, default=32)
     ap.add_argument("--encode-layers", type=int, default=32)
     ap.add_argument("--e8b-layers", type=int, default=8,
-                    help="layers of the 2-bit E8 stack (0: skip that leg)")
+                    help="layers of the 2-bit and 1-bit E8 stacks (0: skip those legs)")
     ap.add_argument("--decode-m", type=str, default=",".join(map(str, DECODE_M)),
                     help="decode batch sizes of the headline step (profiling runs pick one)")
     ap.add_argument("--no-per-linear", action="store_true",
@@ -411,13 +411,24 @@ def bench_encode(torch, N_, dev, layers: int, reps: int = 3, check_rows: int = 6
 E8B_GS = 32  # pack_model_e8's default group size (reference lattice.py:905)
 
 
-def e8b_weight_bytes(N: int, K: int, gs: int = E8B_GS) -> int:
-    return N * K // 4 + N * K // gs * 2
+def e8b_weight_bytes(N: int, K: int, gs: int = E8B_GS, per_byte: int = 4) -> int:
+    return N * K // per_byte + N * K // gs * 2
+
+
+# Low-bit formats of the leg below: C entry points, weights per code byte, CPU oracle encoder,
+# GPU decoder (ops) name.
+LOWBIT = {
+    "2bit": dict(encode="ojx_e8_encode", gemm="ojx_e8_gemm_fwd", per_byte=4,
+                 oracle="e8b_encode", decode="decode2"),
+    "root": dict(encode="ojx_e8r_encode", gemm="ojx_e8r_gemm_fwd", per_byte=8,
+                 oracle="e8r_encode", decode="decode1"),
+}
 
 
 def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m: int = 512,
-              check_rows: int = 32):
-    """2-bit E8 (E8LatticePacker, the default bitrate of E8LatticeLinear/pack_model_e8): a
+              check_rows: int = 32, fmt: str = "2bit"):
+    """2-bit E8 (E8LatticePacker, the default bitrate of E8LatticeLinear/pack_model_e8), or
+    with fmt "root" the 1-bit Root E8 (RootE8LatticePacker) in the same layout of work: a
     `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights (seed 9700 + 7*layer +
     j), group size 32.  Encoder: the stack's encode launches replayed from one hipGraph,
     layer 0 of each shape checked bit for bit against the CPU oracle on its first
@@ -430,16 +441,18 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     from oracle import oracle as O
 
     lib = N_.lib()
+    F = LOWBIT[fmt]
+    enc_fn, gemm_fn, per_byte = getattr(lib, F["encode"]), getattr(lib, F["gemm"]), F["per_byte"]
     items = []
     for layer in range(layers):
         for j, (name, N, K) in enumerate(LAYER_SHAPES):
             g = torch.Generator(device=dev).manual_seed(9700 + 7 * layer + j)
             w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
-            packed = torch.empty(N * K // 4, dtype=torch.uint8, device=dev)
+            packed = torch.empty(N * K // per_byte, dtype=torch.uint8, device=dev)
             scales = torch.empty(N * K // E8B_GS, dtype=torch.float16, device=dev)
             items.append(dict(w=w, packed=packed, scales=scales, name=name, N=N, K=K))
     numel = sum(it["N"] * it["K"] for it in items)
-    wbytes = sum(e8b_weight_bytes(it["N"], it["K"]) for it in items)
+    wbytes = sum(e8b_weight_bytes(it["N"], it["K"], per_byte=per_byte) for it in items)
     stream = torch.cuda.current_stream()
 
     def eager_ms(launch_all, reps):
@@ -476,16 +489,15 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
 
     def encode_all(h):
         for it in items:
-            N_.check(lib.ojx_e8_encode(it["w"].data_ptr(), N_.F16, it["w"].numel(), E8B_GS,
-                                       it["packed"].data_ptr(), it["scales"].data_ptr(), h),
-                     "e8 encode")
+            N_.check(enc_fn(it["w"].data_ptr(), N_.F16, it["w"].numel(), E8B_GS,
+                            it["packed"].data_ptr(), it["scales"].data_ptr(), h), "encode")
 
     enc_ms = replay_ms(encode_all, 3)
     exact = True
     for it in items[:7]:
         rows, K = min(check_rows, it["N"]), it["K"]
-        ref_pk, ref_sc, _ = O.e8b_encode(it["w"][:rows].float().cpu().numpy(), E8B_GS)
-        got_pk = it["packed"][: rows * K // 4].cpu().numpy()
+        ref_pk, ref_sc, _ = getattr(O, F["oracle"])(it["w"][:rows].float().cpu().numpy(), E8B_GS)
+        got_pk = it["packed"][: rows * K // per_byte].cpu().numpy()
         got_sc = it["scales"][: rows * K // E8B_GS].cpu().view(torch.int16).numpy().view(np.uint16)
         exact = exact and np.array_equal(got_pk, ref_pk) and np.array_equal(got_sc, ref_sc)
     for it in items:
@@ -499,17 +511,17 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
 
         def launch_all(h):
             for it, y in zip(items, ys):
-                N_.check(lib.ojx_e8_gemm_fwd(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
-                                             it["scales"].data_ptr(), None, y.data_ptr(), M,
-                                             it["N"], it["K"], E8B_GS, N_.BF16, h), "e8 gemm")
+                N_.check(gemm_fn(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
+                                 it["scales"].data_ptr(), None, y.data_ptr(), M, it["N"], it["K"],
+                                 E8B_GS, N_.BF16, h), "gemm")
 
         ms = replay_ms(launch_all, steps) if M <= 16 else eager_ms(launch_all, steps)
         worst = 0.0
         from ojasx_amd import ops
         for idx in (0, 4, 6):  # q, gate, down of layer 0
             it = items[idx]
-            wd = ops.decode2(it["packed"], it["scales"], it["N"] * it["K"], E8B_GS,
-                             torch.bfloat16).view(it["N"], it["K"]).float()
+            wd = getattr(ops, F["decode"])(it["packed"], it["scales"], it["N"] * it["K"], E8B_GS,
+                                           torch.bfloat16).view(it["N"], it["K"]).float()
             ref = xs[it["K"]].float() @ wd.t().contiguous()
             err = (ys[idx].float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
             worst = max(worst, err)
@@ -966,6 +978,10 @@ def main() -> int:
         result["e8_2bit"] = bench_e8b(torch, N_, dev, args.e8b_layers, args.steps)
         log(f"2-bit: decode M=1 {result['e8_2bit']['decode_per_linear']['1']['weight_GBs']} GB/s, "
             f"encode {result['e8_2bit']['encode']['Gweights_s']} Gweights/s")
+        torch.cuda.empty_cache()
+        log(f"1-bit Root E8 ({args.e8b_layers}-layer stack)")
+        result["e8_1bit"] = bench_e8b(torch, N_, dev, args.e8b_layers, args.steps, fmt="root")
+        log(f"1-bit: decode M=16 {result['e8_1bit']['decode_per_linear']['16']['weight_GBs']} GB/s")
     if not args.no_e2e:
         torch.cuda.empty_cache()
         log(f"end-to-end decoder ({args.e2e_layers} layers)")

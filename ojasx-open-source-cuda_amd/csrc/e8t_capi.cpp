@@ -338,8 +338,9 @@ __attribute__((visibility("default"))) int ojx_e8_gemm_fwd(const void* x, const 
     if (ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
         return done(ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
                     "e8 gemv launch");
-    if (ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype))
-        return done(ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
+    if (ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, ojx::kFmt2Bit))
+        return done(ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
+                                       ojx::kFmt2Bit),
                     "e8 gemv launch");
     if (ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, ojx::kFmt2Bit))
         return done(launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmt2Bit),
@@ -422,6 +423,10 @@ __attribute__((visibility("default"))) int ojx_e8r_gemm_fwd(const void* x, const
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
     hipStream_t s = (hipStream_t)stream;
+    if (ojx::gemv2m_supported(x, codes, scales, y, M, N, K, gs, dtype, ojx::kFmtRoot))
+        return done(ojx::launch_gemv2m(x, codes, scales, bias, y, M, N, K, gs, dtype, s,
+                                       ojx::kFmtRoot),
+                    "e8r gemv launch");
     if (ojx::gemm_mfma_supported(x, codes, scales, M, N, K, gs, dtype, ojx::kFmtRoot))
         return done(launch_mfma(x, codes, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmtRoot),
                     "e8r gemm_mfma launch");

@@ -271,26 +271,6 @@ struct Bit2RowDecoder {
 // except an fp16 overflow of 2 s).  Per scale group the table {S0 = s | rnd(2s) << 16,
 // S1 = -s | -rnd(2s) << 16}; a 256-entry LDS table (4 KB, `kSel1Entries`) maps a code to
 // four v_perm_b32 selector words (selector byte 12 gives the zero bytes).
-constexpr int kSel1Entries = 256;
-
-__device__ __forceinline__ void fill_sel1(uint4* tab, int nthreads) {
-    for (int e = (int)threadIdx.x; e < kSel1Entries; e += nthreads) {
-        uint32_t w[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h)
-            w[h] = root_sel_pair(kRootTable.c[e][2 * h]) |
-                   (root_sel_pair(kRootTable.c[e][2 * h + 1]) << 16);
-        tab[e] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-}
-
-template <int DT>
-__device__ __forceinline__ uint2 values1(uint32_t s16) {
-    const float s = scale_for<DT>(s16 & 0xFFFFu);
-    const uint32_t a = rnd_bits<DT>(s), b = rnd_bits<DT>(2.0f * s);
-    return make_uint2(a | (b << 16), (a ^ 0x8000u) | ((b ^ 0x8000u) << 16));
-}
-
 template <int DT, int GS>
 struct RootRowDecoder {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "1-bit group size 8..64");

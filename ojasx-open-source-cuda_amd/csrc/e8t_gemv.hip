@@ -32,6 +32,7 @@
 #include "e8t_device.h"
 #include "e8t_internal.h"
 #include "e8t_lut.h"
+#include "e8t_root.h"
 
 #include <utility>
 
@@ -1434,6 +1435,32 @@ __device__ __forceinline__ uint4 b2m_operand(const uint4& cp, const uint2& val, 
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// B operand (8 weights) of 1-bit code byte H of this lane's 8 code bytes: the code's four
+// selector words from the 256-entry table, applied to the group's value words.
+template <int H>
+__device__ __forceinline__ uint4 root_operand(const uint4& cp, const uint2& val, const char* tab) {
+    const uint32_t byte = ((H < 4 ? cp.x : cp.y) >> (8 * (H % 4))) & 0xFFu;
+    const uint4 sel = *reinterpret_cast<const uint4*>(tab + 16u * byte);
+    return make_uint4(__builtin_amdgcn_perm(val.x, val.y, sel.x),
+                      __builtin_amdgcn_perm(val.x, val.y, sel.y),
+                      __builtin_amdgcn_perm(val.x, val.y, sel.z),
+                      __builtin_amdgcn_perm(val.x, val.y, sel.w));
+}
+
+// Value words of a scale group in format FMT (2-bit or 1-bit Root E8).
+template <int DT, int FMT>
+__device__ __forceinline__ uint2 values_of(uint32_t s16) {
+    if constexpr (FMT == kFmtRoot) return values1<DT>(s16);
+    else return values2<DT>(s16);
+}
+
+template <int FMT, int H>
+__device__ __forceinline__ uint4 operand_of(const uint4& cp, const uint2& val, const char* lut,
+                                            uint32_t slot) {
+    if constexpr (FMT == kFmtRoot) return root_operand<H>(cp, val, lut);
+    else return b2m_operand<H>(cp, val, lut, slot);
+}
+
 // Scale (fp16 bits) of step H from this lane's scales of the round (64/GS of them).
 template <int GS, int H>
 __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
@@ -1445,7 +1472,7 @@ __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
 // Step h's A fragment: with the lane's offset xo = 8192 w + 512 i16 + 16 ((8g & 16) |
 // ((8g & 8) ^ (i16 & 8)) | (i16 & 7)) (bits 4..6 equal to i16 & 7), piece 8g + h of row
 // i16 sits at xs + (xo ^ 16 h).
-template <int DT, int GS>
+template <int DT, int GS, int FMT>
 struct B2mRound {
     // step H: the A fragment and B operand of step H + 1 are formed before the MFMA of
     // step H is issued
@@ -1456,9 +1483,9 @@ struct B2mRound {
                                                 f32x4& acc) {
         uint4 a_n, b_n;
         if constexpr (H + 1 < 8) {
-            if constexpr ((8 * (H + 1)) % GS == 0) val = values2<DT>(b2m_scale<GS, H + 1>(sp));
+            if constexpr ((8 * (H + 1)) % GS == 0) val = values_of<DT, FMT>(b2m_scale<GS, H + 1>(sp));
             a_n = *reinterpret_cast<const uint4*>(xs + (xo ^ (16u * (H + 1))));
-            b_n = b2m_operand<H + 1>(cp, val, lut, slot);
+            b_n = operand_of<FMT, H + 1>(cp, val, lut, slot);
         }
         acc = mfma16<DT>(a_cur, b_cur, acc);
         if constexpr (H + 1 < 8) {
@@ -1477,9 +1504,9 @@ struct B2mRound {
     __device__ __forceinline__ static void run(const uint4& cp, const uint4& sp, const char* lut,
                                                uint32_t slot, const char* xs, uint32_t xo,
                                                f32x4& acc) {
-        uint2 val = values2<DT>(b2m_scale<GS, 0>(sp));
+        uint2 val = values_of<DT, FMT>(b2m_scale<GS, 0>(sp));
         uint4 a = *reinterpret_cast<const uint4*>(xs + xo);
-        uint4 b = b2m_operand<0>(cp, val, lut, slot);
+        uint4 b = operand_of<FMT, 0>(cp, val, lut, slot);
         steps(cp, sp, lut, slot, xs, xo, a, b, val, acc, std::make_integer_sequence<int, 8>{});
     }
 };
@@ -1515,13 +1542,19 @@ __device__ __forceinline__ void b2m_wait_round() {
 }
 
 // This lane's code piece and scales of round u.
-template <int GS>
+template <int GS, int FMT>
 __device__ __forceinline__ void b2m_load(uint4& cp, uint4& sp, __amdgpu_buffer_rsrc_t pr,
                                          __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
                                          uint32_t vo_scale, int u) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code,
-                                                          uniform_offset((int64_t)u * 64), 0);
-    cp = make_uint4(v.x, v.y, v.z, v.w);
+    if constexpr (FMT == kFmtRoot) {  // 8 code bytes (64 weights)
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(pr, vo_code,
+                                                            uniform_offset((int64_t)u * 32), 0);
+        cp = make_uint4(v[0], v[1], 0u, 0u);
+    } else {                          // 16 code bytes (64 weights)
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code,
+                                                              uniform_offset((int64_t)u * 64), 0);
+        cp = make_uint4(v.x, v.y, v.z, v.w);
+    }
     const int so = uniform_offset((int64_t)u * (2 * kB2mRound / GS));
     if constexpr (GS == 8) {
         const u32x4 s = __builtin_amdgcn_raw_buffer_load_b128(sr, vo_scale, so, 0);
@@ -1536,25 +1569,29 @@ __device__ __forceinline__ void b2m_load(uint4& cp, uint4& sp, __amdgpu_buffer_r
     }
 }
 
-template <int DT, int GS>
+template <int DT, int GS, int FMT>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     int M, int64_t N, int64_t K) {
-    static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "2-bit group size 8..64");
-    __shared__ uint4 lut_storage[kB2LutU4];
+    static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
+    static_assert(FMT == kFmt2Bit || FMT == kFmtRoot, "2-bit or 1-bit codes");
+    // 2-bit: nibble -> selector (32 copies); 1-bit: code -> four selectors
+    __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries : kB2LutU4];
     // two activation buffers per wave, separate LDS objects (see gemv2_kernel)
     __shared__ __attribute__((aligned(128))) char xs0[kB2Waves * kB2mXBytes];
     __shared__ __attribute__((aligned(128))) char xs1[kB2Waves * kB2mXBytes];
     __shared__ f32x4 red[kB2Waves][64];
 
-    fill_b2sel<64 * kB2Waves>(lut_storage);
+    if constexpr (FMT == kFmtRoot) fill_sel1(lut_storage, 64 * kB2Waves);
+    else fill_b2sel<64 * kB2Waves>(lut_storage);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
     const int64_t tile = blockIdx.x;
-    const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
+    constexpr uint32_t kCodeDiv = FMT == kFmtRoot ? 8u : 4u;  // weights per code byte
+    const uint32_t rowbytes = (uint32_t)(K / kCodeDiv), srowbytes = (uint32_t)(K * 2 / GS);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
@@ -1563,7 +1600,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
     // rows past N read zeros (buffer bound) and are never stored
     const uint32_t row = (uint32_t)(tile * 16 + i16);
-    const uint32_t vo_code = row * rowbytes + 16u * g;
+    const uint32_t vo_code = row * rowbytes + (64u / kCodeDiv) * g;
     const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
     const uint32_t slot = (uint32_t)(lane & 31) * 4u;
     uint32_t xo_ld[8];
@@ -1581,28 +1618,28 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     uint4 cp[2], sp[2];
     int u = wave;
     if (u < T) {
-        b2m_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u);
+        b2m_load<GS, FMT>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u);
         b2m_stage_x(xw0, xr, u, xo_ld);
     }
     __syncthreads();  // selector table ready
     const char* lut = reinterpret_cast<const char*>(lut_storage);
     // rounds in pairs, as in gemv2_kernel
     while (u + kB2Waves < T) {  // uniform within the wave
-        b2m_load<GS>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        b2m_load<GS, FMT>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
         b2m_stage_x(xw1, xr, u + kB2Waves, xo_ld);
         b2m_wait_round();  // round u's codes, scales and activations have landed
-        B2mRound<DT, GS>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+        B2mRound<DT, GS, FMT>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
         const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
-        b2m_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, un);
+        b2m_load<GS, FMT>(cp[0], sp[0], pr, sr, vo_code, vo_scale, un);
         b2m_stage_x(xw0, xr, un, xo_ld);
         b2m_wait_round();
-        B2mRound<DT, GS>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
+        B2mRound<DT, GS, FMT>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
         lds_wait_all();
         u += 2 * kB2Waves;
     }
     vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
-    if (u < T) B2mRound<DT, GS>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+    if (u < T) B2mRound<DT, GS, FMT>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
 
     // add the waves' partial sums; lane (g, n) holds rows m = 4g + q of column n
     red[wave][lane] = acc;
@@ -1785,46 +1822,55 @@ static hipError_t launch_gemv2_gs(const void* x, const uint8_t* packed, const ui
 }
 
 bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                      const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+                      const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
+                      int fmt) {
+    if (fmt != kFmt2Bit && fmt != kFmtRoot) return false;
     if (dt != kBF16 && dt != kF16) return false;
     if (M < 1 || M > 16 || N < 1 || K < kB2mRound || K % kB2mRound != 0) return false;
     if (gs != 8 && gs != 16 && gs != 32 && gs != 64) return false;
     if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 15u) || ((uintptr_t)scales & 15u) ||
         ((uintptr_t)y & 1u))
         return false;
-    if ((N + 16) * (K / 4) >= (1ll << 31) || (N + 16) * (K * 2 / gs) >= (1ll << 31) ||
+    if ((N + 16) * (K / (fmt == kFmtRoot ? 8 : 4)) >= (1ll << 31) ||
+        (N + 16) * (K * 2 / gs) >= (1ll << 31) ||
         M * K * 2 >= (1ll << 31))
         return false;
     return true;
 }
 
-template <int DT, int GS>
+template <int DT, int GS, int FMT>
 static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream) {
     const int64_t wgs = (N + 15) / 16;  // one 16-row tile per workgroup
-    hipLaunchKernelGGL((gemv2m_kernel<DT, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
-                       stream, x, packed, scales, bias, y, M, N, K);
+    hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT>), dim3((unsigned)wgs), dim3(64 * kB2Waves),
+                       0, stream, x, packed, scales, bias, y, M, N, K);
     return hipGetLastError();
 }
 
-template <int DT>
+template <int DT, int FMT>
 static hipError_t launch_gemv2m_gs(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int M, int64_t N, int64_t K,
                                    int64_t gs, hipStream_t stream) {
     switch (gs) {
-        case 8: return launch_gemv2m_t<DT, 8>(x, packed, scales, bias, y, M, N, K, stream);
-        case 16: return launch_gemv2m_t<DT, 16>(x, packed, scales, bias, y, M, N, K, stream);
-        case 32: return launch_gemv2m_t<DT, 32>(x, packed, scales, bias, y, M, N, K, stream);
-        default: return launch_gemv2m_t<DT, 64>(x, packed, scales, bias, y, M, N, K, stream);
+        case 8: return launch_gemv2m_t<DT, 8, FMT>(x, packed, scales, bias, y, M, N, K, stream);
+        case 16: return launch_gemv2m_t<DT, 16, FMT>(x, packed, scales, bias, y, M, N, K, stream);
+        case 32: return launch_gemv2m_t<DT, 32, FMT>(x, packed, scales, bias, y, M, N, K, stream);
+        default: return launch_gemv2m_t<DT, 64, FMT>(x, packed, scales, bias, y, M, N, K, stream);
     }
 }
 
 hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                         int dt, hipStream_t stream) {
-    return dt == kBF16 ? launch_gemv2m_gs<kBF16>(x, packed, scales, bias, y, (int)M, N, K, gs, stream)
-                       : launch_gemv2m_gs<kF16>(x, packed, scales, bias, y, (int)M, N, K, gs, stream);
+                         int dt, hipStream_t stream, int fmt) {
+    const int m = (int)M;
+    if (fmt == kFmtRoot)
+        return dt == kBF16
+                   ? launch_gemv2m_gs<kBF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream)
+                   : launch_gemv2m_gs<kF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream);
+    return dt == kBF16
+               ? launch_gemv2m_gs<kBF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream)
+               : launch_gemv2m_gs<kF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream);
 }
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,

@@ -38,13 +38,15 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                         int dt, hipStream_t stream);
 
-// 2-bit decode GEMV with the weights in the B operand (M <= 16, bf16/fp16, K % 256 == 0,
-// gs in {8, 16, 32, 64}, 16-byte aligned buffers).
+// Decode GEMV with the weights in the B operand for the 2-bit (fmt 1) and 1-bit Root-E8
+// (fmt 2) formats: M <= 16, bf16/fp16, K % 256 == 0, gs in {8, 16, 32, 64}, 16-byte aligned
+// buffers.
 bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                      const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+                      const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
+                      int fmt);
 hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                         int dt, hipStream_t stream);
+                         int dt, hipStream_t stream, int fmt);
 
 // General tiled kernels: any M, N, K >= 1 (flat layout), any dtype; fmt selects the code
 // format (0 ternary, 1 2-bit, 2 1-bit Root E8).

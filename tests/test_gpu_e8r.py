@@ -99,8 +99,9 @@ def _layer1(N, K, seed, gs):
 
 
 @pytest.mark.parametrize("M,N,K,gs,dtype", [
-    (1, 256, 512, 32, torch.bfloat16),      # MFMA kernel, small tiles
-    (5, 130, 1024, 8, torch.float16),
+    (1, 256, 512, 32, torch.bfloat16),      # decode GEMV
+    (5, 130, 1024, 8, torch.float16),       # decode GEMV, ragged last tile
+    (2, 256, 320, 32, torch.bfloat16),      # K % 256 != 0: MFMA kernel, small tiles
     (17, 256, 512, 16, torch.bfloat16),
     (100, 1000, 256, 64, torch.float16),
     (300, 520, 512, 32, torch.bfloat16),
@@ -124,6 +125,30 @@ def test_e8r_fwd_matches_oracle(M, N, K, gs, dtype):
         assert float(np.abs(y.cpu().numpy() - ref).max()) <= ABS_TOL_F32 * max(1.0, np.abs(ref).max())
     else:
         assert _rel_err(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (16, 777, 2048, 32, torch.bfloat16),    # one round pair per wave
+    (16, 64, 5120, 64, torch.float16),      # pairs and a tail round
+    (8, 1000, 768, 16, torch.bfloat16),     # three rounds: one wave idle
+    (12, 4096, 14336, 8, torch.bfloat16),   # down-projection shape
+    (1, 4096, 4096, 32, torch.bfloat16),
+    (4, 16, 256, 8, torch.float16),         # a single round
+])
+def test_e8r_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
+    # M <= 16, K % 256 == 0 and gs in {8, 16, 32, 64} select the decode GEMV (weights in
+    # the B operand from the value words and the code's selector words)
+    pk, sc, pk_np, sc_np = _layer1(N, K, seed=2 * N + K + gs, gs=gs)
+    g = torch.Generator().manual_seed(M * 11 + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"e8r gemv M={M} N={N} K={K} gs={gs} {dtype}", flush=True)
+    y = ops.e8r_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, gs)
+    torch.cuda.synchronize()
+    ref = O.e8r_gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, gs,
+                         DT_CODE[dtype])
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel_err(y, ref) <= REL_TOL
 
 
 def test_e8r_prefill_large_shape_against_decoded_matmul():
