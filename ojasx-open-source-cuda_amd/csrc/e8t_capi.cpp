@@ -151,6 +151,13 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
     hipStream_t s = (hipStream_t)stream;
+    // 4 < M <= 16 on a layer too small for the streaming mask kernel (< 1024 row tiles): one
+    // 16-row tile per workgroup, K split over its waves, weights in the B operand
+    if (M > 4 && (N + 15) / 16 < 1024 &&
+        ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, ojx::kFmtTernary))
+        return done(ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
+                                       ojx::kFmtTernary),
+                    "e8t gemv launch");
     if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, N, K, gs, dtype)) {
         ojx::GemvLaunch a{};
         ojx::GemvJob& j = a.inl[0];

@@ -1447,18 +1447,40 @@ __device__ __forceinline__ uint4 root_operand(const uint4& cp, const uint2& val,
                       __builtin_amdgcn_perm(val.x, val.y, sel.w));
 }
 
-// Value words of a scale group in format FMT (2-bit or 1-bit Root E8).
+// B operand (8 weights) of ternary code H of this lane's 8 codes (12 bytes in cp.x..z): the
+// two half-code mask entries of the bank-sliced table (e8t_lut.h) AND-ed with the group's
+// scale word s | s << 16 | 0x80008000 (val.x).
+template <int H>
+__device__ __forceinline__ uint4 ternary_operand(const uint4& cp, const uint2& val,
+                                                 const char* lut, uint32_t slot) {
+    const uint32_t d[3] = {cp.x, cp.y, cp.z};
+    const uint32_t z = code_z<H>(d, slot);
+    const uint32_t h = __umulhi(z, kHiMagic);
+    const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+    const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+    const uint32_t s = val.x;
+    return make_uint4(ml.x & s, ml.y & s, mh.x & s, mh.y & s);
+}
+
+// Value words of a scale group in format FMT: 2-bit or 1-bit Root E8 as above; ternary the
+// mask AND word of the one scale.
 template <int DT, int FMT>
 __device__ __forceinline__ uint2 values_of(uint32_t s16) {
     if constexpr (FMT == kFmtRoot) return values1<DT>(s16);
-    else return values2<DT>(s16);
+    else if constexpr (FMT == kFmt2Bit) return values2<DT>(s16);
+    else {
+        uint32_t w0, w1;
+        scale_words<DT>(s16, w0, w1);
+        return make_uint2(w0, 0u);
+    }
 }
 
 template <int FMT, int H>
 __device__ __forceinline__ uint4 operand_of(const uint4& cp, const uint2& val, const char* lut,
                                             uint32_t slot) {
     if constexpr (FMT == kFmtRoot) return root_operand<H>(cp, val, lut);
-    else return b2m_operand<H>(cp, val, lut, slot);
+    else if constexpr (FMT == kFmt2Bit) return b2m_operand<H>(cp, val, lut, slot);
+    else return ternary_operand<H>(cp, val, lut, slot);
 }
 
 // Scale (fp16 bits) of step H from this lane's scales of the round (64/GS of them).
@@ -1550,6 +1572,10 @@ __device__ __forceinline__ void b2m_load(uint4& cp, uint4& sp, __amdgpu_buffer_r
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(pr, vo_code,
                                                             uniform_offset((int64_t)u * 32), 0);
         cp = make_uint4(v[0], v[1], 0u, 0u);
+    } else if constexpr (FMT == kFmtTernary) {  // 12 code bytes (8 codes, 64 weights)
+        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(pr, vo_code,
+                                                             uniform_offset((int64_t)u * 48), 0);
+        cp = make_uint4(v.x, v.y, v.z, 0u);
     } else {                          // 16 code bytes (64 weights)
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code,
                                                               uniform_offset((int64_t)u * 64), 0);
@@ -1575,23 +1601,32 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
     int M, int64_t N, int64_t K) {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
-    static_assert(FMT == kFmt2Bit || FMT == kFmtRoot, "2-bit or 1-bit codes");
-    // 2-bit: nibble -> selector (32 copies); 1-bit: code -> four selectors
-    __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries : kB2LutU4];
+    static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
+    static_assert(FMT != kFmtTernary || GS == 32, "ternary GEMV: group size 32");
+    // ternary: half-code masks (bank-sliced); 2-bit: nibble -> selector (32 copies); 1-bit:
+    // code -> four selectors
+    __shared__ uint4 lut_storage[FMT == kFmtTernary ? kLutValidStorageU4
+                                 : FMT == kFmtRoot  ? kSel1Entries
+                                                    : kB2LutU4];
     // two activation buffers per wave, separate LDS objects (see gemv2_kernel)
     __shared__ __attribute__((aligned(128))) char xs0[kB2Waves * kB2mXBytes];
     __shared__ __attribute__((aligned(128))) char xs1[kB2Waves * kB2mXBytes];
     __shared__ f32x4 red[kB2Waves][64];
 
-    if constexpr (FMT == kFmtRoot) fill_sel1(lut_storage, 64 * kB2Waves);
+    if constexpr (FMT == kFmtTernary)
+        fill_lut<64 * kB2Waves, kLutValidEntries>(lut_storage, kLutMasks);
+    else if constexpr (FMT == kFmtRoot) fill_sel1(lut_storage, 64 * kB2Waves);
     else fill_b2sel<64 * kB2Waves>(lut_storage);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
     const int64_t tile = blockIdx.x;
-    constexpr uint32_t kCodeDiv = FMT == kFmtRoot ? 8u : 4u;  // weights per code byte
-    const uint32_t rowbytes = (uint32_t)(K / kCodeDiv), srowbytes = (uint32_t)(K * 2 / GS);
+    // code bytes per row, and per lane group (64 weights) of a round
+    const uint32_t rowbytes = (uint32_t)(FMT == kFmtTernary ? K * 3 / 16
+                                         : FMT == kFmtRoot  ? K / 8 : K / 4);
+    constexpr uint32_t kLaneBytes = FMT == kFmtTernary ? 12u : FMT == kFmtRoot ? 8u : 16u;
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
@@ -1600,9 +1635,10 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
     // rows past N read zeros (buffer bound) and are never stored
     const uint32_t row = (uint32_t)(tile * 16 + i16);
-    const uint32_t vo_code = row * rowbytes + (64u / kCodeDiv) * g;
+    const uint32_t vo_code = row * rowbytes + kLaneBytes * g;
     const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
-    const uint32_t slot = (uint32_t)(lane & 31) * 4u;
+    const uint32_t slot = FMT == kFmtTernary ? (uint32_t)(lane & (kLutSlots - 1)) * 8u
+                                             : (uint32_t)(lane & 31) * 4u;
     uint32_t xo_ld[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) xo_ld[q] = b2m_x_offset(q, lane, M, K);
@@ -1622,7 +1658,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
         b2m_stage_x(xw0, xr, u, xo_ld);
     }
     __syncthreads();  // selector table ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage);
+    const char* lut = reinterpret_cast<const char*>(lut_storage) +
+                      (FMT == kFmtTernary ? kLutBaseOffset : 0u);
     // rounds in pairs, as in gemv2_kernel
     while (u + kB2Waves < T) {  // uniform within the wave
         b2m_load<GS, FMT>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
@@ -1824,14 +1861,16 @@ static hipError_t launch_gemv2_gs(const void* x, const uint8_t* packed, const ui
 bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                       const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
                       int fmt) {
-    if (fmt != kFmt2Bit && fmt != kFmtRoot) return false;
+    if (fmt != kFmtTernary && fmt != kFmt2Bit && fmt != kFmtRoot) return false;
+    if (fmt == kFmtTernary && gs != 32) return false;
     if (dt != kBF16 && dt != kF16) return false;
     if (M < 1 || M > 16 || N < 1 || K < kB2mRound || K % kB2mRound != 0) return false;
     if (gs != 8 && gs != 16 && gs != 32 && gs != 64) return false;
     if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 15u) || ((uintptr_t)scales & 15u) ||
         ((uintptr_t)y & 1u))
         return false;
-    if ((N + 16) * (K / (fmt == kFmtRoot ? 8 : 4)) >= (1ll << 31) ||
+    const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : fmt == kFmtRoot ? K / 8 : K / 4;
+    if ((N + 16) * rowbytes >= (1ll << 31) ||
         (N + 16) * (K * 2 / gs) >= (1ll << 31) ||
         M * K * 2 >= (1ll << 31))
         return false;
@@ -1864,6 +1903,10 @@ hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* s
                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                          int dt, hipStream_t stream, int fmt) {
     const int m = (int)M;
+    if (fmt == kFmtTernary)  // group size 32 only
+        return dt == kBF16
+                   ? launch_gemv2m_t<kBF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream)
+                   : launch_gemv2m_t<kF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream);
     if (fmt == kFmtRoot)
         return dt == kBF16
                    ? launch_gemv2m_gs<kBF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream)

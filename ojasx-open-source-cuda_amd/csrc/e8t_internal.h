@@ -38,9 +38,9 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                         int dt, hipStream_t stream);
 
-// Decode GEMV with the weights in the B operand for the 2-bit (fmt 1) and 1-bit Root-E8
-// (fmt 2) formats: M <= 16, bf16/fp16, K % 256 == 0, gs in {8, 16, 32, 64}, 16-byte aligned
-// buffers.
+// Decode GEMV with the weights in the B operand for the ternary (fmt 0, gs 32), 2-bit (fmt 1)
+// and 1-bit Root-E8 (fmt 2) formats: M <= 16, bf16/fp16, K % 256 == 0, gs in {8, 16, 32, 64},
+// 16-byte aligned buffers.
 bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                       const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
                       int fmt);
