@@ -1494,41 +1494,58 @@ __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
 // Step h's A fragment: with the lane's offset xo = 8192 w + 512 i16 + 16 ((8g & 16) |
 // ((8g & 8) ^ (i16 & 8)) | (i16 & 7)) (bits 4..6 equal to i16 & 7), piece 8g + h of row
 // i16 sits at xs + (xo ^ 16 h).
-template <int DT, int GS, int FMT>
+#ifndef OJX_B2M_TILES
+#define OJX_B2M_TILES 1
+#endif
+constexpr int kB2mTiles = OJX_B2M_TILES;  // 16-row tiles per workgroup (each wave takes all)
+static_assert(kB2mTiles == 1 || kB2mTiles == 2, "one or two tiles");
+
+template <int DT, int GS, int FMT, int R>
 struct B2mRound {
-    // step H: the A fragment and B operand of step H + 1 are formed before the MFMA of
-    // step H is issued
+    // step H: the A fragment and B operands of step H + 1 are formed before the MFMAs of
+    // step H are issued; the R tiles share the A fragment
     template <int H>
-    __device__ __forceinline__ static void step(const uint4& cp, const uint4& sp,
+    __device__ __forceinline__ static void step(const uint4 (&cp)[R], const uint4 (&sp)[R],
                                                 const char* lut, uint32_t slot, const char* xs,
-                                                uint32_t xo, uint4& a_cur, uint4& b_cur, uint2& val,
-                                                f32x4& acc) {
-        uint4 a_n, b_n;
+                                                uint32_t xo, uint4& a_cur, uint4 (&b_cur)[R],
+                                                uint2 (&val)[R], f32x4 (&acc)[R]) {
+        uint4 a_n, b_n[R];
         if constexpr (H + 1 < 8) {
-            if constexpr ((8 * (H + 1)) % GS == 0) val = values_of<DT, FMT>(b2m_scale<GS, H + 1>(sp));
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if constexpr ((8 * (H + 1)) % GS == 0)
+                    val[r] = values_of<DT, FMT>(b2m_scale<GS, H + 1>(sp[r]));
+                b_n[r] = operand_of<FMT, H + 1>(cp[r], val[r], lut, slot);
+            }
             a_n = *reinterpret_cast<const uint4*>(xs + (xo ^ (16u * (H + 1))));
-            b_n = operand_of<FMT, H + 1>(cp, val, lut, slot);
         }
-        acc = mfma16<DT>(a_cur, b_cur, acc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = mfma16<DT>(a_cur, b_cur[r], acc[r]);
         if constexpr (H + 1 < 8) {
             a_cur = a_n;
-            b_cur = b_n;
+#pragma unroll
+            for (int r = 0; r < R; ++r) b_cur[r] = b_n[r];
         }
     }
     template <int... H>
-    __device__ __forceinline__ static void steps(const uint4& cp, const uint4& sp,
+    __device__ __forceinline__ static void steps(const uint4 (&cp)[R], const uint4 (&sp)[R],
                                                  const char* lut, uint32_t slot, const char* xs,
-                                                 uint32_t xo, uint4& a, uint4& b, uint2& val,
-                                                 f32x4& acc,
+                                                 uint32_t xo, uint4& a, uint4 (&b)[R],
+                                                 uint2 (&val)[R], f32x4 (&acc)[R],
                                                  std::integer_sequence<int, H...>) {
         (step<H>(cp, sp, lut, slot, xs, xo, a, b, val, acc), ...);
     }
-    __device__ __forceinline__ static void run(const uint4& cp, const uint4& sp, const char* lut,
-                                               uint32_t slot, const char* xs, uint32_t xo,
-                                               f32x4& acc) {
-        uint2 val = values_of<DT, FMT>(b2m_scale<GS, 0>(sp));
+    __device__ __forceinline__ static void run(const uint4 (&cp)[R], const uint4 (&sp)[R],
+                                               const char* lut, uint32_t slot, const char* xs,
+                                               uint32_t xo, f32x4 (&acc)[R]) {
+        uint2 val[R];
+        uint4 b[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            val[r] = values_of<DT, FMT>(b2m_scale<GS, 0>(sp[r]));
+            b[r] = operand_of<FMT, 0>(cp[r], val[r], lut, slot);
+        }
         uint4 a = *reinterpret_cast<const uint4*>(xs + xo);
-        uint4 b = operand_of<FMT, 0>(cp, val, lut, slot);
         steps(cp, sp, lut, slot, xs, xo, a, b, val, acc, std::make_integer_sequence<int, 8>{});
     }
 };
@@ -1557,9 +1574,9 @@ __device__ __forceinline__ void b2m_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, 
 }
 
 // Waits until the older of the two rounds in flight has landed: a round issues one code
-// load, one scale load and eight activation loads (in-order vmcnt).
+// and one scale load per tile and eight activation loads (in-order vmcnt).
 __device__ __forceinline__ void b2m_wait_round() {
-    constexpr int n = 10;
+    constexpr int n = 2 * kB2mTiles + 8;
     __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
 }
 
@@ -1611,7 +1628,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     // two activation buffers per wave, separate LDS objects (see gemv2_kernel)
     __shared__ __attribute__((aligned(128))) char xs0[kB2Waves * kB2mXBytes];
     __shared__ __attribute__((aligned(128))) char xs1[kB2Waves * kB2mXBytes];
-    __shared__ f32x4 red[kB2Waves][64];
+    constexpr int R = kB2mTiles;
+    static_assert(R * 64 * 16 <= kB2mXBytes, "partial sums fit a wave's activation buffer");
 
     if constexpr (FMT == kFmtTernary)
         fill_lut<64 * kB2Waves, kLutValidEntries>(lut_storage, kLutMasks);
@@ -1634,9 +1652,13 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
     // rows past N read zeros (buffer bound) and are never stored
-    const uint32_t row = (uint32_t)(tile * 16 + i16);
-    const uint32_t vo_code = row * rowbytes + kLaneBytes * g;
-    const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
+    uint32_t vo_code[R], vo_scale[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row_r = (uint32_t)((tile * R + r) * 16 + i16);
+        vo_code[r] = row_r * rowbytes + kLaneBytes * g;
+        vo_scale[r] = row_r * srowbytes + (128u / GS) * g;
+    }
     const uint32_t slot = FMT == kFmtTernary ? (uint32_t)(lane & (kLutSlots - 1)) * 8u
                                              : (uint32_t)(lane & 31) * 4u;
     uint32_t xo_ld[8];
@@ -1650,11 +1672,15 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
 
     // wave w takes rounds w, w + W, ...; round u + W is fetched while round u computes
     const int T = (int)(K / kB2mRound);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    uint4 cp[2], sp[2];
+    f32x4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 cp[2][R], sp[2][R];
     int u = wave;
     if (u < T) {
-        b2m_load<GS, FMT>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u);
+        #pragma unroll
+        for (int r = 0; r < R; ++r)
+            b2m_load<GS, FMT>(cp[0][r], sp[0][r], pr, sr, vo_code[r], vo_scale[r], u);
         b2m_stage_x(xw0, xr, u, xo_ld);
     }
     __syncthreads();  // selector table ready
@@ -1662,40 +1688,52 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
                       (FMT == kFmtTernary ? kLutBaseOffset : 0u);
     // rounds in pairs, as in gemv2_kernel
     while (u + kB2Waves < T) {  // uniform within the wave
-        b2m_load<GS, FMT>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        #pragma unroll
+        for (int r = 0; r < R; ++r)
+            b2m_load<GS, FMT>(cp[1][r], sp[1][r], pr, sr, vo_code[r], vo_scale[r], u + kB2Waves);
         b2m_stage_x(xw1, xr, u + kB2Waves, xo_ld);
         b2m_wait_round();  // round u's codes, scales and activations have landed
-        B2mRound<DT, GS, FMT>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+        B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
         const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
-        b2m_load<GS, FMT>(cp[0], sp[0], pr, sr, vo_code, vo_scale, un);
+        #pragma unroll
+        for (int r = 0; r < R; ++r)
+            b2m_load<GS, FMT>(cp[0][r], sp[0][r], pr, sr, vo_code[r], vo_scale[r], un);
         b2m_stage_x(xw0, xr, un, xo_ld);
         b2m_wait_round();
-        B2mRound<DT, GS, FMT>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
+        B2mRound<DT, GS, FMT, R>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
         lds_wait_all();
         u += 2 * kB2Waves;
     }
     vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
-    if (u < T) B2mRound<DT, GS, FMT>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+    if (u < T) B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
 
-    // add the waves' partial sums; lane (g, n) holds rows m = 4g + q of column n
-    red[wave][lane] = acc;
+    // add the waves' partial sums (each wave's in its own, no longer read, part of buffer 0);
+    // lane (g, n) holds rows m = 4g + q of column n
+    f32x4* const red = reinterpret_cast<f32x4*>(xs0);
+    constexpr int kRedWave = kB2mXBytes / 16;  // f32x4 slots per wave
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[wave * kRedWave + r * 64 + lane] = acc[r];
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int w2 = 1; w2 < kB2Waves; ++w2) {
-        const f32x4 o = red[w2][lane];
-        acc[0] += o[0];
-        acc[1] += o[1];
-        acc[2] += o[2];
-        acc[3] += o[3];
-    }
-    if ((int64_t)row < N) {
-        const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
+    for (int r = 0; r < R; ++r) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int m = 4 * g + q;
-            if (m < M) store_from_f32<DT>(y, (int64_t)m * N + row, acc[q] + bv);
+        for (int w2 = 1; w2 < kB2Waves; ++w2) {
+            const f32x4 o = red[w2 * kRedWave + r * 64 + lane];
+            acc[r][0] += o[0];
+            acc[r][1] += o[1];
+            acc[r][2] += o[2];
+            acc[r][3] += o[3];
+        }
+        const int64_t row = (tile * R + r) * 16 + i16;
+        if (row < N) {
+            const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = 4 * g + q;
+                if (m < M) store_from_f32<DT>(y, (int64_t)m * N + row, acc[r][q] + bv);
+            }
         }
     }
 }
@@ -1870,8 +1908,8 @@ bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scal
         ((uintptr_t)y & 1u))
         return false;
     const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : fmt == kFmtRoot ? K / 8 : K / 4;
-    if ((N + 16) * rowbytes >= (1ll << 31) ||
-        (N + 16) * (K * 2 / gs) >= (1ll << 31) ||
+    if ((N + 32) * rowbytes >= (1ll << 31) ||
+        (N + 32) * (K * 2 / gs) >= (1ll << 31) ||
         M * K * 2 >= (1ll << 31))
         return false;
     return true;
@@ -1881,7 +1919,7 @@ template <int DT, int GS, int FMT>
 static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream) {
-    const int64_t wgs = (N + 15) / 16;  // one 16-row tile per workgroup
+    const int64_t wgs = (N + 16 * kB2mTiles - 1) / (16 * kB2mTiles);
     hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT>), dim3((unsigned)wgs), dim3(64 * kB2Waves),
                        0, stream, x, packed, scales, bias, y, M, N, K);
     return hipGetLastError();
