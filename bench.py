@@ -155,7 +155,7 @@ def _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes):
         for i, s in enumerate(stack):
             st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
                                       s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
-                                      s["N"], s["K"], GS, N_.BF16, stream_handle)
+                                      s["N"], s["K"], GS, N_.BF16, None, 0, stream_handle)
             N_.check(st, "gemm_fwd")
 
     for M in Ms:
@@ -265,6 +265,8 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev, Ms=DECODE_M,
 def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = False):
     """Prefill GEMM per shape and M; with backward=True the backward dX of the same layers
     (grad_x[M, K] = grad_y[M, N] . W[N, K], ojx_e8t_gemm_bwd_dx)."""
+    from ojasx_amd import ops
+
     lib = N_.lib()
     by_name = {}
     for s in stack[:7]:
@@ -272,11 +274,14 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = F
     results = {}
     tot_flop = 0.0
     tot_ms = 0.0
+    worst = 0.0
     stream = torch.cuda.current_stream()
     for M in Ms:
         for name, N, K in PREFILL_SHAPES:
             s = by_name[(N, K)]
             g = torch.Generator(device=dev).manual_seed(8400 + M)
+            ws = ops.workspace(ops.FMT_TERNARY, backward, M, N, K, GS, torch.bfloat16, dev)
+            ws_p, ws_n = (0, 0) if ws is None else (ws.data_ptr(), ws.numel())
             if backward:
                 x = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
                 y = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
@@ -284,7 +289,8 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = F
                 def run():
                     N_.check(lib.ojx_e8t_gemm_bwd_dx(x.data_ptr(), s["packed"].data_ptr(),
                                                      s["scales"].data_ptr(), y.data_ptr(), M, N,
-                                                     K, GS, N_.BF16, stream.cuda_stream),
+                                                     K, GS, N_.BF16, ws_p, ws_n,
+                                                     stream.cuda_stream),
                              "gemm_bwd_dx")
             else:
                 x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
@@ -293,7 +299,8 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = F
                 def run():
                     N_.check(lib.ojx_e8t_gemm_fwd(x.data_ptr(), s["packed"].data_ptr(),
                                                   s["scales"].data_ptr(), None, y.data_ptr(), M,
-                                                  N, K, GS, N_.BF16, stream.cuda_stream),
+                                                  N, K, GS, N_.BF16, ws_p, ws_n,
+                                                  stream.cuda_stream),
                              "gemm_fwd")
 
             run()
@@ -314,14 +321,24 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = F
             ms = a.elapsed_time(b) / iters
             flop = 2.0 * M * N * K
             tf = flop / ms / 1e9
+            # output check of what was timed: every element against an fp32 matmul of the
+            # decoded weights (the decoder is bit-exact with the oracle)
+            wdq = ops.decode(s["packed"], s["scales"], N * K, GS, torch.bfloat16).view(N, K)
+            ref = (x.float() @ wdq.float()) if backward else (x.float() @ wdq.float().t())
+            err = ((y.float() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+            worst = max(worst, err)
+            del wdq, ref
             results[f"{name}_M{M}"] = dict(ms=round(ms, 4), TFLOPs=round(tf, 1),
-                                           frac_mfma=round(tf / BF16_MFMA_PEAK_TFLOPS, 4))
+                                           frac_mfma=round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+                                           max_rel_err=float(f"{err:.3g}"))
             tot_flop += flop
             tot_ms += ms
-            del x, y
+            del x, y, ws
     agg = tot_flop / tot_ms / 1e9 if tot_ms > 0 else 0.0
+    if worst > 1e-2:
+        raise RuntimeError(f"prefill output check failed: max rel err {worst:.3g} > 1e-2")
     return dict(cases=results, TFLOPs=round(agg, 1),
-                frac_mfma=round(agg / BF16_MFMA_PEAK_TFLOPS, 4))
+                frac_mfma=round(agg / BF16_MFMA_PEAK_TFLOPS, 4), max_rel_err=worst)
 
 
 # --------------------------------------------------------------------------- encoder
@@ -432,9 +449,9 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights (seed 9700 + 7*layer +
     j), group size 32.  Encoder: the stack's encode launches replayed from one hipGraph,
     layer 0 of each shape checked bit for bit against the CPU oracle on its first
-    `check_rows` rows.  Decode: one ojx_e8_gemm_fwd launch per linear at each M (replayed
-    from a hipGraph for M <= 16, the GEMVs; issued eagerly above, where the MFMA GEMM splits
-    over K); outputs of layer 0 checked against an fp32 matmul of the decoded weights.
+    `check_rows` rows.  Decode: one ojx_e8_gemm_fwd launch per linear at each M, replayed
+    from a hipGraph (the prefill launches with a caller-owned K-split workspace); outputs of
+    layer 0 checked against an fp32 matmul of the decoded weights.
     Prefill: the same at M = `prefill_m`."""
     import numpy as np
 
@@ -454,20 +471,6 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     numel = sum(it["N"] * it["K"] for it in items)
     wbytes = sum(e8b_weight_bytes(it["N"], it["K"], per_byte=per_byte) for it in items)
     stream = torch.cuda.current_stream()
-
-    def eager_ms(launch_all, reps):
-        # launches outside graph capture (the GEMM's K split needs the library's stream
-        # scratch, which is never handed out while a stream is capturing)
-        launch_all(stream.cuda_stream)
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            launch_all(stream.cuda_stream)
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
 
     def replay_ms(launch_all, reps):
         launch_all(stream.cuda_stream)
@@ -508,14 +511,21 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
         xs = {K: torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(9800 + M + K),
                              device=dev).to(torch.bfloat16) for K in (4096, 14336)}
         ys = [torch.empty(M, it["N"], dtype=torch.bfloat16, device=dev) for it in items]
+        # one workspace, as large as the largest launch needs, shared by the stream's launches
+        from ojasx_amd import ops as ops_
+        fmt_code = ops_.FMT_E8 if fmt == "2bit" else ops_.FMT_ROOT
+        wss = [ops_.workspace(fmt_code, False, M, it["N"], it["K"], E8B_GS, torch.bfloat16, dev)
+               for it in items[:7]]
+        ws = max((w for w in wss if w is not None), key=lambda w: w.numel(), default=None)
+        ws_p, ws_n = (0, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
         def launch_all(h):
             for it, y in zip(items, ys):
                 N_.check(gemm_fn(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
                                  it["scales"].data_ptr(), None, y.data_ptr(), M, it["N"], it["K"],
-                                 E8B_GS, N_.BF16, h), "gemm")
+                                 E8B_GS, N_.BF16, ws_p, ws_n, h), "gemm")
 
-        ms = replay_ms(launch_all, steps) if M <= 16 else eager_ms(launch_all, steps)
+        ms = replay_ms(launch_all, steps)
         worst = 0.0
         from ojasx_amd import ops
         for idx in (0, 4, 6):  # q, gate, down of layer 0

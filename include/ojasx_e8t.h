@@ -7,12 +7,13 @@
  * device pointer (HBM) on the current HIP device.  `stream` is a hipStream_t
  * (NULL = the null stream).  Each entry point enqueues its kernels on `stream`
  * and returns without synchronising; results are ready when the stream is.  The
- * only device memory the library allocates is the prefill GEMM's K-split scratch
- * (ojx_e8t_gemm_fwd, M > 16, small grids): one buffer per (device, stream), grown
- * under a lock when a launch needs more (the stream is synchronised before an old
- * buffer is freed), never while the stream is capturing a graph (the launch then
- * runs unsplit), kept until the process ends.  No other mutable global state beyond
- * a per-device architecture check and a thread-local error message.
+ * library never allocates device memory: outputs and the scratch ("workspace") of the
+ * fused GEMMs are the caller's.  A GEMM's workspace holds the fp32 partial sums of its
+ * K split (prefill shapes whose tile grid is too small to fill the GPU); its size comes
+ * from ojx_gemm_workspace_bytes, and a smaller one (or none) only lowers the split
+ * count, down to the unsplit kernel, so results stay correct.  A workspace is in use
+ * until the launch that received it has finished on its stream.  No mutable global
+ * state beyond a per-device architecture check and a thread-local error message.
  *
  * Data layout (identical to the reference's buffers, so existing state_dicts load):
  *   packed  uint8 [padded * 3 / 16]   two 12-bit codes per 3 bytes, little-endian bit
@@ -40,6 +41,9 @@ extern "C" {
 #endif
 
 enum { OJX_F32 = 0, OJX_F16 = 1, OJX_BF16 = 2 };
+
+/* Weight formats (ojx_gemm_workspace_bytes): ternary E8 (1.5 bit), 2-bit E8, 1-bit Root E8. */
+enum { OJX_FMT_TERNARY = 0, OJX_FMT_E8 = 1, OJX_FMT_ROOT = 2 };
 
 enum {
     OJX_OK = 0,
@@ -75,6 +79,16 @@ int ojx_e8t_encode(const void* w, int w_dtype, int64_t numel, int64_t gs, uint8_
 int ojx_e8t_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel, int64_t gs,
                    int out_dtype, void* out, void* stream);
 
+/* Workspace of a fused GEMM launch.  Writes to *bytes the device scratch that
+ * ojx_{e8t,e8,e8r}_gemm_fwd (bwd = 0) or _gemm_bwd_dx (bwd = 1) uses for this shape at its
+ * full K split, 0 when the launch needs none (every decode GEMV, M <= 16, and prefill grids
+ * large enough to run unsplit).  fmt is an OJX_FMT_* code; (M, N, K) are the forward's
+ * sizes (x [M, K], W [N, K]) for both directions.  Host-only: launches nothing.  No
+ * counterpart in the reference, whose native ops allocate nothing but their output
+ * (ojasx_math_bindings.cpp:432); it lets the caller own every byte this library touches. */
+int ojx_gemm_workspace_bytes(int fmt, int bwd, int64_t M, int64_t N, int64_t K, int64_t gs,
+                             int dtype, size_t* bytes);
+
 /* Fused forward y[M,N] = x[M,K] . Wdeq[N,K]^T (+ bias[N]), fp32 accumulation, y in dtype.
  * Replaces fused_ternary_e8_gemm_fwd (ojasx2/math/csrc/ojasx_math_bindings.cpp:407-472,
  * schema at :594) and dispatch_tilelang_e8_gemm (ojasx2/tilelang_kernels.py:370-419);
@@ -82,18 +96,19 @@ int ojx_e8t_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel,
  *   x, y, bias in `dtype`; bias may be NULL.  Wdeq follows the decoder's rule for `dtype`.
  *   Any K >= 1 (flat layout).  F16/BF16 with K % 256 == 0, gs == 32 and M <= 16 run the
  *   MFMA decode GEMV; F16/BF16 with K % 64 == 0, gs == 32 and M > 16 the MFMA prefill
- *   GEMM (split over K for small grids, with the scratch described above); other shapes
- *   and F32 use a general tiled kernel.  Never declines. */
+ *   GEMM; other shapes and F32 use a general tiled kernel.  Never declines.
+ *   workspace: 16-byte aligned device scratch of workspace_bytes (NULL with 0 allowed),
+ *   see ojx_gemm_workspace_bytes. */
 int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                     int dtype, void* stream);
+                     int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Fused backward grad_x[M,K] = grad_y[M,N] . Wdeq[N,K], fp32 accumulation, in dtype.
  * Replaces fused_ternary_e8_gemm_bwd_dx (ojasx_math_bindings.cpp:479-533, schema :594);
- * called from _FusedE8GEMMFunction.backward (lattice.py:656-696). */
+ * called from _FusedE8GEMMFunction.backward (lattice.py:656-696).  Workspace as above. */
 int ojx_e8t_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_t* scales,
                         void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
-                        void* stream);
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- 2-bit E8
  *
@@ -117,13 +132,14 @@ int ojx_e8_decode(const uint8_t* packed, const uint16_t* scales, int64_t numel, 
  * fp32 accumulation.  Replace fused_e8_gemm_fwd / fused_e8_gemm_bwd_dx
  * (ojasx_math_bindings.cpp:274-404, schemas :591-592) and the 2-bit portable path of
  * _FusedE8GEMMFunction (lattice.py:610-640, 684-717).  gs a positive multiple of 4 (the
- * native op's rule, bindings.cpp:285).  Any M, N, K (flat layout). */
+ * native op's rule, bindings.cpp:285).  Any M, N, K (flat layout).  Workspace as for
+ * ojx_e8t_gemm_fwd (fmt OJX_FMT_E8). */
 int ojx_e8_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                     const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                    int dtype, void* stream);
+                    int dtype, void* workspace, size_t workspace_bytes, void* stream);
 int ojx_e8_gemm_bwd_dx(const void* grad_y, const uint8_t* packed, const uint16_t* scales,
                        void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
-                       void* stream);
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- 1-bit Root E8
  *
@@ -147,13 +163,13 @@ int ojx_e8r_decode(const uint8_t* codes, const uint16_t* scales, int64_t numel, 
 /* Fused forward and backward dX over 1-bit weights with the decoder's weight rule and
  * fp32 accumulation.  Replace the 1-bit portable path of _FusedE8GEMMFunction (unpack +
  * F.linear, lattice.py:610-640; backward :684-717).  gs a positive multiple of 8.  Any
- * M, N, K (flat layout). */
+ * M, N, K (flat layout).  Workspace as for ojx_e8t_gemm_fwd (fmt OJX_FMT_ROOT). */
 int ojx_e8r_gemm_fwd(const void* x, const uint8_t* codes, const uint16_t* scales,
                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                     int dtype, void* stream);
+                     int dtype, void* workspace, size_t workspace_bytes, void* stream);
 int ojx_e8r_gemm_bwd_dx(const void* grad_y, const uint8_t* codes, const uint16_t* scales,
                         void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
-                        void* stream);
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- QAT helpers
  *

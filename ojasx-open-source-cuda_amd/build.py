@@ -25,7 +25,6 @@ SOURCES = [
     "e8t_gemv.hip",
     "e8t_gemm_mfma.hip",
     "e8t_qat.hip",
-    "e8t_workspace.cpp",
     "e8t_capi.cpp",
 ]
 

@@ -2,9 +2,9 @@
 // include/ojasx_e8t.h).  Validates arguments the way the reference's native
 // binding does (ojasx_math_bindings.cpp:17-34, 414-433), checks the device,
 // picks a kernel and enqueues it on the caller's stream.  The only mutable state
-// is a per-device arch cache, a thread-local error message and the prefill GEMM's
-// K-split scratch (e8t_workspace.cpp: allocated only when a stream's buffer must
-// grow, never during graph capture).
+// is a per-device arch cache and a thread-local error message.  Nothing here
+// allocates device memory: the prefill GEMM's K-split scratch is the caller's
+// workspace argument (size from ojx_gemm_workspace_bytes).
 
 #include <hip/hip_runtime.h>
 
@@ -73,24 +73,189 @@ int done(hipError_t e, const char* what) {
     return OJX_OK;
 }
 
-int check_gemm_args(const void* a, const uint8_t* packed, const uint16_t* scales, const void* out,
-                    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype) {
-    if (M < 0 || N < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld N=%lld K=%lld",
-                                             (long long)M, (long long)N, (long long)K);
+}  // namespace
+
+// The prefill MFMA GEMM with its tile configuration and K split.  The split's fp32 partial
+// sums live in the caller's workspace; a workspace smaller than the plan's (or none) lowers
+// the split count to what fits, down to the unsplit kernel.
+// bwd: the backward dX (output [M, K], reduction over N).
+static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
+                              const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                              int64_t gs, int dtype, hipStream_t s, int fmt, bool bwd,
+                              void* ws, size_t ws_bytes) {
+    const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
+    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, out_cols, red);
+    const size_t per = (size_t)ojx::split_stride(M, out_cols) * sizeof(float);
+    const int64_t fit = ws ? (int64_t)(ws_bytes / per) : 0;
+    if (c.splits > fit) c.splits = fit < 2 ? 1 : (int)fit;
+    float* part = c.splits > 1 ? static_cast<float*>(ws) : nullptr;
+    return ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s, gs, fmt,
+                                 bwd);
+}
+
+// Workspace pointer contract shared by the GEMM entry points.
+static int check_workspace(const void* ws, size_t ws_bytes) {
+    if (ws_bytes > 0 && !ws) return fail(OJX_EINVAL, "workspace_bytes %zu with a null workspace",
+                                         ws_bytes);
+    if ((uintptr_t)ws & 15u) return fail(OJX_ELAYOUT, "workspace must be 16-byte aligned");
+    return OJX_OK;
+}
+
+// Group-size rule of each format's fused ops: ternary a multiple of 16 (the native op's
+// packing unit, ojasx_math_bindings.cpp:17-34), 2-bit a multiple of 4 (bindings.cpp:285),
+// 1-bit a multiple of 8 (the Root-E8 packer's unit).
+static int check_gs_multiple(int64_t gs, int64_t unit) {
+    if (gs <= 0 || gs % unit != 0)
+        return fail(OJX_ELAYOUT, "group_size must be a positive multiple of %lld (got %lld)",
+                    (long long)unit, (long long)gs);
+    return OJX_OK;
+}
+
+static int64_t gs_unit(int fmt) {
+    return fmt == ojx::kFmtTernary ? 16 : fmt == ojx::kFmt2Bit ? 4 : 8;
+}
+
+// a: x (forward) or grad_y (backward); out: y or grad_x; (M, N, K) the forward's shape.
+static int check_fmt_args(int fmt, const void* a, const uint8_t* packed, const uint16_t* scales,
+                          const void* out, int64_t M, int64_t out_cols, int64_t red, int64_t gs,
+                          int dtype) {
+    if (M < 0 || out_cols < 0 || red < 0)
+        return fail(OJX_EINVAL, "negative size M=%lld, %lld x %lld", (long long)M,
+                    (long long)out_cols, (long long)red);
     if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
-    if (int r = check_gs(gs)) return r;
-    if (M > 0 && N > 0) {
+    if (int r = check_gs_multiple(gs, gs_unit(fmt))) return r;
+    if (M > 0 && out_cols > 0) {
         if (!out) return fail(OJX_EINVAL, "null output pointer");
-        if (K > 0 && (!a || !packed || !scales)) return fail(OJX_EINVAL, "null input pointer");
+        if (red > 0 && (!a || !packed || !scales)) return fail(OJX_EINVAL, "null input pointer");
     }
     return OJX_OK;
 }
 
-}  // namespace
+// Kernel family of a forward / backward launch (the dispatch below).  Pointer alignment
+// takes part in it; the workspace query passes null pointers (aligned).
+enum Route { kRouteGemv2m, kRouteGemv, kRouteGemv2, kRouteMfma, kRouteGeneric };
+
+static Route route_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
+                       const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype) {
+    if (fmt == ojx::kFmtTernary) {
+        // 4 < M <= 16 on a layer too small for the streaming mask kernel (< 1024 row tiles):
+        // one 16-row tile per workgroup, K split over its waves, weights in the B operand
+        if (M > 4 && (N + 15) / 16 < 1024 &&
+            ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, fmt))
+            return kRouteGemv2m;
+        if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, N, K, gs, dtype))
+            return kRouteGemv;
+        if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, fmt))
+            return kRouteMfma;
+        return kRouteGeneric;
+    }
+    if (fmt == ojx::kFmt2Bit && ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
+        return kRouteGemv2;
+    if (ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, fmt)) return kRouteGemv2m;
+    if (ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, fmt)) return kRouteMfma;
+    return kRouteGeneric;
+}
+
+static Route route_bwd(int fmt, const void* gy, const uint8_t* packed, const uint16_t* scales,
+                       int64_t M, int64_t N, int64_t K, int64_t gs, int dtype) {
+    if (N > 0 && ojx::gemm_mfma_supported(gy, packed, scales, M, N, K, gs, dtype, fmt, true))
+        return kRouteMfma;
+    return kRouteGeneric;
+}
+
+static const char* fmt_name(int fmt) {
+    return fmt == ojx::kFmtTernary ? "e8t" : fmt == ojx::kFmt2Bit ? "e8" : "e8r";
+}
+
+// Forward of every format: y[M, N] = x . Wdeq^T (+ bias).
+static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
+                    const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                    int dtype, void* ws, size_t ws_bytes, void* stream) {
+    if (int r = check_fmt_args(fmt, x, packed, scales, y, M, N, K, gs, dtype)) return r;
+    if (int r = check_workspace(ws, ws_bytes)) return r;
+    if (M == 0 || N == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    switch (route_fwd(fmt, x, packed, scales, y, M, N, K, gs, dtype)) {
+    case kRouteGemv2m:
+        e = ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt);
+        break;
+    case kRouteGemv2:
+        e = ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s);
+        break;
+    case kRouteGemv: {
+        ojx::GemvLaunch a{};
+        ojx::GemvJob& j = a.inl[0];
+        j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
+        j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
+        a.njobs = 1;
+        a.M = (int)M;
+        const ojx::GemvPlan plan = ojx::gemv_pick((N + 15) / 16, M);
+        e = ojx::launch_gemv(a, plan, ojx::gemv_wgs_for(N, plan), dtype, s);
+        break;
+    }
+    case kRouteMfma:
+        e = launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt, false, ws,
+                        ws_bytes);
+        break;
+    case kRouteGeneric:
+        e = ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt);
+        break;
+    }
+    if (e != hipSuccess) return fail(OJX_EHIP, "%s gemm_fwd launch: %s", fmt_name(fmt),
+                                     hipGetErrorString(e));
+    g_last_error[0] = '\0';
+    return OJX_OK;
+}
+
+// Backward dX of every format: grad_x[M, K] = grad_y[M, N] . Wdeq[N, K].
+static int gemm_bwd(int fmt, const void* grad_y, const uint8_t* packed, const uint16_t* scales,
+                    void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
+                    void* ws, size_t ws_bytes, void* stream) {
+    if (int r = check_fmt_args(fmt, grad_y, packed, scales, grad_x, M, K, N, gs, dtype)) return r;
+    if (int r = check_workspace(ws, ws_bytes)) return r;
+    if (M == 0 || K == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    if (route_bwd(fmt, grad_y, packed, scales, M, N, K, gs, dtype) == kRouteMfma)
+        e = launch_mfma(grad_y, packed, scales, nullptr, grad_x, M, N, K, gs, dtype, s, fmt, true,
+                        ws, ws_bytes);
+    else
+        e = ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype, s,
+                                         fmt);
+    if (e != hipSuccess) return fail(OJX_EHIP, "%s gemm_bwd_dx launch: %s", fmt_name(fmt),
+                                     hipGetErrorString(e));
+    g_last_error[0] = '\0';
+    return OJX_OK;
+}
+
+// Workspace bytes of a fused forward (bwd 0) or backward dX (bwd 1) launch.
+static int workspace_bytes(int fmt, int bwd, int64_t M, int64_t N, int64_t K, int64_t gs,
+                           int dtype, size_t* bytes) {
+    if (!bytes) return fail(OJX_EINVAL, "null result pointer");
+    *bytes = 0;
+    if (fmt != ojx::kFmtTernary && fmt != ojx::kFmt2Bit && fmt != ojx::kFmtRoot)
+        return fail(OJX_EINVAL, "unknown format code %d", fmt);
+    if (M < 0 || N < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld N=%lld K=%lld",
+                                             (long long)M, (long long)N, (long long)K);
+    if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
+    if (int r = check_gs_multiple(gs, gs_unit(fmt))) return r;
+    if (M == 0 || N == 0 || K == 0) return OJX_OK;
+    const Route r = bwd ? route_bwd(fmt, nullptr, nullptr, nullptr, M, N, K, gs, dtype)
+                        : route_fwd(fmt, nullptr, nullptr, nullptr, nullptr, M, N, K, gs, dtype);
+    if (r == kRouteMfma) {
+        const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
+        *bytes = ojx::gemm_split_bytes(ojx::gemm_mfma_choice(M, out_cols, red), M, out_cols);
+    }
+    g_last_error[0] = '\0';
+    return OJX_OK;
+}
 
 extern "C" {
 
-__attribute__((visibility("default"))) int ojx_e8t_version(void) { return 100; }
+__attribute__((visibility("default"))) int ojx_e8t_version(void) { return 20000; }
 
 __attribute__((visibility("default"))) const char* ojx_e8t_last_error(void) {
     return g_last_error;
@@ -122,59 +287,6 @@ __attribute__((visibility("default"))) int ojx_e8t_decode(const uint8_t* packed,
     if (int r = check_device()) return r;
     return done(ojx::launch_decode(packed, scales, numel, gs, out_dtype, out, (hipStream_t)stream),
                 "e8t decode launch");
-}
-
-// The prefill MFMA GEMM with its tile configuration and K split; the split's fp32 partial
-// sums live in the per-stream workspace (none while the stream is captured: unsplit).
-// bwd: the backward dX (output [M, K], reduction over N).
-static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
-                              const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                              int64_t gs, int dtype, hipStream_t s, int fmt, bool bwd = false) {
-    const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
-    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, out_cols, red);
-    float* part = nullptr;
-    if (c.splits > 1) {
-        part = static_cast<float*>(ojx::stream_workspace(
-            s, (size_t)c.splits * (size_t)ojx::split_stride(M, out_cols) * sizeof(float)));
-        if (!part) c.splits = 1;  // capturing, or no memory: the unsplit kernel
-    }
-    return ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s, gs, fmt,
-                                 bwd);
-}
-
-__attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed,
-                                                            const uint16_t* scales,
-                                                            const void* bias, void* y, int64_t M,
-                                                            int64_t N, int64_t K, int64_t gs,
-                                                            int dtype, void* stream) {
-    if (int r = check_gemm_args(x, packed, scales, y, M, N, K, gs, dtype)) return r;
-    if (M == 0 || N == 0) return OJX_OK;
-    if (int r = check_device()) return r;
-    hipStream_t s = (hipStream_t)stream;
-    // 4 < M <= 16 on a layer too small for the streaming mask kernel (< 1024 row tiles): one
-    // 16-row tile per workgroup, K split over its waves, weights in the B operand
-    if (M > 4 && (N + 15) / 16 < 1024 &&
-        ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, ojx::kFmtTernary))
-        return done(ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
-                                       ojx::kFmtTernary),
-                    "e8t gemv launch");
-    if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, N, K, gs, dtype)) {
-        ojx::GemvLaunch a{};
-        ojx::GemvJob& j = a.inl[0];
-        j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
-        j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
-        a.njobs = 1;
-        a.M = (int)M;
-        const ojx::GemvPlan plan = ojx::gemv_pick((N + 15) / 16, M);
-        return done(ojx::launch_gemv(a, plan, ojx::gemv_wgs_for(N, plan), dtype, s),
-                    "e8t gemv launch");
-    }
-    if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype))
-        return done(launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
-                                ojx::kFmtTernary),
-                    "e8t gemm_mfma launch");
-    return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
-                "e8t gemm_fwd launch");
 }
 
 static_assert(sizeof(ojx_e8t_gemv_job) == sizeof(ojx::GemvJob), "job layout");
@@ -263,33 +375,7 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
                 "e8t grouped gemv launch");
 }
 
-__attribute__((visibility("default"))) int ojx_e8t_gemm_bwd_dx(const void* grad_y,
-                                                               const uint8_t* packed,
-                                                               const uint16_t* scales,
-                                                               void* grad_x, int64_t M, int64_t N,
-                                                               int64_t K, int64_t gs, int dtype,
-                                                               void* stream) {
-    if (int r = check_gemm_args(grad_y, packed, scales, grad_x, M, K, N, gs, dtype)) return r;
-    if (M == 0 || K == 0) return OJX_OK;
-    if (int r = check_device()) return r;
-    hipStream_t s = (hipStream_t)stream;
-    if (N > 0 && ojx::gemm_mfma_supported(grad_y, packed, scales, M, N, K, gs, dtype,
-                                          ojx::kFmtTernary, true))
-        return done(launch_mfma(grad_y, packed, scales, nullptr, grad_x, M, N, K, gs, dtype, s,
-                                ojx::kFmtTernary, true),
-                    "e8t gemm_mfma bwd launch");
-    return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype, s),
-                "e8t gemm_bwd_dx launch");
-}
-
 // ------------------------------------------------------------------ 2-bit E8
-
-static int check_gs_multiple(int64_t gs, int64_t unit) {
-    if (gs <= 0 || gs % unit != 0)
-        return fail(OJX_ELAYOUT, "group_size must be a positive multiple of %lld (got %lld)",
-                    (long long)unit, (long long)gs);
-    return OJX_OK;
-}
 
 __attribute__((visibility("default"))) int ojx_e8_encode(const void* w, int w_dtype,
                                                          int64_t numel, int64_t gs,
@@ -317,64 +403,6 @@ __attribute__((visibility("default"))) int ojx_e8_decode(const uint8_t* packed,
     if (int r = check_device()) return r;
     return done(ojx::launch_decode2(packed, scales, numel, gs, out_dtype, out, (hipStream_t)stream),
                 "e8 decode launch");
-}
-
-static int check_gemm2_args(const void* a, const uint8_t* packed, const uint16_t* scales,
-                            const void* out, int64_t M, int64_t N, int64_t K, int64_t gs,
-                            int dtype) {
-    if (M < 0 || N < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld N=%lld K=%lld",
-                                             (long long)M, (long long)N, (long long)K);
-    if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
-    if (int r = check_gs_multiple(gs, 4)) return r;
-    if (M > 0 && N > 0) {
-        if (!out) return fail(OJX_EINVAL, "null output pointer");
-        if (K > 0 && (!a || !packed || !scales)) return fail(OJX_EINVAL, "null input pointer");
-    }
-    return OJX_OK;
-}
-
-__attribute__((visibility("default"))) int ojx_e8_gemm_fwd(const void* x, const uint8_t* packed,
-                                                           const uint16_t* scales,
-                                                           const void* bias, void* y, int64_t M,
-                                                           int64_t N, int64_t K, int64_t gs,
-                                                           int dtype, void* stream) {
-    if (int r = check_gemm2_args(x, packed, scales, y, M, N, K, gs, dtype)) return r;
-    if (M == 0 || N == 0) return OJX_OK;
-    if (int r = check_device()) return r;
-    hipStream_t s = (hipStream_t)stream;
-    if (ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
-        return done(ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s),
-                    "e8 gemv launch");
-    if (ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, ojx::kFmt2Bit))
-        return done(ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
-                                       ojx::kFmt2Bit),
-                    "e8 gemv launch");
-    if (ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, ojx::kFmt2Bit))
-        return done(launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmt2Bit),
-                    "e8 gemm_mfma launch");
-    return done(ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s,
-                                             ojx::kFmt2Bit),
-                "e8 gemm_fwd launch");
-}
-
-__attribute__((visibility("default"))) int ojx_e8_gemm_bwd_dx(const void* grad_y,
-                                                              const uint8_t* packed,
-                                                              const uint16_t* scales,
-                                                              void* grad_x, int64_t M, int64_t N,
-                                                              int64_t K, int64_t gs, int dtype,
-                                                              void* stream) {
-    if (int r = check_gemm2_args(grad_y, packed, scales, grad_x, M, K, N, gs, dtype)) return r;
-    if (M == 0 || K == 0) return OJX_OK;
-    if (int r = check_device()) return r;
-    hipStream_t s = (hipStream_t)stream;
-    if (N > 0 && ojx::gemm_mfma_supported(grad_y, packed, scales, M, N, K, gs, dtype,
-                                          ojx::kFmt2Bit, true))
-        return done(launch_mfma(grad_y, packed, scales, nullptr, grad_x, M, N, K, gs, dtype, s,
-                                ojx::kFmt2Bit, true),
-                    "e8 gemm_mfma bwd launch");
-    return done(ojx::launch_gemm_generic_bwd(grad_y, packed, scales, grad_x, M, N, K, gs, dtype, s,
-                                             ojx::kFmt2Bit),
-                "e8 gemm_bwd_dx launch");
 }
 
 // ---------------------------------------------------------------- 1-bit Root E8
@@ -407,59 +435,60 @@ __attribute__((visibility("default"))) int ojx_e8r_decode(const uint8_t* codes,
                 "e8r decode launch");
 }
 
-static int check_gemm1_args(const void* a, const uint8_t* codes, const uint16_t* scales,
-                            const void* out, int64_t M, int64_t N, int64_t K, int64_t gs,
-                            int dtype) {
-    if (M < 0 || N < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld N=%lld K=%lld",
-                                             (long long)M, (long long)N, (long long)K);
-    if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
-    if (int r = check_gs_multiple(gs, 8)) return r;
-    if (M > 0 && N > 0) {
-        if (!out) return fail(OJX_EINVAL, "null output pointer");
-        if (K > 0 && (!a || !codes || !scales)) return fail(OJX_EINVAL, "null input pointer");
-    }
-    return OJX_OK;
+
+__attribute__((visibility("default"))) int ojx_gemm_workspace_bytes(int fmt, int bwd, int64_t M,
+                                                                    int64_t N, int64_t K,
+                                                                    int64_t gs, int dtype,
+                                                                    size_t* bytes) {
+    return workspace_bytes(fmt, bwd, M, N, K, gs, dtype, bytes);
 }
 
-__attribute__((visibility("default"))) int ojx_e8r_gemm_fwd(const void* x, const uint8_t* codes,
-                                                            const uint16_t* scales,
-                                                            const void* bias, void* y, int64_t M,
-                                                            int64_t N, int64_t K, int64_t gs,
-                                                            int dtype, void* stream) {
-    if (int r = check_gemm1_args(x, codes, scales, y, M, N, K, gs, dtype)) return r;
-    if (M == 0 || N == 0) return OJX_OK;
-    if (int r = check_device()) return r;
-    hipStream_t s = (hipStream_t)stream;
-    if (ojx::gemv2m_supported(x, codes, scales, y, M, N, K, gs, dtype, ojx::kFmtRoot))
-        return done(ojx::launch_gemv2m(x, codes, scales, bias, y, M, N, K, gs, dtype, s,
-                                       ojx::kFmtRoot),
-                    "e8r gemv launch");
-    if (ojx::gemm_mfma_supported(x, codes, scales, M, N, K, gs, dtype, ojx::kFmtRoot))
-        return done(launch_mfma(x, codes, scales, bias, y, M, N, K, gs, dtype, s, ojx::kFmtRoot),
-                    "e8r gemm_mfma launch");
-    return done(ojx::launch_gemm_generic_fwd(x, codes, scales, bias, y, M, N, K, gs, dtype, s,
-                                             ojx::kFmtRoot),
-                "e8r gemm_fwd launch");
+__attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(
+    const void* x, const uint8_t* packed, const uint16_t* scales, const void* bias, void* y,
+    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    return gemm_fwd(ojx::kFmtTernary, x, packed, scales, bias, y, M, N, K, gs, dtype, workspace,
+                    workspace_bytes, stream);
 }
 
-__attribute__((visibility("default"))) int ojx_e8r_gemm_bwd_dx(const void* grad_y,
-                                                               const uint8_t* codes,
-                                                               const uint16_t* scales,
-                                                               void* grad_x, int64_t M, int64_t N,
-                                                               int64_t K, int64_t gs, int dtype,
-                                                               void* stream) {
-    if (int r = check_gemm1_args(grad_y, codes, scales, grad_x, M, K, N, gs, dtype)) return r;
-    if (M == 0 || K == 0) return OJX_OK;
-    if (int r = check_device()) return r;
-    hipStream_t s = (hipStream_t)stream;
-    if (N > 0 && ojx::gemm_mfma_supported(grad_y, codes, scales, M, N, K, gs, dtype,
-                                          ojx::kFmtRoot, true))
-        return done(launch_mfma(grad_y, codes, scales, nullptr, grad_x, M, N, K, gs, dtype, s,
-                                ojx::kFmtRoot, true),
-                    "e8r gemm_mfma bwd launch");
-    return done(ojx::launch_gemm_generic_bwd(grad_y, codes, scales, grad_x, M, N, K, gs, dtype, s,
-                                             ojx::kFmtRoot),
-                "e8r gemm_bwd_dx launch");
+__attribute__((visibility("default"))) int ojx_e8t_gemm_bwd_dx(
+    const void* grad_y, const uint8_t* packed, const uint16_t* scales, void* grad_x, int64_t M,
+    int64_t N, int64_t K, int64_t gs, int dtype, void* workspace, size_t workspace_bytes,
+    void* stream) {
+    return gemm_bwd(ojx::kFmtTernary, grad_y, packed, scales, grad_x, M, N, K, gs, dtype,
+                    workspace, workspace_bytes, stream);
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemm_fwd(
+    const void* x, const uint8_t* packed, const uint16_t* scales, const void* bias, void* y,
+    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    return gemm_fwd(ojx::kFmt2Bit, x, packed, scales, bias, y, M, N, K, gs, dtype, workspace,
+                    workspace_bytes, stream);
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemm_bwd_dx(
+    const void* grad_y, const uint8_t* packed, const uint16_t* scales, void* grad_x, int64_t M,
+    int64_t N, int64_t K, int64_t gs, int dtype, void* workspace, size_t workspace_bytes,
+    void* stream) {
+    return gemm_bwd(ojx::kFmt2Bit, grad_y, packed, scales, grad_x, M, N, K, gs, dtype, workspace,
+                    workspace_bytes, stream);
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemm_fwd(
+    const void* x, const uint8_t* codes, const uint16_t* scales, const void* bias, void* y,
+    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    return gemm_fwd(ojx::kFmtRoot, x, codes, scales, bias, y, M, N, K, gs, dtype, workspace,
+                    workspace_bytes, stream);
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemm_bwd_dx(
+    const void* grad_y, const uint8_t* codes, const uint16_t* scales, void* grad_x, int64_t M,
+    int64_t N, int64_t K, int64_t gs, int dtype, void* workspace, size_t workspace_bytes,
+    void* stream) {
+    return gemm_bwd(ojx::kFmtRoot, grad_y, codes, scales, grad_x, M, N, K, gs, dtype, workspace,
+                    workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------- QAT helpers

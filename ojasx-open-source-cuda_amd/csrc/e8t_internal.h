@@ -128,9 +128,10 @@ hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t
                             int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs = 32,
                             int fmt = 0, bool bwd = false);
 
-// Scratch device memory owned by the library, one buffer per (device, stream), grown on
-// demand and kept until the process ends.  Returns nullptr (and allocates nothing) while
-// `stream` is being captured into a graph, or if the allocation fails.
-void* stream_workspace(hipStream_t stream, size_t bytes);
+// Bytes of fp32 K-split scratch a launch with choice `c` uses (0 when unsplit).
+inline size_t gemm_split_bytes(const GemmChoice& c, int64_t M, int64_t out_cols) {
+    return c.splits > 1 ? (size_t)c.splits * (size_t)split_stride(M, out_cols) * sizeof(float)
+                        : 0;
+}
 
 }  // namespace ojx

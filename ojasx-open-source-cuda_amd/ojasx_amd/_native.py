@@ -24,6 +24,7 @@ EXPORTS = (
     "ojx_e8t_last_error",
     "ojx_e8t_encode",
     "ojx_e8t_decode",
+    "ojx_gemm_workspace_bytes",
     "ojx_e8t_gemm_fwd",
     "ojx_e8t_gemm_bwd_dx",
     "ojx_e8t_gemv_grouped_plan",
@@ -63,6 +64,7 @@ _lock = threading.Lock()
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
+_SZ = ctypes.c_size_t
 
 
 def lib() -> ctypes.CDLL:
@@ -85,10 +87,14 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8t_encode.argtypes = [_P, _INT, _I64, _I64, _P, _P, _P]
             L.ojx_e8t_decode.restype = _INT
             L.ojx_e8t_decode.argtypes = [_P, _P, _I64, _I64, _INT, _P, _P]
+            L.ojx_gemm_workspace_bytes.restype = _INT
+            L.ojx_gemm_workspace_bytes.argtypes = [_INT, _INT, _I64, _I64, _I64, _I64, _INT, _P]
             L.ojx_e8t_gemm_fwd.restype = _INT
-            L.ojx_e8t_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8t_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
+                                          _SZ, _P]
             L.ojx_e8t_gemm_bwd_dx.restype = _INT
-            L.ojx_e8t_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8t_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
+                                             _SZ, _P]
             L.ojx_e8t_gemv_grouped_plan.restype = _INT
             L.ojx_e8t_gemv_grouped_plan.argtypes = [_P, _INT, _I64, _INT, _P]
             L.ojx_e8t_gemv_grouped.restype = _INT
@@ -98,17 +104,21 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8_decode.restype = _INT
             L.ojx_e8_decode.argtypes = [_P, _P, _I64, _I64, _INT, _P, _P]
             L.ojx_e8_gemm_fwd.restype = _INT
-            L.ojx_e8_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
+                                          _SZ, _P]
             L.ojx_e8_gemm_bwd_dx.restype = _INT
-            L.ojx_e8_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
+                                             _SZ, _P]
             L.ojx_e8r_encode.restype = _INT
             L.ojx_e8r_encode.argtypes = [_P, _INT, _I64, _I64, _P, _P, _P]
             L.ojx_e8r_decode.restype = _INT
             L.ojx_e8r_decode.argtypes = [_P, _P, _I64, _I64, _INT, _P, _P]
             L.ojx_e8r_gemm_fwd.restype = _INT
-            L.ojx_e8r_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8r_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
+                                          _SZ, _P]
             L.ojx_e8r_gemm_bwd_dx.restype = _INT
-            L.ojx_e8r_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]
+            L.ojx_e8r_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
+                                             _SZ, _P]
             L.ojx_e8_cs_project.restype = _INT
             L.ojx_e8_cs_project.argtypes = [_P, _INT, _I64, _P, _P]
             L.ojx_e8_ste_quantize.restype = _INT

@@ -25,6 +25,7 @@ unsupported layouts or non-ROCm tensors; nothing silently declines or falls back
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Tuple
 
 import torch
@@ -123,15 +124,32 @@ def _check_layer_buffers(packed: torch.Tensor, scales: torch.Tensor, out_feature
             f"block_scales holds {scales.numel()} values; needs {padded // group_size}")
 
 
-@torch.library.custom_op(f"{_NS}::e8t_linear", mutates_args=())
-def e8t_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
-               bias: Optional[torch.Tensor], out_features: int, in_features: int,
-               group_size: int) -> torch.Tensor:
+FMT_TERNARY, FMT_E8, FMT_ROOT = 0, 1, 2
+_FWD = {FMT_TERNARY: "ojx_e8t_gemm_fwd", FMT_E8: "ojx_e8_gemm_fwd", FMT_ROOT: "ojx_e8r_gemm_fwd"}
+_BWD = {FMT_TERNARY: "ojx_e8t_gemm_bwd_dx", FMT_E8: "ojx_e8_gemm_bwd_dx",
+        FMT_ROOT: "ojx_e8r_gemm_bwd_dx"}
+
+
+def workspace(fmt: int, bwd: bool, M: int, N_out: int, K: int, group_size: int,
+              dtype: torch.dtype, device: torch.device) -> Optional[torch.Tensor]:
+    """The scratch a fused GEMM launch uses (``ojx_gemm_workspace_bytes``), from torch's
+    caching allocator, or None when the launch needs none.  Allocated per call, so a launch
+    captured into a CUDA graph keeps its workspace in the graph's memory pool."""
+    nbytes = ctypes.c_size_t(0)
+    N.check(N.lib().ojx_gemm_workspace_bytes(fmt, int(bwd), M, N_out, K, group_size,
+                                             _dtype_code(dtype), ctypes.byref(nbytes)),
+            "gemm_workspace_bytes")
+    if nbytes.value == 0:
+        return None
+    return torch.empty(nbytes.value, dtype=torch.uint8, device=device)
+
+
+def _linear_fwd(fmt: int, x: torch.Tensor, packed_weight: torch.Tensor,
+                block_scales: torch.Tensor, bias: Optional[torch.Tensor], out_features: int,
+                in_features: int, group_size: int) -> torch.Tensor:
+    """y = x . Wdeq^T (+ bias) through the format's fused forward.  Every buffer handed to
+    the library is bound to a local that lives until the launch has been enqueued."""
     dev = N.require_device(x, packed_weight, block_scales, bias)
-    _check_gs(group_size)
-    if x.shape[-1] != in_features:
-        raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
-    _check_layer_buffers(packed_weight, block_scales, out_features, in_features, group_size)
     dt = _dtype_code(x.dtype)
     x2 = x.reshape(-1, in_features).contiguous()
     M = x2.shape[0]
@@ -141,14 +159,52 @@ def e8t_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch
         if bias.numel() != out_features:
             raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
         b = bias.to(x.dtype).contiguous()  # the reference casts bias to x's dtype
-    packed_weight = packed_weight.contiguous()
-    block_scales = block_scales.contiguous()
+    pw = packed_weight.contiguous()
+    bs = block_scales.contiguous()
     with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8t_gemm_fwd(N.ptr(x2), N.ptr(packed_weight), N.ptr(block_scales),
-                                         N.ptr(b), N.ptr(y), M, out_features, in_features,
-                                         group_size, dt, N.stream_handle(dev)),
-                "gemm_fwd")
+        ws = workspace(fmt, False, M, out_features, in_features, group_size, x.dtype, dev)
+        N.check(getattr(N.lib(), _FWD[fmt])(N.ptr(x2), N.ptr(pw), N.ptr(bs), N.ptr(b), N.ptr(y),
+                                            M, out_features, in_features, group_size, dt,
+                                            N.ptr(ws), 0 if ws is None else ws.numel(),
+                                            N.stream_handle(dev)),
+                _FWD[fmt][4:])
     return y.reshape(*x.shape[:-1], out_features)
+
+
+def _linear_bwd(fmt: int, grad_y: torch.Tensor, packed_weight: torch.Tensor,
+                block_scales: torch.Tensor, out_features: int, in_features: int,
+                group_size: int) -> torch.Tensor:
+    """grad_x = grad_y . Wdeq through the format's fused backward dX."""
+    dev = N.require_device(grad_y, packed_weight, block_scales)
+    if grad_y.shape[-1] != out_features:
+        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
+    dt = _dtype_code(grad_y.dtype)
+    gy = grad_y.reshape(-1, out_features).contiguous()
+    M = gy.shape[0]
+    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
+    pw = packed_weight.contiguous()
+    bs = block_scales.contiguous()
+    with torch.cuda.device(dev):
+        ws = workspace(fmt, True, M, out_features, in_features, group_size, grad_y.dtype, dev)
+        N.check(getattr(N.lib(), _BWD[fmt])(N.ptr(gy), N.ptr(pw), N.ptr(bs), N.ptr(gx), M,
+                                            out_features, in_features, group_size, dt,
+                                            N.ptr(ws), 0 if ws is None else ws.numel(),
+                                            N.stream_handle(dev)),
+                _BWD[fmt][4:])
+    return gx.reshape(*grad_y.shape[:-1], in_features)
+
+
+@torch.library.custom_op(f"{_NS}::e8t_linear", mutates_args=())
+def e8t_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+               bias: Optional[torch.Tensor], out_features: int, in_features: int,
+               group_size: int) -> torch.Tensor:
+    N.require_device(x, packed_weight, block_scales, bias)
+    _check_gs(group_size)
+    if x.shape[-1] != in_features:
+        raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    _check_layer_buffers(packed_weight, block_scales, out_features, in_features, group_size)
+    return _linear_fwd(FMT_TERNARY, x, packed_weight, block_scales, bias, out_features,
+                       in_features, group_size)
 
 
 @e8t_linear.register_fake
@@ -160,22 +216,11 @@ def _(x, packed_weight, block_scales, bias, out_features, in_features, group_siz
 def e8t_linear_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
                       block_scales: torch.Tensor, out_features: int, in_features: int,
                       group_size: int) -> torch.Tensor:
-    dev = N.require_device(grad_y, packed_weight, block_scales)
+    N.require_device(grad_y, packed_weight, block_scales)
     _check_gs(group_size)
-    if grad_y.shape[-1] != out_features:
-        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
     _check_layer_buffers(packed_weight, block_scales, out_features, in_features, group_size)
-    dt = _dtype_code(grad_y.dtype)
-    gy = grad_y.reshape(-1, out_features).contiguous()
-    M = gy.shape[0]
-    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
-    with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8t_gemm_bwd_dx(N.ptr(gy), N.ptr(packed_weight.contiguous()),
-                                            N.ptr(block_scales.contiguous()), N.ptr(gx), M,
-                                            out_features, in_features, group_size, dt,
-                                            N.stream_handle(dev)),
-                "gemm_bwd_dx")
-    return gx.reshape(*grad_y.shape[:-1], in_features)
+    return _linear_bwd(FMT_TERNARY, grad_y, packed_weight, block_scales, out_features,
+                       in_features, group_size)
 
 
 @e8t_linear_bwd_dx.register_fake
@@ -311,9 +356,11 @@ def decode2(packed: torch.Tensor, scales: torch.Tensor, numel: int, group_size: 
     if packed.numel() < padded // 4 or scales.numel() < padded // group_size:
         raise RuntimeError(
             f"packed/scales too small for {numel} weights at group_size {group_size}")
+    packed = packed.contiguous()
+    scales = scales.contiguous()
     out = torch.empty(numel, dtype=dtype, device=dev)
     with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8_decode(N.ptr(packed.contiguous()), N.ptr(scales.contiguous()),
+        N.check(N.lib().ojx_e8_decode(N.ptr(packed), N.ptr(scales),
                                       numel, group_size, _dtype_code(dtype), N.ptr(out),
                                       N.stream_handle(dev)),
                 "e8 decode")
@@ -346,27 +393,13 @@ def e8_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.
               bias: Optional[torch.Tensor], out_features: int, in_features: int,
               group_size: int) -> torch.Tensor:
     """2-bit fused linear: x . Wdeq^T + bias, Wdeq = (code - 1.5) * scale in x's dtype."""
-    dev = N.require_device(x, packed_weight, block_scales, bias)
+    N.require_device(x, packed_weight, block_scales, bias)
     _check_gs2(group_size, 4)
     if x.shape[-1] != in_features:
         raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
     _check_layer_buffers2(packed_weight, block_scales, out_features, in_features, group_size)
-    dt = _dtype_code(x.dtype)
-    x2 = x.reshape(-1, in_features).contiguous()
-    M = x2.shape[0]
-    y = torch.empty((M, out_features), dtype=x.dtype, device=dev)
-    b = None
-    if bias is not None:
-        if bias.numel() != out_features:
-            raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
-        b = bias.to(x.dtype).contiguous()
-    with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8_gemm_fwd(N.ptr(x2), N.ptr(packed_weight.contiguous()),
-                                        N.ptr(block_scales.contiguous()), N.ptr(b), N.ptr(y), M,
-                                        out_features, in_features, group_size, dt,
-                                        N.stream_handle(dev)),
-                "e8 gemm_fwd")
-    return y.reshape(*x.shape[:-1], out_features)
+    return _linear_fwd(FMT_E8, x, packed_weight, block_scales, bias, out_features, in_features,
+                       group_size)
 
 
 @e8_linear.register_fake
@@ -378,22 +411,11 @@ def _(x, packed_weight, block_scales, bias, out_features, in_features, group_siz
 def e8_linear_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
                      block_scales: torch.Tensor, out_features: int, in_features: int,
                      group_size: int) -> torch.Tensor:
-    dev = N.require_device(grad_y, packed_weight, block_scales)
+    N.require_device(grad_y, packed_weight, block_scales)
     _check_gs2(group_size, 4)
-    if grad_y.shape[-1] != out_features:
-        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
     _check_layer_buffers2(packed_weight, block_scales, out_features, in_features, group_size)
-    dt = _dtype_code(grad_y.dtype)
-    gy = grad_y.reshape(-1, out_features).contiguous()
-    M = gy.shape[0]
-    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
-    with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8_gemm_bwd_dx(N.ptr(gy), N.ptr(packed_weight.contiguous()),
-                                           N.ptr(block_scales.contiguous()), N.ptr(gx), M,
-                                           out_features, in_features, group_size, dt,
-                                           N.stream_handle(dev)),
-                "e8 gemm_bwd_dx")
-    return gx.reshape(*grad_y.shape[:-1], in_features)
+    return _linear_bwd(FMT_E8, grad_y, packed_weight, block_scales, out_features, in_features,
+                       group_size)
 
 
 @e8_linear_bwd_dx.register_fake
@@ -515,9 +537,11 @@ def decode1(codes: torch.Tensor, scales: torch.Tensor, numel: int, group_size: i
     if codes.numel() < padded // 8 or scales.numel() < padded // group_size:
         raise RuntimeError(
             f"codes/scales too small for {numel} weights at group_size {group_size}")
+    codes = codes.contiguous()
+    scales = scales.contiguous()
     out = torch.empty(numel, dtype=dtype, device=dev)
     with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8r_decode(N.ptr(codes.contiguous()), N.ptr(scales.contiguous()),
+        N.check(N.lib().ojx_e8r_decode(N.ptr(codes), N.ptr(scales),
                                        numel, group_size, _dtype_code(dtype), N.ptr(out),
                                        N.stream_handle(dev)),
                 "e8r decode")
@@ -550,27 +574,13 @@ def e8r_linear(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch
                bias: Optional[torch.Tensor], out_features: int, in_features: int,
                group_size: int) -> torch.Tensor:
     """1-bit fused linear: x . Wdeq^T + bias, Wdeq = table[code] * scale in x's dtype."""
-    dev = N.require_device(x, packed_weight, block_scales, bias)
+    N.require_device(x, packed_weight, block_scales, bias)
     _check_gs2(group_size, 8)
     if x.shape[-1] != in_features:
         raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
     _check_layer_buffers1(packed_weight, block_scales, out_features, in_features, group_size)
-    dt = _dtype_code(x.dtype)
-    x2 = x.reshape(-1, in_features).contiguous()
-    M = x2.shape[0]
-    y = torch.empty((M, out_features), dtype=x.dtype, device=dev)
-    b = None
-    if bias is not None:
-        if bias.numel() != out_features:
-            raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
-        b = bias.to(x.dtype).contiguous()
-    with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8r_gemm_fwd(N.ptr(x2), N.ptr(packed_weight.contiguous()),
-                                         N.ptr(block_scales.contiguous()), N.ptr(b), N.ptr(y), M,
-                                         out_features, in_features, group_size, dt,
-                                         N.stream_handle(dev)),
-                "e8r gemm_fwd")
-    return y.reshape(*x.shape[:-1], out_features)
+    return _linear_fwd(FMT_ROOT, x, packed_weight, block_scales, bias, out_features,
+                       in_features, group_size)
 
 
 @e8r_linear.register_fake
@@ -582,22 +592,11 @@ def _(x, packed_weight, block_scales, bias, out_features, in_features, group_siz
 def e8r_linear_bwd_dx(grad_y: torch.Tensor, packed_weight: torch.Tensor,
                       block_scales: torch.Tensor, out_features: int, in_features: int,
                       group_size: int) -> torch.Tensor:
-    dev = N.require_device(grad_y, packed_weight, block_scales)
+    N.require_device(grad_y, packed_weight, block_scales)
     _check_gs2(group_size, 8)
-    if grad_y.shape[-1] != out_features:
-        raise RuntimeError(f"grad_y has {grad_y.shape[-1]} features, expected {out_features}")
     _check_layer_buffers1(packed_weight, block_scales, out_features, in_features, group_size)
-    dt = _dtype_code(grad_y.dtype)
-    gy = grad_y.reshape(-1, out_features).contiguous()
-    M = gy.shape[0]
-    gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
-    with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8r_gemm_bwd_dx(N.ptr(gy), N.ptr(packed_weight.contiguous()),
-                                            N.ptr(block_scales.contiguous()), N.ptr(gx), M,
-                                            out_features, in_features, group_size, dt,
-                                            N.stream_handle(dev)),
-                "e8r gemm_bwd_dx")
-    return gx.reshape(*grad_y.shape[:-1], in_features)
+    return _linear_bwd(FMT_ROOT, grad_y, packed_weight, block_scales, out_features, in_features,
+                       group_size)
 
 
 @e8r_linear_bwd_dx.register_fake

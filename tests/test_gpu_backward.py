@@ -102,7 +102,8 @@ def test_bwd_llama8b_shapes_every_element(fmt, M, name, N, K):
 
 
 def test_bwd_graph_capture_matches_eager():
-    # inside capture the split reduction is off (no scratch): every replay matches eager
+    # the captured launch keeps its K split (caller-owned workspace from the graph's pool):
+    # every replay, with eager split work in between, is bit-identical to the eager result
     M, N, K = 64, 2048, 1024
     gw = torch.Generator(device=DEV).manual_seed(9)
     pk, sc = ops.encode(torch.randn(N, K, generator=gw, device=DEV) * 0.02, 32)
@@ -123,4 +124,4 @@ def test_bwd_graph_capture_matches_eager():
         ops.e8t_linear_bwd_dx(gy, pk, sc, N, K, 32)
         graph.replay()
         torch.cuda.synchronize()
-        assert ((out.float() - eager.float()).abs().max() / eager.float().abs().max()).item() <= 1e-2, rep
+        assert torch.equal(out, eager), rep

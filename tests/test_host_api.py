@@ -22,7 +22,7 @@ HEADER = os.path.join(ROOT, "include", "ojasx_e8t.h")
 
 def _declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(ojx_e8[tr]?_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ojx_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_exports():
@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = N.lib()
     for name in _declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.ojx_e8t_version() >= 100
+    assert lib.ojx_e8t_version() >= 20000
 
 
 def test_library_has_gfx950_code_object():
@@ -51,34 +51,38 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert lib.ojx_e8t_encode(None, 0, 16, 24, None, None, None) == -2
     assert b"multiple of 16" in lib.ojx_e8t_last_error()
     assert lib.ojx_e8t_decode(None, None, 16, 0, 0, None, None) == -2
-    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, -1, 4, 4, 32, 0, None) == -1
-    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 1, 4, 4, 32, 9, None) == -3
-    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 1, 4, 32, 32, 0, None) == -1
-    assert lib.ojx_e8t_gemm_bwd_dx(None, None, None, None, 1, 4, 32, 20, 2, None) == -2
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, -1, 4, 4, 32, 0, None, 0, None) == -1
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 1, 4, 4, 32, 9, None, 0, None) == -3
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 1, 4, 32, 32, 0, None, 0, None) == -1
+    assert lib.ojx_e8t_gemm_bwd_dx(None, None, None, None, 1, 4, 32, 20, 2, None, 0, None) == -2
     # empty work is a no-op success
     assert lib.ojx_e8t_encode(None, 0, 0, 32, None, None, None) == 0
-    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, None) == 0
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, None, 0, None) == 0
     # 2-bit: the packer's group rule (multiple of 8), the native op's (multiple of 4)
     assert lib.ojx_e8_encode(None, 0, 64, 12, None, None, None) == -2
     assert b"multiple of 8" in lib.ojx_e8t_last_error()
     assert lib.ojx_e8_encode(None, 0, -1, 8, None, None, None) == -1
     assert lib.ojx_e8_decode(None, None, 16, 4, 0, None, None) == -2
-    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 1, 4, 8, 6, 0, None) == -2
+    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 1, 4, 8, 6, 0, None, 0, None) == -2
     assert b"multiple of 4" in lib.ojx_e8t_last_error()
-    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 1, 4, 8, 4, 9, None) == -3
-    assert lib.ojx_e8_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None) == -1
+    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 1, 4, 8, 4, 9, None, 0, None) == -3
+    assert lib.ojx_e8_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None, 0, None) == -1
     assert lib.ojx_e8_encode(None, 0, 0, 8, None, None, None) == 0
-    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None) == 0
+    assert lib.ojx_e8_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None, 0, None) == 0
     # 1-bit Root E8: group sizes are multiples of 8 everywhere (the packer coerces first)
     assert lib.ojx_e8r_encode(None, 0, 64, 12, None, None, None) == -2
     assert b"multiple of 8" in lib.ojx_e8t_last_error()
     assert lib.ojx_e8r_encode(None, 0, -1, 8, None, None, None) == -1
     assert lib.ojx_e8r_decode(None, None, 16, 4, 0, None, None) == -2
-    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 1, 4, 8, 4, 0, None) == -2
-    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 1, 4, 8, 8, 9, None) == -3
-    assert lib.ojx_e8r_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None) == -1
+    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 1, 4, 8, 4, 0, None, 0, None) == -2
+    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 1, 4, 8, 8, 9, None, 0, None) == -3
+    assert lib.ojx_e8r_gemm_bwd_dx(None, None, None, None, -1, 4, 8, 8, 0, None, 0, None) == -1
     assert lib.ojx_e8r_encode(None, 0, 0, 8, None, None, None) == 0
-    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None) == 0
+    # a workspace size without a workspace, or a misaligned one, is refused before any launch
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, None, 64,
+                                None) == -1
+    assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, 8, 64, None) == -2
+    assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None, 0, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -285,3 +289,34 @@ def test_randomized_hadamard_transform_matches_reference_steps():
     w3 = torch.randn(5, 7)
     rot3, b1, b2 = ojasx_amd.randomized_hadamard_transform(w3, seed=None)
     assert torch.equal(rot3, (w3 * b2.unsqueeze(0)) * b1.unsqueeze(1))
+
+
+def _ws(fmt, bwd, M, N_out, K, gs=32, dtype=N.BF16):
+    n = ctypes.c_size_t(123)
+    st = N.lib().ojx_gemm_workspace_bytes(fmt, bwd, M, N_out, K, gs, dtype, ctypes.byref(n))
+    assert st == 0, N.lib().ojx_e8t_last_error()
+    return n.value
+
+
+def test_workspace_query_follows_the_dispatch():
+    """ojx_gemm_workspace_bytes is host-only logic: decode GEMVs and large prefill grids need
+    no scratch; small prefill grids split over K and need splits x M x N fp32 partials."""
+    # decode (M <= 16) never needs a workspace, for any format
+    for fmt in (0, 1, 2):
+        for M in (1, 4, 16):
+            assert _ws(fmt, 0, M, 4096, 4096) == 0
+    # M = 8192 on a q-shaped layer fills the GPU unsplit
+    assert _ws(0, 0, 8192, 4096, 4096) == 0
+    # M = 512 on the k/v shape splits: a whole number of M x N fp32 slabs
+    b = _ws(0, 0, 512, 1024, 4096)
+    assert b > 0 and b % (512 * 1024 * 4) == 0 and b // (512 * 1024 * 4) >= 2
+    # backward dX of a small grid also splits (its output is [M, K])
+    b = _ws(0, 1, 512, 1024, 4096)
+    assert b > 0 and b % (512 * 4096 * 4) == 0
+    # fp32 activations run the general kernel: no scratch
+    assert _ws(0, 0, 512, 1024, 4096, dtype=N.F32) == 0
+    # errors: unknown format, bad group size, null result pointer
+    n = ctypes.c_size_t(0)
+    assert N.lib().ojx_gemm_workspace_bytes(7, 0, 1, 1, 32, 32, 2, ctypes.byref(n)) == -1
+    assert N.lib().ojx_gemm_workspace_bytes(0, 0, 1, 1, 32, 24, 2, ctypes.byref(n)) == -2
+    assert N.lib().ojx_gemm_workspace_bytes(0, 0, 1, 1, 32, 32, 2, None) == -1
