@@ -103,6 +103,18 @@ int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scale
                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                      int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of ojx_e8t_gemm_fwd (same arguments minus the workspace, same
+ * kernels and results).  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The prefill K split's partial sums go to a static device array of
+ * 64 MiB (one copy per GPU the library runs this on, held until the process ends; every
+ * Llama-3-8B prefill shape fits).  A shape whose split needs more is refused with
+ * OJX_ELAYOUT before any launch.  All calls on one GPU share that GPU's array: calls on one
+ * stream are ordered, calls that overlap on one GPU (other streams) race. */
+int ojx_e8t_gemm_fwd_noalloc(const void* x, const uint8_t* packed, const uint16_t* scales,
+                             const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                             int64_t gs, int dtype, void* stream);
+
 /* Fused backward grad_x[M,K] = grad_y[M,N] . Wdeq[N,K], fp32 accumulation, in dtype.
  * Replaces fused_ternary_e8_gemm_bwd_dx (ojasx_math_bindings.cpp:479-533, schema :594);
  * called from _FusedE8GEMMFunction.backward (lattice.py:656-696).  Workspace as above. */

@@ -25,6 +25,7 @@ SOURCES = [
     "e8t_gemv.hip",
     "e8t_gemm_mfma.hip",
     "e8t_qat.hip",
+    "e8t_noalloc.hip",
     "e8t_capi.cpp",
 ]
 

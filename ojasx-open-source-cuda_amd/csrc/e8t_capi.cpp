@@ -75,6 +75,10 @@ int done(hipError_t e, const char* what) {
 
 }  // namespace
 
+namespace ojx {
+int api_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace ojx
+
 // The prefill MFMA GEMM with its tile configuration and K split.  The split's fp32 partial
 // sums live in the caller's workspace; a workspace smaller than the plan's (or none) lowers
 // the split count to what fits, down to the unsplit kernel.

@@ -128,6 +128,9 @@ hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t
                             int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs = 32,
                             int fmt = 0, bool bwd = false);
 
+// Records `msg` as the calling thread's last error (ojx_e8t_last_error) and returns `code`.
+int api_fail(int code, const char* msg);
+
 // Bytes of fp32 K-split scratch a launch with choice `c` uses (0 when unsplit).
 inline size_t gemm_split_bytes(const GemmChoice& c, int64_t M, int64_t out_cols) {
     return c.splits > 1 ? (size_t)c.splits * (size_t)split_stride(M, out_cols) * sizeof(float)

@@ -26,6 +26,7 @@ EXPORTS = (
     "ojx_e8t_decode",
     "ojx_gemm_workspace_bytes",
     "ojx_e8t_gemm_fwd",
+    "ojx_e8t_gemm_fwd_noalloc",
     "ojx_e8t_gemm_bwd_dx",
     "ojx_e8t_gemv_grouped_plan",
     "ojx_e8t_gemv_grouped",
@@ -92,6 +93,9 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8t_gemm_fwd.restype = _INT
             L.ojx_e8t_gemm_fwd.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
                                           _SZ, _P]
+            L.ojx_e8t_gemm_fwd_noalloc.restype = _INT
+            L.ojx_e8t_gemm_fwd_noalloc.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                                   _INT, _P]
             L.ojx_e8t_gemm_bwd_dx.restype = _INT
             L.ojx_e8t_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
                                              _SZ, _P]
