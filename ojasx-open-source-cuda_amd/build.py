@@ -68,6 +68,15 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link of libojasx_e8t.so failed")
+    # a kernel template the host pass could not instantiate leaves its launch stub undefined
+    # (the link of a shared library does not catch it); refuse such a library
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--undefined-only", tmp], capture_output=True,
+                             text=True).stdout
+        missing = [l.split()[-1] for l in out.splitlines() if "ojx" in l]
+        if missing:
+            raise RuntimeError("libojasx_e8t.so has undefined symbols: " + ", ".join(missing[:4]))
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)

@@ -137,11 +137,19 @@ static int check_fmt_args(int fmt, const void* a, const uint8_t* packed, const u
 
 // Kernel family of a forward / backward launch (the dispatch below).  Pointer alignment
 // takes part in it; the workspace query passes null pointers (aligned).
-enum Route { kRouteGemv2m, kRouteGemv, kRouteGemv2, kRouteMfma, kRouteGeneric };
+enum Route { kRouteGemvTile, kRouteGemv2m, kRouteGemv, kRouteGemv2, kRouteMfma, kRouteGeneric };
+
+#ifndef OJX_TILE_TILES_BELOW
+#define OJX_TILE_TILES_BELOW 1024
+#endif
 
 static Route route_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
                        const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype) {
     if (fmt == ojx::kFmtTernary) {
+        // layers too small to stream (per-linear decode launches), M <= 4: staged tiles
+        if ((N + 15) / 16 < OJX_TILE_TILES_BELOW &&
+            ojx::gemv_tile_supported(x, packed, scales, y, M, N, K, gs, dtype))
+            return kRouteGemvTile;
         // 4 < M <= 16 on a layer too small for the streaming mask kernel (< 1024 row tiles):
         // one 16-row tile per workgroup, K split over its waves, weights in the B operand
         if (M > 4 && (N + 15) / 16 < 1024 &&
@@ -182,6 +190,16 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = hipSuccess;
     switch (route_fwd(fmt, x, packed, scales, y, M, N, K, gs, dtype)) {
+    case kRouteGemvTile: {
+        ojx::GemvLaunch a{};
+        ojx::GemvJob& j = a.inl[0];
+        j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
+        j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
+        a.njobs = 1;
+        a.M = (int)M;
+        e = ojx::launch_gemv_tile(a, (N + 15) / 16, K, dtype, s);
+        break;
+    }
     case kRouteGemv2m:
         e = ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt);
         break;

@@ -1738,6 +1738,306 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     }
 }
 
+
+// ------------------------------------------------------------------------- staged-tile GEMV
+//
+// Decode GEMV (M <= 4) for launches with few row tiles: the per-linear launches of a
+// decoder's linears (1-15 MB each).  Such a launch never streams long enough to reach the
+// HBM ceiling; its time is the kernel start, one memory round trip and the work that depends
+// on it.  So every wave issues all of its loads at its first instructions: the codes and
+// scales of its own 1024-k rounds of the workgroup's 16-row tile and the matching
+// activations, by 16-byte buffer->LDS loads into the wave's own stage (the 224 per-linear
+// launches of the 32-layer stack move these bytes in about 0.7 ms on MI355X, against 0.68 ms
+// for a plain read of the weights).  The decode table is computed while they are in flight
+// (one workgroup barrier); then each wave waits only for its own loads, round by round, and
+// runs that round's MFMAs while its later rounds still arrive.
+//
+// Work: one workgroup of 4 waves per 16-row tile; wave w takes rounds [w U, min(w U + U, T))
+// of the T = K / 1024 rounds.  In round u lane (g, n) holds codes 32g .. 32g + 31 of row n
+// (k = 1024u + 256g .. + 255) and their 8 group scales; step j (0..31) contracts
+// k = 1024u + 256g + 8j + (0..7) with A row i16 = activation row i16 (lanes of rows >= M
+// skip the read and keep zeros: only M lanes per lane group touch LDS) and B = code j's
+// weights (table masks AND-ed with the scale word, as the other B-operand GEMVs).  Two
+// accumulators alternate between steps; the waves' partial sums are added through LDS and
+// wave 0 stores rows m < M.
+//
+// Stage of one round (each lane of a buffer->LDS load writes a fixed 16-byte slot, so the
+// placement is chosen through the piece each lane fetches): codes, row n's 12 pieces at
+// slots 12n + (p + n/4) mod 12; scales, row n's 4 pieces at 4n + (p + n/4) mod 4; then
+// MM activation rows of 128 pieces, piece p of row m at m * 128 + (p ^ m).  The 16 lanes of
+// a lane group then read 16 distinct bank groups.
+
+constexpr int kTileWaves = 4;
+constexpr uint32_t kTileRoundCodes = 16 * 192;  // one round's codes of 16 rows
+
+template <int MM>
+struct TileStage {
+    static constexpr uint32_t kScales = kTileRoundCodes;          // offset of the scales
+    static constexpr uint32_t kX = kScales + 1024;                // offset of the activations
+    static constexpr int kXLoads = (145 * (MM - 1) + 140 + 63) / 64;  // 1-KB loads of them
+    static constexpr uint32_t kBytes = kX + kXLoads * 1024;           // one round
+    static constexpr int kLoads = 4 + kXLoads;                    // 1-KB loads per round
+};
+
+// One 16-byte-per-lane buffer->LDS load (1 KB per wave) into `dst`.  (Not a template: the
+// host pass drops a kernel template that calls this builtin directly.)
+__device__ __forceinline__ void dma_1k(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(dst), 16, voffset, 0, 0, 0);
+}
+
+// Issues round u's loads into `stg`: three of codes, one of scales, `xloads` of activations.
+__device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
+                                           __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t xr,
+                                           uint32_t row0, uint32_t rowbytes, uint32_t srowbytes,
+                                           uint32_t xrowbytes, int u, int lane, int xloads,
+                                           int M) {
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const uint32_t sl = 64u * t + lane, n = sl / 12u, q = sl - 12u * n;
+        const uint32_t p = (q + 12u - n / 4u) % 12u;
+        dma_1k(pr, stg + 1024 * t, (row0 + n) * rowbytes + 192u * u + 16u * p);
+    }
+    {
+        const uint32_t n = (uint32_t)lane >> 2, q = (uint32_t)lane & 3u;
+        const uint32_t p = (q + 4u - (n / 4u) % 4u) % 4u;
+        dma_1k(sr, stg + kTileRoundCodes, (row0 + n) * srowbytes + 64u * u + 16u * p);
+    }
+    // activations: row m's piece p at slot 145 m + p + 4 (p / 32) (the lane groups' 32-piece
+    // runs 36 slots apart); unused slots and rows >= M read zeros
+    for (int i = 0; i < xloads; ++i) {
+        const uint32_t sl = 64u * i + lane, m = sl / 145u, r = sl - 145u * m;
+        const uint32_t blk = r / 36u, wi = r - 36u * blk;
+        const uint32_t off = (m < (uint32_t)M && blk < 4u && wi < 32u)
+                                 ? m * xrowbytes + 2048u * u + 16u * (32u * blk + wi)
+                                 : 0xFFFFFFF0u;
+        dma_1k(xr, stg + kTileRoundCodes + 1024 + 1024 * i, off);
+    }
+}
+
+// Depth of the software pipeline of a round: the table and activation reads of step
+// J + kTileAhead are issued before the MFMA of step J (with one wave per SIMD, a step that
+// waited for its own reads would expose the whole LDS latency).
+#ifndef OJX_TILE_AHEAD
+#define OJX_TILE_AHEAD 4
+#endif
+constexpr int kTileAhead = OJX_TILE_AHEAD;
+
+// The staged-tile kernel's table: 32 slices (conflict-free b64 reads: 2.2 clk per wave
+// read on MI355X against 3.7 with 16 slices, where neighbouring lanes share banks), holding
+// the coordinates themselves (+-1, 0 in the activation dtype).
+constexpr int kTileSlots = 32;
+using TileLut = LutGeom<kTileSlots>;
+
+// One post-scaled 1024-k round (the layout of gemv_ps_kernel): A row 4g' + m carries
+// activation row m only in lane group g''s k slots (every other lane's fragment is zero), so
+// lane (g', n)'s MFMA result rows 4g' + q are the partial sums of its own codes for
+// activation rows q; after the 4 steps of one scale group they are multiplied by that
+// group's scale into the fp32 accumulators.  The table and activation reads of step
+// J + kTileAhead are issued before the MFMA of step J; two D registers alternate between
+// scale groups.
+template <int DT, int MM>
+struct TileRound {
+    uint32_t cd[12];  // this lane's 32 codes
+    uint32_t scw[4];  // their 8 group scales (fp16 pairs)
+    const char* lut;
+    const char* xa;   // this lane's A fragment of step 0 (activations or a zero run)
+    uint32_t slot;
+
+    struct Pending {
+        uint4 a[kTileAhead], b[kTileAhead];
+    };
+
+    template <int J>
+    __device__ __forceinline__ void reads(Pending& p) const {
+        constexpr int r = J % kTileAhead;
+        p.a[r] = *reinterpret_cast<const uint4*>(xa + 16 * J);
+        const uint32_t d[3] = {cd[3 * (J / 8)], cd[3 * (J / 8) + 1], cd[3 * (J / 8) + 2]};
+        const uint32_t z = code_z<J % 8, TileLut::kCodeShift>(d, slot);
+        const uint32_t h = __umulhi(z, TileLut::kHiMagic);
+        const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of<TileLut::kStride>(h, z));
+        const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * TileLut::kStride + slot));
+        p.b[r] = make_uint4(ml.x, ml.y, mh.x, mh.y);
+    }
+    template <int J>
+    __device__ __forceinline__ void step(Pending& p, f32x4 (&d)[2], float (&acc)[MM]) const {
+        constexpr int r = J % kTileAhead, gi = J / 4;  // scale group of the step
+        f32x4& dg = d[gi & 1];
+        const uint4 a = p.a[r];
+        const uint4 b = p.b[r];
+        if constexpr (J + kTileAhead < 32) reads<(J + kTileAhead < 32 ? J + kTileAhead : 0)>(p);
+        dg = mfma16<DT>(a, b, J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dg);
+        if constexpr (J % 4 == 3) {  // scale group gi complete: post-scale it
+            float s0, s1;
+            scale_pair_f32<DT>(scw[gi / 2], s0, s1);
+            const float sg = (gi & 1) ? s1 : s0;
+#pragma unroll
+            for (int q = 0; q < MM; ++q) acc[q] = __builtin_fmaf(dg[q], sg, acc[q]);
+            keep_mfma_result(dg, acc[0]);
+        }
+    }
+    template <int... J>
+    __device__ __forceinline__ void prologue(Pending& p, std::integer_sequence<int, J...>) const {
+        (reads<J>(p), ...);
+    }
+    template <int... J>
+    __device__ __forceinline__ void steps(float (&acc)[MM], std::integer_sequence<int, J...>) const {
+        Pending p;
+        f32x4 d[2];
+        prologue(p, std::make_integer_sequence<int, kTileAhead>{});
+        (step<J>(p, d, acc), ...);
+    }
+};
+
+// 16-byte item i of a bank-sliced table of `kind` (e8t_lut.h) with SLOTS slices, computed:
+// two slices of entry i / (SLOTS / 2) - guard (the guard entry is zero).
+template <int SLOTS>
+__device__ __forceinline__ uint4 lut_item(int i, int kind) {
+    const int e = i / (SLOTS / 2) - LutGeom<SLOTS>::kGuard;
+    if (e < 0) return make_uint4(0u, 0u, 0u, 0u);
+    const int d0 = e % 3, d1 = (e / 3) % 3, d2 = (e / 9) % 3, d3 = (e / 27) % 3;
+    const uint32_t w0 = lut_half(kind, d0) | (lut_half(kind, d1) << 16);
+    const uint32_t w1 = lut_half(kind, d2) | (lut_half(kind, d3) << 16);
+    return make_uint4(w0, w1, w0, w1);
+}
+
+// Waits until at most n of this wave's loads are outstanding (gfx9 vmcnt encoding).
+template <int n>
+__device__ __forceinline__ void vm_wait_le() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
+}
+
+template <int DT, int MM, int U, int TPW>
+__global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLaunch args) {
+    using S = TileStage<MM>;
+    constexpr int L = S::kLoads;
+    constexpr int NW = kTileWaves * TPW;  // waves of the workgroup
+    static_assert(L * U <= 63, "loads in flight per wave");
+    __shared__ __attribute__((aligned(16))) char stage[NW * U * S::kBytes];
+    __shared__ uint4 lut_storage[TileLut::kValidStorageU4];
+    // zero A fragments: lane l of step J reads zrun[l + J] (distinct addresses, no broadcast);
+    // later the waves' partial sums
+    __shared__ uint4 zrun[NW * 16 > 96 ? NW * 16 : 96];
+
+    int64_t wg = blockIdx.x;
+    GemvJob job;
+    if (args.jobs != nullptr) {
+        job = args.jobs[find_job(args.jobs, args.njobs, wg)];
+    } else {
+        job = args.inl[0];
+#pragma unroll
+        for (int i = 1; i < kGemvInlineJobs; ++i)
+            if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
+    }
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sub = wave / kTileWaves, wt = wave % kTileWaves;  // tile of the workgroup, K part
+    const int64_t tile = (wg - job.wg_begin) * TPW + sub;
+    const void* xbase = job.x ? job.x : args.x;
+    void* ybase = job.y ? job.y : args.y;
+
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t N = job.N, K = job.K;
+    const int M = args.M;
+    const int T = (int)(K / 1024);
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16), srowbytes = (uint32_t)(K / 16);
+    const uint32_t row0 = (uint32_t)(tile * 16);
+    const int u0 = wt * U;
+    const int nr = T - u0 < U ? (T - u0 > 0 ? T - u0 : 0) : U;  // rounds of this wave
+
+    // ---- every load first (rows >= N and activation rows >= M read zeros)
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)xbase, (short)0, (int)(M * K * 2), kRsrcWord3);
+    char* const wstage = stage + wave * U * S::kBytes;
+#pragma unroll
+    for (int i = 0; i < U; ++i)
+        if (i < nr)
+            tile_issue(wstage + i * S::kBytes, pr, sr, xr, row0, rowbytes, srowbytes,
+                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M);
+
+    // ---- decode table (computed) while the loads are in flight
+    for (int i = (int)threadIdx.x; i < TileLut::kValidStorageU4; i += 64 * NW)
+        lut_storage[i] = lut_item<kTileSlots>(i, lut_values_kind<DT>());
+    if (threadIdx.x < 96) zrun[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t bias_bits = 0u;
+    if (wt == 0 && job.bias) {
+        const int64_t r = (int64_t)row0 + i16 < N ? (int64_t)row0 + i16 : N - 1;
+        bias_bits = ((const __attribute__((address_space(1))) uint16_t*)job.bias)[r];
+    }
+    __syncthreads();
+
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + TileLut::kBaseOffset;
+    const uint32_t slot = (uint32_t)(lane & (kTileSlots - 1)) * 8u;
+    // A row i16 = 4g' + m is live in lane group g' for activation rows m < M: piece 32g + J of
+    // row m (slot 145 m + 36 g + J); every other lane reads zeros
+    const int am = i16 & 3;
+    const bool a_live = (i16 >> 2) == g && am < M;
+    const char* const zbase = reinterpret_cast<const char*>(zrun) + 16 * lane;
+    const uint32_t xa0 = 16u * (145u * (uint32_t)am + 36u * (uint32_t)g);
+    const uint32_t rq = (uint32_t)i16 / 4u;
+    float acc[MM];
+#pragma unroll
+    for (int q = 0; q < MM; ++q) acc[q] = 0.f;
+    auto round = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        if (i >= nr) return;
+        // round i's loads have landed when at most the later rounds' are outstanding
+        if (nr == U) vm_wait_le<L * (U - 1 - i)>();
+        else vm_wait_all();
+        const char* stg = wstage + i * S::kBytes;
+        TileRound<DT, MM> r;
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const uint32_t q = (3u * (uint32_t)g + (uint32_t)t + rq) % 12u;
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + (12u * i16 + q) * 16u);
+            r.cd[4 * t] = v.x;
+            r.cd[4 * t + 1] = v.y;
+            r.cd[4 * t + 2] = v.z;
+            r.cd[4 * t + 3] = v.w;
+        }
+        const uint4 sc = *reinterpret_cast<const uint4*>(
+            stg + S::kScales + (4u * i16 + (((uint32_t)g + rq) & 3u)) * 16u);
+        r.scw[0] = sc.x;
+        r.scw[1] = sc.y;
+        r.scw[2] = sc.z;
+        r.scw[3] = sc.w;
+        r.lut = lut;
+        r.xa = a_live ? stg + S::kX + xa0 : zbase;
+        r.slot = slot;
+        r.steps(acc, std::make_integer_sequence<int, 32>{});
+    };
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (round(std::integral_constant<int, I>{}), ...);
+    }(std::make_integer_sequence<int, U>{});
+
+    // sum the four lane groups of each row (lane group q keeps activation row q), then the
+    // waves through LDS (zrun is no longer read)
+    float out = 0.f;
+#pragma unroll
+    for (int q = 0; q < MM; ++q) {
+        float v = acc[q];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (q == g) out = v;
+    }
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(zrun);  // NW x 64 floats
+    red[wave * 64 + lane] = out;
+    __syncthreads();
+    if (wt != 0) return;
+#pragma unroll
+    for (int w2 = 1; w2 < kTileWaves; ++w2) out += red[(wave + w2) * 64 + lane];
+    const int64_t row = (int64_t)row0 + i16;
+    if (g < M && row < N) {
+        const float bv = job.bias ? bias_bits_to_f32<DT>(bias_bits) : 0.f;
+        store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out + bv);
+    }
+}
+
 // ------------------------------------------------------------------------- host side
 
 bool gemv_shape_ok(int64_t N, int64_t K) {
@@ -1952,6 +2252,89 @@ hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* s
     return dt == kBF16
                ? launch_gemv2m_gs<kBF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream)
                : launch_gemv2m_gs<kF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream);
+}
+
+
+// ---- staged-tile GEMV launch
+
+// Rounds per wave (1, 2 or 4) of a staged-tile launch whose longest K has Kmax / 1024
+// rounds, 0 if its stages would not fit: M == 1 up to K = 16384, M <= 4 up to K = 8192.
+int gemv_tile_rounds(int64_t M, int64_t Kmax) {
+    const int64_t T = Kmax / 1024;
+    const int64_t U = (T + kTileWaves - 1) / kTileWaves;
+    if (M < 1 || M > 4 || T < 1) return 0;
+    if (U <= 1) return 1;
+    if (U <= 2) return 2;
+    if (U <= 4 && M == 1) return 4;
+    return 0;
+}
+
+// Row tiles per workgroup of a staged-tile launch over `tiles` row tiles of K <= 4096: two
+// when M == 1 and the launch has too many tiles for one-tile workgroups to be resident at
+// once (their stages and table take 51 KB: three per CU), which shares the table between
+// two tiles.
+#ifndef OJX_TILE_PAIR_FROM
+#define OJX_TILE_PAIR_FROM 768
+#endif
+int gemv_tile_per_wg(int64_t M, int64_t tiles) {
+    return (M == 1 && tiles >= OJX_TILE_PAIR_FROM) ? 2 : 1;
+}
+
+bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                         const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+    if (dt != kBF16 && dt != kF16) return false;
+    if (gs != 32 || N < 1 || K < 1024 || K % 1024 != 0 || gemv_tile_rounds(M, K) == 0)
+        return false;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 15u) || ((uintptr_t)scales & 15u) ||
+        ((uintptr_t)y & 1u))
+        return false;
+    // 32-bit buffer offsets (with one tile of row padding)
+    return (N + 16) * (K * 3 / 16) < (1ll << 31) && M * K * 2 < (1ll << 31);
+}
+
+template <int DT, int MM, int U, int TPW>
+static hipError_t launch_tile_tpw(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW>), dim3((unsigned)((tiles + TPW - 1) / TPW)),
+                       dim3(64 * kTileWaves * TPW), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int DT, int MM, int U>
+static hipError_t launch_tile_t(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
+    return launch_tile_tpw<DT, MM, U, 1>(a, tiles, s);
+}
+
+// two tiles per workgroup: K <= 4096 at M == 1 only (gemv_tile_per_wg)
+template <>
+hipError_t launch_tile_t<kBF16, 1, 1>(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
+    return gemv_tile_per_wg(a.M, tiles) == 2 ? launch_tile_tpw<kBF16, 1, 1, 2>(a, tiles, s)
+                                             : launch_tile_tpw<kBF16, 1, 1, 1>(a, tiles, s);
+}
+template <>
+hipError_t launch_tile_t<kF16, 1, 1>(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
+    return gemv_tile_per_wg(a.M, tiles) == 2 ? launch_tile_tpw<kF16, 1, 1, 2>(a, tiles, s)
+                                             : launch_tile_tpw<kF16, 1, 1, 1>(a, tiles, s);
+}
+
+template <int DT>
+static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, hipStream_t s) {
+    if (a.M == 1) {
+        if (U == 1) return launch_tile_t<DT, 1, 1>(a, wgs, s);
+        if (U == 2) return launch_tile_t<DT, 1, 2>(a, wgs, s);
+        if (U == 4) return launch_tile_t<DT, 1, 4>(a, wgs, s);
+        return hipErrorInvalidValue;
+    }
+    if (U == 1) return launch_tile_t<DT, 4, 1>(a, wgs, s);
+    if (U == 2) return launch_tile_t<DT, 4, 2>(a, wgs, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t wgs, int64_t Kmax, int dt,
+                            hipStream_t s) {
+    if (wgs <= 0) return hipSuccess;
+    const int U = gemv_tile_rounds(a.M, Kmax);
+    if (wgs > 0x7FFFFFFF || U == 0) return hipErrorInvalidValue;
+    return dt == kBF16 ? launch_tile_dt<kBF16>(a, wgs, U, s) : launch_tile_dt<kF16>(a, wgs, U, s);
 }
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,

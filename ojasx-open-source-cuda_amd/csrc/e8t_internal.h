@@ -107,6 +107,16 @@ int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream);
 
+// Staged-tile decode GEMV (per-linear launches of small layers): 1 <= M <= 4, bf16/fp16,
+// ternary codes with group size 32, K % 1024 == 0 up to K = 8192 (M = 1: 16384), 16-byte
+// aligned buffers.  One workgroup per 16-row tile (wgs = the row tiles of the launch's
+// jobs); Kmax the longest K of the jobs.
+int gemv_tile_rounds(int64_t M, int64_t Kmax);
+bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
+                         const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t wgs, int64_t Kmax, int dt,
+                            hipStream_t stream);
+
 // Prefill MFMA GEMM: F16/BF16, K % 64 == 0; fmt 0 (ternary, group size 32), 1 (2-bit) or 2
 // (1-bit Root E8), the last two with group size 8, 16, 32 or 64.
 // bwd: the backward dX y[M, K] = x[M, N] . W[N, K] (also needs N % 64 == 0).

@@ -135,11 +135,25 @@ constexpr int kLutValidStorageU4 = (kLutValidEntries + kLutGuard) * kLutSlots / 
 // Byte offset of entry 0 in the storage.
 constexpr uint32_t kLutBaseOffset = kLutGuard * kLutStride;
 
+// Geometry of a bank-sliced table with SLOTS copies (the constants above are SLOTS =
+// kLutSlots); kernels that need another slice count than the library-wide one use these.
+template <int SLOTS>
+struct LutGeom {
+    static_assert(SLOTS == 8 || SLOTS == 16 || SLOTS == 32, "8, 16 or 32 table slices");
+    static constexpr uint32_t kStride = SLOTS * 8;
+    static constexpr int kCodeShift = SLOTS == 32 ? 9 : (SLOTS == 16 ? 8 : 7);
+    static constexpr uint32_t kHiMagic = SLOTS == 32 ? 207127u : (SLOTS == 16 ? 414253u : 828505u);
+    static constexpr int kGuard = SLOTS == 32 ? 1 : 0;
+    static constexpr int kValidStorageU4 = (81 + kGuard) * SLOTS / 2;
+    static constexpr uint32_t kBaseOffset = kGuard * kStride;
+};
+
 // Z = (code_j << kCodeShift) | slot for code j (0..7) of the 12-byte, 8-code group
 // (d0, d1, d2): code j occupies bits [12j, 12j+12) of the little-endian stream
 // (lattice.py:375-383).
-template <int J>
+template <int J, int SHIFT = kCodeShift>
 __device__ __forceinline__ uint32_t code_z(const uint32_t (&d)[3], uint32_t slot) {
+    constexpr int kCodeShift = SHIFT;
     constexpr int p = 12 * J, w = p / 32, o = p % 32;
     uint32_t t;
     if constexpr (o + 12 <= 32) {
@@ -153,9 +167,10 @@ __device__ __forceinline__ uint32_t code_z(const uint32_t (&d)[3], uint32_t slot
 
 // lo address = Z - 81 * kLutStride * hi = (2c - 81 hi) * kLutStride + slot, as one
 // full-rate 24-bit multiply-add (the compiler otherwise picks a 64-bit v_mad_u64_u32).
+template <uint32_t STRIDE = kLutStride>
 __device__ __forceinline__ uint32_t lo_addr_of(uint32_t h, uint32_t z) {
     uint32_t r;
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(h), "s"(-81 * (int)kLutStride), "v"(z));
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(h), "s"(-81 * (int)STRIDE), "v"(z));
     return r;
 }
 

@@ -57,8 +57,10 @@ def test_gemv_matches_oracle(dtype, M, N, K):
 
 @pytest.mark.parametrize("N", [16 * 256, 16 * 512, 16 * 1024, 16 * 2048, 16 * 8192 + 48])
 def test_gemv_every_variant(N):
-    # tiles = N/16 selects the kernel: < 512 -> K split 4 ways, < 1024 -> K split 2 ways,
-    # >= 1024 -> the streaming (wide) kernel; the last size also has a ragged final tile
+    # per-linear launches at M = 16: < 1024 row tiles run the B-operand GEMV (gemv2m),
+    # >= 1024 the streaming mask kernel; the last size also has a ragged final tile.  (The
+    # in-workgroup K-split GEMV, S = 4 / 2, is reached by grouped launches of < 512 / < 1024
+    # tiles: test_gpu_configs.py::test_grouped_512_to_1023_tiles and the grouped tests here.)
     K, M = 256, 16
     pk, sc, pk_np, sc_np = _encoded(N, K, seed=N)
     x = _x(M, K, seed=3, dtype=torch.bfloat16)
@@ -180,4 +182,37 @@ def test_wide_kernel_fp16_and_subnormal_scales(M):
     y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
     torch.cuda.synchronize()
     ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_F16)
+    assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K", [(1, 1024), (3, 1024), (1, 2048), (4, 3072), (2, 8192),
+                                 (4, 8192), (1, 12288), (1, 16384)])
+def test_staged_tile_gemv_round_counts(dtype, M, K):
+    # per-linear launches of fewer than 1024 row tiles at M <= 4 and K % 1024 == 0 run the
+    # staged-tile kernel: 1..16 rounds of 1024 k over 4 waves (idle waves for K < 4096,
+    # up to 4 rounds per wave), ragged last tile, bias
+    N = 16 * 37 + 9
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=K + M)
+    x = _x(M, K, seed=M * 11 + K, dtype=dtype)
+    bias = _x(1, N, seed=5, dtype=dtype).reshape(N)
+    print(f"staged tile M={M} K={K} {dtype}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32,
+                     DT_CODE[dtype])
+    assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("K", [1024, 4096])
+def test_staged_tile_gemv_two_tile_workgroups(K):
+    # 777 row tiles at M = 1 (two tiles per workgroup): an odd tile count, so the last
+    # workgroup's second tile lies past N, and a ragged last tile
+    N = 16 * 776 + 7
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=N + K)
+    x = _x(1, K, seed=K, dtype=torch.bfloat16)
+    print(f"staged tile pairs N={N} K={K}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
     assert _rel(y, ref) <= REL_TOL
