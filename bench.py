@@ -571,7 +571,9 @@ class E8Decoder:
     """random-init Llama-3-8B-shaped decoder, every linear (and lm_head)
     ternary-E8 packed (group 32), rank-8 bf16 LoRA on q/v, RMSNorm and RoPE in bf16.
     Attention (not part of the E8 path) is computed in fp32 with a pre-transposed K
-    cache; decode steps run the E8 linears as grouped GEMVs (fused q/k/v and gate/up)."""
+    cache; decode steps run the E8 linears as grouped GEMVs (fused q/k/v and gate/up).
+    The adapters are added inside the E8 kernels' epilogue (u = scaling * x @ A by
+    ojx_lora_down, u @ B before the output is rounded), in prefill and decode alike."""
 
     def __init__(self, torch, dev, cfg, layers, seed=9500):
         import ojasx_amd
@@ -634,9 +636,6 @@ class E8Decoder:
         xf = x.float()
         x1, x2 = xf[..., :h], xf[..., h:]
         return self.t.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
-
-    def lora(self, m, h):
-        return m.scaling * ((h @ m.lora_A) @ m.lora_B)
 
     # ---- prefill: M = batch * prompt rows through the prefill MFMA GEMM
     def prefill(self, ids, e8_events=None):
@@ -704,9 +703,9 @@ class E8Decoder:
         for li, ly in enumerate(self.layers):
             h = self.rms(x, ly["n1"])
             qkv = ly["qkv_g"](h)
-            q = qkv[:, :H] + self.lora(ly["q"], h)
+            q = qkv[:, :H]  # the q/v adapters are fused into the grouped launch
             k = qkv[:, H:H + kvd]
-            v = qkv[:, H + kvd:] + self.lora(ly["v"], h)
+            v = qkv[:, H + kvd:]
             q = self.rope(q.view(B, nh, hd), cos, sin)            # fp32 [B, nh, hd]
             k = self.rope(k.view(B, nkv, hd), cos, sin)
             self.kt[li].index_copy_(3, pos, k.unsqueeze(-1))

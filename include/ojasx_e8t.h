@@ -115,6 +115,36 @@ int ojx_e8t_gemm_fwd_noalloc(const void* x, const uint8_t* packed, const uint16_
                              const void* bias, void* y, int64_t M, int64_t N, int64_t K,
                              int64_t gs, int dtype, void* stream);
 
+/* LoRA down-projection u[M, rank] = scaling * x[M, K] . A[K, rank] in fp32 (x and A in
+ * dtype; 1 <= rank <= 64).  The first half of E8LatticeLinear's adapter term
+ * scaling * ((x @ lora_A) @ lora_B) (ojasx2/math/lattice.py:839-842); the fused forwards
+ * below (and grouped GEMV jobs with lora_r > 0) add u @ B in their output epilogue. */
+int ojx_lora_down(const void* x, const void* lora_a, int64_t M, int64_t K, int64_t rank,
+                  float scaling, int dtype, float* u, void* stream);
+
+/* Fused forward with a LoRA adapter: y = x . Wdeq^T (+ bias) + scaling * (x @ A) @ B, the
+ * adapter term added in fp32 before the one rounding to dtype.  Replaces the E8 op plus
+ * the two matmuls and the add of E8LatticeLinear.forward (lattice.py:827-846; A [K, rank]
+ * = lora_A, B [rank, N] = lora_B, both in dtype).  lora_u: caller-owned fp32 [M, rank]
+ * scratch that receives u = scaling * (x @ A) (ojx_lora_down, launched first on the same
+ * stream).  Other arguments and the workspace as ojx_e8t_gemm_fwd; the e8 / e8r variants
+ * take the 2-bit and 1-bit formats. */
+int ojx_e8t_gemm_fwd_lora(const void* x, const uint8_t* packed, const uint16_t* scales,
+                          const void* bias, const void* lora_a, const void* lora_b,
+                          int64_t rank, float scaling, float* lora_u, void* y, int64_t M,
+                          int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int ojx_e8_gemm_fwd_lora(const void* x, const uint8_t* packed, const uint16_t* scales,
+                         const void* bias, const void* lora_a, const void* lora_b, int64_t rank,
+                         float scaling, float* lora_u, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t gs, int dtype, void* workspace, size_t workspace_bytes,
+                         void* stream);
+int ojx_e8r_gemm_fwd_lora(const void* x, const uint8_t* codes, const uint16_t* scales,
+                          const void* bias, const void* lora_a, const void* lora_b,
+                          int64_t rank, float scaling, float* lora_u, void* y, int64_t M,
+                          int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* Fused backward grad_x[M,K] = grad_y[M,N] . Wdeq[N,K], fp32 accumulation, in dtype.
  * Replaces fused_ternary_e8_gemm_bwd_dx (ojasx_math_bindings.cpp:479-533, schema :594);
  * called from _FusedE8GEMMFunction.backward (lattice.py:656-696).  Workspace as above. */
@@ -217,6 +247,10 @@ typedef struct ojx_e8t_gemv_job {
     int64_t y_col;          /* y[m, y_col + n] receives output n of row m          */
     int64_t y_ld;           /* row stride of y in elements (0 means N)             */
     int64_t wg_begin;       /* written by ojx_e8t_gemv_grouped_plan                */
+    const float* lora_u;    /* LoRA adapter (lora_r > 0): u = scaling * (x @ A),   */
+    const void* lora_b;     /*   fp32 [M, lora_r] (row stride lora_ldu, 0 = r),    */
+    int64_t lora_r;         /*   B [lora_r, N] in dtype; y += u @ B is added before */
+    int64_t lora_ldu;       /*   the output is rounded (ojx_lora_down computes u)   */
 } ojx_e8t_gemv_job;
 
 /* Validates `jobs` (host array) for batch M and dtype, fills each wg_begin (and y_ld

@@ -26,6 +26,7 @@ SOURCES = [
     "e8t_gemm_mfma.hip",
     "e8t_qat.hip",
     "e8t_noalloc.hip",
+    "e8t_lora.hip",
     "e8t_capi.cpp",
 ]
 

@@ -86,7 +86,7 @@ int api_fail(int code, const char* msg) { return fail(code, "%s", msg); }
 static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                               const void* bias, void* y, int64_t M, int64_t N, int64_t K,
                               int64_t gs, int dtype, hipStream_t s, int fmt, bool bwd,
-                              void* ws, size_t ws_bytes) {
+                              void* ws, size_t ws_bytes, const ojx::LoraEp& lora = ojx::LoraEp{}) {
     const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
     ojx::GemmChoice c = ojx::gemm_mfma_choice(M, out_cols, red);
     const size_t per = (size_t)ojx::split_stride(M, out_cols) * sizeof(float);
@@ -94,7 +94,7 @@ static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16
     if (c.splits > fit) c.splits = fit < 2 ? 1 : (int)fit;
     float* part = c.splits > 1 ? static_cast<float*>(ws) : nullptr;
     return ojx::launch_gemm_mfma(x, packed, scales, bias, y, part, c, M, N, K, dtype, s, gs, fmt,
-                                 bwd);
+                                 bwd, lora);
 }
 
 // Workspace pointer contract shared by the GEMM entry points.
@@ -182,7 +182,8 @@ static const char* fmt_name(int fmt) {
 // Forward of every format: y[M, N] = x . Wdeq^T (+ bias).
 static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
                     const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                    int dtype, void* ws, size_t ws_bytes, void* stream) {
+                    int dtype, void* ws, size_t ws_bytes, void* stream,
+                    const ojx::LoraEp& lora = ojx::LoraEp{}) {
     if (int r = check_fmt_args(fmt, x, packed, scales, y, M, N, K, gs, dtype)) return r;
     if (int r = check_workspace(ws, ws_bytes)) return r;
     if (M == 0 || N == 0) return OJX_OK;
@@ -195,22 +196,24 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
         ojx::GemvJob& j = a.inl[0];
         j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
         j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
+        j.lora_u = lora.u; j.lora_b = lora.b; j.lora_r = lora.r; j.lora_ldu = lora.ldu;
         a.njobs = 1;
         a.M = (int)M;
         e = ojx::launch_gemv_tile(a, (N + 15) / 16, K, dtype, s);
         break;
     }
     case kRouteGemv2m:
-        e = ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt);
+        e = ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt, lora);
         break;
     case kRouteGemv2:
-        e = ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s);
+        e = ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s, lora);
         break;
     case kRouteGemv: {
         ojx::GemvLaunch a{};
         ojx::GemvJob& j = a.inl[0];
         j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
         j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
+        j.lora_u = lora.u; j.lora_b = lora.b; j.lora_r = lora.r; j.lora_ldu = lora.ldu;
         a.njobs = 1;
         a.M = (int)M;
         const ojx::GemvPlan plan = ojx::gemv_pick((N + 15) / 16, M);
@@ -219,16 +222,38 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
     }
     case kRouteMfma:
         e = launch_mfma(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt, false, ws,
-                        ws_bytes);
+                        ws_bytes, lora);
         break;
     case kRouteGeneric:
-        e = ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt);
+        e = ojx::launch_gemm_generic_fwd(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt,
+                                         lora);
         break;
     }
     if (e != hipSuccess) return fail(OJX_EHIP, "%s gemm_fwd launch: %s", fmt_name(fmt),
                                      hipGetErrorString(e));
     g_last_error[0] = '\0';
     return OJX_OK;
+}
+
+// Forward with a LoRA adapter: u = scaling * (x @ A) into the caller's lora_u, then the
+// format's forward with u @ B added in its output epilogue.
+static int gemm_fwd_lora(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
+                         const void* bias, const void* lora_a, const void* lora_b, int64_t rank,
+                         float scaling, float* lora_u, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t gs, int dtype, void* ws, size_t ws_bytes, void* stream) {
+    if (rank < 1 || rank > ojx::kLoraMaxRank)
+        return fail(OJX_ELAYOUT, "LoRA rank must be in 1..%lld (got %lld)",
+                    (long long)ojx::kLoraMaxRank, (long long)rank);
+    if (M > 0 && N > 0 && (!lora_a || !lora_b || !lora_u))
+        return fail(OJX_EINVAL, "null LoRA pointer");
+    if (int r = check_fmt_args(fmt, x, packed, scales, y, M, N, K, gs, dtype)) return r;
+    if (M == 0 || N == 0) return OJX_OK;
+    if (int r = check_device()) return r;
+    const hipError_t e = ojx::launch_lora_down(x, lora_a, M, K, rank, scaling, dtype, lora_u,
+                                               rank, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(OJX_EHIP, "lora_down launch: %s", hipGetErrorString(e));
+    return gemm_fwd(fmt, x, packed, scales, bias, y, M, N, K, gs, dtype, ws, ws_bytes, stream,
+                    ojx::LoraEp{lora_u, lora_b, rank, rank, N});
 }
 
 // Backward dX of every format: grad_x[M, K] = grad_y[M, N] . Wdeq[N, K].
@@ -334,6 +359,13 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
         if (((uintptr_t)j.packed & 3u) || ((uintptr_t)j.scales & 3u) || ((uintptr_t)j.x & 15u) ||
             ((uintptr_t)j.y & 1u) || ((uintptr_t)j.bias & 1u))
             return fail(OJX_ELAYOUT, "job %d: misaligned pointer", i);
+        if (j.lora_r < 0 || j.lora_r > ojx::kLoraMaxRank)
+            return fail(OJX_ELAYOUT, "job %d: LoRA rank must be in 0..%lld", i,
+                        (long long)ojx::kLoraMaxRank);
+        if (j.lora_r > 0 && (!j.lora_u || !j.lora_b || ((uintptr_t)j.lora_u & 3u) ||
+                             ((uintptr_t)j.lora_b & 1u) ||
+                             (j.lora_ldu != 0 && j.lora_ldu < j.lora_r)))
+            return fail(OJX_EINVAL, "job %d: bad LoRA operands", i);
         const int64_t ld = j.y_ld ? j.y_ld : j.N;
         if (j.y_col < 0 || ld < j.y_col + j.N)
             return fail(OJX_ELAYOUT, "job %d: y_ld %lld < y_col %lld + N %lld", i, (long long)ld,
@@ -471,6 +503,52 @@ __attribute__((visibility("default"))) int ojx_e8t_gemm_fwd(
     size_t workspace_bytes, void* stream) {
     return gemm_fwd(ojx::kFmtTernary, x, packed, scales, bias, y, M, N, K, gs, dtype, workspace,
                     workspace_bytes, stream);
+}
+
+__attribute__((visibility("default"))) int ojx_lora_down(const void* x, const void* lora_a,
+                                                         int64_t M, int64_t K, int64_t rank,
+                                                         float scaling, int dtype, float* u,
+                                                         void* stream) {
+    if (M < 0 || K < 0) return fail(OJX_EINVAL, "negative size M=%lld K=%lld", (long long)M,
+                                    (long long)K);
+    if (!valid_dtype(dtype)) return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
+    if (rank < 1 || rank > ojx::kLoraMaxRank)
+        return fail(OJX_ELAYOUT, "LoRA rank must be in 1..%lld (got %lld)",
+                    (long long)ojx::kLoraMaxRank, (long long)rank);
+    if (M == 0) return OJX_OK;
+    if (!x || !lora_a || !u) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_lora_down(x, lora_a, M, K, rank, scaling, dtype, u, rank,
+                                      (hipStream_t)stream),
+                "lora_down launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8t_gemm_fwd_lora(
+    const void* x, const uint8_t* packed, const uint16_t* scales, const void* bias,
+    const void* lora_a, const void* lora_b, int64_t rank, float scaling, float* lora_u, void* y,
+    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    return gemm_fwd_lora(ojx::kFmtTernary, x, packed, scales, bias, lora_a, lora_b, rank,
+                         scaling, lora_u, y, M, N, K, gs, dtype, workspace, workspace_bytes,
+                         stream);
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemm_fwd_lora(
+    const void* x, const uint8_t* packed, const uint16_t* scales, const void* bias,
+    const void* lora_a, const void* lora_b, int64_t rank, float scaling, float* lora_u, void* y,
+    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    return gemm_fwd_lora(ojx::kFmt2Bit, x, packed, scales, bias, lora_a, lora_b, rank, scaling,
+                         lora_u, y, M, N, K, gs, dtype, workspace, workspace_bytes, stream);
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemm_fwd_lora(
+    const void* x, const uint8_t* codes, const uint16_t* scales, const void* bias,
+    const void* lora_a, const void* lora_b, int64_t rank, float scaling, float* lora_u, void* y,
+    int64_t M, int64_t N, int64_t K, int64_t gs, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    return gemm_fwd_lora(ojx::kFmtRoot, x, codes, scales, bias, lora_a, lora_b, rank, scaling,
+                         lora_u, y, M, N, K, gs, dtype, workspace, workspace_bytes, stream);
 }
 
 __attribute__((visibility("default"))) int ojx_e8t_gemm_bwd_dx(

@@ -63,6 +63,34 @@ template <int DT> __device__ __forceinline__ float scale_for(uint32_t s16) {
     return s;
 }
 
+// ---------------------------------------------------------------- LoRA epilogue
+
+// Low-rank term of a fused forward with a LoRA adapter (E8LatticeLinear.forward,
+// lattice.py:839-842: out + scaling * ((x @ A) @ B)): y[m, n] += sum_j u[m, j] * B[j, n], with
+// u = scaling * (x @ A) in fp32 [M, r] (row stride ldu) and B the up-projection [r, N] in the
+// activation dtype (row stride ldb).  r == 0: no adapter.
+struct LoraEp {
+    const float* u;
+    const void* b;
+    int64_t r;
+    int64_t ldu;
+    int64_t ldb;
+};
+
+template <int DT>
+__device__ __forceinline__ float lora_term(const float* u, const void* b, int64_t r, int64_t ldu,
+                                           int64_t ldb, int64_t m, int64_t n) {
+    float s = 0.f;
+    for (int64_t j = 0; j < r; ++j)
+        s = __builtin_fmaf(u[m * ldu + j], load_as_f32<DT>(b, j * ldb + n), s);
+    return s;
+}
+
+template <int DT>
+__device__ __forceinline__ float lora_term(const LoraEp& l, int64_t m, int64_t n) {
+    return l.r > 0 ? lora_term<DT>(l.u, l.b, l.r, l.ldu, l.ldb, m, n) : 0.f;
+}
+
 // ---------------------------------------------------------------- packed codes
 
 // 12-bit code t of the packed stream (lattice.py:397-405).

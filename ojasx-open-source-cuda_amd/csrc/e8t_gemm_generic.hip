@@ -34,7 +34,7 @@ template <int FMT, int DT>
 __global__ __launch_bounds__(256) void gemm_generic_fwd(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int64_t M, int64_t N, int64_t K, int64_t gs) {
+    int64_t M, int64_t N, int64_t K, int64_t gs, LoraEp lora) {
     __shared__ float xs[kChunk][kTile + 4];
     __shared__ float ws[kChunk][kTile + 4];
     const int tid = threadIdx.x;
@@ -74,6 +74,7 @@ __global__ __launch_bounds__(256) void gemm_generic_fwd(
             if (gn >= N) continue;
             float v = acc[i][j];
             if (bias) v += load_as_f32<DT>(bias, gn);
+            v += lora_term<DT>(lora, gm, gn);
             store_from_f32<DT>(y, gm * N + gn, v);
         }
     }
@@ -136,10 +137,10 @@ __global__ __launch_bounds__(256) void gemm_generic_bwd(
 template <int FMT, int DT>
 static hipError_t fwd_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        hipStream_t stream) {
+                        hipStream_t stream, const LoraEp& lora) {
     dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
     hipLaunchKernelGGL((gemm_generic_fwd<FMT, DT>), grid, dim3(256), 0, stream, x, packed, scales,
-                       bias, y, M, N, K, gs);
+                       bias, y, M, N, K, gs, lora);
     return hipGetLastError();
 }
 
@@ -155,11 +156,11 @@ static hipError_t bwd_t(const void* gy, const uint8_t* packed, const uint16_t* s
 template <int FMT>
 static hipError_t fwd_fmt(const void* x, const uint8_t* packed, const uint16_t* scales,
                           const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                          int dt, hipStream_t stream) {
+                          int dt, hipStream_t stream, const LoraEp& lora) {
     switch (dt) {
-        case kF32: return fwd_t<FMT, kF32>(x, packed, scales, bias, y, M, N, K, gs, stream);
-        case kF16: return fwd_t<FMT, kF16>(x, packed, scales, bias, y, M, N, K, gs, stream);
-        default: return fwd_t<FMT, kBF16>(x, packed, scales, bias, y, M, N, K, gs, stream);
+        case kF32: return fwd_t<FMT, kF32>(x, packed, scales, bias, y, M, N, K, gs, stream, lora);
+        case kF16: return fwd_t<FMT, kF16>(x, packed, scales, bias, y, M, N, K, gs, stream, lora);
+        default: return fwd_t<FMT, kBF16>(x, packed, scales, bias, y, M, N, K, gs, stream, lora);
     }
 }
 
@@ -176,11 +177,13 @@ static hipError_t bwd_fmt(const void* gy, const uint8_t* packed, const uint16_t*
 
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                                   int64_t gs, int dt, hipStream_t stream, int fmt) {
-    if (fmt == kFmtRoot) return fwd_fmt<kFmtRoot>(x, packed, scales, bias, y, M, N, K, gs, dt, stream);
+                                   int64_t gs, int dt, hipStream_t stream, int fmt,
+                                   const LoraEp& lora) {
+    if (fmt == kFmtRoot)
+        return fwd_fmt<kFmtRoot>(x, packed, scales, bias, y, M, N, K, gs, dt, stream, lora);
     return fmt == kFmt2Bit
-               ? fwd_fmt<kFmt2Bit>(x, packed, scales, bias, y, M, N, K, gs, dt, stream)
-               : fwd_fmt<kFmtTernary>(x, packed, scales, bias, y, M, N, K, gs, dt, stream);
+               ? fwd_fmt<kFmt2Bit>(x, packed, scales, bias, y, M, N, K, gs, dt, stream, lora)
+               : fwd_fmt<kFmtTernary>(x, packed, scales, bias, y, M, N, K, gs, dt, stream, lora);
 }
 
 hipError_t launch_gemm_generic_bwd(const void* gy, const uint8_t* packed, const uint16_t* scales,

@@ -530,7 +530,7 @@ template <int DT, typename C, int FMT, int GS2, bool BWD>
 __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    float* __restrict__ part, int splits, int64_t M, int64_t N, int64_t K) {
+    float* __restrict__ part, int splits, int64_t M, int64_t N, int64_t K, LoraEp lora) {
     constexpr bool kTernary = FMT == kFmtTernary;
     const int64_t NO = BWD ? K : N;  // output columns
     const int64_t R = BWD ? N : K;   // reduction length (row length of x)
@@ -702,7 +702,11 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t row = m0 + arow0 + 16 * i + 4 * g + q;
-                if (row < M) store_from_f32<DT>(y, row * NO + col, acc[i][j][q] + bv);
+                if (row < M) {
+                    float v = acc[i][j][q] + bv;
+                    if (!BWD) v += lora_term<DT>(lora, row, col);
+                    store_from_f32<DT>(y, row * NO + col, v);
+                }
             }
         }
     }
@@ -712,7 +716,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 template <int DT>
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     const float* __restrict__ part, int splits, const void* __restrict__ bias,
-    void* __restrict__ y, int64_t M, int64_t N) {
+    void* __restrict__ y, int64_t M, int64_t N, LoraEp lora) {
     const int64_t MN = M * N, stride = split_stride(M, N);
     const int64_t i4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i4 >= MN) return;
@@ -725,15 +729,16 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
         const float v[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float bv = bias ? load_as_f32<DT>(bias, (i4 + e) % N) : 0.f;
-            store_from_f32<DT>(y, i4 + e, v[e] + bv);
+            const int64_t i = i4 + e;
+            const float bv = bias ? load_as_f32<DT>(bias, i % N) : 0.f;
+            store_from_f32<DT>(y, i, v[e] + bv + lora_term<DT>(lora, i / N, i % N));
         }
     } else {
         for (int64_t i = i4; i < MN; ++i) {
             float a = 0.f;
             for (int s = 0; s < splits; ++s) a += part[(int64_t)s * stride + i];
             const float bv = bias ? load_as_f32<DT>(bias, i % N) : 0.f;
-            store_from_f32<DT>(y, i, a + bv);
+            store_from_f32<DT>(y, i, a + bv + lora_term<DT>(lora, i / N, i % N));
         }
     }
 }
@@ -769,17 +774,18 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
 template <int DT, typename C, int FMT, int GS2, bool BWD>
 static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_t* scales,
                              const void* bias, void* y, float* part, int splits, int64_t M,
-                             int64_t N, int64_t K, hipStream_t stream) {
+                             int64_t N, int64_t K, hipStream_t stream, const LoraEp& lora) {
     const int64_t NO = BWD ? K : N;
     const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((NO + C::BN - 1) / C::BN);
     if (tiles * splits > 0x7FFFFFFF) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemm_mfma_kernel<DT, C, FMT, GS2, BWD>), dim3((unsigned)(tiles * splits)),
                        dim3(C::THREADS), 0, stream, x, packed, scales, bias, y, part, splits, M,
-                       N, K);
+                       N, K, lora);
     if (splits == 1) return hipGetLastError();
     const int64_t groups = (M * NO + 1023) / 1024;
     hipLaunchKernelGGL((gemm_split_reduce_kernel<DT>), dim3((unsigned)groups), dim3(256), 0,
-                       stream, part, splits, BWD ? nullptr : bias, y, M, NO);
+                       stream, part, splits, BWD ? nullptr : bias, y, M, NO,
+                       BWD ? LoraEp{} : lora);
     return hipGetLastError();
 }
 
@@ -825,24 +831,25 @@ GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K) {
 template <int DT, typename C, bool BWD>
 static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_t* scales,
                              const void* bias, void* y, float* part, int splits, int64_t M,
-                             int64_t N, int64_t K, int64_t gs, int fmt, hipStream_t stream) {
+                             int64_t N, int64_t K, int64_t gs, int fmt, hipStream_t stream,
+                             const LoraEp& lora) {
     if (fmt == kFmtTernary)
         return launch_cfg<DT, C, kFmtTernary, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N,
-                                                  K, stream);
+                                                  K, stream, lora);
     if (fmt == kFmtRoot) {
         switch (gs) {
         case 8:
             return launch_cfg<DT, C, kFmtRoot, 8, BWD>(x, packed, scales, bias, y, part, splits, M, N,
-                                                  K, stream);
+                                                  K, stream, lora);
         case 16:
             return launch_cfg<DT, C, kFmtRoot, 16, BWD>(x, packed, scales, bias, y, part, splits, M, N,
-                                                   K, stream);
+                                                   K, stream, lora);
         case 32:
             return launch_cfg<DT, C, kFmtRoot, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N,
-                                                   K, stream);
+                                                   K, stream, lora);
         case 64:
             return launch_cfg<DT, C, kFmtRoot, 64, BWD>(x, packed, scales, bias, y, part, splits, M, N,
-                                                   K, stream);
+                                                   K, stream, lora);
         default:
             return hipErrorInvalidValue;
         }
@@ -850,16 +857,16 @@ static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_
     switch (gs) {
     case 8:
         return launch_cfg<DT, C, kFmt2Bit, 8, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
-                                              stream);
+                                              stream, lora);
     case 16:
         return launch_cfg<DT, C, kFmt2Bit, 16, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
-                                               stream);
+                                               stream, lora);
     case 32:
         return launch_cfg<DT, C, kFmt2Bit, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
-                                               stream);
+                                               stream, lora);
     case 64:
         return launch_cfg<DT, C, kFmt2Bit, 64, BWD>(x, packed, scales, bias, y, part, splits, M, N, K,
-                                               stream);
+                                               stream, lora);
     default:
         return hipErrorInvalidValue;
     }
@@ -868,28 +875,28 @@ static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, float* part, GemmChoice c, int64_t M,
                             int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs,
-                            int fmt, bool bwd) {
+                            int fmt, bool bwd, const LoraEp& lora) {
     if (c.splits < 1 || (c.splits > 1 && !part)) return hipErrorInvalidValue;
     if (bwd) {
         if (dt == kBF16)
             return c.small ? launch_fmt<kBF16, CfgSmall, true>(x, packed, scales, bias, y, part,
-                                                               c.splits, M, N, K, gs, fmt, stream)
+                                                               c.splits, M, N, K, gs, fmt, stream, lora)
                            : launch_fmt<kBF16, CfgLarge, true>(x, packed, scales, bias, y, part,
-                                                               c.splits, M, N, K, gs, fmt, stream);
+                                                               c.splits, M, N, K, gs, fmt, stream, lora);
         return c.small ? launch_fmt<kF16, CfgSmall, true>(x, packed, scales, bias, y, part,
-                                                          c.splits, M, N, K, gs, fmt, stream)
+                                                          c.splits, M, N, K, gs, fmt, stream, lora)
                        : launch_fmt<kF16, CfgLarge, true>(x, packed, scales, bias, y, part,
-                                                          c.splits, M, N, K, gs, fmt, stream);
+                                                          c.splits, M, N, K, gs, fmt, stream, lora);
     }
     if (dt == kBF16)
         return c.small ? launch_fmt<kBF16, CfgSmall, false>(x, packed, scales, bias, y, part,
-                                                            c.splits, M, N, K, gs, fmt, stream)
+                                                            c.splits, M, N, K, gs, fmt, stream, lora)
                        : launch_fmt<kBF16, CfgLarge, false>(x, packed, scales, bias, y, part,
-                                                            c.splits, M, N, K, gs, fmt, stream);
+                                                            c.splits, M, N, K, gs, fmt, stream, lora);
     return c.small ? launch_fmt<kF16, CfgSmall, false>(x, packed, scales, bias, y, part, c.splits,
-                                                       M, N, K, gs, fmt, stream)
+                                                       M, N, K, gs, fmt, stream, lora)
                    : launch_fmt<kF16, CfgLarge, false>(x, packed, scales, bias, y, part, c.splits,
-                                                       M, N, K, gs, fmt, stream);
+                                                       M, N, K, gs, fmt, stream, lora);
 }
 
 }  // namespace ojx

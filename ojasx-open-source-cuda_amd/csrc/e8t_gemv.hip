@@ -143,6 +143,14 @@ __device__ __forceinline__ void compute_chunk(const Codes<R>& ch, uint4 (&xa)[8]
     if (cn >= 0) load_x(xa[7], cn, 7, st);
 }
 
+// LoRA term of output (m, n) of a job (0 without an adapter).
+template <int DT>
+__device__ __forceinline__ float job_lora(const GemvJob& job, int64_t m, int64_t n) {
+    if (job.lora_r <= 0) return 0.f;
+    return lora_term<DT>(job.lora_u, job.lora_b, job.lora_r,
+                         job.lora_ldu ? job.lora_ldu : job.lora_r, job.N, m, n);
+}
+
 __device__ __forceinline__ int find_job(const GemvJob* jobs, int njobs, int64_t wg) {
     int lo = 0, hi = njobs - 1;
     while (lo < hi) {  // last job with wg_begin <= wg
@@ -259,7 +267,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
         for (int q = 0; q < 4; ++q) {
             const int m = 4 * g + q;
             if (m < M) store_from_f32<DT>(ybase, (int64_t)m * job.y_ld + job.y_col + row,
-                                          acc[r][q] + bv);
+                                          acc[r][q] + bv + job_lora<DT>(job, m, row));
         }
     }
 }
@@ -623,7 +631,7 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
         for (int q = 0; q < 4; ++q) {
             const int m = 4 * g + q;
             if (m < M) store_from_f32<DT>(ybase, (int64_t)m * job.y_ld + job.y_col + row,
-                                          acc[r][q] + bv);
+                                          acc[r][q] + bv + job_lora<DT>(job, m, row));
         }
     }
 }
@@ -849,7 +857,8 @@ __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M,
             acc[r][q] = 0.f;
         }
         if (row < job.N && g < M)
-            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out + bias_bits_to_f32<DT>(bv[r]));
+            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row,
+                               out + bias_bits_to_f32<DT>(bv[r]) + job_lora<DT>(job, g, row));
     }
 }
 
@@ -1285,7 +1294,7 @@ template <int DT, int MM, int GS>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int M, int64_t N, int64_t K) {
+    int M, int64_t N, int64_t K, LoraEp lora) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
     __shared__ uint4 lut_storage[kB2LutU4];
     // Two activation buffers per wave, each its own LDS object ending in a zero block, so
@@ -1382,7 +1391,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     }
     if ((int64_t)row < N && g < M) {
         const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
-        store_from_f32<DT>(y, (int64_t)g * N + row, out + bv);
+        store_from_f32<DT>(y, (int64_t)g * N + row, out + bv + lora_term<DT>(lora, g, row));
     }
 }
 
@@ -1616,7 +1625,7 @@ template <int DT, int GS, int FMT>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int M, int64_t N, int64_t K) {
+    int M, int64_t N, int64_t K, LoraEp lora) {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
     static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
     static_assert(FMT != kFmtTernary || GS == 32, "ternary GEMV: group size 32");
@@ -1732,7 +1741,9 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int m = 4 * g + q;
-                if (m < M) store_from_f32<DT>(y, (int64_t)m * N + row, acc[r][q] + bv);
+                if (m < M)
+                    store_from_f32<DT>(y, (int64_t)m * N + row,
+                                       acc[r][q] + bv + lora_term<DT>(lora, m, row));
             }
         }
     }
@@ -2034,7 +2045,8 @@ __global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLa
     const int64_t row = (int64_t)row0 + i16;
     if (g < M && row < N) {
         const float bv = job.bias ? bias_bits_to_f32<DT>(bias_bits) : 0.f;
-        store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out + bv);
+        store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row,
+                           out + bv + job_lora<DT>(job, g, row));
     }
 }
 
@@ -2177,22 +2189,22 @@ bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scale
 template <int DT, int MM, int GS>
 static hipError_t launch_gemv2_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                  const void* bias, void* y, int M, int64_t N, int64_t K,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const LoraEp& lora) {
     const int64_t wgs = (N + 15) / 16;  // one 16-row tile per workgroup
     hipLaunchKernelGGL((gemv2_kernel<DT, MM, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
-                       stream, x, packed, scales, bias, y, M, N, K);
+                       stream, x, packed, scales, bias, y, M, N, K, lora);
     return hipGetLastError();
 }
 
 template <int DT, int MM>
 static hipError_t launch_gemv2_gs(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
-                                  int64_t gs, hipStream_t stream) {
+                                  int64_t gs, hipStream_t stream, const LoraEp& lora) {
     switch (gs) {
-        case 8: return launch_gemv2_t<DT, MM, 8>(x, packed, scales, bias, y, M, N, K, stream);
-        case 16: return launch_gemv2_t<DT, MM, 16>(x, packed, scales, bias, y, M, N, K, stream);
-        case 32: return launch_gemv2_t<DT, MM, 32>(x, packed, scales, bias, y, M, N, K, stream);
-        default: return launch_gemv2_t<DT, MM, 64>(x, packed, scales, bias, y, M, N, K, stream);
+        case 8: return launch_gemv2_t<DT, MM, 8>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        case 16: return launch_gemv2_t<DT, MM, 16>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        case 32: return launch_gemv2_t<DT, MM, 32>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        default: return launch_gemv2_t<DT, MM, 64>(x, packed, scales, bias, y, M, N, K, stream, lora);
     }
 }
 
@@ -2218,40 +2230,40 @@ bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scal
 template <int DT, int GS, int FMT>
 static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const LoraEp& lora) {
     const int64_t wgs = (N + 16 * kB2mTiles - 1) / (16 * kB2mTiles);
     hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT>), dim3((unsigned)wgs), dim3(64 * kB2Waves),
-                       0, stream, x, packed, scales, bias, y, M, N, K);
+                       0, stream, x, packed, scales, bias, y, M, N, K, lora);
     return hipGetLastError();
 }
 
 template <int DT, int FMT>
 static hipError_t launch_gemv2m_gs(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int M, int64_t N, int64_t K,
-                                   int64_t gs, hipStream_t stream) {
+                                   int64_t gs, hipStream_t stream, const LoraEp& lora) {
     switch (gs) {
-        case 8: return launch_gemv2m_t<DT, 8, FMT>(x, packed, scales, bias, y, M, N, K, stream);
-        case 16: return launch_gemv2m_t<DT, 16, FMT>(x, packed, scales, bias, y, M, N, K, stream);
-        case 32: return launch_gemv2m_t<DT, 32, FMT>(x, packed, scales, bias, y, M, N, K, stream);
-        default: return launch_gemv2m_t<DT, 64, FMT>(x, packed, scales, bias, y, M, N, K, stream);
+        case 8: return launch_gemv2m_t<DT, 8, FMT>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        case 16: return launch_gemv2m_t<DT, 16, FMT>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        case 32: return launch_gemv2m_t<DT, 32, FMT>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        default: return launch_gemv2m_t<DT, 64, FMT>(x, packed, scales, bias, y, M, N, K, stream, lora);
     }
 }
 
 hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                         int dt, hipStream_t stream, int fmt) {
+                         int dt, hipStream_t stream, int fmt, const LoraEp& lora) {
     const int m = (int)M;
     if (fmt == kFmtTernary)  // group size 32 only
         return dt == kBF16
-                   ? launch_gemv2m_t<kBF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream)
-                   : launch_gemv2m_t<kF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream);
+                   ? launch_gemv2m_t<kBF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora)
+                   : launch_gemv2m_t<kF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora);
     if (fmt == kFmtRoot)
         return dt == kBF16
-                   ? launch_gemv2m_gs<kBF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream)
-                   : launch_gemv2m_gs<kF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream);
+                   ? launch_gemv2m_gs<kBF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
+                   : launch_gemv2m_gs<kF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
     return dt == kBF16
-               ? launch_gemv2m_gs<kBF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream)
-               : launch_gemv2m_gs<kF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream);
+               ? launch_gemv2m_gs<kBF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
+               : launch_gemv2m_gs<kF16, kFmt2Bit>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
 }
 
 
@@ -2339,13 +2351,13 @@ hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t wgs, int64_t Kmax, int 
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        int dt, hipStream_t stream) {
+                        int dt, hipStream_t stream, const LoraEp& lora) {
     const int m = (int)M;
     if (dt == kBF16)
-        return M == 1 ? launch_gemv2_gs<kBF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream)
-                      : launch_gemv2_gs<kBF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream);
-    return M == 1 ? launch_gemv2_gs<kF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream)
-                  : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream);
+        return M == 1 ? launch_gemv2_gs<kBF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
+                      : launch_gemv2_gs<kBF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
+    return M == 1 ? launch_gemv2_gs<kF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
+                  : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
 }
 
 }  // namespace ojx

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "e8t_device.h"
+
 namespace ojx {
 
 hipError_t launch_encode(const void* w, int wdt, int64_t numel, int64_t gs, uint8_t* packed,
@@ -36,7 +38,7 @@ bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scale
                      const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        int dt, hipStream_t stream);
+                        int dt, hipStream_t stream, const LoraEp& lora = LoraEp{});
 
 // Decode GEMV with the weights in the B operand for the ternary (fmt 0, gs 32), 2-bit (fmt 1)
 // and 1-bit Root-E8 (fmt 2) formats: M <= 16, bf16/fp16, K % 256 == 0, gs in {8, 16, 32, 64},
@@ -46,13 +48,14 @@ bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scal
                       int fmt);
 hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                         int dt, hipStream_t stream, int fmt);
+                         int dt, hipStream_t stream, int fmt, const LoraEp& lora = LoraEp{});
 
 // General tiled kernels: any M, N, K >= 1 (flat layout), any dtype; fmt selects the code
 // format (0 ternary, 1 2-bit, 2 1-bit Root E8).
 hipError_t launch_gemm_generic_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,
                                    const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                                   int64_t gs, int dt, hipStream_t stream, int fmt = 0);
+                                   int64_t gs, int dt, hipStream_t stream, int fmt = 0,
+                                   const LoraEp& lora = LoraEp{});
 hipError_t launch_gemm_generic_bwd(const void* gy, const uint8_t* packed, const uint16_t* scales,
                                    void* gx, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
                                    hipStream_t stream, int fmt = 0);
@@ -75,6 +78,10 @@ struct GemvJob {
     int64_t y_col;            // first output column of this job in y
     int64_t y_ld;             // row stride of y in elements
     int64_t wg_begin;         // first workgroup of this job in the launch grid
+    const float* lora_u;      // LoRA: scaling * (x @ A), fp32 [M, lora_r] (stride lora_ldu)
+    const void* lora_b;       // LoRA up-projection [lora_r, N] in the activation dtype
+    int64_t lora_r;           // adapter rank (0: none)
+    int64_t lora_ldu;         // row stride of lora_u
 };
 
 constexpr int kGemvInlineJobs = 4;
@@ -136,7 +143,13 @@ __host__ __device__ inline int64_t split_stride(int64_t M, int64_t N) {
 hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t* scales,
                             const void* bias, void* y, float* part, GemmChoice c, int64_t M,
                             int64_t N, int64_t K, int dt, hipStream_t stream, int64_t gs = 32,
-                            int fmt = 0, bool bwd = false);
+                            int fmt = 0, bool bwd = false, const LoraEp& lora = LoraEp{});
+
+// LoRA down-projection u[m, j] = scaling * sum_k x[m, k] A[k, j] (fp32 out, row stride ldu)
+// for ranks 1 .. kLoraMaxRank; x and A in dtype dt.
+constexpr int64_t kLoraMaxRank = 64;
+hipError_t launch_lora_down(const void* x, const void* a, int64_t M, int64_t K, int64_t r,
+                            float scaling, int dt, float* u, int64_t ldu, hipStream_t stream);
 
 // Records `msg` as the calling thread's last error (ojx_e8t_last_error) and returns `code`.
 int api_fail(int code, const char* msg);

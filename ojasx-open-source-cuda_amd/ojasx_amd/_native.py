@@ -27,6 +27,10 @@ EXPORTS = (
     "ojx_gemm_workspace_bytes",
     "ojx_e8t_gemm_fwd",
     "ojx_e8t_gemm_fwd_noalloc",
+    "ojx_lora_down",
+    "ojx_e8t_gemm_fwd_lora",
+    "ojx_e8_gemm_fwd_lora",
+    "ojx_e8r_gemm_fwd_lora",
     "ojx_e8t_gemm_bwd_dx",
     "ojx_e8t_gemv_grouped_plan",
     "ojx_e8t_gemv_grouped",
@@ -57,6 +61,10 @@ class GemvJob(ctypes.Structure):
         ("y_col", ctypes.c_int64),
         ("y_ld", ctypes.c_int64),
         ("wg_begin", ctypes.c_int64),
+        ("lora_u", ctypes.c_void_p),
+        ("lora_b", ctypes.c_void_p),
+        ("lora_r", ctypes.c_int64),
+        ("lora_ldu", ctypes.c_int64),
     ]
 
 _lib = None
@@ -66,6 +74,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
+_F32 = ctypes.c_float
 
 
 def lib() -> ctypes.CDLL:
@@ -96,6 +105,13 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8t_gemm_fwd_noalloc.restype = _INT
             L.ojx_e8t_gemm_fwd_noalloc.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                                    _INT, _P]
+            L.ojx_lora_down.restype = _INT
+            L.ojx_lora_down.argtypes = [_P, _P, _I64, _I64, _I64, _F32, _INT, _P, _P]
+            for name in ("ojx_e8t_gemm_fwd_lora", "ojx_e8_gemm_fwd_lora", "ojx_e8r_gemm_fwd_lora"):
+                fn = getattr(L, name)
+                fn.restype = _INT
+                fn.argtypes = [_P, _P, _P, _P, _P, _P, _I64, _F32, _P, _P, _I64, _I64, _I64,
+                               _I64, _INT, _P, _SZ, _P]
             L.ojx_e8t_gemm_bwd_dx.restype = _INT
             L.ojx_e8t_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
                                              _SZ, _P]

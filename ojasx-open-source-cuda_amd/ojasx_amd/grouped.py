@@ -12,7 +12,9 @@ Typical uses:
 * fused projections -- ``GroupedGemv.fused(layers, M, dtype)``: the outputs of
   the layers are concatenated along the last dim of one ``[M, sum(N)]`` tensor
   and every job reads the launch's ``x`` (at most 4 jobs travel in the kernel
-  arguments, no device table);
+  arguments, no device table); layers with a LoRA adapter get it fused: each call
+  launches ``ojx_lora_down`` (u = scaling * x @ A) per adapter, and the grouped
+  kernel adds u @ B in its epilogue (E8LatticeLinear.forward, lattice.py:839-842);
 * a fixed table -- explicit ``x`` / ``y`` per job, uploaded once to the device.
 """
 
@@ -24,12 +26,13 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import _native as N
+from . import ops
 
 
 def _job(packed: torch.Tensor, scales: torch.Tensor, bias: Optional[torch.Tensor], n: int,
          k: int, x: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
          y_col: int = 0, y_ld: int = 0) -> N.GemvJob:
-    j = N.GemvJob()
+    j = N.GemvJob()  # zero-initialised: no LoRA adapter
     j.x = N.ptr(x)
     j.packed = packed.data_ptr()
     j.scales = scales.data_ptr()
@@ -57,6 +60,7 @@ class GroupedGemv:
                 "gemv_grouped_plan")
         self.grid = grid.value
         self._keep = list(keep)  # tensors the job pointers refer to
+        self._lora = []          # (layer, u buffer, K) of the jobs with a fused adapter
         self._dev = None
         if self.n > 4:
             raw = bytes(ctypes.string_at(ctypes.addressof(self._arr), ctypes.sizeof(self._arr)))
@@ -66,21 +70,43 @@ class GroupedGemv:
     def fused(cls, layers: Sequence[torch.nn.Module], M: int, dtype: torch.dtype
               ) -> "GroupedGemv":
         """Jobs for E8LatticeLinear-like layers (packed_weight, block_scales, bias,
-        out_features, in_features) whose outputs are concatenated along dim -1."""
+        out_features, in_features; rank, lora_A, lora_B, scaling for adapters) whose outputs
+        are concatenated along dim -1."""
         n_total = sum(int(l.out_features) for l in layers)
-        jobs, col, keep = [], 0, []
+        jobs, col, keep, lora = [], 0, [], []
+        dev = layers[0].packed_weight.device
         for l in layers:
             if int(l.group_size) != 32:
                 raise RuntimeError("grouped GEMV needs group_size 32")
+            if float(getattr(l, "bitrate", 1.5)) != 1.5:
+                raise RuntimeError("grouped GEMV runs ternary (bitrate 1.5) layers only")
             bias = l.bias.detach().to(dtype).contiguous() if l.bias is not None else None
             if bias is not None:
                 keep.append(bias)
-            jobs.append(_job(l.packed_weight, l.block_scales, bias, int(l.out_features),
-                             int(l.in_features), y_col=col, y_ld=n_total))
-            keep += [l.packed_weight, l.block_scales]
+            # fp16 scale bits; a module cast (.to(bfloat16)) leaves the buffer in another dtype
+            scales = l.block_scales.detach().to(torch.float16).contiguous()
+            j = _job(l.packed_weight, scales, bias, int(l.out_features),
+                     int(l.in_features), y_col=col, y_ld=n_total)
+            if getattr(l, "rank", 0) > 0 and getattr(l, "lora_A", None) is not None:
+                if getattr(l, "use_hadamard", False):
+                    raise RuntimeError("grouped GEMV: adapters of Hadamard-rotated layers are "
+                                       "not fused")
+                if l.lora_B.dtype != dtype or not l.lora_B.is_contiguous():
+                    raise RuntimeError("grouped GEMV: lora_B must be contiguous in the "
+                                       "activation dtype")
+                r = int(l.lora_A.shape[-1])
+                if not 1 <= r <= ops.LORA_MAX_RANK:
+                    raise RuntimeError(f"grouped GEMV: LoRA rank {r} out of range")
+                u = torch.empty((int(M), r), dtype=torch.float32, device=dev)
+                j.lora_u, j.lora_b, j.lora_r, j.lora_ldu = u.data_ptr(), l.lora_B.data_ptr(), r, r
+                keep += [u, l.lora_B]
+                lora.append((l, u, int(l.in_features)))
+            jobs.append(j)
+            keep += [l.packed_weight, scales]
             col += int(l.out_features)
-        g = cls(jobs, M, dtype, layers[0].packed_weight.device, keep)
+        g = cls(jobs, M, dtype, dev, keep)
         g.n_total = n_total
+        g._lora = lora
         return g
 
     def __call__(self, x: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
@@ -93,6 +119,12 @@ class GroupedGemv:
         if y is None and hasattr(self, "n_total") and x is not None:
             y = torch.empty((*x.shape[:-1], self.n_total), dtype=self.dtype, device=self.device)
         s = stream.cuda_stream if stream is not None else N.stream_handle(self.device)
+        for l, u, k in self._lora:  # u = scaling * (x @ A) for each fused adapter
+            a = l.lora_A.detach()
+            a = a if a.dtype == self.dtype and a.is_contiguous() else a.to(self.dtype).contiguous()
+            N.check(N.lib().ojx_lora_down(N.ptr(x), N.ptr(a), self.M, k, int(a.shape[-1]),
+                                          float(l.scaling), N.DTYPE_CODE[self.dtype], N.ptr(u),
+                                          s), "lora_down")
         N.check(N.lib().ojx_e8t_gemv_grouped(ctypes.addressof(self._arr),
                                              N.ptr(self._dev), self.n, N.ptr(x), N.ptr(y),
                                              self.M, N.DTYPE_CODE[self.dtype], s),

@@ -249,7 +249,8 @@ class TernaryE8LatticePacker:
         total = shape[0] * shape[1]
         padded = (packed_codes.numel() // 3) * 16
         group_size = padded // max(1, scales.numel())  # inferred as in lattice.py:407-409
-        out = ops.decode(_on_gpu(packed_codes), _on_gpu(scales), total, group_size, dtype)
+        out = ops.decode(_on_gpu(packed_codes), _on_gpu(scales).to(torch.float16), total,
+                         group_size, dtype)
         if packed_codes.device.type != "cuda":
             out = out.to(packed_codes.device)
         return out.view(shape)
@@ -276,7 +277,8 @@ class E8LatticePacker:
         total = shape[0] * shape[1]
         padded = packed_codes.numel() * 4
         group_size = padded // max(1, scales.numel())  # inferred as in lattice.py:264-266
-        out = ops.decode2(_on_gpu(packed_codes), _on_gpu(scales), total, group_size, dtype)
+        out = ops.decode2(_on_gpu(packed_codes), _on_gpu(scales).to(torch.float16), total,
+                          group_size, dtype)
         if packed_codes.device.type != "cuda":
             out = out.to(packed_codes.device)
         return out.view(shape)
@@ -340,7 +342,8 @@ class RootE8LatticePacker:
         total = shape[0] * shape[1]
         padded = packed_codes.numel() * 8
         group_size = padded // max(1, scales.numel())  # inferred as in lattice.py:524-525
-        out = ops.decode1(_on_gpu(packed_codes), _on_gpu(scales), total, group_size, dtype)
+        out = ops.decode1(_on_gpu(packed_codes), _on_gpu(scales).to(torch.float16), total,
+                          group_size, dtype)
         if packed_codes.device.type != "cuda":
             out = out.to(packed_codes.device)
         return out.view(shape)
@@ -479,10 +482,21 @@ class E8LatticeLinear(nn.Module):
         return fwht_block32(w) if self.use_hadamard else w
 
     def forward_fused(self, x: torch.Tensor) -> torch.Tensor:
+        has_lora = self.rank > 0 and self.lora_A is not None and self.lora_B is not None
+        if (has_lora and not self.use_hadamard and self.lora_A.shape[-1] <= ops.LORA_MAX_RANK
+                and x.is_cuda):
+            # the adapter term scaling * ((x @ A) @ B) (lattice.py:839-842) added inside the
+            # E8 kernel's epilogue; with a Hadamard rotation the E8 op sees the rotated x
+            # while the adapter takes the original, so that case stays unfused below
+            _require_supported(self.bitrate)
+            fmt = {1.5: ops.FMT_TERNARY, 1.0: ops.FMT_ROOT}.get(float(self.bitrate), ops.FMT_E8)
+            return ops.linear_lora(x, self.packed_weight, self.block_scales, self.bias,
+                                   self.lora_A, self.lora_B, float(self.scaling), fmt,
+                                   self.out_features, self.in_features, self.group_size)
         out = _FusedE8GEMMFunction.apply(x, self.packed_weight, self.block_scales, self.bias,
                                          self.out_features, self.in_features, self.group_size,
                                          self.bitrate, self.use_hadamard)
-        if self.rank > 0 and self.lora_A is not None and self.lora_B is not None:
+        if has_lora:
             lora_a = self.lora_A.to(x.dtype) if self.lora_A.dtype != x.dtype else self.lora_A
             lora_b = self.lora_B.to(x.dtype) if self.lora_B.dtype != x.dtype else self.lora_B
             out = out + self.scaling * ((x @ lora_a) @ lora_b)

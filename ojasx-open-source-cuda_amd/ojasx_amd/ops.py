@@ -112,8 +112,8 @@ def _check_layer_buffers(packed: torch.Tensor, scales: torch.Tensor, out_feature
                          in_features: int, group_size: int) -> None:
     if packed.dtype != torch.uint8:
         raise RuntimeError("packed_weight must be uint8")
-    if scales.dtype != torch.float16:
-        raise RuntimeError("block_scales must be float16")
+    if not scales.is_floating_point():
+        raise RuntimeError("block_scales must be a floating-point tensor (float16 bits)")
     padded = _padded(out_features * in_features, group_size)
     if packed.numel() < padded * 3 // 16:
         raise RuntimeError(
@@ -160,7 +160,9 @@ def _linear_fwd(fmt: int, x: torch.Tensor, packed_weight: torch.Tensor,
             raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
         b = bias.to(x.dtype).contiguous()  # the reference casts bias to x's dtype
     pw = packed_weight.contiguous()
-    bs = block_scales.contiguous()
+    # the buffer holds fp16 scales; a module cast (e.g. .to(bfloat16)) leaves them in another
+    # float dtype, which the reference tolerates (scales.to(dtype), lattice.py:414-418)
+    bs = block_scales.to(torch.float16).contiguous()
     with torch.cuda.device(dev):
         ws = workspace(fmt, False, M, out_features, in_features, group_size, x.dtype, dev)
         N.check(getattr(N.lib(), _FWD[fmt])(N.ptr(x2), N.ptr(pw), N.ptr(bs), N.ptr(b), N.ptr(y),
@@ -183,7 +185,9 @@ def _linear_bwd(fmt: int, grad_y: torch.Tensor, packed_weight: torch.Tensor,
     M = gy.shape[0]
     gx = torch.empty((M, in_features), dtype=grad_y.dtype, device=dev)
     pw = packed_weight.contiguous()
-    bs = block_scales.contiguous()
+    # the buffer holds fp16 scales; a module cast (e.g. .to(bfloat16)) leaves them in another
+    # float dtype, which the reference tolerates (scales.to(dtype), lattice.py:414-418)
+    bs = block_scales.to(torch.float16).contiguous()
     with torch.cuda.device(dev):
         ws = workspace(fmt, True, M, out_features, in_features, group_size, grad_y.dtype, dev)
         N.check(getattr(N.lib(), _BWD[fmt])(N.ptr(gy), N.ptr(pw), N.ptr(bs), N.ptr(gx), M,
@@ -247,6 +251,117 @@ def _linear_backward(ctx, grad_y):
 
 
 e8t_linear.register_autograd(_linear_backward, setup_context=_linear_setup_context)
+
+
+# ----------------------------------------------------------- fused LoRA epilogue
+
+_FWD_LORA = {FMT_TERNARY: "ojx_e8t_gemm_fwd_lora", FMT_E8: "ojx_e8_gemm_fwd_lora",
+             FMT_ROOT: "ojx_e8r_gemm_fwd_lora"}
+LORA_MAX_RANK = 64  # ojx_lora_down's rank range (include/ojasx_e8t.h)
+
+
+def _check_fmt_layer(fmt: int, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+                     out_features: int, in_features: int, group_size: int) -> None:
+    if fmt == FMT_TERNARY:
+        _check_gs(group_size)
+        _check_layer_buffers(packed_weight, block_scales, out_features, in_features, group_size)
+    elif fmt == FMT_E8:
+        _check_gs2(group_size, 4)
+        _check_layer_buffers2(packed_weight, block_scales, out_features, in_features, group_size)
+    elif fmt == FMT_ROOT:
+        _check_gs2(group_size, 8)
+        _check_layer_buffers1(packed_weight, block_scales, out_features, in_features, group_size)
+    else:
+        raise RuntimeError(f"unknown weight format {fmt}")
+
+
+@torch.library.custom_op(f"{_NS}::linear_lora", mutates_args=())
+def linear_lora(x: torch.Tensor, packed_weight: torch.Tensor, block_scales: torch.Tensor,
+                bias: Optional[torch.Tensor], lora_a: torch.Tensor, lora_b: torch.Tensor,
+                scaling: float, fmt: int, out_features: int, in_features: int,
+                group_size: int) -> torch.Tensor:
+    """x . Wdeq^T (+ bias) + scaling * (x @ lora_a) @ lora_b in one fused forward: the E8
+    op and E8LatticeLinear's adapter term (lattice.py:839-842), lora_a [in, r] and lora_b
+    [r, out] in x's dtype, the adapter term added in fp32 in the E8 kernel's epilogue."""
+    dev = N.require_device(x, packed_weight, block_scales, bias, lora_a, lora_b)
+    if x.shape[-1] != in_features:
+        raise RuntimeError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    _check_fmt_layer(fmt, packed_weight, block_scales, out_features, in_features, group_size)
+    r = lora_a.shape[-1]
+    if lora_a.dim() != 2 or lora_a.shape[0] != in_features or tuple(lora_b.shape) != (r, out_features):
+        raise RuntimeError(f"LoRA factors must be [{in_features}, r] and [r, {out_features}] "
+                           f"(got {tuple(lora_a.shape)} and {tuple(lora_b.shape)})")
+    if not 1 <= r <= LORA_MAX_RANK:
+        raise RuntimeError(f"fused LoRA supports ranks 1..{LORA_MAX_RANK} (got {r})")
+    dt = _dtype_code(x.dtype)
+    x2 = x.reshape(-1, in_features).contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, out_features), dtype=x.dtype, device=dev)
+    b = None
+    if bias is not None:
+        if bias.numel() != out_features:
+            raise RuntimeError(f"bias has {bias.numel()} elements, expected {out_features}")
+        b = bias.to(x.dtype).contiguous()
+    la = lora_a.to(x.dtype).contiguous()
+    lb = lora_b.to(x.dtype).contiguous()
+    pw = packed_weight.contiguous()
+    # the buffer holds fp16 scales; a module cast (e.g. .to(bfloat16)) leaves them in another
+    # float dtype, which the reference tolerates (scales.to(dtype), lattice.py:414-418)
+    bs = block_scales.to(torch.float16).contiguous()
+    u = torch.empty((M, r), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws = workspace(fmt, False, M, out_features, in_features, group_size, x.dtype, dev)
+        N.check(getattr(N.lib(), _FWD_LORA[fmt])(
+            N.ptr(x2), N.ptr(pw), N.ptr(bs), N.ptr(b), N.ptr(la), N.ptr(lb), r, float(scaling),
+            N.ptr(u), N.ptr(y), M, out_features, in_features, group_size, dt, N.ptr(ws),
+            0 if ws is None else ws.numel(), N.stream_handle(dev)),
+            _FWD_LORA[fmt][4:])
+    return y.reshape(*x.shape[:-1], out_features)
+
+
+@linear_lora.register_fake
+def _(x, packed_weight, block_scales, bias, lora_a, lora_b, scaling, fmt, out_features,
+      in_features, group_size):
+    return x.new_empty((*x.shape[:-1], out_features))
+
+
+def _linear_lora_setup_context(ctx, inputs, output):
+    (x, packed_weight, block_scales, bias, lora_a, lora_b, scaling, fmt, out_features,
+     in_features, group_size) = inputs
+    ctx.save_for_backward(x, packed_weight, block_scales, lora_a, lora_b)
+    ctx.dims = (out_features, in_features, group_size)
+    ctx.fmt = fmt
+    ctx.scaling = float(scaling)
+    ctx.has_bias = bias is not None
+    ctx.bias_dtype = None if bias is None else bias.dtype
+
+
+def _linear_lora_backward(ctx, grad_y):
+    """grad_x through the fused backward dX plus the adapter's term; the adapter's own
+    gradients (and the bias's) in torch, as the reference computes them."""
+    x, packed_weight, block_scales, lora_a, lora_b = ctx.saved_tensors
+    out_features, in_features, group_size = ctx.dims
+    sc = ctx.scaling
+    gy = grad_y.reshape(-1, out_features).contiguous()
+    x2 = x.reshape(-1, in_features)
+    la = lora_a.to(grad_y.dtype)
+    lb = lora_b.to(grad_y.dtype)
+    gyb = gy @ lb.t().contiguous()                       # [M, r]
+    grad_x = grad_a = grad_b = grad_bias = None
+    if ctx.needs_input_grad[0]:
+        grad_x = _linear_bwd(ctx.fmt, gy, packed_weight, block_scales, out_features,
+                             in_features, group_size)
+        grad_x = (grad_x + sc * (gyb @ la.t().contiguous())).reshape(x.shape)
+    if ctx.needs_input_grad[4]:
+        grad_a = (sc * (x2.t().contiguous() @ gyb)).to(lora_a.dtype)
+    if ctx.needs_input_grad[5]:
+        grad_b = (sc * ((x2 @ la).t().contiguous() @ gy)).to(lora_b.dtype)
+    if ctx.has_bias and ctx.needs_input_grad[3]:
+        grad_bias = gy.sum(dim=0).to(ctx.bias_dtype)
+    return grad_x, None, None, grad_bias, grad_a, grad_b, None, None, None, None, None
+
+
+linear_lora.register_autograd(_linear_lora_backward, setup_context=_linear_lora_setup_context)
 
 
 # ------------------------------------------------------- reference native op schemas
@@ -376,8 +491,8 @@ def _check_layer_buffers2(packed: torch.Tensor, scales: torch.Tensor, out_featur
                           in_features: int, group_size: int) -> None:
     if packed.dtype != torch.uint8:
         raise RuntimeError("packed_weight must be uint8")
-    if scales.dtype != torch.float16:
-        raise RuntimeError("block_scales must be float16")
+    if not scales.is_floating_point():
+        raise RuntimeError("block_scales must be a floating-point tensor (float16 bits)")
     padded = _padded(out_features * in_features, group_size)
     if packed.numel() < padded // 4:
         raise RuntimeError(
@@ -557,8 +672,8 @@ def _check_layer_buffers1(codes: torch.Tensor, scales: torch.Tensor, out_feature
                           in_features: int, group_size: int) -> None:
     if codes.dtype != torch.uint8:
         raise RuntimeError("packed_weight must be uint8")
-    if scales.dtype != torch.float16:
-        raise RuntimeError("block_scales must be float16")
+    if not scales.is_floating_point():
+        raise RuntimeError("block_scales must be a floating-point tensor (float16 bits)")
     padded = _padded(out_features * in_features, group_size)
     if codes.numel() < padded // 8:
         raise RuntimeError(
