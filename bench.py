@@ -91,7 +91,7 @@ def parse_args():
     ap.add_argument("--prefill-m", type=str, default=",".join(map(str, PREFILL_M)))
     ap.add_argument("--prefill-time", type=float, default=0.15,
                     help="target seconds of timed work per prefill case")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="bounded CPU-baseline sample length")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -829,8 +829,12 @@ def bench_e2e(torch, dev, layers: int):
 # --------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(seconds: float):
-    """the reference's Linux CPU path (unpack into the workspace, then
-    F.linear), restated in oracle/portable.py, on one 4096x4096 layer at M=1 fp32."""
+    """The reference's Linux CPU path (unpack into the workspace, then F.linear), restated in
+    oracle/portable.py, timed on the host cores:
+      * configs[0]: one 4096x4096 layer at M = 1 in fp32 for about `seconds` (the `value`);
+      * configs[1]/[2] CPU side: the same path in fp32 on each of the four Llama-3-8B shapes
+        at M in {1, 4, 16} (median of 3 calls after one warm-up);
+      * configs[3] CPU side: the C oracle encoder (OpenMP) on one layer of each shape."""
     import platform
 
     import numpy as np
@@ -859,6 +863,32 @@ def cpu_baseline(seconds: float):
             break
     per = el / n
     wb = weight_bytes(4096, 4096)
+
+    shapes, encoder = {}, {}
+    for name, N, K in (("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
+                       ("down", 4096, 14336)):
+        gw = torch.Generator().manual_seed(8110 + N + K)
+        wl = (torch.randn(N, K, generator=gw) * 0.02).numpy()
+        t1 = time.perf_counter()
+        pk, sc, _ = O.encode(wl, GS, nthreads=cores)
+        enc_s = time.perf_counter() - t1
+        encoder[name] = dict(weights_per_s=round(N * K / enc_s / 1e9, 4), unit="G weights/s",
+                             seconds=round(enc_s, 3))
+        del wl
+        pk_t, sc_t = torch.from_numpy(pk), torch.from_numpy(sc.view(np.float16).copy())
+        for M in (1, 4, 16):
+            xs = torch.randn(M, K, generator=gw)
+            portable.linear(xs, pk_t, sc_t, None, N, K)
+            ts = []
+            for _ in range(3):
+                t1 = time.perf_counter()
+                portable.linear(xs, pk_t, sc_t, None, N, K)
+                ts.append(time.perf_counter() - t1)
+            med = sorted(ts)[1]
+            shapes[f"{name}_M{M}"] = dict(ms=round(med * 1e3, 3),
+                                          weight_GBs=round(weight_bytes(N, K) / med / 1e9, 3))
+    portable._WS.clear()  # the fp32 workspace of the largest shape (235 MB)
+
     cpu_model = platform.processor() or ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -872,7 +902,8 @@ def cpu_baseline(seconds: float):
                 sample=(f"configs[0]: 4096x4096 ternary-E8 layer (seed 8101), x[1,4096] fp32 "
                         f"(seed 8102); unpack(use_workspace)+F.linear restated in "
                         f"oracle/portable.py; {n} calls in {el:.1f} s = {per * 1e3:.2f} ms/call; "
-                        f"{cpu_model}"))
+                        f"{cpu_model}"),
+                cpu_model=cpu_model, per_shape_fp32=shapes, oracle_encoder=encoder)
 
 
 # --------------------------------------------------------------------------- main

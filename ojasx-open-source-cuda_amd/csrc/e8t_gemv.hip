@@ -1503,11 +1503,9 @@ __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
 // Step h's A fragment: with the lane's offset xo = 8192 w + 512 i16 + 16 ((8g & 16) |
 // ((8g & 8) ^ (i16 & 8)) | (i16 & 7)) (bits 4..6 equal to i16 & 7), piece 8g + h of row
 // i16 sits at xs + (xo ^ 16 h).
-#ifndef OJX_B2M_TILES
-#define OJX_B2M_TILES 1
-#endif
-constexpr int kB2mTiles = OJX_B2M_TILES;  // 16-row tiles per workgroup (each wave takes all)
-static_assert(kB2mTiles == 1 || kB2mTiles == 2, "one or two tiles");
+// One 16-row tile per workgroup: two (half the staged activation bytes per weight, half
+// the workgroups) measured slower for every format, these launches need the workgroups.
+constexpr int kB2mTiles = 1;
 
 template <int DT, int GS, int FMT, int R>
 struct B2mRound {
