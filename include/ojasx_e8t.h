@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-enum { OJX_F32 = 0, OJX_F16 = 1, OJX_BF16 = 2 };
+enum { OJX_F32 = 0, OJX_F16 = 1, OJX_BF16 = 2, OJX_F64 = 3 /* ojx_fwht32 only */ };
 
 /* Weight formats (ojx_gemm_workspace_bytes): ternary E8 (1.5 bit), 2-bit E8, 1-bit Root E8. */
 enum { OJX_FMT_TERNARY = 0, OJX_FMT_E8 = 1, OJX_FMT_ROOT = 2 };
@@ -212,6 +212,18 @@ int ojx_e8r_gemm_fwd(const void* x, const uint8_t* codes, const uint16_t* scales
 int ojx_e8r_gemm_bwd_dx(const void* grad_y, const uint8_t* codes, const uint16_t* scales,
                         void* grad_x, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- Hadamard rotation
+ *
+ * fwht_block32 (ojasx2/math/lattice.py:91-102): the normalised 32-point Walsh-Hadamard
+ * transform of each of the numel / 32 contiguous 32-element blocks of x into y (y == x is
+ * allowed), with the reference's rounded operations (butterflies at distance 1, 2, 4, 8, 16,
+ * each rounded to dtype; one multiply by 0.1767766952966369 in the compute type), so the
+ * result is bit-identical to the torch evaluation.  The fused linear applies it to x before
+ * the E8 op and to grad_x after the backward when use_hadamard is set (lattice.py:564-565,
+ * 669-679, 713-714).  dtype: OJX_F32, OJX_F16, OJX_BF16 or OJX_F64; numel a multiple of 32;
+ * x and y 16-byte aligned. */
+int ojx_fwht32(const void* x, int dtype, int64_t numel, void* y, void* stream);
 
 /* ---------------------------------------------------------------- QAT helpers
  *

@@ -24,6 +24,7 @@ SOURCES = [
     "e8t_gemm_generic.hip",
     "e8t_gemv.hip",
     "e8t_gemm_mfma.hip",
+    "e8t_hadamard.hip",
     "e8t_qat.hip",
     "e8t_noalloc.hip",
     "e8t_lora.hip",

@@ -591,6 +591,23 @@ __attribute__((visibility("default"))) int ojx_e8r_gemm_bwd_dx(
                     workspace_bytes, stream);
 }
 
+// ---------------------------------------------------------------- Hadamard rotation
+
+__attribute__((visibility("default"))) int ojx_fwht32(const void* x, int dtype, int64_t numel,
+                                                      void* y, void* stream) {
+    if (!valid_dtype(dtype) && dtype != OJX_F64)
+        return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
+    if (numel < 0 || numel % 32 != 0)
+        return fail(OJX_ELAYOUT, "numel %lld is not a multiple of 32", (long long)numel);
+    if (numel == 0) return OJX_OK;
+    if (!x || !y) return fail(OJX_EINVAL, "null pointer");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 15u))
+        return fail(OJX_ELAYOUT, "x and y must be 16-byte aligned");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_fwht32(x, dtype, numel / 32, y, (hipStream_t)stream),
+                "fwht32 launch");
+}
+
 // ---------------------------------------------------------------- QAT helpers
 
 __attribute__((visibility("default"))) int ojx_e8_cs_project(const void* x, int f64,

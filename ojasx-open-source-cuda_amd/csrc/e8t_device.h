@@ -7,7 +7,7 @@
 
 namespace ojx {
 
-enum : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 2, kF64 = 3 /* fwht32 only */ };
 
 // ---------------------------------------------------------------- conversions
 

@@ -28,6 +28,8 @@ hipError_t launch_decode1(const uint8_t* codes, const uint16_t* scales, int64_t 
 
 // Conway-Sloane E8 projection (fp32 or fp64, nvec 8-vectors) and the QAT straight-through
 // quantizer (fp32 weights).
+// fwht_block32 of `blocks` contiguous 32-element blocks (dt: kF32, kF16, kBF16, kF64).
+hipError_t launch_fwht32(const void* x, int dt, int64_t blocks, void* y, hipStream_t stream);
 hipError_t launch_cs_project(const void* x, bool f64, int64_t nvec, void* out,
                              hipStream_t stream);
 hipError_t launch_ste_quantize(const float* w, int64_t numel, float* out, hipStream_t stream);

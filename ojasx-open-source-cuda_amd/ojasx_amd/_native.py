@@ -42,6 +42,7 @@ EXPORTS = (
     "ojx_e8r_decode",
     "ojx_e8r_gemm_fwd",
     "ojx_e8r_gemm_bwd_dx",
+    "ojx_fwht32",
     "ojx_e8_cs_project",
     "ojx_e8_ste_quantize",
 )
@@ -139,6 +140,8 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8r_gemm_bwd_dx.restype = _INT
             L.ojx_e8r_gemm_bwd_dx.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P,
                                              _SZ, _P]
+            L.ojx_fwht32.restype = _INT
+            L.ojx_fwht32.argtypes = [_P, _INT, _I64, _P, _P]
             L.ojx_e8_cs_project.restype = _INT
             L.ojx_e8_cs_project.argtypes = [_P, _INT, _I64, _P, _P]
             L.ojx_e8_ste_quantize.restype = _INT

@@ -69,11 +69,15 @@ def fwht_block32(x: torch.Tensor) -> torch.Tensor:
     Radix-2 butterflies at distances 1, 2, 4, 8, 16 (sum to the lower index,
     difference to the upper), then one multiply by 1/sqrt(32): the same sequence
     of rounded operations as the reference, so packed codes of a Hadamard layer
-    match bit for bit.  Returns ``x`` unchanged if the last dim is not a
-    positive multiple of 32."""
+    match bit for bit.  GPU tensors (fp32/fp16/bf16/fp64) run one HIP kernel
+    (``ops.fwht32``, differentiable); tensors on the CPU are transformed there
+    with torch stages, as the reference transforms them.  Returns ``x``
+    unchanged if the last dim is not a positive multiple of 32."""
     shape = x.shape
     if shape[-1] == 0 or shape[-1] % 32 != 0:
         return x
+    if x.is_cuda and x.dtype in ops._FWHT_CODE:
+        return ops.fwht32(x)  # one HIP kernel, the same rounded operations
     h = x.reshape(-1, 32)
     for dist in (1, 2, 4, 8, 16):
         v = h.reshape(-1, 32 // (2 * dist), 2, dist)

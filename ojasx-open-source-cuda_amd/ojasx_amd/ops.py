@@ -733,6 +733,46 @@ def _linear1_backward(ctx, grad_y):
 e8r_linear.register_autograd(_linear1_backward, setup_context=_linear_setup_context)
 
 
+# --------------------------------------------------------------------------- Hadamard rotation
+
+_FWHT_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
+
+
+@torch.library.custom_op(f"{_NS}::fwht32", mutates_args=())
+def fwht32(x: torch.Tensor) -> torch.Tensor:
+    """fwht_block32 (lattice.py:91-102) of every 32-element block along the last dim, one HIP
+    kernel, bit-identical to the reference's torch stages (fp32, fp16, bf16, fp64)."""
+    dev = N.require_device(x)
+    if x.dtype not in _FWHT_CODE:
+        raise RuntimeError(f"fwht32 supports float32/float16/bfloat16/float64 (got {x.dtype})")
+    if x.shape[-1] == 0 or x.shape[-1] % 32 != 0:
+        raise RuntimeError(f"last dimension must be a positive multiple of 32 (got {x.shape[-1]})")
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    with torch.cuda.device(dev):
+        N.check(N.lib().ojx_fwht32(N.ptr(xc), _FWHT_CODE[x.dtype], xc.numel(), N.ptr(out),
+                                   N.stream_handle(dev)),
+                "fwht32")
+    return out
+
+
+@fwht32.register_fake
+def _(x):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _fwht32_setup(ctx, inputs, output):
+    pass
+
+
+def _fwht32_backward(ctx, grad):
+    # the normalised Hadamard matrix is symmetric: the vector-Jacobian product is the transform
+    return fwht32(grad.contiguous())
+
+
+fwht32.register_autograd(_fwht32_backward, setup_context=_fwht32_setup)
+
+
 # --------------------------------------------------------------------------- QAT helpers
 
 @torch.library.custom_op(f"{_NS}::cs_project", mutates_args=())
