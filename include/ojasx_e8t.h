@@ -259,10 +259,19 @@ typedef struct ojx_e8t_gemv_job {
     int64_t y_col;          /* y[m, y_col + n] receives output n of row m          */
     int64_t y_ld;           /* row stride of y in elements (0 means N)             */
     int64_t wg_begin;       /* written by ojx_e8t_gemv_grouped_plan                */
-    const float* lora_u;    /* LoRA adapter (lora_r > 0): u = scaling * (x @ A),   */
-    const void* lora_b;     /*   fp32 [M, lora_r] (row stride lora_ldu, 0 = r),    */
-    int64_t lora_r;         /*   B [lora_r, N] in dtype; y += u @ B is added before */
-    int64_t lora_ldu;       /*   the output is rounded (ojx_lora_down computes u)   */
+    /* LoRA adapter (lora_r in 1..64; 0 = none), E8LatticeLinear.forward's
+     * scaling * ((x @ A) @ B) (lattice.py:839-842): ojx_e8t_gemv_grouped first writes
+     * u = lora_scaling * (x @ A) into the caller's fp32 scratch lora_u [M, lora_r] (row
+     * stride lora_ldu, 0 = lora_r; adapters on the same x share one launch), then the
+     * GEMV adds u @ B before the output is rounded.  A [K, lora_r], B [lora_r, N] in
+     * dtype. */
+    float* lora_u;
+    const void* lora_b;
+    int64_t lora_r;
+    int64_t lora_ldu;
+    const void* lora_a;
+    float lora_scaling;
+    int32_t reserved;       /* 0 */
 } ojx_e8t_gemv_job;
 
 /* Validates `jobs` (host array) for batch M and dtype, fills each wg_begin (and y_ld

@@ -347,9 +347,14 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
         return fail(OJX_EDTYPE, "grouped GEMV takes F16 or BF16 activations (got %d)", dtype);
     if (M < 1 || M > 16) return fail(OJX_ELAYOUT, "grouped GEMV needs 1 <= M <= 16 (got %lld)",
                                      (long long)M);
-    int64_t tiles = 0;
+    int64_t tiles = 0, kmax = 0;
+    bool tile_ok = M <= 4;
     for (int i = 0; i < njobs; ++i) {
         const ojx_e8t_gemv_job& j = jobs[i];
+        kmax = j.K > kmax ? j.K : kmax;
+        tile_ok = tile_ok && j.K % 1024 == 0 && ((uintptr_t)j.packed & 15u) == 0 &&
+                  ((uintptr_t)j.scales & 15u) == 0 && (j.N + 16) * (j.K * 3 / 16) < (1ll << 31) &&
+                  M * j.K * 2 < (1ll << 31);
         if (j.N < 1 || j.K < 256 || j.K % 256 != 0)
             return fail(OJX_ELAYOUT, "job %d: needs N >= 1 and K %% 256 == 0 (N=%lld K=%lld)", i,
                         (long long)j.N, (long long)j.K);
@@ -362,8 +367,8 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
         if (j.lora_r < 0 || j.lora_r > ojx::kLoraMaxRank)
             return fail(OJX_ELAYOUT, "job %d: LoRA rank must be in 0..%lld", i,
                         (long long)ojx::kLoraMaxRank);
-        if (j.lora_r > 0 && (!j.lora_u || !j.lora_b || ((uintptr_t)j.lora_u & 3u) ||
-                             ((uintptr_t)j.lora_b & 1u) ||
+        if (j.lora_r > 0 && (!j.lora_u || !j.lora_b || !j.lora_a || ((uintptr_t)j.lora_u & 3u) ||
+                             ((uintptr_t)j.lora_b & 1u) || ((uintptr_t)j.lora_a & 1u) ||
                              (j.lora_ldu != 0 && j.lora_ldu < j.lora_r)))
             return fail(OJX_EINVAL, "job %d: bad LoRA operands", i);
         const int64_t ld = j.y_ld ? j.y_ld : j.N;
@@ -372,7 +377,7 @@ static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, in
                         (long long)j.y_col, (long long)j.N);
         tiles += (j.N + 15) / 16;
     }
-    *plan = ojx::gemv_pick(tiles, M);
+    *plan = ojx::gemv_pick_grouped(tiles, M, kmax, tile_ok);
     int64_t wg = 0;
     for (int i = 0; i < njobs; ++i) {
         if (fill) {
@@ -425,6 +430,25 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
     a.y = y;
     a.njobs = njobs;
     a.M = (int)M;
+    // the adapters' down-projections before the GEMV: consecutive adapter jobs on the same
+    // activations (same x, same K) share a launch
+    for (int i = 0; i < njobs;) {
+        if (jobs[i].lora_r <= 0) { ++i; continue; }
+        const void* xi = jobs[i].x ? jobs[i].x : x;
+        const int64_t Ki = jobs[i].K;
+        ojx::LoraDown items[ojx::kLoraDownItems];
+        int n = 0;
+        for (; i < njobs && n < ojx::kLoraDownItems; ++i) {
+            const ojx_e8t_gemv_job& j = jobs[i];
+            if (j.lora_r <= 0) continue;
+            if ((j.x ? j.x : x) != xi || j.K != Ki) break;
+            items[n++] = ojx::LoraDown{j.lora_a, const_cast<float*>(j.lora_u), j.lora_r,
+                                       j.lora_ldu ? j.lora_ldu : j.lora_r, j.lora_scaling};
+        }
+        const hipError_t e = ojx::launch_lora_down(xi, M, Ki, dtype, items, n,
+                                                   (hipStream_t)stream);
+        if (e != hipSuccess) return fail(OJX_EHIP, "lora_down launch: %s", hipGetErrorString(e));
+    }
     return done(ojx::launch_gemv(a, plan, grid, dtype, (hipStream_t)stream),
                 "e8t grouped gemv launch");
 }

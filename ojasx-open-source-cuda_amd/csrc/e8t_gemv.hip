@@ -2103,7 +2103,8 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
 
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p) {
     const int64_t tiles = (N + 15) / 16;
-    const int64_t per_wg = p.split_ps ? 1
+    const int64_t per_wg = p.tile     ? p.tpw
+                           : p.split_ps ? 1
                            : p.wide   ? (int64_t)p.W * p.R * p.C
                                       : (int64_t)(4 / p.S) * p.R;
     return (tiles + per_wg - 1) / per_wg;
@@ -2161,10 +2162,14 @@ static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
     return hipErrorInvalidValue;
 }
 
+static hipError_t launch_tile_plan(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
+                                  int dt, hipStream_t s);
+
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream) {
     if (wgs <= 0) return hipSuccess;
     if (wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
+    if (p.tile) return launch_tile_plan(a, p, wgs, dt, stream);
     return dt == kBF16 ? launch_dt<kBF16>(a, p, wgs, stream)
                        : launch_dt<kF16>(a, p, wgs, stream);
 }
@@ -2302,49 +2307,62 @@ bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* s
     return (N + 16) * (K * 3 / 16) < (1ll << 31) && M * K * 2 < (1ll << 31);
 }
 
+#ifndef OJX_TILE_GROUPED_BELOW
+#define OJX_TILE_GROUPED_BELOW 4096
+#endif
+GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool tile_ok) {
+    const int U = tile_ok ? gemv_tile_rounds(M, kmax) : 0;
+    if (U == 0 || total_tiles >= OJX_TILE_GROUPED_BELOW) return gemv_pick(total_tiles, M);
+    GemvPlan p{};
+    p.tile = true;
+    p.U = U;
+    p.tpw = U == 1 ? gemv_tile_per_wg(M, total_tiles) : 1;
+    p.R = p.S = p.W = p.C = 1;
+    p.mmax = M == 1 ? 1 : 4;
+    return p;
+}
+
+// `wgs` workgroups of TPW row tiles each (each job's tiles start a new workgroup)
 template <int DT, int MM, int U, int TPW>
-static hipError_t launch_tile_tpw(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW>), dim3((unsigned)((tiles + TPW - 1) / TPW)),
+static hipError_t launch_tile_grid(const GemvLaunch& a, int64_t wgs, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW>), dim3((unsigned)wgs),
                        dim3(64 * kTileWaves * TPW), 0, s, a);
     return hipGetLastError();
 }
 
-template <int DT, int MM, int U>
-static hipError_t launch_tile_t(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
-    return launch_tile_tpw<DT, MM, U, 1>(a, tiles, s);
-}
-
-// two tiles per workgroup: K <= 4096 at M == 1 only (gemv_tile_per_wg)
-template <>
-hipError_t launch_tile_t<kBF16, 1, 1>(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
-    return gemv_tile_per_wg(a.M, tiles) == 2 ? launch_tile_tpw<kBF16, 1, 1, 2>(a, tiles, s)
-                                             : launch_tile_tpw<kBF16, 1, 1, 1>(a, tiles, s);
-}
-template <>
-hipError_t launch_tile_t<kF16, 1, 1>(const GemvLaunch& a, int64_t tiles, hipStream_t s) {
-    return gemv_tile_per_wg(a.M, tiles) == 2 ? launch_tile_tpw<kF16, 1, 1, 2>(a, tiles, s)
-                                             : launch_tile_tpw<kF16, 1, 1, 1>(a, tiles, s);
-}
-
+// two tiles per workgroup exist for U == 1 at M == 1 only (gemv_tile_per_wg)
 template <int DT>
-static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, hipStream_t s) {
+static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, int tpw,
+                                 hipStream_t s) {
     if (a.M == 1) {
-        if (U == 1) return launch_tile_t<DT, 1, 1>(a, wgs, s);
-        if (U == 2) return launch_tile_t<DT, 1, 2>(a, wgs, s);
-        if (U == 4) return launch_tile_t<DT, 1, 4>(a, wgs, s);
+        if (U == 1) return tpw == 2 ? launch_tile_grid<DT, 1, 1, 2>(a, wgs, s)
+                                    : launch_tile_grid<DT, 1, 1, 1>(a, wgs, s);
+        if (tpw != 1) return hipErrorInvalidValue;
+        if (U == 2) return launch_tile_grid<DT, 1, 2, 1>(a, wgs, s);
+        if (U == 4) return launch_tile_grid<DT, 1, 4, 1>(a, wgs, s);
         return hipErrorInvalidValue;
     }
-    if (U == 1) return launch_tile_t<DT, 4, 1>(a, wgs, s);
-    if (U == 2) return launch_tile_t<DT, 4, 2>(a, wgs, s);
+    if (tpw != 1) return hipErrorInvalidValue;
+    if (U == 1) return launch_tile_grid<DT, 4, 1, 1>(a, wgs, s);
+    if (U == 2) return launch_tile_grid<DT, 4, 2, 1>(a, wgs, s);
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t wgs, int64_t Kmax, int dt,
+static hipError_t launch_tile_plan(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
+                                   int dt, hipStream_t s) {
+    return dt == kBF16 ? launch_tile_dt<kBF16>(a, wgs, p.U, p.tpw, s)
+                       : launch_tile_dt<kF16>(a, wgs, p.U, p.tpw, s);
+}
+
+// One job of `tiles` row tiles (per-linear launch).
+hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t tiles, int64_t Kmax, int dt,
                             hipStream_t s) {
-    if (wgs <= 0) return hipSuccess;
+    if (tiles <= 0) return hipSuccess;
     const int U = gemv_tile_rounds(a.M, Kmax);
-    if (wgs > 0x7FFFFFFF || U == 0) return hipErrorInvalidValue;
-    return dt == kBF16 ? launch_tile_dt<kBF16>(a, wgs, U, s) : launch_tile_dt<kF16>(a, wgs, U, s);
+    if (tiles > 0x7FFFFFFF || U == 0) return hipErrorInvalidValue;
+    const int tpw = U == 1 ? gemv_tile_per_wg(a.M, tiles) : 1;
+    return dt == kBF16 ? launch_tile_dt<kBF16>(a, (tiles + tpw - 1) / tpw, U, tpw, s)
+                       : launch_tile_dt<kF16>(a, (tiles + tpw - 1) / tpw, U, tpw, s);
 }
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,

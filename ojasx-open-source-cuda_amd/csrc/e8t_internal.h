@@ -84,6 +84,9 @@ struct GemvJob {
     const void* lora_b;       // LoRA up-projection [lora_r, N] in the activation dtype
     int64_t lora_r;           // adapter rank (0: none)
     int64_t lora_ldu;         // row stride of lora_u
+    const void* lora_a;       // LoRA down-projection A [K, lora_r] (u is computed from it)
+    float lora_scaling;
+    int32_t reserved;
 };
 
 constexpr int kGemvInlineJobs = 4;
@@ -110,8 +113,15 @@ struct GemvPlan {
     int mmax;    // activation rows staged in LDS (wide only): 1, 4 (post-scaled) or 16
     int C;       // consecutive tile groups per workgroup (post-scaled kernel; else 1)
     bool split_ps;  // small-layer post-scaled kernel: one tile per workgroup, K split over waves
+    bool tile;   // staged-tile kernel: U rounds per wave, tpw row tiles per workgroup
+    int U;
+    int tpw;
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
+// gemv_pick for a grouped launch, preferring the staged-tile kernel for launches of fewer
+// than OJX_TILE_GROUPED_BELOW row tiles when every job allows it (K % 1024 == 0, M <= 4,
+// 16-byte aligned codes and scales; kmax the longest K).
+GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool tile_ok);
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
                        hipStream_t stream);
@@ -125,6 +135,8 @@ bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* s
                          const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
 hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t wgs, int64_t Kmax, int dt,
                             hipStream_t stream);
+// Row tiles per workgroup of a one-job staged-tile launch over `tiles` row tiles.
+int gemv_tile_per_wg(int64_t M, int64_t tiles);
 
 // Prefill MFMA GEMM: F16/BF16, K % 64 == 0; fmt 0 (ternary, group size 32), 1 (2-bit) or 2
 // (1-bit Root E8), the last two with group size 8, 16, 32 or 64.
@@ -152,6 +164,17 @@ hipError_t launch_gemm_mfma(const void* x, const uint8_t* packed, const uint16_t
 constexpr int64_t kLoraMaxRank = 64;
 hipError_t launch_lora_down(const void* x, const void* a, int64_t M, int64_t K, int64_t r,
                             float scaling, int dt, float* u, int64_t ldu, hipStream_t stream);
+// Several adapters on the same x (up to kLoraDownItems per launch).
+struct LoraDown {
+    const void* a;   // [K, r] in dtype
+    float* u;        // fp32 [M, r], row stride ldu
+    int64_t r;
+    int64_t ldu;
+    float scaling;
+};
+constexpr int kLoraDownItems = 4;
+hipError_t launch_lora_down(const void* x, int64_t M, int64_t K, int dt, const LoraDown* items,
+                            int n, hipStream_t stream);
 
 // Records `msg` as the calling thread's last error (ojx_e8t_last_error) and returns `code`.
 int api_fail(int code, const char* msg);

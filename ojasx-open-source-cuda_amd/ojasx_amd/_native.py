@@ -66,6 +66,9 @@ class GemvJob(ctypes.Structure):
         ("lora_b", ctypes.c_void_p),
         ("lora_r", ctypes.c_int64),
         ("lora_ldu", ctypes.c_int64),
+        ("lora_a", ctypes.c_void_p),
+        ("lora_scaling", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
     ]
 
 _lib = None

@@ -12,9 +12,12 @@ Typical uses:
 * fused projections -- ``GroupedGemv.fused(layers, M, dtype)``: the outputs of
   the layers are concatenated along the last dim of one ``[M, sum(N)]`` tensor
   and every job reads the launch's ``x`` (at most 4 jobs travel in the kernel
-  arguments, no device table); layers with a LoRA adapter get it fused: each call
-  launches ``ojx_lora_down`` (u = scaling * x @ A) per adapter, and the grouped
-  kernel adds u @ B in its epilogue (E8LatticeLinear.forward, lattice.py:839-842);
+  arguments, no device table); layers with a LoRA adapter get it fused: the grouped
+  launch first computes u = scaling * x @ A for all adapters (one launch), and the
+  GEMV adds u @ B in its epilogue (E8LatticeLinear.forward, lattice.py:839-842).  The
+  plan holds the adapter tensors themselves (lora_A / lora_B must already be
+  contiguous in the activation dtype), so in-place updates of them are seen; a new
+  scaling needs a new plan;
 * a fixed table -- explicit ``x`` / ``y`` per job, uploaded once to the device.
 """
 
@@ -60,7 +63,7 @@ class GroupedGemv:
                 "gemv_grouped_plan")
         self.grid = grid.value
         self._keep = list(keep)  # tensors the job pointers refer to
-        self._lora = []          # (layer, u buffer, K) of the jobs with a fused adapter
+        self._lora = []          # layers whose adapter is fused (A, B, scaling read at plan time)
         self._dev = None
         if self.n > 4:
             raw = bytes(ctypes.string_at(ctypes.addressof(self._arr), ctypes.sizeof(self._arr)))
@@ -91,16 +94,19 @@ class GroupedGemv:
                 if getattr(l, "use_hadamard", False):
                     raise RuntimeError("grouped GEMV: adapters of Hadamard-rotated layers are "
                                        "not fused")
-                if l.lora_B.dtype != dtype or not l.lora_B.is_contiguous():
-                    raise RuntimeError("grouped GEMV: lora_B must be contiguous in the "
-                                       "activation dtype")
+                for name in ("lora_A", "lora_B"):
+                    t = getattr(l, name)
+                    if t.dtype != dtype or not t.is_contiguous():
+                        raise RuntimeError(f"grouped GEMV: {name} must be contiguous in the "
+                                           "activation dtype")
                 r = int(l.lora_A.shape[-1])
                 if not 1 <= r <= ops.LORA_MAX_RANK:
                     raise RuntimeError(f"grouped GEMV: LoRA rank {r} out of range")
                 u = torch.empty((int(M), r), dtype=torch.float32, device=dev)
                 j.lora_u, j.lora_b, j.lora_r, j.lora_ldu = u.data_ptr(), l.lora_B.data_ptr(), r, r
-                keep += [u, l.lora_B]
-                lora.append((l, u, int(l.in_features)))
+                j.lora_a, j.lora_scaling = l.lora_A.data_ptr(), float(l.scaling)
+                keep += [u, l.lora_A, l.lora_B]
+                lora.append(l)
             jobs.append(j)
             keep += [l.packed_weight, scales]
             col += int(l.out_features)
@@ -119,12 +125,6 @@ class GroupedGemv:
         if y is None and hasattr(self, "n_total") and x is not None:
             y = torch.empty((*x.shape[:-1], self.n_total), dtype=self.dtype, device=self.device)
         s = stream.cuda_stream if stream is not None else N.stream_handle(self.device)
-        for l, u, k in self._lora:  # u = scaling * (x @ A) for each fused adapter
-            a = l.lora_A.detach()
-            a = a if a.dtype == self.dtype and a.is_contiguous() else a.to(self.dtype).contiguous()
-            N.check(N.lib().ojx_lora_down(N.ptr(x), N.ptr(a), self.M, k, int(a.shape[-1]),
-                                          float(l.scaling), N.DTYPE_CODE[self.dtype], N.ptr(u),
-                                          s), "lora_down")
         N.check(N.lib().ojx_e8t_gemv_grouped(ctypes.addressof(self._arr),
                                              N.ptr(self._dev), self.n, N.ptr(x), N.ptr(y),
                                              self.M, N.DTYPE_CODE[self.dtype], s),

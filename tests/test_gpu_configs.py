@@ -70,22 +70,26 @@ def layer0():
     return [(name, N, K) + _gpu_layer(N, K, 8200 + j) for j, (name, N, K) in enumerate(LAYER)]
 
 
+@pytest.mark.parametrize("copies", [1, 2])
 @pytest.mark.parametrize("M", [1, 4, 16])
-def test_grouped_full_decoder_layer(layer0, M):
+def test_grouped_full_decoder_layer(layer0, M, copies):
     """the headline grouped launch (device job table, explicit x and y per job)
-    over one whole decoder layer: 2,688 row tiles select the streaming kernels."""
+    over one whole decoder layer (2,688 row tiles: the staged-tile kernel at M = 1, the
+    streaming kernels at M = 4 and 16) and over the layer twice (5,376 row tiles: the
+    streaming kernels at every M, as in the benchmark's 224-linear stack)."""
     xs = {K: torch.randn(M, K, generator=torch.Generator(device=DEV).manual_seed(8300 + M + K),
                          device=DEV).to(torch.bfloat16) for K in (4096, 14336)}
+    lin = layer0 * copies
     ys = [torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
-          for _, N, K, _, _ in layer0]
-    jobs = [_job(pk, sc, None, N, K, x=xs[K], y=y) for (_, N, K, pk, sc), y in zip(layer0, ys)]
+          for _, N, K, _, _ in lin]
+    jobs = [_job(pk, sc, None, N, K, x=xs[K], y=y) for (_, N, K, pk, sc), y in zip(lin, ys)]
     g = GroupedGemv(jobs, M, torch.bfloat16, DEV, keep=list(xs.values()) + ys)
-    print(f"grouped layer M={M} jobs={g.n} grid={g.grid}", flush=True)
-    assert g.n == 7 and sum((N + 15) // 16 for _, N, _, _, _ in layer0) == 2688
+    print(f"grouped layer x{copies} M={M} jobs={g.n} grid={g.grid}", flush=True)
+    assert g.n == 7 * copies and sum((N + 15) // 16 for _, N, _, _, _ in lin) == 2688 * copies
     for rep in range(2):
         g()
         torch.cuda.synchronize()
-        for (name, N, K, pk, sc), y in zip(layer0, ys):
+        for (name, N, K, pk, sc), y in zip(lin, ys):
             assert torch.isfinite(y).all(), name
             pk_np, sc_np = _np(pk, sc)
             x_np = xs[K].float().cpu().numpy()

@@ -72,7 +72,7 @@ def test_fused_lora_matches_oracle_plus_adapter(fmt, M):
            torch.bfloat16)
 
 
-@pytest.mark.parametrize("r", [1, 16, 64])
+@pytest.mark.parametrize("r", [1, 16, 24, 64])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_fused_lora_ranks_and_dtypes(r, dtype):
     # fp32 activations run the general kernel; fp16 the fast routes
