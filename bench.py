@@ -151,8 +151,10 @@ def _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes):
     """The stack's GEMVs as one launch per linear, replayed from one hipGraph per M."""
     stream = torch.cuda.current_stream()
 
-    def launch_all(M, stream_handle):
+    def launch_all(M, stream_handle, name=None):
         for i, s in enumerate(stack):
+            if name is not None and s["name"] != name:
+                continue
             st = lib.ojx_e8t_gemm_fwd(xs[(M, s["K"])].data_ptr(), s["packed"].data_ptr(),
                                       s["scales"].data_ptr(), None, ys[(M, i)].data_ptr(), M,
                                       s["N"], s["K"], GS, N_.BF16, None, 0, stream_handle)
@@ -184,6 +186,29 @@ def _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes):
         per_linear[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
                                   frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
                                   launches=len(stack))
+    # per shape: the stack's linears of one shape (one per layer, distinct weights), one
+    # hipGraph per (M, shape); microseconds per launch
+    for M in Ms:
+        shapes = {}
+        for name, N, K in LAYER_SHAPES:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cap_stream):
+                launch_all(M, torch.cuda.current_stream().cuda_stream, name)
+            g.replay()
+            torch.cuda.synchronize()
+            n = sum(1 for s in stack if s["name"] == name)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(steps):
+                g.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / steps / n
+            shapes[name] = dict(us=round(us, 2),
+                                weight_GBs=round(weight_bytes(N, K) / us / 1e3, 1))
+            del g
+        per_linear[str(M)]["per_shape"] = shapes
     return per_linear
 
 
@@ -343,11 +368,11 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = F
 
 # --------------------------------------------------------------------------- encoder
 
-def bench_encode(torch, N_, dev, layers: int, reps: int = 3, check_rows: int = 64):
+def bench_encode(torch, N_, dev, layers: int, reps: int = 3):
     """encode a `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights
     with 0.1% of entries set to +-8 sigma (seed 9000 + 7*layer + j), layer by layer: one
     encode launch per linear, the whole stack replayed from one hipGraph.  One layer of each
-    shape is checked bit for bit against the CPU oracle on its first `check_rows` rows, and
+    shape (layer 0: 218 M weights) is checked bit for bit against the CPU oracle, whole, and
     the oracle's own encode rate on one q-shaped layer is reported beside it."""
     import numpy as np
 
@@ -395,17 +420,17 @@ def bench_encode(torch, N_, dev, layers: int, reps: int = 3, check_rows: int = 6
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
 
-    # bit-exactness sample: the first check_rows rows of layer 0 of each shape
+    # bit-exactness: every linear of layer 0 (one per shape), whole, against the CPU oracle
+    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
     exact = True
     for w, pk, sc, name, N, K in items[:7]:
-        rows = min(check_rows, N)
-        ref_pk, ref_sc, _ = O.encode(w[:rows].float().cpu().numpy(), GS)
-        got_pk = pk[: rows * K * 3 // 16].cpu().numpy()
-        got_sc = sc[: rows * K // GS].cpu().view(torch.int16).numpy().view(np.uint16)
+        ref_pk, ref_sc, _ = O.encode(w.float().cpu().numpy(), GS, cores)
+        got_pk = pk.cpu().numpy()
+        got_sc = sc.cpu().view(torch.int16).numpy().view(np.uint16)
         exact = exact and np.array_equal(got_pk, ref_pk) and np.array_equal(got_sc, ref_sc)
+        del ref_pk, ref_sc, got_pk, got_sc
 
     # the CPU oracle's encode rate (host cores) on one q-shaped layer of the stack
-    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
     wq = items[0][0].float().cpu().numpy()
     O.encode(wq[:64], GS, cores)
     t1 = time.perf_counter()
@@ -417,7 +442,7 @@ def bench_encode(torch, N_, dev, layers: int, reps: int = 3, check_rows: int = 6
                 Gweights_s=round(numel / ms / 1e6, 1), GBs=round(numel * 2.25 / ms / 1e6, 1),
                 frac_hbm=round(numel * 2.25 / ms / 1e6 / HBM_PEAK_GBS, 4),
                 bytes_per_weight=2.25, bit_exact_sample=exact,
-                sample=f"first {check_rows} rows of layer 0 of each shape vs oracle/e8t_oracle.c",
+                sample="all of layer 0 (7 linears, 218 M weights) vs oracle/e8t_oracle.c",
                 generate_s=round(gen_s, 1),
                 cpu_oracle=dict(Gweights_s=round(wq.size / cpu_s / 1e9, 3), cores=cores,
                                 sample="one 4096x4096 layer, oracle/e8t_oracle.c (OpenMP)"))
