@@ -280,6 +280,10 @@ typedef struct ojx_e8t_gemv_job {
 int ojx_e8t_gemv_grouped_plan(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype,
                               int64_t* grid);
 
+/* Workgroups are issued in job order, and a job's workgroups run K / 1024 rounds each:
+ * ordering the jobs by decreasing K keeps the longest workgroups from forming the launch's
+ * tail (ojasx_amd.grouped.GroupedGemv does so). */
+
 /* Launches a planned group.  `jobs` is the planned host array; `jobs_dev` is NULL (then
  * njobs <= 4 and the jobs travel in the kernel arguments) or a device copy of `jobs`.
  * `x` and `y` are the defaults for jobs whose x / y are NULL. */

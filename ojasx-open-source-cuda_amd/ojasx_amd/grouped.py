@@ -56,6 +56,10 @@ class GroupedGemv:
         self.dtype = dtype
         self.device = torch.device(device)
         self.n = len(jobs)
+        # Workgroups start in job order; a job's workgroups run K / 1024 rounds each, so the
+        # longest-K jobs go first and the launch does not end on a tail of long workgroups
+        # (224-linear stack, M = 1: 439 -> 378 us).  Every job keeps its own output place.
+        jobs = sorted(jobs, key=lambda j: -int(j.K))
         self._arr = (N.GemvJob * self.n)(*jobs)
         grid = ctypes.c_int64(0)
         N.check(N.lib().ojx_e8t_gemv_grouped_plan(ctypes.addressof(self._arr), self.n, self.M,
