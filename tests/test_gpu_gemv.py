@@ -155,7 +155,7 @@ def test_grouped_plan_rejects_bad_jobs():
         g()
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 5, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16])
 @pytest.mark.parametrize("K", [1280, 4096])
 def test_wide_kernel_partial_rounds_and_ragged_rows(M, K):
     # >= 1024 row tiles selects the streaming kernel; K = 1280 leaves a partial
@@ -169,6 +169,31 @@ def test_wide_kernel_partial_rounds_and_ragged_rows(M, K):
     torch.cuda.synchronize()
     ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, O.DT_BF16)
     assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_wide_bf16_activation_dynamic_range(M):
+    # activations with a wide dynamic range through the streaming kernels at M <= 4:
+    # outliers (x1000), tiny values (x1e-3), blocks of zeros, a block of 1e-30 and a row far
+    # larger than the others; each row stays within the bar against its own scale
+    N, K = 16 * 1024 + 16, 2048
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=91)
+    g = torch.Generator().manual_seed(92)
+    x = torch.randn(M, K, generator=g)
+    idx = torch.randperm(M * K, generator=g)
+    x.view(-1)[idx[: M * K // 100]] *= 1000.0
+    x.view(-1)[idx[M * K // 100: M * K // 50]] *= 1e-3
+    x[:, 64:96] = 0.0
+    x[0, 1000:1032] = 1e-30
+    if M > 1:
+        x[1] *= 1e6
+    x = x.to(torch.bfloat16)
+    print(f"dynamic range M={M}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
+    for m in range(M):  # each row against its own scale
+        assert _rel(y[m:m + 1], ref[m:m + 1]) <= REL_TOL, m
 
 
 @pytest.mark.parametrize("M", [4, 12])
