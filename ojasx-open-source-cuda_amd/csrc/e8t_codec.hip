@@ -53,14 +53,25 @@ __device__ __forceinline__ float div_rn(float w, const GroupRecip& g) {
     return __builtin_fmaf(r, g.ys, q);
 }
 
+// The same quotient without the 2^48 scaling, for weights that came from fp16: every
+// nonzero fp16 value is at least 2^-24 in magnitude, so the residual is a normal fp32
+// number already (checked against true division for every finite fp16 w over 6,000 scales
+// from 2^-40 to 2^42: 0 mismatches).  w = -0 gives +0 here, as in div_rn.
+__device__ __forceinline__ float div_rn_f16in(float w, const GroupRecip& g) {
+#pragma clang fp contract(off)
+    const float q = w * g.y;
+    const float r = __builtin_fmaf(-q, g.s, w);
+    return __builtin_fmaf(r, g.y, q);
+}
+
 // Nearest point of one 8-vector of the group with fp32 scale s, as lattice.py:357-373:
 //   v = w / s (correctly rounded)
 //   q = clamp(rint(v), -1, 1); alt = q == 0 ? (v >= 0 ? 1 : -1) : 0
 //   pen = (alt - v)^2 - (q - v)^2 (three rounded ops, never contracted)
 //   odd sum(q): q[first argmin pen] = alt;  code = sum (q_i + 1) 3^i / 2.
-// All integer-valued quantities are carried in fp32, where they are exact.
-template <bool EXACT>
-__device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, const GroupRecip& g) {
+// All integer-valued quantities are carried in fp32, where they are exact.  This is the
+// literal form, used when the group's scale is not finite (true division).
+__device__ __forceinline__ uint32_t quantize8_exact(const float* __restrict__ w, float s) {
 #pragma clang fp contract(off)
     const float pow3[8] = {1.f, 3.f, 9.f, 27.f, 81.f, 243.f, 729.f, 2187.f};
     float v[8], q[8];
@@ -68,7 +79,7 @@ __device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, const
     float raw = 3280.f;  // sum of 3^i: the "+1" of every digit
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        v[i] = EXACT ? w[i] / g.s : div_rn(w[i], g);
+        v[i] = w[i] / s;
         float r = __builtin_rintf(v[i]);
         r = fmaxf(r, -1.f);
         r = fminf(r, 1.f);
@@ -97,6 +108,46 @@ __device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, const
     return ((uint32_t)raw) >> 1;
 }
 
+// The same nearest point for a finite scale, in a reduced form with the same results.
+// With d = fl(1 - |v|) and t = fl(fl(d * d) - fl(v * v)):
+//   * pen == |t| for every finite fp32 v (q == 0 puts both cases' squares in the same two
+//     rounded products: alt - v = +-d, q - v = -v; q != 0 swaps them), so the first argmin
+//     of pen is the first argmin of |t|;
+//   * alt - q == sgn(v) * sgn(t) for every v with |v| < 2^24 other than -0 (t >= 0 exactly
+//     when q == 0), so the flip adds +-3^i with the sign bit of v XOR t.
+// Both identities were checked exhaustively over all 2^32 fp32 bit patterns.  Here
+// |v| <= sqrt(gs) * (1 + eps) (the group's norm bounds every weight) and the residual
+// division returns +0 for w = -0.  The parity of sum(q) is the parity of the code's base-3
+// value, since every power of 3 is odd.  F16IN: the weights came from fp16.
+template <bool F16IN>
+__device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, const GroupRecip& g) {
+#pragma clang fp contract(off)
+    const float pow3[8] = {1.f, 3.f, 9.f, 27.f, 81.f, 243.f, 729.f, 2187.f};
+    float raw = 3280.f;  // sum of 3^i: the "+1" of every digit
+    float best_t = 0.f, best_v = 0.f, best_p = 0.f;  // t, v and 3^i of the first argmin
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float v = F16IN ? div_rn_f16in(w[i], g) : div_rn(w[i], g);
+        float r = __builtin_rintf(v);
+        r = fmaxf(r, -1.f);
+        r = fminf(r, 1.f);
+        raw = __builtin_fmaf(r, pow3[i], raw);
+        const float d = 1.f - fabsf(v);
+        const float d2 = d * d;
+        const float v2 = v * v;
+        const float t = d2 - v2;
+        if (i == 0 || fabsf(t) < fabsf(best_t)) {
+            best_t = t;
+            best_v = v;
+            best_p = pow3[i];
+        }
+    }
+    const uint32_t sg = (__float_as_uint(best_v) ^ __float_as_uint(best_t)) & 0x80000000u;
+    const int ri = (int)raw;  // exact: 0 .. 6560
+    const int fix = (ri & 1) ? (int)__uint_as_float(__float_as_uint(best_p) | sg) : 0;
+    return (uint32_t)(ri + fix) >> 1;
+}
+
 // Group scale (lattice.py:355-356) with torch's CPU norm order:
 // 8 fmaf lanes, lane j over elements j, j+8, ...; lanes summed left to right;
 // correctly rounded sqrt; true division by fp32(sqrt(gs)); + fp32(1e-8).
@@ -123,6 +174,30 @@ __device__ __forceinline__ void pack_pair(uint8_t* b, uint32_t c0, uint32_t c1) 
     b[0] = (uint8_t)(c0 & 0xFFu);
     b[1] = (uint8_t)(((c0 >> 8) & 0x0Fu) | ((c1 & 0x0Fu) << 4));
     b[2] = (uint8_t)((c1 >> 4) & 0xFFu);
+}
+
+// Eight weights from a 16-byte aligned, in-range address, as fp32.
+template <int WDT>
+__device__ __forceinline__ void load8_vec(const void* __restrict__ w, int64_t base, float* out) {
+    if constexpr (WDT == kF32) {
+        const float4* p = reinterpret_cast<const float4*>((const float*)w + base);
+        float4 a = p[0], b = p[1];
+        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    } else {
+        uint4 a = *reinterpret_cast<const uint4*>((const uint16_t*)w + base);
+        uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (WDT == kF16) {
+                out[2 * i] = f16_bits_to_f32(u[i] & 0xFFFFu);
+                out[2 * i + 1] = f16_bits_to_f32(u[i] >> 16);
+            } else {
+                out[2 * i] = bf16_bits_to_f32(u[i] & 0xFFFFu);
+                out[2 * i + 1] = bf16_bits_to_f32(u[i] >> 16);
+            }
+        }
+    }
 }
 
 template <int WDT>
@@ -169,20 +244,25 @@ __global__ __launch_bounds__(kEncThreads) void encode_kernel(
     const int64_t g = g0 + threadIdx.x;
     if (g < ngroups) {
         float x[GS];
+        if (vec_ok && (g + 1) * GS <= numel) {  // the whole group in range: one address
 #pragma unroll
-        for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+            for (int t = 0; t < NV; ++t) load8_vec<WDT>(w, g * GS + 8 * t, x + 8 * t);
+        } else {
+#pragma unroll
+            for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+        }
         const float s = group_scale<GS>(x, root);
         const GroupRecip gr = group_recip(s);
         uint8_t* st = stage + threadIdx.x * BYTES;
         if (!gr.exact) {
 #pragma unroll
             for (int p = 0; p < NV / 2; ++p)
-                pack_pair(st + 3 * p, quantize8<false>(x + 16 * p, gr),
-                          quantize8<false>(x + 16 * p + 8, gr));
+                pack_pair(st + 3 * p, quantize8<WDT == kF16>(x + 16 * p, gr),
+                          quantize8<WDT == kF16>(x + 16 * p + 8, gr));
         } else {
             for (int p = 0; p < NV / 2; ++p)
-                pack_pair(st + 3 * p, quantize8<true>(x + 16 * p, gr),
-                          quantize8<true>(x + 16 * p + 8, gr));
+                pack_pair(st + 3 * p, quantize8_exact(x + 16 * p, s),
+                          quantize8_exact(x + 16 * p + 8, s));
         }
         scales[g] = (uint16_t)f32_to_f16_bits(s);
     }
@@ -230,8 +310,9 @@ __global__ __launch_bounds__(kEncThreads) void encode_kernel_any(
         float x[16];
         load8<WDT>(w, base + 16 * p, numel, false, x);
         load8<WDT>(w, base + 16 * p + 8, numel, false, x + 8);
-        if (!gr.exact) pack_pair(dst + 3 * p, quantize8<false>(x, gr), quantize8<false>(x + 8, gr));
-        else pack_pair(dst + 3 * p, quantize8<true>(x, gr), quantize8<true>(x + 8, gr));
+        if (!gr.exact)
+            pack_pair(dst + 3 * p, quantize8<WDT == kF16>(x, gr), quantize8<WDT == kF16>(x + 8, gr));
+        else pack_pair(dst + 3 * p, quantize8_exact(x, s), quantize8_exact(x + 8, s));
     }
     scales[g] = (uint16_t)f32_to_f16_bits(s);
 }
@@ -405,8 +486,13 @@ __global__ __launch_bounds__(kEncThreads) void encode2_kernel(
     const int64_t g = g0 + threadIdx.x;
     if (g < ngroups) {
         float x[GS];
+        if (vec_ok && (g + 1) * GS <= numel) {  // the whole group in range: one address
 #pragma unroll
-        for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+            for (int t = 0; t < NV; ++t) load8_vec<WDT>(w, g * GS + 8 * t, x + 8 * t);
+        } else {
+#pragma unroll
+            for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+        }
         const float s = group_scale<GS>(x, root);
         const GroupRecip gr = group_recip(s);
         uint8_t* st = stage + threadIdx.x * BYTES;
