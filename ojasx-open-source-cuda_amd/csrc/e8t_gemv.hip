@@ -304,6 +304,13 @@ constexpr int kPsWaves = OJX_PS_WAVES;
 #define OJX_PS_TILES 2
 #endif
 constexpr int kPsTiles = OJX_PS_TILES;
+// Table slices of the post-scaled kernel at M = 1.  Measured on MI355X (32-layer grouped
+// stack, same box): 32 slices 0.361 ms against 0.400 ms with 16; at M = 4 the 32-slice
+// table costs a workgroup per CU of residency and runs 0.470 against 0.441 ms.
+#ifndef OJX_PS_SLOTS_M1
+#define OJX_PS_SLOTS_M1 32
+#endif
+constexpr int kPsSlotsM1 = OJX_PS_SLOTS_M1;
 // Optional occupancy request for the post-scaled kernel (waves per SIMD), e.g. 5.
 #ifdef OJX_PS_MIN_WAVES
 #define OJX_PS_OCC __attribute__((amdgpu_waves_per_eu(OJX_PS_MIN_WAVES)))
@@ -342,18 +349,20 @@ __device__ __forceinline__ void stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int6
     }
 }
 
-// Table reads of code J of each tile's code words (NW words = 8 codes per 3 words).
-template <int R, int NW, int J>
+// Table reads of code J of each tile's code words (NW words = 8 codes per 3 words), from a
+// table of SL bank slices.
+template <int R, int NW, int J, int SL = kLutSlots>
 __device__ __forceinline__ void codes_lut(const uint32_t (&cd)[R][NW], const char* lut,
                                           uint32_t slot, uint2 (&ml)[R], uint2 (&mh)[R]) {
+    using G = LutGeom<SL>;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t d[3] = {cd[r][3 * (J / 8)], cd[r][3 * (J / 8) + 1],
                                cd[r][3 * (J / 8) + 2]};
-        const uint32_t z = code_z<J % 8>(d, slot);
-        const uint32_t h = __umulhi(z, kHiMagic);
-        ml[r] = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
-        mh[r] = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+        const uint32_t z = code_z<J % 8, G::kCodeShift>(d, slot);
+        const uint32_t h = __umulhi(z, G::kHiMagic);
+        ml[r] = *reinterpret_cast<const uint2*>(lut + lo_addr_of<G::kStride>(h, z));
+        mh[r] = *reinterpret_cast<const uint2*>(lut + (h * G::kStride + slot));
     }
 }
 
@@ -364,11 +373,11 @@ __device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut,
 }
 
 // The same table reads, as one 4-word B operand per tile (lo words, hi words).
-template <int R, int NW, int J>
+template <int R, int NW, int J, int SL = kLutSlots>
 __device__ __forceinline__ void codes_lut4(const uint32_t (&cd)[R][NW], const char* lut,
                                            uint32_t slot, uint4 (&b)[R]) {
     uint2 ml[R], mh[R];
-    codes_lut<R, NW, J>(cd, lut, slot, ml, mh);
+    codes_lut<R, NW, J, SL>(cd, lut, slot, ml, mh);
 #pragma unroll
     for (int r = 0; r < R; ++r) b[r] = make_uint4(ml[r].x, ml[r].y, mh[r].x, mh[r].y);
 }
@@ -405,14 +414,14 @@ __device__ __forceinline__ void ahead_shift(Ahead<R>& ah, const uint4& xa_n, con
 }
 
 // Reads the operands of steps 0 .. kLookahead-1 of a round.
-template <int R, int NW>
+template <int R, int NW, int SL = kLutSlots>
 __device__ __forceinline__ void ahead_fill(Ahead<R>& ah, const uint32_t (&cd)[R][NW],
                                            const char* lut, uint32_t slot, const char* xa_base) {
     ah.xa[0] = *reinterpret_cast<const uint4*>(xa_base);
-    codes_lut4<R, NW, 0>(cd, lut, slot, ah.b[0]);
+    codes_lut4<R, NW, 0, SL>(cd, lut, slot, ah.b[0]);
     if constexpr (kLookahead > 1) {
         ah.xa[1] = *reinterpret_cast<const uint4*>(xa_base + 16);
-        codes_lut4<R, NW, 1>(cd, lut, slot, ah.b[1]);
+        codes_lut4<R, NW, 1, SL>(cd, lut, slot, ah.b[1]);
     }
 }
 
@@ -746,8 +755,9 @@ __device__ __forceinline__ void keep_mfma_result(const f32x4& d, float& consumer
     asm volatile("" : "+v"(consumer) : "v"(d));
 }
 
-// Step J of a post-scaled round; d[r] accumulates the current scale group of tile r.
-template <int DT, int R, int MM, int J>
+// Step J of a post-scaled round; d[r] accumulates the current scale group of tile r.  SL:
+// bank slices of the table.
+template <int DT, int R, int MM, int J, int SL>
 __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<R>& sc,
                                         const char* lut, uint32_t slot, const char* xa_base,
                                         Ahead<R>& ah, float (&sf)[R][2], f32x4 (&d)[R],
@@ -771,7 +781,7 @@ __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<
     uint4 xa_n, b_n[R];
     if constexpr (kFresh) {
         xa_n = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + kLookahead));
-        codes_lut4<R, 12, (kFresh ? J + kLookahead : 0)>(w.cd, lut, slot, b_n);
+        codes_lut4<R, 12, (kFresh ? J + kLookahead : 0), SL>(w.cd, lut, slot, b_n);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -788,24 +798,24 @@ __device__ __forceinline__ void ps_step(const WideCodes<R>& w, const WideScales<
     }
 }
 
-template <int DT, int R, int MM, int... J>
+template <int DT, int R, int MM, int SL, int... J>
 __device__ __forceinline__ void ps_steps(const WideCodes<R>& w, const WideScales<R>& sc,
                                          const char* lut, uint32_t slot, const char* xa_base,
                                          Ahead<R>& ah, float (&sf)[R][2], f32x4 (&d)[R],
                                          float (&acc)[R][MM], std::integer_sequence<int, J...>) {
-    (ps_step<DT, R, MM, J>(w, sc, lut, slot, xa_base, ah, sf, d, acc), ...);
+    (ps_step<DT, R, MM, J, SL>(w, sc, lut, slot, xa_base, ah, sf, d, acc), ...);
 }
 
-template <int DT, int R, int MM>
+template <int DT, int R, int MM, int SL = kLutSlots>
 __device__ __forceinline__ void ps_round(const WideCodes<R>& w, const WideScales<R>& sc,
                                          const char* lut, uint32_t slot, const char* xa_base,
                                          float (&acc)[R][MM]) {
     Ahead<R> ah;
     float sf[R][2];
     f32x4 d[R];
-    ahead_fill<R, 12>(ah, w.cd, lut, slot, xa_base);
-    ps_steps<DT, R, MM>(w, sc, lut, slot, xa_base, ah, sf, d, acc,
-                        std::make_integer_sequence<int, 32>{});
+    ahead_fill<R, 12, SL>(ah, w.cd, lut, slot, xa_base);
+    ps_steps<DT, R, MM, SL>(w, sc, lut, slot, xa_base, ah, sf, d, acc,
+                            std::make_integer_sequence<int, 32>{});
 }
 
 // Bias bits of this lane's rows of one tile group (0 without bias; rows past N read row
@@ -870,7 +880,11 @@ __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M,
 template <int DT, int R, int MM, int W>
 __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch args) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
-    __shared__ uint4 lut_storage[kLutValidStorageU4];
+    // Table slices: 32 at M = 1 (conflict-free 8-byte reads; the 20 KB table still leaves
+    // three workgroups per CU), 16 at M <= 4, whose larger activation buffers need the LDS.
+    constexpr int SL = MM == 1 ? kPsSlotsM1 : kLutSlots;
+    using G = LutGeom<SL>;
+    __shared__ uint4 lut_storage[G::kValidStorageU4];
     // Two activation buffers, separate LDS objects, each ending in 512 zero bytes (the A rows
     // outside a lane's group): every activation read then points into one known buffer, so
     // the compiler does not hold it behind the pending buffer->LDS loads into the other one
@@ -880,7 +894,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     __shared__ __attribute__((aligned(16))) char xsb[kXBytes + 512];
     __shared__ PsStage<R> stage[W];
 
-    fill_lut<64 * W, kLutValidEntries>(lut_storage, lut_values_kind<DT>());
+    fill_lut<64 * W, kLutValidEntries, SL>(lut_storage, lut_values_kind<DT>());
     if (threadIdx.x < 32) {
         reinterpret_cast<uint4*>(xsa + kXBytes)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
         reinterpret_cast<uint4*>(xsb + kXBytes)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
@@ -935,7 +949,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     for (int r = 0; r < R; ++r) st.vo_scale[r] = (row0 + 16u * r + i16) * srowbytes + 16u * g;
     const uint32_t q_me = ((uint32_t)g + ps_tau((uint32_t)i16)) & 3u;
     st.rd_code = (12u * i16 + 3u * q_me) * 16u;
-    const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+    const uint32_t slot = (uint32_t)(lane & (SL - 1)) * 8u;
 
     // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
     const int am = i16 & 3;
@@ -966,7 +980,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     stage_x(xsa, st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // table, zero blocks, round-0 weights and activations ready
-    const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
+    const char* lut = reinterpret_cast<const char*>(lut_storage) + G::kBaseOffset;
 
     int c = 0, u = 0;
     // one item: computes from the activation buffer behind xa_cur, fetches the next item
@@ -984,7 +998,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
             ps_load_scales<R>(sc_next, st, cn * scale_gshift, un, K, g);
             stage_x(xs_next, st.x, un, M, K, wave, lane, W);
         }
-        ps_round<DT, R, MM>(w, sc, lut, slot, xa_cur, acc);
+        ps_round<DT, R, MM, SL>(w, sc, lut, slot, xa_cur, acc);
         if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tg, lane, acc, bv);
         if (!has) return false;
         vm_wait_all();

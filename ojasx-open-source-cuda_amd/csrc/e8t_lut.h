@@ -7,8 +7,9 @@
 // coord*s exactly, since group scales are >= 0.  hi = floor(2c/81) is one mul_hi
 // (exact for every valid code, checked exhaustively).  The table is "bank sliced":
 // kLutSlots copies, lane l reading copy l % kLutSlots, which occupies only its own bank
-// pair.  16 copies (13 KB) measured as fast as 32 (26 KB) on MI355X and leave LDS for the
-// kernels' staging buffers; 8 copies lose more to bank conflicts than they gain.  The
+// pair.  16 copies (13 KB) leave LDS for the kernels' staging buffers; 8 copies lose more
+// to bank conflicts than they gain.  Kernels whose staging leaves room take 32 (LutGeom<32>:
+// 2.2 instead of 3.7 clock cycles per wave-wide 8-byte read on MI355X).  The
 // table is filled from a constant base table in device memory (one 8-byte load per
 // thread-item), not recomputed per entry.
 #pragma once
@@ -88,10 +89,11 @@ static __device__ const LutBase kLutBaseTab[3] = {
 // first write.  NT: threads of the workgroup.
 // Items (16-byte words, two slices of one entry) each thread of an NT-thread workgroup
 // writes for a table of ENTRIES entries.
-template <int NT, int ENTRIES>
+template <int NT, int ENTRIES, int SLOTS = kLutSlots>
 struct LutFill {
-    static constexpr int kPairs = kLutSlots / 2;
-    static constexpr int kItems = (ENTRIES + kLutGuard) * kPairs;
+    static constexpr int kGuardE = SLOTS == 32 ? 1 : 0;  // zero guard entry (32 slices)
+    static constexpr int kPairs = SLOTS / 2;
+    static constexpr int kItems = (ENTRIES + kGuardE) * kPairs;
     static constexpr int kPer = (kItems + NT - 1) / NT;
     uint2 v[kPer];
 
@@ -103,7 +105,7 @@ struct LutFill {
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int i = (int)threadIdx.x + k * NT;
-            v[k] = tab[(i < kItems ? i : 0) / kPairs + 1 - kLutGuard];
+            v[k] = tab[(i < kItems ? i : 0) / kPairs + 1 - kGuardE];
         }
     }
     __device__ __forceinline__ void store(uint4* storage) const {
@@ -116,11 +118,11 @@ struct LutFill {
 };
 
 // Fills the bank-sliced table from the base table in device memory: entry e (-1 = guard),
-// slice c at byte offset (e + kLutGuard) * kLutStride + c * 8 of the storage.  NT: threads
+// slice c at byte offset (e + guard) * (8 * SLOTS) + c * 8 of the storage.  NT: threads
 // of the workgroup.
-template <int NT, int ENTRIES = kLutEntries>
+template <int NT, int ENTRIES = kLutEntries, int SLOTS = kLutSlots>
 __device__ __forceinline__ void fill_lut(uint4* storage, int kind) {
-    LutFill<NT, ENTRIES> f;
+    LutFill<NT, ENTRIES, SLOTS> f;
     f.load(kind);
     f.store(storage);
 }
