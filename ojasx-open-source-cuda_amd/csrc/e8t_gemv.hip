@@ -1793,13 +1793,15 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
 constexpr int kTileWaves = 4;
 constexpr uint32_t kTileRoundCodes = 16 * 192;  // one round's codes of 16 rows
 
-template <int MM>
+// One wave's stage of one round for RT row tiles: the tiles' codes, their scales, then the
+// activations (shared by the tiles).
+template <int MM, int RT>
 struct TileStage {
-    static constexpr uint32_t kScales = kTileRoundCodes;          // offset of the scales
-    static constexpr uint32_t kX = kScales + 1024;                // offset of the activations
+    static constexpr uint32_t kScales = RT * kTileRoundCodes;     // offset of the scales
+    static constexpr uint32_t kX = kScales + RT * 1024;           // offset of the activations
     static constexpr int kXLoads = (145 * (MM - 1) + 140 + 63) / 64;  // 1-KB loads of them
     static constexpr uint32_t kBytes = kX + kXLoads * 1024;           // one round
-    static constexpr int kLoads = 4 + kXLoads;                    // 1-KB loads per round
+    static constexpr int kLoads = 4 * RT + kXLoads;               // 1-KB loads per round
 };
 
 // One 16-byte-per-lane buffer->LDS load (1 KB per wave) into `dst`.  (Not a template: the
@@ -1808,22 +1810,27 @@ __device__ __forceinline__ void dma_1k(__amdgpu_buffer_rsrc_t r, char* dst, uint
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(dst), 16, voffset, 0, 0, 0);
 }
 
-// Issues round u's loads into `stg`: three of codes, one of scales, `xloads` of activations.
+// Issues round u's loads into `stg`: for each of the rt row tiles (rows row0 + 16 r) three
+// of codes and one of scales, then `xloads` of activations.
 __device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
                                            __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t xr,
                                            uint32_t row0, uint32_t rowbytes, uint32_t srowbytes,
                                            uint32_t xrowbytes, int u, int lane, int xloads,
-                                           int M) {
+                                           int M, int rt) {
+    for (int r = 0; r < rt; ++r) {
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
-        const uint32_t sl = 64u * t + lane, n = sl / 12u, q = sl - 12u * n;
-        const uint32_t p = (q + 12u - n / 4u) % 12u;
-        dma_1k(pr, stg + 1024 * t, (row0 + n) * rowbytes + 192u * u + 16u * p);
+        for (int t = 0; t < 3; ++t) {
+            const uint32_t sl = 64u * t + lane, n = sl / 12u, q = sl - 12u * n;
+            const uint32_t p = (q + 12u - n / 4u) % 12u;
+            dma_1k(pr, stg + kTileRoundCodes * r + 1024 * t,
+                   (row0 + 16u * r + n) * rowbytes + 192u * u + 16u * p);
+        }
     }
-    {
+    for (int r = 0; r < rt; ++r) {
         const uint32_t n = (uint32_t)lane >> 2, q = (uint32_t)lane & 3u;
         const uint32_t p = (q + 4u - (n / 4u) % 4u) % 4u;
-        dma_1k(sr, stg + kTileRoundCodes, (row0 + n) * srowbytes + 64u * u + 16u * p);
+        dma_1k(sr, stg + kTileRoundCodes * rt + 1024 * r,
+               (row0 + 16u * r + n) * srowbytes + 64u * u + 16u * p);
     }
     // activations: row m's piece p at slot 145 m + p + 4 (p / 32) (the lane groups' 32-piece
     // runs 36 slots apart); unused slots and rows >= M read zeros
@@ -1833,7 +1840,7 @@ __device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
         const uint32_t off = (m < (uint32_t)M && blk < 4u && wi < 32u)
                                  ? m * xrowbytes + 2048u * u + 16u * (32u * blk + wi)
                                  : 0xFFFFFFF0u;
-        dma_1k(xr, stg + kTileRoundCodes + 1024 + 1024 * i, off);
+        dma_1k(xr, stg + (kTileRoundCodes + 1024) * rt + 1024 * i, off);
     }
 }
 
@@ -1847,9 +1854,9 @@ constexpr int kTileAhead = OJX_TILE_AHEAD;
 
 // The staged-tile kernel's table: 32 slices (conflict-free b64 reads: 2.2 clk per wave
 // read on MI355X against 3.7 with 16 slices, where neighbouring lanes share banks), holding
-// the coordinates themselves (+-1, 0 in the activation dtype).
-constexpr int kTileSlots = 32;
-using TileLut = LutGeom<kTileSlots>;
+// the coordinates themselves (+-1, 0 in the activation dtype); 16 slices where two row tiles
+// per wave need the LDS for their stages.
+template <int RT> constexpr int tile_slots() { return RT == 1 ? 32 : 16; }
 
 // One post-scaled 1024-k round (the layout of gemv_ps_kernel): A row 4g' + m carries
 // activation row m only in lane group g''s k slots (every other lane's fragment is zero), so
@@ -1858,44 +1865,59 @@ using TileLut = LutGeom<kTileSlots>;
 // group's scale into the fp32 accumulators.  The table and activation reads of step
 // J + kTileAhead are issued before the MFMA of step J; two D registers alternate between
 // scale groups.
-template <int DT, int MM>
+template <int DT, int MM, int RT>
 struct TileRound {
-    uint32_t cd[12];  // this lane's 32 codes
-    uint32_t scw[4];  // their 8 group scales (fp16 pairs)
+    using G = LutGeom<tile_slots<RT>()>;
+    uint32_t cd[RT][12];  // this lane's 32 codes of each row tile
+    uint32_t scw[RT][4];  // their 8 group scales (fp16 pairs)
     const char* lut;
     const char* xa;   // this lane's A fragment of step 0 (activations or a zero run)
     uint32_t slot;
 
     struct Pending {
-        uint4 a[kTileAhead], b[kTileAhead];
+        uint4 a[kTileAhead], b[kTileAhead][RT];
     };
 
     template <int J>
     __device__ __forceinline__ void reads(Pending& p) const {
         constexpr int r = J % kTileAhead;
         p.a[r] = *reinterpret_cast<const uint4*>(xa + 16 * J);
-        const uint32_t d[3] = {cd[3 * (J / 8)], cd[3 * (J / 8) + 1], cd[3 * (J / 8) + 2]};
-        const uint32_t z = code_z<J % 8, TileLut::kCodeShift>(d, slot);
-        const uint32_t h = __umulhi(z, TileLut::kHiMagic);
-        const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of<TileLut::kStride>(h, z));
-        const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * TileLut::kStride + slot));
-        p.b[r] = make_uint4(ml.x, ml.y, mh.x, mh.y);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t d[3] = {cd[t][3 * (J / 8)], cd[t][3 * (J / 8) + 1],
+                                   cd[t][3 * (J / 8) + 2]};
+            const uint32_t z = code_z<J % 8, G::kCodeShift>(d, slot);
+            const uint32_t h = __umulhi(z, G::kHiMagic);
+            const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of<G::kStride>(h, z));
+            const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * G::kStride + slot));
+            p.b[r][t] = make_uint4(ml.x, ml.y, mh.x, mh.y);
+        }
     }
     template <int J>
-    __device__ __forceinline__ void step(Pending& p, f32x4 (&d)[2], float (&acc)[MM]) const {
+    __device__ __forceinline__ void step(Pending& p, f32x4 (&d)[2][RT],
+                                         float (&acc)[RT][MM]) const {
         constexpr int r = J % kTileAhead, gi = J / 4;  // scale group of the step
-        f32x4& dg = d[gi & 1];
         const uint4 a = p.a[r];
-        const uint4 b = p.b[r];
-        if constexpr (J + kTileAhead < 32) reads<(J + kTileAhead < 32 ? J + kTileAhead : 0)>(p);
-        dg = mfma16<DT>(a, b, J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dg);
-        if constexpr (J % 4 == 3) {  // scale group gi complete: post-scale it
-            float s0, s1;
-            scale_pair_f32<DT>(scw[gi / 2], s0, s1);
-            const float sg = (gi & 1) ? s1 : s0;
+        uint4 b[RT];
 #pragma unroll
-            for (int q = 0; q < MM; ++q) acc[q] = __builtin_fmaf(dg[q], sg, acc[q]);
-            keep_mfma_result(dg, acc[0]);
+        for (int t = 0; t < RT; ++t) b[t] = p.b[r][t];
+        if constexpr (J + kTileAhead < 32) reads<(J + kTileAhead < 32 ? J + kTileAhead : 0)>(p);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            f32x4& dg = d[gi & 1][t];
+            dg = mfma16<DT>(a, b[t], J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dg);
+        }
+        if constexpr (J % 4 == 3) {  // scale group gi complete: post-scale it
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                f32x4& dg = d[gi & 1][t];
+                float s0, s1;
+                scale_pair_f32<DT>(scw[t][gi / 2], s0, s1);
+                const float sg = (gi & 1) ? s1 : s0;
+#pragma unroll
+                for (int q = 0; q < MM; ++q) acc[t][q] = __builtin_fmaf(dg[q], sg, acc[t][q]);
+                keep_mfma_result(dg, acc[t][0]);
+            }
         }
     }
     template <int... J>
@@ -1903,9 +1925,9 @@ struct TileRound {
         (reads<J>(p), ...);
     }
     template <int... J>
-    __device__ __forceinline__ void steps(float (&acc)[MM], std::integer_sequence<int, J...>) const {
+    __device__ __forceinline__ void steps(float (&acc)[RT][MM], std::integer_sequence<int, J...>) const {
         Pending p;
-        f32x4 d[2];
+        f32x4 d[2][RT];
         prologue(p, std::make_integer_sequence<int, kTileAhead>{});
         (step<J>(p, d, acc), ...);
     }
@@ -1930,17 +1952,21 @@ __device__ __forceinline__ void vm_wait_le() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
 }
 
-template <int DT, int MM, int U, int TPW>
-__global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLaunch args) {
-    using S = TileStage<MM>;
+// RT: row tiles per wave (they share the activation stage and the A fragment reads); a
+// workgroup covers TPW * RT row tiles.
+template <int DT, int MM, int U, int TPW, int RT>
+__global__ __launch_bounds__(64 * kTileWaves * TPW)
+__attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(GemvLaunch args) {
+    using S = TileStage<MM, RT>;
+    constexpr int SL = tile_slots<RT>();
+    using TileLut = LutGeom<SL>;
     constexpr int L = S::kLoads;
     constexpr int NW = kTileWaves * TPW;  // waves of the workgroup
     static_assert(L * U <= 63, "loads in flight per wave");
     __shared__ __attribute__((aligned(16))) char stage[NW * U * S::kBytes];
     __shared__ uint4 lut_storage[TileLut::kValidStorageU4];
-    // zero A fragments: lane l of step J reads zrun[l + J] (distinct addresses, no broadcast);
-    // later the waves' partial sums
-    __shared__ uint4 zrun[NW * 16 > 96 ? NW * 16 : 96];
+    // zero A fragments: lane l of step J reads zrun[l + J] (distinct addresses, no broadcast)
+    __shared__ uint4 zrun[96];
 
     int64_t wg = blockIdx.x;
     GemvJob job;
@@ -1954,7 +1980,7 @@ __global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLa
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int sub = wave / kTileWaves, wt = wave % kTileWaves;  // tile of the workgroup, K part
-    const int64_t tile = (wg - job.wg_begin) * TPW + sub;
+    const int64_t tile = ((wg - job.wg_begin) * TPW + sub) * RT;  // the wave's first tile
     const void* xbase = job.x ? job.x : args.x;
     void* ybase = job.y ? job.y : args.y;
 
@@ -1980,21 +2006,25 @@ __global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLa
     for (int i = 0; i < U; ++i)
         if (i < nr)
             tile_issue(wstage + i * S::kBytes, pr, sr, xr, row0, rowbytes, srowbytes,
-                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M);
+                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M, RT);
 
     // ---- decode table (computed) while the loads are in flight
     for (int i = (int)threadIdx.x; i < TileLut::kValidStorageU4; i += 64 * NW)
-        lut_storage[i] = lut_item<kTileSlots>(i, lut_values_kind<DT>());
+        lut_storage[i] = lut_item<SL>(i, lut_values_kind<DT>());
     if (threadIdx.x < 96) zrun[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t bias_bits = 0u;
-    if (wt == 0 && job.bias) {
-        const int64_t r = (int64_t)row0 + i16 < N ? (int64_t)row0 + i16 : N - 1;
-        bias_bits = ((const __attribute__((address_space(1))) uint16_t*)job.bias)[r];
+    uint32_t bias_bits[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        bias_bits[t] = 0u;
+        if (wt == 0 && job.bias) {
+            const int64_t r0 = (int64_t)row0 + 16 * t + i16;
+            bias_bits[t] = ((const __attribute__((address_space(1))) uint16_t*)job.bias)[r0 < N ? r0 : N - 1];
+        }
     }
     __syncthreads();
 
     const char* lut = reinterpret_cast<const char*>(lut_storage) + TileLut::kBaseOffset;
-    const uint32_t slot = (uint32_t)(lane & (kTileSlots - 1)) * 8u;
+    const uint32_t slot = (uint32_t)(lane & (SL - 1)) * 8u;
     // A row i16 = 4g' + m is live in lane group g' for activation rows m < M: piece 32g + J of
     // row m (slot 145 m + 36 g + J); every other lane reads zeros
     const int am = i16 & 3;
@@ -2002,9 +2032,11 @@ __global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLa
     const char* const zbase = reinterpret_cast<const char*>(zrun) + 16 * lane;
     const uint32_t xa0 = 16u * (145u * (uint32_t)am + 36u * (uint32_t)g);
     const uint32_t rq = (uint32_t)i16 / 4u;
-    float acc[MM];
+    float acc[RT][MM];
 #pragma unroll
-    for (int q = 0; q < MM; ++q) acc[q] = 0.f;
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int q = 0; q < MM; ++q) acc[t][q] = 0.f;
     auto round = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
         if (i >= nr) return;
@@ -2012,22 +2044,26 @@ __global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLa
         if (nr == U) vm_wait_le<L * (U - 1 - i)>();
         else vm_wait_all();
         const char* stg = wstage + i * S::kBytes;
-        TileRound<DT, MM> r;
+        TileRound<DT, MM, RT> r;
 #pragma unroll
-        for (int t = 0; t < 3; ++t) {
-            const uint32_t q = (3u * (uint32_t)g + (uint32_t)t + rq) % 12u;
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + (12u * i16 + q) * 16u);
-            r.cd[4 * t] = v.x;
-            r.cd[4 * t + 1] = v.y;
-            r.cd[4 * t + 2] = v.z;
-            r.cd[4 * t + 3] = v.w;
+        for (int tt = 0; tt < RT; ++tt) {
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                const uint32_t q = (3u * (uint32_t)g + (uint32_t)t + rq) % 12u;
+                const uint4 v = *reinterpret_cast<const uint4*>(stg + kTileRoundCodes * tt +
+                                                                (12u * i16 + q) * 16u);
+                r.cd[tt][4 * t] = v.x;
+                r.cd[tt][4 * t + 1] = v.y;
+                r.cd[tt][4 * t + 2] = v.z;
+                r.cd[tt][4 * t + 3] = v.w;
+            }
+            const uint4 sc = *reinterpret_cast<const uint4*>(
+                stg + S::kScales + 1024 * tt + (4u * i16 + (((uint32_t)g + rq) & 3u)) * 16u);
+            r.scw[tt][0] = sc.x;
+            r.scw[tt][1] = sc.y;
+            r.scw[tt][2] = sc.z;
+            r.scw[tt][3] = sc.w;
         }
-        const uint4 sc = *reinterpret_cast<const uint4*>(
-            stg + S::kScales + (4u * i16 + (((uint32_t)g + rq) & 3u)) * 16u);
-        r.scw[0] = sc.x;
-        r.scw[1] = sc.y;
-        r.scw[2] = sc.z;
-        r.scw[3] = sc.w;
         r.lut = lut;
         r.xa = a_live ? stg + S::kX + xa0 : zbase;
         r.slot = slot;
@@ -2039,26 +2075,36 @@ __global__ __launch_bounds__(64 * kTileWaves * TPW) void gemv_tile_kernel(GemvLa
 
     // sum the four lane groups of each row (lane group q keeps activation row q), then the
     // waves through LDS (zrun is no longer read)
-    float out = 0.f;
+    float out[RT];
 #pragma unroll
-    for (int q = 0; q < MM; ++q) {
-        float v = acc[q];
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
-        if (q == g) out = v;
+    for (int t = 0; t < RT; ++t) {
+        out[t] = 0.f;
+#pragma unroll
+        for (int q = 0; q < MM; ++q) {
+            float v = acc[t][q];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (q == g) out[t] = v;
+        }
     }
     __syncthreads();
-    float* red = reinterpret_cast<float*>(zrun);  // NW x 64 floats
-    red[wave * 64 + lane] = out;
+    // the waves' partial sums, in the stage (every wave has waited for all of its loads and
+    // read its stage before the barrier)
+    float* red = reinterpret_cast<float*>(stage);  // NW x RT x 64 floats
+#pragma unroll
+    for (int t = 0; t < RT; ++t) red[(wave * RT + t) * 64 + lane] = out[t];
     __syncthreads();
     if (wt != 0) return;
 #pragma unroll
-    for (int w2 = 1; w2 < kTileWaves; ++w2) out += red[(wave + w2) * 64 + lane];
-    const int64_t row = (int64_t)row0 + i16;
-    if (g < M && row < N) {
-        const float bv = job.bias ? bias_bits_to_f32<DT>(bias_bits) : 0.f;
-        store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row,
-                           out + bv + job_lora<DT>(job, g, row));
+    for (int t = 0; t < RT; ++t) {
+#pragma unroll
+        for (int w2 = 1; w2 < kTileWaves; ++w2) out[t] += red[((wave + w2) * RT + t) * 64 + lane];
+        const int64_t row = (int64_t)row0 + 16 * t + i16;
+        if (g < M && row < N) {
+            const float bv = job.bias ? bias_bits_to_f32<DT>(bias_bits[t]) : 0.f;
+            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row,
+                               out[t] + bv + job_lora<DT>(job, g, row));
+        }
     }
 }
 
@@ -2309,6 +2355,17 @@ int gemv_tile_per_wg(int64_t M, int64_t tiles) {
     return (M == 1 && tiles >= OJX_TILE_PAIR_FROM) ? 2 : 1;
 }
 
+// Row tiles per wave of a staged-tile launch: two at 1 < M <= 4 with one round per wave when
+// the launch has many tiles (the tiles share the activation stage, 9 KB per wave and round
+// at M = 4, and the A fragment reads; the stages of a workgroup then still fit twice per CU
+// with a 16-slice table).
+#ifndef OJX_TILE_RT2_FROM
+#define OJX_TILE_RT2_FROM 768
+#endif
+int gemv_tile_rows_per_wave(int64_t M, int64_t tiles, int U) {
+    return (M > 1 && U == 1 && tiles >= OJX_TILE_RT2_FROM) ? 2 : 1;
+}
+
 bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
     if (dt != kBF16 && dt != kF16) return false;
@@ -2330,42 +2387,47 @@ GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool ti
     GemvPlan p{};
     p.tile = true;
     p.U = U;
-    p.tpw = U == 1 ? gemv_tile_per_wg(M, total_tiles) : 1;
+    p.rt = gemv_tile_rows_per_wave(M, total_tiles, U);
+    p.tpw = (U == 1 ? gemv_tile_per_wg(M, total_tiles) : 1) * p.rt;
     p.R = p.S = p.W = p.C = 1;
     p.mmax = M == 1 ? 1 : 4;
     return p;
 }
 
-// `wgs` workgroups of TPW row tiles each (each job's tiles start a new workgroup)
-template <int DT, int MM, int U, int TPW>
+// `wgs` workgroups of TPW * RT row tiles each (each job's tiles start a new workgroup)
+template <int DT, int MM, int U, int TPW, int RT>
 static hipError_t launch_tile_grid(const GemvLaunch& a, int64_t wgs, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW>), dim3((unsigned)wgs),
+    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT>), dim3((unsigned)wgs),
                        dim3(64 * kTileWaves * TPW), 0, s, a);
     return hipGetLastError();
 }
 
-// two tiles per workgroup exist for U == 1 at M == 1 only (gemv_tile_per_wg)
+// tpw: row tiles per workgroup, rt of them per wave.  Two wave sets per workgroup exist for
+// U == 1 at M == 1 only (gemv_tile_per_wg), two tiles per wave for U == 1 at M > 1 only
+// (gemv_tile_rows_per_wave).
 template <int DT>
-static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, int tpw,
+static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, int tpw, int rt,
                                  hipStream_t s) {
     if (a.M == 1) {
-        if (U == 1) return tpw == 2 ? launch_tile_grid<DT, 1, 1, 2>(a, wgs, s)
-                                    : launch_tile_grid<DT, 1, 1, 1>(a, wgs, s);
+        if (rt != 1) return hipErrorInvalidValue;
+        if (U == 1) return tpw == 2 ? launch_tile_grid<DT, 1, 1, 2, 1>(a, wgs, s)
+                                    : launch_tile_grid<DT, 1, 1, 1, 1>(a, wgs, s);
         if (tpw != 1) return hipErrorInvalidValue;
-        if (U == 2) return launch_tile_grid<DT, 1, 2, 1>(a, wgs, s);
-        if (U == 4) return launch_tile_grid<DT, 1, 4, 1>(a, wgs, s);
+        if (U == 2) return launch_tile_grid<DT, 1, 2, 1, 1>(a, wgs, s);
+        if (U == 4) return launch_tile_grid<DT, 1, 4, 1, 1>(a, wgs, s);
         return hipErrorInvalidValue;
     }
-    if (tpw != 1) return hipErrorInvalidValue;
-    if (U == 1) return launch_tile_grid<DT, 4, 1, 1>(a, wgs, s);
-    if (U == 2) return launch_tile_grid<DT, 4, 2, 1>(a, wgs, s);
+    if (tpw != rt) return hipErrorInvalidValue;
+    if (U == 1) return rt == 2 ? launch_tile_grid<DT, 4, 1, 1, 2>(a, wgs, s)
+                               : launch_tile_grid<DT, 4, 1, 1, 1>(a, wgs, s);
+    if (U == 2 && rt == 1) return launch_tile_grid<DT, 4, 2, 1, 1>(a, wgs, s);
     return hipErrorInvalidValue;
 }
 
 static hipError_t launch_tile_plan(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                                    int dt, hipStream_t s) {
-    return dt == kBF16 ? launch_tile_dt<kBF16>(a, wgs, p.U, p.tpw, s)
-                       : launch_tile_dt<kF16>(a, wgs, p.U, p.tpw, s);
+    return dt == kBF16 ? launch_tile_dt<kBF16>(a, wgs, p.U, p.tpw, p.rt, s)
+                       : launch_tile_dt<kF16>(a, wgs, p.U, p.tpw, p.rt, s);
 }
 
 // One job of `tiles` row tiles (per-linear launch).
@@ -2374,9 +2436,10 @@ hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t tiles, int64_t Kmax, in
     if (tiles <= 0) return hipSuccess;
     const int U = gemv_tile_rounds(a.M, Kmax);
     if (tiles > 0x7FFFFFFF || U == 0) return hipErrorInvalidValue;
-    const int tpw = U == 1 ? gemv_tile_per_wg(a.M, tiles) : 1;
-    return dt == kBF16 ? launch_tile_dt<kBF16>(a, (tiles + tpw - 1) / tpw, U, tpw, s)
-                       : launch_tile_dt<kF16>(a, (tiles + tpw - 1) / tpw, U, tpw, s);
+    const int rt = gemv_tile_rows_per_wave(a.M, tiles, U);
+    const int tpw = (U == 1 ? gemv_tile_per_wg(a.M, tiles) : 1) * rt;
+    return dt == kBF16 ? launch_tile_dt<kBF16>(a, (tiles + tpw - 1) / tpw, U, tpw, rt, s)
+                       : launch_tile_dt<kF16>(a, (tiles + tpw - 1) / tpw, U, tpw, rt, s);
 }
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,

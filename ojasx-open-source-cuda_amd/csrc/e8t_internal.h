@@ -113,9 +113,10 @@ struct GemvPlan {
     int mmax;    // activation rows staged in LDS (wide only): 1, 4 (post-scaled) or 16
     int C;       // consecutive tile groups per workgroup (post-scaled kernel; else 1)
     bool split_ps;  // small-layer post-scaled kernel: one tile per workgroup, K split over waves
-    bool tile;   // staged-tile kernel: U rounds per wave, tpw row tiles per workgroup
-    int U;
+    bool tile;   // staged-tile kernel: U rounds per wave, tpw row tiles per workgroup, rt
+    int U;       //   of them per wave
     int tpw;
+    int rt;
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
 // gemv_pick for a grouped launch, preferring the staged-tile kernel for launches of fewer
