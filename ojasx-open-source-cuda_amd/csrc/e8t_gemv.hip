@@ -304,6 +304,15 @@ constexpr int kPsWaves = OJX_PS_WAVES;
 #define OJX_PS_TILES 2
 #endif
 constexpr int kPsTiles = OJX_PS_TILES;
+// Post-scaled launches at 1 < M <= 4 with fewer row tiles than this take one tile per wave
+// (64-row workgroups: twice the workgroups, each activation round shared by 64 rows).
+// Measured on the decoder's fused gate/up (1792 tiles, M = 4), per decode step of 32 layers:
+// 86 us less than the staged-tile kernel; launches of 8016 tiles (lm_head) gain nothing and
+// the 10,752-tile stack loses 10-15%, so they keep two tiles per wave.
+#ifndef OJX_PS_ONE_TILE_BELOW
+#define OJX_PS_ONE_TILE_BELOW 4096
+#endif
+constexpr int64_t kPsOneTileBelow = OJX_PS_ONE_TILE_BELOW;
 // Table slices of the post-scaled kernel at M = 1.  Measured on MI355X (32-layer grouped
 // stack, same box): 32 slices 0.361 ms against 0.400 ms with 16; at M = 4 the 32-slice
 // table costs a workgroup per CU of residency and runs 0.470 against 0.441 ms.
@@ -2135,7 +2144,7 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         p.S = 1;
         // M <= 4: post-scaled kernel (mmax 1 or 4); otherwise the mask kernel
         p.mmax = M == 1 ? 1 : (M <= 4 ? 4 : 16);
-        p.R = p.mmax == 16 ? 2 : kPsTiles;
+        p.R = p.mmax == 16 ? 2 : (p.mmax == 4 && total_tiles < kPsOneTileBelow ? 1 : kPsTiles);
         // post-scaled kernel: consecutive tile groups per workgroup
         p.C = p.mmax == 16 ? 1 : kPsChunk;
         // waves sharing one table copy and one activation stage
@@ -2213,6 +2222,8 @@ static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
             return launch_ps<DT, kPsTiles, 1, kPsWaves>(a, p, wgs, stream);
         if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 4)
             return launch_ps<DT, kPsTiles, 4, kPsWaves>(a, p, wgs, stream);
+        if (p.W == kPsWaves && p.R == 1 && p.mmax == 4)
+            return launch_ps<DT, 1, 4, kPsWaves>(a, p, wgs, stream);
         if (p.W == kMaskWaves && p.R == 2 && p.mmax == 16)
             return launch_mask<DT, 16, kMaskWaves>(a, wgs, stream);
         return hipErrorInvalidValue;
@@ -2378,12 +2389,18 @@ bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* s
     return (N + 16) * (K * 3 / 16) < (1ll << 31) && M * K * 2 < (1ll << 31);
 }
 
+// Grouped launches below these row-tile counts take the staged-tile kernel: M == 1 and
+// 1 < M <= 4 (from 1024 tiles the post-scaled kernel with one tile per wave is faster there).
 #ifndef OJX_TILE_GROUPED_BELOW
 #define OJX_TILE_GROUPED_BELOW 4096
 #endif
+#ifndef OJX_TILE_GROUPED_BELOW_M4
+#define OJX_TILE_GROUPED_BELOW_M4 1024
+#endif
 GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool tile_ok) {
     const int U = tile_ok ? gemv_tile_rounds(M, kmax) : 0;
-    if (U == 0 || total_tiles >= OJX_TILE_GROUPED_BELOW) return gemv_pick(total_tiles, M);
+    const int64_t below = M == 1 ? OJX_TILE_GROUPED_BELOW : OJX_TILE_GROUPED_BELOW_M4;
+    if (U == 0 || total_tiles >= below) return gemv_pick(total_tiles, M);
     GemvPlan p{};
     p.tile = true;
     p.U = U;

@@ -120,8 +120,9 @@ struct GemvPlan {
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
 // gemv_pick for a grouped launch, preferring the staged-tile kernel for launches of fewer
-// than OJX_TILE_GROUPED_BELOW row tiles when every job allows it (K % 1024 == 0, M <= 4,
-// 16-byte aligned codes and scales; kmax the longest K).
+// than OJX_TILE_GROUPED_BELOW (M == 1) or OJX_TILE_GROUPED_BELOW_M4 (1 < M <= 4) row tiles
+// when every job allows it (K % 1024 == 0, 16-byte aligned codes and scales; kmax the
+// longest K).
 GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool tile_ok);
 int64_t gemv_wgs_for(int64_t N, const GemvPlan& p);
 hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int dt,
