@@ -1526,9 +1526,14 @@ __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
 // Step h's A fragment: with the lane's offset xo = 8192 w + 512 i16 + 16 ((8g & 16) |
 // ((8g & 8) ^ (i16 & 8)) | (i16 & 7)) (bits 4..6 equal to i16 & 7), piece 8g + h of row
 // i16 sits at xs + (xo ^ 16 h).
-// One 16-row tile per workgroup: two (half the staged activation bytes per weight, half
-// the workgroups) measured slower for every format, these launches need the workgroups.
-constexpr int kB2mTiles = 1;
+// Row tiles per workgroup: one below kB2mTwoTilesFrom row tiles (these launches need the
+// workgroups), two from there (half the staged activation bytes per weight).  Measured on
+// MI355X, per-linear M = 16 (same box): gate/up 17.0 -> 13.5 us with two; four 14.2 us;
+// two from 256 tiles on (q/o, down) 5.7 -> 7.4 and 13.9 -> 18.8 us.
+#ifndef OJX_B2M_TWO_TILES_FROM
+#define OJX_B2M_TWO_TILES_FROM 512
+#endif
+constexpr int64_t kB2mTwoTilesFrom = OJX_B2M_TWO_TILES_FROM;
 
 template <int DT, int GS, int FMT, int R>
 struct B2mRound {
@@ -1605,8 +1610,9 @@ __device__ __forceinline__ void b2m_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, 
 
 // Waits until the older of the two rounds in flight has landed: a round issues one code
 // and one scale load per tile and eight activation loads (in-order vmcnt).
+template <int R>
 __device__ __forceinline__ void b2m_wait_round() {
-    constexpr int n = 2 * kB2mTiles + 8;
+    constexpr int n = 2 * R + 8;
     __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
 }
 
@@ -1642,7 +1648,7 @@ __device__ __forceinline__ void b2m_load(uint4& cp, uint4& sp, __amdgpu_buffer_r
     }
 }
 
-template <int DT, int GS, int FMT>
+template <int DT, int GS, int FMT, int R>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
@@ -1658,7 +1664,6 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     // two activation buffers per wave, separate LDS objects (see gemv2_kernel)
     __shared__ __attribute__((aligned(128))) char xs0[kB2Waves * kB2mXBytes];
     __shared__ __attribute__((aligned(128))) char xs1[kB2Waves * kB2mXBytes];
-    constexpr int R = kB2mTiles;
     static_assert(R * 64 * 16 <= kB2mXBytes, "partial sums fit a wave's activation buffer");
 
     if constexpr (FMT == kFmtTernary)
@@ -1722,7 +1727,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
         for (int r = 0; r < R; ++r)
             b2m_load<GS, FMT>(cp[1][r], sp[1][r], pr, sr, vo_code[r], vo_scale[r], u + kB2Waves);
         b2m_stage_x(xw1, xr, u + kB2Waves, xo_ld);
-        b2m_wait_round();  // round u's codes, scales and activations have landed
+        b2m_wait_round<R>();  // round u's codes, scales and activations have landed
         B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
         const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
@@ -1730,7 +1735,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
         for (int r = 0; r < R; ++r)
             b2m_load<GS, FMT>(cp[0][r], sp[0][r], pr, sr, vo_code[r], vo_scale[r], un);
         b2m_stage_x(xw0, xr, un, xo_ld);
-        b2m_wait_round();
+        b2m_wait_round<R>();
         B2mRound<DT, GS, FMT, R>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
         lds_wait_all();
         u += 2 * kB2Waves;
@@ -2305,9 +2310,15 @@ template <int DT, int GS, int FMT>
 static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream, const LoraEp& lora) {
-    const int64_t wgs = (N + 16 * kB2mTiles - 1) / (16 * kB2mTiles);
-    hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT>), dim3((unsigned)wgs), dim3(64 * kB2Waves),
-                       0, stream, x, packed, scales, bias, y, M, N, K, lora);
+    const int64_t tiles = (N + 15) / 16;
+    if (tiles >= kB2mTwoTilesFrom)
+        hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 2>), dim3((unsigned)((tiles + 1) / 2)),
+                           dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N, K,
+                           lora);
+    else
+        hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 1>), dim3((unsigned)tiles),
+                           dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N, K,
+                           lora);
     return hipGetLastError();
 }
 
