@@ -720,7 +720,9 @@ struct TorchRowSum {
 
 // Codes of one group whose weights are read 8 at a time by `get(t, x)`; accumulates the
 // MMSE sums; returns the fp16 scale bits.
-template <typename Get>
+// NV: the group's 8-blocks when known at compile time (the loop is then unrolled and a
+// register-resident group is indexed statically), else 0 and gs / 8 at run time.
+template <int NV = 0, typename Get>
 __device__ __forceinline__ uint32_t root_group(const Get& get, int64_t gs, float s,
                                                uint8_t* codes_out) {
 #pragma clang fp contract(off)
@@ -728,12 +730,14 @@ __device__ __forceinline__ uint32_t root_group(const Get& get, int64_t gs, float
     TorchRowSum num, den;
     num.init(gs);
     den.init(gs);
-    for (int64_t t = 0; t < gs / 8; ++t) {
+    const int64_t nv = NV > 0 ? NV : gs / 8;
+#pragma unroll
+    for (int64_t t = 0; t < nv; ++t) {
         float x[8], v[8];
         get(t, x);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = gr.exact ? x[i] / s : div_rn(x[i], gr);
-        const uint32_t c = root_code(v);
+        const uint32_t c = gr.exact ? root_code_full(v) : root_code_fast(v);
         codes_out[t] = (uint8_t)c;
         float wq[8], qq[8];
 #pragma unroll
@@ -762,14 +766,19 @@ __global__ __launch_bounds__(kEncThreads) void encode1_kernel(
     const int64_t g = g0 + threadIdx.x;
     if (g < ngroups) {
         float x[GS];
+        if (vec_ok && (g + 1) * GS <= numel) {  // the whole group in range: one address
 #pragma unroll
-        for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+            for (int t = 0; t < NV; ++t) load8_vec<WDT>(w, g * GS + 8 * t, x + 8 * t);
+        } else {
+#pragma unroll
+            for (int t = 0; t < NV; ++t) load8<WDT>(w, g * GS + 8 * t, numel, vec_ok, x + 8 * t);
+        }
         const float s = group_scale<GS>(x, root);
         auto get = [&](int64_t t, float (&o)[8]) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = x[8 * t + i];
         };
-        scales[g] = (uint16_t)root_group(get, GS, s, stage + threadIdx.x * NV);
+        scales[g] = (uint16_t)root_group<NV>(get, GS, s, stage + threadIdx.x * NV);
     }
     __syncthreads();
     const int64_t ng = (ngroups - g0) < kEncThreads ? (ngroups - g0) : kEncThreads;

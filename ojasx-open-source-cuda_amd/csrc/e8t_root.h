@@ -162,6 +162,132 @@ __host__ __device__ inline uint32_t root_code(const float (&v)[8]) {
 }
 
 
+// The full search out of line: its 64 partial chains stay out of the callers' registers.
+__host__ __device__ __attribute__((noinline)) inline uint32_t root_code_full(const float (&v)[8]) {
+    return root_code(v);
+}
+
+// root_code with the same result from a handful of candidate rows.  Per row family the best
+// exact-arithmetic dot (constants c1 = 2 c2 as above; a_k = |v_k|, S = sum a_k) is known in
+// closed form, and so is the runner-up:
+//   rows +-2 at i, j:  c1 (a_i + a_j) with signs matching v: best pair (1st, 2nd largest a),
+//                      then (1st, 3rd); every other row <= c1 max(m2 + m3, m1 + m4)
+//   rows (+-1)^8:      c2 (S - 2 sum_F a) over flip sets F of the parity that keeps an even
+//                      number of minus signs: F = {} or {smallest}, then {two smallest} or
+//                      {second smallest}; every other row <= c2 (S - 2 (a(1) + a(3))) or
+//                      c2 (S - 2 a(3))
+//   rows +-2 at i:     a_i: largest, then second largest; every other row <= m3
+// (m1 >= m2 >= ... the largest, a(1) <= a(2) <= ... the smallest magnitudes).  The six
+// candidates' dots are evaluated as the reference's fp32 chains (exactly as root_code does)
+// and the largest wins, the lower row index on ties.  That is the reference's argmax when the
+// winner exceeds the bound on all other rows by more than the chains' rounding error (at
+// most ~2^-16 (1 + S)): the margin used is 2^-12 (1 + S).  Otherwise (near-ties of three
+// rows, zero vectors) the full search runs.  Magnitudes are ordered by a 19-comparator
+// sorting network on keys whose low 3 bits hold the coordinate (order ties are harmless:
+// the bounds absorb them), the exact magnitudes of the chosen coordinates recovered from
+// the keys and a word of the dropped low bits.
+__host__ __device__ inline uint32_t root_code_fast(const float (&v)[8]) {
+#pragma clang fp contract(off)
+    const float n8 = __builtin_sqrtf(8.0f);
+    const float c1 = 2.0f / n8, c2 = 1.0f / n8;
+    float a[8];
+    uint32_t key[8];
+    uint32_t low = 0u, neg = 0u;  // low bits of a_k (3 per k); bit k: v_k < 0
+    float S = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        a[k] = __builtin_fabsf(v[k]);
+        uint32_t bits;
+        __builtin_memcpy(&bits, &a[k], 4);
+        key[k] = (bits & ~7u) | (uint32_t)k;
+        low |= (bits & 7u) << (3 * k);
+        neg |= (v[k] < 0.f ? 1u : 0u) << k;
+        S = k == 0 ? a[0] : S + a[k];
+    }
+    // ascending sort (Knuth's 19-comparator network for 8 inputs)
+    constexpr int kNet[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6},
+                                 {3, 7}, {0, 1}, {2, 3}, {4, 5}, {6, 7}, {2, 4}, {3, 5},
+                                 {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+    for (int c = 0; c < 19; ++c) {
+        const uint32_t x = key[kNet[c][0]], y = key[kNet[c][1]];
+        key[kNet[c][0]] = x < y ? x : y;
+        key[kNet[c][1]] = x < y ? y : x;
+    }
+    auto approx = [](uint32_t k) {
+        const uint32_t b = k & ~7u;
+        float f;
+        __builtin_memcpy(&f, &b, 4);
+        return f;
+    };
+    auto exact = [&](uint32_t k) {  // a of the key's coordinate
+        const uint32_t i = k & 7u, b = (k & ~7u) | ((low >> (3u * i)) & 7u);
+        float f;
+        __builtin_memcpy(&f, &b, 4);
+        return f;
+    };
+    const uint32_t i1 = key[7] & 7u, i2 = key[6] & 7u, i3 = key[5] & 7u;
+    const uint32_t b1 = key[0] & 7u, b2 = key[1] & 7u;
+    const float e1 = exact(key[7]), e2 = exact(key[6]), e3 = exact(key[5]);
+    // rows +-2 at i, j: the pair's lower coordinate takes the first fma
+    auto pair = [&](uint32_t p, float ap, uint32_t q, float aq, float& d) {
+        const uint32_t i = p < q ? p : q, j = p < q ? q : p;
+        const float ai = p < q ? ap : aq, aj = p < q ? aq : ap;
+        d = __builtin_fmaf(aj, c1, __builtin_fmaf(ai, c1, 0.f));
+        const uint32_t pidx = (i * (15u - i)) / 2u + (j - i - 1u);
+        return 4u * pidx + (((neg >> i) & 1u) ? 0u : 2u) + (((neg >> j) & 1u) ? 0u : 1u);
+    };
+    float dA1, dA2;
+    const uint32_t xA1 = pair(i1, e1, i2, e2, dA1);
+    const uint32_t xA2 = pair(i1, e1, i3, e3, dA2);
+    // rows (+-1)^8: flip sets by parity
+    const bool odd = (__builtin_popcount(neg) & 1) != 0;
+    const uint32_t f1 = odd ? (1u << b1) : 0u;
+    const uint32_t f2 = odd ? (1u << b2) : ((1u << b1) | (1u << b2));
+    auto chain = [&](uint32_t flip, float& d) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            acc = __builtin_fmaf(((flip >> k) & 1u) ? -a[k] : a[k], c2, acc);
+        d = acc;
+        const uint32_t minus = neg ^ flip;  // coordinates with sign -
+        uint32_t plus7 = 0u;                // bit 6 - k: + at coordinate k (k < 7)
+#pragma unroll
+        for (int k = 0; k < 7; ++k) plus7 |= (((minus >> k) & 1u) ^ 1u) << (6 - k);
+        return 112u + plus7;
+    };
+    float dB1, dB2;
+    const uint32_t xB1 = chain(f1, dB1);
+    const uint32_t xB2 = chain(f2, dB2);
+    // rows +-2 at i
+    const uint32_t xC1 = 240u + 2u * i1 + (((neg >> i1) & 1u) ? 0u : 1u);
+    const uint32_t xC2 = 240u + 2u * i2 + (((neg >> i2) & 1u) ? 0u : 1u);
+    float best = dA1;
+    uint32_t bi = xA1;
+    auto take = [&](float d, uint32_t x) {
+        if (d > best || (d == best && x < bi)) {
+            best = d;
+            bi = x;
+        }
+    };
+    take(dA2, xA2);
+    take(dB1, xB1);
+    take(dB2, xB2);
+    take(e1, xC1);
+    take(e2, xC2);
+    // bound on every other row
+    const float m1 = approx(key[7]), m2 = approx(key[6]), m3 = approx(key[5]),
+                m4 = approx(key[4]);
+    const float s1 = approx(key[0]), s3 = approx(key[2]);
+    const float pa = m2 + m3, pb = m1 + m4;
+    const float nA = c1 * (pa > pb ? pa : pb);
+    const float nB = c2 * (odd ? S - 2.f * s3 : S - 2.f * (s1 + s3));
+    float bound = nA > nB ? nA : nB;
+    bound = bound > m3 ? bound : m3;
+    if (best > bound + 0x1p-12f * (1.f + S)) return bi;
+    return root_code_full(v);
+}
+
 // 1-bit value words and v_perm_b32 selectors: per scale group the weights +-s and +-rnd(2s)
 // in the activation dtype, S0 = s | rnd(2s) << 16, S1 = -s | -rnd(2s) << 16; a 256-entry
 // table (4 KB) maps a code to the four selector words of its 8 weights.

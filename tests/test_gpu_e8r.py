@@ -73,6 +73,37 @@ def test_e8r_encode_large_fp16_layer():
     assert np.array_equal(_u16(scales), so)
 
 
+def _tie_heavy_weights(kind, shape, seed):
+    """Weights whose 8-vectors often have equal or nearly equal magnitudes or zeros: rows of
+    the code search then tie (the kernel's candidate search must defer to the full search)."""
+    g = torch.Generator().manual_seed(seed)
+    if kind == "levels":       # a few quantization levels: many exactly equal magnitudes
+        return (torch.randint(-3, 4, shape, generator=g).float() * 0.01).to(torch.float16)
+    if kind == "pruned":       # a third of the weights exactly zero
+        w = torch.randn(*shape, generator=g) * 0.02
+        return (w * (torch.rand(*shape, generator=g) > 0.33)).to(torch.float16)
+    if kind == "near":         # equal magnitudes up to a few ulps, random signs
+        sign = torch.where(torch.rand(*shape, generator=g) < 0.5, -1.0, 1.0)
+        return sign * 0.02 * (1 + torch.randint(0, 4, shape, generator=g).float() * 1e-7)
+    w = torch.zeros(*shape)     # "sparse": one or two nonzeros per 8-vector
+    v = w.view(-1, 8)
+    v[:, 0] = torch.randn(v.shape[0], generator=g) * 0.02
+    v[::2, 5] = v[::2, 0]
+    return w
+
+
+@pytest.mark.parametrize("kind", ["levels", "pruned", "near", "sparse"])
+@pytest.mark.parametrize("gs", [8, 32, 64])
+def test_e8r_encode_bit_exact_with_ties(kind, gs):
+    w = _tie_heavy_weights(kind, (512, 1024), 31 * gs + len(kind))
+    print(f"e8r encode ties {kind} gs={gs}", flush=True)
+    codes, scales = ops.encode1(w.to(DEV), gs)
+    torch.cuda.synchronize()
+    co, so, _ = O.e8r_encode(w.float().numpy(), gs)
+    assert np.array_equal(codes.cpu().numpy(), co)
+    assert np.array_equal(_u16(scales), so)
+
+
 @pytest.mark.parametrize("gs", [8, 32])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_e8r_decode_bit_exact(gs, dtype):
