@@ -1033,6 +1033,16 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
 // a q/o-sized layer (256 tiles) occupies 256 workgroups for about one memory round trip,
 // instead of a chain of dependent activation loads per chunk.
 
+// Waves per workgroup at M <= 4 (the rounds of a tile spread over more waves: the kernel's
+// main customer, the down projection at M = 4, K = 14336, runs 14 rounds per tile; with one
+// workgroup per CU, 4 waves leave one wave per SIMD to run 3-4 rounds back to back).
+// Measured on MI355X (same box): 4 waves 12.0 us, 8 waves 9.7 us; a second activation
+// buffer per wave (double buffering) instead: 11.9 us.
+#ifndef OJX_PSK_WAVES_M4
+#define OJX_PSK_WAVES_M4 8
+#endif
+constexpr int kPskWavesM4 = OJX_PSK_WAVES_M4;
+
 template <int DT, int MM, int W>
 __global__ __launch_bounds__(64 * W) void gemv_psk_kernel(GemvLaunch args) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
@@ -2210,7 +2220,9 @@ static hipError_t launch_ps(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
 
 template <int DT, int MM>
 static hipError_t launch_psk(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_psk_kernel<DT, MM, 4>), dim3((unsigned)wgs), dim3(256), 0, stream, a);
+    constexpr int W = MM == 4 ? kPskWavesM4 : 4;
+    hipLaunchKernelGGL((gemv_psk_kernel<DT, MM, W>), dim3((unsigned)wgs), dim3(64 * W), 0, stream,
+                       a);
     return hipGetLastError();
 }
 
