@@ -1978,14 +1978,15 @@ __device__ __forceinline__ void vm_wait_le() {
 
 // RT: row tiles per wave (they share the activation stage and the A fragment reads); a
 // workgroup covers TPW * RT row tiles.
-template <int DT, int MM, int U, int TPW, int RT>
-__global__ __launch_bounds__(64 * kTileWaves * TPW)
+// TW: waves per row tile (the tile's K / 1024 rounds are spread over them, U each).
+template <int DT, int MM, int U, int TPW, int RT, int TW>
+__global__ __launch_bounds__(64 * TW * TPW)
 __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(GemvLaunch args) {
     using S = TileStage<MM, RT>;
     constexpr int SL = tile_slots<RT>();
     using TileLut = LutGeom<SL>;
     constexpr int L = S::kLoads;
-    constexpr int NW = kTileWaves * TPW;  // waves of the workgroup
+    constexpr int NW = TW * TPW;  // waves of the workgroup
     static_assert(L * U <= 63, "loads in flight per wave");
     __shared__ __attribute__((aligned(16))) char stage[NW * U * S::kBytes];
     __shared__ uint4 lut_storage[TileLut::kValidStorageU4];
@@ -2003,7 +2004,7 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
             if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int sub = wave / kTileWaves, wt = wave % kTileWaves;  // tile of the workgroup, K part
+    const int sub = wave / TW, wt = wave % TW;  // tile of the workgroup, K part
     const int64_t tile = ((wg - job.wg_begin) * TPW + sub) * RT;  // the wave's first tile
     const void* xbase = job.x ? job.x : args.x;
     void* ybase = job.y ? job.y : args.y;
@@ -2122,7 +2123,7 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
 #pragma unroll
-        for (int w2 = 1; w2 < kTileWaves; ++w2) out[t] += red[((wave + w2) * RT + t) * 64 + lane];
+        for (int w2 = 1; w2 < TW; ++w2) out[t] += red[((wave + w2) * RT + t) * 64 + lane];
         const int64_t row = (int64_t)row0 + 16 * t + i16;
         if (g < M && row < N) {
             const float bv = job.bias ? bias_bits_to_f32<DT>(bias_bits[t]) : 0.f;
@@ -2435,10 +2436,10 @@ GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool ti
 }
 
 // `wgs` workgroups of TPW * RT row tiles each (each job's tiles start a new workgroup)
-template <int DT, int MM, int U, int TPW, int RT>
+template <int DT, int MM, int U, int TPW, int RT, int TW = kTileWaves>
 static hipError_t launch_tile_grid(const GemvLaunch& a, int64_t wgs, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT>), dim3((unsigned)wgs),
-                       dim3(64 * kTileWaves * TPW), 0, s, a);
+    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT, TW>), dim3((unsigned)wgs),
+                       dim3(64 * TW * TPW), 0, s, a);
     return hipGetLastError();
 }
 
@@ -2453,14 +2454,16 @@ static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, int tp
         if (U == 1) return tpw == 2 ? launch_tile_grid<DT, 1, 1, 2, 1>(a, wgs, s)
                                     : launch_tile_grid<DT, 1, 1, 1, 1>(a, wgs, s);
         if (tpw != 1) return hipErrorInvalidValue;
-        if (U == 2) return launch_tile_grid<DT, 1, 2, 1, 1>(a, wgs, s);
-        if (U == 4) return launch_tile_grid<DT, 1, 4, 1, 1>(a, wgs, s);
+        // a tile's rounds over 8 or 16 waves, one each (the same stage bytes per workgroup
+        // as 4 waves of 2 or 4 rounds, but more waves per SIMD to run them)
+        if (U == 2) return launch_tile_grid<DT, 1, 1, 1, 1, 8>(a, wgs, s);
+        if (U == 4) return launch_tile_grid<DT, 1, 1, 1, 1, 16>(a, wgs, s);
         return hipErrorInvalidValue;
     }
     if (tpw != rt) return hipErrorInvalidValue;
     if (U == 1) return rt == 2 ? launch_tile_grid<DT, 4, 1, 1, 2>(a, wgs, s)
                                : launch_tile_grid<DT, 4, 1, 1, 1>(a, wgs, s);
-    if (U == 2 && rt == 1) return launch_tile_grid<DT, 4, 2, 1, 1>(a, wgs, s);
+    if (U == 2 && rt == 1) return launch_tile_grid<DT, 4, 1, 1, 1, 8>(a, wgs, s);
     return hipErrorInvalidValue;
 }
 
