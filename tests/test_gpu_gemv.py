@@ -241,3 +241,51 @@ def test_staged_tile_gemv_two_tile_workgroups(K):
     torch.cuda.synchronize()
     ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_BF16)
     assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_staged_tile_gemv_two_tiles_per_wave(M):
+    # 777 row tiles at 1 < M <= 4 run two row tiles per wave: an odd tile count, so the last
+    # wave's second tile lies past N, and a ragged last tile, with bias
+    N, K = 16 * 776 + 7, 4096
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=N + M)
+    x = _x(M, K, seed=M * 3 + 1, dtype=torch.bfloat16)
+    bias = _x(1, N, seed=8, dtype=torch.bfloat16).reshape(N)
+    print(f"staged tile two tiles per wave M={M}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M", [2, 3])
+def test_gemv_down_shape_small_layer_kernel(M):
+    # K = 14336 at 1 < M <= 4: the small-layer post-scaled kernel (8 waves per workgroup,
+    # 14 rounds per tile: two on the first six waves, one on the last two)
+    N, K = 4096, 14336
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=8206 + M)
+    x = _x(M, K, seed=8400 + M, dtype=torch.float16)
+    print(f"gemv down small-layer kernel M={M}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, None, N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, None, N, K, 32, O.DT_F16)
+    assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_grouped_mid_size_launch_one_tile_per_wave(M):
+    # grouped launches of 1024..4095 row tiles at 1 < M <= 4 stream with one row tile per
+    # wave (the decoder's fused gate/up: 2 x 896 tiles); ragged second job
+    K = 4096
+    layers = [_L(14336, K, 31), _L(14336 - 40, K, 32)]
+    x = _x(M, K, seed=40 + M, dtype=torch.bfloat16).to(DEV)
+    g = GroupedGemv.fused(layers, M, torch.bfloat16)
+    print(f"grouped mid-size M={M} grid={g.grid}", flush=True)
+    y = g(x)
+    torch.cuda.synchronize()
+    col = 0
+    for l in layers:
+        ref = O.gemm_f64(x.float().cpu().numpy(), l.pk_np, l.sc_np, None, l.out_features, K, 32,
+                         O.DT_BF16)
+        assert _rel(y[:, col:col + l.out_features], ref) <= REL_TOL
+        col += l.out_features
