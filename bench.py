@@ -19,6 +19,9 @@ after the headline region and reported beside it.
 
 value   = effective weight bandwidth: packed-code + scale bytes of the stack x 3
           passes / measured step time (GB/s), as the metric defines it.
+warm-up = W untimed steps, then --settle-s (0.5) seconds of the same launches, untimed, so
+          that the timed steps run at the GPU's steady clocks; every other leg likewise
+          runs its own launches untimed for a fraction of that right before its timing.
 roofline= HBM-bound: ALGORITHMIC bytes of the grouped GEMV launches in the timed
           region (codes + scales + x + y) / their summed durations (HIP events
           around each launch, on its stream), against 8 TB/s.
@@ -78,6 +81,22 @@ def weight_bytes(N: int, K: int) -> int:
     return N * K * 3 // 16 + (N * K // GS) * 2
 
 
+# Seconds of untimed work before each timed region (--settle-s).
+SETTLE_S = 0.5
+
+
+def settle(torch, fn, seconds=None) -> None:
+    """Runs `fn` (the leg's own launches) untimed for `seconds` of wall time right before a
+    timed region.  From idle the GPU's clocks take a few hundred milliseconds of work to
+    reach their steady state: the grouped M = 1 decode launch averaged 0.43 ms over 30
+    launches from idle, 0.369 ms over 300 and 0.361 ms over 2000."""
+    s = SETTLE_S if seconds is None else seconds
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < s:
+        fn()
+        torch.cuda.synchronize()
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -105,6 +124,9 @@ def parse_args():
                     help="decode batch sizes of the headline step (profiling runs pick one)")
     ap.add_argument("--no-per-linear", action="store_true",
                     help="skip the per-linear hipGraph timing beside the headline")
+    ap.add_argument("--settle-s", type=float, default=0.5,
+                    help="seconds of each leg's own launches run untimed right before its "
+                         "timed region, after the warm-up steps (0: none)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run three device-to-device copies of this many MiB (the "
                          "known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE) and exit")
@@ -175,6 +197,7 @@ def _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes):
     torch.cuda.synchronize()
     per_linear = {}
     for M in Ms:
+        settle(torch, graphs[M].replay, SETTLE_S / 2)
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(stream)
@@ -196,6 +219,7 @@ def _bench_per_linear(torch, N_, lib, stack, xs, ys, steps, Ms, wbytes):
                 launch_all(M, torch.cuda.current_stream().cuda_stream, name)
             g.replay()
             torch.cuda.synchronize()
+            settle(torch, g.replay, SETTLE_S / 5)
             n = sum(1 for s in stack if s["name"] == name)
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
@@ -240,6 +264,7 @@ def bench_decode(torch, N_, stack, steps: int, warmup: int, dev, Ms=DECODE_M,
         for M in Ms:
             plans[M]()
     torch.cuda.synchronize()
+    settle(torch, lambda: [plans[M]() for M in Ms])
 
     # ---- timed region: exactly `steps` steps, synchronised on both sides
     ev = {M: [] for M in Ms}
@@ -338,6 +363,7 @@ def bench_prefill(torch, N_, stack, Ms, target_s: float, dev, backward: bool = F
             torch.cuda.synchronize()
             one = max(a.elapsed_time(b), 1e-3)
             iters = max(1, min(200, int(target_s * 1e3 / one)))
+            settle(torch, run, SETTLE_S / 5)
             a.record(stream)
             for _ in range(iters):
                 run()
@@ -411,6 +437,7 @@ def bench_encode(torch, N_, dev, layers: int, reps: int = 3):
         launch_all(torch.cuda.current_stream().cuda_stream)
     graph.replay()
     torch.cuda.synchronize()
+    settle(torch, graph.replay)
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record(stream)
@@ -506,6 +533,7 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
             launch_all(torch.cuda.current_stream().cuda_stream)
         graph.replay()
         torch.cuda.synchronize()
+        settle(torch, graph.replay, SETTLE_S / 2)
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(stream)
@@ -769,6 +797,7 @@ def bench_e2e(torch, dev, layers: int):
     # warm-up prefill (also first token), then the timed prefill
     model.prefill(prompt)
     torch.cuda.synchronize()
+    settle(torch, lambda: model.prefill(prompt), SETTLE_S / 2)
     ev = []
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
@@ -812,6 +841,13 @@ def bench_e2e(torch, dev, layers: int):
     torch.cuda.synchronize()
     match = all(bool((x == y).all()) for x, y in zip(eager, graph_tokens))
 
+    def replay_all():  # G replays from the first decode position (KV rows S .. S+G-1)
+        ids.copy_(first)
+        pos.fill_(S)
+        for _ in range(G):
+            graph.replay()
+
+    settle(torch, replay_all)
     ids.copy_(first)
     pos.fill_(S)
     torch.cuda.synchronize()
@@ -832,6 +868,7 @@ def bench_e2e(torch, dev, layers: int):
     with torch.cuda.graph(g_e8, stream=cap):
         model.decode_step_e8_only(xin, ain)
     torch.cuda.synchronize()
+    settle(torch, g_e8.replay, SETTLE_S / 2)
     a.record(stream)
     for _ in range(G):
         g_e8.replay()
@@ -938,6 +975,8 @@ def cpu_baseline(seconds: float):
 
 def main() -> int:
     args = parse_args()
+    global SETTLE_S
+    SETTLE_S = max(0.0, args.settle_s)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only (the E8 path is benchmarked on a "
@@ -988,6 +1027,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

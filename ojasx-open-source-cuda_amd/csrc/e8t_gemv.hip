@@ -299,6 +299,16 @@ constexpr int kPsChunk = OJX_PS_CHUNK;
 #define OJX_PS_WAVES 4
 #endif
 constexpr int kPsWaves = OJX_PS_WAVES;
+// Waves per workgroup and table slices of the post-scaled kernel at 1 < M <= 4, two tiles
+// per wave.
+#ifndef OJX_PS_WAVES_M4
+#define OJX_PS_WAVES_M4 4
+#endif
+constexpr int kPsWavesM4 = OJX_PS_WAVES_M4;
+#ifndef OJX_PS_SLOTS_M4
+#define OJX_PS_SLOTS_M4 16
+#endif
+constexpr int kPsSlotsM4 = OJX_PS_SLOTS_M4;
 // Row tiles (16 rows) per wave of the post-scaled kernel.
 #ifndef OJX_PS_TILES
 #define OJX_PS_TILES 2
@@ -891,7 +901,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
     // Table slices: 32 at M = 1 (conflict-free 8-byte reads; the 20 KB table still leaves
     // three workgroups per CU), 16 at M <= 4, whose larger activation buffers need the LDS.
-    constexpr int SL = MM == 1 ? kPsSlotsM1 : kLutSlots;
+    constexpr int SL = MM == 1 ? kPsSlotsM1 : (R == kPsTiles ? kPsSlotsM4 : kLutSlots);
     using G = LutGeom<SL>;
     __shared__ uint4 lut_storage[G::kValidStorageU4];
     // Two activation buffers, separate LDS objects, each ending in 512 zero bytes (the A rows
@@ -2164,7 +2174,7 @@ GemvPlan gemv_pick(int64_t total_tiles, int64_t M) {
         // post-scaled kernel: consecutive tile groups per workgroup
         p.C = p.mmax == 16 ? 1 : kPsChunk;
         // waves sharing one table copy and one activation stage
-        p.W = p.mmax == 16 ? kMaskWaves : kPsWaves;
+        p.W = p.mmax == 16 ? kMaskWaves : (p.mmax == 4 && p.R == kPsTiles ? kPsWavesM4 : kPsWaves);
     } else if (M <= 4) {
         // small layers, M <= 4: one tile per workgroup, rounds split over its waves
         p.wide = false;
@@ -2238,8 +2248,8 @@ static hipError_t launch_dt(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
     if (p.wide) {
         if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 1)
             return launch_ps<DT, kPsTiles, 1, kPsWaves>(a, p, wgs, stream);
-        if (p.W == kPsWaves && p.R == kPsTiles && p.mmax == 4)
-            return launch_ps<DT, kPsTiles, 4, kPsWaves>(a, p, wgs, stream);
+        if (p.W == kPsWavesM4 && p.R == kPsTiles && p.mmax == 4)
+            return launch_ps<DT, kPsTiles, 4, kPsWavesM4>(a, p, wgs, stream);
         if (p.W == kPsWaves && p.R == 1 && p.mmax == 4)
             return launch_ps<DT, 1, 4, kPsWaves>(a, p, wgs, stream);
         if (p.W == kMaskWaves && p.R == 2 && p.mmax == 16)
