@@ -127,8 +127,10 @@ int ojx_lora_down(const void* x, const void* lora_a, int64_t M, int64_t K, int64
  * the two matmuls and the add of E8LatticeLinear.forward (lattice.py:827-846; A [K, rank]
  * = lora_A, B [rank, N] = lora_B, both in dtype).  lora_u: caller-owned fp32 [M, rank]
  * scratch that receives u = scaling * (x @ A) (ojx_lora_down, launched first on the same
- * stream).  Other arguments and the workspace as ojx_e8t_gemm_fwd; the e8 / e8r variants
- * take the 2-bit and 1-bit formats. */
+ * stream) -- except where the decode GEMV forms u inside its own launch (ternary, M <= 4 on
+ * the staged-tile route with one 1024-k round per wave, rank 8, A 16-byte aligned): then
+ * lora_u is not written.  Other arguments and the workspace as ojx_e8t_gemm_fwd; the e8 /
+ * e8r variants take the 2-bit and 1-bit formats. */
 int ojx_e8t_gemm_fwd_lora(const void* x, const uint8_t* packed, const uint16_t* scales,
                           const void* bias, const void* lora_a, const void* lora_b,
                           int64_t rank, float scaling, float* lora_u, void* y, int64_t M,
@@ -264,7 +266,9 @@ typedef struct ojx_e8t_gemv_job {
      * u = lora_scaling * (x @ A) into the caller's fp32 scratch lora_u [M, lora_r] (row
      * stride lora_ldu, 0 = lora_r; adapters on the same x share one launch), then the
      * GEMV adds u @ B before the output is rounded.  A [K, lora_r], B [lora_r, N] in
-     * dtype. */
+     * dtype.  A launch on the staged-tile kernel with one round per wave and one row tile
+     * per workgroup (small grouped launches, M <= 4) forms u itself when every adapter has
+     * rank 8 and a 16-byte aligned A: one launch, lora_u not written. */
     float* lora_u;
     const void* lora_b;
     int64_t lora_r;

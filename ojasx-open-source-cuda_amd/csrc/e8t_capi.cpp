@@ -183,7 +183,8 @@ static const char* fmt_name(int fmt) {
 static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
                     const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                     int dtype, void* ws, size_t ws_bytes, void* stream,
-                    const ojx::LoraEp& lora = ojx::LoraEp{}) {
+                    const ojx::LoraEp& lora = ojx::LoraEp{}, const void* lora_a_in = nullptr,
+                    float lora_scaling = 0.f) {
     if (int r = check_fmt_args(fmt, x, packed, scales, y, M, N, K, gs, dtype)) return r;
     if (int r = check_workspace(ws, ws_bytes)) return r;
     if (M == 0 || N == 0) return OJX_OK;
@@ -197,6 +198,11 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
         j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
         j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
         j.lora_u = lora.u; j.lora_b = lora.b; j.lora_r = lora.r; j.lora_ldu = lora.ldu;
+        if (lora_a_in) {  // u formed inside the launch (gemm_fwd_lora checked the plan)
+            j.lora_a = lora_a_in;
+            j.lora_scaling = lora_scaling;
+            a.lora_inline = 1;
+        }
         a.njobs = 1;
         a.M = (int)M;
         e = ojx::launch_gemv_tile(a, (N + 15) / 16, K, dtype, s);
@@ -236,7 +242,8 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
 }
 
 // Forward with a LoRA adapter: u = scaling * (x @ A) into the caller's lora_u, then the
-// format's forward with u @ B added in its output epilogue.
+// format's forward with u @ B added in its output epilogue.  The staged-tile GEMV with one
+// round per wave forms u itself (rank 8): one launch, lora_u left untouched.
 static int gemm_fwd_lora(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* bias, const void* lora_a, const void* lora_b, int64_t rank,
                          float scaling, float* lora_u, void* y, int64_t M, int64_t N, int64_t K,
@@ -249,11 +256,17 @@ static int gemm_fwd_lora(int fmt, const void* x, const uint8_t* packed, const ui
     if (int r = check_fmt_args(fmt, x, packed, scales, y, M, N, K, gs, dtype)) return r;
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
-    const hipError_t e = ojx::launch_lora_down(x, lora_a, M, K, rank, scaling, dtype, lora_u,
-                                               rank, (hipStream_t)stream);
-    if (e != hipSuccess) return fail(OJX_EHIP, "lora_down launch: %s", hipGetErrorString(e));
+    const bool inline_u =
+        route_fwd(fmt, x, packed, scales, y, M, N, K, gs, dtype) == kRouteGemvTile &&
+        ojx::gemv_tile_lora_inline_ok(M, N, K, rank, lora_a);
+    if (!inline_u) {
+        const hipError_t e = ojx::launch_lora_down(x, lora_a, M, K, rank, scaling, dtype,
+                                                   lora_u, rank, (hipStream_t)stream);
+        if (e != hipSuccess) return fail(OJX_EHIP, "lora_down launch: %s", hipGetErrorString(e));
+    }
     return gemm_fwd(fmt, x, packed, scales, bias, y, M, N, K, gs, dtype, ws, ws_bytes, stream,
-                    ojx::LoraEp{lora_u, lora_b, rank, rank, N});
+                    ojx::LoraEp{lora_u, lora_b, rank, rank, N}, inline_u ? lora_a : nullptr,
+                    scaling);
 }
 
 // Backward dX of every format: grad_x[M, K] = grad_y[M, N] . Wdeq[N, K].
@@ -430,9 +443,16 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
     a.y = y;
     a.njobs = njobs;
     a.M = (int)M;
-    // the adapters' down-projections before the GEMV: consecutive adapter jobs on the same
-    // activations (same x, same K) share a launch
-    for (int i = 0; i < njobs;) {
+    // staged-tile plans with one round per wave form the (rank-8) adapters' u themselves
+    bool inline_u = plan.tile;
+    for (int i = 0; i < njobs; ++i)
+        if (jobs[i].lora_r > 0)
+            inline_u = inline_u && ojx::gemv_lora_inline_ok(plan.U, plan.rt, plan.tpw,
+                                                             jobs[i].lora_r, jobs[i].lora_a);
+    a.lora_inline = inline_u ? 1 : 0;
+    // otherwise the adapters' down-projections run before the GEMV: consecutive adapter jobs
+    // on the same activations (same x, same K) share a launch
+    for (int i = 0; i < njobs && !inline_u;) {
         if (jobs[i].lora_r <= 0) { ++i; continue; }
         const void* xi = jobs[i].x ? jobs[i].x : x;
         const int64_t Ki = jobs[i].K;

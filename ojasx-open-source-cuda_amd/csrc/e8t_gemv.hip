@@ -1986,6 +1986,101 @@ __device__ __forceinline__ void vm_wait_le() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
 }
 
+// ---- LoRA down-projection inside the staged-tile launch (one round per wave, rank 8)
+//
+// The fused epilogue adds u @ B with u = scaling * (x @ A) [M, 8] (lattice.py:839-842).
+// Instead of a separate down-projection launch before the GEMV, every workgroup of an
+// adapter job forms u itself: each wave of its first tile set adds the k range of its own
+// round, whose activations are already in its stage.  Lane l takes k = 16 l .. 16 l + 15 of
+// the round: 16 rows of A (16 bytes each, loaded when the round's weights are requested),
+// two 16-byte activation pieces per row m, and v_dot2 products of k pairs (the pair of A
+// values of one column is put together by one v_perm).  The lanes' partial sums are added
+// through the wave's own stage, the waves' through LDS, and the epilogue lanes read u there.
+constexpr int kLoraInlineRank = 8;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+template <int DT>
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float c) {
+    if constexpr (DT == kBF16)
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                               __builtin_bit_cast(bf16x2_t, b), c, false);
+    else
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a),
+                                      __builtin_bit_cast(f16x2_t, b), c, false);
+}
+
+// Rows k0 + 16 lane .. + 15 of A [K, 8] (16-byte rows), through buffer (not flat) loads: a
+// flat load could read LDS, so the compiler would first wait for every pending
+// buffer->LDS load of the stage.
+__device__ __forceinline__ void lora_load_a(const void* a, int64_t K, int64_t k0, int lane,
+                                            uint4 (&ar)[16]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a, (short)0, (int)(K * 2 * kLoraInlineRank), kRsrcWord3);
+    const uint32_t vo = (uint32_t)(k0 + 16 * lane) * 16u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo + 16u * i, 0, 0);
+        ar[i] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+}
+
+// part[m][j] += sum over this lane's 16 k of x[m][k] A[k][j]; x piece p (8 k) of activation
+// row m at xst + 16 (145 m + p + 4 (p / 32)) (the staged-tile layout; rows >= M are zeros).
+template <int DT, int MM>
+__device__ __forceinline__ void lora_round_part(const uint4 (&ar)[16], const char* xst, int lane,
+                                                float (&part)[MM][kLoraInlineRank]) {
+    uint32_t lo[8][4], hi[8][4];  // (A[k][c], A[k + 1][c]) for k pair kp, columns 2h, 2h + 1
+#pragma unroll
+    for (int kp = 0; kp < 8; ++kp) {
+        const uint32_t r0[4] = {ar[2 * kp].x, ar[2 * kp].y, ar[2 * kp].z, ar[2 * kp].w};
+        const uint32_t r1[4] = {ar[2 * kp + 1].x, ar[2 * kp + 1].y, ar[2 * kp + 1].z,
+                                ar[2 * kp + 1].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            lo[kp][h] = __builtin_amdgcn_perm(r1[h], r0[h], 0x05040100u);
+            hi[kp][h] = __builtin_amdgcn_perm(r1[h], r0[h], 0x07060302u);
+        }
+    }
+    const uint32_t p0 = 2u * (uint32_t)lane;  // pieces p0, p0 + 1 (same 32-piece run)
+    lds_wait_all();
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        const char* xp = xst + 16u * (145u * (uint32_t)m + p0 + 4u * (p0 >> 5));
+        const uint4 x0 = *reinterpret_cast<const uint4*>(xp);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(xp + 16);
+        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int kp = 0; kp < 8; ++kp)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                part[m][2 * h] = dot2_acc<DT>(xw[kp], lo[kp][h], part[m][2 * h]);
+                part[m][2 * h + 1] = dot2_acc<DT>(xw[kp], hi[kp][h], part[m][2 * h + 1]);
+            }
+    }
+}
+
+// Sum of part over the wave's 64 lanes through `scr` (64 x (V + 1) floats of this wave's own
+// LDS); lane c < V returns the total of column c = 8 m + j.
+template <int MM>
+__device__ __forceinline__ float lora_wave_sum(const float (&part)[MM][kLoraInlineRank], float* scr,
+                                               int lane) {
+    constexpr int V = MM * kLoraInlineRank, G = 64 / V;  // G lane groups share a column
+    lds_wait_all();  // the activation reads of the stage are done before it is written
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int j = 0; j < kLoraInlineRank; ++j) scr[lane * (V + 1) + 8 * m + j] = part[m][j];
+    lds_wait_all();
+    const int c = lane % V, r0 = (lane / V) * (64 / G);
+    float v = 0.f;
+#pragma unroll
+    for (int r = 0; r < 64 / G; ++r) v += scr[(r0 + r) * (V + 1) + c];
+#pragma unroll
+    for (int o = V; o < 64; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
 // RT: row tiles per wave (they share the activation stage and the A fragment reads); a
 // workgroup covers TPW * RT row tiles.
 // TW: waves per row tile (the tile's K / 1024 rounds are spread over them, U each).
@@ -2002,6 +2097,11 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     __shared__ uint4 lut_storage[TileLut::kValidStorageU4];
     // zero A fragments: lane l of step J reads zrun[l + J] (distinct addresses, no broadcast)
     __shared__ uint4 zrun[96];
+    // in-launch LoRA down-projection (the instantiation with one round per wave of 4, one
+    // tile per wave and workgroup; elsewhere the extra registers would cost occupancy):
+    // each wave's total of x @ A over its round
+    constexpr bool kLoraIn = U == 1 && RT == 1 && TPW == 1 && TW == kTileWaves;
+    __shared__ float lora_tot[kLoraIn ? TW : 1][MM * kLoraInlineRank];
 
     int64_t wg = blockIdx.x;
     GemvJob job;
@@ -2042,6 +2142,22 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
         if (i < nr)
             tile_issue(wstage + i * S::kBytes, pr, sr, xr, row0, rowbytes, srowbytes,
                        (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M, RT);
+    // the adapter's rows of A for this wave's round (the waves of tile set 0 form u)
+    const bool lora_in = kLoraIn && args.lora_inline && job.lora_r > 0;  // uniform
+    const bool lora_wave = lora_in && sub == 0 && nr > 0;
+    uint4 lora_a[16];
+    if (lora_wave) lora_load_a(job.lora_a, K, (int64_t)u0 * 1024, lane, lora_a);
+    // ... and the epilogue lanes' column of B (rows past N read row N - 1)
+    uint32_t lora_bq[kLoraIn ? kLoraInlineRank : 1];
+    if constexpr (kLoraIn) {
+        if (lora_in && wt == 0) {
+            const int64_t rr = (int64_t)row0 + i16 < N ? (int64_t)row0 + i16 : N - 1;
+            const __attribute__((address_space(1))) uint16_t* bp =
+                (const __attribute__((address_space(1))) uint16_t*)job.lora_b;
+#pragma unroll
+            for (int j = 0; j < kLoraInlineRank; ++j) lora_bq[j] = bp[j * N + rr];
+        }
+    }
 
     // ---- decode table (computed) while the loads are in flight
     for (int i = (int)threadIdx.x; i < TileLut::kValidStorageU4; i += 64 * NW)
@@ -2075,9 +2191,16 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     auto round = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
         if (i >= nr) return;
-        // round i's loads have landed when at most the later rounds' are outstanding
-        if (nr == U) vm_wait_le<L * (U - 1 - i)>();
-        else vm_wait_all();
+        // round i's loads have landed when at most the later rounds' are outstanding (and
+        // the adapter rows of A, requested after them)
+        if constexpr (kLoraIn) {
+            if (lora_wave && wt == 0) vm_wait_le<16 + kLoraInlineRank>();
+            else if (lora_wave) vm_wait_le<16>();
+            else vm_wait_all();
+        } else {
+            if (nr == U) vm_wait_le<L * (U - 1 - i)>();
+            else vm_wait_all();
+        }
         const char* stg = wstage + i * S::kBytes;
         TileRound<DT, MM, RT> r;
 #pragma unroll
@@ -2107,6 +2230,18 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     [&]<int... I>(std::integer_sequence<int, I...>) {
         (round(std::integral_constant<int, I>{}), ...);
     }(std::make_integer_sequence<int, U>{});
+    if constexpr (kLoraIn) {
+        if (lora_in) {
+            float part[MM][kLoraInlineRank];
+#pragma unroll
+            for (int m = 0; m < MM; ++m)
+#pragma unroll
+                for (int j = 0; j < kLoraInlineRank; ++j) part[m][j] = 0.f;
+            if (lora_wave) lora_round_part<DT, MM>(lora_a, wstage + S::kX, lane, part);
+            const float v = lora_wave_sum<MM>(part, reinterpret_cast<float*>(wstage), lane);
+            if (lane < MM * kLoraInlineRank) lora_tot[wt][lane] = v;
+        }
+    }
 
     // sum the four lane groups of each row (lane group q keeps activation row q), then the
     // waves through LDS (zrun is no longer read)
@@ -2137,8 +2272,20 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
         const int64_t row = (int64_t)row0 + 16 * t + i16;
         if (g < M && row < N) {
             const float bv = job.bias ? bias_bits_to_f32<DT>(bias_bits[t]) : 0.f;
-            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row,
-                               out[t] + bv + job_lora<DT>(job, g, row));
+            float lt = 0.f;
+            if (lora_in) {  // u[g][j] from the waves' totals, then u[g] . B[:, row]
+#pragma unroll
+                for (int j = 0; j < kLoraInlineRank; ++j) {
+                    float uj = 0.f;
+#pragma unroll
+                    for (int w2 = 0; w2 < TW; ++w2) uj += lora_tot[kLoraIn ? w2 : 0][8 * g + j];
+                    lt = __builtin_fmaf(job.lora_scaling * uj,
+                                        bias_bits_to_f32<DT>(lora_bq[kLoraIn ? j : 0]), lt);
+                }
+            } else {
+                lt = job_lora<DT>(job, g, row);
+            }
+            store_from_f32<DT>(ybase, (int64_t)g * job.y_ld + job.y_col + row, out[t] + bv + lt);
         }
     }
 }
@@ -2409,6 +2556,19 @@ int gemv_tile_per_wg(int64_t M, int64_t tiles) {
 #endif
 int gemv_tile_rows_per_wave(int64_t M, int64_t tiles, int U) {
     return (M > 1 && U == 1 && tiles >= OJX_TILE_RT2_FROM) ? 2 : 1;
+}
+
+bool gemv_lora_inline_ok(int U, int rt, int tpw, int64_t rank, const void* lora_a) {
+    return U == 1 && rt == 1 && tpw == 1 && rank == kLoraInlineRank &&
+           ((uintptr_t)lora_a & 15u) == 0;
+}
+
+bool gemv_tile_lora_inline_ok(int64_t M, int64_t N, int64_t K, int64_t rank,
+                              const void* lora_a) {
+    const int64_t tiles = (N + 15) / 16;
+    const int U = gemv_tile_rounds(M, K);
+    return gemv_lora_inline_ok(U, gemv_tile_rows_per_wave(M, tiles, U),
+                               U == 1 ? gemv_tile_per_wg(M, tiles) : 1, rank, lora_a);
 }
 
 bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* scales,

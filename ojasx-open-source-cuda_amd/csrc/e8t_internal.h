@@ -99,9 +99,17 @@ struct GemvLaunch {
     int njobs;
     int M;
     int chunk;                     // post-scaled kernel: tile groups per workgroup
+    int lora_inline;               // staged-tile kernel, one round per wave: jobs with an
+                                   // adapter form u from lora_a themselves (lora_u unused)
 };
 
 bool gemv_shape_ok(int64_t N, int64_t K);
+// Whether a staged-tile launch forms the adapters' u inside the launch: one round per wave
+// (U == 1), one row tile per wave and per workgroup (rt == tpw == 1), rank-8 adapters with
+// 16-byte aligned A.  The second form plans a per-linear launch of an [N, K] layer.
+bool gemv_lora_inline_ok(int U, int rt, int tpw, int64_t rank, const void* lora_a);
+bool gemv_tile_lora_inline_ok(int64_t M, int64_t N, int64_t K, int64_t rank,
+                              const void* lora_a);
 bool gemv_supported(const void* x, const uint8_t* packed, const uint16_t* scales, const void* y,
                     int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
 // Kernel variant of a decode-GEMV launch.

@@ -181,3 +181,61 @@ def test_grouped_fused_projection_with_adapters():
             got = y[:, col:col + l.out_features].double()
             assert ((got - ref).abs().max() / ref.abs().max()).item() <= 1e-2
             col += l.out_features
+
+
+@pytest.mark.parametrize("r", [8, 16])
+@pytest.mark.parametrize("K", [1024, 4096])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_fused_lora_tile_route_u_in_launch(M, K, r):
+    # per-linear decode on the staged-tile route: a rank-8 adapter's u is formed inside the
+    # GEMV launch (each wave adds its own round's k range; at K = 1024 three of the four
+    # waves have none), a rank-16 one by the separate down-projection launch first
+    N, gs, scaling = 512 + 16, 32, 2.0
+    pk, sc, pk_np, s16 = _layer(ops.FMT_TERNARY, N, K, gs, seed=1000 + 10 * M + K // 1024 + r)
+    g = torch.Generator().manual_seed(M + K + r)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    a = (torch.randn(K, r, generator=g) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(r, N, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    print(f"lora tile M={M} K={K} r={r}", flush=True)
+    y = ops.linear_lora(x.to(DEV), pk, sc, bias.to(DEV), a.to(DEV), b.to(DEV), scaling,
+                        ops.FMT_TERNARY, N, K, gs)
+    torch.cuda.synchronize()
+    _check(y, _ref(ops.FMT_TERNARY, x, pk_np, s16, bias, a, b, scaling, N, K, gs,
+                   torch.bfloat16), torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [1, 4])
+def test_grouped_adapters_u_in_launch_against_oracle(M, dtype):
+    # configs[4]'s q/k/v at K = 4096 in one grouped launch (staged-tile kernel, one round per
+    # wave): the rank-8 adapters of q and v are formed inside the launch; every output
+    # column against the fp64 oracle of the E8 op plus the adapter term
+    K, gs, scaling = 4096, 32, 2.0
+    shapes = ((1024, 8), (256, 0), (256, 8))
+    layers, refs_in = [], []
+    for i, (n, r) in enumerate(shapes):
+        pk, sc, pk_np, s16 = _layer(ops.FMT_TERNARY, n, K, gs, seed=2000 + i)
+        g = torch.Generator().manual_seed(2100 + i)
+        a = (torch.randn(K, max(r, 1), generator=g) * 0.05).to(dtype)
+        b = (torch.randn(max(r, 1), n, generator=g) * 0.05).to(dtype)
+        lyr = type("L", (), {})()
+        lyr.packed_weight, lyr.block_scales, lyr.bias = pk, sc, None
+        lyr.out_features, lyr.in_features, lyr.group_size, lyr.bitrate = n, K, gs, 1.5
+        lyr.rank = r
+        if r:
+            lyr.lora_A, lyr.lora_B, lyr.scaling = a.to(DEV), b.to(DEV), scaling
+        layers.append(lyr)
+        refs_in.append((pk_np, s16, n, r, a, b))
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(dtype)
+    grp = GroupedGemv.fused(layers, M, dtype)
+    y = grp(x.to(DEV))
+    torch.cuda.synchronize()
+    col = 0
+    for pk_np, s16, n, r, a, b in refs_in:
+        if r:
+            ref = _ref(ops.FMT_TERNARY, x, pk_np, s16, None, a, b, scaling, n, K, gs, dtype)
+        else:
+            ref = O.gemm_f64(x.float().numpy(), pk_np, s16, None, n, K, gs, DT_CODE[dtype])
+        _check(y[:, col:col + n], ref, dtype)
+        col += n
