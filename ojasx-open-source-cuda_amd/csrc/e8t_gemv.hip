@@ -448,6 +448,13 @@ __device__ __forceinline__ void vm_wait_all() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
 }
 
+// Waits until at most n of this wave's loads are outstanding (gfx9 vmcnt encoding).
+template <int n>
+__device__ __forceinline__ void vm_wait_le() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
+}
+
 __device__ __forceinline__ void lds_wait_all() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
@@ -500,37 +507,37 @@ __device__ __forceinline__ void mk_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, i
                                                  uniform_offset(u * kMRound * 2), 0, 0);
 }
 
-// Step J (0..15) of a mask-kernel round.
-template <int DT, int J>
-__device__ __forceinline__ void mk_step(const uint32_t (&cd)[2][6], const uint32_t (&sc)[2][2],
+// Step J (0..15) of a mask-kernel round (R row tiles).
+template <int DT, int R, int J>
+__device__ __forceinline__ void mk_step(const uint32_t (&cd)[R][6], const uint32_t (&sc)[R][2],
                                         const char* lut, uint32_t slot, const char* xa_base,
-                                        Ahead<2>& ah, uint32_t (&sw)[2][2], f32x4 (&acc)[2]) {
+                                        Ahead<R>& ah, uint32_t (&sw)[R][2], f32x4 (&acc)[R]) {
     if constexpr (J % 8 == 0) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) scale_words<DT>(sc[r][J / 8], sw[r][0], sw[r][1]);
+        for (int r = 0; r < R; ++r) scale_words<DT>(sc[r][J / 8], sw[r][0], sw[r][1]);
     }
     constexpr bool kFresh = J + kLookahead < 16;
-    uint4 xa_n, b_n[2];
+    uint4 xa_n, b_n[R];
     if constexpr (kFresh) {
         xa_n = *reinterpret_cast<const uint4*>(xa_base + 16 * (J + kLookahead));
-        codes_lut4<2, 6, (kFresh ? J + kLookahead : 0)>(cd, lut, slot, b_n);
+        codes_lut4<R, 6, (kFresh ? J + kLookahead : 0)>(cd, lut, slot, b_n);
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < R; ++r) {
         const uint32_t s = sw[r][(J / 4) & 1];
         const uint4 m = ah.b[0][r];
         const uint4 b = make_uint4(m.x & s, m.y & s, m.z & s, m.w & s);
         acc[r] = mfma16<DT>(ah.xa[0], b, acc[r]);
     }
-    if constexpr (J + 1 < 16) ahead_shift<2>(ah, xa_n, b_n, kFresh);
+    if constexpr (J + 1 < 16) ahead_shift<R>(ah, xa_n, b_n, kFresh);
 }
 
-template <int DT, int... J>
-__device__ __forceinline__ void mk_steps(const uint32_t (&cd)[2][6], const uint32_t (&sc)[2][2],
+template <int DT, int R, int... J>
+__device__ __forceinline__ void mk_steps(const uint32_t (&cd)[R][6], const uint32_t (&sc)[R][2],
                                          const char* lut, uint32_t slot, const char* xa_base,
-                                         Ahead<2>& ah, uint32_t (&sw)[2][2], f32x4 (&acc)[2],
+                                         Ahead<R>& ah, uint32_t (&sw)[R][2], f32x4 (&acc)[R],
                                          std::integer_sequence<int, J...>) {
-    (mk_step<DT, J>(cd, sc, lut, slot, xa_base, ah, sw, acc), ...);
+    (mk_step<DT, R, J>(cd, sc, lut, slot, xa_base, ah, sw, acc), ...);
 }
 
 // MMAX: activation rows staged (M <= MMAX); W: waves per workgroup (they share the table
@@ -642,7 +649,7 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
         Ahead<R> ah;
         uint32_t sw[R][2];
         ahead_fill<R, 6>(ah, cd, lut, slot, xa_base);
-        mk_steps<DT>(cd, sc, lut, slot, xa_base, ah, sw, acc,
+        mk_steps<DT, 2>(cd, sc, lut, slot, xa_base, ah, sw, acc,
                      std::make_integer_sequence<int, 16>{});
         if (!has) break;
         vm_wait_all();
@@ -1979,12 +1986,6 @@ __device__ __forceinline__ uint4 lut_item(int i, int kind) {
     return make_uint4(w0, w1, w0, w1);
 }
 
-// Waits until at most n of this wave's loads are outstanding (gfx9 vmcnt encoding).
-template <int n>
-__device__ __forceinline__ void vm_wait_le() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
-}
 
 // ---- LoRA down-projection inside the staged-tile launch (one round per wave, rank 8)
 //

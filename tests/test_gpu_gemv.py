@@ -71,6 +71,26 @@ def test_gemv_every_variant(N):
     assert _rel(y, ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("M", [5, 16])
+@pytest.mark.parametrize("K", [768, 1280, 1536, 2048])
+def test_streaming_m16_round_counts(K, M):
+    # >= 1024 row tiles at 4 < M <= 16: the streaming mask kernel's 512-k rounds -- a partial
+    # last round (768, 1280: lane groups past K), odd and even round counts (1536, 2048), and
+    # a partial last workgroup of 16 tiles (1026 tiles)
+    N = 16 * 1026
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=K + 7 * M)
+    x = _x(M, K, seed=M + K, dtype=torch.bfloat16)
+    bias = _x(1, N, seed=4, dtype=torch.bfloat16).reshape(N)
+    print(f"streaming M={M} K={K}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32,
+                     O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+    for m in range(M):  # each activation row against its own scale
+        assert _rel(y[m:m + 1], ref[m:m + 1]) <= REL_TOL, m
+
+
 def test_gemv_llama_down_shape_all_m():
     N, K = 4096, 14336
     pk, sc, pk_np, sc_np = _encoded(N, K, seed=8206)
