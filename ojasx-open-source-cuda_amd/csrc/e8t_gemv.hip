@@ -1803,6 +1803,192 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
 }
 
 
+// ---- the B-operand GEMV at M <= 4: four activation rows staged, four rounds in flight
+//
+// At M <= 4 the kernel above still stages 16 activation rows per round (8 KB of its wave's
+// LDS), which is what limits it to two rounds in flight.  Staging only rows 0..3 (2 KB per
+// round; A rows i16 >= 4 read row i16 & 3, and no lane stores their outputs) leaves room for
+// four rounds per wave in four buffers, so a wave of a decode-sized layer (K = 4096: four
+// rounds) requests all of its weights at once.  Spare slots past a wave's last round load
+// from past every buffer's end: zeros, no memory traffic, and the same count of loads per
+// slot, so that one wait count fits every slot.
+constexpr int kB2sRows = 4;
+#ifndef OJX_B2S
+#define OJX_B2S 1
+#endif
+constexpr int kB2sXBytes = kB2sRows * kB2mRound * 2;  // 2 KB per wave and round
+constexpr uint32_t kB2sOob = 0x80000000u;             // past every buffer here (< 2^31 bytes)
+
+// b2m_load of round u, or (live == false) the same loads past the buffers' ends.
+template <int GS, int FMT>
+__device__ __forceinline__ void b2s_load(uint4& cp, uint4& sp, __amdgpu_buffer_rsrc_t pr,
+                                         __amdgpu_buffer_rsrc_t sr, uint32_t vo_code,
+                                         uint32_t vo_scale, int u, bool live) {
+    const uint32_t vc = live ? vo_code : kB2sOob, vs = live ? vo_scale : kB2sOob;
+    constexpr int kCodeRound = FMT == kFmtRoot ? 32 : FMT == kFmtTernary ? 48 : 64;
+    const int sc = live ? uniform_offset((int64_t)u * kCodeRound) : 0;
+    const int ss = live ? uniform_offset((int64_t)u * (2 * kB2mRound / GS)) : 0;
+    if constexpr (FMT == kFmtRoot) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(pr, vc, sc, 0);
+        cp = make_uint4(v[0], v[1], 0u, 0u);
+    } else if constexpr (FMT == kFmtTernary) {
+        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(pr, vc, sc, 0);
+        cp = make_uint4(v.x, v.y, v.z, 0u);
+    } else {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vc, sc, 0);
+        cp = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    if constexpr (GS == 8) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(sr, vs, ss, 0);
+        sp = make_uint4(v.x, v.y, v.z, v.w);
+    } else if constexpr (GS == 16) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(sr, vs, ss, 0);
+        sp = make_uint4(v[0], v[1], 0u, 0u);
+    } else if constexpr (GS == 32) {
+        sp = make_uint4(__builtin_amdgcn_raw_buffer_load_b32(sr, vs, ss, 0), 0u, 0u, 0u);
+    } else {
+        sp = make_uint4(__builtin_amdgcn_raw_buffer_load_b16(sr, vs, ss, 0), 0u, 0u, 0u);
+    }
+}
+
+// Issues one round's loads into pipeline slot buffer `xb` (this wave's part of it).  (Not
+// a template: the host pass rejects the LDS-load builtin in a kernel template's callee.)
+__device__ __forceinline__ void b2s_stage_x(char* xb, __amdgpu_buffer_rsrc_t x, uint32_t xo0,
+                                            uint32_t xo1, int so) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(x, lds_ptr(xb), 16, xo0, so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(x, lds_ptr(xb + 1024), 16, xo1, so, 0, 0);
+}
+
+template <int DT, int GS, int FMT, int R>
+__global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
+    const void* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
+    int M, int64_t N, int64_t K, LoraEp lora) {
+    static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
+    static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
+    static_assert(FMT != kFmtTernary || GS == 32, "ternary GEMV: group size 32");
+    static_assert(R * 64 * 16 <= kB2sXBytes, "partial sums fit a wave's activation buffer");
+    constexpr int L = 2 * R + 2;  // loads per round: codes and scales per tile, 2 of rows
+    __shared__ uint4 lut_storage[FMT == kFmtTernary ? kLutValidStorageU4
+                                 : FMT == kFmtRoot  ? kSel1Entries
+                                                    : kB2LutU4];
+    // four pipeline buffers, separate LDS objects (the compiler then knows that a read of
+    // one does not wait for loads into another)
+    __shared__ __attribute__((aligned(128))) char xs0[kB2Waves * kB2sXBytes];
+    __shared__ __attribute__((aligned(128))) char xs1[kB2Waves * kB2sXBytes];
+    __shared__ __attribute__((aligned(128))) char xs2[kB2Waves * kB2sXBytes];
+    __shared__ __attribute__((aligned(128))) char xs3[kB2Waves * kB2sXBytes];
+
+    if constexpr (FMT == kFmtTernary)
+        fill_lut<64 * kB2Waves, kLutValidEntries>(lut_storage, kLutMasks);
+    else if constexpr (FMT == kFmtRoot) fill_sel1(lut_storage, 64 * kB2Waves);
+    else fill_b2sel<64 * kB2Waves>(lut_storage);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t tile = blockIdx.x;
+    const uint32_t rowbytes = (uint32_t)(FMT == kFmtTernary ? K * 3 / 16
+                                         : FMT == kFmtRoot  ? K / 8 : K / 4);
+    constexpr uint32_t kLaneBytes = FMT == kFmtTernary ? 12u : FMT == kFmtRoot ? 8u : 16u;
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+    // rows past N read zeros (buffer bound) and are never stored
+    uint32_t vo_code[R], vo_scale[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row_r = (uint32_t)((tile * R + r) * 16 + i16);
+        vo_code[r] = row_r * rowbytes + kLaneBytes * g;
+        vo_scale[r] = row_r * srowbytes + (128u / GS) * g;
+    }
+    const uint32_t slot = FMT == kFmtTernary ? (uint32_t)(lane & (kLutSlots - 1)) * 8u
+                                             : (uint32_t)(lane & 31) * 4u;
+    // activation rows 0..3 (rows >= M re-read row M - 1); the buffer layout of gemv2m_kernel
+    const uint32_t xo_ld0 = b2m_x_offset(0, lane, M, K), xo_ld1 = b2m_x_offset(1, lane, M, K);
+    // A row i16 reads row i16 & 3: piece 8g + h at position 8g + (m ^ h) of row m
+    const uint32_t am = (uint32_t)i16 & 3u;
+    const uint32_t xo = (uint32_t)wave * kB2sXBytes + 512u * am + 128u * (uint32_t)g + 16u * am;
+
+    // wave w takes rounds u = w + W i, i = 0 .. nr - 1, four of them in flight
+    const int T = (int)(K / kB2mRound);
+    const int nr = wave < T ? (T - 1 - wave) / kB2Waves + 1 : 0;
+    f32x4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 cp[4][R], sp[4][R];
+    char* const xsb[4] = {xs0, xs1, xs2, xs3};
+    auto issue = [&](auto jc, int i) {
+        constexpr int j = decltype(jc)::value;
+        const bool live = i < nr;  // uniform
+        const int u = wave + kB2Waves * i;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            b2s_load<GS, FMT>(cp[j][r], sp[j][r], pr, sr, vo_code[r], vo_scale[r], u, live);
+        b2s_stage_x(xsb[j] + wave * kB2sXBytes, xr, live ? xo_ld0 : kB2sOob,
+                    live ? xo_ld1 : kB2sOob,
+                    live ? uniform_offset((int64_t)u * kB2mRound * 2) : 0);
+    };
+    if (nr > 0) {
+        issue(std::integral_constant<int, 0>{}, 0);
+        issue(std::integral_constant<int, 1>{}, 1);
+        issue(std::integral_constant<int, 2>{}, 2);
+        issue(std::integral_constant<int, 3>{}, 3);
+    }
+    __syncthreads();  // selector table ready
+    const char* lut = reinterpret_cast<const char*>(lut_storage) +
+                      (FMT == kFmtTernary ? kLutBaseOffset : 0u);
+    for (int i0 = 0; i0 < nr; i0 += 4) {  // uniform within the wave
+        [&]<int... J>(std::integer_sequence<int, J...>) {
+            (([&] {
+                 vm_wait_le<3 * L>();  // slot J's round has landed; the other three may fly
+                 if (i0 + J < nr)
+                     B2mRound<DT, GS, FMT, R>::run(cp[J], sp[J], lut, slot, xsb[J], xo, acc);
+                 lds_wait_all();  // this wave's reads of slot J's buffer are done
+                 issue(std::integral_constant<int, J>{}, i0 + 4 + J);
+             })(),
+             ...);
+        }(std::make_integer_sequence<int, 4>{});
+    }
+    vm_wait_all();  // the spare slots' loads
+
+    // add the waves' partial sums (each wave's in its own part of buffer 0); lane (g, n)
+    // holds rows m = 4g + q of column n
+    f32x4* const red = reinterpret_cast<f32x4*>(xs0);
+    constexpr int kRedWave = kB2sXBytes / 16;
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[wave * kRedWave + r * 64 + lane] = acc[r];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int w2 = 1; w2 < kB2Waves; ++w2) {
+            const f32x4 o = red[w2 * kRedWave + r * 64 + lane];
+            acc[r][0] += o[0];
+            acc[r][1] += o[1];
+            acc[r][2] += o[2];
+            acc[r][3] += o[3];
+        }
+        const int64_t row = (tile * R + r) * 16 + i16;
+        if (row < N) {
+            const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = 4 * g + q;
+                if (m < M)
+                    store_from_f32<DT>(y, (int64_t)m * N + row,
+                                       acc[r][q] + bv + lora_term<DT>(lora, m, row));
+            }
+        }
+    }
+}
+
+
 // ------------------------------------------------------------------------- staged-tile GEMV
 //
 // Decode GEMV (M <= 4) for launches with few row tiles: the per-linear launches of a
@@ -2482,7 +2668,16 @@ static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const ui
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream, const LoraEp& lora) {
     const int64_t tiles = (N + 15) / 16;
-    if (tiles >= kB2mTwoTilesFrom)
+    if (M <= kB2sRows && OJX_B2S) {
+        if (tiles >= kB2mTwoTilesFrom)
+            hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 2>), dim3((unsigned)((tiles + 1) / 2)),
+                               dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N,
+                               K, lora);
+        else
+            hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 1>), dim3((unsigned)tiles),
+                               dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N,
+                               K, lora);
+    } else if (tiles >= kB2mTwoTilesFrom)
         hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 2>), dim3((unsigned)((tiles + 1) / 2)),
                            dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N, K,
                            lora);

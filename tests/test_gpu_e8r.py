@@ -182,6 +182,32 @@ def test_e8r_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
     assert _rel_err(y, ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (1, 16 * 37 + 5, 256, 32, torch.bfloat16),    # one round: three waves only load spares
+    (3, 16 * 37 + 5, 1280, 8, torch.float16),     # five rounds: one wave has two
+    (4, 16 * 37 + 5, 4096, 64, torch.bfloat16),   # four rounds per wave: all in flight
+    (2, 16 * 37 + 5, 5120, 16, torch.bfloat16),   # five rounds per wave: a second pass
+    (4, 16 * 600, 1024, 32, torch.bfloat16),      # two row tiles per workgroup
+    (1, 16 * 600 + 7, 2048, 8, torch.float16),    # ... ragged last tile
+])
+def test_e8r_gemv_m4_pipeline_matches_oracle(M, N, K, gs, dtype):
+    # M <= 4: the B-operand GEMV that stages activation rows 0..3 and keeps four rounds per
+    # wave in flight (spare slots past a wave's last round load nothing)
+    pk, sc, pk_np, sc_np = _layer1(N, K, seed=3 * N + K + gs, gs=gs)
+    g = torch.Generator().manual_seed(M * 13 + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"e8r gemv m4 M={M} N={N} K={K} gs={gs} {dtype}", flush=True)
+    y = ops.e8r_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, gs)
+    torch.cuda.synchronize()
+    ref = O.e8r_gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, gs,
+                         DT_CODE[dtype])
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel_err(y, ref) <= REL_TOL
+    for m in range(M):  # each activation row against its own scale
+        assert _rel_err(y[m:m + 1], ref[m:m + 1]) <= REL_TOL, m
+
+
 def test_e8r_prefill_large_shape_against_decoded_matmul():
     N, K, M, gs = 14336, 4096, 512, 32
     gw = torch.Generator(device=DEV).manual_seed(77)
