@@ -420,6 +420,103 @@ struct TernaryBwdDecoder {
     }
 };
 
+// Ternary backward dX with the step's code and scale bytes staged in LDS: the 64 weight rows
+// of a K step need 48 code bytes and 16 scale bytes each for the tile's 256 output columns
+// (4 KB), which every thread fetches as one 16-byte piece (threads t and t + 256 fetch the
+// same piece, so that every wave issues one load per step); the first 256 threads write
+// them into a three-step ring in LDS one step after the fetch.  A thread then reads the two
+// dwords that hold its row's 12-bit code and the 16-bit scale from LDS instead of issuing
+// twelve byte loads per step.  Step t is fetched during step t - 3 and written during step
+// t - 2, so its slot was read by the expansion of step t - 3, two barriers earlier.
+constexpr uint32_t kBwdStageBytes = 4096;  // 64 rows x (48 code + 16 scale) bytes
+
+// One 16-byte-per-lane buffer->LDS load (a wave's 1 KB) at `dst`.  (Not a template: the host
+// pass drops a kernel template that calls this builtin directly.)
+__device__ __forceinline__ void bwd_stage_dma(char* dst, __amdgpu_buffer_rsrc_t r, uint32_t vo,
+                                              int so) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                             vo, so, 0, 0);
+}
+#ifndef OJX_BWD_STAGED
+#define OJX_BWD_STAGED 1
+#endif
+
+template <int DT>
+struct TernaryBwdStagedDecoder {
+    static constexpr int kLoads = 1;
+    static constexpr bool kStaged = true;
+    uint32_t r[4][4];
+    uint32_t vo_piece, rowbytes, srowbytes;  // this thread's piece of a step (step 0)
+    bool scale_piece;                        // the piece holds scales (threads 192..255)
+    uint32_t rd_code, rd_shift, rd_scale;    // its own code's dwords and scale in a slot
+    bool writer;                             // tid < 256: writes its piece to the ring
+    u32x4 pend;                              // fetched piece of step `nl - 1`
+    int nl;                                  // next step to fetch (relative to the first)
+    int np;                                  // next step to expand
+    int64_t k_first;
+    char* ring;                              // three slots of kBwdStageBytes
+    const char* lut;
+    uint32_t slot;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    BwdBlock bk;
+    __device__ __forceinline__ u32x4 fetch(int t) const {
+        const int64_t n0 = k_first + (int64_t)t * kBK;
+        return scale_piece
+                   ? __builtin_amdgcn_raw_buffer_load_b128(sr, vo_piece,
+                                                           uniform_offset(n0 * srowbytes), 0)
+                   : __builtin_amdgcn_raw_buffer_load_b128(pr, vo_piece,
+                                                           uniform_offset(n0 * rowbytes), 0);
+    }
+    __device__ __forceinline__ void put(int t, const u32x4& v) const {
+        if (writer)
+            *reinterpret_cast<uint4*>(ring + (t % 3) * kBwdStageBytes + 16u * (threadIdx.x & 255u)) =
+                make_uint4(v.x, v.y, v.z, v.w);
+    }
+    // the first three steps, loaded straight into the ring by the writer waves (buffer->LDS;
+    // the caller waits for every load before its barrier)
+    __device__ __forceinline__ void init(int64_t k0) {
+        k_first = k0;
+        if (writer) {
+            for (int t = 0; t < 3; ++t) {
+                const int64_t n0 = k0 + (int64_t)t * kBK;
+                bwd_stage_dma(ring + t * kBwdStageBytes + 16u * ((threadIdx.x & 255u) & ~63u),
+                              scale_piece ? sr : pr, vo_piece,
+                              uniform_offset(n0 * (scale_piece ? srowbytes : rowbytes)));
+            }
+        }
+        nl = 3;
+        np = 0;
+    }
+    // write the piece fetched one step ago, fetch the next one
+    __device__ __forceinline__ void load(int64_t) {
+        if (nl > 3) put(nl - 1, pend);
+        pend = fetch(nl);
+        ++nl;
+    }
+    __device__ __forceinline__ void prep() {
+        const char* sl = ring + (np % 3) * kBwdStageBytes;
+        ++np;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t* cw = reinterpret_cast<const uint32_t*>(sl + 48u * q + rd_code);
+            const uint32_t code = __builtin_amdgcn_alignbit(cw[1], cw[0], rd_shift) & 0xFFFu;
+            const uint32_t s16 = *reinterpret_cast<const uint16_t*>(sl + 16u * q + rd_scale);
+            const uint32_t z = (code << kCodeShift) | slot;
+            const uint32_t h = __umulhi(z, kHiMagic);
+            const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
+            const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
+            const uint32_t sw = scale_word1<DT>(s16);
+            r[q][0] = ml.x & sw;
+            r[q][1] = ml.y & sw;
+            r[q][2] = mh.x & sw;
+            r[q][3] = mh.y & sw;
+        }
+    }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
+        bwd_store_cols(r, p, tile, bk);
+    }
+};
+
 template <int DT, int GS>
 struct Bit2BwdDecoder {
     static constexpr int kLoads = 8;
@@ -486,6 +583,12 @@ struct RootBwdDecoder {
         bwd_store_cols(r, p, tile, bk);
     }
 };
+
+// Decoders that stage their codes through an LDS ring (declare kStaged).
+template <typename D, typename = void>
+struct IsStaged : std::false_type {};
+template <typename D>
+struct IsStaged<D, std::void_t<decltype(D::kStaged)>> : std::bool_constant<D::kStaged> {};
 
 // One K step (64) of the wave's block.
 //   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read,
@@ -606,13 +709,36 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         kTernary, TernaryRowDecoder<DT>,
         std::conditional_t<FMT == kFmt2Bit, Bit2RowDecoder<DT, GS2>, RootRowDecoder<DT, GS2>>>;
     using BwdDec = std::conditional_t<
-        kTernary, TernaryBwdDecoder<DT>,
+        kTernary,
+        std::conditional_t<OJX_BWD_STAGED && C::BN == 256, TernaryBwdStagedDecoder<DT>,
+                           TernaryBwdDecoder<DT>>,
         std::conditional_t<FMT == kFmt2Bit, Bit2BwdDecoder<DT, GS2>, RootBwdDecoder<DT, GS2>>>;
     using Dec = std::conditional_t<BWD, BwdDec, FwdDec>;
+    constexpr bool kStagedDec = IsStaged<Dec>::value;
+    __shared__ __attribute__((aligned(16))) char dec_ring[kStagedDec ? 3 * kBwdStageBytes : 16];
     Dec dec;
     dec.pr = pr;
     dec.sr = sr;
-    if constexpr (BWD) {
+    if constexpr (kStagedDec) {
+        // block rows n and output columns k = n0 + bk.col .. + 7, as the unstaged decoder;
+        // the tile's 256 columns are codes 0..31 of a 48-byte run of each row
+        dec.bk = bwd_block(tid);
+        dec.rowbytes = rowbytes;
+        dec.srowbytes = srowbytes;
+        dec.lut = lut;
+        dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+        const uint32_t jj = dec.bk.col / 8u;
+        dec.rd_code = 48u * dec.bk.rows + 4u * ((12u * jj) >> 5);
+        dec.rd_shift = (12u * jj) & 31u;
+        dec.rd_scale = 3072u + 16u * dec.bk.rows + 2u * (jj >> 2);
+        const uint32_t t = (uint32_t)tid & 255u;
+        dec.scale_piece = t >= 192u;
+        dec.vo_piece = dec.scale_piece
+                           ? (t - 192u) * srowbytes + (uint32_t)n0 / 16u
+                           : (t / 3u) * rowbytes + (uint32_t)n0 * 3u / 16u + 16u * (t % 3u);
+        dec.writer = tid < 256;
+        dec.ring = dec_ring;
+    } else if constexpr (BWD) {
         // block rows n (per step) and output columns k = n0 + bk.col .. + 7 (n0 is the
         // tile's first output column here)
         dec.bk = bwd_block(tid);
@@ -663,8 +789,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     // ahead of the MFMAs.  Branch-free body: loads past the last step fetch bytes past the
     // operands (zeros, or the next row's data) into buffers that are never read.
     load_x_tile(xs[0], xr, m0, k_begin, R, wave, lane, C::XLOADS);
-    dec.load(k_begin);
-    __syncthreads();  // table ready
+    if constexpr (kStagedDec) {
+        dec.init(k_begin);
+        vm_wait_le<0>();  // the ring's first three steps have landed
+    } else {
+        dec.load(k_begin);
+    }
+    __syncthreads();  // table (and the staged decoder's first steps) ready
     dec.prep();
 #pragma unroll
     for (int p = 0; p < 4; ++p) dec.store(p, ws[0], wrow, half);
