@@ -420,15 +420,31 @@ struct TernaryBwdDecoder {
     }
 };
 
-// Ternary backward dX with the step's code and scale bytes staged in LDS: the 64 weight rows
-// of a K step need 48 code bytes and 16 scale bytes each for the tile's 256 output columns
-// (4 KB), which every thread fetches as one 16-byte piece (threads t and t + 256 fetch the
-// same piece, so that every wave issues one load per step); the first 256 threads write
-// them into a three-step ring in LDS one step after the fetch.  A thread then reads the two
-// dwords that hold its row's 12-bit code and the 16-bit scale from LDS instead of issuing
-// twelve byte loads per step.  Step t is fetched during step t - 3 and written during step
-// t - 2, so its slot was read by the expansion of step t - 3, two barriers earlier.
-constexpr uint32_t kBwdStageBytes = 4096;  // 64 rows x (48 code + 16 scale) bytes
+// Ternary backward dX with the step's code bytes (and at BN = 256 its scale bytes) staged in
+// LDS.  The 64 weight rows of a K step need BN * 3 / 16 code bytes and BN / 16 scale bytes
+// each for the tile's BN output columns, fetched as pieces of BN / 16 bytes: three code
+// pieces per row, then (BN = 256) one scale piece per row.  Each of the first 256 threads
+// fetches one piece per step (at BN = 256 threads t and t + 256 fetch the same piece, so that
+// every wave issues one load per step; at BN = 128 the fourth wave fetches nothing, from past
+// the buffer's end) and writes it into a ring of step slots in LDS one step after the fetch.
+// A thread then reads the two dwords that hold its row's 12-bit code (and its 16-bit scale)
+// from LDS instead of issuing twelve byte loads per step; at BN = 128 the scales stay four
+// 16-bit loads per thread (a staged scale slot would take the LDS that lets two workgroups
+// share a CU).  The loop step that computes step s expands step s + 1, writes step
+// s + kSlots and fetches step s + kSlots + 1, so a slot is rewritten one barrier after its
+// last expansion.  Three slots at BN = 256 (2-3% faster than two there), two at BN = 128
+// (the LDS of two workgroups per CU).
+template <int BN>
+struct BwdStage {
+    static constexpr bool kScales = BN == 256;          // scales staged as well
+    static constexpr uint32_t kCodeRow = BN * 3 / 16;   // code bytes per row and step
+    static constexpr uint32_t kScaleRow = BN / 16;      // scale bytes per row and step
+    static constexpr uint32_t kPiece = BN / 16;         // bytes per fetched piece
+    static constexpr uint32_t kBytes = 64 * (kCodeRow + (kScales ? kScaleRow : 0));
+    static constexpr int kSlots = BN == 256 ? 3 : 2;
+    static_assert(kCodeRow == 3 * kPiece, "three code pieces per row");
+};
+constexpr uint32_t kBwdOob = 0x80000000u;  // a buffer offset past every operand: loads zeros
 
 // One 16-byte-per-lane buffer->LDS load (a wave's 1 KB) at `dst`.  (Not a template: the host
 // pass drops a kernel template that calls this builtin directly.)
@@ -441,66 +457,91 @@ __device__ __forceinline__ void bwd_stage_dma(char* dst, __amdgpu_buffer_rsrc_t 
 #define OJX_BWD_STAGED 1
 #endif
 
-template <int DT>
+template <int DT, int BN>
 struct TernaryBwdStagedDecoder {
-    static constexpr int kLoads = 1;
+    using St = BwdStage<BN>;
+    static_assert(BN == 256 || BN == 128, "16- or 8-byte pieces");
+    static_assert(BN == 256 || St::kSlots == 2, "init fills two slots through registers");
+    static constexpr int kLoads = St::kScales ? 1 : 5;
     static constexpr bool kStaged = true;
+    using Piece = std::conditional_t<BN == 256, u32x4, u32x2>;
     uint32_t r[4][4];
     uint32_t vo_piece, rowbytes, srowbytes;  // this thread's piece of a step (step 0)
-    bool scale_piece;                        // the piece holds scales (threads 192..255)
+    bool scale_piece;                        // the piece holds scales (BN = 256, t >= 192)
     uint32_t rd_code, rd_shift, rd_scale;    // its own code's dwords and scale in a slot
-    bool writer;                             // tid < 256: writes its piece to the ring
-    u32x4 pend;                              // fetched piece of step `nl - 1`
+    bool writer;                             // writes its piece to the ring
+    Piece pend;                              // fetched piece of step `nl - 1`
+    uint32_t sc[4], vo_scale[4];             // BN = 128: the scales of the thread's rows
     int nl;                                  // next step to fetch (relative to the first)
     int np;                                  // next step to expand
     int64_t k_first;
-    char* ring;                              // three slots of kBwdStageBytes
+    char* ring;                              // St::kSlots slots of St::kBytes
     const char* lut;
     uint32_t slot;
     __amdgpu_buffer_rsrc_t pr, sr;
     BwdBlock bk;
-    __device__ __forceinline__ u32x4 fetch(int t) const {
+    __device__ __forceinline__ Piece fetch(int t) const {
         const int64_t n0 = k_first + (int64_t)t * kBK;
-        return scale_piece
-                   ? __builtin_amdgcn_raw_buffer_load_b128(sr, vo_piece,
-                                                           uniform_offset(n0 * srowbytes), 0)
-                   : __builtin_amdgcn_raw_buffer_load_b128(pr, vo_piece,
-                                                           uniform_offset(n0 * rowbytes), 0);
+        const __amdgpu_buffer_rsrc_t rs = scale_piece ? sr : pr;
+        const int so = uniform_offset(n0 * (scale_piece ? srowbytes : rowbytes));
+        if constexpr (BN == 256) return __builtin_amdgcn_raw_buffer_load_b128(rs, vo_piece, so, 0);
+        else return __builtin_amdgcn_raw_buffer_load_b64(rs, vo_piece, so, 0);
     }
-    __device__ __forceinline__ void put(int t, const u32x4& v) const {
-        if (writer)
-            *reinterpret_cast<uint4*>(ring + (t % 3) * kBwdStageBytes + 16u * (threadIdx.x & 255u)) =
-                make_uint4(v.x, v.y, v.z, v.w);
+    __device__ __forceinline__ void load_scales(int64_t n0) {
+        if constexpr (!St::kScales) {
+            const int ss = uniform_offset(n0 * srowbytes);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
+        }
     }
-    // the first three steps, loaded straight into the ring by the writer waves (buffer->LDS;
-    // the caller waits for every load before its barrier)
+    __device__ __forceinline__ void put(int t, const Piece& v) const {
+        char* dst = ring + (t % St::kSlots) * St::kBytes + St::kPiece * (threadIdx.x & 255u);
+        if (writer) {
+            if constexpr (BN == 256) *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
+            else *reinterpret_cast<uint2*>(dst) = make_uint2(v[0], v[1]);
+        }
+    }
+    // the ring's first steps: BN = 256 loads them straight into the ring (buffer->LDS, 16
+    // bytes per lane), BN = 128 through registers.  The caller waits for every load before
+    // its barrier.
     __device__ __forceinline__ void init(int64_t k0) {
         k_first = k0;
-        if (writer) {
-            for (int t = 0; t < 3; ++t) {
-                const int64_t n0 = k0 + (int64_t)t * kBK;
-                bwd_stage_dma(ring + t * kBwdStageBytes + 16u * ((threadIdx.x & 255u) & ~63u),
-                              scale_piece ? sr : pr, vo_piece,
-                              uniform_offset(n0 * (scale_piece ? srowbytes : rowbytes)));
+        if constexpr (BN == 256) {
+            if (writer) {
+                for (int t = 0; t < St::kSlots; ++t) {
+                    const int64_t n0 = k0 + (int64_t)t * kBK;
+                    bwd_stage_dma(ring + t * St::kBytes + 16u * ((threadIdx.x & 255u) & ~63u),
+                                  scale_piece ? sr : pr, vo_piece,
+                                  uniform_offset(n0 * (scale_piece ? srowbytes : rowbytes)));
+                }
             }
+        } else {
+            const Piece v0 = fetch(0), v1 = fetch(1);
+            load_scales(k0);
+            put(0, v0);
+            put(1, v1);
         }
-        nl = 3;
+        nl = St::kSlots;
         np = 0;
     }
-    // write the piece fetched one step ago, fetch the next one
-    __device__ __forceinline__ void load(int64_t) {
-        if (nl > 3) put(nl - 1, pend);
+    // write the piece fetched one step ago, fetch the next one (and the scales of step n0)
+    __device__ __forceinline__ void load(int64_t n0) {
+        if (nl > St::kSlots) put(nl - 1, pend);
         pend = fetch(nl);
         ++nl;
+        load_scales(n0);
     }
     __device__ __forceinline__ void prep() {
-        const char* sl = ring + (np % 3) * kBwdStageBytes;
+        const char* sl = ring + (np % St::kSlots) * St::kBytes;
         ++np;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint32_t* cw = reinterpret_cast<const uint32_t*>(sl + 48u * q + rd_code);
+            const uint32_t* cw = reinterpret_cast<const uint32_t*>(sl + St::kCodeRow * q + rd_code);
             const uint32_t code = __builtin_amdgcn_alignbit(cw[1], cw[0], rd_shift) & 0xFFFu;
-            const uint32_t s16 = *reinterpret_cast<const uint16_t*>(sl + 16u * q + rd_scale);
+            const uint32_t s16 =
+                St::kScales ? *reinterpret_cast<const uint16_t*>(sl + St::kScaleRow * q + rd_scale)
+                            : sc[q];
             const uint32_t z = (code << kCodeShift) | slot;
             const uint32_t h = __umulhi(z, kHiMagic);
             const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
@@ -710,33 +751,38 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         std::conditional_t<FMT == kFmt2Bit, Bit2RowDecoder<DT, GS2>, RootRowDecoder<DT, GS2>>>;
     using BwdDec = std::conditional_t<
         kTernary,
-        std::conditional_t<OJX_BWD_STAGED && C::BN == 256, TernaryBwdStagedDecoder<DT>,
+        std::conditional_t<OJX_BWD_STAGED != 0, TernaryBwdStagedDecoder<DT, C::BN>,
                            TernaryBwdDecoder<DT>>,
         std::conditional_t<FMT == kFmt2Bit, Bit2BwdDecoder<DT, GS2>, RootBwdDecoder<DT, GS2>>>;
     using Dec = std::conditional_t<BWD, BwdDec, FwdDec>;
     constexpr bool kStagedDec = IsStaged<Dec>::value;
-    __shared__ __attribute__((aligned(16))) char dec_ring[kStagedDec ? 3 * kBwdStageBytes : 16];
+    // (+16: the dword after a BN = 128 slot's last code row, which its last codes' reads touch)
+    __shared__ __attribute__((aligned(16)))
+    char dec_ring[kStagedDec ? BwdStage<C::BN>::kSlots * BwdStage<C::BN>::kBytes + 16 : 16];
     Dec dec;
     dec.pr = pr;
     dec.sr = sr;
     if constexpr (kStagedDec) {
         // block rows n and output columns k = n0 + bk.col .. + 7, as the unstaged decoder;
-        // the tile's 256 columns are codes 0..31 of a 48-byte run of each row
+        // the tile's BN columns are codes 0 .. BN / 8 - 1 of a run of each row
+        using St = BwdStage<C::BN>;
         dec.bk = bwd_block(tid);
         dec.rowbytes = rowbytes;
         dec.srowbytes = srowbytes;
         dec.lut = lut;
         dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
         const uint32_t jj = dec.bk.col / 8u;
-        dec.rd_code = 48u * dec.bk.rows + 4u * ((12u * jj) >> 5);
+        dec.rd_code = St::kCodeRow * dec.bk.rows + 4u * ((12u * jj) >> 5);
         dec.rd_shift = (12u * jj) & 31u;
-        dec.rd_scale = 3072u + 16u * dec.bk.rows + 2u * (jj >> 2);
+        dec.rd_scale = 64u * St::kCodeRow + St::kScaleRow * dec.bk.rows + 2u * (jj >> 2);
         const uint32_t t = (uint32_t)tid & 255u;
-        dec.scale_piece = t >= 192u;
-        dec.vo_piece = dec.scale_piece
-                           ? (t - 192u) * srowbytes + (uint32_t)n0 / 16u
-                           : (t / 3u) * rowbytes + (uint32_t)n0 * 3u / 16u + 16u * (t % 3u);
-        dec.writer = tid < 256;
+        dec.scale_piece = St::kScales && t >= 192u;
+        dec.vo_piece = t >= 192u ? (St::kScales ? (t - 192u) * srowbytes + (uint32_t)n0 / 16u : kBwdOob)
+                                 : (t / 3u) * rowbytes + (uint32_t)n0 * 3u / 16u + St::kPiece * (t % 3u);
+        dec.writer = St::kScales ? tid < 256 : t < 192u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dec.vo_scale[q] = (dec.bk.rows + (uint32_t)q) * srowbytes + 2u * (((uint32_t)n0 + dec.bk.col) / 32u);
         dec.ring = dec_ring;
     } else if constexpr (BWD) {
         // block rows n (per step) and output columns k = n0 + bk.col .. + 7 (n0 is the
@@ -947,13 +993,14 @@ static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_
 //    keeps at least kMinLargeSplitSteps K steps and the split grid still covers three
 //    quarters of the CUs;
 //  * otherwise small tiles, split over K towards two workgroups per CU (the small
-//    configuration's residency), at least kMinSplitSteps K steps per split.
+//    configuration's residency), at least kMinSplitSteps K steps per split (8: at 4 the
+//    fp32 partials of the k/v shape at M = 512 cost more than the extra workgroups gain).
 // The fp32 partial sums of a split stay under kSplitBytesMax.
 #ifndef OJX_SPLIT_TARGET_WGS
 #define OJX_SPLIT_TARGET_WGS 512
 #endif
 constexpr int kMaxSplits = 16;
-constexpr int64_t kMinSplitSteps = 4;
+constexpr int64_t kMinSplitSteps = 8;
 constexpr int64_t kMinLargeSplitSteps = 16;
 constexpr int64_t kSplitBytesMax = 256ll << 20;
 constexpr int64_t kLargeTargetWgs = 256;

@@ -21,6 +21,7 @@ namespace ojx {
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 typedef __attribute__((ext_vector_type(3))) uint32_t u32x3;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 

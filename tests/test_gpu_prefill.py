@@ -92,10 +92,10 @@ def test_prefill_unaligned_input_falls_back():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M,N,K", [(201, 301, 1344), (40, 1024, 4096), (129, 640, 2048)])
+@pytest.mark.parametrize("M,N,K", [(201, 301, 1344), (40, 1024, 8192), (129, 640, 2048)])
 def test_prefill_k_split_uneven_steps_and_ragged_tail(dtype, M, N, K):
-    # small grids run split over K: 21 K steps over 5 splits (uneven), up to 16 splits, and
-    # M*N not a multiple of 4 (the reduction's scalar tail)
+    # small grids run split over K: 21 K steps over 2 splits (uneven), 128 steps over the
+    # maximum of 16 splits, and M*N not a multiple of 4 (the reduction's scalar tail)
     pk, sc, pk_np, sc_np = _encoded(N, K, seed=M * 3 + N + K)
     g = torch.Generator().manual_seed(M + K)
     x = torch.randn(M, K, generator=g).to(dtype)
