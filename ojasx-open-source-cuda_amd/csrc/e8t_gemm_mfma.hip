@@ -480,6 +480,31 @@ struct TernaryBwdStagedDecoder {
     uint32_t slot;
     __amdgpu_buffer_rsrc_t pr, sr;
     BwdBlock bk;
+    // (+16: the dword after a BN = 128 slot's last code row, which its last codes' reads touch)
+    static constexpr uint32_t kRingBytes = St::kSlots * St::kBytes + 16;
+    // block rows n and output columns k = n0 + bk.col .. + 7, as the unstaged decoder; the
+    // tile's BN columns are codes 0 .. BN / 8 - 1 of a run of each row
+    __device__ __forceinline__ void setup(int tid, int lane, int64_t n0, uint32_t rb, uint32_t srb,
+                                          const char* table, char* ring_lds) {
+        bk = bwd_block(tid);
+        rowbytes = rb;
+        srowbytes = srb;
+        lut = table;
+        slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
+        const uint32_t jj = bk.col / 8u;
+        rd_code = St::kCodeRow * bk.rows + 4u * ((12u * jj) >> 5);
+        rd_shift = (12u * jj) & 31u;
+        rd_scale = 64u * St::kCodeRow + St::kScaleRow * bk.rows + 2u * (jj >> 2);
+        const uint32_t t = (uint32_t)tid & 255u;
+        scale_piece = St::kScales && t >= 192u;
+        vo_piece = t >= 192u ? (St::kScales ? (t - 192u) * srb + (uint32_t)n0 / 16u : kBwdOob)
+                             : (t / 3u) * rb + (uint32_t)n0 * 3u / 16u + St::kPiece * (t % 3u);
+        writer = St::kScales ? tid < 256 : t < 192u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            vo_scale[q] = (bk.rows + (uint32_t)q) * srb + 2u * (((uint32_t)n0 + bk.col) / 32u);
+        ring = ring_lds;
+    }
     __device__ __forceinline__ Piece fetch(int t) const {
         const int64_t n0 = k_first + (int64_t)t * kBK;
         const __amdgpu_buffer_rsrc_t rs = scale_piece ? sr : pr;
@@ -625,11 +650,150 @@ struct RootBwdDecoder {
     }
 };
 
+// B bytes (1, 2, 4, 8 or 16) from a buffer, in the low bytes of four dwords, and back to LDS.
+template <int B>
+__device__ __forceinline__ u32x4 piece_load(__amdgpu_buffer_rsrc_t r, uint32_t vo, int so) {
+    static_assert(B == 1 || B == 2 || B == 4 || B == 8 || B == 16, "piece size");
+    if constexpr (B == 16) {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+    } else if constexpr (B == 8) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+        return u32x4{v[0], v[1], 0u, 0u};
+    } else if constexpr (B == 4) {
+        return u32x4{__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0), 0u, 0u, 0u};
+    } else if constexpr (B == 2) {
+        return u32x4{(uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0), 0u, 0u, 0u};
+    } else {
+        return u32x4{(uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, vo, so, 0), 0u, 0u, 0u};
+    }
+}
+template <int B>
+__device__ __forceinline__ void piece_store(char* dst, const u32x4& v) {
+    if constexpr (B == 16) *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
+    if constexpr (B == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(v[0], v[1]);
+    if constexpr (B == 4) *reinterpret_cast<uint32_t*>(dst) = v[0];
+    if constexpr (B == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)v[0];
+    if constexpr (B == 1) *reinterpret_cast<uint8_t*>(dst) = (uint8_t)v[0];
+}
+
+// 2-bit and 1-bit backward dX with the step's code and scale bytes staged in LDS, as the
+// ternary staged decoder: the 64 weight rows of a K step need BN / 4 (2-bit) or BN / 8
+// (1-bit) code bytes and 2 BN / GS scale bytes each for the tile's BN output columns; four
+// threads share a row, each fetching a quarter of its codes and a quarter of its scales (one
+// load of each per step; at BN = 256 threads t and t + 256 fetch the same pieces).  The
+// pieces go into a two-slot ring one step after the fetch; each thread then reads its four
+// rows' code bytes (two for 2-bit, one for 1-bit) and scales from LDS instead of issuing
+// eight loads per step.
+template <int DT, int BN, int FMT, int GS>
+struct LowbitBwdStagedDecoder {
+    static constexpr bool kTwoBit = FMT == kFmt2Bit;
+    static constexpr uint32_t kCodeRow = kTwoBit ? BN / 4 : BN / 8;  // code bytes per row, step
+    static constexpr uint32_t kScaleRow = 2 * BN / GS;               // scale bytes per row, step
+    static constexpr int kCP = (int)kCodeRow / 4, kSP = (int)kScaleRow / 4;  // bytes per thread
+    static constexpr uint32_t kCodeBytes = 64 * kCodeRow;
+    static constexpr uint32_t kBytes = 64 * (kCodeRow + kScaleRow);
+    static constexpr int kSlots = 2;
+    static constexpr uint32_t kRingBytes = kSlots * kBytes;
+    static constexpr int kLoads = 2;
+    static constexpr bool kStaged = true;
+    static_assert(kCP >= 4 && kCP <= 16 && kSP >= 1 && kSP <= 16, "piece sizes");
+    uint32_t r[4][4];
+    uint32_t vo_code, vo_scale, rowbytes, srowbytes;  // this thread's pieces of step 0
+    uint32_t rd_code, rd_scale;                       // its rows' code and scale bytes in a slot
+    bool writer;
+    u32x4 pc, ps;                                     // fetched pieces of step `nl - 1`
+    int nl, np;
+    int64_t k_first;
+    char* ring;
+    const char* tab;
+    __amdgpu_buffer_rsrc_t pr, sr;
+    BwdBlock bk;
+    __device__ __forceinline__ void setup(int tid, int, int64_t n0, uint32_t rb, uint32_t srb,
+                                          const char* table, char* ring_lds) {
+        bk = bwd_block(tid);
+        rowbytes = rb;
+        srowbytes = srb;
+        tab = table;
+        const uint32_t t = (uint32_t)tid & 255u;
+        vo_code = (t / 4u) * rb + (uint32_t)n0 / (kTwoBit ? 4u : 8u) + (uint32_t)kCP * (t % 4u);
+        vo_scale = (t / 4u) * srb + 2u * ((uint32_t)n0 / GS) + (uint32_t)kSP * (t % 4u);
+        rd_code = kCodeRow * bk.rows + bk.col / (kTwoBit ? 4u : 8u);
+        rd_scale = kCodeBytes + kScaleRow * bk.rows + 2u * (bk.col / GS);
+        writer = tid < 256;
+        ring = ring_lds;
+    }
+    __device__ __forceinline__ void fetch(int t, u32x4& c, u32x4& sv) const {
+        const int64_t n0 = k_first + (int64_t)t * kBK;
+        c = piece_load<kCP>(pr, vo_code, uniform_offset(n0 * rowbytes));
+        sv = piece_load<kSP>(sr, vo_scale, uniform_offset(n0 * srowbytes));
+    }
+    __device__ __forceinline__ void put(int t, const u32x4& c, const u32x4& sv) const {
+        char* sl = ring + (t % kSlots) * kBytes;
+        const uint32_t i = threadIdx.x & 255u;
+        if (writer) {
+            piece_store<kCP>(sl + (uint32_t)kCP * i, c);
+            piece_store<kSP>(sl + kCodeBytes + (uint32_t)kSP * i, sv);
+        }
+    }
+    __device__ __forceinline__ void init(int64_t k0) {
+        k_first = k0;
+        u32x4 c0, s0, c1, s1;
+        fetch(0, c0, s0);
+        fetch(1, c1, s1);
+        put(0, c0, s0);
+        put(1, c1, s1);
+        nl = kSlots;
+        np = 0;
+    }
+    __device__ __forceinline__ void load(int64_t) {
+        if (nl > kSlots) put(nl - 1, pc, ps);
+        fetch(nl, pc, ps);
+        ++nl;
+    }
+    __device__ __forceinline__ void prep() {
+        const char* sl = ring + (np % kSlots) * kBytes;
+        ++np;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t s16 = *reinterpret_cast<const uint16_t*>(sl + rd_scale + kScaleRow * q);
+            if constexpr (kTwoBit) {
+                const uint32_t cw = *reinterpret_cast<const uint16_t*>(sl + rd_code + kCodeRow * q);
+                const uint2 v = values2<DT>(s16);
+                const uint2 a = *reinterpret_cast<const uint2*>(tab + 8u * (cw & 0xFFu));
+                const uint2 b = *reinterpret_cast<const uint2*>(tab + 8u * (cw >> 8));
+                r[q][0] = __builtin_amdgcn_perm(v.x, v.y, a.x);
+                r[q][1] = __builtin_amdgcn_perm(v.x, v.y, a.y);
+                r[q][2] = __builtin_amdgcn_perm(v.x, v.y, b.x);
+                r[q][3] = __builtin_amdgcn_perm(v.x, v.y, b.y);
+            } else {
+                const uint32_t cd = *reinterpret_cast<const uint8_t*>(sl + rd_code + kCodeRow * q);
+                const uint2 v = values1<DT>(s16);
+                const uint4 e = *reinterpret_cast<const uint4*>(tab + 16u * cd);
+                r[q][0] = __builtin_amdgcn_perm(v.x, v.y, e.x);
+                r[q][1] = __builtin_amdgcn_perm(v.x, v.y, e.y);
+                r[q][2] = __builtin_amdgcn_perm(v.x, v.y, e.z);
+                r[q][3] = __builtin_amdgcn_perm(v.x, v.y, e.w);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
+        bwd_store_cols(r, p, tile, bk);
+    }
+};
+#ifndef OJX_BWD_STAGED_LOWBIT
+#define OJX_BWD_STAGED_LOWBIT 1
+#endif
+
 // Decoders that stage their codes through an LDS ring (declare kStaged).
 template <typename D, typename = void>
 struct IsStaged : std::false_type {};
 template <typename D>
 struct IsStaged<D, std::void_t<decltype(D::kStaged)>> : std::bool_constant<D::kStaged> {};
+template <typename D, typename = void>
+struct RingBytes : std::integral_constant<uint32_t, 16> {};
+template <typename D>
+struct RingBytes<D, std::void_t<decltype(D::kRingBytes)>>
+    : std::integral_constant<uint32_t, D::kRingBytes> {};
 
 // One K step (64) of the wave's block.
 //   1. sub-step 0 on fragments already in registers (a0/b0) while sub-step 1's are read,
@@ -753,37 +917,17 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         kTernary,
         std::conditional_t<OJX_BWD_STAGED != 0, TernaryBwdStagedDecoder<DT, C::BN>,
                            TernaryBwdDecoder<DT>>,
-        std::conditional_t<FMT == kFmt2Bit, Bit2BwdDecoder<DT, GS2>, RootBwdDecoder<DT, GS2>>>;
+        std::conditional_t<
+            OJX_BWD_STAGED_LOWBIT != 0, LowbitBwdStagedDecoder<DT, C::BN, FMT, GS2>,
+            std::conditional_t<FMT == kFmt2Bit, Bit2BwdDecoder<DT, GS2>, RootBwdDecoder<DT, GS2>>>>;
     using Dec = std::conditional_t<BWD, BwdDec, FwdDec>;
     constexpr bool kStagedDec = IsStaged<Dec>::value;
-    // (+16: the dword after a BN = 128 slot's last code row, which its last codes' reads touch)
-    __shared__ __attribute__((aligned(16)))
-    char dec_ring[kStagedDec ? BwdStage<C::BN>::kSlots * BwdStage<C::BN>::kBytes + 16 : 16];
+    __shared__ __attribute__((aligned(16))) char dec_ring[RingBytes<Dec>::value];
     Dec dec;
     dec.pr = pr;
     dec.sr = sr;
     if constexpr (kStagedDec) {
-        // block rows n and output columns k = n0 + bk.col .. + 7, as the unstaged decoder;
-        // the tile's BN columns are codes 0 .. BN / 8 - 1 of a run of each row
-        using St = BwdStage<C::BN>;
-        dec.bk = bwd_block(tid);
-        dec.rowbytes = rowbytes;
-        dec.srowbytes = srowbytes;
-        dec.lut = lut;
-        dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
-        const uint32_t jj = dec.bk.col / 8u;
-        dec.rd_code = St::kCodeRow * dec.bk.rows + 4u * ((12u * jj) >> 5);
-        dec.rd_shift = (12u * jj) & 31u;
-        dec.rd_scale = 64u * St::kCodeRow + St::kScaleRow * dec.bk.rows + 2u * (jj >> 2);
-        const uint32_t t = (uint32_t)tid & 255u;
-        dec.scale_piece = St::kScales && t >= 192u;
-        dec.vo_piece = t >= 192u ? (St::kScales ? (t - 192u) * srowbytes + (uint32_t)n0 / 16u : kBwdOob)
-                                 : (t / 3u) * rowbytes + (uint32_t)n0 * 3u / 16u + St::kPiece * (t % 3u);
-        dec.writer = St::kScales ? tid < 256 : t < 192u;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            dec.vo_scale[q] = (dec.bk.rows + (uint32_t)q) * srowbytes + 2u * (((uint32_t)n0 + dec.bk.col) / 32u);
-        dec.ring = dec_ring;
+        dec.setup(tid, lane, n0, rowbytes, srowbytes, lut, dec_ring);
     } else if constexpr (BWD) {
         // block rows n (per step) and output columns k = n0 + bk.col .. + 7 (n0 is the
         // tile's first output column here)

@@ -101,6 +101,34 @@ def test_bwd_llama8b_shapes_every_element(fmt, M, name, N, K):
     assert ((gx.float() - ref).abs().max() / ref.abs().max()).item() <= REL_TOL
 
 
+@pytest.mark.parametrize("fmt", ["2bit", "1bit"])
+@pytest.mark.parametrize("gs", [8, 16, 32, 64])
+@pytest.mark.parametrize("M,N,K", [(2000, 320, 6208), (512, 1024, 4096)])
+def test_lowbit_bwd_every_group_size_both_tiles(fmt, gs, M, N, K):
+    # (2000, 320, 6208): 8 x 25 large tiles, unsplit, ragged rows and a last column tile
+    # with 64 of its 256 output columns; (512, 1024, 4096): small tiles split over N.  Every
+    # element against an fp32 matmul of the bit-exact decoded weights.
+    gw = torch.Generator(device=DEV).manual_seed(5200 + gs + M)
+    w = torch.randn(N, K, generator=gw, device=DEV) * 0.02
+    dtype = torch.bfloat16 if gs in (8, 32) else torch.float16
+    if fmt == "2bit":
+        pk, sc = ops.encode2(w, gs)
+        wdq = ops.decode2(pk, sc, N * K, gs, dtype)
+        bwd = lambda gy: ops.e8_linear_bwd_dx(gy, pk, sc, N, K, gs)
+    else:
+        pk, sc = ops.encode1(w, gs)
+        wdq = ops.decode1(pk, sc, N * K, gs, dtype)
+        bwd = lambda gy: ops.e8r_linear_bwd_dx(gy, pk, sc, N, K, gs)
+    del w
+    gy = torch.randn(M, N, generator=gw, device=DEV).to(dtype)
+    print(f"bwd {fmt} gs={gs} M={M} N={N} K={K}", flush=True)
+    gx = bwd(gy)
+    ref = gy.float() @ wdq.view(N, K).float()
+    torch.cuda.synchronize()
+    assert gx.shape == (M, K) and torch.isfinite(gx).all()
+    assert ((gx.float() - ref).abs().max() / ref.abs().max()).item() <= REL_TOL
+
+
 def test_bwd_graph_capture_matches_eager():
     # the captured launch keeps its K split (caller-owned workspace from the graph's pool):
     # every replay, with eager split work in between, is bit-identical to the eager result
