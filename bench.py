@@ -29,8 +29,9 @@ roofline= HBM-bound: ALGORITHMIC bytes of the grouped GEMV launches in the timed
 Also reported (not the headline): prefill GEMM TFLOP/s on the four shapes at
 M in {512, 2048, 8192} and the backward dX of the same layers, encoder
 throughput on one layer of fp16
-weights with 0.1% +-8 sigma outliers, the 2-bit E8 format (encoder, decode
-GEMV and prefill per linear on an 8-layer stack), and the CPU baseline: this
+weights with 0.1% +-8 sigma outliers, the 2-bit E8 and 1-bit Root E8 formats
+(encoder, decode GEMV, prefill and backward dX per linear on an 8-layer stack), and the CPU
+baseline: this
 repo's torch restatement of the reference's portable decode-then-matmul path
 (configs[0]) timed on the host cores.
 """
@@ -487,10 +488,10 @@ def e8b_weight_bytes(N: int, K: int, gs: int = E8B_GS, per_byte: int = 4) -> int
 # Low-bit formats of the leg below: C entry points, weights per code byte, CPU oracle encoder,
 # GPU decoder (ops) name.
 LOWBIT = {
-    "2bit": dict(encode="ojx_e8_encode", gemm="ojx_e8_gemm_fwd", per_byte=4,
-                 oracle="e8b_encode", decode="decode2"),
-    "root": dict(encode="ojx_e8r_encode", gemm="ojx_e8r_gemm_fwd", per_byte=8,
-                 oracle="e8r_encode", decode="decode1"),
+    "2bit": dict(encode="ojx_e8_encode", gemm="ojx_e8_gemm_fwd", bwd="ojx_e8_gemm_bwd_dx",
+                 per_byte=4, oracle="e8b_encode", decode="decode2"),
+    "root": dict(encode="ojx_e8r_encode", gemm="ojx_e8r_gemm_fwd", bwd="ojx_e8r_gemm_bwd_dx",
+                 per_byte=8, oracle="e8r_encode", decode="decode1"),
 }
 
 
@@ -504,7 +505,8 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     `check_rows` rows.  Decode: one ojx_e8_gemm_fwd launch per linear at each M, replayed
     from a hipGraph (the prefill launches with a caller-owned K-split workspace); outputs of
     layer 0 checked against an fp32 matmul of the decoded weights.
-    Prefill: the same at M = `prefill_m`."""
+    Prefill: the same at M = `prefill_m`; backward: the backward dX launches (grad_x[M, K] =
+    grad_y[M, N] . W) of the stack at M = `prefill_m`, checked the same way."""
     import numpy as np
 
     from oracle import oracle as O
@@ -512,6 +514,7 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     lib = N_.lib()
     F = LOWBIT[fmt]
     enc_fn, gemm_fn, per_byte = getattr(lib, F["encode"]), getattr(lib, F["gemm"]), F["per_byte"]
+    bwd_fn = getattr(lib, F["bwd"])
     items = []
     for layer in range(layers):
         for j, (name, N, K) in enumerate(LAYER_SHAPES):
@@ -560,23 +563,31 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
         del it["w"]
     torch.cuda.empty_cache()
 
-    def gemm_leg(M):
-        xs = {K: torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(9800 + M + K),
-                             device=dev).to(torch.bfloat16) for K in (4096, 14336)}
-        ys = [torch.empty(M, it["N"], dtype=torch.bfloat16, device=dev) for it in items]
+    def gemm_leg(M, bwd=False):
+        # forward: x[M, K] -> y[M, N]; backward dX: grad_y[M, N] -> grad_x[M, K]
+        xin = (lambda it: it["N"]) if bwd else (lambda it: it["K"])
+        xout = (lambda it: it["K"]) if bwd else (lambda it: it["N"])
+        xs = {n: torch.randn(M, n, generator=torch.Generator(device=dev).manual_seed(9800 + M + n),
+                             device=dev).to(torch.bfloat16) for n in {xin(it) for it in items[:7]}}
+        ys = [torch.empty(M, xout(it), dtype=torch.bfloat16, device=dev) for it in items]
         # one workspace, as large as the largest launch needs, shared by the stream's launches
         from ojasx_amd import ops as ops_
         fmt_code = ops_.FMT_E8 if fmt == "2bit" else ops_.FMT_ROOT
-        wss = [ops_.workspace(fmt_code, False, M, it["N"], it["K"], E8B_GS, torch.bfloat16, dev)
+        wss = [ops_.workspace(fmt_code, bwd, M, it["N"], it["K"], E8B_GS, torch.bfloat16, dev)
                for it in items[:7]]
         ws = max((w for w in wss if w is not None), key=lambda w: w.numel(), default=None)
         ws_p, ws_n = (0, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
         def launch_all(h):
             for it, y in zip(items, ys):
-                N_.check(gemm_fn(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
-                                 it["scales"].data_ptr(), None, y.data_ptr(), M, it["N"], it["K"],
-                                 E8B_GS, N_.BF16, ws_p, ws_n, h), "gemm")
+                if bwd:
+                    N_.check(bwd_fn(xs[it["N"]].data_ptr(), it["packed"].data_ptr(),
+                                    it["scales"].data_ptr(), y.data_ptr(), M, it["N"], it["K"],
+                                    E8B_GS, N_.BF16, ws_p, ws_n, h), "gemm_bwd_dx")
+                else:
+                    N_.check(gemm_fn(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
+                                     it["scales"].data_ptr(), None, y.data_ptr(), M, it["N"],
+                                     it["K"], E8B_GS, N_.BF16, ws_p, ws_n, h), "gemm")
 
         ms = replay_ms(launch_all, steps)
         worst = 0.0
@@ -585,7 +596,7 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
             it = items[idx]
             wd = getattr(ops, F["decode"])(it["packed"], it["scales"], it["N"] * it["K"], E8B_GS,
                                            torch.bfloat16).view(it["N"], it["K"]).float()
-            ref = xs[it["K"]].float() @ wd.t().contiguous()
+            ref = (xs[it["N"]].float() @ wd) if bwd else (xs[it["K"]].float() @ wd.t().contiguous())
             err = (ys[idx].float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
             worst = max(worst, err)
         return ms, worst
@@ -602,6 +613,10 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
     flops = 2.0 * prefill_m * numel
     prefill = dict(M=prefill_m, ms=round(ms, 3), TFLOPs=round(flops / ms / 1e9, 1),
                    frac_mfma=round(flops / ms / 1e9 / BF16_MFMA_PEAK_TFLOPS, 4))
+    ms, err = gemm_leg(prefill_m, bwd=True)
+    worst = max(worst, err)
+    backward = dict(M=prefill_m, ms=round(ms, 3), TFLOPs=round(flops / ms / 1e9, 1),
+                    frac_mfma=round(flops / ms / 1e9 / BF16_MFMA_PEAK_TFLOPS, 4))
     del items
     torch.cuda.empty_cache()
     return dict(layers=layers, linears=7 * layers, group_size=E8B_GS, weights=numel,
@@ -610,7 +625,8 @@ def bench_e8b(torch, N_, dev, layers: int, steps: int, Ms=(1, 4, 16), prefill_m:
                             bit_exact_sample=exact,
                             sample=f"first {check_rows} rows of layer 0 of each shape vs "
                                    "oracle/e8t_oracle.c"),
-                decode_per_linear=decode, prefill_per_linear=prefill, max_rel_err=worst)
+                decode_per_linear=decode, prefill_per_linear=prefill,
+                backward_dx_per_linear=backward, max_rel_err=worst)
 
 
 # --------------------------------------------------------------------------- end-to-end decoder
