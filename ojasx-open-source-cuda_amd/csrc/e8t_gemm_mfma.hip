@@ -1050,7 +1050,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         const int64_t kx = (s + 1) * kBK;
         // forward: the step's MFMA sections run at raised wave priority, so that of the two
         // waves on a SIMD the one with MFMAs to issue goes first while the other waits on
-        // LDS (+2.8% on the prefill cases; the backward dX measured -0.7% and keeps priority 0)
+        // LDS (+2.8% on the prefill cases; the backward dX measured -0.7% with per-thread weight
+        // loads and +-0 with its staged rings, and keeps priority 0)
         if constexpr (!BWD) __builtin_amdgcn_s_setprio(1);
         kstep<DT, kTM, kTN>(xs[cur], ws[cur], fl, a0, b0, a1, b1, dec, ws[nxt], wrow, half,
                             acc, (s + 2) * kBK,
