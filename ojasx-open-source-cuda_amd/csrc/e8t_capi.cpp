@@ -88,7 +88,7 @@ static hipError_t launch_mfma(const void* x, const uint8_t* packed, const uint16
                               int64_t gs, int dtype, hipStream_t s, int fmt, bool bwd,
                               void* ws, size_t ws_bytes, const ojx::LoraEp& lora = ojx::LoraEp{}) {
     const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
-    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, out_cols, red);
+    ojx::GemmChoice c = ojx::gemm_mfma_choice(M, out_cols, red, bwd);
     const size_t per = (size_t)ojx::split_stride(M, out_cols) * sizeof(float);
     const int64_t fit = ws ? (int64_t)(ws_bytes / per) : 0;
     if (c.splits > fit) c.splits = fit < 2 ? 1 : (int)fit;
@@ -307,7 +307,8 @@ static int workspace_bytes(int fmt, int bwd, int64_t M, int64_t N, int64_t K, in
                         : route_fwd(fmt, nullptr, nullptr, nullptr, nullptr, M, N, K, gs, dtype);
     if (r == kRouteMfma) {
         const int64_t out_cols = bwd ? K : N, red = bwd ? N : K;
-        *bytes = ojx::gemm_split_bytes(ojx::gemm_mfma_choice(M, out_cols, red), M, out_cols);
+        *bytes = ojx::gemm_split_bytes(ojx::gemm_mfma_choice(M, out_cols, red, bwd != 0), M,
+                                       out_cols);
     }
     g_last_error[0] = '\0';
     return OJX_OK;

@@ -160,7 +160,7 @@ struct GemmChoice {
     bool small;  // 128 x 128 tiles (else 256 x 256)
     int splits;
 };
-GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K);
+GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K, bool bwd);
 __host__ __device__ inline int64_t split_stride(int64_t M, int64_t N) {
     return (M * N + 3) & ~(int64_t)3;  // 16-byte aligned per split
 }

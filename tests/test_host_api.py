@@ -310,9 +310,11 @@ def test_workspace_query_follows_the_dispatch():
     # M = 512 on the k/v shape splits: a whole number of M x N fp32 slabs
     b = _ws(0, 0, 512, 1024, 4096)
     assert b > 0 and b % (512 * 1024 * 4) == 0 and b // (512 * 1024 * 4) >= 2
-    # backward dX of a small grid also splits (its output is [M, K])
-    b = _ws(0, 1, 512, 1024, 4096)
+    # backward dX of a small grid also splits (its output is [M, K]) when its reduction (N)
+    # has at least 32 steps of 64; the k/v shape's 16 steps at M = 512 run unsplit
+    b = _ws(0, 1, 512, 4096, 4096)
     assert b > 0 and b % (512 * 4096 * 4) == 0
+    assert _ws(0, 1, 512, 1024, 4096) == 0
     # fp32 activations run the general kernel: no scratch
     assert _ws(0, 0, 512, 1024, 4096, dtype=N.F32) == 0
     # errors: unknown format, bad group size, null result pointer
