@@ -7,7 +7,7 @@ Workload (the metric's headline): decode GEMV
 y[M,N] = x[M,K] . Wq[N,K]^T on a stack of L (default 32) Llama-3-8B-shaped
 decoder layers, each with seven E8-packed linears q 4096x4096, k/v 1024x4096,
 o 4096x4096, gate/up 14336x4096, down 4096x14336 (ternary-E8 codes, group-32
-fp16 scales, 1,751,252,992 bytes at L=32), at batch M in {1, 4, 16} with bf16
+fp16 scales, 1,744,830,464 bytes at L=32), at batch M in {1, 4, 16} with bf16
 activations.  Weights are drawn N(0, 0.02) in fp32 on the GPU (seeded) and
 encoded by this library's encoder; activations are bf16 N(0, 1).
 

@@ -108,9 +108,12 @@ int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scale
  * allocate device memory (code under graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The prefill K split's partial sums go to a static device array of
  * 64 MiB (one copy per GPU the library runs this on, held until the process ends; every
- * Llama-3-8B prefill shape fits).  A shape whose split needs more is refused with
- * OJX_ELAYOUT before any launch.  All calls on one GPU share that GPU's array: calls on one
- * stream are ordered, calls that overlap on one GPU (other streams) race. */
+ * Llama-3-8B prefill shape fits).  A shape whose planned split needs more is refused with
+ * OJX_ELAYOUT before any launch.  That refusal is a policy, not a limit of the kernels:
+ * ojx_e8t_gemm_fwd would run such a shape with fewer splits, but a lower split count
+ * changes the fp32 summation order, and this entry point promises the workspace entry
+ * point's exact kernels, split and output.  All calls on one GPU share that GPU's array:
+ * calls on one stream are ordered, calls that overlap on one GPU (other streams) race. */
 int ojx_e8t_gemm_fwd_noalloc(const void* x, const uint8_t* packed, const uint16_t* scales,
                              const void* bias, void* y, int64_t M, int64_t N, int64_t K,
                              int64_t gs, int dtype, void* stream);

@@ -139,15 +139,12 @@ static int check_fmt_args(int fmt, const void* a, const uint8_t* packed, const u
 // takes part in it; the workspace query passes null pointers (aligned).
 enum Route { kRouteGemvTile, kRouteGemv2m, kRouteGemv, kRouteGemv2, kRouteMfma, kRouteGeneric };
 
-#ifndef OJX_TILE_TILES_BELOW
-#define OJX_TILE_TILES_BELOW 1024
-#endif
 
 static Route route_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_t* scales,
                        const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dtype) {
     if (fmt == ojx::kFmtTernary) {
         // layers too small to stream (per-linear decode launches), M <= 4: staged tiles
-        if ((N + 15) / 16 < OJX_TILE_TILES_BELOW &&
+        if ((N + 15) / 16 < 1024 &&
             ojx::gemv_tile_supported(x, packed, scales, y, M, N, K, gs, dtype))
             return kRouteGemvTile;
         // 4 < M <= 16 on a layer too small for the streaming mask kernel (< 1024 row tiles):
@@ -253,7 +250,12 @@ static int gemm_fwd_lora(int fmt, const void* x, const uint8_t* packed, const ui
                     (long long)ojx::kLoraMaxRank, (long long)rank);
     if (M > 0 && N > 0 && (!lora_a || !lora_b || !lora_u))
         return fail(OJX_EINVAL, "null LoRA pointer");
+    // every check of the forward runs before the down-projection is enqueued: a refused call
+    // launches nothing
+    if (((uintptr_t)lora_u & 3u) || ((uintptr_t)lora_a & 1u) || ((uintptr_t)lora_b & 1u))
+        return fail(OJX_ELAYOUT, "misaligned LoRA operand (lora_u 4-byte, A and B 2-byte)");
     if (int r = check_fmt_args(fmt, x, packed, scales, y, M, N, K, gs, dtype)) return r;
+    if (int r = check_workspace(ws, ws_bytes)) return r;
     if (M == 0 || N == 0) return OJX_OK;
     if (int r = check_device()) return r;
     const bool inline_u =

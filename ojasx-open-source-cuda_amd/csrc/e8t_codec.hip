@@ -113,12 +113,15 @@ __device__ __forceinline__ uint32_t quantize8_exact(const float* __restrict__ w,
 //   * pen == |t| for every finite fp32 v (q == 0 puts both cases' squares in the same two
 //     rounded products: alt - v = +-d, q - v = -v; q != 0 swaps them), so the first argmin
 //     of pen is the first argmin of |t|;
-//   * alt - q == sgn(v) * sgn(t) for every v with |v| < 2^24 other than -0 (t >= 0 exactly
-//     when q == 0), so the flip adds +-3^i with the sign bit of v XOR t.
+//   * alt - q == sgn(v) * sgn(t) for every v with |v| < 2^24, where sgn(-0) = +1 (t >= 0
+//     exactly when q == 0, and the reference's alt is +1 for v = -0 since -0 >= 0), so the
+//     flip adds +-3^i with the sign of (v < 0) XOR t.
 // Both identities were checked exhaustively over all 2^32 fp32 bit patterns.  Here
-// |v| <= sqrt(gs) * (1 + eps) (the group's norm bounds every weight) and the residual
-// division returns +0 for w = -0.  The parity of sum(q) is the parity of the code's base-3
-// value, since every power of 3 is odd.  F16IN: the weights came from fp16.
+// |v| <= sqrt(gs) * (1 + eps) (the group's norm bounds every weight).  The quotient can be
+// -0: the residual division returns +0 for w = -0, but a negative subnormal weight over a
+// scale >= 2 rounds to -0, so v's sign is taken by a comparison, not from its sign bit.
+// The parity of sum(q) is the parity of the code's base-3 value, since every power of 3
+// is odd.  F16IN: the weights came from fp16.
 template <bool F16IN>
 __device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, const GroupRecip& g) {
 #pragma clang fp contract(off)
@@ -142,7 +145,7 @@ __device__ __forceinline__ uint32_t quantize8(const float* __restrict__ w, const
             best_p = pow3[i];
         }
     }
-    const uint32_t sg = (__float_as_uint(best_v) ^ __float_as_uint(best_t)) & 0x80000000u;
+    const uint32_t sg = (best_v < 0.f ? 0x80000000u : 0u) ^ (__float_as_uint(best_t) & 0x80000000u);
     const int ri = (int)raw;  // exact: 0 .. 6560
     const int fix = (ri & 1) ? (int)__uint_as_float(__float_as_uint(best_p) | sg) : 0;
     return (uint32_t)(ri + fix) >> 1;

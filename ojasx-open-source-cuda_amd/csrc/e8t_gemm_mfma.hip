@@ -33,17 +33,8 @@ namespace ojx {
 
 constexpr int kBK = 64;
 constexpr int kXcds = 8;
-#ifndef OJX_XCD_MAP
-#define OJX_XCD_MAP 1
-#endif
-#ifndef OJX_GROUP_M
-#define OJX_GROUP_M 8
-#endif
-constexpr int kGroupM = OJX_GROUP_M;  // M tiles per group of the tile order
-#ifndef OJX_GROUP4_FROM_TN
-#define OJX_GROUP4_FROM_TN 32
-#endif
-constexpr int64_t kGroup4FromTn = OJX_GROUP4_FROM_TN;  // column tiles from which groups hold 4
+constexpr int kGroupM = 8;  // M tiles per group of the tile order
+constexpr int64_t kGroup4FromTn = 32;  // column tiles from which groups hold 4
 
 // Tile configuration: BM x BN output tile per workgroup, WAVES_M x WAVES_N waves of
 // (BM / WAVES_M) x (BN / WAVES_N) each.  Two threads decode each weight row of the tile.
@@ -357,10 +348,6 @@ __device__ __forceinline__ BwdBlock bwd_block(int tid) {
     return k;
 }
 
-#ifndef OJX_BWD_PAIRED
-#define OJX_BWD_PAIRED 1
-#endif
-
 // Writes columns 2p and 2p + 1 of a thread pair's 8 x 8 block (r[row][dword of k pairs], the
 // thread's 4 rows) as dwords of n pairs.  Paired: each thread of the pair builds its 8-byte
 // half of both columns, swaps one with its neighbour lane, and writes the whole 16-byte piece
@@ -370,7 +357,7 @@ __device__ __forceinline__ BwdBlock bwd_block(int tid) {
 template <bool Paired>
 __device__ __forceinline__ void bwd_store_cols(const uint32_t (&r)[4][4], int p, char* tile,
                                                const BwdBlock& bk) {
-    if constexpr (Paired && OJX_BWD_PAIRED != 0) {
+    if constexpr (Paired) {
         const bool odd = bk.hoff != 0;
         const uint32_t selk = odd ? 0x07060302u : 0x05040100u;  // column 2p + h: kept
         const uint32_t sels = odd ? 0x05040100u : 0x07060302u;  // column 2p + 1 - h: sent
@@ -404,45 +391,6 @@ __device__ __forceinline__ uint32_t scale_word1(uint32_t s16) {
     else p = s16 & 0xFFFFu;
     return (p | (p << 16)) | 0x80008000u;
 }
-
-template <int DT>
-struct TernaryBwdDecoder {
-    static constexpr int kLoads = 12;
-    uint32_t lo[4], hi[4], sc[4];  // the code's two bytes and the scale of each row
-    uint32_t r[4][4];
-    const char* lut;
-    uint32_t slot, odd;            // odd: the code is the second of its 3-byte pair
-    uint32_t vo_code[4], vo_scale[4], rowbytes, srowbytes;
-    __amdgpu_buffer_rsrc_t pr, sr;
-    BwdBlock bk;
-    __device__ __forceinline__ void load(int64_t n0) {
-        const int so = uniform_offset(n0 * rowbytes), ss = uniform_offset(n0 * srowbytes);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            lo[q] = __builtin_amdgcn_raw_buffer_load_b8(pr, vo_code[q], so, 0);
-            hi[q] = __builtin_amdgcn_raw_buffer_load_b8(pr, vo_code[q] + 1u, so, 0);
-            sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
-        }
-    }
-    __device__ __forceinline__ void prep() {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t code = odd ? ((lo[q] >> 4) | (hi[q] << 4)) : (lo[q] | ((hi[q] & 0xFu) << 8));
-            const uint32_t z = (code << kCodeShift) | slot;
-            const uint32_t h = __umulhi(z, kHiMagic);
-            const uint2 ml = *reinterpret_cast<const uint2*>(lut + lo_addr_of(h, z));
-            const uint2 mh = *reinterpret_cast<const uint2*>(lut + (h * kLutStride + slot));
-            const uint32_t sw = scale_word1<DT>(sc[q]);
-            r[q][0] = ml.x & sw;
-            r[q][1] = ml.y & sw;
-            r[q][2] = mh.x & sw;
-            r[q][3] = mh.y & sw;
-        }
-    }
-    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
-        bwd_store_cols<true>(r, p, tile, bk);
-    }
-};
 
 // Ternary backward dX with the step's code bytes (and at BN = 256 its scale bytes) staged in
 // LDS.  The 64 weight rows of a K step need BN * 3 / 16 code bytes and BN / 16 scale bytes
@@ -485,9 +433,6 @@ __device__ __forceinline__ void bwd_stage_dma(char* dst, __amdgpu_buffer_rsrc_t 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
                                              vo, so, 0, 0);
 }
-#ifndef OJX_BWD_STAGED
-#define OJX_BWD_STAGED 1
-#endif
 
 template <int DT, int BN>
 struct TernaryBwdStagedDecoder {
@@ -612,73 +557,6 @@ struct TernaryBwdStagedDecoder {
     }
     __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
         bwd_store_cols<true>(r, p, tile, bk);
-    }
-};
-
-template <int DT, int GS>
-struct Bit2BwdDecoder {
-    static constexpr int kLoads = 8;
-    uint32_t cw[4], sc[4];  // each row's two code bytes (8 weights) and scale
-    uint32_t r[4][4];
-    const char* tab;
-    uint32_t vo_code[4], vo_scale[4], rowbytes, srowbytes;
-    __amdgpu_buffer_rsrc_t pr, sr;
-    BwdBlock bk;
-    __device__ __forceinline__ void load(int64_t n0) {
-        const int so = uniform_offset(n0 * rowbytes), ss = uniform_offset(n0 * srowbytes);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            cw[q] = __builtin_amdgcn_raw_buffer_load_b16(pr, vo_code[q], so, 0);
-            sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
-        }
-    }
-    __device__ __forceinline__ void prep() {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint2 v = values2<DT>(sc[q]);
-            const uint2 a = *reinterpret_cast<const uint2*>(tab + 8u * (cw[q] & 0xFFu));
-            const uint2 b = *reinterpret_cast<const uint2*>(tab + 8u * ((cw[q] >> 8) & 0xFFu));
-            r[q][0] = __builtin_amdgcn_perm(v.x, v.y, a.x);
-            r[q][1] = __builtin_amdgcn_perm(v.x, v.y, a.y);
-            r[q][2] = __builtin_amdgcn_perm(v.x, v.y, b.x);
-            r[q][3] = __builtin_amdgcn_perm(v.x, v.y, b.y);
-        }
-    }
-    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
-        bwd_store_cols<true>(r, p, tile, bk);
-    }
-};
-
-template <int DT, int GS>
-struct RootBwdDecoder {
-    static constexpr int kLoads = 8;
-    uint32_t cd[4], sc[4];  // each row's code byte (8 weights) and scale
-    uint32_t r[4][4];
-    const char* tab;
-    uint32_t vo_code[4], vo_scale[4], rowbytes, srowbytes;
-    __amdgpu_buffer_rsrc_t pr, sr;
-    BwdBlock bk;
-    __device__ __forceinline__ void load(int64_t n0) {
-        const int so = uniform_offset(n0 * rowbytes), ss = uniform_offset(n0 * srowbytes);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            cd[q] = __builtin_amdgcn_raw_buffer_load_b8(pr, vo_code[q], so, 0);
-            sc[q] = __builtin_amdgcn_raw_buffer_load_b16(sr, vo_scale[q], ss, 0);
-        }
-    }
-    __device__ __forceinline__ void prep() {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint2 v = values1<DT>(sc[q]);
-            const uint4 sl = *reinterpret_cast<const uint4*>(tab + 16u * (cd[q] & 0xFFu));
-            r[q][0] = __builtin_amdgcn_perm(v.x, v.y, sl.x);
-            r[q][1] = __builtin_amdgcn_perm(v.x, v.y, sl.y);
-            r[q][2] = __builtin_amdgcn_perm(v.x, v.y, sl.z);
-            r[q][3] = __builtin_amdgcn_perm(v.x, v.y, sl.w);
-        }
-    }
-    __device__ __forceinline__ void store(int p, char* tile, uint32_t, int) const {
-        bwd_store_cols<false>(r, p, tile, bk);
     }
 };
 
@@ -828,9 +706,6 @@ struct LowbitBwdStagedDecoder {
         bwd_store_cols<kTwoBit>(r, p, tile, bk);
     }
 };
-#ifndef OJX_BWD_STAGED_LOWBIT
-#define OJX_BWD_STAGED_LOWBIT 1
-#endif
 
 // Decoders that stage their codes through an LDS ring (declare kStaged).
 template <typename D, typename = void>
@@ -919,7 +794,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
     const int64_t xcd = bid % kXcds, slot_in = bid / kXcds;
     int64_t t = xcd * per_xcd + slot_in;
-    if (!OJX_XCD_MAP || per_xcd * kXcds != tiles) {
+    if (per_xcd * kXcds != tiles) {
         // grid not a multiple of the XCD count: fall back to the plain order
         t = bid;
     }
@@ -961,13 +836,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     using FwdDec = std::conditional_t<
         kTernary, TernaryRowDecoder<DT>,
         std::conditional_t<FMT == kFmt2Bit, Bit2RowDecoder<DT, GS2>, RootRowDecoder<DT, GS2>>>;
-    using BwdDec = std::conditional_t<
-        kTernary,
-        std::conditional_t<OJX_BWD_STAGED != 0, TernaryBwdStagedDecoder<DT, C::BN>,
-                           TernaryBwdDecoder<DT>>,
-        std::conditional_t<
-            OJX_BWD_STAGED_LOWBIT != 0, LowbitBwdStagedDecoder<DT, C::BN, FMT, GS2>,
-            std::conditional_t<FMT == kFmt2Bit, Bit2BwdDecoder<DT, GS2>, RootBwdDecoder<DT, GS2>>>>;
+    using BwdDec = std::conditional_t<kTernary, TernaryBwdStagedDecoder<DT, C::BN>,
+                                      LowbitBwdStagedDecoder<DT, C::BN, FMT, GS2>>;
     using Dec = std::conditional_t<BWD, BwdDec, FwdDec>;
     constexpr bool kStagedDec = IsStaged<Dec>::value;
     __shared__ __attribute__((aligned(16))) char dec_ring[RingBytes<Dec>::value];
@@ -976,31 +846,6 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     dec.sr = sr;
     if constexpr (kStagedDec) {
         dec.setup(tid, lane, n0, rowbytes, srowbytes, lut, dec_ring);
-    } else if constexpr (BWD) {
-        // block rows n (per step) and output columns k = n0 + bk.col .. + 7 (n0 is the
-        // tile's first output column here)
-        dec.bk = bwd_block(tid);
-        dec.rowbytes = rowbytes;
-        dec.srowbytes = srowbytes;
-        const uint32_t kcol = (uint32_t)n0 + dec.bk.col;
-        uint32_t cbyte, sbyte;
-        if constexpr (kTernary) {
-            dec.lut = lut;
-            dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
-            const uint32_t j = kcol / 8u;  // code index in the row
-            dec.odd = j & 1u;
-            cbyte = 3u * (j >> 1) + (j & 1u);
-            sbyte = 2u * (kcol / 32u);
-        } else {
-            dec.tab = lut;
-            cbyte = FMT == kFmt2Bit ? kcol / 4u : kcol / 8u;
-            sbyte = 2u * (kcol / (uint32_t)GS2);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            dec.vo_code[q] = (dec.bk.rows + (uint32_t)q) * rowbytes + cbyte;
-            dec.vo_scale[q] = (dec.bk.rows + (uint32_t)q) * srowbytes + sbyte;
-        }
     } else if constexpr (kTernary) {
         dec.lut = lut;
         dec.slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
@@ -1158,9 +1003,6 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
 
 // Grids of large tiles that leave CUs idle (under about one workgroup per CU) run the
 // small-tile configuration, which has four times the tiles and two workgroups per CU.
-#ifndef OJX_GEMM_SMALL_BELOW
-#define OJX_GEMM_SMALL_BELOW 192
-#endif
 
 template <int DT, typename C, int FMT, int GS2, bool BWD>
 static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_t* scales,
@@ -1181,7 +1023,7 @@ static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_
 }
 
 // Tile configuration and K split of a launch.
-//  * Grids of at least OJX_GEMM_SMALL_BELOW large tiles: large tiles, unsplit.
+//  * Grids of at least 192 large tiles: large tiles, unsplit.
 //  * Smaller grids: large tiles split over K towards one workgroup per CU, if every split
 //    keeps at least kMinLargeSplitSteps K steps and the split grid still covers three
 //    quarters of the CUs;
@@ -1190,9 +1032,6 @@ static hipError_t launch_cfg(const void* x, const uint8_t* packed, const uint16_
 //    fp32 partials of the k/v shape at M = 512 cost more than the extra workgroups gain;
 //    16 for the backward dX, whose k/v shape at M = 512 runs 12% faster unsplit).
 // The fp32 partial sums of a split stay under kSplitBytesMax.
-#ifndef OJX_SPLIT_TARGET_WGS
-#define OJX_SPLIT_TARGET_WGS 512
-#endif
 constexpr int kMaxSplits = 16;
 constexpr int64_t kMinSplitSteps = 8;
 constexpr int64_t kMinSplitStepsBwd = 16;
@@ -1213,13 +1052,13 @@ static int64_t splits_for(int64_t tiles, int64_t target, int64_t min_steps, int6
 GemmChoice gemm_mfma_choice(int64_t M, int64_t N, int64_t K, bool bwd) {
     const int64_t large = ((M + CfgLarge::BM - 1) / CfgLarge::BM) *
                           ((N + CfgLarge::BN - 1) / CfgLarge::BN);
-    if (large >= OJX_GEMM_SMALL_BELOW) return GemmChoice{false, 1};
+    if (large >= 192) return GemmChoice{false, 1};
     const int64_t sl = splits_for(large, kLargeTargetWgs, kMinLargeSplitSteps, M, N, K);
     if (large * sl >= kLargeMinWgs) return GemmChoice{false, (int)sl};
     const int64_t tiles = ((M + CfgSmall::BM - 1) / CfgSmall::BM) *
                           ((N + CfgSmall::BN - 1) / CfgSmall::BN);
     return GemmChoice{true,
-                      (int)splits_for(tiles, OJX_SPLIT_TARGET_WGS,
+                      (int)splits_for(tiles, 512,
                                       bwd ? kMinSplitStepsBwd : kMinSplitSteps, M, N, K)};
 }
 

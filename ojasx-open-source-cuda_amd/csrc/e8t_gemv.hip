@@ -290,52 +290,25 @@ constexpr int kRound = 1024;                      // K per round
 // Post-scaled kernel: tile groups per workgroup.  Measured on MI355X (32-layer decode
 // stack, M = 1): 1 -> 3.7-3.8 TB/s, 2 -> 3.5, 4 -> 3.3, 8 -> 2.9; longer workgroups save
 // table fills and prologue latency but leave a longer tail of partly idle CUs.
-#ifndef OJX_PS_CHUNK
-#define OJX_PS_CHUNK 1
-#endif
-constexpr int kPsChunk = OJX_PS_CHUNK;
+constexpr int kPsChunk = 1;
 // Waves per workgroup of the post-scaled kernel.
-#ifndef OJX_PS_WAVES
-#define OJX_PS_WAVES 4
-#endif
-constexpr int kPsWaves = OJX_PS_WAVES;
+constexpr int kPsWaves = 4;
 // Waves per workgroup and table slices of the post-scaled kernel at 1 < M <= 4, two tiles
 // per wave.
-#ifndef OJX_PS_WAVES_M4
-#define OJX_PS_WAVES_M4 4
-#endif
-constexpr int kPsWavesM4 = OJX_PS_WAVES_M4;
-#ifndef OJX_PS_SLOTS_M4
-#define OJX_PS_SLOTS_M4 16
-#endif
-constexpr int kPsSlotsM4 = OJX_PS_SLOTS_M4;
+constexpr int kPsWavesM4 = 4;
+constexpr int kPsSlotsM4 = 16;
 // Row tiles (16 rows) per wave of the post-scaled kernel.
-#ifndef OJX_PS_TILES
-#define OJX_PS_TILES 2
-#endif
-constexpr int kPsTiles = OJX_PS_TILES;
+constexpr int kPsTiles = 2;
 // Post-scaled launches at 1 < M <= 4 with fewer row tiles than this take one tile per wave
 // (64-row workgroups: twice the workgroups, each activation round shared by 64 rows).
 // Measured on the decoder's fused gate/up (1792 tiles, M = 4), per decode step of 32 layers:
 // 86 us less than the staged-tile kernel; launches of 8016 tiles (lm_head) gain nothing and
 // the 10,752-tile stack loses 10-15%, so they keep two tiles per wave.
-#ifndef OJX_PS_ONE_TILE_BELOW
-#define OJX_PS_ONE_TILE_BELOW 4096
-#endif
-constexpr int64_t kPsOneTileBelow = OJX_PS_ONE_TILE_BELOW;
+constexpr int64_t kPsOneTileBelow = 4096;
 // Table slices of the post-scaled kernel at M = 1.  Measured on MI355X (32-layer grouped
 // stack, same box): 32 slices 0.361 ms against 0.400 ms with 16; at M = 4 the 32-slice
 // table costs a workgroup per CU of residency and runs 0.470 against 0.441 ms.
-#ifndef OJX_PS_SLOTS_M1
-#define OJX_PS_SLOTS_M1 32
-#endif
-constexpr int kPsSlotsM1 = OJX_PS_SLOTS_M1;
-// Optional occupancy request for the post-scaled kernel (waves per SIMD), e.g. 5.
-#ifdef OJX_PS_MIN_WAVES
-#define OJX_PS_OCC __attribute__((amdgpu_waves_per_eu(OJX_PS_MIN_WAVES)))
-#else
-#define OJX_PS_OCC
-#endif
+constexpr int kPsSlotsM1 = 32;
 constexpr uint32_t kXRow = kRound * 2 + 16;       // bytes per padded activation row in LDS
 
 template <int R>
@@ -403,11 +376,7 @@ __device__ __forceinline__ void codes_lut4(const uint32_t (&cd)[R][NW], const ch
 
 // Operands (A fragment and table words) of the next kLookahead steps of a round, read
 // ahead so that the table reads of a step have kLookahead steps of other work to land.
-#ifndef OJX_LOOKAHEAD
-#define OJX_LOOKAHEAD 2
-#endif
-constexpr int kLookahead = OJX_LOOKAHEAD;
-static_assert(kLookahead == 1 || kLookahead == 2, "read-ahead depth 1 or 2");
+constexpr int kLookahead = 2;
 
 template <int R>
 struct Ahead {
@@ -438,10 +407,8 @@ __device__ __forceinline__ void ahead_fill(Ahead<R>& ah, const uint32_t (&cd)[R]
                                            const char* lut, uint32_t slot, const char* xa_base) {
     ah.xa[0] = *reinterpret_cast<const uint4*>(xa_base);
     codes_lut4<R, NW, 0, SL>(cd, lut, slot, ah.b[0]);
-    if constexpr (kLookahead > 1) {
-        ah.xa[1] = *reinterpret_cast<const uint4*>(xa_base + 16);
-        codes_lut4<R, NW, 1, SL>(cd, lut, slot, ah.b[1]);
-    }
+    ah.xa[1] = *reinterpret_cast<const uint4*>(xa_base + 16);
+    codes_lut4<R, NW, 1, SL>(cd, lut, slot, ah.b[1]);
 }
 
 __device__ __forceinline__ void vm_wait_all() {
@@ -471,10 +438,7 @@ __device__ __forceinline__ void lds_wait_all() {
 // p ^ ((n/4 + n/8) & 1).
 
 constexpr int kMRound = 512;                      // K per round of the mask kernel
-#ifndef OJX_MASK_WAVES
-#define OJX_MASK_WAVES 8
-#endif
-constexpr int kMaskWaves = OJX_MASK_WAVES;        // waves per workgroup
+constexpr int kMaskWaves = 8;        // waves per workgroup
 constexpr uint32_t kMXRow = kMRound * 2 + 16;     // bytes per padded activation row in LDS
 constexpr uint32_t kMStageBytes = 4096;           // codes 3 KB + scales 1 KB (two tiles)
 
@@ -904,7 +868,7 @@ __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M,
 // table once.  Tile group c of the workgroup reads rows 16 W R c further down the same
 // buffers: the shift is a wave-uniform offset.
 template <int DT, int R, int MM, int W>
-__global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch args) {
+__global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
     // Table slices: 32 at M = 1 (conflict-free 8-byte reads; the 20 KB table still leaves
     // three workgroups per CU), 16 at M <= 4, whose larger activation buffers need the LDS.
@@ -1055,10 +1019,7 @@ __global__ __launch_bounds__(64 * W) OJX_PS_OCC void gemv_ps_kernel(GemvLaunch a
 // workgroup per CU, 4 waves leave one wave per SIMD to run 3-4 rounds back to back).
 // Measured on MI355X (same box): 4 waves 12.0 us, 8 waves 9.7 us; a second activation
 // buffer per wave (double buffering) instead: 11.9 us.
-#ifndef OJX_PSK_WAVES_M4
-#define OJX_PSK_WAVES_M4 8
-#endif
-constexpr int kPskWavesM4 = OJX_PSK_WAVES_M4;
+constexpr int kPskWavesM4 = 8;
 
 template <int DT, int MM, int W>
 __global__ __launch_bounds__(64 * W) void gemv_psk_kernel(GemvLaunch args) {
@@ -1557,10 +1518,7 @@ __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
 // workgroups), two from there (half the staged activation bytes per weight).  Measured on
 // MI355X, per-linear M = 16 (same box): gate/up 17.0 -> 13.5 us with two; four 14.2 us;
 // two from 256 tiles on (q/o, down) 5.7 -> 7.4 and 13.9 -> 18.8 us.
-#ifndef OJX_B2M_TWO_TILES_FROM
-#define OJX_B2M_TWO_TILES_FROM 512
-#endif
-constexpr int64_t kB2mTwoTilesFrom = OJX_B2M_TWO_TILES_FROM;
+constexpr int64_t kB2mTwoTilesFrom = 512;
 
 template <int DT, int GS, int FMT, int R>
 struct B2mRound {
@@ -1813,9 +1771,6 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
 // from past every buffer's end: zeros, no memory traffic, and the same count of loads per
 // slot, so that one wait count fits every slot.
 constexpr int kB2sRows = 4;
-#ifndef OJX_B2S
-#define OJX_B2S 1
-#endif
 constexpr int kB2sXBytes = kB2sRows * kB2mRound * 2;  // 2 KB per wave and round
 constexpr uint32_t kB2sOob = 0x80000000u;             // past every buffer here (< 2^31 bytes)
 
@@ -2074,10 +2029,7 @@ __device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
 // Depth of the software pipeline of a round: the table and activation reads of step
 // J + kTileAhead are issued before the MFMA of step J (with one wave per SIMD, a step that
 // waited for its own reads would expose the whole LDS latency).
-#ifndef OJX_TILE_AHEAD
-#define OJX_TILE_AHEAD 4
-#endif
-constexpr int kTileAhead = OJX_TILE_AHEAD;
+constexpr int kTileAhead = 4;
 
 // The staged-tile kernel's table: 32 slices (conflict-free b64 reads: 2.2 clk per wave
 // read on MI355X against 3.7 with 16 slices, where neighbouring lanes share banks), holding
@@ -2668,7 +2620,7 @@ static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const ui
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream, const LoraEp& lora) {
     const int64_t tiles = (N + 15) / 16;
-    if (M <= kB2sRows && OJX_B2S) {
+    if (M <= kB2sRows) {
         if (tiles >= kB2mTwoTilesFrom)
             hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 2>), dim3((unsigned)((tiles + 1) / 2)),
                                dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N,
@@ -2736,22 +2688,16 @@ int gemv_tile_rounds(int64_t M, int64_t Kmax) {
 // when M == 1 and the launch has too many tiles for one-tile workgroups to be resident at
 // once (their stages and table take 51 KB: three per CU), which shares the table between
 // two tiles.
-#ifndef OJX_TILE_PAIR_FROM
-#define OJX_TILE_PAIR_FROM 768
-#endif
 int gemv_tile_per_wg(int64_t M, int64_t tiles) {
-    return (M == 1 && tiles >= OJX_TILE_PAIR_FROM) ? 2 : 1;
+    return (M == 1 && tiles >= 768) ? 2 : 1;
 }
 
 // Row tiles per wave of a staged-tile launch: two at 1 < M <= 4 with one round per wave when
 // the launch has many tiles (the tiles share the activation stage, 9 KB per wave and round
 // at M = 4, and the A fragment reads; the stages of a workgroup then still fit twice per CU
 // with a 16-slice table).
-#ifndef OJX_TILE_RT2_FROM
-#define OJX_TILE_RT2_FROM 768
-#endif
 int gemv_tile_rows_per_wave(int64_t M, int64_t tiles, int U) {
-    return (M > 1 && U == 1 && tiles >= OJX_TILE_RT2_FROM) ? 2 : 1;
+    return (M > 1 && U == 1 && tiles >= 768) ? 2 : 1;
 }
 
 bool gemv_lora_inline_ok(int U, int rt, int tpw, int64_t rank, const void* lora_a) {
@@ -2781,15 +2727,9 @@ bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* s
 
 // Grouped launches below these row-tile counts take the staged-tile kernel: M == 1 and
 // 1 < M <= 4 (from 1024 tiles the post-scaled kernel with one tile per wave is faster there).
-#ifndef OJX_TILE_GROUPED_BELOW
-#define OJX_TILE_GROUPED_BELOW 4096
-#endif
-#ifndef OJX_TILE_GROUPED_BELOW_M4
-#define OJX_TILE_GROUPED_BELOW_M4 1024
-#endif
 GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool tile_ok) {
     const int U = tile_ok ? gemv_tile_rounds(M, kmax) : 0;
-    const int64_t below = M == 1 ? OJX_TILE_GROUPED_BELOW : OJX_TILE_GROUPED_BELOW_M4;
+    const int64_t below = M == 1 ? 4096 : 1024;
     if (U == 0 || total_tiles >= below) return gemv_pick(total_tiles, M);
     GemvPlan p{};
     p.tile = true;

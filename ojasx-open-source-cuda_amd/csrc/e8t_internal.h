@@ -128,7 +128,7 @@ struct GemvPlan {
 };
 GemvPlan gemv_pick(int64_t total_tiles, int64_t M);
 // gemv_pick for a grouped launch, preferring the staged-tile kernel for launches of fewer
-// than OJX_TILE_GROUPED_BELOW (M == 1) or OJX_TILE_GROUPED_BELOW_M4 (1 < M <= 4) row tiles
+// than 4096 (M == 1) or 1024 (1 < M <= 4) row tiles
 // when every job allows it (K % 1024 == 0, 16-byte aligned codes and scales; kmax the
 // longest K).
 GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool tile_ok);

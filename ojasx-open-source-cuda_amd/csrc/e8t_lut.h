@@ -25,12 +25,9 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 typedef __attribute__((ext_vector_type(3))) uint32_t u32x3;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
-#ifndef OJX_LUT_SLOTS
-#define OJX_LUT_SLOTS 16
-#endif
 
 constexpr int kLutEntries = 102;            // 81 valid + slack so that any 12-bit code stays in bounds
-constexpr int kLutSlots = OJX_LUT_SLOTS;    // bank slices: lane l reads slice l % kLutSlots
+constexpr int kLutSlots = 16;    // bank slices: lane l reads slice l % kLutSlots
 static_assert(kLutSlots == 8 || kLutSlots == 16 || kLutSlots == 32, "8, 16 or 32 table slices");
 constexpr uint32_t kLutStride = kLutSlots * 8;  // bytes per table entry (all slices)
 // Z = 2 * code * kLutStride + slot = (code << kCodeShift) | slot; kHiMagic makes

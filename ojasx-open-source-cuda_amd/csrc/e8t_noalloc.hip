@@ -8,6 +8,11 @@
 // name as an address (on the host it is only a stand-in symbol): the device address of each
 // GPU's copy is looked up once per device with hipGetSymbolAddress and kept.
 //
+// A shape whose planned K split needs more than kScratchBytes is refused.  That is a policy:
+// the workspace entry point would run it with the split capped to what fits, but a smaller
+// split sums the partials in another order, and this entry point's output is defined as the
+// workspace entry point's output with the planned workspace, bit for bit.
+//
 // Every call on one GPU shares that GPU's copy.  Calls ordered on one stream are safe;
 // calls that overlap on one GPU (different streams, or several host threads on different
 // streams) race on it.  The split kernels write every partial sum they later read, so the

@@ -17,7 +17,11 @@ Typical uses:
   GEMV adds u @ B in its epilogue (E8LatticeLinear.forward, lattice.py:839-842).  The
   plan holds the adapter tensors themselves (lora_A / lora_B must already be
   contiguous in the activation dtype), so in-place updates of them are seen; a new
-  scaling needs a new plan;
+  scaling needs a new plan.  Such a plan also owns one fp32 u buffer per adapter, which
+  every call writes and then reads: unless the launch forms u inside the GEMV (rank-8
+  adapters on the single-round staged-tile route), calls of one plan that overlap (two
+  streams, or graph replays that are not ordered on one stream) race on it, so use such a
+  plan from one stream at a time (or build one plan per stream);
 * a fixed table -- explicit ``x`` / ``y`` per job, uploaded once to the device.
 """
 

@@ -5,7 +5,10 @@ flipping the coordinate with the first smallest pen = (alt - v)^2 - (q - v)^2, e
 rounded in fp32, with q = clamp(rint(v), -1, 1) and alt = q == 0 ? (v >= 0 ? 1 : -1) : 0.
 The kernel evaluates instead d = fl(1 - |v|), t = fl(fl(d * d) - fl(v * v)) and relies on
   pen == |t|                         for every finite v, and
-  alt - q == sgn(v) * sgn(t)         for every v with |v| < 2^24 other than -0.
+  alt - q == sgn(v) * sgn(t)         for every v with |v| < 2^24, with sgn(-0) = +1 (the
+                                     reference's alt is +1 for v = -0, since -0 >= 0).
+The kernel's quotient v can be -0 (a negative subnormal weight over a scale >= 2), so the
+kernel takes v's sign from v < 0, not from its sign bit, and this test includes -0.
 Both were checked over all 2^32 fp32 bit patterns when the kernel was written; this test
 re-checks every fp32 value with |v| < 8 (the kernel's range is |v| <= sqrt(gs)(1 + eps)) at a
 stride, densely around the decision points 0.5 and 1.5, and at the extremes.  numpy's float32
@@ -17,7 +20,6 @@ import numpy as np
 
 def _check(bits: np.ndarray) -> None:
     bits = bits[(bits & 0x7F800000) != 0x7F800000]   # finite only
-    bits = bits[bits != 0x80000000]                   # -0 (the kernel's quotient is never -0)
     v = bits.view(np.float32)
     with np.errstate(over="ignore", invalid="ignore"):
         _check_values(v)
@@ -35,9 +37,17 @@ def _check_values(v: np.ndarray) -> None:
     assert pen.dtype == np.float32 and t.dtype == np.float32
     assert np.array_equal(pen, np.abs(t), equal_nan=True), "pen != |t|"  # both NaN past ~1.8e19
     small = np.abs(v) < np.float32(2.0 ** 24)
-    sign = ((v.view(np.uint32) ^ t.view(np.uint32)) & np.uint32(0x80000000)) != 0
+    sign = (v < 0) ^ ((t.view(np.uint32) & np.uint32(0x80000000)) != 0)
     flip = np.where(sign, -one, one)
     assert np.array_equal((alt - q)[small], flip[small]), "alt - q != sgn(v) sgn(t)"
+
+
+def test_reduced_form_minus_zero():
+    # v = -0: q = 0 and alt = +1 (the reference tests v >= 0); the sign bit of v would say -1
+    _check(np.array([0x80000000, 0x00000000], dtype=np.uint32))
+    v = np.array([-0.0], dtype=np.float32)
+    sign_bit = (v.view(np.uint32) & np.uint32(0x80000000)) != 0
+    assert sign_bit[0] and not (v < 0)[0]
 
 
 def test_reduced_form_strided_below_8():

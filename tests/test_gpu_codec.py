@@ -85,6 +85,25 @@ def test_encode_edge_magnitudes():
         assert np.array_equal(pg, po), gs
 
 
+def test_encode_minus_zero_quotient():
+    # a negative subnormal weight next to a large one: its quotient by the group scale
+    # rounds to -0, where the reference's parity fix flips up (alt = +1 for v >= 0)
+    # (fp32 only: a half-precision subnormal over a scale fp16 can hold is never -0)
+    rows = []
+    for tiny, big in ((-1e-45, 12.0), (-3e-45, 12.0), (-3e-45, 100.0), (-1e-45, 0.5)):
+        for pos in (0, 5, 8, 31):
+            r = torch.zeros(64)
+            r[pos] = tiny
+            r[(pos + 1) % 64] = big
+            rows.append(r)
+    w = torch.stack(rows)
+    for gs in (16, 32, 64):
+        pg, sg = _gpu_encode(w, gs)
+        po, so = _oracle_encode(w, gs)
+        assert np.array_equal(sg, so), gs
+        assert np.array_equal(pg, po), gs
+
+
 def test_encode_c1_layer_bit_exact():
     # BASELINE C1: W fp32 4096x4096 ~ N(0, 0.02), CPU generator seed 8101, gs 32
     g = torch.Generator().manual_seed(8101)

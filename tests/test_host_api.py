@@ -83,6 +83,26 @@ def test_abi_rejects_bad_arguments_before_launch():
                                 None) == -1
     assert lib.ojx_e8t_gemm_fwd(None, None, None, None, None, 0, 4, 4, 32, 0, 8, 64, None) == -2
     assert lib.ojx_e8r_gemm_fwd(None, None, None, None, None, 0, 4, 8, 8, 0, None, 0, None) == 0
+    # the LoRA forward checks every operand, the workspace included, before it enqueues the
+    # down-projection (fake but aligned device addresses; nothing here reaches a GPU call)
+    A, X, P, S, Y, U, B = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000, 0x70000
+    for f in (lib.ojx_e8t_gemm_fwd_lora, lib.ojx_e8_gemm_fwd_lora, lib.ojx_e8r_gemm_fwd_lora):
+        args = dict(x=X, p=P, s=S, bias=None, a=A, b=B, r=8, sc=2.0, u=U, y=Y, M=1, N=64, K=256,
+                    gs=32, dt=2, ws=None, wsb=0)
+
+        def call(**kw):
+            a = dict(args, **kw)
+            return f(a["x"], a["p"], a["s"], a["bias"], a["a"], a["b"], a["r"], a["sc"], a["u"],
+                     a["y"], a["M"], a["N"], a["K"], a["gs"], a["dt"], a["ws"], a["wsb"], None)
+
+        assert call(u=U + 2) == -2 and b"misaligned LoRA" in lib.ojx_e8t_last_error()
+        assert call(b=B + 1) == -2
+        assert call(a=A + 1) == -2
+        assert call(wsb=64) == -1 and b"null workspace" in lib.ojx_e8t_last_error()
+        assert call(ws=0x80008, wsb=64) == -2
+        assert call(r=0) == -2 and call(r=65) == -2
+        assert call(u=None) == -1
+        assert call(M=0) == 0
 
 
 def test_ops_refuse_cpu_tensors():

@@ -184,6 +184,36 @@ def test_encode_group_known_answers():
 
 # ---------------------------------------------------------------- layout
 
+def _minus_zero_group() -> np.ndarray:
+    # the first weight is fp32's smallest negative subnormal; its quotient by the group scale
+    # (~2.12) rounds to -0, and the parity fix then flips coordinate 0 (pen 1, the first
+    # minimum).  Only fp32 inputs reach -0: a bf16/fp16 subnormal over a scale that fp16 can
+    # hold still has a nonzero quotient.
+    w = np.zeros(32, dtype=np.float32)
+    w[0] = -np.float32(1e-45)
+    w[1] = 12.0
+    return w
+
+
+def test_encode_minus_zero_quotient_flips_up():
+    # lattice.py:361-365: alt = +1 where v >= 0, and -0 >= 0 holds, so coordinate 0 becomes
+    # +1: coords [1, 1, 0, ...] -> raw = 2 + 2*3 + (3280 - 1 - 3) = 3284 -> code 1642; the
+    # three all-zero 8-vectors have code 1640 (Appendix-A closed form)
+    p, _, _ = O.encode(_minus_zero_group()[None, :], 32)
+    want = np.array([b for c0, c1 in ((1642, 1640), (1640, 1640))
+                     for b in (c0 & 0xFF, ((c0 >> 8) & 0xF) | ((c1 & 0xF) << 4), (c1 >> 4) & 0xFF)],
+                    dtype=np.uint8)
+    assert np.array_equal(p, want), p
+    # the reference's expressions evaluated by torch: v[0] is -0 and its alt is +1
+    w = torch.from_numpy(_minus_zero_group())
+    sc = torch.norm(w) / math.sqrt(32) + 1e-8
+    v = w.view(4, 8) / sc
+    assert str(float(v[0, 0])) == "-0.0"
+    q = torch.clamp(torch.round(v), -1, 1)
+    alt = torch.where(q == 0, torch.where(v >= 0, 1.0, -1.0), 0.0)
+    assert float(alt[0, 0]) == 1.0
+
+
 def test_packed_sizes_match_reference_invariants():
     # reference tests/test_sub2bit_lattice.py:40-62: 64x128 at gs 32
     rng = np.random.default_rng(99)
