@@ -128,6 +128,10 @@ def parse_args():
     ap.add_argument("--settle-s", type=float, default=0.5,
                     help="seconds of each leg's own launches run untimed right before its "
                          "timed region, after the warm-up steps (0: none)")
+    ap.add_argument("--launch-probe", action="store_true",
+                    help="only measure the cost of a decode-sized launch (a one-workgroup GEMV "
+                         "and a one-element torch kernel, eager and replayed from a hipGraph) "
+                         "and exit")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run three device-to-device copies of this many MiB (the "
                          "known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE) and exit")
@@ -989,6 +993,59 @@ def cpu_baseline(seconds: float):
 
 # --------------------------------------------------------------------------- main
 
+def launch_probe(torch, N_, ops, dev, launches: int = 224, reps: int = 20) -> dict:
+    """Cost of one decode-sized launch: microseconds per launch of (a) this library's GEMV on
+    a 16 x 1024 layer at M = 1 (one workgroup, 3 KB of codes) and (b) torch's elementwise add
+    on one element, each issued `launches` times back to back, eagerly and from a hipGraph
+    (the way the per-linear decode stack is replayed)."""
+    lib = N_.lib()
+    g = torch.Generator(device=dev).manual_seed(7)
+    w = torch.randn(16, 1024, generator=g, device=dev) * 0.02
+    packed, scales = ops.encode(w, GS)
+    x = torch.randn(1, 1024, generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, 16, dtype=torch.bfloat16, device=dev)
+    a = torch.ones(1, device=dev)
+
+    def gemv(stream_handle):
+        for _ in range(launches):
+            N_.check(lib.ojx_e8t_gemm_fwd(x.data_ptr(), packed.data_ptr(), scales.data_ptr(),
+                                          None, y.data_ptr(), 1, 16, 1024, GS, N_.BF16, None, 0,
+                                          stream_handle), "gemm_fwd")
+
+    def add(stream_handle):
+        for _ in range(launches):
+            a.add_(1.0)
+
+    out = {"launches": launches, "reps": reps}
+    for name, fn in (("gemv_16x1024_M1", gemv), ("torch_add_1elem", add)):
+        fn(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        cap = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            fn(torch.cuda.current_stream().cuda_stream)
+        res = {}
+        for mode in ("eager", "graph"):
+            run = (lambda: graph.replay()) if mode == "graph" else \
+                (lambda: fn(torch.cuda.current_stream().cuda_stream))
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                run()
+            e1.record()
+            torch.cuda.synchronize()
+            res[mode + "_us_per_launch"] = round(e0.elapsed_time(e1) * 1e3 / (reps * launches), 3)
+        out[name] = res
+        log(f"launch probe {name}: {res}")
+    err = (y.float() - (x.float() @ ops.decode(packed, scales, 16 * 1024, GS,
+                                              torch.bfloat16).view(16, 1024).float().t())).abs()
+    out["gemv_max_abs_err"] = float(err.max())
+    return out
+
+
 def main() -> int:
     args = parse_args()
     global SETTLE_S
@@ -1021,6 +1078,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n,
                           "launches": 3, "kernel": "torch.neg (elementwise) fp32"}), flush=True)
+        return 0
+    if args.launch_probe:
+        print(json.dumps(launch_probe(torch, N_, ops, dev)), flush=True)
         return 0
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
