@@ -94,9 +94,9 @@ int ojx_gemm_workspace_bytes(int fmt, int bwd, int64_t M, int64_t N, int64_t K, 
  * schema at :594) and dispatch_tilelang_e8_gemm (ojasx2/tilelang_kernels.py:370-419);
  * called from _FusedE8GEMMFunction.forward (lattice.py:584-608).
  *   x, y, bias in `dtype`; bias may be NULL.  Wdeq follows the decoder's rule for `dtype`.
- *   Any K >= 1 (flat layout).  F16/BF16 with K % 256 == 0, gs == 32 and M <= 16 run the
- *   MFMA decode GEMV; F16/BF16 with K % 64 == 0, gs == 32 and M > 16 the MFMA prefill
- *   GEMM; other shapes and F32 use a general tiled kernel.  Never declines.
+ *   Any K >= 1 (flat layout).  F16/BF16 with K % 256 == 0, gs in {16, 32, 64} and M <= 16
+ *   run an MFMA decode GEMV; F16/BF16 with K % 64 == 0, gs in {16, 32, 64} and M > 16 the
+ *   MFMA prefill GEMM; other shapes and F32 use a general tiled kernel.  Never declines.
  *   workspace: 16-byte aligned device scratch of workspace_bytes (NULL with 0 allowed),
  *   see ojx_gemm_workspace_bytes. */
 int ojx_e8t_gemm_fwd(const void* x, const uint8_t* packed, const uint16_t* scales,

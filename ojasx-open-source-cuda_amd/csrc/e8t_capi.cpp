@@ -152,6 +152,10 @@ static Route route_fwd(int fmt, const void* x, const uint8_t* packed, const uint
         if (M > 4 && (N + 15) / 16 < 1024 &&
             ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, fmt))
             return kRouteGemv2m;
+        // group sizes 16 and 64 at M <= 16: the B-operand GEMV at every layer size
+        if (gs != 32 && M <= 16 &&
+            ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, fmt))
+            return kRouteGemv2m;
         if (K > 0 && ojx::gemv_supported(x, packed, scales, y, M, N, K, gs, dtype))
             return kRouteGemv;
         if (M > 16 && ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, fmt))

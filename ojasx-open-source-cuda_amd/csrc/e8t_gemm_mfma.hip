@@ -78,18 +78,31 @@ __device__ __forceinline__ void load_x_tile(char* tile, __amdgpu_buffer_rsrc_t x
 
 struct RowCodes {
     uint32_t d[3];  // 8 codes of this thread's weight row for one K step
-    uint32_t s;     // its two group scales (fp16 bits)
+    uint32_t s[2];  // the step's group scales (fp16 bits): 4 at GS 16, 2 at GS 32, 1 at GS 64
 };
 
+// Codes and scales of K step k0 of this thread's row (group size GS: 64 / GS scales, or the
+// one scale a GS = 64 group shares between two steps).
+template <int GS>
 __device__ __forceinline__ void load_codes_row(RowCodes& rc, __amdgpu_buffer_rsrc_t packed,
                                                __amdgpu_buffer_rsrc_t scales, uint32_t vo_code,
                                                uint32_t vo_scale, int64_t k0) {
+    static_assert(GS == 16 || GS == 32 || GS == 64, "ternary group size 16, 32 or 64");
     const u32x3 v =
         __builtin_amdgcn_raw_buffer_load_b96(packed, vo_code, uniform_offset(k0 * 3 / 16), 0);
     rc.d[0] = v.x;
     rc.d[1] = v.y;
     rc.d[2] = v.z;
-    rc.s = __builtin_amdgcn_raw_buffer_load_b32(scales, vo_scale, uniform_offset(k0 / 16), 0);
+    const int so = uniform_offset(k0 * 2 / GS);
+    if constexpr (GS == 16) {
+        const u32x2 sv = __builtin_amdgcn_raw_buffer_load_b64(scales, vo_scale, so, 0);
+        rc.s[0] = sv[0];
+        rc.s[1] = sv[1];
+    } else if constexpr (GS == 32) {
+        rc.s[0] = __builtin_amdgcn_raw_buffer_load_b32(scales, vo_scale, so, 0);
+    } else {
+        rc.s[0] = __builtin_amdgcn_raw_buffer_load_b16(scales, vo_scale, so, 0);
+    }
 }
 
 template <int DT, int TN>
@@ -160,28 +173,34 @@ __device__ __forceinline__ void lut_reads_half(const RowCodes& rc, const char* l
 //   prep()    table reads and scale words for the codes loaded earlier (one step ahead);
 //   piece(p)  the p-th 16-byte piece (8 weights) from what prep() read.
 
-// Ternary E8: 8 codes (12 bytes) of the whole row per step; the thread expands 4 of them.
-template <int DT>
+// Ternary E8: 8 codes (12 bytes) of the whole row per step; the thread expands 4 of them
+// (32 k: two scale groups at GS 16, one at GS 32, half of one at GS 64).
+template <int DT, int GS>
 struct TernaryRowDecoder {
     static constexpr int kLoads = 2;  // loads issued by load()
     RowCodes rc;
     uint2 ml[4], mh[4];
-    uint32_t sw;
+    uint32_t sw[2];  // scale words of pieces 0-1 and 2-3
     const char* lut;
     uint32_t slot, vo_code, vo_scale;
     __amdgpu_buffer_rsrc_t pr, sr;
     int half;
     __device__ __forceinline__ void load(int64_t k0) {
-        load_codes_row(rc, pr, sr, vo_code, vo_scale, k0);
+        load_codes_row<GS>(rc, pr, sr, vo_code, vo_scale, k0);
     }
     __device__ __forceinline__ void prep() {
         lut_reads_half(rc, lut, slot, half, ml, mh);
-        uint32_t w0, w1;
-        scale_words<DT>(rc.s, w0, w1);
-        sw = half ? w1 : w0;
+        if constexpr (GS == 16) {
+            scale_words<DT>(half ? rc.s[1] : rc.s[0], sw[0], sw[1]);
+        } else {
+            uint32_t w0, w1;
+            scale_words<DT>(rc.s[0], w0, w1);
+            sw[0] = sw[1] = (GS == 32 && half) ? w1 : w0;
+        }
     }
     __device__ __forceinline__ uint4 piece(int p) const {
-        return make_uint4(ml[p].x & sw, ml[p].y & sw, mh[p].x & sw, mh[p].y & sw);
+        const uint32_t s = sw[p >> 1];
+        return make_uint4(ml[p].x & s, ml[p].y & s, mh[p].x & s, mh[p].y & s);
     }
     __device__ __forceinline__ void store(int p, char* tile, uint32_t wrow, int hf) const {
         *reinterpret_cast<uint4*>(tile + swz(wrow, 4u * hf + p)) = piece(p);
@@ -414,9 +433,10 @@ __device__ __forceinline__ uint32_t scale_word1(uint32_t s16) {
 // the ring is filled in position order (as the LDS DMA writes it).
 __device__ __forceinline__ uint32_t bwd_ring_row(uint32_t R) { return 4u * (R & 15u) + (R >> 4); }
 
-template <int BN>
+template <int BN, int GS>
 struct BwdStage {
-    static constexpr bool kScales = BN == 256;          // scales staged as well
+    // scales staged as well at BN = 256 and group size 32 (one 16-byte piece per row)
+    static constexpr bool kScales = BN == 256 && GS == 32;
     static constexpr uint32_t kCodeRow = BN * 3 / 16;   // code bytes per row and step
     static constexpr uint32_t kScaleRow = BN / 16;      // scale bytes per row and step
     static constexpr uint32_t kPiece = BN / 16;         // bytes per fetched piece
@@ -434,9 +454,9 @@ __device__ __forceinline__ void bwd_stage_dma(char* dst, __amdgpu_buffer_rsrc_t 
                                              vo, so, 0, 0);
 }
 
-template <int DT, int BN>
+template <int DT, int BN, int GS>
 struct TernaryBwdStagedDecoder {
-    using St = BwdStage<BN>;
+    using St = BwdStage<BN, GS>;
     static_assert(BN == 256 || BN == 128, "16- or 8-byte pieces");
     static_assert(BN == 256 || St::kSlots == 2, "init fills two slots through registers");
     static constexpr int kLoads = St::kScales ? 1 : 5;
@@ -479,7 +499,7 @@ struct TernaryBwdStagedDecoder {
         writer = St::kScales ? tid < 256 : t < 192u;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            vo_scale[q] = (bk.rows + (uint32_t)q) * srb + 2u * (((uint32_t)n0 + bk.col) / 32u);
+            vo_scale[q] = (bk.rows + (uint32_t)q) * srb + 2u * (((uint32_t)n0 + bk.col) / GS);
         ring = ring_lds;
     }
     __device__ __forceinline__ Piece fetch(int t) const {
@@ -510,6 +530,7 @@ struct TernaryBwdStagedDecoder {
     __device__ __forceinline__ void init(int64_t k0) {
         k_first = k0;
         if constexpr (BN == 256) {
+            load_scales(k0);  // scales not staged (group size other than 32): step 0's
             if (writer) {
                 for (int t = 0; t < St::kSlots; ++t) {
                     const int64_t n0 = k0 + (int64_t)t * kBK;
@@ -764,7 +785,7 @@ __device__ __forceinline__ void vm_wait_le() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-// FMT: kFmtTernary (group size 32), kFmt2Bit or kFmtRoot (group size GS2).  BWD = false:
+// FMT: kFmtTernary (group size GS2 = 16, 32 or 64), kFmt2Bit or kFmtRoot (GS2 = 8 .. 64).  BWD = false:
 // y[M, N] = x[M, K] . W[N, K]^T + bias; BWD = true: y[M, K] = x[M, N] . W[N, K] (backward
 // dX; x is grad_y, bias unused).  The weight matrix is W[N, K] in both.
 template <int DT, typename C, int FMT, int GS2, bool BWD>
@@ -823,7 +844,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
         (void*)x, (short)0, (int)(M * R * 2), kRsrcWord3);
     const uint32_t rowbytes = kTernary ? (uint32_t)(K * 3 / 16)
                                        : (FMT == kFmt2Bit ? (uint32_t)(K / 4) : (uint32_t)(K / 8));
-    const uint32_t srowbytes = kTernary ? (uint32_t)(K / 16) : (uint32_t)(K * 2 / GS2);
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS2);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
@@ -834,9 +855,9 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
     const uint32_t vo_scale = (uint32_t)(n0 + wrow) * srowbytes;
     const char* lut = reinterpret_cast<const char*>(lut_storage) + (kTernary ? kLutBaseOffset : 0);
     using FwdDec = std::conditional_t<
-        kTernary, TernaryRowDecoder<DT>,
+        kTernary, TernaryRowDecoder<DT, GS2>,
         std::conditional_t<FMT == kFmt2Bit, Bit2RowDecoder<DT, GS2>, RootRowDecoder<DT, GS2>>>;
-    using BwdDec = std::conditional_t<kTernary, TernaryBwdStagedDecoder<DT, C::BN>,
+    using BwdDec = std::conditional_t<kTernary, TernaryBwdStagedDecoder<DT, C::BN, GS2>,
                                       LowbitBwdStagedDecoder<DT, C::BN, FMT, GS2>>;
     using Dec = std::conditional_t<BWD, BwdDec, FwdDec>;
     constexpr bool kStagedDec = IsStaged<Dec>::value;
@@ -986,7 +1007,8 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
     if (M < 1 || N < 1 || K < kBK || K % kBK != 0) return false;
     if (bwd && N % kBK != 0) return false;  // the backward reduces over N
     const int64_t R = bwd ? N : K;
-    if (fmt == kFmtTernary ? gs != 32 : (gs != 8 && gs != 16 && gs != 32 && gs != 64))
+    if (fmt == kFmtTernary ? (gs != 16 && gs != 32 && gs != 64)
+                           : (gs != 8 && gs != 16 && gs != 32 && gs != 64))
         return false;
     if (fmt != kFmtTernary && fmt != kFmt2Bit && fmt != kFmtRoot) return false;
     if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 7u) || ((uintptr_t)scales & 7u))
@@ -994,7 +1016,7 @@ bool gemm_mfma_supported(const void* x, const uint8_t* packed, const uint16_t* s
     // 32-bit buffer offsets: the activation matrix and the weight buffers (plus one tile
     // of padding rows) must stay below 2^31 bytes
     const int64_t rowbytes = fmt == kFmtTernary ? K * 3 / 16 : (fmt == kFmt2Bit ? K / 4 : K / 8);
-    const int64_t srowbytes = fmt == kFmtTernary ? K / 16 : K * 2 / gs;
+    const int64_t srowbytes = K * 2 / gs;
     if ((M + CfgLarge::BM) * R * 2 >= (1ll << 31) || (N + CfgLarge::BN) * rowbytes >= (1ll << 31) ||
         (N + CfgLarge::BN) * srowbytes >= (1ll << 31))
         return false;
@@ -1067,9 +1089,21 @@ static hipError_t launch_fmt(const void* x, const uint8_t* packed, const uint16_
                              const void* bias, void* y, float* part, int splits, int64_t M,
                              int64_t N, int64_t K, int64_t gs, int fmt, hipStream_t stream,
                              const LoraEp& lora) {
-    if (fmt == kFmtTernary)
-        return launch_cfg<DT, C, kFmtTernary, 32, BWD>(x, packed, scales, bias, y, part, splits, M, N,
-                                                  K, stream, lora);
+    if (fmt == kFmtTernary) {
+        switch (gs) {
+        case 16:
+            return launch_cfg<DT, C, kFmtTernary, 16, BWD>(x, packed, scales, bias, y, part, splits,
+                                                          M, N, K, stream, lora);
+        case 32:
+            return launch_cfg<DT, C, kFmtTernary, 32, BWD>(x, packed, scales, bias, y, part, splits,
+                                                          M, N, K, stream, lora);
+        case 64:
+            return launch_cfg<DT, C, kFmtTernary, 64, BWD>(x, packed, scales, bias, y, part, splits,
+                                                          M, N, K, stream, lora);
+        default:
+            return hipErrorInvalidValue;
+        }
+    }
     if (fmt == kFmtRoot) {
         switch (gs) {
         case 8:

@@ -1640,7 +1640,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     int M, int64_t N, int64_t K, LoraEp lora) {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
     static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
-    static_assert(FMT != kFmtTernary || GS == 32, "ternary GEMV: group size 32");
+    static_assert(FMT != kFmtTernary || GS >= 16, "ternary group sizes are multiples of 16");
     // ternary: half-code masks (bank-sliced); 2-bit: nibble -> selector (32 copies); 1-bit:
     // code -> four selectors
     __shared__ uint4 lut_storage[FMT == kFmtTernary ? kLutValidStorageU4
@@ -1821,7 +1821,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
     int M, int64_t N, int64_t K, LoraEp lora) {
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
     static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
-    static_assert(FMT != kFmtTernary || GS == 32, "ternary GEMV: group size 32");
+    static_assert(FMT != kFmtTernary || GS >= 16, "ternary group sizes are multiples of 16");
     static_assert(R * 64 * 16 <= kB2sXBytes, "partial sums fit a wave's activation buffer");
     constexpr int L = 2 * R + 2;  // loads per round: codes and scales per tile, 2 of rows
     __shared__ uint4 lut_storage[FMT == kFmtTernary ? kLutValidStorageU4
@@ -2600,7 +2600,7 @@ bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scal
                       const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt,
                       int fmt) {
     if (fmt != kFmtTernary && fmt != kFmt2Bit && fmt != kFmtRoot) return false;
-    if (fmt == kFmtTernary && gs != 32) return false;
+    if (fmt == kFmtTernary && gs != 16 && gs != 32 && gs != 64) return false;
     if (dt != kBF16 && dt != kF16) return false;
     if (M < 1 || M > 16 || N < 1 || K < kB2mRound || K % kB2mRound != 0) return false;
     if (gs != 8 && gs != 16 && gs != 32 && gs != 64) return false;
@@ -2656,10 +2656,19 @@ hipError_t launch_gemv2m(const void* x, const uint8_t* packed, const uint16_t* s
                          const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                          int dt, hipStream_t stream, int fmt, const LoraEp& lora) {
     const int m = (int)M;
-    if (fmt == kFmtTernary)  // group size 32 only
+    if (fmt == kFmtTernary) {  // group sizes 16, 32, 64
+        if (gs == 16)
+            return dt == kBF16
+                       ? launch_gemv2m_t<kBF16, 16, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora)
+                       : launch_gemv2m_t<kF16, 16, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora);
+        if (gs == 64)
+            return dt == kBF16
+                       ? launch_gemv2m_t<kBF16, 64, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora)
+                       : launch_gemv2m_t<kF16, 64, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora);
         return dt == kBF16
                    ? launch_gemv2m_t<kBF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora)
                    : launch_gemv2m_t<kF16, 32, kFmtTernary>(x, packed, scales, bias, y, m, N, K, stream, lora);
+    }
     if (fmt == kFmtRoot)
         return dt == kBF16
                    ? launch_gemv2m_gs<kBF16, kFmtRoot>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
