@@ -128,6 +128,8 @@ def parse_args():
     ap.add_argument("--settle-s", type=float, default=0.5,
                     help="seconds of each leg's own launches run untimed right before its "
                          "timed region, after the warm-up steps (0: none)")
+    ap.add_argument("--gs-layers", type=int, default=8,
+                    help="layers of the ternary group-size leg (group 32 against 64; 0: skip)")
     ap.add_argument("--launch-probe", action="store_true",
                     help="only measure the cost of a decode-sized launch (a one-workgroup GEMV "
                          "and a one-element torch kernel, eager and replayed from a hipGraph) "
@@ -800,6 +802,109 @@ class E8Decoder:
         return nxt
 
 
+def bench_ternary_gs(torch, N_, dev, layers: int, steps: int, gs_list=(32, 64), Ms=(1, 4, 16),
+                     prefill_m: int = 2048) -> dict:
+    """Ternary E8 at the reference's other group sizes: one `layers`-layer Llama-3-8B-shaped
+    stack of fp32 N(0, 0.02) weights (seed 9900 + 7*layer + j) encoded at each group size
+    in `gs_list` (the reference's published decoder run uses ternary group 64,
+    reports/apple_m5_1b_to_27b_gpu_benchmark.json:23-24), timed as per-linear
+    ojx_e8t_gemm_fwd launches replayed from a hipGraph at the decode M, the prefill forward
+    and the backward dX at M = `prefill_m`; outputs of layer 0's q, gate and down checked
+    against an fp32 matmul of the decoded weights."""
+    from ojasx_amd import ops
+
+    lib = N_.lib()
+    stream = torch.cuda.current_stream()
+    ws_items = {}
+    for layer in range(layers):
+        for j, (name, N, K) in enumerate(LAYER_SHAPES):
+            g = torch.Generator(device=dev).manual_seed(9900 + 7 * layer + j)
+            w = torch.randn(N, K, generator=g, device=dev) * 0.02
+            for gs in gs_list:
+                packed, scales = ops.encode(w, gs)
+                ws_items.setdefault(gs, []).append(dict(packed=packed, scales=scales, name=name,
+                                                        N=N, K=K))
+            del w
+    torch.cuda.synchronize()
+
+    def replay_ms(launch_all, reps):
+        launch_all(stream.cuda_stream)
+        torch.cuda.synchronize()
+        cap = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            launch_all(torch.cuda.current_stream().cuda_stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        settle(torch, graph.replay, SETTLE_S / 2)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def leg(items, gs, M, bwd=False):
+        xin = (lambda it: it["N"]) if bwd else (lambda it: it["K"])
+        xout = (lambda it: it["K"]) if bwd else (lambda it: it["N"])
+        xs = {n: torch.randn(M, n, generator=torch.Generator(device=dev).manual_seed(9800 + M + n),
+                             device=dev).to(torch.bfloat16) for n in {xin(it) for it in items[:7]}}
+        ys = [torch.empty(M, xout(it), dtype=torch.bfloat16, device=dev) for it in items]
+        wss = [ops.workspace(ops.FMT_TERNARY, bwd, M, it["N"], it["K"], gs, torch.bfloat16, dev)
+               for it in items[:7]]
+        ws = max((w for w in wss if w is not None), key=lambda w: w.numel(), default=None)
+        ws_p, ws_n = (0, 0) if ws is None else (ws.data_ptr(), ws.numel())
+
+        def launch_all(h):
+            for it, y in zip(items, ys):
+                if bwd:
+                    N_.check(lib.ojx_e8t_gemm_bwd_dx(xs[it["N"]].data_ptr(), it["packed"].data_ptr(),
+                                                     it["scales"].data_ptr(), y.data_ptr(), M,
+                                                     it["N"], it["K"], gs, N_.BF16, ws_p, ws_n, h),
+                             "gemm_bwd_dx")
+                else:
+                    N_.check(lib.ojx_e8t_gemm_fwd(xs[it["K"]].data_ptr(), it["packed"].data_ptr(),
+                                                  it["scales"].data_ptr(), None, y.data_ptr(), M,
+                                                  it["N"], it["K"], gs, N_.BF16, ws_p, ws_n, h),
+                             "gemm_fwd")
+
+        ms = replay_ms(launch_all, steps)
+        worst = 0.0
+        for idx in (0, 4, 6):
+            it = items[idx]
+            wd = ops.decode(it["packed"], it["scales"], it["N"] * it["K"], gs,
+                            torch.bfloat16).view(it["N"], it["K"]).float()
+            ref = (xs[it["N"]].float() @ wd) if bwd else (xs[it["K"]].float() @ wd.t())
+            err = (ys[idx].float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+            worst = max(worst, err)
+        return ms, worst
+
+    out = {"layers": layers, "linears": 7 * layers, "prefill_M": prefill_m}
+    worst = 0.0
+    numel = sum(it["N"] * it["K"] for it in ws_items[gs_list[0]])
+    for gs in gs_list:
+        items = ws_items[gs]
+        wbytes = sum(it["packed"].numel() + 2 * it["scales"].numel() for it in items)
+        res = {"stack_weight_bytes": wbytes, "decode_per_linear": {}}
+        for M in Ms:
+            ms, err = leg(items, gs, M)
+            worst = max(worst, err)
+            res["decode_per_linear"][str(M)] = dict(ms=round(ms, 4),
+                                                    weight_GBs=round(wbytes / ms / 1e6, 1))
+        for key, bwd in (("prefill", False), ("backward_dx", True)):
+            ms, err = leg(items, gs, prefill_m, bwd)
+            worst = max(worst, err)
+            flops = 2.0 * prefill_m * numel
+            res[key] = dict(ms=round(ms, 3), TFLOPs=round(flops / ms / 1e9, 1),
+                            frac_mfma=round(flops / ms / 1e9 / BF16_MFMA_PEAK_TFLOPS, 4))
+        out["gs" + str(gs)] = res
+        log(f"ternary gs {gs}: decode M=1 {res['decode_per_linear'][str(Ms[0])]['ms']} ms, "
+            f"prefill {res['prefill']['TFLOPs']} TFLOP/s")
+    out["max_rel_err"] = worst
+    return out
+
+
 def bench_e2e(torch, dev, layers: int):
     """batch 4, 512 random prompt tokens, 128 greedy steps.  Decode steps are
     replayed from one captured hipGraph; the E8 linears of a decode step are also timed
@@ -1166,6 +1271,10 @@ def main() -> int:
         log(f"1-bit Root E8 ({args.e8b_layers}-layer stack)")
         result["e8_1bit"] = bench_e8b(torch, N_, dev, args.e8b_layers, args.steps, fmt="root")
         log(f"1-bit: decode M=16 {result['e8_1bit']['decode_per_linear']['16']['weight_GBs']} GB/s")
+    if args.gs_layers > 0:
+        torch.cuda.empty_cache()
+        log(f"ternary group sizes 32 / 64 ({args.gs_layers}-layer stack)")
+        result["ternary_gs"] = bench_ternary_gs(torch, N_, dev, args.gs_layers, args.steps)
     if not args.no_e2e:
         torch.cuda.empty_cache()
         log(f"end-to-end decoder ({args.e2e_layers} layers)")

@@ -206,7 +206,7 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
         }
         a.njobs = 1;
         a.M = (int)M;
-        e = ojx::launch_gemv_tile(a, (N + 15) / 16, K, dtype, s);
+        e = ojx::launch_gemv_tile(a, (N + 15) / 16, K, dtype, s, gs);
         break;
     }
     case kRouteGemv2m:

@@ -1968,22 +1968,29 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
 //
 // Stage of one round (each lane of a buffer->LDS load writes a fixed 16-byte slot, so the
 // placement is chosen through the piece each lane fetches): codes, row n's 12 pieces at
-// slots 12n + (p + n/4) mod 12; scales, row n's 4 pieces at 4n + (p + n/4) mod 4; then
-// MM activation rows of 128 pieces, piece p of row m at m * 128 + (p ^ m).  The 16 lanes of
-// a lane group then read 16 distinct bank groups.
+// slots 12n + (p + n/4) mod 12; scales at group size 32, row n's 4 pieces at 4n + (p + n/4)
+// mod 4 (group size 16: 8 pieces at 8n + (p + n/2) mod 8; group size 64: 2 pieces at
+// 2n + (p + n/8) mod 2); then MM activation rows of 128 pieces, piece p of row m at
+// m * 128 + (p ^ m).  The 16 lanes of a lane group then read 16 distinct bank groups.
 
 constexpr int kTileWaves = 4;
 constexpr uint32_t kTileRoundCodes = 16 * 192;  // one round's codes of 16 rows
 
+// Scale bytes of one round of one 16-row tile at group size gs (1024 k per row: 2048 / gs
+// bytes), in whole 1-KB loads: 2 KB at group size 16, 1 KB at 32, 1 KB at 64 (half used).
+__host__ __device__ constexpr uint32_t tile_scale_region(int gs) { return gs == 16 ? 2048u : 1024u; }
+
 // One wave's stage of one round for RT row tiles: the tiles' codes, their scales, then the
 // activations (shared by the tiles).
-template <int MM, int RT>
+template <int MM, int RT, int GS>
 struct TileStage {
+    static_assert(GS == 16 || GS == 32 || GS == 64, "group size 16, 32 or 64");
+    static constexpr uint32_t kScaleRegion = tile_scale_region(GS);
     static constexpr uint32_t kScales = RT * kTileRoundCodes;     // offset of the scales
-    static constexpr uint32_t kX = kScales + RT * 1024;           // offset of the activations
+    static constexpr uint32_t kX = kScales + RT * kScaleRegion;   // offset of the activations
     static constexpr int kXLoads = (145 * (MM - 1) + 140 + 63) / 64;  // 1-KB loads of them
     static constexpr uint32_t kBytes = kX + kXLoads * 1024;           // one round
-    static constexpr int kLoads = 4 * RT + kXLoads;               // 1-KB loads per round
+    static constexpr int kLoads = (3 + (int)kScaleRegion / 1024) * RT + kXLoads;  // per round
 };
 
 // One 16-byte-per-lane buffer->LDS load (1 KB per wave) into `dst`.  (Not a template: the
@@ -1993,12 +2000,13 @@ __device__ __forceinline__ void dma_1k(__amdgpu_buffer_rsrc_t r, char* dst, uint
 }
 
 // Issues round u's loads into `stg`: for each of the rt row tiles (rows row0 + 16 r) three
-// of codes and one of scales, then `xloads` of activations.
+// of codes and the scales (group size gs: one load, two at 16), then `xloads` of
+// activations.
 __device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
                                            __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t xr,
                                            uint32_t row0, uint32_t rowbytes, uint32_t srowbytes,
                                            uint32_t xrowbytes, int u, int lane, int xloads,
-                                           int M, int rt) {
+                                           int M, int rt, int gs) {
     for (int r = 0; r < rt; ++r) {
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
@@ -2008,11 +2016,25 @@ __device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
                    (row0 + 16u * r + n) * rowbytes + 192u * u + 16u * p);
         }
     }
+    const uint32_t sreg = tile_scale_region(gs);
     for (int r = 0; r < rt; ++r) {
-        const uint32_t n = (uint32_t)lane >> 2, q = (uint32_t)lane & 3u;
-        const uint32_t p = (q + 4u - (n / 4u) % 4u) % 4u;
-        dma_1k(sr, stg + kTileRoundCodes * rt + 1024 * r,
-               (row0 + 16u * r + n) * srowbytes + 64u * u + 16u * p);
+        char* const sdst = stg + kTileRoundCodes * rt + sreg * r;
+        if (gs == 32) {
+            const uint32_t n = (uint32_t)lane >> 2, q = (uint32_t)lane & 3u;
+            const uint32_t p = (q + 4u - (n / 4u) % 4u) % 4u;
+            dma_1k(sr, sdst, (row0 + 16u * r + n) * srowbytes + 64u * u + 16u * p);
+        } else if (gs == 16) {
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t n = 8u * h + ((uint32_t)lane >> 3), q = (uint32_t)lane & 7u;
+                const uint32_t p = (q - (n >> 1)) & 7u;
+                dma_1k(sr, sdst + 1024 * h, (row0 + 16u * r + n) * srowbytes + 128u * u + 16u * p);
+            }
+        } else {  // 64: 16 rows x 32 bytes from lanes 0..31; the others read zeros
+            const uint32_t n = ((uint32_t)lane >> 1) & 15u, q = (uint32_t)lane & 1u;
+            const uint32_t p = (q - (n >> 3)) & 1u;
+            dma_1k(sr, sdst, lane < 32 ? (row0 + 16u * r + n) * srowbytes + 32u * u + 16u * p
+                                       : 0xFFFFFFF0u);
+        }
     }
     // activations: row m's piece p at slot 145 m + p + 4 (p / 32) (the lane groups' 32-piece
     // runs 36 slots apart); unused slots and rows >= M read zeros
@@ -2022,7 +2044,7 @@ __device__ __forceinline__ void tile_issue(char* stg, __amdgpu_buffer_rsrc_t pr,
         const uint32_t off = (m < (uint32_t)M && blk < 4u && wi < 32u)
                                  ? m * xrowbytes + 2048u * u + 16u * (32u * blk + wi)
                                  : 0xFFFFFFF0u;
-        dma_1k(xr, stg + (kTileRoundCodes + 1024) * rt + 1024 * i, off);
+        dma_1k(xr, stg + (kTileRoundCodes + sreg) * rt + 1024 * i, off);
     }
 }
 
@@ -2044,11 +2066,12 @@ template <int RT> constexpr int tile_slots() { return RT == 1 ? 32 : 16; }
 // group's scale into the fp32 accumulators.  The table and activation reads of step
 // J + kTileAhead are issued before the MFMA of step J; two D registers alternate between
 // scale groups.
-template <int DT, int MM, int RT>
+template <int DT, int MM, int RT, int GS>
 struct TileRound {
     using G = LutGeom<tile_slots<RT>()>;
+    static constexpr int kSpg = GS / 8;   // steps per scale group
     uint32_t cd[RT][12];  // this lane's 32 codes of each row tile
-    uint32_t scw[RT][4];  // their 8 group scales (fp16 pairs)
+    uint32_t scw[RT][128 / GS];  // their 256 / GS group scales (fp16 pairs)
     const char* lut;
     const char* xa;   // this lane's A fragment of step 0 (activations or a zero run)
     uint32_t slot;
@@ -2075,7 +2098,7 @@ struct TileRound {
     template <int J>
     __device__ __forceinline__ void step(Pending& p, f32x4 (&d)[2][RT],
                                          float (&acc)[RT][MM]) const {
-        constexpr int r = J % kTileAhead, gi = J / 4;  // scale group of the step
+        constexpr int r = J % kTileAhead, gi = J / kSpg;  // scale group of the step
         const uint4 a = p.a[r];
         uint4 b[RT];
 #pragma unroll
@@ -2084,9 +2107,9 @@ struct TileRound {
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             f32x4& dg = d[gi & 1][t];
-            dg = mfma16<DT>(a, b[t], J % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dg);
+            dg = mfma16<DT>(a, b[t], J % kSpg == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dg);
         }
-        if constexpr (J % 4 == 3) {  // scale group gi complete: post-scale it
+        if constexpr (J % kSpg == kSpg - 1) {  // scale group gi complete: post-scale it
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
                 f32x4& dg = d[gi & 1][t];
@@ -2223,10 +2246,10 @@ __device__ __forceinline__ float lora_wave_sum(const float (&part)[MM][kLoraInli
 // RT: row tiles per wave (they share the activation stage and the A fragment reads); a
 // workgroup covers TPW * RT row tiles.
 // TW: waves per row tile (the tile's K / 1024 rounds are spread over them, U each).
-template <int DT, int MM, int U, int TPW, int RT, int TW>
+template <int DT, int MM, int U, int TPW, int RT, int TW, int GS>
 __global__ __launch_bounds__(64 * TW * TPW)
 __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(GemvLaunch args) {
-    using S = TileStage<MM, RT>;
+    using S = TileStage<MM, RT, GS>;
     constexpr int SL = tile_slots<RT>();
     using TileLut = LutGeom<SL>;
     constexpr int L = S::kLoads;
@@ -2263,7 +2286,7 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     const int64_t N = job.N, K = job.K;
     const int M = args.M;
     const int T = (int)(K / 1024);
-    const uint32_t rowbytes = (uint32_t)(K * 3 / 16), srowbytes = (uint32_t)(K / 16);
+    const uint32_t rowbytes = (uint32_t)(K * 3 / 16), srowbytes = (uint32_t)(K * 2 / GS);
     const uint32_t row0 = (uint32_t)(tile * 16);
     const int u0 = wt * U;
     const int nr = T - u0 < U ? (T - u0 > 0 ? T - u0 : 0) : U;  // rounds of this wave
@@ -2280,7 +2303,7 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     for (int i = 0; i < U; ++i)
         if (i < nr)
             tile_issue(wstage + i * S::kBytes, pr, sr, xr, row0, rowbytes, srowbytes,
-                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M, RT);
+                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M, RT, GS);
     // the adapter's rows of A for this wave's round (the waves of tile set 0 form u)
     const bool lora_in = kLoraIn && args.lora_inline && job.lora_r > 0;  // uniform
     const bool lora_wave = lora_in && sub == 0 && nr > 0;
@@ -2341,7 +2364,7 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
             else vm_wait_all();
         }
         const char* stg = wstage + i * S::kBytes;
-        TileRound<DT, MM, RT> r;
+        TileRound<DT, MM, RT, GS> r;
 #pragma unroll
         for (int tt = 0; tt < RT; ++tt) {
 #pragma unroll
@@ -2354,12 +2377,33 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
                 r.cd[tt][4 * t + 2] = v.z;
                 r.cd[tt][4 * t + 3] = v.w;
             }
-            const uint4 sc = *reinterpret_cast<const uint4*>(
-                stg + S::kScales + 1024 * tt + (4u * i16 + (((uint32_t)g + rq) & 3u)) * 16u);
-            r.scw[tt][0] = sc.x;
-            r.scw[tt][1] = sc.y;
-            r.scw[tt][2] = sc.z;
-            r.scw[tt][3] = sc.w;
+            // this lane's scales: the 2048 / GS bytes of its 256 k (GS 16: pieces 2g, 2g + 1;
+            // GS 32: piece g; GS 64: half g & 1 of piece g / 2)
+            const char* const sreg = stg + S::kScales + S::kScaleRegion * tt;
+            if constexpr (GS == 32) {
+                const uint4 sc = *reinterpret_cast<const uint4*>(
+                    sreg + (4u * i16 + (((uint32_t)g + rq) & 3u)) * 16u);
+                r.scw[tt][0] = sc.x;
+                r.scw[tt][1] = sc.y;
+                r.scw[tt][2] = sc.z;
+                r.scw[tt][3] = sc.w;
+            } else if constexpr (GS == 16) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t pos = (2u * (uint32_t)g + h + ((uint32_t)i16 >> 1)) & 7u;
+                    const uint4 sc = *reinterpret_cast<const uint4*>(sreg + 128u * i16 + 16u * pos);
+                    r.scw[tt][4 * h] = sc.x;
+                    r.scw[tt][4 * h + 1] = sc.y;
+                    r.scw[tt][4 * h + 2] = sc.z;
+                    r.scw[tt][4 * h + 3] = sc.w;
+                }
+            } else {
+                const uint32_t pos = (((uint32_t)g >> 1) + ((uint32_t)i16 >> 3)) & 1u;
+                const uint2 sc = *reinterpret_cast<const uint2*>(
+                    sreg + 32u * i16 + 16u * pos + 8u * ((uint32_t)g & 1u));
+                r.scw[tt][0] = sc.x;
+                r.scw[tt][1] = sc.y;
+            }
         }
         r.lut = lut;
         r.xa = a_live ? stg + S::kX + xa0 : zbase;
@@ -2725,7 +2769,8 @@ bool gemv_tile_lora_inline_ok(int64_t M, int64_t N, int64_t K, int64_t rank,
 bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
     if (dt != kBF16 && dt != kF16) return false;
-    if (gs != 32 || N < 1 || K < 1024 || K % 1024 != 0 || gemv_tile_rounds(M, K) == 0)
+    if ((gs != 16 && gs != 32 && gs != 64) || N < 1 || K < 1024 || K % 1024 != 0 ||
+        gemv_tile_rounds(M, K) == 0)
         return false;
     if (((uintptr_t)x & 15u) || ((uintptr_t)packed & 15u) || ((uintptr_t)scales & 15u) ||
         ((uintptr_t)y & 1u))
@@ -2751,9 +2796,9 @@ GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool ti
 }
 
 // `wgs` workgroups of TPW * RT row tiles each (each job's tiles start a new workgroup)
-template <int DT, int MM, int U, int TPW, int RT, int TW = kTileWaves>
+template <int DT, int GS, int MM, int U, int TPW, int RT, int TW = kTileWaves>
 static hipError_t launch_tile_grid(const GemvLaunch& a, int64_t wgs, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT, TW>), dim3((unsigned)wgs),
+    hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT, TW, GS>), dim3((unsigned)wgs),
                        dim3(64 * TW * TPW), 0, s, a);
     return hipGetLastError();
 }
@@ -2761,43 +2806,52 @@ static hipError_t launch_tile_grid(const GemvLaunch& a, int64_t wgs, hipStream_t
 // tpw: row tiles per workgroup, rt of them per wave.  Two wave sets per workgroup exist for
 // U == 1 at M == 1 only (gemv_tile_per_wg), two tiles per wave for U == 1 at M > 1 only
 // (gemv_tile_rows_per_wave).
-template <int DT>
+template <int DT, int GS>
 static hipError_t launch_tile_dt(const GemvLaunch& a, int64_t wgs, int U, int tpw, int rt,
                                  hipStream_t s) {
     if (a.M == 1) {
         if (rt != 1) return hipErrorInvalidValue;
-        if (U == 1) return tpw == 2 ? launch_tile_grid<DT, 1, 1, 2, 1>(a, wgs, s)
-                                    : launch_tile_grid<DT, 1, 1, 1, 1>(a, wgs, s);
+        if (U == 1) return tpw == 2 ? launch_tile_grid<DT, GS, 1, 1, 2, 1>(a, wgs, s)
+                                    : launch_tile_grid<DT, GS, 1, 1, 1, 1>(a, wgs, s);
         if (tpw != 1) return hipErrorInvalidValue;
         // a tile's rounds over 8 or 16 waves, one each (the same stage bytes per workgroup
         // as 4 waves of 2 or 4 rounds, but more waves per SIMD to run them)
-        if (U == 2) return launch_tile_grid<DT, 1, 1, 1, 1, 8>(a, wgs, s);
-        if (U == 4) return launch_tile_grid<DT, 1, 1, 1, 1, 16>(a, wgs, s);
+        if (U == 2) return launch_tile_grid<DT, GS, 1, 1, 1, 1, 8>(a, wgs, s);
+        if (U == 4) return launch_tile_grid<DT, GS, 1, 1, 1, 1, 16>(a, wgs, s);
         return hipErrorInvalidValue;
     }
     if (tpw != rt) return hipErrorInvalidValue;
-    if (U == 1) return rt == 2 ? launch_tile_grid<DT, 4, 1, 1, 2>(a, wgs, s)
-                               : launch_tile_grid<DT, 4, 1, 1, 1>(a, wgs, s);
-    if (U == 2 && rt == 1) return launch_tile_grid<DT, 4, 1, 1, 1, 8>(a, wgs, s);
+    if (U == 1) return rt == 2 ? launch_tile_grid<DT, GS, 4, 1, 1, 2>(a, wgs, s)
+                               : launch_tile_grid<DT, GS, 4, 1, 1, 1>(a, wgs, s);
+    if (U == 2 && rt == 1) return launch_tile_grid<DT, GS, 4, 1, 1, 1, 8>(a, wgs, s);
     return hipErrorInvalidValue;
 }
 
+// Grouped launches (group size 32).
 static hipError_t launch_tile_plan(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                                    int dt, hipStream_t s) {
-    return dt == kBF16 ? launch_tile_dt<kBF16>(a, wgs, p.U, p.tpw, p.rt, s)
-                       : launch_tile_dt<kF16>(a, wgs, p.U, p.tpw, p.rt, s);
+    return dt == kBF16 ? launch_tile_dt<kBF16, 32>(a, wgs, p.U, p.tpw, p.rt, s)
+                       : launch_tile_dt<kF16, 32>(a, wgs, p.U, p.tpw, p.rt, s);
+}
+template <int GS>
+static hipError_t launch_gemv_tile_gs(const GemvLaunch& a, int64_t wgs, int U, int tpw, int rt,
+                                      int dt, hipStream_t s) {
+    return dt == kBF16 ? launch_tile_dt<kBF16, GS>(a, wgs, U, tpw, rt, s)
+                       : launch_tile_dt<kF16, GS>(a, wgs, U, tpw, rt, s);
 }
 
-// One job of `tiles` row tiles (per-linear launch).
+// One job of `tiles` row tiles (per-linear launch) at group size gs (16, 32 or 64).
 hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t tiles, int64_t Kmax, int dt,
-                            hipStream_t s) {
+                            hipStream_t s, int64_t gs) {
     if (tiles <= 0) return hipSuccess;
     const int U = gemv_tile_rounds(a.M, Kmax);
     if (tiles > 0x7FFFFFFF || U == 0) return hipErrorInvalidValue;
     const int rt = gemv_tile_rows_per_wave(a.M, tiles, U);
     const int tpw = (U == 1 ? gemv_tile_per_wg(a.M, tiles) : 1) * rt;
-    return dt == kBF16 ? launch_tile_dt<kBF16>(a, (tiles + tpw - 1) / tpw, U, tpw, rt, s)
-                       : launch_tile_dt<kF16>(a, (tiles + tpw - 1) / tpw, U, tpw, rt, s);
+    const int64_t wgs = (tiles + tpw - 1) / tpw;
+    if (gs == 16) return launch_gemv_tile_gs<16>(a, wgs, U, tpw, rt, dt, s);
+    if (gs == 64) return launch_gemv_tile_gs<64>(a, wgs, U, tpw, rt, dt, s);
+    return launch_gemv_tile_gs<32>(a, wgs, U, tpw, rt, dt, s);
 }
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,

@@ -143,8 +143,8 @@ hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int 
 int gemv_tile_rounds(int64_t M, int64_t Kmax);
 bool gemv_tile_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
                          const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
-hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t wgs, int64_t Kmax, int dt,
-                            hipStream_t stream);
+hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t tiles, int64_t Kmax, int dt,
+                            hipStream_t stream, int64_t gs = 32);
 // Row tiles per workgroup of a one-job staged-tile launch over `tiles` row tiles.
 int gemv_tile_per_wg(int64_t M, int64_t tiles);
 
