@@ -243,6 +243,17 @@ int ojx_e8_cs_project(const void* x, int f64, int64_t nvec, void* out, void* str
  * project(w / s) * s. */
 int ojx_e8_ste_quantize(const float* w, int64_t numel, float* out, void* stream);
 
+/* The projection for x and out in `dtype`: OJX_F32 or OJX_F64 as above, OJX_F16 or OJX_BF16
+ * as the reference's torch expressions evaluate on such a tensor (lattice.py:180-203 in the
+ * tensor's dtype): every elementwise op rounded to the dtype, sums over the 8 coordinates
+ * added in fp32 and rounded once (the parity test reads that rounded sum). */
+int ojx_e8_cs_project_dt(const void* x, int dtype, int64_t nvec, void* out, void* stream);
+
+/* The STE forward for w and out in `dtype` (OJX_F32, OJX_F16 or OJX_BF16), every op of
+ * lattice.py:855-865 rounded to the dtype: norm, / sqrt(8), + 1e-8 (an fp16 zero 8-vector
+ * gets s = 0 and NaN outputs, as the reference does), w / s, the projection, * s. */
+int ojx_e8_ste_quantize_dt(const void* w, int dtype, int64_t numel, void* out, void* stream);
+
 /* ---------------------------------------------------------------- grouped decode GEMV
  *
  * One launch runs the decode GEMV (batch M <= 16) of several independent linears: a

@@ -672,6 +672,32 @@ __attribute__((visibility("default"))) int ojx_e8_cs_project(const void* x, int 
                 "e8 cs_project launch");
 }
 
+__attribute__((visibility("default"))) int ojx_e8_cs_project_dt(const void* x, int dtype,
+                                                                int64_t nvec, void* out,
+                                                                void* stream) {
+    if (nvec < 0) return fail(OJX_EINVAL, "negative vector count %lld", (long long)nvec);
+    if (dtype != OJX_F32 && dtype != OJX_F64 && dtype != OJX_F16 && dtype != OJX_BF16)
+        return fail(OJX_EDTYPE, "unknown dtype code %d", dtype);
+    if (nvec == 0) return OJX_OK;
+    if (!x || !out) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_cs_project_dt(x, dtype, nvec, out, (hipStream_t)stream),
+                "e8 cs_project launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8_ste_quantize_dt(const void* w, int dtype,
+                                                                  int64_t numel, void* out,
+                                                                  void* stream) {
+    if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);
+    if (dtype != OJX_F32 && dtype != OJX_F16 && dtype != OJX_BF16)
+        return fail(OJX_EDTYPE, "ste_quantize takes F32, F16 or BF16 weights (got %d)", dtype);
+    if (numel == 0) return OJX_OK;
+    if (!w || !out) return fail(OJX_EINVAL, "null pointer");
+    if (int r = check_device()) return r;
+    return done(ojx::launch_ste_quantize_dt(w, dtype, numel, out, (hipStream_t)stream),
+                "e8 ste_quantize launch");
+}
+
 __attribute__((visibility("default"))) int ojx_e8_ste_quantize(const float* w, int64_t numel,
                                                                float* out, void* stream) {
     if (numel < 0) return fail(OJX_EINVAL, "negative numel %lld", (long long)numel);

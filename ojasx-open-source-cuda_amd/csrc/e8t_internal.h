@@ -33,6 +33,12 @@ hipError_t launch_fwht32(const void* x, int dt, int64_t blocks, void* y, hipStre
 hipError_t launch_cs_project(const void* x, bool f64, int64_t nvec, void* out,
                              hipStream_t stream);
 hipError_t launch_ste_quantize(const float* w, int64_t numel, float* out, hipStream_t stream);
+// The same for dtype dt (kF32, kF64 for the projection, kF16, kBF16: every op rounded to the
+// half type, as torch evaluates the reference on such tensors).
+hipError_t launch_cs_project_dt(const void* x, int dt, int64_t nvec, void* out,
+                                hipStream_t stream);
+hipError_t launch_ste_quantize_dt(const void* w, int dt, int64_t numel, void* out,
+                                  hipStream_t stream);
 
 // 2-bit decode GEMV (M <= 4, bf16/fp16, K % 1024 == 0, gs in {8, 16, 32, 64}, 16-byte
 // aligned buffers).

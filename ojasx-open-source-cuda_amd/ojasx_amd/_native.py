@@ -16,7 +16,7 @@ import torch
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libojasx_e8t.so")
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, F64 = 0, 1, 2, 3
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
@@ -45,6 +45,8 @@ EXPORTS = (
     "ojx_fwht32",
     "ojx_e8_cs_project",
     "ojx_e8_ste_quantize",
+    "ojx_e8_cs_project_dt",
+    "ojx_e8_ste_quantize_dt",
 )
 
 
@@ -149,6 +151,10 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8_cs_project.argtypes = [_P, _INT, _I64, _P, _P]
             L.ojx_e8_ste_quantize.restype = _INT
             L.ojx_e8_ste_quantize.argtypes = [_P, _I64, _P, _P]
+            L.ojx_e8_cs_project_dt.restype = _INT
+            L.ojx_e8_cs_project_dt.argtypes = [_P, _INT, _I64, _P, _P]
+            L.ojx_e8_ste_quantize_dt.restype = _INT
+            L.ojx_e8_ste_quantize_dt.argtypes = [_P, _INT, _I64, _P, _P]
             _lib = L
     return _lib
 

@@ -92,8 +92,10 @@ def conway_sloane_e8_project(x: torch.Tensor, prefer_native: bool = True) -> tor
     One HIP kernel, with the arithmetic of the reference's torch path (round half to even;
     an odd sum moves the first coordinate with the largest rounding error towards x; D8
     wins ties of the squared distances).  ``prefer_native`` selected the reference's CPU
-    kernel, which rounds halves away from zero; it is accepted and ignored.  fp32 and fp64
-    tensors; CPU tensors are processed on the current GPU and returned on the CPU."""
+    kernel, which rounds halves away from zero; it is accepted and ignored.  fp32, fp64, and
+    fp16 / bf16 tensors (every op rounded to the dtype, as the reference's torch expressions
+    compute on such a tensor); CPU tensors are processed on the current GPU and returned on
+    the CPU."""
     del prefer_native
     if x.shape[-1] != 8:
         raise ValueError(f"Last dimension must be 8 for E8 lattice (got {x.shape[-1]}).")
@@ -105,8 +107,9 @@ def conway_sloane_e8_project(x: torch.Tensor, prefer_native: bool = True) -> tor
 
 class _E8STEFunction(torch.autograd.Function):
     """Straight-through E8 weight quantizer (lattice.py:853-869): the forward snaps each flat
-    8-vector, scaled by its norm / sqrt(8) + 1e-8, to E8 (one HIP kernel, fp32 weights);
-    the backward passes the gradient through unchanged."""
+    8-vector, scaled by its norm / sqrt(8) + 1e-8, to E8 (one HIP kernel, in the weight's
+    dtype: fp32, or fp16 / bf16 with every op rounded to it as in the reference); the
+    backward passes the gradient through unchanged."""
 
     @staticmethod
     def forward(ctx, w: torch.Tensor) -> torch.Tensor:

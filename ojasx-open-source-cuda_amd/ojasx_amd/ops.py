@@ -777,18 +777,21 @@ fwht32.register_autograd(_fwht32_backward, setup_context=_fwht32_setup)
 
 @torch.library.custom_op(f"{_NS}::cs_project", mutates_args=())
 def cs_project(x: torch.Tensor) -> torch.Tensor:
-    """Conway-Sloane nearest E8 point of every 8-vector of x (fp32 or fp64, last dim 8),
-    as conway_sloane_e8_project's torch path computes it (lattice.py:180-203)."""
+    """Conway-Sloane nearest E8 point of every 8-vector of x (last dim 8) as
+    conway_sloane_e8_project's torch path computes it (lattice.py:180-203) in x's dtype:
+    float32, float64, or float16 / bfloat16 with every op rounded to that dtype."""
     dev = N.require_device(x)
-    if x.dtype not in (torch.float32, torch.float64):
-        raise RuntimeError(f"cs_project supports float32 and float64 tensors (got {x.dtype})")
+    if x.dtype not in (torch.float32, torch.float64, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"cs_project supports float32, float64, float16 and bfloat16 "
+                           f"tensors (got {x.dtype})")
     if x.shape[-1] != 8:
         raise RuntimeError(f"last dimension must be 8 (got {x.shape[-1]})")
     xc = x.contiguous()
     out = torch.empty_like(xc)
+    code = N.F64 if x.dtype == torch.float64 else N.DTYPE_CODE[x.dtype]
     with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8_cs_project(N.ptr(xc), int(x.dtype == torch.float64),
-                                          xc.numel() // 8, N.ptr(out), N.stream_handle(dev)),
+        N.check(N.lib().ojx_e8_cs_project_dt(N.ptr(xc), code, xc.numel() // 8, N.ptr(out),
+                                             N.stream_handle(dev)),
                 "e8 cs_project")
     return out
 
@@ -800,15 +803,17 @@ def _(x):
 
 @torch.library.custom_op(f"{_NS}::ste_quantize", mutates_args=())
 def ste_quantize(w: torch.Tensor) -> torch.Tensor:
-    """Forward of _E8STEFunction (lattice.py:853-865) on fp32 weights."""
+    """Forward of _E8STEFunction (lattice.py:853-865) in w's dtype (float32, float16 or
+    bfloat16; the half types round every op as the reference's torch expressions do)."""
     dev = N.require_device(w)
-    if w.dtype != torch.float32:
-        raise RuntimeError(f"ste_quantize supports float32 weights (got {w.dtype})")
+    if w.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"ste_quantize supports float32, float16 and bfloat16 weights "
+                           f"(got {w.dtype})")
     wc = w.contiguous()
     out = torch.empty_like(wc)
     with torch.cuda.device(dev):
-        N.check(N.lib().ojx_e8_ste_quantize(N.ptr(wc), wc.numel(), N.ptr(out),
-                                            N.stream_handle(dev)),
+        N.check(N.lib().ojx_e8_ste_quantize_dt(N.ptr(wc), N.DTYPE_CODE[w.dtype], wc.numel(),
+                                               N.ptr(out), N.stream_handle(dev)),
                 "e8 ste_quantize")
     return out
 

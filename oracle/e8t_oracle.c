@@ -812,6 +812,78 @@ OJO_API void ojo_e8r_quantize8_array(const float* v, int64_t nvec, int32_t* code
 OJO_CS_DEFINE(ojo_e8_cs_project_f32, float, rintf, fabsf)
 OJO_CS_DEFINE(ojo_e8_cs_project_f64, double, rint, fabs)
 
+/* The same projection on fp16 (half = 0) or bf16 (half = 1) tensors, as torch evaluates the
+ * reference's expressions (lattice.py:180-203) on such a tensor: every elementwise op is
+ * computed in fp32 and rounded to the tensor's type; a sum over the last dim adds the
+ * fp32 values left to right and rounds once (the parity test reads that rounded sum, so a
+ * sum that rounds to an even number counts as even); x - 0.5, the parity move f +- 1 and
+ * c + 0.5 are each rounded, and so are x - c and its square.  Values are fp32 holding
+ * exact half values; outputs too. */
+static float ojo_rnd_half(float v, int half) {
+    return half ? ojo_bf16_to_f32(ojo_f32_to_bf16(v)) : ojo_f16_to_f32(ojo_f32_to_f16(v));
+}
+
+static void ojo_cs_half_candidate(const float* x, int shifted, int half, float out[8]) {
+    float f[8], xs[8];
+    float sum = 0.0f;
+    int worst = 0;
+    float werr = 0.0f;
+    for (int i = 0; i < 8; ++i) {
+        xs[i] = shifted ? ojo_rnd_half(x[i] - 0.5f, half) : x[i];
+        f[i] = rintf(xs[i]);
+        sum = sum + f[i];
+        float err = ojo_rnd_half(fabsf(xs[i] - f[i]), half);
+        if (i == 0 || err > werr) { werr = err; worst = i; }
+    }
+    long isum = (long)ojo_rnd_half(sum, half);
+    if (isum % 2 != 0) {
+        float d = xs[worst] - f[worst];
+        f[worst] = ojo_rnd_half(f[worst] + ((d < 0) ? -1.0f : 1.0f), half);
+    }
+    for (int i = 0; i < 8; ++i) out[i] = shifted ? ojo_rnd_half(f[i] + 0.5f, half) : f[i];
+}
+
+OJO_API void ojo_e8_cs_project_half(const float* x, float* out, int64_t nvec, int half) {
+    for (int64_t b = 0; b < nvec; ++b) {
+        const float* v = x + 8 * b;
+        float c1[8], c2[8];
+        ojo_cs_half_candidate(v, 0, half, c1);
+        ojo_cs_half_candidate(v, 1, half, c2);
+        float d1 = 0.0f, d2 = 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            float a = ojo_rnd_half(v[i] - c1[i], half), bb = ojo_rnd_half(v[i] - c2[i], half);
+            d1 = d1 + ojo_rnd_half(a * a, half);
+            d2 = d2 + ojo_rnd_half(bb * bb, half);
+        }
+        d1 = ojo_rnd_half(d1, half);
+        d2 = ojo_rnd_half(d2, half);
+        const float* ch = (d1 <= d2) ? c1 : c2;
+        for (int i = 0; i < 8; ++i) out[8 * b + i] = ch[i];
+    }
+}
+
+/* _E8STEFunction.forward on fp16 / bf16 weights (fp32 holding exact half values), every op
+ * rounded to the type: n = torch.norm(w8) (fp32 squares added left to right, sqrt, one
+ * rounding), s = rnd(rnd(n / fp32(sqrt 8)) + fp32(1e-8)) (an fp16 zero vector gets s = 0
+ * and NaN outputs, as the reference does), v = rnd(w / s), p = project(v) in the type,
+ * out = rnd(p * s). */
+OJO_API void ojo_e8_ste_quantize_half(const float* w, int64_t numel, float* out, int half) {
+    int64_t nvec = (numel + 7) / 8;
+    for (int64_t b = 0; b < nvec; ++b) {
+        float x[8], v[8], p[8];
+        for (int i = 0; i < 8; ++i) x[i] = (8 * b + i < numel) ? w[8 * b + i] : 0.0f;
+        float acc = x[0] * x[0];
+        for (int i = 1; i < 8; ++i) acc = acc + x[i] * x[i];
+        float n = ojo_rnd_half(sqrtf(acc), half);
+        float s = ojo_rnd_half(n / 2.8284271247461903f, half);
+        s = ojo_rnd_half(s + 9.99999993922529e-09f, half);
+        for (int i = 0; i < 8; ++i) v[i] = ojo_rnd_half(x[i] / s, half);
+        ojo_e8_cs_project_half(v, p, 1, half);
+        for (int i = 0; i < 8; ++i)
+            if (8 * b + i < numel) out[8 * b + i] = ojo_rnd_half(p[i] * s, half);
+    }
+}
+
 /* _E8STEFunction.forward (lattice.py:853-865) on fp32 weights: flat, zero padded to a
  * multiple of 8; per 8-vector s = torch.norm(w8)/sqrt(8) + 1e-8 (the CPU norm order),
  * out = project(w8 / s) * s; the first numel values. */

@@ -116,6 +116,10 @@ def lib() -> ctypes.CDLL:
         L.ojo_e8_cs_project_f64.argtypes = [_P, _P, _I64]
         L.ojo_e8_ste_quantize_f32.restype = None
         L.ojo_e8_ste_quantize_f32.argtypes = [_P, _I64, _P]
+        L.ojo_e8_cs_project_half.restype = None
+        L.ojo_e8_cs_project_half.argtypes = [_P, _P, _I64, ctypes.c_int]
+        L.ojo_e8_ste_quantize_half.restype = None
+        L.ojo_e8_ste_quantize_half.argtypes = [_P, _I64, _P, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -502,4 +506,21 @@ def ste_quantize(w: np.ndarray) -> np.ndarray:
     a = np.ascontiguousarray(w, dtype=np.float32)
     out = np.empty_like(a)
     lib().ojo_e8_ste_quantize_f32(_ptr(a), a.size, _ptr(out))
+    return out
+
+
+def cs_project_half(x: np.ndarray, bf16: bool) -> np.ndarray:
+    """The projection on an fp16 (bf16=False) or bf16 tensor, every op rounded to the type;
+    ``x`` holds the tensor's values as fp32 (exact), the result likewise."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().ojo_e8_cs_project_half(_ptr(a), _ptr(out), a.size // 8, int(bf16))
+    return out
+
+
+def ste_quantize_half(w: np.ndarray, bf16: bool) -> np.ndarray:
+    """_E8STEFunction.forward on fp16 (bf16=False) or bf16 weights held as fp32 values."""
+    a = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().ojo_e8_ste_quantize_half(_ptr(a), a.size, _ptr(out), int(bf16))
     return out

@@ -1,5 +1,6 @@
 """Pins the Conway-Sloane projection and the QAT straight-through quantizer of the CPU
-oracle (oracle/e8t_oracle.c: ojo_e8_cs_project_*, ojo_e8_ste_quantize_f32).
+oracle (oracle/e8t_oracle.c: ojo_e8_cs_project_*, ojo_e8_ste_quantize_f32 and the fp16 /
+bf16 forms ojo_e8_cs_project_half, ojo_e8_ste_quantize_half).
 
 The reference's projection (ojasx2/math/lattice.py:180-203) and _E8STEFunction
 (:853-865) are torch expressions: each check evaluates them with torch itself, bit for
@@ -96,3 +97,43 @@ def test_ste_quantize_matches_torch_expression():
         w = torch.randn(*shape, generator=g) * 0.05
         w.view(-1)[: min(4, w.numel())] = 0.0
         assert np.array_equal(O.ste_quantize(w.numpy()), ste_torch(w).numpy())
+
+
+def _half_inputs(dtype, n=200_000, seed=5):
+    x = _inputs(torch.float32, n, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    # large magnitudes, where x - 0.5, f +- 1 and the rounded parity sum lose precision in
+    # the half type (fp16 integers are exact to 2048, bf16 ones to 256)
+    x[4000:6000] = torch.randn(2000, 8, generator=g) * 400
+    x[6000:7000] = torch.round(torch.randn(1000, 8, generator=g) * 300)
+    x[7000:7100] = torch.tensor([256.0, 1, 1, 1, 1, 1, 1, 1])
+    x[7100:7200] = torch.tensor([2048.0, 1, 1, 1, 1, 1, 1, 0.5])
+    x[7200:7300] = torch.tensor([1000.5, -3.5, 2.5, 0.5, -0.5, 7.5, 1.5, 0.25])
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_cs_project_half_matches_torch_path(dtype):
+    # the reference's torch path evaluated by torch on an fp16 / bf16 tensor: every op
+    # rounds to the tensor's dtype (lattice.py:180-203)
+    x = _half_inputs(dtype)
+    got = O.cs_project_half(x.float().numpy(), dtype == torch.bfloat16)
+    ref = cs_torch(x).float().numpy()
+    assert np.array_equal(got, ref, equal_nan=True)
+    # the half rounding matters: the fp32 projection of the same values differs somewhere
+    assert not np.array_equal(O.cs_project(x.float().numpy()), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_ste_quantize_half_matches_torch_expression(dtype):
+    g = torch.Generator().manual_seed(6)
+    for shape in ((1000, 37), (64, 64), (3, 5), (1, 1), (256, 256)):
+        w = (torch.randn(*shape, generator=g) * 0.05).to(dtype)
+        w.view(-1)[: min(4, w.numel())] = 0.0
+        if w.numel() >= 64:
+            w.view(-1)[8:16] = 0.0          # a zero 8-vector: s = rnd(0 + 1e-8) (0 in fp16)
+            w.view(-1)[16:24] = 3e-5        # a tiny one
+            w.view(-1)[24:32] = torch.tensor([60.0, 1e-3, 0, 0, 0, 0, 0, -2.0])
+        got = O.ste_quantize_half(w.float().numpy(), dtype == torch.bfloat16)
+        ref = ste_torch(w).float().numpy()
+        assert np.array_equal(got, ref, equal_nan=True), shape
