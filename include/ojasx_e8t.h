@@ -308,6 +308,19 @@ int ojx_e8t_gemv_grouped_plan(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int 
 int ojx_e8t_gemv_grouped(const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev,
                          int njobs, const void* x, void* y, int64_t M, int dtype, void* stream);
 
+/* The same for 2-bit E8 linears (E8LatticePacker, the reference's default bitrate,
+ * lattice.py:210-279, 735, 906): `packed` is [N * K / 4] bytes, `scales` [N * K / gs] fp16,
+ * every job with the one group size gs (8, 16, 32 or 64).  Requirements per job: K % 256 ==
+ * 0, 1 <= M <= 16, packed / scales / x 16-byte aligned; adapters as above (their
+ * down-projections run before the GEMV).  M <= 4 with every K a multiple of 1024 runs the
+ * post-scaled 2-bit kernel, otherwise the B-operand kernel.  No counterpart in the
+ * reference, which decodes each linear to a dense matrix (lattice.py:610-624). */
+int ojx_e8_gemv_grouped_plan(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs,
+                             int dtype, int64_t* grid);
+int ojx_e8_gemv_grouped(const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev,
+                        int njobs, const void* x, void* y, int64_t M, int64_t gs, int dtype,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

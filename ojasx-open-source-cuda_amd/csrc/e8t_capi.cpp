@@ -360,6 +360,30 @@ static_assert(sizeof(ojx_e8t_gemv_job) == sizeof(ojx::GemvJob), "job layout");
 static_assert(offsetof(ojx_e8t_gemv_job, wg_begin) == offsetof(ojx::GemvJob, wg_begin),
               "job layout");
 
+// The adapters' down-projections u = scaling * x @ A of a job table, before its GEMV:
+// consecutive adapter jobs on the same activations (same x, same K) share a launch.
+static int lora_downs(const ojx_e8t_gemv_job* jobs, int njobs, const void* x, int64_t M,
+                      int dtype, void* stream) {
+    for (int i = 0; i < njobs;) {
+        if (jobs[i].lora_r <= 0) { ++i; continue; }
+        const void* xi = jobs[i].x ? jobs[i].x : x;
+        const int64_t Ki = jobs[i].K;
+        ojx::LoraDown items[ojx::kLoraDownItems];
+        int n = 0;
+        for (; i < njobs && n < ojx::kLoraDownItems; ++i) {
+            const ojx_e8t_gemv_job& j = jobs[i];
+            if (j.lora_r <= 0) continue;
+            if ((j.x ? j.x : x) != xi || j.K != Ki) break;
+            items[n++] = ojx::LoraDown{j.lora_a, const_cast<float*>(j.lora_u), j.lora_r,
+                                       j.lora_ldu ? j.lora_ldu : j.lora_r, j.lora_scaling};
+        }
+        const hipError_t e = ojx::launch_lora_down(xi, M, Ki, dtype, items, n,
+                                                   (hipStream_t)stream);
+        if (e != hipSuccess) return fail(OJX_EHIP, "lora_down launch: %s", hipGetErrorString(e));
+    }
+    return OJX_OK;
+}
+
 static int plan_jobs(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int dtype, int64_t* grid,
                      ojx::GemvPlan* plan, bool fill) {
     if (njobs <= 0 || !jobs) return fail(OJX_EINVAL, "empty job list");
@@ -457,27 +481,111 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
             inline_u = inline_u && ojx::gemv_lora_inline_ok(plan.U, plan.rt, plan.tpw,
                                                              jobs[i].lora_r, jobs[i].lora_a);
     a.lora_inline = inline_u ? 1 : 0;
-    // otherwise the adapters' down-projections run before the GEMV: consecutive adapter jobs
-    // on the same activations (same x, same K) share a launch
-    for (int i = 0; i < njobs && !inline_u;) {
-        if (jobs[i].lora_r <= 0) { ++i; continue; }
-        const void* xi = jobs[i].x ? jobs[i].x : x;
-        const int64_t Ki = jobs[i].K;
-        ojx::LoraDown items[ojx::kLoraDownItems];
-        int n = 0;
-        for (; i < njobs && n < ojx::kLoraDownItems; ++i) {
-            const ojx_e8t_gemv_job& j = jobs[i];
-            if (j.lora_r <= 0) continue;
-            if ((j.x ? j.x : x) != xi || j.K != Ki) break;
-            items[n++] = ojx::LoraDown{j.lora_a, const_cast<float*>(j.lora_u), j.lora_r,
-                                       j.lora_ldu ? j.lora_ldu : j.lora_r, j.lora_scaling};
-        }
-        const hipError_t e = ojx::launch_lora_down(xi, M, Ki, dtype, items, n,
-                                                   (hipStream_t)stream);
-        if (e != hipSuccess) return fail(OJX_EHIP, "lora_down launch: %s", hipGetErrorString(e));
-    }
+    if (!inline_u)
+        if (int r = lora_downs(jobs, njobs, x, M, dtype, stream)) return r;
     return done(ojx::launch_gemv(a, plan, grid, dtype, (hipStream_t)stream),
                 "e8t grouped gemv launch");
+}
+
+// ------------------------------------------------------------------ grouped 2-bit GEMV
+
+// Validates a 2-bit job table for batch M and group size gs, picks the plan and (fill) sets
+// each job's first workgroup and default y_ld, or (!fill) checks that they were so set.
+static int plan_jobs2(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs, int dtype,
+                      int64_t* grid, ojx::Gemv2Plan* plan, bool fill) {
+    if (njobs <= 0 || !jobs) return fail(OJX_EINVAL, "empty job list");
+    if (dtype != OJX_BF16 && dtype != OJX_F16)
+        return fail(OJX_EDTYPE, "grouped GEMV takes F16 or BF16 activations (got %d)", dtype);
+    if (M < 1 || M > 16) return fail(OJX_ELAYOUT, "grouped GEMV needs 1 <= M <= 16 (got %lld)",
+                                     (long long)M);
+    if (gs != 8 && gs != 16 && gs != 32 && gs != 64)
+        return fail(OJX_ELAYOUT, "grouped 2-bit GEMV needs group size 8, 16, 32 or 64 (got %lld)",
+                    (long long)gs);
+    int64_t tiles = 0;
+    bool k1024 = true;
+    for (int i = 0; i < njobs; ++i) {
+        const ojx_e8t_gemv_job& j = jobs[i];
+        if (j.N < 1 || j.K < 256 || j.K % 256 != 0)
+            return fail(OJX_ELAYOUT, "job %d: needs N >= 1 and K %% 256 == 0 (N=%lld K=%lld)", i,
+                        (long long)j.N, (long long)j.K);
+        if ((j.N + 32) * (j.K / 4) >= (1ll << 31) || (j.N + 32) * (j.K * 2 / gs) >= (1ll << 31) ||
+            M * j.K * 2 >= (1ll << 31))
+            return fail(OJX_ELAYOUT, "job %d: layer too large for 32-bit offsets", i);
+        if (!j.packed || !j.scales) return fail(OJX_EINVAL, "job %d: null weight pointer", i);
+        if (((uintptr_t)j.packed & 15u) || ((uintptr_t)j.scales & 15u) || ((uintptr_t)j.x & 15u) ||
+            ((uintptr_t)j.y & 1u) || ((uintptr_t)j.bias & 1u))
+            return fail(OJX_ELAYOUT, "job %d: misaligned pointer", i);
+        if (j.lora_r < 0 || j.lora_r > ojx::kLoraMaxRank)
+            return fail(OJX_ELAYOUT, "job %d: LoRA rank must be in 0..%lld", i,
+                        (long long)ojx::kLoraMaxRank);
+        if (j.lora_r > 0 && (!j.lora_u || !j.lora_b || !j.lora_a || ((uintptr_t)j.lora_u & 3u) ||
+                             ((uintptr_t)j.lora_b & 1u) || ((uintptr_t)j.lora_a & 1u) ||
+                             (j.lora_ldu != 0 && j.lora_ldu < j.lora_r)))
+            return fail(OJX_EINVAL, "job %d: bad LoRA operands", i);
+        const int64_t ld = j.y_ld ? j.y_ld : j.N;
+        if (j.y_col < 0 || ld < j.y_col + j.N)
+            return fail(OJX_ELAYOUT, "job %d: y_ld %lld < y_col %lld + N %lld", i, (long long)ld,
+                        (long long)j.y_col, (long long)j.N);
+        k1024 = k1024 && j.K % 1024 == 0;
+        tiles += (j.N + 15) / 16;
+    }
+    *plan = ojx::gemv2_pick_grouped(tiles, M, k1024);
+    int64_t wg = 0;
+    for (int i = 0; i < njobs; ++i) {
+        if (fill) {
+            jobs[i].wg_begin = wg;
+            if (jobs[i].y_ld == 0) jobs[i].y_ld = jobs[i].N;
+        } else if (jobs[i].wg_begin != wg || jobs[i].y_ld == 0) {
+            return fail(OJX_EINVAL, "job %d: the job array was not planned for this M", i);
+        }
+        wg += ojx::gemv2_wgs_for(jobs[i].N, *plan);
+    }
+    if (wg > 0x7FFFFFFF) return fail(OJX_ELAYOUT, "grouped GEMV grid too large");
+    *grid = wg;
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemv_grouped_plan(ojx_e8t_gemv_job* jobs,
+                                                                    int njobs, int64_t M,
+                                                                    int64_t gs, int dtype,
+                                                                    int64_t* grid) {
+    int64_t g = 0;
+    ojx::Gemv2Plan plan{};
+    if (int r = plan_jobs2(jobs, njobs, M, gs, dtype, &g, &plan, true)) return r;
+    if (grid) *grid = g;
+    g_last_error[0] = '\0';
+    return OJX_OK;
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemv_grouped(
+    const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev, int njobs, const void* x,
+    void* y, int64_t M, int64_t gs, int dtype, void* stream) {
+    int64_t grid = 0;
+    ojx::Gemv2Plan plan{};
+    if (int r = plan_jobs2(const_cast<ojx_e8t_gemv_job*>(jobs), njobs, M, gs, dtype, &grid, &plan,
+                           false))
+        return r;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 1u))
+        return fail(OJX_ELAYOUT, "misaligned default x / y");
+    for (int i = 0; i < njobs; ++i) {
+        if (!jobs[i].x && !x) return fail(OJX_EINVAL, "job %d has no activations", i);
+        if (!jobs[i].y && !y) return fail(OJX_EINVAL, "job %d has no output", i);
+    }
+    if (!jobs_dev && njobs > ojx::kGemvInlineJobs)
+        return fail(OJX_EINVAL, "more than %d jobs need a device job table",
+                    ojx::kGemvInlineJobs);
+    if (int r = check_device()) return r;
+    ojx::GemvLaunch a{};
+    if (!jobs_dev)
+        for (int i = 0; i < njobs; ++i) std::memcpy(&a.inl[i], &jobs[i], sizeof(ojx::GemvJob));
+    a.jobs = reinterpret_cast<const ojx::GemvJob*>(jobs_dev);
+    a.x = x;
+    a.y = y;
+    a.njobs = njobs;
+    a.M = (int)M;
+    if (int r = lora_downs(jobs, njobs, x, M, dtype, stream)) return r;
+    return done(ojx::launch_gemv2_grouped(a, plan, grid, gs, dtype, (hipStream_t)stream),
+                "e8 grouped gemv launch");
 }
 
 // ------------------------------------------------------------------ 2-bit E8

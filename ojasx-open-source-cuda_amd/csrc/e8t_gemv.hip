@@ -161,6 +161,22 @@ __device__ __forceinline__ int find_job(const GemvJob* jobs, int njobs, int64_t 
     return lo;
 }
 
+// The job of workgroup `wg` of a launch (the device table, or the launch's inline jobs);
+// `wg` becomes the workgroup's index within the job.
+__device__ __forceinline__ GemvJob gemv_job_of(const GemvLaunch& args, int64_t& wg) {
+    GemvJob job;
+    if (args.jobs != nullptr) {
+        job = args.jobs[find_job(args.jobs, args.njobs, wg)];
+    } else {
+        job = args.inl[0];
+#pragma unroll
+        for (int i = 1; i < kGemvInlineJobs; ++i)
+            if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
+    }
+    wg -= job.wg_begin;
+    return job;
+}
+
 // R: n-tiles (16 rows) per wave.  S: K-split ways inside the workgroup (1, 2 or 4);
 // the workgroup's 4 waves are (4/S) tile sets x S K ranges, reduced through LDS.
 template <int DT, int R, int S>
@@ -1303,9 +1319,19 @@ __device__ __forceinline__ void b2_load(uint4 (&cp)[4], uint4 (&sp)[4],
 
 template <int DT, int MM, int GS>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
-    const void* __restrict__ x, const uint8_t* __restrict__ packed,
-    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int M, int64_t N, int64_t K, LoraEp lora) {
+    GemvLaunch args) {
+    // this workgroup's linear: the launch's one job (per-linear launch) or a grouped job
+    int64_t wg = blockIdx.x;
+    const GemvJob job = gemv_job_of(args, wg);
+    const void* const x = job.x ? job.x : args.x;
+    const uint8_t* const packed = job.packed;
+    const uint16_t* const scales = job.scales;
+    const void* const bias = job.bias;
+    void* const y = job.y ? job.y : args.y;
+    const int M = args.M;
+    const int64_t N = job.N, K = job.K;
+    const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
+                      job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
     __shared__ uint4 lut_storage[kB2LutU4];
     // Two activation buffers per wave, each its own LDS object ending in a zero block, so
@@ -1325,7 +1351,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = wg;
     const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
@@ -1402,7 +1428,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     }
     if ((int64_t)row < N && g < M) {
         const float bv = bias ? load_as_f32<DT>(bias, row) : 0.f;
-        store_from_f32<DT>(y, (int64_t)g * N + row, out + bv + lora_term<DT>(lora, g, row));
+        store_from_f32<DT>(y, (int64_t)g * job.y_ld + job.y_col + row,
+                           out + bv + lora_term<DT>(lora, g, row));
     }
 }
 
@@ -1635,9 +1662,19 @@ __device__ __forceinline__ void b2m_load(uint4& cp, uint4& sp, __amdgpu_buffer_r
 
 template <int DT, int GS, int FMT, int R>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
-    const void* __restrict__ x, const uint8_t* __restrict__ packed,
-    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int M, int64_t N, int64_t K, LoraEp lora) {
+    GemvLaunch args) {
+    // this workgroup's linear: the launch's one job (per-linear launch) or a grouped job
+    int64_t wg = blockIdx.x;
+    const GemvJob job = gemv_job_of(args, wg);
+    const void* const x = job.x ? job.x : args.x;
+    const uint8_t* const packed = job.packed;
+    const uint16_t* const scales = job.scales;
+    const void* const bias = job.bias;
+    void* const y = job.y ? job.y : args.y;
+    const int M = args.M;
+    const int64_t N = job.N, K = job.K;
+    const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
+                      job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
     static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
     static_assert(FMT != kFmtTernary || GS >= 16, "ternary group sizes are multiples of 16");
@@ -1659,7 +1696,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = wg;
     // code bytes per row, and per lane group (64 weights) of a round
     const uint32_t rowbytes = (uint32_t)(FMT == kFmtTernary ? K * 3 / 16
                                          : FMT == kFmtRoot  ? K / 8 : K / 4);
@@ -1753,7 +1790,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
             for (int q = 0; q < 4; ++q) {
                 const int m = 4 * g + q;
                 if (m < M)
-                    store_from_f32<DT>(y, (int64_t)m * N + row,
+                    store_from_f32<DT>(y, (int64_t)m * job.y_ld + job.y_col + row,
                                        acc[r][q] + bv + lora_term<DT>(lora, m, row));
             }
         }
@@ -1816,9 +1853,19 @@ __device__ __forceinline__ void b2s_stage_x(char* xb, __amdgpu_buffer_rsrc_t x, 
 
 template <int DT, int GS, int FMT, int R>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
-    const void* __restrict__ x, const uint8_t* __restrict__ packed,
-    const uint16_t* __restrict__ scales, const void* __restrict__ bias, void* __restrict__ y,
-    int M, int64_t N, int64_t K, LoraEp lora) {
+    GemvLaunch args) {
+    // this workgroup's linear: the launch's one job (per-linear launch) or a grouped job
+    int64_t wg = blockIdx.x;
+    const GemvJob job = gemv_job_of(args, wg);
+    const void* const x = job.x ? job.x : args.x;
+    const uint8_t* const packed = job.packed;
+    const uint16_t* const scales = job.scales;
+    const void* const bias = job.bias;
+    void* const y = job.y ? job.y : args.y;
+    const int M = args.M;
+    const int64_t N = job.N, K = job.K;
+    const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
+                      job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
     static_assert(GS == 8 || GS == 16 || GS == 32 || GS == 64, "group size 8..64");
     static_assert(FMT == kFmtTernary || FMT == kFmt2Bit || FMT == kFmtRoot, "code format");
     static_assert(FMT != kFmtTernary || GS >= 16, "ternary group sizes are multiples of 16");
@@ -1842,7 +1889,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = wg;
     const uint32_t rowbytes = (uint32_t)(FMT == kFmtTernary ? K * 3 / 16
                                          : FMT == kFmtRoot  ? K / 8 : K / 4);
     constexpr uint32_t kLaneBytes = FMT == kFmtTernary ? 12u : FMT == kFmtRoot ? 8u : 16u;
@@ -1936,7 +1983,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
             for (int q = 0; q < 4; ++q) {
                 const int m = 4 * g + q;
                 if (m < M)
-                    store_from_f32<DT>(y, (int64_t)m * N + row,
+                    store_from_f32<DT>(y, (int64_t)m * job.y_ld + job.y_col + row,
                                        acc[r][q] + bv + lora_term<DT>(lora, m, row));
             }
         }
@@ -2618,14 +2665,34 @@ bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scale
     return true;
 }
 
+// One linear as a launch of one inline job.
+static GemvLaunch one_job(const void* x, const uint8_t* packed, const uint16_t* scales,
+                          const void* bias, void* y, int M, int64_t N, int64_t K,
+                          const LoraEp& lora) {
+    GemvLaunch a{};
+    GemvJob& j = a.inl[0];
+    j.x = x; j.packed = packed; j.scales = scales; j.bias = bias; j.y = y;
+    j.N = N; j.K = K; j.y_col = 0; j.y_ld = N; j.wg_begin = 0;
+    j.lora_u = lora.u; j.lora_b = lora.b; j.lora_r = lora.r; j.lora_ldu = lora.ldu;
+    a.njobs = 1;
+    a.M = M;
+    return a;
+}
+
+// `wgs` workgroups of one 16-row tile each (each job's tiles start a new workgroup)
+template <int DT, int MM, int GS>
+static hipError_t launch_gemv2_grid(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
+    hipLaunchKernelGGL((gemv2_kernel<DT, MM, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
 template <int DT, int MM, int GS>
 static hipError_t launch_gemv2_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                  const void* bias, void* y, int M, int64_t N, int64_t K,
                                  hipStream_t stream, const LoraEp& lora) {
-    const int64_t wgs = (N + 15) / 16;  // one 16-row tile per workgroup
-    hipLaunchKernelGGL((gemv2_kernel<DT, MM, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
-                       stream, x, packed, scales, bias, y, M, N, K, lora);
-    return hipGetLastError();
+    return launch_gemv2_grid<DT, MM, GS>(one_job(x, packed, scales, bias, y, M, N, K, lora),
+                                         (N + 15) / 16, stream);
 }
 
 template <int DT, int MM>
@@ -2659,29 +2726,35 @@ bool gemv2m_supported(const void* x, const uint8_t* packed, const uint16_t* scal
     return true;
 }
 
+// `wgs` workgroups of R 16-row tiles each; M <= 4 stages four activation rows
+template <int DT, int GS, int FMT>
+static hipError_t launch_gemv2m_grid(const GemvLaunch& a, int64_t wgs, int R,
+                                     hipStream_t stream) {
+    if (a.M <= kB2sRows) {
+        if (R == 2)
+            hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 2>), dim3((unsigned)wgs),
+                               dim3(64 * kB2Waves), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 1>), dim3((unsigned)wgs),
+                               dim3(64 * kB2Waves), 0, stream, a);
+    } else if (R == 2) {
+        hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 2>), dim3((unsigned)wgs),
+                           dim3(64 * kB2Waves), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 1>), dim3((unsigned)wgs),
+                           dim3(64 * kB2Waves), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
 template <int DT, int GS, int FMT>
 static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream, const LoraEp& lora) {
     const int64_t tiles = (N + 15) / 16;
-    if (M <= kB2sRows) {
-        if (tiles >= kB2mTwoTilesFrom)
-            hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 2>), dim3((unsigned)((tiles + 1) / 2)),
-                               dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N,
-                               K, lora);
-        else
-            hipLaunchKernelGGL((gemv2s_kernel<DT, GS, FMT, 1>), dim3((unsigned)tiles),
-                               dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N,
-                               K, lora);
-    } else if (tiles >= kB2mTwoTilesFrom)
-        hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 2>), dim3((unsigned)((tiles + 1) / 2)),
-                           dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N, K,
-                           lora);
-    else
-        hipLaunchKernelGGL((gemv2m_kernel<DT, GS, FMT, 1>), dim3((unsigned)tiles),
-                           dim3(64 * kB2Waves), 0, stream, x, packed, scales, bias, y, M, N, K,
-                           lora);
-    return hipGetLastError();
+    const int R = tiles >= kB2mTwoTilesFrom ? 2 : 1;
+    return launch_gemv2m_grid<DT, GS, FMT>(one_job(x, packed, scales, bias, y, M, N, K, lora),
+                                           (tiles + R - 1) / R, R, stream);
 }
 
 template <int DT, int FMT>
@@ -2863,6 +2936,40 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
                       : launch_gemv2_gs<kBF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
     return M == 1 ? launch_gemv2_gs<kF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
                   : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
+}
+
+// ---- grouped 2-bit decode GEMV: many linears of one group size in one launch
+Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024) {
+    Gemv2Plan p{};
+    p.post = M <= 4 && k1024;  // post-scaled 1024-k rounds (gemv2_kernel), one tile per wg
+    p.R = p.post ? 1 : (total_tiles >= kB2mTwoTilesFrom ? 2 : 1);
+    return p;
+}
+int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p) { return ((N + 15) / 16 + p.R - 1) / p.R; }
+
+template <int DT, int GS>
+static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
+                                         hipStream_t s) {
+    if (p.post) return a.M == 1 ? launch_gemv2_grid<DT, 1, GS>(a, wgs, s)
+                                : launch_gemv2_grid<DT, 4, GS>(a, wgs, s);
+    return launch_gemv2m_grid<DT, GS, kFmt2Bit>(a, wgs, p.R, s);
+}
+template <int DT>
+static hipError_t launch_gemv2_grouped_dt(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
+                                          int64_t gs, hipStream_t s) {
+    switch (gs) {
+        case 8: return launch_gemv2_grouped_t<DT, 8>(a, p, wgs, s);
+        case 16: return launch_gemv2_grouped_t<DT, 16>(a, p, wgs, s);
+        case 32: return launch_gemv2_grouped_t<DT, 32>(a, p, wgs, s);
+        case 64: return launch_gemv2_grouped_t<DT, 64>(a, p, wgs, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+hipError_t launch_gemv2_grouped(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
+                                int64_t gs, int dt, hipStream_t s) {
+    if (wgs <= 0) return hipSuccess;
+    return dt == kBF16 ? launch_gemv2_grouped_dt<kBF16>(a, p, wgs, gs, s)
+                       : launch_gemv2_grouped_dt<kF16>(a, p, wgs, gs, s);
 }
 
 }  // namespace ojx

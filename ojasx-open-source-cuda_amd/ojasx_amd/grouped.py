@@ -23,6 +23,10 @@ Typical uses:
   streams, or graph replays that are not ordered on one stream) race on it, so use such a
   plan from one stream at a time (or build one plan per stream);
 * a fixed table -- explicit ``x`` / ``y`` per job, uploaded once to the device.
+
+Ternary (bitrate 1.5) groups take group size 32 (``ojx_e8t_gemv_grouped``); 2-bit groups
+(bitrate 2.0, ``E8LatticePacker``, the reference's default) take group size 8, 16, 32 or 64,
+one per group (``ojx_e8_gemv_grouped``).
 """
 
 from __future__ import annotations
@@ -53,9 +57,16 @@ class GroupedGemv:
     """A planned group of decode-GEMV jobs for batch ``M`` and activation ``dtype``."""
 
     def __init__(self, jobs: Sequence[N.GemvJob], M: int, dtype: torch.dtype,
-                 device: torch.device, keep: Sequence[torch.Tensor] = ()) -> None:
+                 device: torch.device, keep: Sequence[torch.Tensor] = (), bitrate: float = 1.5,
+                 group_size: int = 32) -> None:
         if dtype not in (torch.bfloat16, torch.float16):
             raise RuntimeError("grouped GEMV takes bfloat16 or float16 activations")
+        if float(bitrate) not in (1.5, 2.0):
+            raise RuntimeError("grouped GEMV runs ternary (1.5) or 2-bit (2.0) linears")
+        self.bitrate = float(bitrate)
+        self.group_size = int(group_size)
+        if self.bitrate == 1.5 and self.group_size != 32:
+            raise RuntimeError("grouped ternary GEMV needs group_size 32")
         self.M = int(M)
         self.dtype = dtype
         self.device = torch.device(device)
@@ -66,9 +77,14 @@ class GroupedGemv:
         jobs = sorted(jobs, key=lambda j: -int(j.K))
         self._arr = (N.GemvJob * self.n)(*jobs)
         grid = ctypes.c_int64(0)
-        N.check(N.lib().ojx_e8t_gemv_grouped_plan(ctypes.addressof(self._arr), self.n, self.M,
-                                                  N.DTYPE_CODE[dtype], ctypes.byref(grid)),
-                "gemv_grouped_plan")
+        if self.bitrate == 1.5:
+            N.check(N.lib().ojx_e8t_gemv_grouped_plan(ctypes.addressof(self._arr), self.n,
+                                                      self.M, N.DTYPE_CODE[dtype],
+                                                      ctypes.byref(grid)), "gemv_grouped_plan")
+        else:
+            N.check(N.lib().ojx_e8_gemv_grouped_plan(ctypes.addressof(self._arr), self.n, self.M,
+                                                     self.group_size, N.DTYPE_CODE[dtype],
+                                                     ctypes.byref(grid)), "e8 gemv_grouped_plan")
         self.grid = grid.value
         self._keep = list(keep)  # tensors the job pointers refer to
         self._lora = []          # layers whose adapter is fused (A, B, scaling read at plan time)
@@ -86,11 +102,12 @@ class GroupedGemv:
         n_total = sum(int(l.out_features) for l in layers)
         jobs, col, keep, lora = [], 0, [], []
         dev = layers[0].packed_weight.device
+        bitrate = float(getattr(layers[0], "bitrate", 1.5))
+        gs = int(layers[0].group_size)
         for l in layers:
-            if int(l.group_size) != 32:
-                raise RuntimeError("grouped GEMV needs group_size 32")
-            if float(getattr(l, "bitrate", 1.5)) != 1.5:
-                raise RuntimeError("grouped GEMV runs ternary (bitrate 1.5) layers only")
+            if float(getattr(l, "bitrate", 1.5)) != bitrate or int(l.group_size) != gs:
+                raise RuntimeError("grouped GEMV: every layer needs the same bitrate and "
+                                   "group_size")
             bias = l.bias.detach().to(dtype).contiguous() if l.bias is not None else None
             if bias is not None:
                 keep.append(bias)
@@ -118,7 +135,7 @@ class GroupedGemv:
             jobs.append(j)
             keep += [l.packed_weight, scales]
             col += int(l.out_features)
-        g = cls(jobs, M, dtype, dev, keep)
+        g = cls(jobs, M, dtype, dev, keep, bitrate=bitrate, group_size=gs)
         g.n_total = n_total
         g._lora = lora
         return g
@@ -133,10 +150,16 @@ class GroupedGemv:
         if y is None and hasattr(self, "n_total") and x is not None:
             y = torch.empty((*x.shape[:-1], self.n_total), dtype=self.dtype, device=self.device)
         s = stream.cuda_stream if stream is not None else N.stream_handle(self.device)
-        N.check(N.lib().ojx_e8t_gemv_grouped(ctypes.addressof(self._arr),
-                                             N.ptr(self._dev), self.n, N.ptr(x), N.ptr(y),
-                                             self.M, N.DTYPE_CODE[self.dtype], s),
-                "gemv_grouped")
+        if self.bitrate == 1.5:
+            N.check(N.lib().ojx_e8t_gemv_grouped(ctypes.addressof(self._arr),
+                                                 N.ptr(self._dev), self.n, N.ptr(x), N.ptr(y),
+                                                 self.M, N.DTYPE_CODE[self.dtype], s),
+                    "gemv_grouped")
+        else:
+            N.check(N.lib().ojx_e8_gemv_grouped(ctypes.addressof(self._arr), N.ptr(self._dev),
+                                                self.n, N.ptr(x), N.ptr(y), self.M,
+                                                self.group_size, N.DTYPE_CODE[self.dtype], s),
+                    "e8 gemv_grouped")
         return y
 
 
