@@ -128,6 +128,8 @@ def parse_args():
     ap.add_argument("--settle-s", type=float, default=0.5,
                     help="seconds of each leg's own launches run untimed right before its "
                          "timed region, after the warm-up steps (0: none)")
+    ap.add_argument("--e8b-grouped-layers", type=int, default=32,
+                    help="layers of the grouped 2-bit decode leg (0: skip)")
     ap.add_argument("--gs-layers", type=int, default=8,
                     help="layers of the ternary group-size leg (group 32 against 64; 0: skip)")
     ap.add_argument("--launch-probe", action="store_true",
@@ -802,6 +804,67 @@ class E8Decoder:
         return nxt
 
 
+def bench_e8b_grouped(torch, dev, layers: int, steps: int, warmup: int, Ms=(1, 4, 16),
+                      gs: int = 32) -> dict:
+    """2-bit E8 (the reference's default bitrate, lattice.py:735, 906) decode over a
+    `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights (seed 9700 + 7*layer + j,
+    group size `gs`): one grouped launch (ojx_e8_gemv_grouped, device job table) per M over
+    every linear, timed with HIP events as the ternary headline; outputs of layer 0's q, gate
+    and down checked against an fp32 matmul of the decoded weights."""
+    from ojasx_amd import ops
+    from ojasx_amd.grouped import GroupedGemv, stack_jobs
+
+    stack = []
+    for layer in range(layers):
+        for j, (name, N, K) in enumerate(LAYER_SHAPES):
+            g = torch.Generator(device=dev).manual_seed(9700 + 7 * layer + j)
+            w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+            packed, scales = ops.encode2(w, gs)
+            del w
+            stack.append(dict(name=name, N=N, K=K, packed=packed, scales=scales))
+    torch.cuda.synchronize()
+    wbytes = sum(s["packed"].numel() + 2 * s["scales"].numel() for s in stack)
+    plans, xs, ys = {}, {}, {}
+    for M in Ms:
+        xk = {K: torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(8300 + M + K),
+                             device=dev).to(torch.bfloat16) for K in (4096, 14336)}
+        yl = [torch.empty(M, s["N"], dtype=torch.bfloat16, device=dev) for s in stack]
+        xs[M], ys[M] = xk, yl
+        plans[M] = GroupedGemv(stack_jobs(stack, xk, yl), M, torch.bfloat16, dev,
+                               keep=list(xk.values()) + yl, bitrate=2.0, group_size=gs)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        for M in Ms:
+            plans[M]()
+    torch.cuda.synchronize()
+    settle(torch, lambda: [plans[M]() for M in Ms])
+    ev = {M: [] for M in Ms}
+    for _ in range(steps):
+        for M in Ms:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            plans[M]()
+            b.record(stream)
+            ev[M].append((a, b))
+    torch.cuda.synchronize()
+    per_m, worst = {}, 0.0
+    for M in Ms:
+        ms = sum(a.elapsed_time(b) for a, b in ev[M]) / steps
+        per_m[str(M)] = dict(ms=round(ms, 4), weight_GBs=round(wbytes / ms / 1e6, 1),
+                             frac_hbm=round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                             grid=plans[M].grid)
+        for idx in (0, 4, 6):
+            s = stack[idx]
+            wd = ops.decode2(s["packed"], s["scales"], s["N"] * s["K"], gs,
+                             torch.bfloat16).view(s["N"], s["K"]).float()
+            ref = xs[M][s["K"]].float() @ wd.t()
+            err = (ys[M][idx].float() - ref).abs().max().item() / max(ref.abs().max().item(),
+                                                                      1e-30)
+            worst = max(worst, err)
+    return dict(layers=layers, linears=len(stack), group_size=gs, stack_weight_bytes=wbytes,
+                per_M=per_m, max_rel_err=worst)
+
+
 def bench_ternary_gs(torch, N_, dev, layers: int, steps: int, gs_list=(32, 64), Ms=(1, 4, 16),
                      prefill_m: int = 2048) -> dict:
     """Ternary E8 at the reference's other group sizes: one `layers`-layer Llama-3-8B-shaped
@@ -1271,6 +1334,12 @@ def main() -> int:
         log(f"1-bit Root E8 ({args.e8b_layers}-layer stack)")
         result["e8_1bit"] = bench_e8b(torch, N_, dev, args.e8b_layers, args.steps, fmt="root")
         log(f"1-bit: decode M=16 {result['e8_1bit']['decode_per_linear']['16']['weight_GBs']} GB/s")
+    if args.e8b_grouped_layers > 0:
+        torch.cuda.empty_cache()
+        log(f"2-bit E8 grouped decode ({args.e8b_grouped_layers}-layer stack)")
+        result["e8_2bit_grouped"] = bench_e8b_grouped(torch, dev, args.e8b_grouped_layers,
+                                                      args.steps, args.warmup)
+        log(f"2-bit grouped: {result['e8_2bit_grouped']['per_M']}")
     if args.gs_layers > 0:
         torch.cuda.empty_cache()
         log(f"ternary group sizes 32 / 64 ({args.gs_layers}-layer stack)")

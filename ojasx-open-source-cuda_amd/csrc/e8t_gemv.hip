@@ -2938,11 +2938,197 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
                   : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
 }
 
+// ---- streaming 2-bit GEMV for grouped launches
+//
+// The per-linear 2-bit kernels above give each workgroup one or two 16-row tiles and split
+// K over its waves, so every workgroup stages the activations of all of K for 16-32 rows:
+// in a grouped launch over a whole stack that re-reads x from L2 more often than the
+// weights themselves (at M = 4, 32 KB of x against 20 KB of weights per K = 4096 tile).
+// Here the W waves of a workgroup own R row tiles each over all of K and share one
+// activation stage per round (W * R * 16 rows per x round), with one barrier per round.
+// Each lane loads its codes and scales of the next round into registers while the current
+// round computes (the per-linear kernels' load pattern: 64 contiguous bytes of 16 rows per
+// instruction).  MM <= 4: post-scaled 1024-k rounds (B2Round); MM = 16: the B-operand
+// 256-k rounds (B2mRound, R tiles sharing each A fragment).
+template <int DT, int GS, int MM, int R, int W>
+__global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
+    constexpr bool kPost = MM <= 4;
+    static_assert(MM == 1 || MM == 4 || MM == 16, "activation rows 1, 4 or 16");
+    constexpr int kXBytes = kPost ? MM * (int)kXRow : kB2mXBytes;  // one round's stage
+    __shared__ uint4 lut_storage[kB2LutU4];
+    // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
+    // (the A fragments of lanes outside their lane group)
+    __shared__ __attribute__((aligned(128))) char xs0[kXBytes + (kPost ? kB2ZeroBytes : 0)];
+    __shared__ __attribute__((aligned(128))) char xs1[kXBytes + (kPost ? kB2ZeroBytes : 0)];
+
+    if constexpr (kPost) {
+        fill_b2lut<DT, 64 * W>(lut_storage);
+        for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * W) {
+            reinterpret_cast<uint4*>(xs0 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
+            reinterpret_cast<uint4*>(xs1 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    } else {
+        fill_b2sel<64 * W>(lut_storage);
+    }
+
+    int64_t wg = blockIdx.x;
+    const GemvJob job = gemv_job_of(args, wg);
+    const void* const x = job.x ? job.x : args.x;
+    void* const y = job.y ? job.y : args.y;
+    const int M = args.M;
+    const int64_t N = job.N, K = job.K;
+    const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
+                      job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t tile0 = (wg * W + wave) * R;
+    const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+    // rows past N read zeros (buffer bound) and are never stored
+    uint32_t vo_code[R], vo_scale[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
+        vo_code[r] = row * rowbytes + 16u * g;
+        vo_scale[r] = row * srowbytes + (128u / GS) * g;
+    }
+    const uint32_t slot = (uint32_t)(lane & 31) * 4u;
+    const int T = (int)(K / (kPost ? kRound : kB2mRound));
+
+    // this lane's activation reads: post-scaled A row i16 = 4 g' + m is live in lane group g'
+    // only (others read the zero block); B-operand: the swizzled 16-row stage
+    const int am = i16 & 3;
+    const bool a_live = (i16 >> 2) == g && am < M;
+    const int aoff = a_live ? am * (int)kXRow + 128 * g : kXBytes;
+    const uint32_t gu = (uint32_t)g, iu = (uint32_t)i16;
+    const uint32_t xo = 512u * iu + 16u * ((8u * gu & 16u) | ((8u * gu & 8u) ^ (iu & 8u)) | (iu & 7u));
+    uint32_t xo_ld[8];
+    if constexpr (!kPost) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xo_ld[q] = b2m_x_offset(q, lane, M, K);
+    }
+
+    // the workgroup's share of one round's activation loads: post-scaled 2 MM 1-KB loads
+    // (rows m >= M re-read row M - 1 into rows no lane reads), B-operand eight
+    auto stage = [&](char* xs, int u) {
+        if constexpr (kPost) {
+            for (int q = wave; q < 2 * MM; q += W) {
+                const int m = q >> 1, half = q & 1;
+                const int msrc = m < M ? m : M - 1;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    xr, lds_ptr(xs + m * kXRow + half * 1024), 16,
+                    (uint32_t)(msrc * K * 2 + half * 1024 + lane * 16),
+                    uniform_offset((int64_t)u * kRound * 2), 0, 0);
+            }
+        } else {
+            for (int q = wave; q < 8; q += W)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, lds_ptr(xs + 1024 * q), 16, xo_ld[q],
+                                                         uniform_offset((int64_t)u * kB2mRound * 2),
+                                                         0, 0);
+        }
+    };
+    using Piece = std::conditional_t<kPost, uint4[4], uint4>;
+    Piece cp0[R], sp0[R], cp1[R], sp1[R];
+    auto load = [&](Piece (&cp)[R], Piece (&sp)[R], int u) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if constexpr (kPost) b2_load<GS>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
+            else b2m_load<GS, kFmt2Bit>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
+        }
+    };
+    float accp[R][kPost ? MM : 1];
+    f32x4 accm[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        accm[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < (kPost ? MM : 1); ++q) accp[r][q] = 0.f;
+    }
+    const char* lut = reinterpret_cast<const char*>(lut_storage);
+    auto compute = [&](const Piece (&cp)[R], const Piece (&sp)[R], const char* xs) {
+        if constexpr (kPost) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                B2Round<DT, MM, GS>::run(cp[r], sp[r], lut, slot, xs + aoff, accp[r]);
+        } else {
+            B2mRound<DT, GS, kFmt2Bit, R>::run(cp, sp, lut, slot, xs, xo, accm);
+        }
+    };
+
+    load(cp0, sp0, 0);
+    stage(xs0, 0);
+    vm_wait_all();
+    __syncthreads();  // table, zero blocks, round 0 ready
+    // rounds in pairs, so that each register set and stage is a compile-time choice; round u
+    // fetches round u + 1 while it computes, then the workgroup waits for it
+    for (int u = 0; u < T; u += 2) {
+        if (u + 1 < T) {
+            load(cp1, sp1, u + 1);
+            stage(xs1, u + 1);
+        }
+        compute(cp0, sp0, xs0);
+        vm_wait_all();
+        __syncthreads();
+        if (u + 1 >= T) break;
+        if (u + 2 < T) {
+            load(cp0, sp0, u + 2);
+            stage(xs0, u + 2);
+        }
+        compute(cp1, sp1, xs1);
+        vm_wait_all();
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = (tile0 + r) * 16 + i16;
+        if constexpr (kPost) {
+            // the four lane groups of each row; lane group q keeps activation row q
+            float out = 0.f;
+#pragma unroll
+            for (int q = 0; q < MM; ++q) {
+                float v = accp[r][q];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                if (q == g) out = v;
+            }
+            if (row < N && g < M) {
+                const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
+                store_from_f32<DT>(y, (int64_t)g * job.y_ld + job.y_col + row,
+                                   out + bv + lora_term<DT>(lora, g, row));
+            }
+        } else if (row < N) {
+            // lane (g, n) holds rows m = 4g + q of column n
+            const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = 4 * g + q;
+                if (m < M)
+                    store_from_f32<DT>(y, (int64_t)m * job.y_ld + job.y_col + row,
+                                       accm[r][q] + bv + lora_term<DT>(lora, m, row));
+            }
+        }
+    }
+}
+
 // ---- grouped 2-bit decode GEMV: many linears of one group size in one launch
+// Streaming 2-bit kernel geometry of a grouped launch: waves per workgroup and row tiles per
+// wave; M <= 4 needs every K a multiple of 1024 (post-scaled rounds), otherwise the 16-row
+// B-operand rounds take it.
+constexpr int kB2gWaves = 4;
+constexpr int kB2gTiles = 2;
 Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024) {
+    (void)total_tiles;
     Gemv2Plan p{};
-    p.post = M <= 4 && k1024;  // post-scaled 1024-k rounds (gemv2_kernel), one tile per wg
-    p.R = p.post ? 1 : (total_tiles >= kB2mTwoTilesFrom ? 2 : 1);
+    p.post = M <= 4 && k1024;
+    p.R = kB2gWaves * kB2gTiles;  // row tiles per workgroup
     return p;
 }
 int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p) { return ((N + 15) / 16 + p.R - 1) / p.R; }
@@ -2950,9 +3136,18 @@ int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p) { return ((N + 15) / 16 + p
 template <int DT, int GS>
 static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
                                          hipStream_t s) {
-    if (p.post) return a.M == 1 ? launch_gemv2_grid<DT, 1, GS>(a, wgs, s)
-                                : launch_gemv2_grid<DT, 4, GS>(a, wgs, s);
-    return launch_gemv2m_grid<DT, GS, kFmt2Bit>(a, wgs, p.R, s);
+    if (p.post) {
+        if (a.M == 1)
+            hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 1, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
+                               dim3(64 * kB2gWaves), 0, s, a);
+        else
+            hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 4, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
+                               dim3(64 * kB2gWaves), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
+                           dim3(64 * kB2gWaves), 0, s, a);
+    }
+    return hipGetLastError();
 }
 template <int DT>
 static hipError_t launch_gemv2_grouped_dt(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,

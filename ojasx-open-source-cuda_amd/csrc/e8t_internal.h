@@ -109,9 +109,9 @@ struct GemvLaunch {
                                    // adapter form u from lora_a themselves (lora_u unused)
 };
 
-// Grouped 2-bit decode GEMV: M <= 4 with every K a multiple of 1024 runs the post-scaled
-// kernel (one 16-row tile per workgroup), otherwise the B-operand kernel with R row tiles
-// per workgroup.  Each job's tiles start a new workgroup.
+// Grouped 2-bit decode GEMV (streaming kernel): M <= 4 with every K a multiple of 1024
+// runs post-scaled 1024-k rounds, otherwise B-operand 256-k rounds; R row tiles per
+// workgroup.  Each job's tiles start a new workgroup.
 struct Gemv2Plan {
     bool post;
     int R;
