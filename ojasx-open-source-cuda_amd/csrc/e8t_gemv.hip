@@ -1157,9 +1157,14 @@ __global__ __launch_bounds__(64 * W) void gemv_psk_kernel(GemvLaunch args) {
 // (a zero block elsewhere), so the MFMA output of lane (g', n) is the partial sum of its own
 // k slots and its group scale can multiply it every gs/8 steps; the four lane groups are
 // added at the end.
+//
+// The byte table (BL): each code byte (four codes) indexes a 256-entry table of four weights
+// (8 bytes) with 16 copies, lane l reading copy l % 16: two conflict-free b64 reads and two
+// address computations per 8 weights instead of four of each.  It takes 32 KB of LDS.
 
 constexpr int kB2Waves = 4;
 constexpr int kB2LutU4 = 16 * 32 * 4 / 16;  // 16 entries x 32 copies x 4 bytes
+constexpr int kB2ByteLutU4 = 256 * 16 * 8 / 16;  // 256 entries x 16 copies x 8 bytes
 constexpr int kB2ZeroBytes = 2048;          // covers the largest A-fragment offset of a round
 
 template <int DT>
@@ -1177,16 +1182,41 @@ __device__ __forceinline__ void fill_b2lut(uint4* lut) {
     }
 }
 
-// B operand of the 8 codes in half-word H of dword dw: four table reads.
-template <int H>
-__device__ __forceinline__ uint4 b2_operand(uint32_t dw, const char* lut, uint32_t slot) {
-    uint32_t v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * H + 4 * i, 4) << 7) | slot;
-        v[i] = *reinterpret_cast<const uint32_t*>(lut + a);
+template <int DT, int NT>
+__device__ __forceinline__ void fill_b2blut(uint4* lut) {
+    for (int i = (int)threadIdx.x; i < kB2ByteLutU4; i += NT) {
+        const int e = i >> 3;  // 8 items (16 copies x 8 bytes) per entry
+        const uint32_t lo = b2_half<DT>(e & 3) | (b2_half<DT>((e >> 2) & 3) << 16);
+        const uint32_t hi = b2_half<DT>((e >> 4) & 3) | (b2_half<DT>(e >> 6) << 16);
+        lut[i] = make_uint4(lo, hi, lo, hi);
     }
-    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// The table slot of a lane: 32 copies of 4 bytes, or 16 copies of 8 bytes (byte table).
+template <bool BL>
+__device__ __forceinline__ uint32_t b2_slot(int lane) {
+    return BL ? (uint32_t)(lane & 15) * 8u : (uint32_t)(lane & 31) * 4u;
+}
+
+// B operand of the 8 codes in half-word H of dword dw: four nibble-table reads, or two
+// byte-table reads.
+template <int H, bool BL>
+__device__ __forceinline__ uint4 b2_operand(uint32_t dw, const char* lut, uint32_t slot) {
+    if constexpr (BL) {
+        const uint32_t a0 = (__builtin_amdgcn_ubfe(dw, 16 * H, 8) << 7) | slot;
+        const uint32_t a1 = (__builtin_amdgcn_ubfe(dw, 16 * H + 8, 8) << 7) | slot;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(lut + a0);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(lut + a1);
+        return make_uint4(v0.x, v0.y, v1.x, v1.y);
+    } else {
+        uint32_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * H + 4 * i, 4) << 7) | slot;
+            v[i] = *reinterpret_cast<const uint32_t*>(lut + a);
+        }
+        return make_uint4(v[0], v[1], v[2], v[3]);
+    }
 }
 
 // Scale (fp16 bits) of step J for group size GS from this lane's scale pieces of the round.
@@ -1199,61 +1229,76 @@ __device__ __forceinline__ uint32_t b2_scale(const uint4 (&sp)[4]) {
     return half ? (w >> 16) : (w & 0xFFFFu);
 }
 
-template <int DT, int MM, int GS>
+// One round of R row tiles of one wave: steps 0..31, the A fragment read once per step for
+// all R tiles, with the table reads and A fragment of step J + 1 issued before the MFMAs of
+// step J and the scale of a finished group applied after the next group's first MFMA.
+template <int DT, int MM, int GS, int R, bool BL>
 struct B2Round {
-    // one round of one wave: steps 0..31 with the table reads and A fragment of step J + 1
-    // issued before the MFMA of step J, the scale of a finished group applied after the
-    // next group's first MFMA has been issued
     static constexpr int kSpg = GS / 8;  // steps per scale group
+    using Pieces = uint4[R][4];
     template <int J>
-    __device__ __forceinline__ static void step(const uint4 (&cp)[4], const uint4 (&sp)[4],
+    __device__ __forceinline__ static void step(const Pieces& cp, const Pieces& sp,
                                                 const char* lut, uint32_t slot,
-                                                const char* xa, uint4& a_cur, uint4& b_cur,
-                                                f32x4 (&d)[2], float& sf_prev,
-                                                float (&acc)[MM]) {
-        uint4 a_n, b_n;
+                                                const char* xa, uint4& a_cur, uint4 (&b_cur)[R],
+                                                f32x4 (&d)[R][2], float (&sf_prev)[R],
+                                                float (&acc)[R][MM]) {
+        uint4 a_n, b_n[R];
         if constexpr (J + 1 < 32) {
             constexpr int t = (J + 1) / 8, hw = (J + 1) % 8;
             a_n = *reinterpret_cast<const uint4*>(xa + 512 * t + 16 * hw);
-            const uint32_t dw = (hw / 2) == 0 ? cp[t].x : (hw / 2) == 1 ? cp[t].y
-                              : (hw / 2) == 2 ? cp[t].z : cp[t].w;
-            b_n = b2_operand<(hw % 2)>(dw, lut, slot);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t dw = (hw / 2) == 0 ? cp[r][t].x : (hw / 2) == 1 ? cp[r][t].y
+                                  : (hw / 2) == 2 ? cp[r][t].z : cp[r][t].w;
+                b_n[r] = b2_operand<(hw % 2), BL>(dw, lut, slot);
+            }
         }
         constexpr int grp = J / kSpg, slot_d = grp & 1;
         constexpr bool first = (J % kSpg) == 0;
-        d[slot_d] = mfma16<DT>(a_cur, b_cur, first ? f32x4{0.f, 0.f, 0.f, 0.f} : d[slot_d]);
-        if constexpr (first && J > 0) {
-            // group grp - 1 is complete in the other accumulator
 #pragma unroll
-            for (int q = 0; q < MM; ++q)
-                acc[q] = __builtin_fmaf(d[slot_d ^ 1][q], sf_prev, acc[q]);
-            keep_mfma_result(d[slot_d ^ 1], acc[0]);
-        }
-        if constexpr (first) sf_prev = scale_for<DT>(b2_scale<GS, J>(sp));
-        if constexpr (J == 31) {
+        for (int r = 0; r < R; ++r)
+            d[r][slot_d] = mfma16<DT>(a_cur, b_cur[r],
+                                      first ? f32x4{0.f, 0.f, 0.f, 0.f} : d[r][slot_d]);
 #pragma unroll
-            for (int q = 0; q < MM; ++q) acc[q] = __builtin_fmaf(d[slot_d][q], sf_prev, acc[q]);
-            keep_mfma_result(d[slot_d], acc[0]);
+        for (int r = 0; r < R; ++r) {
+            if constexpr (first && J > 0) {
+                // group grp - 1 is complete in the other accumulator
+#pragma unroll
+                for (int q = 0; q < MM; ++q)
+                    acc[r][q] = __builtin_fmaf(d[r][slot_d ^ 1][q], sf_prev[r], acc[r][q]);
+                keep_mfma_result(d[r][slot_d ^ 1], acc[r][0]);
+            }
+            if constexpr (first) sf_prev[r] = scale_for<DT>(b2_scale<GS, J>(sp[r]));
+            if constexpr (J == 31) {
+#pragma unroll
+                for (int q = 0; q < MM; ++q)
+                    acc[r][q] = __builtin_fmaf(d[r][slot_d][q], sf_prev[r], acc[r][q]);
+                keep_mfma_result(d[r][slot_d], acc[r][0]);
+            }
         }
         if constexpr (J + 1 < 32) {
             a_cur = a_n;
-            b_cur = b_n;
+#pragma unroll
+            for (int r = 0; r < R; ++r) b_cur[r] = b_n[r];
         }
     }
     template <int... J>
-    __device__ __forceinline__ static void steps(const uint4 (&cp)[4], const uint4 (&sp)[4],
+    __device__ __forceinline__ static void steps(const Pieces& cp, const Pieces& sp,
                                                  const char* lut, uint32_t slot, const char* xa,
-                                                 uint4& a, uint4& b, f32x4 (&d)[2], float& sf,
-                                                 float (&acc)[MM], std::integer_sequence<int, J...>) {
+                                                 uint4& a, uint4 (&b)[R], f32x4 (&d)[R][2],
+                                                 float (&sf)[R], float (&acc)[R][MM],
+                                                 std::integer_sequence<int, J...>) {
         (step<J>(cp, sp, lut, slot, xa, a, b, d, sf, acc), ...);
     }
-    __device__ __forceinline__ static void run(const uint4 (&cp)[4], const uint4 (&sp)[4],
+    __device__ __forceinline__ static void run(const Pieces& cp, const Pieces& sp,
                                                const char* lut, uint32_t slot, const char* xa,
-                                               float (&acc)[MM]) {
+                                               float (&acc)[R][MM]) {
         uint4 a = *reinterpret_cast<const uint4*>(xa);
-        uint4 b = b2_operand<0>(cp[0].x, lut, slot);
-        f32x4 d[2];
-        float sf = 0.f;
+        uint4 b[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) b[r] = b2_operand<0, BL>(cp[r][0].x, lut, slot);
+        f32x4 d[R][2];
+        float sf[R];
         steps(cp, sp, lut, slot, xa, a, b, d, sf, acc, std::make_integer_sequence<int, 32>{});
     }
 };
@@ -1333,7 +1378,10 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
                       job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
-    __shared__ uint4 lut_storage[kB2LutU4];
+    // the nibble table: filling the byte table's 32 KB costs a per-linear launch more than
+    // its reads save (M = 1 per-linear 2-bit stack 0.497 -> 0.588 ms, same box)
+    constexpr bool BL = false;
+    __shared__ uint4 lut_storage[BL ? kB2ByteLutU4 : kB2LutU4];
     // Two activation buffers per wave, each its own LDS object ending in a zero block, so
     // that the compiler can tell the reads of one from the DMA into the other (it waits for
     // every outstanding load before an LDS read that may alias a pending DMA target).
@@ -1342,7 +1390,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     __shared__ __attribute__((aligned(16))) char xs1[kXsBytes + kB2ZeroBytes];
     __shared__ float red[kB2Waves][MM][64];
 
-    fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
+    if constexpr (BL) fill_b2blut<DT, 64 * kB2Waves>(lut_storage);
+    else fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
     for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * kB2Waves) {
         reinterpret_cast<uint4*>(xs0 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
         reinterpret_cast<uint4*>(xs1 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -1362,7 +1411,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const uint32_t row = (uint32_t)(tile * 16 + i16);
     const uint32_t vo_code = row * rowbytes + 16u * g;
     const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
-    const uint32_t slot = (uint32_t)(lane & 31) * 4u;
+    const uint32_t slot = b2_slot<BL>(lane);
 
     // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
     const int am = i16 & 3;
@@ -1377,13 +1426,14 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     // wave w takes rounds w, w + W, ...: its own register sets and activation buffers, so
     // the waves never wait for each other inside the loop
     const int T = (int)(K / kRound);
-    float acc[MM];
+    float acc[1][MM];
 #pragma unroll
-    for (int q = 0; q < MM; ++q) acc[q] = 0.f;
-    uint4 cp[2][4], sp[2][4];
+    for (int q = 0; q < MM; ++q) acc[0][q] = 0.f;
+    uint4 cp[2][1][4], sp[2][1][4];
+    using Round = B2Round<DT, MM, GS, 1, BL>;
     int u = wave;
     if (u < T) {
-        b2_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, u);
+        b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, u);
         b2_stage_x<MM>(xw0, xr, u, M, K, lane);
     }
     __syncthreads();  // table and zero block ready
@@ -1395,25 +1445,25 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     // second half's prefetch of round u + 2W re-fetches round T - 1 (an L2 hit, never
     // read) when there is none.
     while (u + kB2Waves < T) {  // uniform within the wave
-        b2_load<GS>(cp[1], sp[1], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        b2_load<GS>(cp[1][0], sp[1][0], pr, sr, vo_code, vo_scale, u + kB2Waves);
         b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
         vm_wait_le_round<GS, MM>();  // round u's codes, scales and activations have landed
-        B2Round<DT, MM, GS>::run(cp[0], sp[0], lut, slot, xa0, acc);
+        Round::run(cp[0], sp[0], lut, slot, xa0, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
         const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
-        b2_load<GS>(cp[0], sp[0], pr, sr, vo_code, vo_scale, un);
+        b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, un);
         b2_stage_x<MM>(xw0, xr, un, M, K, lane);
         vm_wait_le_round<GS, MM>();
-        B2Round<DT, MM, GS>::run(cp[1], sp[1], lut, slot, xa1, acc);
+        Round::run(cp[1], sp[1], lut, slot, xa1, acc);
         lds_wait_all();
         u += 2 * kB2Waves;
     }
     vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
-    if (u < T) B2Round<DT, MM, GS>::run(cp[0], sp[0], lut, slot, xa0, acc);
+    if (u < T) Round::run(cp[0], sp[0], lut, slot, xa0, acc);
 
     // add the waves' partial sums, then the four lane groups; lane group q stores row q
 #pragma unroll
-    for (int q = 0; q < MM; ++q) red[wave][q][lane] = acc[q];
+    for (int q = 0; q < MM; ++q) red[wave][q][lane] = acc[0][q];
     __syncthreads();
     if (wave != 0) return;
     float out = 0.f;
@@ -2199,12 +2249,12 @@ __device__ __forceinline__ uint4 lut_item(int i, int kind) {
 //
 // The fused epilogue adds u @ B with u = scaling * (x @ A) [M, 8] (lattice.py:839-842).
 // Instead of a separate down-projection launch before the GEMV, every workgroup of an
-// adapter job forms u itself: each wave of its first tile set adds the k range of its own
-// round, whose activations are already in its stage.  Lane l takes k = 16 l .. 16 l + 15 of
-// the round: 16 rows of A (16 bytes each, loaded when the round's weights are requested),
-// two 16-byte activation pieces per row m, and v_dot2 products of k pairs (the pair of A
-// values of one column is put together by one v_perm).  The lanes' partial sums are added
-// through the wave's own stage, the waves' through LDS, and the epilogue lanes read u there.
+// adapter job forms u itself: each wave adds the k range of its own round.  Lane l takes
+// k = 16 l .. 16 l + 15 of the round: 16 rows of A (16 bytes each) and two 16-byte
+// activation pieces per row m, loaded into registers before the round's weights are
+// requested, so that the v_dot2 products of k pairs (the pair of A values of one column is
+// put together by one v_perm) and the lanes' sum run while the weights are in flight.  The
+// waves' totals meet in LDS, and the epilogue lanes read u there.
 constexpr int kLoraInlineRank = 8;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -2234,11 +2284,38 @@ __device__ __forceinline__ void lora_load_a(const void* a, int64_t K, int64_t k0
     }
 }
 
-// part[m][j] += sum over this lane's 16 k of x[m][k] A[k][j]; x piece p (8 k) of activation
-// row m at xst + 16 (145 m + p + 4 (p / 32)) (the staged-tile layout; rows >= M are zeros).
+// B[j][row] for j < 8 (bf16/fp16 bits), from a buffer of `live` columns (0: zeros).
+__device__ __forceinline__ void lora_load_bcol(const void* b, int64_t live, int64_t N,
+                                               int64_t row, uint32_t (&bq)[kLoraInlineRank]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)b, (short)0, (int)(live * kLoraInlineRank * 2), kRsrcWord3);
+#pragma unroll
+    for (int j = 0; j < kLoraInlineRank; ++j)
+        bq[j] = __builtin_amdgcn_raw_buffer_load_b16(r, (uint32_t)(j * N + row) * 2u, 0, 0);
+}
+
+// x[m][k0 + 16 lane .. + 15] for m < MM as two 16-byte pieces per row (rows >= M lie past
+// the buffer's M * K * 2 bytes and read zeros).
+template <int MM>
+__device__ __forceinline__ void lora_load_x(const void* x, int M, int64_t K, int64_t k0,
+                                            int lane, uint4 (&xr)[2 * MM]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        const uint32_t vo = (uint32_t)((int64_t)m * K + k0 + 16 * lane) * 2u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo + 16u * h, 0, 0);
+            xr[2 * m + h] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    }
+}
+
+// part[m][j] = sum over this lane's 16 k of x[m][k] A[k][j].
 template <int DT, int MM>
-__device__ __forceinline__ void lora_round_part(const uint4 (&ar)[16], const char* xst, int lane,
-                                                float (&part)[MM][kLoraInlineRank]) {
+__device__ __forceinline__ void lora_lane_part(const uint4 (&ar)[16], const uint4 (&xr)[2 * MM],
+                                               float (&part)[MM][kLoraInlineRank]) {
     uint32_t lo[8][4], hi[8][4];  // (A[k][c], A[k + 1][c]) for k pair kp, columns 2h, 2h + 1
 #pragma unroll
     for (int kp = 0; kp < 8; ++kp) {
@@ -2251,14 +2328,12 @@ __device__ __forceinline__ void lora_round_part(const uint4 (&ar)[16], const cha
             hi[kp][h] = __builtin_amdgcn_perm(r1[h], r0[h], 0x07060302u);
         }
     }
-    const uint32_t p0 = 2u * (uint32_t)lane;  // pieces p0, p0 + 1 (same 32-piece run)
-    lds_wait_all();
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
-        const char* xp = xst + 16u * (145u * (uint32_t)m + p0 + 4u * (p0 >> 5));
-        const uint4 x0 = *reinterpret_cast<const uint4*>(xp);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(xp + 16);
+        const uint4 x0 = xr[2 * m], x1 = xr[2 * m + 1];
         const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int j = 0; j < kLoraInlineRank; ++j) part[m][j] = 0.f;
 #pragma unroll
         for (int kp = 0; kp < 8; ++kp)
 #pragma unroll
@@ -2269,25 +2344,34 @@ __device__ __forceinline__ void lora_round_part(const uint4 (&ar)[16], const cha
     }
 }
 
-// Sum of part over the wave's 64 lanes through `scr` (64 x (V + 1) floats of this wave's own
-// LDS); lane c < V returns the total of column c = 8 m + j.
-template <int MM>
-__device__ __forceinline__ float lora_wave_sum(const float (&part)[MM][kLoraInlineRank], float* scr,
-                                               int lane) {
-    constexpr int V = MM * kLoraInlineRank, G = 64 / V;  // G lane groups share a column
-    lds_wait_all();  // the activation reads of the stage are done before it is written
+// One halving exchange of wave_sum_scatter at offset 32 >> ST over the first 2h values, with
+// every index a compile-time constant (a select between array elements indexed by a loop
+// variable becomes a dynamically indexed private array).
+template <int h, int o, int... I>
+__device__ __forceinline__ void halve_exchange(float* w, bool up, std::integer_sequence<int, I...>) {
+    ((w[I] = (up ? w[I + h] : w[I]) + __shfl_xor(up ? w[I] : w[I + h], o)), ...);
+}
+
+// Sum of v[c] over the wave's 64 lanes for each of its V values (V a power of two <= 64),
+// by halving exchanges: at offset o = 32, 16, ... a lane keeps the upper half of its live
+// values if lane & o, sends the other half to lane ^ o and adds what it receives; then the
+// lanes holding the same value add theirs.  Lane l returns the total of value l >> (6 - log2 V).
+template <int V>
+__device__ __forceinline__ float wave_sum_scatter(const float (&v)[V], int lane) {
+    constexpr int LV = V == 1 ? 0 : V == 2 ? 1 : V == 4 ? 2 : V == 8 ? 3 : V == 16 ? 4 : V == 32 ? 5 : 6;
+    static_assert((1 << LV) == V, "V is a power of two <= 64");
+    float w[V];
+    [&]<int... I>(std::integer_sequence<int, I...>) { ((w[I] = v[I]), ...); }(
+        std::make_integer_sequence<int, V>{});
+    [&]<int... ST>(std::integer_sequence<int, ST...>) {
+        ((halve_exchange<(V >> ST) / 2, (32 >> ST)>(w, (lane & (32 >> ST)) != 0,
+                                                    std::make_integer_sequence<int, (V >> ST) / 2>{})),
+         ...);
+    }(std::make_integer_sequence<int, LV>{});
+    float t = w[0];
 #pragma unroll
-    for (int m = 0; m < MM; ++m)
-#pragma unroll
-        for (int j = 0; j < kLoraInlineRank; ++j) scr[lane * (V + 1) + 8 * m + j] = part[m][j];
-    lds_wait_all();
-    const int c = lane % V, r0 = (lane / V) * (64 / G);
-    float v = 0.f;
-#pragma unroll
-    for (int r = 0; r < 64 / G; ++r) v += scr[(r0 + r) * (V + 1) + c];
-#pragma unroll
-    for (int o = V; o < 64; o <<= 1) v += __shfl_xor(v, o);
-    return v;
+    for (int o = 32 >> LV; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+    return t;
 }
 
 // RT: row tiles per wave (they share the activation stage and the A fragment reads); a
@@ -2339,39 +2423,63 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     const int nr = T - u0 < U ? (T - u0 > 0 ? T - u0 : 0) : U;  // rounds of this wave
 
     // ---- every load first (rows >= N and activation rows >= M read zeros)
+    // The in-launch adapter issues every load on every wave, with no branch, so that the
+    // compiler's wait for the adapter's registers counts the stage loads issued after them
+    // (a branch would make it wait for all of them); loads a wave does not need go to empty
+    // buffers, which return zeros without a memory access.
+    const bool dead = kLoraIn && nr == 0;  // a wave without a round (K < 4096)
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+        (void*)job.packed, (short)0, dead ? 0 : (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)job.scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+        (void*)job.scales, (short)0, dead ? 0 : (int)(N * srowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)xbase, (short)0, (int)(M * K * 2), kRsrcWord3);
+        (void*)xbase, (short)0, dead ? 0 : (int)(M * K * 2), kRsrcWord3);
     char* const wstage = stage + wave * U * S::kBytes;
-#pragma unroll
-    for (int i = 0; i < U; ++i)
-        if (i < nr)
-            tile_issue(wstage + i * S::kBytes, pr, sr, xr, row0, rowbytes, srowbytes,
-                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M, RT, GS);
-    // the adapter's rows of A for this wave's round (the waves of tile set 0 form u)
+    // the adapter's operands first (x and A of this wave's round, into registers; the
+    // epilogue lanes' column of B, rows past N reading row N - 1), so that u is formed
+    // while the weights are in flight
     const bool lora_in = kLoraIn && args.lora_inline && job.lora_r > 0;  // uniform
-    const bool lora_wave = lora_in && sub == 0 && nr > 0;
-    uint4 lora_a[16];
-    if (lora_wave) lora_load_a(job.lora_a, K, (int64_t)u0 * 1024, lane, lora_a);
-    // ... and the epilogue lanes' column of B (rows past N read row N - 1)
+    const bool lora_wave = lora_in && nr > 0;
+    uint4 lora_a[kLoraIn ? 16 : 1], lora_x[kLoraIn ? 2 * MM : 1];
     uint32_t lora_bq[kLoraIn ? kLoraInlineRank : 1];
     if constexpr (kLoraIn) {
-        if (lora_in && wt == 0) {
-            const int64_t rr = (int64_t)row0 + i16 < N ? (int64_t)row0 + i16 : N - 1;
-            const __attribute__((address_space(1))) uint16_t* bp =
-                (const __attribute__((address_space(1))) uint16_t*)job.lora_b;
-#pragma unroll
-            for (int j = 0; j < kLoraInlineRank; ++j) lora_bq[j] = bp[j * N + rr];
-        }
+        const int64_t k0 = (int64_t)u0 * 1024;
+        lora_load_x<MM>(xbase, lora_wave ? M : 0, K, k0, lane, lora_x);
+        lora_load_a(job.lora_a, lora_wave ? K : 0, k0, lane, lora_a);
+        lora_load_bcol(job.lora_b, lora_in && wt == 0 ? N : 0, N,
+                       (int64_t)row0 + i16 < N ? (int64_t)row0 + i16 : N - 1, lora_bq);
     }
+#pragma unroll
+    for (int i = 0; i < U; ++i)
+        if (kLoraIn || i < nr)
+            tile_issue(wstage + i * S::kBytes, pr, sr, xr, row0, rowbytes, srowbytes,
+                       (uint32_t)(K * 2), u0 + i, lane, S::kXLoads, M, RT, GS);
 
     // ---- decode table (computed) while the loads are in flight
     for (int i = (int)threadIdx.x; i < TileLut::kValidStorageU4; i += 64 * NW)
         lut_storage[i] = lut_item<SL>(i, lut_values_kind<DT>());
     if (threadIdx.x < 96) zrun[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+
+    // this wave's total of x @ A over its round (lanes 2c, 2c + 1 hold column c = 8 m + j;
+    // lanes 8c .. 8c + 7 at M = 1) while the stage's loads are in flight: before the
+    // barrier, which waits for every load of the wave
+    if constexpr (kLoraIn) {
+        if (lora_in) {
+            constexpr int V = MM * kLoraInlineRank;
+            float part[MM][kLoraInlineRank];
+            if (lora_wave) {
+                lora_lane_part<DT, MM>(lora_a, lora_x, part);
+            } else {
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+#pragma unroll
+                    for (int j = 0; j < kLoraInlineRank; ++j) part[m][j] = 0.f;
+            }
+            const float v = wave_sum_scatter<V>(reinterpret_cast<const float(&)[V]>(part), lane);
+            if ((lane & (64 / V - 1)) == 0) lora_tot[wt][lane / (64 / V)] = v;
+        }
+    }
+
     uint32_t bias_bits[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
@@ -2400,16 +2508,9 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     auto round = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
         if (i >= nr) return;
-        // round i's loads have landed when at most the later rounds' are outstanding (and
-        // the adapter rows of A, requested after them)
-        if constexpr (kLoraIn) {
-            if (lora_wave && wt == 0) vm_wait_le<16 + kLoraInlineRank>();
-            else if (lora_wave) vm_wait_le<16>();
-            else vm_wait_all();
-        } else {
-            if (nr == U) vm_wait_le<L * (U - 1 - i)>();
-            else vm_wait_all();
-        }
+        // round i's loads have landed when at most the later rounds' are outstanding
+        if (nr == U) vm_wait_le<L * (U - 1 - i)>();
+        else vm_wait_all();
         const char* stg = wstage + i * S::kBytes;
         TileRound<DT, MM, RT, GS> r;
 #pragma unroll
@@ -2460,19 +2561,6 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     [&]<int... I>(std::integer_sequence<int, I...>) {
         (round(std::integral_constant<int, I>{}), ...);
     }(std::make_integer_sequence<int, U>{});
-    if constexpr (kLoraIn) {
-        if (lora_in) {
-            float part[MM][kLoraInlineRank];
-#pragma unroll
-            for (int m = 0; m < MM; ++m)
-#pragma unroll
-                for (int j = 0; j < kLoraInlineRank; ++j) part[m][j] = 0.f;
-            if (lora_wave) lora_round_part<DT, MM>(lora_a, wstage + S::kX, lane, part);
-            const float v = lora_wave_sum<MM>(part, reinterpret_cast<float*>(wstage), lane);
-            if (lane < MM * kLoraInlineRank) lora_tot[wt][lane] = v;
-        }
-    }
-
     // sum the four lane groups of each row (lane group q keeps activation row q), then the
     // waves through LDS (zrun is no longer read)
     float out[RT];
@@ -2948,21 +3036,26 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
 // activation stage per round (W * R * 16 rows per x round), with one barrier per round.
 // Each lane loads its codes and scales of the next round into registers while the current
 // round computes (the per-linear kernels' load pattern: 64 contiguous bytes of 16 rows per
-// instruction).  MM <= 4: post-scaled 1024-k rounds (B2Round); MM = 16: the B-operand
-// 256-k rounds (B2mRound, R tiles sharing each A fragment).
+// instruction).  MM <= 4: post-scaled 1024-k rounds (B2Round over the byte table, R tiles
+// sharing each A fragment; the nibble table's four reads and address computations per 8
+// weights made the kernel VALU- and LDS-issue-bound: 17.2 VALU and 5.0 LDS instructions per
+// MFMA against 10.5 and 2.5, M = 4 stack 0.725 -> 0.605 ms, same box); MM = 16: the
+// B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).
 template <int DT, int GS, int MM, int R, int W>
 __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
     static_assert(MM == 1 || MM == 4 || MM == 16, "activation rows 1, 4 or 16");
     constexpr int kXBytes = kPost ? MM * (int)kXRow : kB2mXBytes;  // one round's stage
-    __shared__ uint4 lut_storage[kB2LutU4];
+    constexpr bool BL = kPost;  // byte table (post-scaled), selector table (B operand)
+    __shared__ uint4 lut_storage[BL ? kB2ByteLutU4 : kB2LutU4];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
     // (the A fragments of lanes outside their lane group)
     __shared__ __attribute__((aligned(128))) char xs0[kXBytes + (kPost ? kB2ZeroBytes : 0)];
     __shared__ __attribute__((aligned(128))) char xs1[kXBytes + (kPost ? kB2ZeroBytes : 0)];
 
     if constexpr (kPost) {
-        fill_b2lut<DT, 64 * W>(lut_storage);
+        if constexpr (BL) fill_b2blut<DT, 64 * W>(lut_storage);
+        else fill_b2lut<DT, 64 * W>(lut_storage);
         for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * W) {
             reinterpret_cast<uint4*>(xs0 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
             reinterpret_cast<uint4*>(xs1 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -2999,7 +3092,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
         vo_code[r] = row * rowbytes + 16u * g;
         vo_scale[r] = row * srowbytes + (128u / GS) * g;
     }
-    const uint32_t slot = (uint32_t)(lane & 31) * 4u;
+    const uint32_t slot = kPost ? b2_slot<BL>(lane) : (uint32_t)(lane & 31) * 4u;
     const int T = (int)(K / (kPost ? kRound : kB2mRound));
 
     // this lane's activation reads: post-scaled A row i16 = 4 g' + m is live in lane group g'
@@ -3054,9 +3147,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     const char* lut = reinterpret_cast<const char*>(lut_storage);
     auto compute = [&](const Piece (&cp)[R], const Piece (&sp)[R], const char* xs) {
         if constexpr (kPost) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                B2Round<DT, MM, GS>::run(cp[r], sp[r], lut, slot, xs + aoff, accp[r]);
+            B2Round<DT, MM, GS, R, BL>::run(cp, sp, lut, slot, xs + aoff, accp);
         } else {
             B2mRound<DT, GS, kFmt2Bit, R>::run(cp, sp, lut, slot, xs, xo, accm);
         }
