@@ -1158,13 +1158,16 @@ __global__ __launch_bounds__(64 * W) void gemv_psk_kernel(GemvLaunch args) {
 // k slots and its group scale can multiply it every gs/8 steps; the four lane groups are
 // added at the end.
 //
-// The byte table (BL): each code byte (four codes) indexes a 256-entry table of four weights
-// (8 bytes) with 16 copies, lane l reading copy l % 16: two conflict-free b64 reads and two
-// address computations per 8 weights instead of four of each.  It takes 32 KB of LDS.
+// The byte table (BC copies, BC = 0: the nibble table): each code byte (four codes) indexes a
+// 256-entry table of four weights (8 bytes) with BC copies, lane l reading copy l % BC: two
+// b64 reads and two address computations per 8 weights instead of four of each.  16 copies
+// (32 KB) leave two 4-wave workgroups per CU at M = 4; 32 copies (64 KB) make the reads
+// conflict-free.
 
 constexpr int kB2Waves = 4;
 constexpr int kB2LutU4 = 16 * 32 * 4 / 16;  // 16 entries x 32 copies x 4 bytes
-constexpr int kB2ByteLutU4 = 256 * 16 * 8 / 16;  // 256 entries x 16 copies x 8 bytes
+template <int BC>
+constexpr int kB2ByteLutU4 = 256 * BC * 8 / 16;  // 256 entries x BC copies x 8 bytes
 constexpr int kB2ZeroBytes = 2048;          // covers the largest A-fragment offset of a round
 
 template <int DT>
@@ -1182,10 +1185,10 @@ __device__ __forceinline__ void fill_b2lut(uint4* lut) {
     }
 }
 
-template <int DT, int NT>
+template <int DT, int NT, int BC>
 __device__ __forceinline__ void fill_b2blut(uint4* lut) {
-    for (int i = (int)threadIdx.x; i < kB2ByteLutU4; i += NT) {
-        const int e = i >> 3;  // 8 items (16 copies x 8 bytes) per entry
+    for (int i = (int)threadIdx.x; i < kB2ByteLutU4<BC>; i += NT) {
+        const int e = i / (BC / 2);  // BC / 2 items (BC copies x 8 bytes) per entry
         const uint32_t lo = b2_half<DT>(e & 3) | (b2_half<DT>((e >> 2) & 3) << 16);
         const uint32_t hi = b2_half<DT>((e >> 4) & 3) | (b2_half<DT>(e >> 6) << 16);
         lut[i] = make_uint4(lo, hi, lo, hi);
@@ -1193,18 +1196,19 @@ __device__ __forceinline__ void fill_b2blut(uint4* lut) {
 }
 
 // The table slot of a lane: 32 copies of 4 bytes, or 16 copies of 8 bytes (byte table).
-template <bool BL>
+template <int BC>
 __device__ __forceinline__ uint32_t b2_slot(int lane) {
-    return BL ? (uint32_t)(lane & 15) * 8u : (uint32_t)(lane & 31) * 4u;
+    return BC ? (uint32_t)(lane & (BC - 1)) * 8u : (uint32_t)(lane & 31) * 4u;
 }
 
 // B operand of the 8 codes in half-word H of dword dw: four nibble-table reads, or two
 // byte-table reads.
-template <int H, bool BL>
+template <int H, int BC>
 __device__ __forceinline__ uint4 b2_operand(uint32_t dw, const char* lut, uint32_t slot) {
-    if constexpr (BL) {
-        const uint32_t a0 = (__builtin_amdgcn_ubfe(dw, 16 * H, 8) << 7) | slot;
-        const uint32_t a1 = (__builtin_amdgcn_ubfe(dw, 16 * H + 8, 8) << 7) | slot;
+    if constexpr (BC != 0) {
+        constexpr int sh = BC == 32 ? 8 : 7;  // entry stride BC x 8 bytes
+        const uint32_t a0 = (__builtin_amdgcn_ubfe(dw, 16 * H, 8) << sh) | slot;
+        const uint32_t a1 = (__builtin_amdgcn_ubfe(dw, 16 * H + 8, 8) << sh) | slot;
         const uint2 v0 = *reinterpret_cast<const uint2*>(lut + a0);
         const uint2 v1 = *reinterpret_cast<const uint2*>(lut + a1);
         return make_uint4(v0.x, v0.y, v1.x, v1.y);
@@ -1232,7 +1236,7 @@ __device__ __forceinline__ uint32_t b2_scale(const uint4 (&sp)[4]) {
 // One round of R row tiles of one wave: steps 0..31, the A fragment read once per step for
 // all R tiles, with the table reads and A fragment of step J + 1 issued before the MFMAs of
 // step J and the scale of a finished group applied after the next group's first MFMA.
-template <int DT, int MM, int GS, int R, bool BL>
+template <int DT, int MM, int GS, int R, int BC>
 struct B2Round {
     static constexpr int kSpg = GS / 8;  // steps per scale group
     using Pieces = uint4[R][4];
@@ -1250,7 +1254,7 @@ struct B2Round {
             for (int r = 0; r < R; ++r) {
                 const uint32_t dw = (hw / 2) == 0 ? cp[r][t].x : (hw / 2) == 1 ? cp[r][t].y
                                   : (hw / 2) == 2 ? cp[r][t].z : cp[r][t].w;
-                b_n[r] = b2_operand<(hw % 2), BL>(dw, lut, slot);
+                b_n[r] = b2_operand<(hw % 2), BC>(dw, lut, slot);
             }
         }
         constexpr int grp = J / kSpg, slot_d = grp & 1;
@@ -1296,7 +1300,7 @@ struct B2Round {
         uint4 a = *reinterpret_cast<const uint4*>(xa);
         uint4 b[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) b[r] = b2_operand<0, BL>(cp[r][0].x, lut, slot);
+        for (int r = 0; r < R; ++r) b[r] = b2_operand<0, BC>(cp[r][0].x, lut, slot);
         f32x4 d[R][2];
         float sf[R];
         steps(cp, sp, lut, slot, xa, a, b, d, sf, acc, std::make_integer_sequence<int, 32>{});
@@ -1380,8 +1384,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
     // the nibble table: filling the byte table's 32 KB costs a per-linear launch more than
     // its reads save (M = 1 per-linear 2-bit stack 0.497 -> 0.588 ms, same box)
-    constexpr bool BL = false;
-    __shared__ uint4 lut_storage[BL ? kB2ByteLutU4 : kB2LutU4];
+    constexpr int BC = 0;
+    __shared__ uint4 lut_storage[kB2LutU4];
     // Two activation buffers per wave, each its own LDS object ending in a zero block, so
     // that the compiler can tell the reads of one from the DMA into the other (it waits for
     // every outstanding load before an LDS read that may alias a pending DMA target).
@@ -1390,8 +1394,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     __shared__ __attribute__((aligned(16))) char xs1[kXsBytes + kB2ZeroBytes];
     __shared__ float red[kB2Waves][MM][64];
 
-    if constexpr (BL) fill_b2blut<DT, 64 * kB2Waves>(lut_storage);
-    else fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
+    fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
     for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * kB2Waves) {
         reinterpret_cast<uint4*>(xs0 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
         reinterpret_cast<uint4*>(xs1 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -1411,7 +1414,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const uint32_t row = (uint32_t)(tile * 16 + i16);
     const uint32_t vo_code = row * rowbytes + 16u * g;
     const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
-    const uint32_t slot = b2_slot<BL>(lane);
+    const uint32_t slot = b2_slot<BC>(lane);
 
     // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
     const int am = i16 & 3;
@@ -1430,7 +1433,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
 #pragma unroll
     for (int q = 0; q < MM; ++q) acc[0][q] = 0.f;
     uint4 cp[2][1][4], sp[2][1][4];
-    using Round = B2Round<DT, MM, GS, 1, BL>;
+    using Round = B2Round<DT, MM, GS, 1, BC>;
     int u = wave;
     if (u < T) {
         b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, u);
@@ -1517,17 +1520,44 @@ __device__ __forceinline__ void fill_b2sel(uint4* lut) {
     }
 }
 
-// B operand (8 weights) of half-word H of this lane's 16-byte code piece.
-template <int H>
+// The byte form (BC copies, as the post-scaled byte table): a code byte -> the selector
+// words of its two nibbles (8 bytes), one b64 read per four weights.
+template <int NT, int BC>
+__device__ __forceinline__ void fill_b2bsel(uint4* lut) {
+    auto sel = [](uint32_t n) {
+        const uint32_t c0 = n & 3u, c1 = n >> 2;
+        return (2u * c0) | ((2u * c0 + 1u) << 8) | ((2u * c1) << 16) | ((2u * c1 + 1u) << 24);
+    };
+    for (int i = (int)threadIdx.x; i < kB2ByteLutU4<BC>; i += NT) {
+        const uint32_t e = (uint32_t)i / (BC / 2);
+        const uint32_t lo = sel(e & 15u), hi = sel(e >> 4);
+        lut[i] = make_uint4(lo, hi, lo, hi);
+    }
+}
+
+// B operand (8 weights) of half-word H of this lane's 16-byte code piece: nibble selectors
+// (BC = 0) or byte selector pairs.
+template <int H, int BC = 0>
 __device__ __forceinline__ uint4 b2m_operand(const uint4& cp, const uint2& val, const char* lut,
                                              uint32_t slot) {
     const uint32_t dw = (H / 2) == 0 ? cp.x : (H / 2) == 1 ? cp.y : (H / 2) == 2 ? cp.z : cp.w;
     uint32_t v[4];
+    if constexpr (BC != 0) {
+        constexpr int sh = BC == 32 ? 8 : 7;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * (H % 2) + 4 * i, 4) << 7) | slot;
-        const uint32_t sel = *reinterpret_cast<const uint32_t*>(lut + a);
-        v[i] = __builtin_amdgcn_perm(val.x, val.y, sel);
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * (H % 2) + 8 * j, 8) << sh) | slot;
+            const uint2 sel = *reinterpret_cast<const uint2*>(lut + a);
+            v[2 * j] = __builtin_amdgcn_perm(val.x, val.y, sel.x);
+            v[2 * j + 1] = __builtin_amdgcn_perm(val.x, val.y, sel.y);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = (__builtin_amdgcn_ubfe(dw, 16 * (H % 2) + 4 * i, 4) << 7) | slot;
+            const uint32_t sel = *reinterpret_cast<const uint32_t*>(lut + a);
+            v[i] = __builtin_amdgcn_perm(val.x, val.y, sel);
+        }
     }
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
@@ -1572,11 +1602,11 @@ __device__ __forceinline__ uint2 values_of(uint32_t s16) {
     }
 }
 
-template <int FMT, int H>
+template <int FMT, int H, int BC = 0>
 __device__ __forceinline__ uint4 operand_of(const uint4& cp, const uint2& val, const char* lut,
                                             uint32_t slot) {
     if constexpr (FMT == kFmtRoot) return root_operand<H>(cp, val, lut);
-    else if constexpr (FMT == kFmt2Bit) return b2m_operand<H>(cp, val, lut, slot);
+    else if constexpr (FMT == kFmt2Bit) return b2m_operand<H, BC>(cp, val, lut, slot);
     else return ternary_operand<H>(cp, val, lut, slot);
 }
 
@@ -1597,7 +1627,7 @@ __device__ __forceinline__ uint32_t b2m_scale(const uint4& sp) {
 // two from 256 tiles on (q/o, down) 5.7 -> 7.4 and 13.9 -> 18.8 us.
 constexpr int64_t kB2mTwoTilesFrom = 512;
 
-template <int DT, int GS, int FMT, int R>
+template <int DT, int GS, int FMT, int R, int BC = 0>
 struct B2mRound {
     // step H: the A fragment and B operands of step H + 1 are formed before the MFMAs of
     // step H are issued; the R tiles share the A fragment
@@ -1612,7 +1642,7 @@ struct B2mRound {
             for (int r = 0; r < R; ++r) {
                 if constexpr ((8 * (H + 1)) % GS == 0)
                     val[r] = values_of<DT, FMT>(b2m_scale<GS, H + 1>(sp[r]));
-                b_n[r] = operand_of<FMT, H + 1>(cp[r], val[r], lut, slot);
+                b_n[r] = operand_of<FMT, H + 1, BC>(cp[r], val[r], lut, slot);
             }
             a_n = *reinterpret_cast<const uint4*>(xs + (xo ^ (16u * (H + 1))));
         }
@@ -1640,7 +1670,7 @@ struct B2mRound {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             val[r] = values_of<DT, FMT>(b2m_scale<GS, 0>(sp[r]));
-            b[r] = operand_of<FMT, 0>(cp[r], val[r], lut, slot);
+            b[r] = operand_of<FMT, 0, BC>(cp[r], val[r], lut, slot);
         }
         uint4 a = *reinterpret_cast<const uint4*>(xs + xo);
         steps(cp, sp, lut, slot, xs, xo, a, b, val, acc, std::make_integer_sequence<int, 8>{});
@@ -3046,22 +3076,23 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
     static_assert(MM == 1 || MM == 4 || MM == 16, "activation rows 1, 4 or 16");
     constexpr int kXBytes = kPost ? MM * (int)kXRow : kB2mXBytes;  // one round's stage
-    constexpr bool BL = kPost;  // byte table (post-scaled), selector table (B operand)
-    __shared__ uint4 lut_storage[BL ? kB2ByteLutU4 : kB2LutU4];
+    // the byte tables (16 copies; 32 copies, conflict-free, measured 2% slower at M = 1):
+    // weights (post-scaled) or selector pairs (B operand)
+    constexpr int BC = 16;
+    __shared__ uint4 lut_storage[kB2ByteLutU4<BC>];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
     // (the A fragments of lanes outside their lane group)
     __shared__ __attribute__((aligned(128))) char xs0[kXBytes + (kPost ? kB2ZeroBytes : 0)];
     __shared__ __attribute__((aligned(128))) char xs1[kXBytes + (kPost ? kB2ZeroBytes : 0)];
 
     if constexpr (kPost) {
-        if constexpr (BL) fill_b2blut<DT, 64 * W>(lut_storage);
-        else fill_b2lut<DT, 64 * W>(lut_storage);
+        fill_b2blut<DT, 64 * W, BC>(lut_storage);
         for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * W) {
             reinterpret_cast<uint4*>(xs0 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
             reinterpret_cast<uint4*>(xs1 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
         }
     } else {
-        fill_b2sel<64 * W>(lut_storage);
+        fill_b2bsel<64 * W, BC>(lut_storage);
     }
 
     int64_t wg = blockIdx.x;
@@ -3092,7 +3123,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
         vo_code[r] = row * rowbytes + 16u * g;
         vo_scale[r] = row * srowbytes + (128u / GS) * g;
     }
-    const uint32_t slot = kPost ? b2_slot<BL>(lane) : (uint32_t)(lane & 31) * 4u;
+    const uint32_t slot = b2_slot<BC>(lane);
     const int T = (int)(K / (kPost ? kRound : kB2mRound));
 
     // this lane's activation reads: post-scaled A row i16 = 4 g' + m is live in lane group g'
@@ -3147,9 +3178,9 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     const char* lut = reinterpret_cast<const char*>(lut_storage);
     auto compute = [&](const Piece (&cp)[R], const Piece (&sp)[R], const char* xs) {
         if constexpr (kPost) {
-            B2Round<DT, MM, GS, R, BL>::run(cp, sp, lut, slot, xs + aoff, accp);
+            B2Round<DT, MM, GS, R, BC>::run(cp, sp, lut, slot, xs + aoff, accp);
         } else {
-            B2mRound<DT, GS, kFmt2Bit, R>::run(cp, sp, lut, slot, xs, xo, accm);
+            B2mRound<DT, GS, kFmt2Bit, R, BC>::run(cp, sp, lut, slot, xs, xo, accm);
         }
     };
 
