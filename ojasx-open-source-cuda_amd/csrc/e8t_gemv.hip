@@ -1444,25 +1444,33 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     // Rounds in pairs (u, u + W), each prefetching the next: the loop body has no branch
     // between the two halves, so the compiler neither sinks the prefetch of the second
     // half's codes below the first half's compute nor loses track of which activation
-    // buffer a pending DMA writes (either would make it wait for the prefetch).  The
-    // second half's prefetch of round u + 2W re-fetches round T - 1 (an L2 hit, never
-    // read) when there is none.
-    while (u + kB2Waves < T) {  // uniform within the wave
+    // buffer a pending DMA writes (either would make it wait for the prefetch).  The last
+    // pair or round runs after the loop, with nothing fetched behind it (a spare fetch
+    // would add a memory round trip to the wave's end).
+    while (u + 2 * kB2Waves < T) {  // uniform within the wave
         b2_load<GS>(cp[1][0], sp[1][0], pr, sr, vo_code, vo_scale, u + kB2Waves);
         b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
         vm_wait_le_round<GS, MM>();  // round u's codes, scales and activations have landed
         Round::run(cp[0], sp[0], lut, slot, xa0, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
-        const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
-        b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, un);
-        b2_stage_x<MM>(xw0, xr, un, M, K, lane);
+        b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, u + 2 * kB2Waves);
+        b2_stage_x<MM>(xw0, xr, u + 2 * kB2Waves, M, K, lane);
         vm_wait_le_round<GS, MM>();
         Round::run(cp[1], sp[1], lut, slot, xa1, acc);
         lds_wait_all();
         u += 2 * kB2Waves;
     }
-    vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
-    if (u < T) Round::run(cp[0], sp[0], lut, slot, xa0, acc);
+    if (u + kB2Waves < T) {  // a last pair
+        b2_load<GS>(cp[1][0], sp[1][0], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
+        vm_wait_le_round<GS, MM>();
+        Round::run(cp[0], sp[0], lut, slot, xa0, acc);
+        vm_wait_all();
+        Round::run(cp[1], sp[1], lut, slot, xa1, acc);
+    } else if (u < T) {  // a last round
+        vm_wait_all();
+        Round::run(cp[0], sp[0], lut, slot, xa0, acc);
+    }
 
     // add the waves' partial sums, then the four lane groups; lane group q stores row q
 #pragma unroll
@@ -1823,8 +1831,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
     __syncthreads();  // selector table ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) +
                       (FMT == kFmtTernary ? kLutBaseOffset : 0u);
-    // rounds in pairs, as in gemv2_kernel
-    while (u + kB2Waves < T) {  // uniform within the wave
+    // rounds in pairs, as in gemv2_kernel (the last pair or round after the loop)
+    while (u + 2 * kB2Waves < T) {  // uniform within the wave
         #pragma unroll
         for (int r = 0; r < R; ++r)
             b2m_load<GS, FMT>(cp[1][r], sp[1][r], pr, sr, vo_code[r], vo_scale[r], u + kB2Waves);
@@ -1832,18 +1840,29 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
         b2m_wait_round<R>();  // round u's codes, scales and activations have landed
         B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
-        const int un = u + 2 * kB2Waves < T ? u + 2 * kB2Waves : T - 1;
         #pragma unroll
         for (int r = 0; r < R; ++r)
-            b2m_load<GS, FMT>(cp[0][r], sp[0][r], pr, sr, vo_code[r], vo_scale[r], un);
-        b2m_stage_x(xw0, xr, un, xo_ld);
+            b2m_load<GS, FMT>(cp[0][r], sp[0][r], pr, sr, vo_code[r], vo_scale[r],
+                              u + 2 * kB2Waves);
+        b2m_stage_x(xw0, xr, u + 2 * kB2Waves, xo_ld);
         b2m_wait_round<R>();
         B2mRound<DT, GS, FMT, R>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
         lds_wait_all();
         u += 2 * kB2Waves;
     }
-    vm_wait_all();  // the last round's loads (or a spare re-fetch) have landed
-    if (u < T) B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+    if (u + kB2Waves < T) {  // a last pair
+        #pragma unroll
+        for (int r = 0; r < R; ++r)
+            b2m_load<GS, FMT>(cp[1][r], sp[1][r], pr, sr, vo_code[r], vo_scale[r], u + kB2Waves);
+        b2m_stage_x(xw1, xr, u + kB2Waves, xo_ld);
+        b2m_wait_round<R>();
+        B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+        vm_wait_all();
+        B2mRound<DT, GS, FMT, R>::run(cp[1], sp[1], lut, slot, xs1, xo, acc);
+    } else if (u < T) {  // a last round
+        vm_wait_all();
+        B2mRound<DT, GS, FMT, R>::run(cp[0], sp[0], lut, slot, xs0, xo, acc);
+    }
 
     // add the waves' partial sums (each wave's in its own, no longer read, part of buffer 0);
     // lane (g, n) holds rows m = 4g + q of column n
@@ -2025,18 +2044,31 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
     const char* lut = reinterpret_cast<const char*>(lut_storage) +
                       (FMT == kFmtTernary ? kLutBaseOffset : 0u);
     for (int i0 = 0; i0 < nr; i0 += 4) {  // uniform within the wave
-        [&]<int... J>(std::integer_sequence<int, J...>) {
-            (([&] {
-                 vm_wait_le<3 * L>();  // slot J's round has landed; the other three may fly
-                 if (i0 + J < nr)
-                     B2mRound<DT, GS, FMT, R>::run(cp[J], sp[J], lut, slot, xsb[J], xo, acc);
-                 lds_wait_all();  // this wave's reads of slot J's buffer are done
-                 issue(std::integral_constant<int, J>{}, i0 + 4 + J);
-             })(),
-             ...);
-        }(std::make_integer_sequence<int, 4>{});
+        if (i0 + 4 < nr) {
+            [&]<int... J>(std::integer_sequence<int, J...>) {
+                (([&] {
+                     vm_wait_le<3 * L>();  // slot J's round has landed; the other three may fly
+                     if (i0 + J < nr)
+                         B2mRound<DT, GS, FMT, R>::run(cp[J], sp[J], lut, slot, xsb[J], xo, acc);
+                     lds_wait_all();  // this wave's reads of slot J's buffer are done
+                     issue(std::integral_constant<int, J>{}, i0 + 4 + J);
+                 })(),
+                 ...);
+            }(std::make_integer_sequence<int, 4>{});
+        } else {
+            // the last four slots: no refills (a spare load past the buffers' ends still
+            // takes a memory round trip to return, which the wave's end would wait for)
+            [&]<int... J>(std::integer_sequence<int, J...>) {
+                (([&] {
+                     vm_wait_le<(3 - J) * L>();
+                     if (i0 + J < nr)
+                         B2mRound<DT, GS, FMT, R>::run(cp[J], sp[J], lut, slot, xsb[J], xo, acc);
+                 })(),
+                 ...);
+            }(std::make_integer_sequence<int, 4>{});
+        }
     }
-    vm_wait_all();  // the spare slots' loads
+    vm_wait_all();  // every load has landed (the last pass waited for them all)
 
     // add the waves' partial sums (each wave's in its own part of buffer 0); lane (g, n)
     // holds rows m = 4g + q of column n
