@@ -2103,6 +2103,163 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
 }
 
 
+// ---- the B-operand GEMV at 4 < M <= 16 for K <= 4096: activations resident, every load issued first
+//
+// gemv2m_kernel stages each wave's 16 activation rows per 256-k round (8 KB of LDS per round
+// for 1 KB of a tile's weights), so LDS limits it to two rounds in flight per wave and a
+// per-linear launch pays several memory round trips.  Here a workgroup of 8 waves stages
+// all 16 x K activations once (at most 128 KB: one workgroup per CU) for its TPW row tiles,
+// and each wave requests the codes and scales of all of its rounds (u = w, w + 8: K is split
+// over the 8 waves) for all TPW tiles into registers at its first instructions; the tiles
+// share each A fragment read.  Rounds past K load past the buffers' ends (zeros, no memory
+// traffic) and are not computed.  The activation stage is block b (round b, 8 KB) at 8 KB b
+// in gemv2m_kernel's layout; wave w stages blocks w and w + 8; an explicit wait for those
+// loads (the weights may still be in flight) and a plain barrier make them visible to
+// every wave.  The 8 waves' partial sums of each tile meet in LDS.
+constexpr int kB2xWaves = 8;
+constexpr int kB2xMaxK = 4096;
+
+template <int SLOTS>
+__device__ __forceinline__ uint4 lut_item(int i, int kind);
+
+__device__ __forceinline__ void b2x_stage_block(char* xb, __amdgpu_buffer_rsrc_t x,
+                                                const uint32_t (&xo)[8], int so) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x, lds_ptr(xb + 1024 * q), 16, xo[q], so, 0, 0);
+}
+
+template <int DT, int GS, int FMT, int TPW>
+__global__ __launch_bounds__(64 * kB2xWaves) void gemv2x_kernel(GemvLaunch args) {
+    int64_t wg = blockIdx.x;
+    const GemvJob job = gemv_job_of(args, wg);
+    const void* const x = job.x ? job.x : args.x;
+    void* const y = job.y ? job.y : args.y;
+    const int M = args.M;
+    const int64_t N = job.N, K = job.K;
+    const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
+                      job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
+    static_assert(TPW == 1 || TPW == 2 || TPW == 4, "row tiles per workgroup");
+    // formats whose decode table is computed, not read from memory (a load there would make
+    // the table writes wait for every load issued before it)
+    static_assert(FMT == kFmtTernary || FMT == kFmt2Bit, "ternary or 2-bit codes");
+    constexpr int kBlocks = kB2xMaxK / kB2mRound;  // 16 rounds of 256 k
+    constexpr int NR = kBlocks / kB2xWaves;       // rounds per wave
+    constexpr int L = 2 * TPW;                    // loads per round: codes and scales per tile
+    static_assert(NR * L < 64, "wait count range");
+    __shared__ uint4 lut_storage[FMT == kFmtTernary ? kLutValidStorageU4 : kB2LutU4];
+    __shared__ __attribute__((aligned(128))) char xs[kBlocks * kB2mXBytes];
+    static_assert(kB2xWaves * TPW * 64 * 16 <= kBlocks * kB2mXBytes, "partial sums fit");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const int T = (int)(K / kB2mRound);
+    const uint32_t rowbytes = (uint32_t)(FMT == kFmtTernary ? K * 3 / 16 : K / 4);
+    constexpr uint32_t kLaneBytes = FMT == kFmtTernary ? 12u : 16u;
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+
+    // this wave's activation blocks first (every block is read by every wave of a round)
+    uint32_t xo_ld[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xo_ld[q] = b2m_x_offset(q, lane, M, K);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int b = wave + kB2xWaves * i;
+        uint32_t xo_b[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xo_b[q] = b < T ? xo_ld[q] : kB2sOob;
+        b2x_stage_block(xs + b * kB2mXBytes, xr, xo_b,
+                        b < T ? uniform_offset((int64_t)b * kB2mRound * 2) : 0);
+    }
+    // then the codes and scales of its rounds of every tile (rows past N read zeros)
+    uint32_t vo_code[TPW], vo_scale[TPW];
+#pragma unroll
+    for (int r = 0; r < TPW; ++r) {
+        const uint32_t row = (uint32_t)((wg * TPW + r) * 16 + i16);
+        vo_code[r] = row * rowbytes + kLaneBytes * g;
+        vo_scale[r] = row * srowbytes + (128u / GS) * g;
+    }
+    uint4 cp[NR][TPW], sp[NR][TPW];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int u = wave + kB2xWaves * i;
+#pragma unroll
+        for (int r = 0; r < TPW; ++r)
+            b2s_load<GS, FMT>(cp[i][r], sp[i][r], pr, sr, vo_code[r], vo_scale[r], u, u < T);
+    }
+
+    // decode table (computed) while the loads fly
+    if constexpr (FMT == kFmtTernary) {
+        for (int i = (int)threadIdx.x; i < kLutValidStorageU4; i += 64 * kB2xWaves)
+            lut_storage[i] = lut_item<kLutSlots>(i, kLutMasks);
+    } else {
+        fill_b2sel<64 * kB2xWaves>(lut_storage);
+    }
+    // this wave's activation blocks have landed when at most its weight loads fly; the
+    // plain barrier (no fence) leaves those in flight
+    vm_wait_le<NR * L>();
+    lds_wait_all();
+    asm volatile("s_barrier" ::: "memory");
+
+    const char* lut = reinterpret_cast<const char*>(lut_storage) +
+                      (FMT == kFmtTernary ? kLutBaseOffset : 0u);
+    const uint32_t slot = FMT == kFmtTernary ? (uint32_t)(lane & (kLutSlots - 1)) * 8u
+                                             : (uint32_t)(lane & 31) * 4u;
+    const uint32_t gu = (uint32_t)g, iu = (uint32_t)i16;
+    const uint32_t xo =
+        512u * iu + 16u * ((8u * gu & 16u) | ((8u * gu & 8u) ^ (iu & 8u)) | (iu & 7u));
+    f32x4 acc[TPW];
+#pragma unroll
+    for (int r = 0; r < TPW; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+             vm_wait_le<L * (NR - 1 - I)>();  // round I's code and scale loads have landed
+             const int u = wave + kB2xWaves * I;
+             if (u < T)
+                 B2mRound<DT, GS, FMT, TPW>::run(cp[I], sp[I], lut, slot, xs + u * kB2mXBytes,
+                                                 xo, acc);
+         })(),
+         ...);
+    }(std::make_integer_sequence<int, NR>{});
+
+    // every wave's partial sums of every tile through the (no longer read) stage; wave r <
+    // TPW adds tile r's; lane (g, n) holds rows m = 4g + q of column n
+    f32x4* const red = reinterpret_cast<f32x4*>(xs);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < TPW; ++r) red[(wave * TPW + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    if (wave >= TPW) return;
+    f32x4 o = red[wave * 64 + lane];
+#pragma unroll
+    for (int w2 = 1; w2 < kB2xWaves; ++w2) {
+        const f32x4 p = red[(w2 * TPW + wave) * 64 + lane];
+        o[0] += p[0];
+        o[1] += p[1];
+        o[2] += p[2];
+        o[3] += p[3];
+    }
+    const int64_t row = (wg * TPW + wave) * 16 + i16;
+    if (row < N) {
+        const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = 4 * g + q;
+            if (m < M)
+                store_from_f32<DT>(y, (int64_t)m * job.y_ld + job.y_col + row,
+                                   o[q] + bv + lora_term<DT>(lora, m, row));
+        }
+    }
+}
+
+
 // ------------------------------------------------------------------------- staged-tile GEMV
 //
 // Decode GEMV (M <= 4) for launches with few row tiles: the per-linear launches of a
@@ -2902,9 +3059,27 @@ static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const ui
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
                                   hipStream_t stream, const LoraEp& lora) {
     const int64_t tiles = (N + 15) / 16;
+    const GemvLaunch a = one_job(x, packed, scales, bias, y, M, N, K, lora);
+    if constexpr (FMT != kFmtRoot) {
+        if (M > kB2sRows && K <= kB2xMaxK) {
+            // activations resident (one workgroup per CU): up to four tiles per workgroup,
+            // so that the grid stays within one workgroup per CU where it can
+            const int tpw = tiles > 512 ? 4 : tiles > 256 ? 2 : 1;
+            const int64_t wgs = (tiles + tpw - 1) / tpw;
+            if (tpw == 4)
+                hipLaunchKernelGGL((gemv2x_kernel<DT, GS, FMT, 4>), dim3((unsigned)wgs),
+                                   dim3(64 * kB2xWaves), 0, stream, a);
+            else if (tpw == 2)
+                hipLaunchKernelGGL((gemv2x_kernel<DT, GS, FMT, 2>), dim3((unsigned)wgs),
+                                   dim3(64 * kB2xWaves), 0, stream, a);
+            else
+                hipLaunchKernelGGL((gemv2x_kernel<DT, GS, FMT, 1>), dim3((unsigned)wgs),
+                                   dim3(64 * kB2xWaves), 0, stream, a);
+            return hipGetLastError();
+        }
+    }
     const int R = tiles >= kB2mTwoTilesFrom ? 2 : 1;
-    return launch_gemv2m_grid<DT, GS, FMT>(one_job(x, packed, scales, bias, y, M, N, K, lora),
-                                           (tiles + R - 1) / R, R, stream);
+    return launch_gemv2m_grid<DT, GS, FMT>(a, (tiles + R - 1) / R, R, stream);
 }
 
 template <int DT, int FMT>
