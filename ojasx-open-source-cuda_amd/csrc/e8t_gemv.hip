@@ -2596,7 +2596,9 @@ __device__ __forceinline__ float wave_sum_scatter(const float (&v)[V], int lane)
 // RT: row tiles per wave (they share the activation stage and the A fragment reads); a
 // workgroup covers TPW * RT row tiles.
 // TW: waves per row tile (the tile's K / 1024 rounds are spread over them, U each).
-template <int DT, int MM, int U, int TPW, int RT, int TW, int GS>
+// LI: the launch forms LoRA u inside (args.lora_inline); a separate instantiation, since its
+// adapter loads are issued on every wave of the launch.
+template <int DT, int MM, int U, int TPW, int RT, int TW, int GS, bool LI = false>
 __global__ __launch_bounds__(64 * TW * TPW)
 __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(GemvLaunch args) {
     using S = TileStage<MM, RT, GS>;
@@ -2612,7 +2614,7 @@ __attribute__((amdgpu_waves_per_eu(RT == 2 ? 2 : 1))) void gemv_tile_kernel(Gemv
     // in-launch LoRA down-projection (the instantiation with one round per wave of 4, one
     // tile per wave and workgroup; elsewhere the extra registers would cost occupancy):
     // each wave's total of x @ A over its round
-    constexpr bool kLoraIn = U == 1 && RT == 1 && TPW == 1 && TW == kTileWaves;
+    constexpr bool kLoraIn = LI && U == 1 && RT == 1 && TPW == 1 && TW == kTileWaves;
     __shared__ float lora_tot[kLoraIn ? TW : 1][MM * kLoraInlineRank];
 
     int64_t wg = blockIdx.x;
@@ -3196,6 +3198,13 @@ GemvPlan gemv_pick_grouped(int64_t total_tiles, int64_t M, int64_t kmax, bool ti
 // `wgs` workgroups of TPW * RT row tiles each (each job's tiles start a new workgroup)
 template <int DT, int GS, int MM, int U, int TPW, int RT, int TW = kTileWaves>
 static hipError_t launch_tile_grid(const GemvLaunch& a, int64_t wgs, hipStream_t s) {
+    if constexpr (U == 1 && TPW == 1 && RT == 1 && TW == kTileWaves) {
+        if (a.lora_inline) {
+            hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT, TW, GS, true>),
+                               dim3((unsigned)wgs), dim3(64 * TW * TPW), 0, s, a);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((gemv_tile_kernel<DT, MM, U, TPW, RT, TW, GS>), dim3((unsigned)wgs),
                        dim3(64 * TW * TPW), 0, s, a);
     return hipGetLastError();
