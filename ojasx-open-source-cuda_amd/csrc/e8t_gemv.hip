@@ -3460,13 +3460,16 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
 // Streaming 2-bit kernel geometry of a grouped launch: waves per workgroup and row tiles per
 // wave; M <= 4 needs every K a multiple of 1024 (post-scaled rounds), otherwise the 16-row
 // B-operand rounds take it.
+// Measured (32-layer stack, same box): post-scaled 4 waves x 2 tiles (8 x 1 equal, 8 x 2
+// 0.536 -> 0.646 ms at M = 1); B operand 8 waves x 2 tiles (0.674 -> 0.659 ms at M = 16).
 constexpr int kB2gWaves = 4;
+constexpr int kB2gWavesB = 8;
 constexpr int kB2gTiles = 2;
 Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024) {
     (void)total_tiles;
     Gemv2Plan p{};
     p.post = M <= 4 && k1024;
-    p.R = kB2gWaves * kB2gTiles;  // row tiles per workgroup
+    p.R = (p.post ? kB2gWaves : kB2gWavesB) * kB2gTiles;  // row tiles per workgroup
     return p;
 }
 int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p) { return ((N + 15) / 16 + p.R - 1) / p.R; }
@@ -3482,8 +3485,8 @@ static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p
             hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 4, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
                                dim3(64 * kB2gWaves), 0, s, a);
     } else {
-        hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
-                           dim3(64 * kB2gWaves), 0, s, a);
+        hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB>), dim3((unsigned)wgs),
+                           dim3(64 * kB2gWavesB), 0, s, a);
     }
     return hipGetLastError();
 }
