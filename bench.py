@@ -865,11 +865,12 @@ def bench_e8b_grouped(torch, dev, layers: int, steps: int, warmup: int, Ms=(1, 4
                 per_M=per_m, max_rel_err=worst)
 
 
-def bench_ternary_gs(torch, N_, dev, layers: int, steps: int, gs_list=(32, 64), Ms=(1, 4, 16),
-                     prefill_m: int = 2048) -> dict:
+def bench_ternary_gs(torch, N_, dev, layers: int, steps: int, gs_list=(32, 16, 64),
+                     Ms=(1, 4, 16), prefill_m: int = 2048) -> dict:
     """Ternary E8 at the reference's other group sizes: one `layers`-layer Llama-3-8B-shaped
     stack of fp32 N(0, 0.02) weights (seed 9900 + 7*layer + j) encoded at each group size
-    in `gs_list` (the reference's published decoder run uses ternary group 64,
+    in `gs_list` (E8LatticeLinear's default group size 8 becomes 16 at bitrate 1.5,
+    lattice.py:752, 793; the reference's published decoder run uses ternary group 64,
     reports/apple_m5_1b_to_27b_gpu_benchmark.json:23-24), timed as per-linear
     ojx_e8t_gemm_fwd launches replayed from a hipGraph at the decode M, the prefill forward
     and the backward dX at M = `prefill_m`; outputs of layer 0's q, gate and down checked
