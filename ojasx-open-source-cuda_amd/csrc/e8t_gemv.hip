@@ -2260,6 +2260,141 @@ __global__ __launch_bounds__(64 * kB2xWaves) void gemv2x_kernel(GemvLaunch args)
 }
 
 
+// ---- the same for 4096 < K <= 16384 (down): weights prefetched, activations double-buffered per wave
+//
+// One row tile per workgroup of 8 waves; wave w takes the 256-k rounds u = w + 8 i, i < 8,
+// requests the codes and scales of all of them into registers at its first instructions
+// (rounds past K load past the buffers' ends: zeros, no traffic, issued with the others so
+// that they add no round trip at the end), and stages the activations of its own rounds two
+// ahead in its own two 8 KB buffers (the 16 activation rows come from L2), so that no wave
+// reads another's stage and only the decode table needs a barrier.
+constexpr int kB2xkRounds = 8;  // rounds per wave: K <= 8 * 8 * 256
+
+template <int DT, int GS, int FMT>
+__global__ __launch_bounds__(64 * kB2xWaves) void gemv2xk_kernel(GemvLaunch args) {
+    int64_t wg = blockIdx.x;
+    const GemvJob job = gemv_job_of(args, wg);
+    const void* const x = job.x ? job.x : args.x;
+    void* const y = job.y ? job.y : args.y;
+    const int M = args.M;
+    const int64_t N = job.N, K = job.K;
+    const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
+                      job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
+    static_assert(FMT == kFmtTernary || FMT == kFmt2Bit, "ternary or 2-bit codes");
+    constexpr int NR = kB2xkRounds;
+    __shared__ uint4 lut_storage[FMT == kFmtTernary ? kLutValidStorageU4 : kB2LutU4];
+    __shared__ __attribute__((aligned(128))) char xs0[kB2xWaves * kB2mXBytes];
+    __shared__ __attribute__((aligned(128))) char xs1[kB2xWaves * kB2mXBytes];
+    static_assert(kB2xWaves * 64 * 16 <= kB2xWaves * kB2mXBytes, "partial sums fit");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i16 = lane & 15;
+    const int T = (int)(K / kB2mRound);
+    const int nr = wave < T ? (T - 1 - wave) / kB2xWaves + 1 : 0;  // this wave's rounds
+    const uint32_t rowbytes = (uint32_t)(FMT == kFmtTernary ? K * 3 / 16 : K / 4);
+    constexpr uint32_t kLaneBytes = FMT == kFmtTernary ? 12u : 16u;
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)job.scales, (short)0, (int)(N * srowbytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
+    uint32_t xo_ld[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xo_ld[q] = b2m_x_offset(q, lane, M, K);
+    char* const xw0 = xs0 + wave * kB2mXBytes;
+    char* const xw1 = xs1 + wave * kB2mXBytes;
+    auto stage = [&](char* xw, int i) {  // activations of this wave's round i
+        const int u = wave + kB2xWaves * i;
+        uint32_t xo_b[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xo_b[q] = i < nr ? xo_ld[q] : kB2sOob;
+        b2x_stage_block(xw, xr, xo_b, i < nr ? uniform_offset((int64_t)u * kB2mRound * 2) : 0);
+    };
+
+    // round 0's activations, every round's codes and scales, round 1's activations
+    stage(xw0, 0);
+    const uint32_t row = (uint32_t)(wg * 16 + i16);  // rows past N read zeros
+    const uint32_t vo_code = row * rowbytes + kLaneBytes * g;
+    const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
+    uint4 cp[NR], sp[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+        b2s_load<GS, FMT>(cp[i], sp[i], pr, sr, vo_code, vo_scale, wave + kB2xWaves * i, i < nr);
+    stage(xw1, 1);
+
+    if constexpr (FMT == kFmtTernary) {
+        for (int i = (int)threadIdx.x; i < kLutValidStorageU4; i += 64 * kB2xWaves)
+            lut_storage[i] = lut_item<kLutSlots>(i, kLutMasks);
+    } else {
+        fill_b2sel<64 * kB2xWaves>(lut_storage);
+    }
+    lds_wait_all();
+    asm volatile("s_barrier" ::: "memory");  // the table (the loads stay in flight)
+
+    const char* lut = reinterpret_cast<const char*>(lut_storage) +
+                      (FMT == kFmtTernary ? kLutBaseOffset : 0u);
+    const uint32_t slot = FMT == kFmtTernary ? (uint32_t)(lane & (kLutSlots - 1)) * 8u
+                                             : (uint32_t)(lane & 31) * 4u;
+    const uint32_t gu = (uint32_t)g, iu = (uint32_t)i16;
+    const uint32_t xo =
+        512u * iu + 16u * ((8u * gu & 16u) | ((8u * gu & 8u) ^ (iu & 8u)) | (iu & 7u));
+    f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+    // round i: its activations have landed when at most the next round's (and, for round 0,
+    // the weights') loads fly (none past the wave's last round); then its buffer takes round
+    // i + 2 if there is one
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+             if (I < nr) {  // uniform
+                 if constexpr (I == 0) vm_wait_le<2 * NR + 8>();
+                 else if (I + 1 < nr) vm_wait_le<8>();
+                 else vm_wait_all();
+                 char* const xw = (I % 2) ? xw1 : xw0;
+                 B2mRound<DT, GS, FMT, 1>::run(reinterpret_cast<const uint4(&)[1]>(cp[I]),
+                                               reinterpret_cast<const uint4(&)[1]>(sp[I]), lut,
+                                               slot, xw, xo, acc);
+                 if constexpr (I + 2 < NR) {
+                     if (I + 2 < nr) {
+                         lds_wait_all();  // this wave's reads of the buffer are done
+                         stage(xw, I + 2);
+                     }
+                 }
+             }
+         })(),
+         ...);
+    }(std::make_integer_sequence<int, NR>{});
+
+    // the 8 waves' partial sums through the (no longer read) stage; lane (g, n) holds rows
+    // m = 4g + q of column n
+    f32x4* const red = reinterpret_cast<f32x4*>(xs0);
+    __syncthreads();
+    red[wave * 64 + lane] = acc[0];
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4 o = acc[0];
+#pragma unroll
+    for (int w2 = 1; w2 < kB2xWaves; ++w2) {
+        const f32x4 p = red[w2 * 64 + lane];
+        o[0] += p[0];
+        o[1] += p[1];
+        o[2] += p[2];
+        o[3] += p[3];
+    }
+    if ((int64_t)row < N) {
+        const float bv = job.bias ? load_as_f32<DT>(job.bias, row) : 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = 4 * g + q;
+            if (m < M)
+                store_from_f32<DT>(y, (int64_t)m * job.y_ld + job.y_col + row,
+                                   o[q] + bv + lora_term<DT>(lora, m, row));
+        }
+    }
+}
+
+
 // ------------------------------------------------------------------------- staged-tile GEMV
 //
 // Decode GEMV (M <= 4) for launches with few row tiles: the per-linear launches of a
@@ -3077,6 +3212,13 @@ static hipError_t launch_gemv2m_t(const void* x, const uint8_t* packed, const ui
             else
                 hipLaunchKernelGGL((gemv2x_kernel<DT, GS, FMT, 1>), dim3((unsigned)wgs),
                                    dim3(64 * kB2xWaves), 0, stream, a);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (FMT != kFmtRoot) {
+        if (M > kB2sRows && K <= kB2xWaves * kB2xkRounds * kB2mRound) {
+            hipLaunchKernelGGL((gemv2xk_kernel<DT, GS, FMT>), dim3((unsigned)tiles),
+                               dim3(64 * kB2xWaves), 0, stream, a);
             return hipGetLastError();
         }
     }
