@@ -309,3 +309,23 @@ def test_grouped_mid_size_launch_one_tile_per_wave(M):
                          O.DT_BF16)
         assert _rel(y[:, col:col + l.out_features], ref) <= REL_TOL
         col += l.out_features
+
+
+@pytest.mark.parametrize("M", [5, 12, 16])
+@pytest.mark.parametrize("N,K", [(100, 1280), (16 * 300 + 5, 2304), (16 * 600 + 9, 1280),
+                                 (100, 4352), (16 * 40 + 3, 6400), (48, 16384)])
+def test_per_linear_b_operand_resident_and_prefetched(M, N, K):
+    # per-linear 4 < M <= 16 launches below 1024 row tiles: K <= 4096 stages the activations
+    # once per workgroup (1, 2 or 4 row tiles per workgroup by the tile count; rounds past K
+    # on some waves), 4096 < K <= 16384 prefetches every round's weights (waves with one
+    # round more than others at K = 4352; all eight rounds per wave at K = 16384); ragged N
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=N + 3 * K + M)
+    x = _x(M, K, seed=5 * M + K, dtype=torch.bfloat16)
+    bias = _x(1, N, seed=N + 1, dtype=torch.bfloat16).reshape(N)
+    print(f"b-operand per-linear M={M} N={N} K={K}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+    for m in range(M):
+        assert _rel(y[m:m + 1], ref[m:m + 1]) <= REL_TOL, m
