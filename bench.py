@@ -129,7 +129,7 @@ def parse_args():
                     help="seconds of each leg's own launches run untimed right before its "
                          "timed region, after the warm-up steps (0: none)")
     ap.add_argument("--e8b-grouped-layers", type=int, default=32,
-                    help="layers of the grouped 2-bit decode leg (0: skip)")
+                    help="layers of the grouped 2-bit and 1-bit decode legs (0: skip)")
     ap.add_argument("--gs-layers", type=int, default=8,
                     help="layers of the ternary group-size leg (group 32 against 64; 0: skip)")
     ap.add_argument("--launch-probe", action="store_true",
@@ -805,21 +805,24 @@ class E8Decoder:
 
 
 def bench_e8b_grouped(torch, dev, layers: int, steps: int, warmup: int, Ms=(1, 4, 16),
-                      gs: int = 32) -> dict:
-    """2-bit E8 (the reference's default bitrate, lattice.py:735, 906) decode over a
-    `layers`-layer Llama-3-8B-shaped stack of fp16 N(0, 0.02) weights (seed 9700 + 7*layer + j,
-    group size `gs`): one grouped launch (ojx_e8_gemv_grouped, device job table) per M over
-    every linear, timed with HIP events as the ternary headline; outputs of layer 0's q, gate
-    and down checked against an fp32 matmul of the decoded weights."""
+                      gs: int = 32, bitrate: float = 2.0) -> dict:
+    """2-bit E8 (the reference's default bitrate, lattice.py:735, 906) or, with bitrate 1.0,
+    1-bit Root E8 (lattice.py:426-533) decode over a `layers`-layer Llama-3-8B-shaped stack of
+    fp16 N(0, 0.02) weights (seed 9700 + 7*layer + j, group size `gs`): one grouped launch
+    (ojx_e8_gemv_grouped / ojx_e8r_gemv_grouped, device job table) per M over every linear,
+    timed with HIP events as the ternary headline; outputs of layer 0's q, gate and down
+    checked against an fp32 matmul of the decoded weights."""
     from ojasx_amd import ops
     from ojasx_amd.grouped import GroupedGemv, stack_jobs
 
+    encode = ops.encode2 if bitrate == 2.0 else ops.encode1
+    decode = ops.decode2 if bitrate == 2.0 else ops.decode1
     stack = []
     for layer in range(layers):
         for j, (name, N, K) in enumerate(LAYER_SHAPES):
             g = torch.Generator(device=dev).manual_seed(9700 + 7 * layer + j)
             w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
-            packed, scales = ops.encode2(w, gs)
+            packed, scales = encode(w, gs)
             del w
             stack.append(dict(name=name, N=N, K=K, packed=packed, scales=scales))
     torch.cuda.synchronize()
@@ -831,7 +834,7 @@ def bench_e8b_grouped(torch, dev, layers: int, steps: int, warmup: int, Ms=(1, 4
         yl = [torch.empty(M, s["N"], dtype=torch.bfloat16, device=dev) for s in stack]
         xs[M], ys[M] = xk, yl
         plans[M] = GroupedGemv(stack_jobs(stack, xk, yl), M, torch.bfloat16, dev,
-                               keep=list(xk.values()) + yl, bitrate=2.0, group_size=gs)
+                               keep=list(xk.values()) + yl, bitrate=bitrate, group_size=gs)
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         for M in Ms:
@@ -855,8 +858,8 @@ def bench_e8b_grouped(torch, dev, layers: int, steps: int, warmup: int, Ms=(1, 4
                              grid=plans[M].grid)
         for idx in (0, 4, 6):
             s = stack[idx]
-            wd = ops.decode2(s["packed"], s["scales"], s["N"] * s["K"], gs,
-                             torch.bfloat16).view(s["N"], s["K"]).float()
+            wd = decode(s["packed"], s["scales"], s["N"] * s["K"], gs,
+                        torch.bfloat16).view(s["N"], s["K"]).float()
             ref = xs[M][s["K"]].float() @ wd.t()
             err = (ys[M][idx].float() - ref).abs().max().item() / max(ref.abs().max().item(),
                                                                       1e-30)
@@ -1341,9 +1344,14 @@ def main() -> int:
         result["e8_2bit_grouped"] = bench_e8b_grouped(torch, dev, args.e8b_grouped_layers,
                                                       args.steps, args.warmup)
         log(f"2-bit grouped: {result['e8_2bit_grouped']['per_M']}")
+        torch.cuda.empty_cache()
+        log(f"1-bit Root E8 grouped decode ({args.e8b_grouped_layers}-layer stack)")
+        result["e8_1bit_grouped"] = bench_e8b_grouped(torch, dev, args.e8b_grouped_layers,
+                                                      args.steps, args.warmup, bitrate=1.0)
+        log(f"1-bit grouped: {result['e8_1bit_grouped']['per_M']}")
     if args.gs_layers > 0:
         torch.cuda.empty_cache()
-        log(f"ternary group sizes 32 / 64 ({args.gs_layers}-layer stack)")
+        log(f"ternary group sizes 32 / 16 / 64 ({args.gs_layers}-layer stack)")
         result["ternary_gs"] = bench_ternary_gs(torch, N_, dev, args.gs_layers, args.steps)
     if not args.no_e2e:
         torch.cuda.empty_cache()

@@ -321,6 +321,16 @@ int ojx_e8_gemv_grouped(const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jo
                         int njobs, const void* x, void* y, int64_t M, int64_t gs, int dtype,
                         void* stream);
 
+/* The same for 1-bit Root E8 linears (RootE8LatticePacker, lattice.py:426-533): `packed` is
+ * [N * K / 8] bytes (one 8-bit code per 8 weights), `scales` [N * K / gs] fp16, gs 8, 16, 32
+ * or 64; the B-operand kernel at every M.  No counterpart in the reference (its 1-bit
+ * forward unpacks each linear, lattice.py:610-640). */
+int ojx_e8r_gemv_grouped_plan(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs,
+                              int dtype, int64_t* grid);
+int ojx_e8r_gemv_grouped(const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev,
+                         int njobs, const void* x, void* y, int64_t M, int64_t gs, int dtype,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -487,20 +487,22 @@ __attribute__((visibility("default"))) int ojx_e8t_gemv_grouped(
                 "e8t grouped gemv launch");
 }
 
-// ------------------------------------------------------------------ grouped 2-bit GEMV
+// ------------------------------------------------------------------ grouped 2-bit / 1-bit GEMV
 
-// Validates a 2-bit job table for batch M and group size gs, picks the plan and (fill) sets
-// each job's first workgroup and default y_ld, or (!fill) checks that they were so set.
+// Validates a 2-bit (fmt kFmt2Bit) or 1-bit (kFmtRoot) job table for batch M and group size
+// gs, picks the plan and (fill) sets each job's first workgroup and default y_ld, or (!fill)
+// checks that they were so set.
 static int plan_jobs2(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs, int dtype,
-                      int64_t* grid, ojx::Gemv2Plan* plan, bool fill) {
+                      int64_t* grid, ojx::Gemv2Plan* plan, bool fill, int fmt) {
+    const int64_t cdiv = fmt == ojx::kFmtRoot ? 8 : 4;  // weights per code byte
     if (njobs <= 0 || !jobs) return fail(OJX_EINVAL, "empty job list");
     if (dtype != OJX_BF16 && dtype != OJX_F16)
         return fail(OJX_EDTYPE, "grouped GEMV takes F16 or BF16 activations (got %d)", dtype);
     if (M < 1 || M > 16) return fail(OJX_ELAYOUT, "grouped GEMV needs 1 <= M <= 16 (got %lld)",
                                      (long long)M);
     if (gs != 8 && gs != 16 && gs != 32 && gs != 64)
-        return fail(OJX_ELAYOUT, "grouped 2-bit GEMV needs group size 8, 16, 32 or 64 (got %lld)",
-                    (long long)gs);
+        return fail(OJX_ELAYOUT, "grouped %s GEMV needs group size 8, 16, 32 or 64 (got %lld)",
+                    fmt == ojx::kFmtRoot ? "1-bit" : "2-bit", (long long)gs);
     int64_t tiles = 0;
     bool k1024 = true;
     for (int i = 0; i < njobs; ++i) {
@@ -508,7 +510,7 @@ static int plan_jobs2(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs, 
         if (j.N < 1 || j.K < 256 || j.K % 256 != 0)
             return fail(OJX_ELAYOUT, "job %d: needs N >= 1 and K %% 256 == 0 (N=%lld K=%lld)", i,
                         (long long)j.N, (long long)j.K);
-        if ((j.N + 32) * (j.K / 4) >= (1ll << 31) || (j.N + 32) * (j.K * 2 / gs) >= (1ll << 31) ||
+        if ((j.N + 32) * (j.K / cdiv) >= (1ll << 31) || (j.N + 32) * (j.K * 2 / gs) >= (1ll << 31) ||
             M * j.K * 2 >= (1ll << 31))
             return fail(OJX_ELAYOUT, "job %d: layer too large for 32-bit offsets", i);
         if (!j.packed || !j.scales) return fail(OJX_EINVAL, "job %d: null weight pointer", i);
@@ -529,7 +531,7 @@ static int plan_jobs2(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs, 
         k1024 = k1024 && j.K % 1024 == 0;
         tiles += (j.N + 15) / 16;
     }
-    *plan = ojx::gemv2_pick_grouped(tiles, M, k1024);
+    *plan = ojx::gemv2_pick_grouped(tiles, M, k1024, fmt);
     int64_t wg = 0;
     for (int i = 0; i < njobs; ++i) {
         if (fill) {
@@ -545,25 +547,23 @@ static int plan_jobs2(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs, 
     return OJX_OK;
 }
 
-__attribute__((visibility("default"))) int ojx_e8_gemv_grouped_plan(ojx_e8t_gemv_job* jobs,
-                                                                    int njobs, int64_t M,
-                                                                    int64_t gs, int dtype,
-                                                                    int64_t* grid) {
+static int gemv2_grouped_plan(ojx_e8t_gemv_job* jobs, int njobs, int64_t M, int64_t gs,
+                              int dtype, int64_t* grid, int fmt) {
     int64_t g = 0;
     ojx::Gemv2Plan plan{};
-    if (int r = plan_jobs2(jobs, njobs, M, gs, dtype, &g, &plan, true)) return r;
+    if (int r = plan_jobs2(jobs, njobs, M, gs, dtype, &g, &plan, true, fmt)) return r;
     if (grid) *grid = g;
     g_last_error[0] = '\0';
     return OJX_OK;
 }
 
-__attribute__((visibility("default"))) int ojx_e8_gemv_grouped(
-    const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev, int njobs, const void* x,
-    void* y, int64_t M, int64_t gs, int dtype, void* stream) {
+static int gemv2_grouped(const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev,
+                         int njobs, const void* x, void* y, int64_t M, int64_t gs, int dtype,
+                         void* stream, int fmt) {
     int64_t grid = 0;
     ojx::Gemv2Plan plan{};
     if (int r = plan_jobs2(const_cast<ojx_e8t_gemv_job*>(jobs), njobs, M, gs, dtype, &grid, &plan,
-                           false))
+                           false, fmt))
         return r;
     if (((uintptr_t)x & 15u) || ((uintptr_t)y & 1u))
         return fail(OJX_ELAYOUT, "misaligned default x / y");
@@ -584,8 +584,34 @@ __attribute__((visibility("default"))) int ojx_e8_gemv_grouped(
     a.njobs = njobs;
     a.M = (int)M;
     if (int r = lora_downs(jobs, njobs, x, M, dtype, stream)) return r;
-    return done(ojx::launch_gemv2_grouped(a, plan, grid, gs, dtype, (hipStream_t)stream),
-                "e8 grouped gemv launch");
+    return done(ojx::launch_gemv2_grouped(a, plan, grid, gs, dtype, fmt, (hipStream_t)stream),
+                fmt == ojx::kFmtRoot ? "e8r grouped gemv launch" : "e8 grouped gemv launch");
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemv_grouped_plan(ojx_e8t_gemv_job* jobs,
+                                                                    int njobs, int64_t M,
+                                                                    int64_t gs, int dtype,
+                                                                    int64_t* grid) {
+    return gemv2_grouped_plan(jobs, njobs, M, gs, dtype, grid, ojx::kFmt2Bit);
+}
+
+__attribute__((visibility("default"))) int ojx_e8_gemv_grouped(
+    const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev, int njobs, const void* x,
+    void* y, int64_t M, int64_t gs, int dtype, void* stream) {
+    return gemv2_grouped(jobs, jobs_dev, njobs, x, y, M, gs, dtype, stream, ojx::kFmt2Bit);
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemv_grouped_plan(ojx_e8t_gemv_job* jobs,
+                                                                     int njobs, int64_t M,
+                                                                     int64_t gs, int dtype,
+                                                                     int64_t* grid) {
+    return gemv2_grouped_plan(jobs, njobs, M, gs, dtype, grid, ojx::kFmtRoot);
+}
+
+__attribute__((visibility("default"))) int ojx_e8r_gemv_grouped(
+    const ojx_e8t_gemv_job* jobs, const ojx_e8t_gemv_job* jobs_dev, int njobs, const void* x,
+    void* y, int64_t M, int64_t gs, int dtype, void* stream) {
+    return gemv2_grouped(jobs, jobs_dev, njobs, x, y, M, gs, dtype, stream, ojx::kFmtRoot);
 }
 
 // ------------------------------------------------------------------ 2-bit E8

@@ -1571,11 +1571,13 @@ __device__ __forceinline__ uint4 b2m_operand(const uint4& cp, const uint2& val, 
 }
 
 // B operand (8 weights) of 1-bit code byte H of this lane's 8 code bytes: the code's four
-// selector words from the 256-entry table, applied to the group's value words.
-template <int H>
-__device__ __forceinline__ uint4 root_operand(const uint4& cp, const uint2& val, const char* tab) {
+// selector words from the 256-entry table (C copies, this lane's at byte `slot` of an
+// entry), applied to the group's value words.
+template <int H, int C = 1>
+__device__ __forceinline__ uint4 root_operand(const uint4& cp, const uint2& val, const char* tab,
+                                              uint32_t slot = 0) {
     const uint32_t byte = ((H < 4 ? cp.x : cp.y) >> (8 * (H % 4))) & 0xFFu;
-    const uint4 sel = *reinterpret_cast<const uint4*>(tab + 16u * byte);
+    const uint4 sel = *reinterpret_cast<const uint4*>(tab + 16u * C * byte + slot);
     return make_uint4(__builtin_amdgcn_perm(val.x, val.y, sel.x),
                       __builtin_amdgcn_perm(val.x, val.y, sel.y),
                       __builtin_amdgcn_perm(val.x, val.y, sel.z),
@@ -1613,7 +1615,8 @@ __device__ __forceinline__ uint2 values_of(uint32_t s16) {
 template <int FMT, int H, int BC = 0>
 __device__ __forceinline__ uint4 operand_of(const uint4& cp, const uint2& val, const char* lut,
                                             uint32_t slot) {
-    if constexpr (FMT == kFmtRoot) return root_operand<H>(cp, val, lut);
+    if constexpr (FMT == kFmtRoot)  // the single-copy table has no slot
+        return root_operand<H, (BC ? BC : 1)>(cp, val, lut, BC ? slot : 0u);
     else if constexpr (FMT == kFmt2Bit) return b2m_operand<H, BC>(cp, val, lut, slot);
     else return ternary_operand<H>(cp, val, lut, slot);
 }
@@ -3429,15 +3432,19 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
 // weights made the kernel VALU- and LDS-issue-bound: 17.2 VALU and 5.0 LDS instructions per
 // MFMA against 10.5 and 2.5, M = 4 stack 0.725 -> 0.605 ms, same box); MM = 16: the
 // B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).
-template <int DT, int GS, int MM, int R, int W>
+template <int DT, int GS, int MM, int R, int W, int FMT = kFmt2Bit>
 __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
+    // 1-bit Root E8 (FMT kFmtRoot): the B-operand form with its code -> selector table
+    static_assert(FMT == kFmt2Bit || (FMT == kFmtRoot && !kPost), "2-bit, or 1-bit at MM 16");
     static_assert(MM == 1 || MM == 4 || MM == 16, "activation rows 1, 4 or 16");
     constexpr int kXBytes = kPost ? MM * (int)kXRow : kB2mXBytes;  // one round's stage
     // the byte tables (16 copies; 32 copies, conflict-free, measured 2% slower at M = 1):
     // weights (post-scaled) or selector pairs (B operand)
-    constexpr int BC = 16;
-    __shared__ uint4 lut_storage[kB2ByteLutU4<BC>];
+    // table copies: 16 for the 2-bit byte tables (8-byte entries); one 4 KB 1-bit selector
+    // table (8 copies, 32 KB, conflict-free: 0.569 -> 0.585 ms at M = 1 over a 32-layer stack)
+    constexpr int BC = FMT == kFmtRoot ? 1 : 16;
+    __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries * BC : kB2ByteLutU4<16>];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
     // (the A fragments of lanes outside their lane group)
     __shared__ __attribute__((aligned(128))) char xs0[kXBytes + (kPost ? kB2ZeroBytes : 0)];
@@ -3450,7 +3457,8 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
             reinterpret_cast<uint4*>(xs1 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
         }
     } else {
-        fill_b2bsel<64 * W, BC>(lut_storage);
+        if constexpr (FMT == kFmtRoot) fill_sel1c<BC>(lut_storage, 64 * W);
+        else fill_b2bsel<64 * W, BC>(lut_storage);
     }
 
     int64_t wg = blockIdx.x;
@@ -3466,7 +3474,9 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
     const int64_t tile0 = (wg * W + wave) * R;
-    const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
+    const uint32_t rowbytes = (uint32_t)(FMT == kFmtRoot ? K / 8 : K / 4);
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS);
+    constexpr uint32_t kLaneBytes = FMT == kFmtRoot ? 8u : 16u;  // a lane's codes per round
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)job.packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
@@ -3478,10 +3488,10 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t row = (uint32_t)((tile0 + r) * 16 + i16);
-        vo_code[r] = row * rowbytes + 16u * g;
+        vo_code[r] = row * rowbytes + kLaneBytes * g;
         vo_scale[r] = row * srowbytes + (128u / GS) * g;
     }
-    const uint32_t slot = b2_slot<BC>(lane);
+    const uint32_t slot = FMT == kFmtRoot ? (uint32_t)(lane & (BC - 1)) * 16u : b2_slot<BC>(lane);
     const int T = (int)(K / (kPost ? kRound : kB2mRound));
 
     // this lane's activation reads: post-scaled A row i16 = 4 g' + m is live in lane group g'
@@ -3522,7 +3532,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if constexpr (kPost) b2_load<GS>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
-            else b2m_load<GS, kFmt2Bit>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
+            else b2m_load<GS, FMT>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
         }
     };
     float accp[R][kPost ? MM : 1];
@@ -3538,7 +3548,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
         if constexpr (kPost) {
             B2Round<DT, MM, GS, R, BC>::run(cp, sp, lut, slot, xs + aoff, accp);
         } else {
-            B2mRound<DT, GS, kFmt2Bit, R, BC>::run(cp, sp, lut, slot, xs, xo, accm);
+            B2mRound<DT, GS, FMT, R, BC>::run(cp, sp, lut, slot, xs, xo, accm);
         }
     };
 
@@ -3607,10 +3617,10 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
 constexpr int kB2gWaves = 4;
 constexpr int kB2gWavesB = 8;
 constexpr int kB2gTiles = 2;
-Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024) {
+Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024, int fmt) {
     (void)total_tiles;
     Gemv2Plan p{};
-    p.post = M <= 4 && k1024;
+    p.post = fmt == kFmt2Bit && M <= 4 && k1024;
     p.R = (p.post ? kB2gWaves : kB2gWavesB) * kB2gTiles;  // row tiles per workgroup
     return p;
 }
@@ -3618,8 +3628,11 @@ int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p) { return ((N + 15) / 16 + p
 
 template <int DT, int GS>
 static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
-                                         hipStream_t s) {
-    if (p.post) {
+                                         int fmt, hipStream_t s) {
+    if (fmt == kFmtRoot) {
+        hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB, kFmtRoot>),
+                           dim3((unsigned)wgs), dim3(64 * kB2gWavesB), 0, s, a);
+    } else if (p.post) {
         if (a.M == 1)
             hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 1, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
                                dim3(64 * kB2gWaves), 0, s, a);
@@ -3634,20 +3647,21 @@ static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p
 }
 template <int DT>
 static hipError_t launch_gemv2_grouped_dt(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
-                                          int64_t gs, hipStream_t s) {
+                                          int64_t gs, int fmt, hipStream_t s) {
     switch (gs) {
-        case 8: return launch_gemv2_grouped_t<DT, 8>(a, p, wgs, s);
-        case 16: return launch_gemv2_grouped_t<DT, 16>(a, p, wgs, s);
-        case 32: return launch_gemv2_grouped_t<DT, 32>(a, p, wgs, s);
-        case 64: return launch_gemv2_grouped_t<DT, 64>(a, p, wgs, s);
+        case 8: return launch_gemv2_grouped_t<DT, 8>(a, p, wgs, fmt, s);
+        case 16: return launch_gemv2_grouped_t<DT, 16>(a, p, wgs, fmt, s);
+        case 32: return launch_gemv2_grouped_t<DT, 32>(a, p, wgs, fmt, s);
+        case 64: return launch_gemv2_grouped_t<DT, 64>(a, p, wgs, fmt, s);
         default: return hipErrorInvalidValue;
     }
 }
 hipError_t launch_gemv2_grouped(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
-                                int64_t gs, int dt, hipStream_t s) {
+                                int64_t gs, int dt, int fmt, hipStream_t s) {
     if (wgs <= 0) return hipSuccess;
-    return dt == kBF16 ? launch_gemv2_grouped_dt<kBF16>(a, p, wgs, gs, s)
-                       : launch_gemv2_grouped_dt<kF16>(a, p, wgs, gs, s);
+    if (fmt != kFmt2Bit && fmt != kFmtRoot) return hipErrorInvalidValue;
+    return dt == kBF16 ? launch_gemv2_grouped_dt<kBF16>(a, p, wgs, gs, fmt, s)
+                       : launch_gemv2_grouped_dt<kF16>(a, p, wgs, gs, fmt, s);
 }
 
 }  // namespace ojx

@@ -109,17 +109,17 @@ struct GemvLaunch {
                                    // adapter form u from lora_a themselves (lora_u unused)
 };
 
-// Grouped 2-bit decode GEMV (streaming kernel): M <= 4 with every K a multiple of 1024
-// runs post-scaled 1024-k rounds, otherwise B-operand 256-k rounds; R row tiles per
-// workgroup.  Each job's tiles start a new workgroup.
+// Grouped 2-bit or 1-bit decode GEMV (streaming kernel, fmt kFmt2Bit / kFmtRoot): 2-bit at
+// M <= 4 with every K a multiple of 1024 runs post-scaled 1024-k rounds, otherwise B-operand
+// 256-k rounds; R row tiles per workgroup.  Each job's tiles start a new workgroup.
 struct Gemv2Plan {
     bool post;
     int R;
 };
-Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024);
+Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024, int fmt);
 int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p);
 hipError_t launch_gemv2_grouped(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
-                                int64_t gs, int dt, hipStream_t s);
+                                int64_t gs, int dt, int fmt, hipStream_t s);
 bool gemv_shape_ok(int64_t N, int64_t K);
 // Whether a staged-tile launch forms the adapters' u inside the launch: one round per wave
 // (U == 1), one row tile per wave and per workgroup (rt == tpw == 1), rank-8 adapters with

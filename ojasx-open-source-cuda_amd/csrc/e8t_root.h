@@ -304,6 +304,21 @@ __device__ __forceinline__ void fill_sel1(uint4* tab, int nthreads) {
     }
 }
 
+// The same table with C copies of each entry (entry stride 16 C bytes), lane l reading copy
+// l % C: with C = 8 the eight lanes a b128 read serves per cycle hit distinct banks.
+template <int C>
+__device__ __forceinline__ void fill_sel1c(uint4* tab, int nthreads) {
+    for (int i = (int)threadIdx.x; i < kSel1Entries * C; i += nthreads) {
+        const int e = i / C;
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            w[h] = root_sel_pair(kRootTable.c[e][2 * h]) |
+                   (root_sel_pair(kRootTable.c[e][2 * h + 1]) << 16);
+        tab[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 template <int DT>
 __device__ __forceinline__ uint2 values1(uint32_t s16) {
     const float s = scale_for<DT>(s16 & 0xFFFFu);

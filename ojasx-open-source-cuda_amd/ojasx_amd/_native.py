@@ -36,6 +36,8 @@ EXPORTS = (
     "ojx_e8t_gemv_grouped",
     "ojx_e8_gemv_grouped_plan",
     "ojx_e8_gemv_grouped",
+    "ojx_e8r_gemv_grouped_plan",
+    "ojx_e8r_gemv_grouped",
     "ojx_e8_encode",
     "ojx_e8_decode",
     "ojx_e8_gemm_fwd",
@@ -131,6 +133,10 @@ def lib() -> ctypes.CDLL:
             L.ojx_e8_gemv_grouped_plan.argtypes = [_P, _INT, _I64, _I64, _INT, _P]
             L.ojx_e8_gemv_grouped.restype = _INT
             L.ojx_e8_gemv_grouped.argtypes = [_P, _P, _INT, _P, _P, _I64, _I64, _INT, _P]
+            L.ojx_e8r_gemv_grouped_plan.restype = _INT
+            L.ojx_e8r_gemv_grouped_plan.argtypes = [_P, _INT, _I64, _I64, _INT, _P]
+            L.ojx_e8r_gemv_grouped.restype = _INT
+            L.ojx_e8r_gemv_grouped.argtypes = [_P, _P, _INT, _P, _P, _I64, _I64, _INT, _P]
             L.ojx_e8_encode.restype = _INT
             L.ojx_e8_encode.argtypes = [_P, _INT, _I64, _I64, _P, _P, _P]
             L.ojx_e8_decode.restype = _INT

@@ -25,8 +25,9 @@ Typical uses:
 * a fixed table -- explicit ``x`` / ``y`` per job, uploaded once to the device.
 
 Ternary (bitrate 1.5) groups take group size 32 (``ojx_e8t_gemv_grouped``); 2-bit groups
-(bitrate 2.0, ``E8LatticePacker``, the reference's default) take group size 8, 16, 32 or 64,
-one per group (``ojx_e8_gemv_grouped``).
+(bitrate 2.0, ``E8LatticePacker``, the reference's default) and 1-bit groups (bitrate 1.0,
+``RootE8LatticePacker``) take group size 8, 16, 32 or 64, one per group
+(``ojx_e8_gemv_grouped``, ``ojx_e8r_gemv_grouped``).
 """
 
 from __future__ import annotations
@@ -61,8 +62,9 @@ class GroupedGemv:
                  group_size: int = 32) -> None:
         if dtype not in (torch.bfloat16, torch.float16):
             raise RuntimeError("grouped GEMV takes bfloat16 or float16 activations")
-        if float(bitrate) not in (1.5, 2.0):
-            raise RuntimeError("grouped GEMV runs ternary (1.5) or 2-bit (2.0) linears")
+        if float(bitrate) not in (1.0, 1.5, 2.0):
+            raise RuntimeError("grouped GEMV runs ternary (1.5), 2-bit (2.0) or 1-bit (1.0) "
+                               "linears")
         self.bitrate = float(bitrate)
         self.group_size = int(group_size)
         if self.bitrate == 1.5 and self.group_size != 32:
@@ -82,9 +84,10 @@ class GroupedGemv:
                                                       self.M, N.DTYPE_CODE[dtype],
                                                       ctypes.byref(grid)), "gemv_grouped_plan")
         else:
-            N.check(N.lib().ojx_e8_gemv_grouped_plan(ctypes.addressof(self._arr), self.n, self.M,
-                                                     self.group_size, N.DTYPE_CODE[dtype],
-                                                     ctypes.byref(grid)), "e8 gemv_grouped_plan")
+            plan = (N.lib().ojx_e8_gemv_grouped_plan if self.bitrate == 2.0
+                    else N.lib().ojx_e8r_gemv_grouped_plan)
+            N.check(plan(ctypes.addressof(self._arr), self.n, self.M, self.group_size,
+                         N.DTYPE_CODE[dtype], ctypes.byref(grid)), "e8/e8r gemv_grouped_plan")
         self.grid = grid.value
         self._keep = list(keep)  # tensors the job pointers refer to
         self._lora = []          # layers whose adapter is fused (A, B, scaling read at plan time)
@@ -156,10 +159,11 @@ class GroupedGemv:
                                                  self.M, N.DTYPE_CODE[self.dtype], s),
                     "gemv_grouped")
         else:
-            N.check(N.lib().ojx_e8_gemv_grouped(ctypes.addressof(self._arr), N.ptr(self._dev),
-                                                self.n, N.ptr(x), N.ptr(y), self.M,
-                                                self.group_size, N.DTYPE_CODE[self.dtype], s),
-                    "e8 gemv_grouped")
+            launch = (N.lib().ojx_e8_gemv_grouped if self.bitrate == 2.0
+                      else N.lib().ojx_e8r_gemv_grouped)
+            N.check(launch(ctypes.addressof(self._arr), N.ptr(self._dev), self.n, N.ptr(x),
+                           N.ptr(y), self.M, self.group_size, N.DTYPE_CODE[self.dtype], s),
+                    "e8/e8r gemv_grouped")
         return y
 
 
