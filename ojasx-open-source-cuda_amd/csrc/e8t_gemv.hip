@@ -1233,10 +1233,27 @@ __device__ __forceinline__ uint32_t b2_scale(const uint4 (&sp)[4]) {
     return half ? (w >> 16) : (w & 0xFFFFu);
 }
 
+// The post-scaled B operand of step (piece T, 8-weight unit HW) from a lane's four code
+// pieces: 2-bit, half-word HW of piece T through the nibble or byte table; 1-bit Root E8, code
+// byte HW of piece T (8 bytes) through the 256-entry table of the code's 8 coordinates in the
+// activation dtype (BC copies of 16 bytes, this lane's at `slot`).
+template <int FMT, int T, int HW, int BC>
+__device__ __forceinline__ uint4 post_operand(const uint4 (&cp)[4], const char* lut,
+                                              uint32_t slot) {
+    if constexpr (FMT == kFmtRoot) {
+        const uint32_t code = ((HW < 4 ? cp[T].x : cp[T].y) >> (8 * (HW % 4))) & 0xFFu;
+        return *reinterpret_cast<const uint4*>(lut + 16u * BC * code + slot);
+    } else {
+        const uint32_t dw = (HW / 2) == 0 ? cp[T].x : (HW / 2) == 1 ? cp[T].y
+                          : (HW / 2) == 2 ? cp[T].z : cp[T].w;
+        return b2_operand<(HW % 2), BC>(dw, lut, slot);
+    }
+}
+
 // One round of R row tiles of one wave: steps 0..31, the A fragment read once per step for
 // all R tiles, with the table reads and A fragment of step J + 1 issued before the MFMAs of
 // step J and the scale of a finished group applied after the next group's first MFMA.
-template <int DT, int MM, int GS, int R, int BC>
+template <int DT, int MM, int GS, int R, int BC, int FMT = kFmt2Bit>
 struct B2Round {
     static constexpr int kSpg = GS / 8;  // steps per scale group
     using Pieces = uint4[R][4];
@@ -1251,11 +1268,7 @@ struct B2Round {
             constexpr int t = (J + 1) / 8, hw = (J + 1) % 8;
             a_n = *reinterpret_cast<const uint4*>(xa + 512 * t + 16 * hw);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t dw = (hw / 2) == 0 ? cp[r][t].x : (hw / 2) == 1 ? cp[r][t].y
-                                  : (hw / 2) == 2 ? cp[r][t].z : cp[r][t].w;
-                b_n[r] = b2_operand<(hw % 2), BC>(dw, lut, slot);
-            }
+            for (int r = 0; r < R; ++r) b_n[r] = post_operand<FMT, t, hw, BC>(cp[r], lut, slot);
         }
         constexpr int grp = J / kSpg, slot_d = grp & 1;
         constexpr bool first = (J % kSpg) == 0;
@@ -1300,7 +1313,7 @@ struct B2Round {
         uint4 a = *reinterpret_cast<const uint4*>(xa);
         uint4 b[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) b[r] = b2_operand<0, BC>(cp[r][0].x, lut, slot);
+        for (int r = 0; r < R; ++r) b[r] = post_operand<FMT, 0, 0, BC>(cp[r], lut, slot);
         f32x4 d[R][2];
         float sf[R];
         steps(cp, sp, lut, slot, xa, a, b, d, sf, acc, std::make_integer_sequence<int, 32>{});
@@ -1336,17 +1349,11 @@ __device__ __forceinline__ void vm_wait_le_round() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
 }
 
-// This lane's code and scale pieces of round u (t = 0..3: piece 4t + g).
+// This lane's scale pieces of round u (the 128 / gs scale bytes of code piece 4t + g).
 template <int GS>
-__device__ __forceinline__ void b2_load(uint4 (&cp)[4], uint4 (&sp)[4],
-                                        __amdgpu_buffer_rsrc_t pr, __amdgpu_buffer_rsrc_t sr,
-                                        uint32_t vo_code, uint32_t vo_scale, int u) {
-    const int so_c = uniform_offset((int64_t)u * 256), so_s = uniform_offset((int64_t)u * 2048 / GS);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code + 64u * t, so_c, 0);
-        cp[t] = make_uint4(v.x, v.y, v.z, v.w);
-    }
+__device__ __forceinline__ void b2_scales(uint4 (&sp)[4], __amdgpu_buffer_rsrc_t sr,
+                                          uint32_t vo_scale, int u) {
+    const int so_s = uniform_offset((int64_t)u * 2048 / GS);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         constexpr uint32_t kPiece = 128 / GS;  // scale bytes per code piece
@@ -1363,6 +1370,55 @@ __device__ __forceinline__ void b2_load(uint4 (&cp)[4], uint4 (&sp)[4],
         } else {
             sp[t] = make_uint4(__builtin_amdgcn_raw_buffer_load_b16(sr, o, so_s, 0), 0u, 0u, 0u);
         }
+    }
+}
+
+// This lane's code and scale pieces of round u (t = 0..3: piece 4t + g).
+template <int GS>
+__device__ __forceinline__ void b2_load(uint4 (&cp)[4], uint4 (&sp)[4],
+                                        __amdgpu_buffer_rsrc_t pr, __amdgpu_buffer_rsrc_t sr,
+                                        uint32_t vo_code, uint32_t vo_scale, int u) {
+    const int so_c = uniform_offset((int64_t)u * 256);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(pr, vo_code + 64u * t, so_c, 0);
+        cp[t] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    b2_scales<GS>(sp, sr, vo_scale, u);
+}
+
+// The same for 1-bit codes: four 8-byte pieces (one code byte per 8 weights) at the same k,
+// piece 4t + g at byte 8 (4t + g) of the row's round (128 bytes); the scales as b2_load.
+template <int GS>
+__device__ __forceinline__ void b1_load(uint4 (&cp)[4], uint4 (&sp)[4],
+                                        __amdgpu_buffer_rsrc_t pr, __amdgpu_buffer_rsrc_t sr,
+                                        uint32_t vo_code, uint32_t vo_scale, int u) {
+    const int so_c = uniform_offset((int64_t)u * 128);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(pr, vo_code + 32u * t, so_c, 0);
+        cp[t] = make_uint4(v[0], v[1], 0u, 0u);
+    }
+    b2_scales<GS>(sp, sr, vo_scale, u);
+}
+
+// The 1-bit post-scaled table: code -> its 8 coordinates (0, +-1, +-2) in the activation
+// dtype, C copies of each 16-byte entry.
+template <int DT, int C>
+__device__ __forceinline__ void fill_v1(uint4* tab, int nthreads) {
+    auto half = [](int c) -> uint32_t {
+        if constexpr (DT == kBF16)
+            return c == 0 ? 0u : c == 1 ? 0x3F80u : c == 2 ? 0x4000u : c == -1 ? 0xBF80u : 0xC000u;
+        else
+            return c == 0 ? 0u : c == 1 ? 0x3C00u : c == 2 ? 0x4000u : c == -1 ? 0xBC00u : 0xC000u;
+    };
+    for (int i = (int)threadIdx.x; i < kSel1Entries * C; i += nthreads) {
+        const int e = i / C;
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            w[h] = half(kRootTable.c[e][2 * h]) | (half(kRootTable.c[e][2 * h + 1]) << 16);
+        tab[i] = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
@@ -3432,17 +3488,22 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
 // weights made the kernel VALU- and LDS-issue-bound: 17.2 VALU and 5.0 LDS instructions per
 // MFMA against 10.5 and 2.5, M = 4 stack 0.725 -> 0.605 ms, same box); MM = 16: the
 // B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).
+// 2-bit post-scaled: at most 168 VGPRs, 3 waves per SIMD (214 -> 160, M = 1 / 4 stack 0.533 /
+// 0.580 -> 0.525 / 0.561 ms; the 1-bit form at 190 VGPRs gains nothing from 3 or 4).
 template <int DT, int GS, int MM, int R, int W, int FMT = kFmt2Bit>
-__global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(
+    FMT == kFmt2Bit && MM <= 4 ? 3 : 1))) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
-    // 1-bit Root E8 (FMT kFmtRoot): the B-operand form with its code -> selector table
-    static_assert(FMT == kFmt2Bit || (FMT == kFmtRoot && !kPost), "2-bit, or 1-bit at MM 16");
+    // 1-bit Root E8 (FMT kFmtRoot): post-scaled with its code -> coordinates table, or the
+    // B-operand form with its code -> selector table
+    static_assert(FMT == kFmt2Bit || FMT == kFmtRoot, "2-bit or 1-bit codes");
     static_assert(MM == 1 || MM == 4 || MM == 16, "activation rows 1, 4 or 16");
     constexpr int kXBytes = kPost ? MM * (int)kXRow : kB2mXBytes;  // one round's stage
     // the byte tables (16 copies; 32 copies, conflict-free, measured 2% slower at M = 1):
     // weights (post-scaled) or selector pairs (B operand)
-    // table copies: 16 for the 2-bit byte tables (8-byte entries); one 4 KB 1-bit selector
-    // table (8 copies, 32 KB, conflict-free: 0.569 -> 0.585 ms at M = 1 over a 32-layer stack)
+    // table copies: 16 for the 2-bit byte tables (8-byte entries); one 4 KB 1-bit table of
+    // 16-byte entries (8 copies, conflict-free, of the selector table: 0.569 -> 0.585 ms at
+    // M = 1 over a 32-layer stack)
     constexpr int BC = FMT == kFmtRoot ? 1 : 16;
     __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries * BC : kB2ByteLutU4<16>];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
@@ -3451,7 +3512,8 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     __shared__ __attribute__((aligned(128))) char xs1[kXBytes + (kPost ? kB2ZeroBytes : 0)];
 
     if constexpr (kPost) {
-        fill_b2blut<DT, 64 * W, BC>(lut_storage);
+        if constexpr (FMT == kFmtRoot) fill_v1<DT, BC>(lut_storage, 64 * W);
+        else fill_b2blut<DT, 64 * W, BC>(lut_storage);
         for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * W) {
             reinterpret_cast<uint4*>(xs0 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
             reinterpret_cast<uint4*>(xs1 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -3531,7 +3593,10 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     auto load = [&](Piece (&cp)[R], Piece (&sp)[R], int u) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if constexpr (kPost) b2_load<GS>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
+            if constexpr (kPost && FMT == kFmtRoot)
+                b1_load<GS>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
+            else if constexpr (kPost)
+                b2_load<GS>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
             else b2m_load<GS, FMT>(cp[r], sp[r], pr, sr, vo_code[r], vo_scale[r], u);
         }
     };
@@ -3546,7 +3611,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     const char* lut = reinterpret_cast<const char*>(lut_storage);
     auto compute = [&](const Piece (&cp)[R], const Piece (&sp)[R], const char* xs) {
         if constexpr (kPost) {
-            B2Round<DT, MM, GS, R, BC>::run(cp, sp, lut, slot, xs + aoff, accp);
+            B2Round<DT, MM, GS, R, BC, FMT>::run(cp, sp, lut, slot, xs + aoff, accp);
         } else {
             B2mRound<DT, GS, FMT, R, BC>::run(cp, sp, lut, slot, xs, xo, accm);
         }
@@ -3617,11 +3682,15 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
 constexpr int kB2gWaves = 4;
 constexpr int kB2gWavesB = 8;
 constexpr int kB2gTiles = 2;
+constexpr int kB1gTiles = 2;  // 1-bit post-scaled
+constexpr int kB1gWaves = 4;
 Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024, int fmt) {
     (void)total_tiles;
     Gemv2Plan p{};
-    p.post = fmt == kFmt2Bit && M <= 4 && k1024;
-    p.R = (p.post ? kB2gWaves : kB2gWavesB) * kB2gTiles;  // row tiles per workgroup
+    p.post = M <= 4 && k1024;
+    // row tiles per workgroup
+    p.R = !p.post ? kB2gWavesB * kB2gTiles
+                  : fmt == kFmtRoot ? kB1gWaves * kB1gTiles : kB2gWaves * kB2gTiles;
     return p;
 }
 int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p) { return ((N + 15) / 16 + p.R - 1) / p.R; }
@@ -3630,8 +3699,15 @@ template <int DT, int GS>
 static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p, int64_t wgs,
                                          int fmt, hipStream_t s) {
     if (fmt == kFmtRoot) {
-        hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB, kFmtRoot>),
-                           dim3((unsigned)wgs), dim3(64 * kB2gWavesB), 0, s, a);
+        if (p.post && a.M == 1)
+            hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 1, kB1gTiles, kB1gWaves, kFmtRoot>),
+                               dim3((unsigned)wgs), dim3(64 * kB1gWaves), 0, s, a);
+        else if (p.post)
+            hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 4, kB1gTiles, kB1gWaves, kFmtRoot>),
+                               dim3((unsigned)wgs), dim3(64 * kB1gWaves), 0, s, a);
+        else
+            hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB, kFmtRoot>),
+                               dim3((unsigned)wgs), dim3(64 * kB2gWavesB), 0, s, a);
     } else if (p.post) {
         if (a.M == 1)
             hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 1, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
