@@ -162,7 +162,7 @@ static Route route_fwd(int fmt, const void* x, const uint8_t* packed, const uint
             return kRouteMfma;
         return kRouteGeneric;
     }
-    if (fmt == ojx::kFmt2Bit && ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype))
+    if (ojx::gemv2_supported(x, packed, scales, y, M, N, K, gs, dtype, fmt))
         return kRouteGemv2;
     if (ojx::gemv2m_supported(x, packed, scales, y, M, N, K, gs, dtype, fmt)) return kRouteGemv2m;
     if (ojx::gemm_mfma_supported(x, packed, scales, M, N, K, gs, dtype, fmt)) return kRouteMfma;
@@ -213,7 +213,7 @@ static int gemm_fwd(int fmt, const void* x, const uint8_t* packed, const uint16_
         e = ojx::launch_gemv2m(x, packed, scales, bias, y, M, N, K, gs, dtype, s, fmt, lora);
         break;
     case kRouteGemv2:
-        e = ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s, lora);
+        e = ojx::launch_gemv2(x, packed, scales, bias, y, M, N, K, gs, dtype, s, lora, fmt);
         break;
     case kRouteGemv: {
         ojx::GemvLaunch a{};

@@ -1422,7 +1422,9 @@ __device__ __forceinline__ void fill_v1(uint4* tab, int nthreads) {
     }
 }
 
-template <int DT, int MM, int GS>
+// FMT: 2-bit codes (nibble table of values) or 1-bit Root E8 codes (one 4-KB table of each
+// code's 8 coordinates, 8 code bytes per lane and round).
+template <int DT, int MM, int GS, int FMT = kFmt2Bit>
 __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     GemvLaunch args) {
     // this workgroup's linear: the launch's one job (per-linear launch) or a grouped job
@@ -1438,10 +1440,12 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const LoraEp lora{job.lora_u, job.lora_b, job.lora_r,
                       job.lora_ldu ? job.lora_ldu : job.lora_r, job.N};
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
-    // the nibble table: filling the byte table's 32 KB costs a per-linear launch more than
-    // its reads save (M = 1 per-linear 2-bit stack 0.497 -> 0.588 ms, same box)
-    constexpr int BC = 0;
-    __shared__ uint4 lut_storage[kB2LutU4];
+    static_assert(FMT == kFmt2Bit || FMT == kFmtRoot, "2-bit or 1-bit codes");
+    constexpr bool kRoot = FMT == kFmtRoot;
+    // 2-bit: the nibble table (filling the byte table's 32 KB costs a per-linear launch more
+    // than its reads save: M = 1 per-linear 2-bit stack 0.497 -> 0.588 ms, same box)
+    constexpr int BC = kRoot ? 1 : 0;
+    __shared__ uint4 lut_storage[kRoot ? kSel1Entries : kB2LutU4];
     // Two activation buffers per wave, each its own LDS object ending in a zero block, so
     // that the compiler can tell the reads of one from the DMA into the other (it waits for
     // every outstanding load before an LDS read that may alias a pending DMA target).
@@ -1450,7 +1454,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     __shared__ __attribute__((aligned(16))) char xs1[kXsBytes + kB2ZeroBytes];
     __shared__ float red[kB2Waves][MM][64];
 
-    fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
+    if constexpr (kRoot) fill_v1<DT, 1>(lut_storage, 64 * kB2Waves);
+    else fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
     for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * kB2Waves) {
         reinterpret_cast<uint4*>(xs0 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
         reinterpret_cast<uint4*>(xs1 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -1460,7 +1465,8 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i16 = lane & 15;
     const int64_t tile = wg;
-    const uint32_t rowbytes = (uint32_t)(K / 4), srowbytes = (uint32_t)(K * 2 / GS);
+    const uint32_t rowbytes = (uint32_t)(kRoot ? K / 8 : K / 4);
+    const uint32_t srowbytes = (uint32_t)(K * 2 / GS);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)packed, (short)0, (int)(N * rowbytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
@@ -1468,9 +1474,14 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)x, (short)0, (int)(M * K * 2), kRsrcWord3);
     const uint32_t row = (uint32_t)(tile * 16 + i16);
-    const uint32_t vo_code = row * rowbytes + 16u * g;
+    const uint32_t vo_code = row * rowbytes + (kRoot ? 8u : 16u) * g;
     const uint32_t vo_scale = row * srowbytes + (128u / GS) * g;
-    const uint32_t slot = b2_slot<BC>(lane);
+    const uint32_t slot = kRoot ? 0u : b2_slot<BC>(lane);
+    // this lane's codes and scales of round v (the same number of loads in both formats)
+    auto load = [&](uint4 (&cp)[4], uint4 (&sp)[4], int v) {
+        if constexpr (kRoot) b1_load<GS>(cp, sp, pr, sr, vo_code, vo_scale, v);
+        else b2_load<GS>(cp, sp, pr, sr, vo_code, vo_scale, v);
+    };
 
     // A row i16 = 4 g' + m: live in lane group g' only, for activation rows m < M
     const int am = i16 & 3;
@@ -1489,10 +1500,10 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
 #pragma unroll
     for (int q = 0; q < MM; ++q) acc[0][q] = 0.f;
     uint4 cp[2][1][4], sp[2][1][4];
-    using Round = B2Round<DT, MM, GS, 1, BC>;
+    using Round = B2Round<DT, MM, GS, 1, BC, FMT>;
     int u = wave;
     if (u < T) {
-        b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, u);
+        load(cp[0][0], sp[0][0], u);
         b2_stage_x<MM>(xw0, xr, u, M, K, lane);
     }
     __syncthreads();  // table and zero block ready
@@ -1504,12 +1515,12 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     // pair or round runs after the loop, with nothing fetched behind it (a spare fetch
     // would add a memory round trip to the wave's end).
     while (u + 2 * kB2Waves < T) {  // uniform within the wave
-        b2_load<GS>(cp[1][0], sp[1][0], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        load(cp[1][0], sp[1][0], u + kB2Waves);
         b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
         vm_wait_le_round<GS, MM>();  // round u's codes, scales and activations have landed
         Round::run(cp[0], sp[0], lut, slot, xa0, acc);
         lds_wait_all();  // this wave's reads of buffer 0 are done: it may be refilled
-        b2_load<GS>(cp[0][0], sp[0][0], pr, sr, vo_code, vo_scale, u + 2 * kB2Waves);
+        load(cp[0][0], sp[0][0], u + 2 * kB2Waves);
         b2_stage_x<MM>(xw0, xr, u + 2 * kB2Waves, M, K, lane);
         vm_wait_le_round<GS, MM>();
         Round::run(cp[1], sp[1], lut, slot, xa1, acc);
@@ -1517,7 +1528,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
         u += 2 * kB2Waves;
     }
     if (u + kB2Waves < T) {  // a last pair
-        b2_load<GS>(cp[1][0], sp[1][0], pr, sr, vo_code, vo_scale, u + kB2Waves);
+        load(cp[1][0], sp[1][0], u + kB2Waves);
         b2_stage_x<MM>(xw1, xr, u + kB2Waves, M, K, lane);
         vm_wait_le_round<GS, MM>();
         Round::run(cp[0], sp[0], lut, slot, xa0, acc);
@@ -3154,7 +3165,11 @@ hipError_t launch_gemv(const GemvLaunch& a, const GemvPlan& p, int64_t wgs, int 
 }
 
 bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                     const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt) {
+                     const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt) {
+    if (fmt != kFmt2Bit && fmt != kFmtRoot) return false;
+    // 1-bit at M = 1 only: per-linear 8-layer stack M = 1 0.528 -> 0.456 ms, M = 4 0.548 ->
+    // 0.561 ms against the B-operand kernel (same box)
+    if (fmt == kFmtRoot && M != 1) return false;
     if (dt != kBF16 && dt != kF16) return false;
     if (M < 1 || M > 4 || N < 1 || K < kRound || K % kRound != 0) return false;
     if (gs != 8 && gs != 16 && gs != 32 && gs != 64) return false;
@@ -3162,7 +3177,8 @@ bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scale
         ((uintptr_t)y & 1u))
         return false;
     // 32-bit buffer offsets (codes, scales, activations, with one tile of row padding)
-    if ((N + 64) * (K / 4) >= (1ll << 31) || (N + 64) * (K * 2 / gs) >= (1ll << 31) ||
+    const int64_t rowbytes = fmt == kFmtRoot ? K / 8 : K / 4;
+    if ((N + 64) * rowbytes >= (1ll << 31) || (N + 64) * (K * 2 / gs) >= (1ll << 31) ||
         M * K * 2 >= (1ll << 31))
         return false;
     return true;
@@ -3184,29 +3200,29 @@ static GemvLaunch one_job(const void* x, const uint8_t* packed, const uint16_t* 
 
 // `wgs` workgroups of one 16-row tile each (each job's tiles start a new workgroup)
 template <int DT, int MM, int GS>
-static hipError_t launch_gemv2_grid(const GemvLaunch& a, int64_t wgs, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv2_kernel<DT, MM, GS>), dim3((unsigned)wgs), dim3(64 * kB2Waves), 0,
-                       stream, a);
-    return hipGetLastError();
-}
-
-template <int DT, int MM, int GS>
 static hipError_t launch_gemv2_t(const void* x, const uint8_t* packed, const uint16_t* scales,
                                  const void* bias, void* y, int M, int64_t N, int64_t K,
-                                 hipStream_t stream, const LoraEp& lora) {
-    return launch_gemv2_grid<DT, MM, GS>(one_job(x, packed, scales, bias, y, M, N, K, lora),
-                                         (N + 15) / 16, stream);
+                                 hipStream_t stream, const LoraEp& lora, int fmt) {
+    const GemvLaunch a = one_job(x, packed, scales, bias, y, M, N, K, lora);
+    const dim3 grid((unsigned)((N + 15) / 16)), block(64 * kB2Waves);
+    if (fmt == kFmtRoot) {
+        if constexpr (MM != 1) return hipErrorInvalidValue;  // gemv2_supported: M == 1
+        else hipLaunchKernelGGL((gemv2_kernel<DT, 1, GS, kFmtRoot>), grid, block, 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((gemv2_kernel<DT, MM, GS>), grid, block, 0, stream, a);
+    }
+    return hipGetLastError();
 }
 
 template <int DT, int MM>
 static hipError_t launch_gemv2_gs(const void* x, const uint8_t* packed, const uint16_t* scales,
                                   const void* bias, void* y, int M, int64_t N, int64_t K,
-                                  int64_t gs, hipStream_t stream, const LoraEp& lora) {
+                                  int64_t gs, hipStream_t stream, const LoraEp& lora, int fmt) {
     switch (gs) {
-        case 8: return launch_gemv2_t<DT, MM, 8>(x, packed, scales, bias, y, M, N, K, stream, lora);
-        case 16: return launch_gemv2_t<DT, MM, 16>(x, packed, scales, bias, y, M, N, K, stream, lora);
-        case 32: return launch_gemv2_t<DT, MM, 32>(x, packed, scales, bias, y, M, N, K, stream, lora);
-        default: return launch_gemv2_t<DT, MM, 64>(x, packed, scales, bias, y, M, N, K, stream, lora);
+        case 8: return launch_gemv2_t<DT, MM, 8>(x, packed, scales, bias, y, M, N, K, stream, lora, fmt);
+        case 16: return launch_gemv2_t<DT, MM, 16>(x, packed, scales, bias, y, M, N, K, stream, lora, fmt);
+        case 32: return launch_gemv2_t<DT, MM, 32>(x, packed, scales, bias, y, M, N, K, stream, lora, fmt);
+        default: return launch_gemv2_t<DT, MM, 64>(x, packed, scales, bias, y, M, N, K, stream, lora, fmt);
     }
 }
 
@@ -3464,13 +3480,13 @@ hipError_t launch_gemv_tile(const GemvLaunch& a, int64_t tiles, int64_t Kmax, in
 
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        int dt, hipStream_t stream, const LoraEp& lora) {
+                        int dt, hipStream_t stream, const LoraEp& lora, int fmt) {
     const int m = (int)M;
     if (dt == kBF16)
-        return M == 1 ? launch_gemv2_gs<kBF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
-                      : launch_gemv2_gs<kBF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
-    return M == 1 ? launch_gemv2_gs<kF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora)
-                  : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora);
+        return M == 1 ? launch_gemv2_gs<kBF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora, fmt)
+                      : launch_gemv2_gs<kBF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora, fmt);
+    return M == 1 ? launch_gemv2_gs<kF16, 1>(x, packed, scales, bias, y, m, N, K, gs, stream, lora, fmt)
+                  : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora, fmt);
 }
 
 // ---- streaming 2-bit GEMV for grouped launches

@@ -40,13 +40,13 @@ hipError_t launch_cs_project_dt(const void* x, int dt, int64_t nvec, void* out,
 hipError_t launch_ste_quantize_dt(const void* w, int dt, int64_t numel, void* out,
                                   hipStream_t stream);
 
-// 2-bit decode GEMV (M <= 4, bf16/fp16, K % 1024 == 0, gs in {8, 16, 32, 64}, 16-byte
-// aligned buffers).
+// Post-scaled decode GEMV of 2-bit (fmt 1, M <= 4) or 1-bit Root-E8 (fmt 2, M == 1) codes
+// (bf16/fp16, K % 1024 == 0, gs in {8, 16, 32, 64}, 16-byte aligned buffers).
 bool gemv2_supported(const void* x, const uint8_t* packed, const uint16_t* scales,
-                     const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt);
+                     const void* y, int64_t M, int64_t N, int64_t K, int64_t gs, int dt, int fmt);
 hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* scales,
                         const void* bias, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        int dt, hipStream_t stream, const LoraEp& lora = LoraEp{});
+                        int dt, hipStream_t stream, const LoraEp& lora, int fmt);
 
 // Decode GEMV with the weights in the B operand for the ternary (fmt 0, gs 32), 2-bit (fmt 1)
 // and 1-bit Root-E8 (fmt 2) formats: M <= 16, bf16/fp16, K % 256 == 0, gs in {8, 16, 32, 64},
