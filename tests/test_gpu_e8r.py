@@ -188,11 +188,12 @@ def test_e8r_gemv_kernel_matches_oracle(M, N, K, gs, dtype):
     (4, 16 * 37 + 5, 4096, 64, torch.bfloat16),   # four rounds per wave: all in flight
     (2, 16 * 37 + 5, 5120, 16, torch.bfloat16),   # five rounds per wave: a second pass
     (4, 16 * 600, 1024, 32, torch.bfloat16),      # two row tiles per workgroup
-    (1, 16 * 600 + 7, 2048, 8, torch.float16),    # ... ragged last tile
+    (2, 16 * 600 + 7, 2048, 8, torch.float16),    # ... ragged last tile
 ])
 def test_e8r_gemv_m4_pipeline_matches_oracle(M, N, K, gs, dtype):
-    # M <= 4: the B-operand GEMV that stages activation rows 0..3 and keeps four rounds per
-    # wave in flight (spare slots past a wave's last round load nothing)
+    # M <= 4 (M = 1 only where K % 1024 != 0): the B-operand GEMV that stages activation rows
+    # 0..3 and keeps four rounds per wave in flight (spare slots past a wave's last round load
+    # nothing)
     pk, sc, pk_np, sc_np = _layer1(N, K, seed=3 * N + K + gs, gs=gs)
     g = torch.Generator().manual_seed(M * 13 + K)
     x = torch.randn(M, K, generator=g).to(dtype)
@@ -206,6 +207,35 @@ def test_e8r_gemv_m4_pipeline_matches_oracle(M, N, K, gs, dtype):
     assert _rel_err(y, ref) <= REL_TOL
     for m in range(M):  # each activation row against its own scale
         assert _rel_err(y[m:m + 1], ref[m:m + 1]) <= REL_TOL, m
+
+
+@pytest.mark.parametrize("N,K,gs,dtype,bias", [
+    (16 * 37 + 5, 1024, 32, torch.bfloat16, True),    # one round: three waves idle
+    (16 * 37 + 5, 3072, 8, torch.float16, True),      # three rounds, one per wave
+    (16 * 300 + 9, 5120, 16, torch.bfloat16, False),  # wave 0: a last pair
+    (1000, 9216, 64, torch.float16, True),            # wave 0: a round pair, then a last round
+    (4096, 14336, 32, torch.bfloat16, True),          # down projection: the loop and a pair
+])
+def test_e8r_post_scaled_m1_matches_oracle(N, K, gs, dtype, bias):
+    # M = 1, K % 1024 == 0: the post-scaled GEMV (a code byte's eight coordinates from the
+    # table, the group scale applied to fp32 partial sums), one row tile per workgroup and
+    # rounds u = w, w + 4, ... per wave
+    pk, sc, pk_np, sc_np = _layer1(N, K, seed=5 * N + K + gs, gs=gs)
+    g = torch.Generator().manual_seed(K + gs)
+    x = torch.randn(1, K, generator=g).to(dtype)
+    b = torch.randn(N, generator=g).to(dtype) if bias else None
+    print(f"e8r post-scaled M=1 N={N} K={K} gs={gs} {dtype} bias={bias}", flush=True)
+    y = ops.e8r_linear(x.to(DEV), pk, sc, b.to(DEV) if bias else None, N, K, gs)
+    torch.cuda.synchronize()
+    ref = O.e8r_gemm_f64(x.float().numpy(), pk_np, sc_np, b.float().numpy() if bias else None,
+                         N, K, gs, DT_CODE[dtype])
+    assert y.shape == (1, N) and y.dtype == dtype
+    assert _rel_err(y, ref) <= REL_TOL
+    # the same weights through the B-operand GEMV (two activation rows) agree row by row
+    x2 = torch.cat([x, x]).to(DEV)
+    y2 = ops.e8r_linear(x2, pk, sc, b.to(DEV) if bias else None, N, K, gs)
+    torch.cuda.synchronize()
+    assert _rel_err(y2[1:2], ref) <= REL_TOL
 
 
 def test_e8r_prefill_large_shape_against_decoded_matmul():
