@@ -3504,11 +3504,8 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
 // weights made the kernel VALU- and LDS-issue-bound: 17.2 VALU and 5.0 LDS instructions per
 // MFMA against 10.5 and 2.5, M = 4 stack 0.725 -> 0.605 ms, same box); MM = 16: the
 // B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).
-// 2-bit post-scaled: at most 168 VGPRs, 3 waves per SIMD (214 -> 160, M = 1 / 4 stack 0.533 /
-// 0.580 -> 0.525 / 0.561 ms; the 1-bit form at 190 VGPRs gains nothing from 3 or 4).
 template <int DT, int GS, int MM, int R, int W, int FMT = kFmt2Bit>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(
-    FMT == kFmt2Bit && MM <= 4 ? 3 : 1))) void gemv2g_kernel(GemvLaunch args) {
+__global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
     // 1-bit Root E8 (FMT kFmtRoot): post-scaled with its code -> coordinates table, or the
     // B-operand form with its code -> selector table
