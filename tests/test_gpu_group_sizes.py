@@ -47,7 +47,7 @@ def _layer(N, K, seed, gs):
 def _rel(y: torch.Tensor, ref) -> float:
     ref = ref if isinstance(ref, torch.Tensor) else torch.from_numpy(ref)
     ref = ref.to(y.device).float()
-    return float((y.float() - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+    return float((y.detach().float() - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
 
 
 def _dense(pk, sc, N, K, gs, dtype):
