@@ -3489,7 +3489,7 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
                   : launch_gemv2_gs<kF16, 4>(x, packed, scales, bias, y, m, N, K, gs, stream, lora, fmt);
 }
 
-// ---- streaming 2-bit GEMV for grouped launches
+// ---- streaming 2-bit and 1-bit GEMV for grouped launches
 //
 // The per-linear 2-bit kernels above give each workgroup one or two 16-row tiles and split
 // K over its waves, so every workgroup stages the activations of all of K for 16-32 rows:
@@ -3503,7 +3503,8 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
 // sharing each A fragment; the nibble table's four reads and address computations per 8
 // weights made the kernel VALU- and LDS-issue-bound: 17.2 VALU and 5.0 LDS instructions per
 // MFMA against 10.5 and 2.5, M = 4 stack 0.725 -> 0.605 ms, same box); MM = 16: the
-// B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).
+// B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).  1-bit codes take the
+// same rounds with 8-byte code pieces per lane and the 1-bit tables.
 template <int DT, int GS, int MM, int R, int W, int FMT = kFmt2Bit>
 __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
@@ -3686,12 +3687,14 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     }
 }
 
-// ---- grouped 2-bit decode GEMV: many linears of one group size in one launch
-// Streaming 2-bit kernel geometry of a grouped launch: waves per workgroup and row tiles per
-// wave; M <= 4 needs every K a multiple of 1024 (post-scaled rounds), otherwise the 16-row
+// ---- grouped 2-bit / 1-bit decode GEMV: many linears of one group size in one launch
+// Streaming kernel geometry of a grouped launch: waves per workgroup and row tiles per wave;
+// M <= 4 needs every K a multiple of 1024 (post-scaled rounds), otherwise the 16-row
 // B-operand rounds take it.
-// Measured (32-layer stack, same box): post-scaled 4 waves x 2 tiles (8 x 1 equal, 8 x 2
-// 0.536 -> 0.646 ms at M = 1); B operand 8 waves x 2 tiles (0.674 -> 0.659 ms at M = 16).
+// Measured (32-layer stack, same box): 2-bit post-scaled 4 waves x 2 tiles (8 x 1 equal,
+// 8 x 2 0.536 -> 0.646 ms at M = 1); B operand 8 waves x 2 tiles (0.674 -> 0.659 ms at
+// M = 16).  1-bit post-scaled 4 waves x 2 tiles: 0.478 ms at M = 1 against 0.50 with 3 or 4
+// tiles and 0.59-0.61 with 8 waves.
 constexpr int kB2gWaves = 4;
 constexpr int kB2gWavesB = 8;
 constexpr int kB2gTiles = 2;
