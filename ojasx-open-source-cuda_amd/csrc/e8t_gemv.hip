@@ -3513,11 +3513,13 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     static_assert(FMT == kFmt2Bit || FMT == kFmtRoot, "2-bit or 1-bit codes");
     static_assert(MM == 1 || MM == 4 || MM == 16, "activation rows 1, 4 or 16");
     constexpr int kXBytes = kPost ? MM * (int)kXRow : kB2mXBytes;  // one round's stage
-    // the byte tables (16 copies; 32 copies, conflict-free, measured 2% slower at M = 1):
-    // weights (post-scaled) or selector pairs (B operand)
-    // table copies: 16 for the 2-bit byte tables (8-byte entries); one 4 KB 1-bit table of
-    // 16-byte entries (8 copies, conflict-free, of the selector table: 0.569 -> 0.585 ms at
-    // M = 1 over a 32-layer stack)
+    // table copies (lane l reads copy l % BC): 16 of the 2-bit byte tables, whose 8-byte
+    // entries hold four weights (post-scaled) or two selector words (B operand; 32 copies,
+    // conflict-free, measured 2% slower at M = 1); one of the 4 KB 1-bit tables, whose
+    // 16-byte entries hold a code's coordinates (post-scaled) or selector words (B operand):
+    // more copies cost more to fill than their bank conflicts (32-layer stack: coordinates
+    // 0.478 ms at M = 1 with one copy, 0.50 / 0.54 / 0.59 with 2 / 4 / 8; selectors 0.569
+    // against 0.585 ms with 8)
     constexpr int BC = FMT == kFmtRoot ? 1 : 16;
     __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries * BC : kB2ByteLutU4<16>];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
