@@ -73,12 +73,14 @@ def test_grouped_e8b_full_decoder_layer(layer_gs32, M, copies):
             assert _rel(y, sep.double().cpu().numpy()) <= REL_TOL, name
 
 
+@pytest.mark.parametrize("shapes", [
+    [(200, 1024), (77, 768), (1030, 2048)],   # a K % 1024 != 0: B-operand rounds at every M
+    [(200, 1024), (77, 3072), (1030, 2048)],  # every K % 1024 == 0: post-scaled at M <= 4
+], ids=["k256", "k1024"])
 @pytest.mark.parametrize("gs", [8, 16, 64])
 @pytest.mark.parametrize("M", [1, 3, 8])
-def test_grouped_e8b_group_sizes_and_ragged_jobs(gs, M):
-    # ragged N, a K that is not a multiple of 1024 (the B-operand kernel at every M), jobs
-    # sharing one output (y_col)
-    shapes = [(200, 1024), (77, 768), (1030, 2048)]
+def test_grouped_e8b_group_sizes_and_ragged_jobs(gs, M, shapes):
+    # ragged N, jobs sharing one output (y_col)
     layers = []
     for i, (N, K) in enumerate(shapes):
         g = torch.Generator().manual_seed(600 + i + gs)
