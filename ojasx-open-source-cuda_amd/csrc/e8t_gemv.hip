@@ -374,12 +374,6 @@ __device__ __forceinline__ void codes_lut(const uint32_t (&cd)[R][NW], const cha
     }
 }
 
-template <int R, int J>
-__device__ __forceinline__ void wide_lut(const WideCodes<R>& w, const char* lut, uint32_t slot,
-                                         uint2 (&ml)[R], uint2 (&mh)[R]) {
-    codes_lut<R, 12, J>(w.cd, lut, slot, ml, mh);
-}
-
 // The same table reads, as one 4-word B operand per tile (lo words, hi words).
 template <int R, int NW, int J, int SL = kLutSlots>
 __device__ __forceinline__ void codes_lut4(const uint32_t (&cd)[R][NW], const char* lut,
