@@ -162,7 +162,14 @@ __device__ __forceinline__ int find_job(const GemvJob* jobs, int njobs, int64_t 
 }
 
 // The job of workgroup `wg` of a launch (the device table, or the launch's inline jobs);
-// `wg` becomes the workgroup's index within the job.
+// `wg` becomes the workgroup's index within the job.  The compiler may merge the two sources
+// into one copy through a generic pointer (flat loads into vector registers); with kScalar
+// every word is then passed through readfirstlane, so that the pointers and sizes derived
+// from the job, uniform by construction, stay in scalar registers: a buffer descriptor it
+// cannot prove uniform makes it wrap every buffer load in a loop over the wave's distinct
+// values (measured: grouped 2-bit stack 0.54 / 0.60 -> 0.47 / 0.52 ms at M = 1 / 4, 1-bit
+// 0.48 / 0.51 -> 0.45 / 0.47; per-linear down at M = 16 14.9 -> 13.6 us).
+template <bool kScalar = true>
 __device__ __forceinline__ GemvJob gemv_job_of(const GemvLaunch& args, int64_t& wg) {
     GemvJob job;
     if (args.jobs != nullptr) {
@@ -172,6 +179,15 @@ __device__ __forceinline__ GemvJob gemv_job_of(const GemvLaunch& args, int64_t& 
 #pragma unroll
         for (int i = 1; i < kGemvInlineJobs; ++i)
             if (i < args.njobs && wg >= args.inl[i].wg_begin) job = args.inl[i];
+    }
+    if constexpr (kScalar) {
+        static_assert(sizeof(GemvJob) % 4 == 0, "job words");
+        uint32_t words[sizeof(GemvJob) / 4];
+        __builtin_memcpy(words, &job, sizeof(GemvJob));
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(GemvJob) / 4); ++i)
+            words[i] = __builtin_amdgcn_readfirstlane(words[i]);
+        __builtin_memcpy(&job, words, sizeof(GemvJob));
     }
     wg -= job.wg_begin;
     return job;
@@ -2196,7 +2212,9 @@ __device__ __forceinline__ void b2x_stage_block(char* xb, __amdgpu_buffer_rsrc_t
 template <int DT, int GS, int FMT, int TPW>
 __global__ __launch_bounds__(64 * kB2xWaves) void gemv2x_kernel(GemvLaunch args) {
     int64_t wg = blockIdx.x;
-    const GemvJob job = gemv_job_of(args, wg);
+    // the job as loaded (per-linear q/o at M = 16 measured 6.7 us against 7.1 with the
+    // scalar copy, which the other kernels take)
+    const GemvJob job = gemv_job_of<false>(args, wg);
     const void* const x = job.x ? job.x : args.x;
     void* const y = job.y ? job.y : args.y;
     const int M = args.M;

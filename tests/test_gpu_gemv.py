@@ -191,6 +191,24 @@ def test_wide_kernel_partial_rounds_and_ragged_rows(M, K):
     assert _rel(y, ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("M", [2, 4])
+@pytest.mark.parametrize("K", [1024, 3072, 4608, 9216])
+def test_wide_one_tile_per_wave_round_counts(M, K):
+    # 1024..4095 row tiles at 1 < M <= 4: the streaming kernel with one row tile per wave, at
+    # one to nine rounds per wave (4608: a partial fifth round)
+    N = 16 * 1024 + 40
+    pk, sc, pk_np, sc_np = _encoded(N, K, seed=2 * K + M)
+    x = _x(M, K, seed=M * 5 + K, dtype=torch.bfloat16)
+    bias = _x(1, N, seed=6, dtype=torch.bfloat16).reshape(N)
+    print(f"wide one tile per wave M={M} K={K}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, O.DT_BF16)
+    assert _rel(y, ref) <= REL_TOL
+    for m in range(M):  # each activation row against its own reference
+        assert _rel(y[m:m + 1], ref[m:m + 1]) <= REL_TOL, m
+
+
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_wide_bf16_activation_dynamic_range(M):
     # activations with a wide dynamic range through the streaming kernels at M <= 4:
