@@ -493,10 +493,14 @@ struct TernaryBwdStagedDecoder {
         rd_shift = (12u * jj) & 31u;
         rd_scale = 64u * St::kCodeRow + St::kScaleRow * (bk.rows >> 2) + 2u * (jj >> 2);
         const uint32_t t = (uint32_t)tid & 255u;
-        scale_piece = St::kScales && t >= 192u;
+        // t >= 192 and tid < 256 are properties of the wave: taken from its (scalar) index,
+        // the descriptor choice below stays scalar (a per-lane choice makes the compiler wrap
+        // every load in a loop over the wave's distinct descriptors)
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        scale_piece = St::kScales && (wv & 3) == 3;
         vo_piece = t >= 192u ? (St::kScales ? bwd_ring_row(t - 192u) * srb + (uint32_t)n0 / 16u : kBwdOob)
                              : bwd_ring_row(t / 3u) * rb + (uint32_t)n0 * 3u / 16u + St::kPiece * (t % 3u);
-        writer = St::kScales ? tid < 256 : t < 192u;
+        writer = St::kScales ? wv < 4 : (wv & 3) < 3;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             vo_scale[q] = (bk.rows + (uint32_t)q) * srb + 2u * (((uint32_t)n0 + bk.col) / GS);
@@ -666,7 +670,7 @@ struct LowbitBwdStagedDecoder {
         rd_code = kCodeRow * k + (uint32_t)kCP * ((cb / kCP) ^ swz<kCodeRow>(k)) + cb % kCP;
         rd_scale = kCodeBytes + kScaleRow * k + (uint32_t)kSP * ((sb / kSP) ^ swz<kScaleRow>(k)) +
                    sb % kSP;
-        writer = tid < 256;
+        writer = __builtin_amdgcn_readfirstlane(tid >> 6) < 4;  // a property of the wave
         ring = ring_lds;
     }
     __device__ __forceinline__ void fetch(int t, u32x4& c, u32x4& sv) const {
