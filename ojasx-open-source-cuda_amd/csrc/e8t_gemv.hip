@@ -3517,9 +3517,17 @@ hipError_t launch_gemv2(const void* x, const uint8_t* packed, const uint16_t* sc
 // MFMA against 10.5 and 2.5, M = 4 stack 0.725 -> 0.605 ms, same box); MM = 16: the
 // B-operand 256-k rounds (B2mRound, R tiles sharing each A fragment).  1-bit codes take the
 // same rounds with 8-byte code pieces per lane and the 1-bit tables.
-template <int DT, int GS, int MM, int R, int W, int FMT = kFmt2Bit>
+// G (B-operand form): rounds per load group.  A 256-k round takes 64 bytes of a 2-bit row and
+// 32 bytes of a 1-bit row, so 2 or 4 consecutive rounds share each 128-byte line; fetched one
+// round at a time, a line's later parts were requested a round after its first, often after
+// L2 had evicted it (traffic 1.8x / 2.7x the algorithmic bytes at M = 16).  A group's rounds
+// are requested back to back and computed in turn (every K % (256 G) == 0): 32-layer stack
+// at M = 16, 2-bit (G = 2) 0.66 -> 0.62 ms, 1-bit (G = 4) 0.568 -> 0.547 ms (one tile per
+// wave instead: 0.66 and 0.62 ms).
+template <int DT, int GS, int MM, int R, int W, int FMT = kFmt2Bit, int G = 1>
 __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     constexpr bool kPost = MM <= 4;
+    static_assert(G == 1 || !kPost, "load groups in the B-operand form only");
     // 1-bit Root E8 (FMT kFmtRoot): post-scaled with its code -> coordinates table, or the
     // B-operand form with its code -> selector table
     static_assert(FMT == kFmt2Bit || FMT == kFmtRoot, "2-bit or 1-bit codes");
@@ -3536,8 +3544,8 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries * BC : kB2ByteLutU4<16>];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
     // (the A fragments of lanes outside their lane group)
-    __shared__ __attribute__((aligned(128))) char xs0[kXBytes + (kPost ? kB2ZeroBytes : 0)];
-    __shared__ __attribute__((aligned(128))) char xs1[kXBytes + (kPost ? kB2ZeroBytes : 0)];
+    __shared__ __attribute__((aligned(128))) char xs0[G * kXBytes + (kPost ? kB2ZeroBytes : 0)];
+    __shared__ __attribute__((aligned(128))) char xs1[G * kXBytes + (kPost ? kB2ZeroBytes : 0)];
 
     if constexpr (kPost) {
         if constexpr (FMT == kFmtRoot) fill_v1<DT, BC>(lut_storage, 64 * W);
@@ -3617,7 +3625,7 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
         }
     };
     using Piece = std::conditional_t<kPost, uint4[4], uint4>;
-    Piece cp0[R], sp0[R], cp1[R], sp1[R];
+    Piece cp0[G][R], sp0[G][R], cp1[G][R], sp1[G][R];
     auto load = [&](Piece (&cp)[R], Piece (&sp)[R], int u) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -3645,26 +3653,32 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
         }
     };
 
-    load(cp0, sp0, 0);
-    stage(xs0, 0);
+    // load group v: rounds G v .. G v + G - 1 (codes and scales, then their activations)
+    auto fetch = [&](Piece (&cp)[G][R], Piece (&sp)[G][R], char* xs, int v) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) load(cp[j], sp[j], G * v + j);
+#pragma unroll
+        for (int j = 0; j < G; ++j) stage(xs + j * kXBytes, G * v + j);
+    };
+    auto compute_group = [&](const Piece (&cp)[G][R], const Piece (&sp)[G][R], const char* xs) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) compute(cp[j], sp[j], xs + j * kXBytes);
+    };
+    const int TG = T / G;
+
+    fetch(cp0, sp0, xs0, 0);
     vm_wait_all();
-    __syncthreads();  // table, zero blocks, round 0 ready
-    // rounds in pairs, so that each register set and stage is a compile-time choice; round u
-    // fetches round u + 1 while it computes, then the workgroup waits for it
-    for (int u = 0; u < T; u += 2) {
-        if (u + 1 < T) {
-            load(cp1, sp1, u + 1);
-            stage(xs1, u + 1);
-        }
-        compute(cp0, sp0, xs0);
+    __syncthreads();  // table, zero blocks, load group 0 ready
+    // load groups in pairs, so that each register set and stage is a compile-time choice;
+    // group v fetches group v + 1 while it computes, then the workgroup waits for it
+    for (int v = 0; v < TG; v += 2) {
+        if (v + 1 < TG) fetch(cp1, sp1, xs1, v + 1);
+        compute_group(cp0, sp0, xs0);
         vm_wait_all();
         __syncthreads();
-        if (u + 1 >= T) break;
-        if (u + 2 < T) {
-            load(cp0, sp0, u + 2);
-            stage(xs0, u + 2);
-        }
-        compute(cp1, sp1, xs1);
+        if (v + 1 >= TG) break;
+        if (v + 2 < TG) fetch(cp0, sp0, xs0, v + 2);
+        compute_group(cp1, sp1, xs1);
         vm_wait_all();
         __syncthreads();
     }
@@ -3714,10 +3728,14 @@ constexpr int kB2gWavesB = 8;
 constexpr int kB2gTiles = 2;
 constexpr int kB1gTiles = 2;  // 1-bit post-scaled
 constexpr int kB1gWaves = 4;
+// B-operand form where every K % 1024 == 0: rounds per load group (2-bit, 1-bit)
+constexpr int kB2gGroupB2 = 2;
+constexpr int kB2gGroupB1 = 4;
 Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024, int fmt) {
     (void)total_tiles;
     Gemv2Plan p{};
     p.post = M <= 4 && k1024;
+    p.grouped_rounds = !p.post && k1024;
     // row tiles per workgroup
     p.R = !p.post ? kB2gWavesB * kB2gTiles
                   : fmt == kFmtRoot ? kB1gWaves * kB1gTiles : kB2gWaves * kB2gTiles;
@@ -3735,6 +3753,10 @@ static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p
         else if (p.post)
             hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 4, kB1gTiles, kB1gWaves, kFmtRoot>),
                                dim3((unsigned)wgs), dim3(64 * kB1gWaves), 0, s, a);
+        else if (p.grouped_rounds)
+            hipLaunchKernelGGL(
+                (gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB, kFmtRoot, kB2gGroupB1>),
+                dim3((unsigned)wgs), dim3(64 * kB2gWavesB), 0, s, a);
         else
             hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB, kFmtRoot>),
                                dim3((unsigned)wgs), dim3(64 * kB2gWavesB), 0, s, a);
@@ -3745,6 +3767,10 @@ static hipError_t launch_gemv2_grouped_t(const GemvLaunch& a, const Gemv2Plan& p
         else
             hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 4, kB2gTiles, kB2gWaves>), dim3((unsigned)wgs),
                                dim3(64 * kB2gWaves), 0, s, a);
+    } else if (p.grouped_rounds) {
+        hipLaunchKernelGGL(
+            (gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB, kFmt2Bit, kB2gGroupB2>),
+            dim3((unsigned)wgs), dim3(64 * kB2gWavesB), 0, s, a);
     } else {
         hipLaunchKernelGGL((gemv2g_kernel<DT, GS, 16, kB2gTiles, kB2gWavesB>), dim3((unsigned)wgs),
                            dim3(64 * kB2gWavesB), 0, s, a);

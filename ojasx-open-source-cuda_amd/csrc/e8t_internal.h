@@ -113,8 +113,9 @@ struct GemvLaunch {
 // M <= 4 with every K a multiple of 1024 runs post-scaled 1024-k rounds, otherwise B-operand
 // 256-k rounds; R row tiles per workgroup.  Each job's tiles start a new workgroup.
 struct Gemv2Plan {
-    bool post;
-    int R;
+    bool post;            // post-scaled form (M <= 4), else the B-operand form
+    bool grouped_rounds;  // B-operand form: rounds fetched in load groups (every K % 1024 == 0)
+    int R;                // row tiles per workgroup
 };
 Gemv2Plan gemv2_pick_grouped(int64_t total_tiles, int64_t M, bool k1024, int fmt);
 int64_t gemv2_wgs_for(int64_t N, const Gemv2Plan& p);
