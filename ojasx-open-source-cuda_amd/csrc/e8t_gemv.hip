@@ -455,36 +455,53 @@ __device__ __forceinline__ void lds_wait_all() {
 // ------------------------------------------------------------------------- mask kernel
 //
 // M <= 16.  Rounds of 512 k: lane group g covers k = 512u + 128g + 8j, j = 0..15, i.e. 16
-// codes (24 bytes) and 4 group scales (8 bytes) of each of its rows.  A wave's round is 32
-// rows x 96 code bytes + 32 rows x 32 scale bytes = 4 KB, fetched into its stage by four
-// 1-KB loads.  Step j decodes code j of every lane into 8 weights (table masks AND-ed with
-// the group scale word) and runs one v_mfma_f32_16x16x32 per tile with the 16 activation
-// rows as A.  Stage rows are rotated to spread the read-backs over the LDS banks: piece p
-// (16 bytes) of code row n sits at position (p + n/4) mod 6, scale piece p at
-// p ^ ((n/4 + n/8) & 1).
+// codes (24 bytes) and 4 group scales (8 bytes) of each of its rows.  A wave's round of
+// codes is 32 rows x 96 bytes = 3 KB, fetched into its stage by three 1-KB loads.  Step j
+// decodes code j of every lane into 8 weights (table masks AND-ed with the group scale word)
+// and runs one v_mfma_f32_16x16x32 per tile with the 16 activation rows as A.  Stage rows
+// are rotated to spread the read-backs over the LDS banks: piece p (16 bytes) of code row n
+// sits at position (p + n/4) mod 6.
+//
+// Scales go straight to registers in blocks of four rounds: a row's scales of rounds
+// 4b .. 4b+3 are the 128 bytes at 128b, one 128-byte line (rows are K/16 bytes, a multiple
+// of 128 when K % 2048 == 0), requested by four back-to-back 8-byte loads per tile (lane
+// (g, n) takes bytes 32q + 8g .. 32q + 8g + 7 for round 4b + q).  Fetched a round at a time,
+// each line was requested again in each of the next three rounds, by when L2 had often
+// evicted it (about 4x the scale bytes read from HBM).
 
 constexpr int kMRound = 512;                      // K per round of the mask kernel
 constexpr int kMaskWaves = 8;        // waves per workgroup
 constexpr uint32_t kMXRow = kMRound * 2 + 16;     // bytes per padded activation row in LDS
-constexpr uint32_t kMStageBytes = 4096;           // codes 3 KB + scales 1 KB (two tiles)
+constexpr uint32_t kMStageBytes = 3072;           // codes of one round (two tiles)
 
 __device__ __forceinline__ uint32_t mk_rot(uint32_t n) { return n >> 2; }
-__device__ __forceinline__ uint32_t mk_rot_s(uint32_t n) { return ((n >> 2) + (n >> 3)) & 1u; }
 
-// Issues round u's four stage loads (three of codes, one of scales) of the tile group
-// whose rows start `code_shift` / `scale_shift` bytes after this wave's first rows.
+// Issues round u's three code loads into the wave's stage.
 __device__ __forceinline__ void mk_issue(char* stg, __amdgpu_buffer_rsrc_t packed,
-                                         __amdgpu_buffer_rsrc_t scales, const uint32_t* ld_code,
-                                         uint32_t ld_scale, int64_t code_shift,
-                                         int64_t scale_shift, int u) {
-    const int so_c = uniform_offset(code_shift + (int64_t)u * 96);
-    const int so_s = uniform_offset(scale_shift + (int64_t)u * 32);
+                                         const uint32_t* ld_code, int u) {
+    const int so_c = uniform_offset((int64_t)u * 96);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16, ld_code[i],
                                                  so_c, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(scales, lds_ptr(stg + 3072), 16, ld_scale, so_s,
-                                             0, 0);
+}
+
+// Loads scale block b (rounds 4b .. 4b+3) of R row tiles into registers: s[r][q] = the
+// 8 bytes of lane group g in round 4b + q.  Past the row's end (K % 2048 != 0) the loads
+// read the next row or, past the buffer, zero; those rounds do not exist.
+template <int R>
+__device__ __forceinline__ void mk_load_scales(uint32_t (&s)[R][4][2],
+                                               __amdgpu_buffer_rsrc_t scales,
+                                               const uint32_t (&vo_scale)[R], int b) {
+    const int so = uniform_offset((int64_t)b * 128);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(scales, vo_scale[r] + 32u * q, so, 0);
+            s[r][q][0] = v[0];
+            s[r][q][1] = v[1];
+        }
 }
 
 // Stages x[m][512u .. 512u + 512) for m < M into `xs` (row stride kMXRow): one 1-KB load
@@ -582,12 +599,9 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
         const uint32_t p = (pos + 6u - mk_rot(n)) % 6u;
         ld_code[i] = (row0 + 16u * r + n) * rowbytes + 16u * p;
     }
-    uint32_t ld_scale;
-    {
-        const uint32_t r = (uint32_t)lane >> 5, w32 = (uint32_t)lane & 31u;
-        const uint32_t n = w32 >> 1, p = (w32 & 1u) ^ mk_rot_s(n);
-        ld_scale = (row0 + 16u * r + n) * srowbytes + 16u * p;
-    }
+    uint32_t vo_scale[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) vo_scale[r] = (row0 + 16u * r + i16) * srowbytes + 8u * g;
     // read-back offsets of this lane's 8-byte words (codes: words 3g .. 3g+2 of its row)
     uint32_t rd_code[3];
 #pragma unroll
@@ -595,8 +609,6 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
         const uint32_t wd = 3u * g + t, p = wd >> 1;
         rd_code[t] = 96u * i16 + 16u * ((p + mk_rot(i16)) % 6u) + 8u * (wd & 1u);
     }
-    const uint32_t rd_scale =
-        3072u + 32u * i16 + 16u * (((uint32_t)g >> 1) ^ mk_rot_s(i16)) + 8u * (g & 1);
     const uint32_t slot = (uint32_t)(lane & (kLutSlots - 1)) * 8u;
     const int mrow = i16 < M ? i16 : M - 1;
     const uint32_t xa_off = (uint32_t)(mrow * kMXRow + 256 * g);
@@ -607,7 +619,9 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     char* const stg = stage[wave];
-    mk_issue(stg, packed, scales, ld_code, ld_scale, 0, 0, 0);
+    uint32_t scb[R][4][2];
+    mk_issue(stg, packed, ld_code, 0);
+    mk_load_scales<R>(scb, scales, vo_scale, 0);
     mk_stage_x(xs_storage[0], xr, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // table, round-0 weights and activations ready
@@ -623,17 +637,27 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
                 cd[r][2 * t] = v.x;
                 cd[r][2 * t + 1] = v.y;
             }
-            const uint2 v = *reinterpret_cast<const uint2*>(stg + 512 * r + rd_scale);
+            // round u's scales: block entry u % 4 (wave-uniform select)
+            const int q = u & 3;
+            uint32_t s0 = scb[r][0][0], s1 = scb[r][0][1];
+            s0 = q == 1 ? scb[r][1][0] : s0;
+            s1 = q == 1 ? scb[r][1][1] : s1;
+            s0 = q == 2 ? scb[r][2][0] : s0;
+            s1 = q == 2 ? scb[r][2][1] : s1;
+            s0 = q == 3 ? scb[r][3][0] : s0;
+            s1 = q == 3 ? scb[r][3][1] : s1;
             // lane groups past K in a partial last round hold the next row's codes
             const bool live = (int64_t)u * kMRound + 128 * g < K;
-            sc[r][0] = live ? v.x : 0u;
-            sc[r][1] = live ? v.y : 0u;
+            sc[r][0] = live ? s0 : 0u;
+            sc[r][1] = live ? s1 : 0u;
         }
         lds_wait_all();  // the read-back has landed: the stage may be refilled
         const bool has = u + 1 < T;  // uniform over the workgroup
         if (has) {
-            mk_issue(stg, packed, scales, ld_code, ld_scale, 0, 0, u + 1);
+            mk_issue(stg, packed, ld_code, u + 1);
             mk_stage_x(xs_storage[(u + 1) & 1], xr, u + 1, M, K, wave, lane, W);
+            // the block's last round has taken its scales: fetch the next block
+            if ((u & 3) == 3) mk_load_scales<R>(scb, scales, vo_scale, (u + 1) >> 2);
         }
         const char* xa_base = xs_storage[u & 1] + xa_off;
         Ahead<R> ah;
