@@ -767,6 +767,34 @@ __device__ __forceinline__ void ps_load_scales(WideScales<R>& sc, const PsStream
     }
 }
 
+// The scales of rounds u and u + 1 (u even): a row's 128 scale bytes of the pair are one
+// 128-byte line (rows are K/16 bytes, a multiple of 128 when K % 2048 == 0), requested by
+// two back-to-back loads per tile instead of one half a round apart, by when L2 may have
+// evicted the line.  s1 of a pair past the last round (odd round count) reads the next
+// row's scales, or zeros past the buffer, and is never used.
+template <int R>
+__device__ __forceinline__ void ps_load_scale_pair(WideScales<R>& s0, WideScales<R>& s1,
+                                                   const PsStream<R>& st, int64_t scale_shift,
+                                                   int u, int64_t K, int g) {
+    s0.live = (int64_t)u * kRound + 256 * g < K;
+    s1.live = (int64_t)(u + 1) * kRound + 256 * g < K;
+    const int so = uniform_offset(scale_shift + (int64_t)u * 64);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r], so, 0);
+        const u32x4 v1 =
+            __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r] + 64u, so, 0);
+        s0.sc[r][0] = v0.x;
+        s0.sc[r][1] = v0.y;
+        s0.sc[r][2] = v0.z;
+        s0.sc[r][3] = v0.w;
+        s1.sc[r][0] = v1.x;
+        s1.sc[r][1] = v1.y;
+        s1.sc[r][2] = v1.z;
+        s1.sc[r][3] = v1.w;
+    }
+}
+
 // This lane's codes of the staged round (MFMA layout).
 template <int R>
 __device__ __forceinline__ void ps_readback(const PsStage<R>& stg, const PsStream<R>& st,
@@ -1014,9 +1042,9 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     const PsStage<R>& stg = stage[wave];
     char* const stg_bytes = reinterpret_cast<char*>(&stage[wave]);
     WideCodes<R> w;
-    WideScales<R> sc, sc_next;
+    WideScales<R> sc, sc_next, sc_odd;  // sc_odd: the odd round of the current scale pair
     ps_issue(stg_bytes, st.packed, st.ld_code, R, 0, 0);
-    ps_load_scales<R>(sc, st, 0, 0, K, g);
+    ps_load_scale_pair<R>(sc, sc_odd, st, 0, 0, K, g);
     stage_x(xsa, st.x, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // table, zero blocks, round-0 weights and activations ready
@@ -1035,7 +1063,10 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
         const bool has = cn < ngroups;  // uniform over the workgroup
         if (has) {
             ps_issue(stg_bytes, st.packed, st.ld_code, R, cn * code_gshift, un);
-            ps_load_scales<R>(sc_next, st, cn * scale_gshift, un, K, g);
+            if ((un & 1) == 0)
+                ps_load_scale_pair<R>(sc_next, sc_odd, st, cn * scale_gshift, un, K, g);
+            else
+                sc_next = sc_odd;
             stage_x(xs_next, st.x, un, M, K, wave, lane, W);
         }
         ps_round<DT, R, MM, SL>(w, sc, lut, slot, xa_cur, acc);
