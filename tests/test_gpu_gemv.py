@@ -72,11 +72,13 @@ def test_gemv_every_variant(N):
 
 
 @pytest.mark.parametrize("M", [5, 16])
-@pytest.mark.parametrize("K", [768, 1280, 1536, 2048])
+@pytest.mark.parametrize("K", [768, 1280, 1536, 2048, 2560, 3328, 4608])
 def test_streaming_m16_round_counts(K, M):
     # >= 1024 row tiles at 4 < M <= 16: the streaming mask kernel's 512-k rounds -- a partial
-    # last round (768, 1280: lane groups past K), odd and even round counts (1536, 2048), and
-    # a partial last workgroup of 16 tiles (1026 tiles)
+    # last round (768, 1280, 3328: lane groups past K), odd and even round counts (1536,
+    # 2048), a partial last workgroup of 16 tiles (1026 tiles), and scale blocks of four
+    # rounds that the rounds fill exactly (2048), cross (2560: 5 rounds, 3328: 7, 4608: 9)
+    # or leave past the row's end (768 .. 1536)
     N = 16 * 1026
     pk, sc, pk_np, sc_np = _encoded(N, K, seed=K + 7 * M)
     x = _x(M, K, seed=M + K, dtype=torch.bfloat16)
@@ -189,6 +191,40 @@ def test_wide_kernel_partial_rounds_and_ragged_rows(M, K):
     torch.cuda.synchronize()
     ref = O.gemm_f64(x.float().numpy(), pk_np, sc_np, bias.float().numpy(), N, K, 32, O.DT_BF16)
     assert _rel(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("K", [3072, 3328, 5120])
+def test_post_scaled_scale_pairs_round_counts(M, K):
+    # the post-scaled streaming kernel (two tiles per wave) fetches the scales of rounds 2v
+    # and 2v + 1 together: odd round counts (3072: 3 rounds, 5120: 5) end on a pair whose
+    # second round does not exist, 3328 (3.25 rounds) on a partial round in a pair's second
+    # half; 4099 row tiles keep it on that kernel at M = 3 and 4.  The layer is encoded on
+    # the GPU (bit-exact with the oracle's encoder, test_gpu_codec.py); every element is
+    # checked against an fp32 matmul of the decoded weights and row samples against the
+    # fp64 oracle.
+    N = 4 * 16 * 1024 + 40
+    w = torch.randn(N, K, generator=torch.Generator(device=DEV).manual_seed(3 * K + M),
+                    device=DEV) * 0.02
+    pk, sc = ops.encode(w, 32)
+    del w
+    x = _x(M, K, seed=M * 7 + K, dtype=torch.bfloat16)
+    bias = _x(1, N, seed=8, dtype=torch.bfloat16).reshape(N)
+    print(f"post-scaled scale pairs M={M} K={K}", flush=True)
+    y = ops.e8t_linear(x.to(DEV), pk, sc, bias.to(DEV), N, K, 32)
+    torch.cuda.synchronize()
+    dense = ops.decode(pk, sc, N * K, 32, torch.bfloat16).view(N, K).float()
+    full = x.to(DEV).float() @ dense.t() + bias.to(DEV).float()
+    del dense
+    assert _rel(y, full.double().cpu().numpy()) <= REL_TOL
+    pk_np, sc_np = pk.cpu().numpy(), sc.cpu().view(torch.int16).numpy().view(np.uint16)
+    for r0, r1 in [(0, 64), (N // 2 - 32, N // 2 + 32), (N - 64, N)]:
+        ref = O.gemm_f64(x.float().numpy(), pk_np[r0 * K * 3 // 16: r1 * K * 3 // 16],
+                         sc_np[r0 * K // 32: r1 * K // 32], bias[r0:r1].float().numpy(),
+                         r1 - r0, K, 32, O.DT_BF16)
+        assert _rel(y[:, r0:r1], ref) <= REL_TOL, r0
+        for m in range(M):  # each activation row against its own reference
+            assert _rel(y[m:m + 1, r0:r1], ref[m:m + 1]) <= REL_TOL, (r0, m)
 
 
 @pytest.mark.parametrize("M", [2, 4])
