@@ -487,18 +487,21 @@ __device__ __forceinline__ void mk_issue(char* stg, __amdgpu_buffer_rsrc_t packe
 }
 
 // Loads scale block b (rounds 4b .. 4b+3) of R row tiles into registers: s[r][q] = the
-// 8 bytes of lane group g in round 4b + q.  Past the row's end (K % 2048 != 0) the loads
-// read the next row or, past the buffer, zero; those rounds do not exist.
+// 8 bytes of lane group g in round 4b + q.  Rounds past the last (K % 2048 != 0) do not
+// exist: their loads take an out-of-range vector offset and read nothing (zeros), so no
+// load reaches past the last row's scales.  Every load is issued either way: a branch
+// around some of them would make the results' registers wait for the loads.
 template <int R>
 __device__ __forceinline__ void mk_load_scales(uint32_t (&s)[R][4][2],
                                                __amdgpu_buffer_rsrc_t scales,
-                                               const uint32_t (&vo_scale)[R], int b) {
+                                               const uint32_t (&vo_scale)[R], int b, int T) {
     const int so = uniform_offset((int64_t)b * 128);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(scales, vo_scale[r] + 32u * q, so, 0);
+            const uint32_t o = 4 * b + q < T ? vo_scale[r] + 32u * q : kNoRecordOffset;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(scales, o, so, 0);
             s[r][q][0] = v[0];
             s[r][q][1] = v[1];
         }
@@ -621,7 +624,7 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
     char* const stg = stage[wave];
     uint32_t scb[R][4][2];
     mk_issue(stg, packed, ld_code, 0);
-    mk_load_scales<R>(scb, scales, vo_scale, 0);
+    mk_load_scales<R>(scb, scales, vo_scale, 0, T);
     mk_stage_x(xs_storage[0], xr, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // table, round-0 weights and activations ready
@@ -657,7 +660,7 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
             mk_issue(stg, packed, ld_code, u + 1);
             mk_stage_x(xs_storage[(u + 1) & 1], xr, u + 1, M, K, wave, lane, W);
             // the block's last round has taken its scales: fetch the next block
-            if ((u & 3) == 3) mk_load_scales<R>(scb, scales, vo_scale, (u + 1) >> 2);
+            if ((u & 3) == 3) mk_load_scales<R>(scb, scales, vo_scale, (u + 1) >> 2, T);
         }
         const char* xa_base = xs_storage[u & 1] + xa_off;
         Ahead<R> ah;
@@ -770,20 +773,22 @@ __device__ __forceinline__ void ps_load_scales(WideScales<R>& sc, const PsStream
 // The scales of rounds u and u + 1 (u even): a row's 128 scale bytes of the pair are one
 // 128-byte line (rows are K/16 bytes, a multiple of 128 when K % 2048 == 0), requested by
 // two back-to-back loads per tile instead of one half a round apart, by when L2 may have
-// evicted the line.  s1 of a pair past the last round (odd round count) reads the next
-// row's scales, or zeros past the buffer, and is never used.
+// evicted the line.  A pair whose second round does not exist (odd round count) points
+// that load at an out-of-range vector offset: it reads nothing (zeros), and s1 is then
+// never used.
 template <int R>
 __device__ __forceinline__ void ps_load_scale_pair(WideScales<R>& s0, WideScales<R>& s1,
                                                    const PsStream<R>& st, int64_t scale_shift,
                                                    int u, int64_t K, int g) {
     s0.live = (int64_t)u * kRound + 256 * g < K;
     s1.live = (int64_t)(u + 1) * kRound + 256 * g < K;
+    const bool second = (int64_t)(u + 1) * kRound < K;  // wave-uniform
     const int so = uniform_offset(scale_shift + (int64_t)u * 64);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r], so, 0);
-        const u32x4 v1 =
-            __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r] + 64u, so, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(
+            st.scales, second ? st.vo_scale[r] + 64u : kNoRecordOffset, so, 0);
         s0.sc[r][0] = v0.x;
         s0.sc[r][1] = v0.y;
         s0.sc[r][2] = v0.z;

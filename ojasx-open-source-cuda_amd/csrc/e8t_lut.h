@@ -40,6 +40,9 @@ constexpr uint32_t kHiMagic = kLutSlots == 32 ? 207127u : (kLutSlots == 16 ? 414
 // guard entry precedes the table.  With 8 or 16 slices every address is >= 0.
 constexpr int kLutGuard = kLutSlots == 32 ? 1 : 0;
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
+// Vector offset of a buffer load that must read nothing: at or above every record count
+// used here (< 2^31), so the range check returns zeros whatever the scalar offset adds.
+constexpr uint32_t kNoRecordOffset = 0x80000000u;
 
 // Scalar (SOFFSET) operand of a buffer instruction: the value is wave-uniform by
 // construction; readfirstlane keeps it in an SGPR (the compiler otherwise may compute it
