@@ -366,11 +366,10 @@ __device__ __forceinline__ void stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int6
                                         int64_t K, int wave, int lane, int waves) {
     for (int q = wave; q < 2 * M; q += waves) {
         const int m = q >> 1, half = q & 1;
-        // the round offset in the vector offset: the range check (which does not see a
-        // scalar offset) then turns a partial last round's pieces past the last row into zeros
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             x, lds_ptr(xs + m * kXRow + half * 1024), 16,
-            (uint32_t)(m * K * 2 + u * kRound * 2 + half * 1024 + lane * 16), 0, 0, 0);
+            (uint32_t)(m * K * 2 + half * 1024 + lane * 16), uniform_offset(u * kRound * 2), 0,
+            0);
     }
 }
 
@@ -477,36 +476,32 @@ constexpr uint32_t kMStageBytes = 3072;           // codes of one round (two til
 
 __device__ __forceinline__ uint32_t mk_rot(uint32_t n) { return n >> 2; }
 
-// Issues round u's three code loads into the wave's stage.  The round offset is part of
-// the vector offset: the buffer range check does not see a scalar offset, and a partial
-// last round (K % 512 != 0) would otherwise read past a job's last row.
+// Issues round u's three code loads into the wave's stage.
 __device__ __forceinline__ void mk_issue(char* stg, __amdgpu_buffer_rsrc_t packed,
                                          const uint32_t* ld_code, int u) {
-    const uint32_t ro = (uint32_t)u * 96u;
+    const int so_c = uniform_offset((int64_t)u * 96);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16,
-                                                 ld_code[i] + ro, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16, ld_code[i],
+                                                 so_c, 0, 0);
 }
 
 // Loads scale block b (rounds 4b .. 4b+3) of R row tiles into registers: s[r][q] = the
 // 8 bytes of lane group g in round 4b + q.  Rounds past the last (K % 2048 != 0) do not
-// exist: their loads take an out-of-range vector offset and read nothing.  The block
-// offset is part of the vector offset, so that a partial last round's lane groups past K
-// read zeros past the last row (the range check does not see a scalar offset).  Every load
-// is issued either way: a branch around some of them would make the results' registers
-// wait for the loads.
+// exist: their loads take an out-of-range vector offset and read nothing (zeros, no memory
+// traffic) rather than the next row's scales.  Every load is issued either way: a branch
+// around some of them would make the results' registers wait for the loads.
 template <int R>
 __device__ __forceinline__ void mk_load_scales(uint32_t (&s)[R][4][2],
                                                __amdgpu_buffer_rsrc_t scales,
                                                const uint32_t (&vo_scale)[R], int b, int T) {
+    const int so = uniform_offset((int64_t)b * 128);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint32_t o =
-                4 * b + q < T ? vo_scale[r] + 128u * (uint32_t)b + 32u * q : kNoRecordOffset;
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(scales, o, 0, 0);
+            const uint32_t o = 4 * b + q < T ? vo_scale[r] + 32u * q : kNoRecordOffset;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(scales, o, so, 0);
             s[r][q][0] = v[0];
             s[r][q][1] = v[1];
         }
@@ -516,10 +511,10 @@ __device__ __forceinline__ void mk_load_scales(uint32_t (&s)[R][4][2],
 // per activation row, spread over the workgroup's waves.
 __device__ __forceinline__ void mk_stage_x(char* xs, __amdgpu_buffer_rsrc_t x, int64_t u, int M,
                                            int64_t K, int wave, int lane, int waves) {
-    for (int m = wave; m < M; m += waves)  // round offset in the vector offset (see stage_x)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            x, lds_ptr(xs + m * kMXRow), 16, (uint32_t)(m * K * 2 + u * kMRound * 2 + lane * 16),
-            0, 0, 0);
+    for (int m = wave; m < M; m += waves)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x, lds_ptr(xs + m * kMXRow), 16,
+                                                 (uint32_t)(m * K * 2 + lane * 16),
+                                                 uniform_offset(u * kMRound * 2), 0, 0);
 }
 
 // Step J (0..15) of a mask-kernel round (R row tiles).
@@ -741,19 +736,17 @@ struct PsStream {
 
 
 // Issues the code loads of round u of the tile group whose rows start `code_shift` bytes
-// after tile group c0's into the stage at `stg` (a PsStage of `tiles` tiles).  The shift
-// and the round offset are part of the vector offset, so that the buffer range check (which
-// does not see a scalar offset) turns loads past the buffer's end into zeros: rows past N,
-// and a partial last round's pieces past a job's last row.  (Not a template: the host pass
-// rejects this builtin inside a function template instantiated from a kernel template.)
+// after tile group c0's into the stage at `stg` (a PsStage of `tiles` tiles).  Loads past
+// the buffer's end read zeros.  (Not a template: the host pass rejects this builtin inside
+// a function template instantiated from a kernel template.)
 __device__ __forceinline__ void ps_issue(char* stg, __amdgpu_buffer_rsrc_t packed,
                                          const uint32_t* ld_code, int tiles, int64_t code_shift,
                                          int u) {
-    const uint32_t ro = (uint32_t)(code_shift + (int64_t)u * 192);
+    const int so = uniform_offset(code_shift + (int64_t)u * 192);
 #pragma unroll
     for (int i = 0; i < 3 * tiles; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16,
-                                                 ld_code[i] + ro, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(packed, lds_ptr(stg + 1024 * i), 16, ld_code[i],
+                                                 so, 0, 0);
 }
 
 // The 8 scales of this lane's codes in round u (16 contiguous bytes per lane: every load
@@ -765,11 +758,11 @@ template <int R>
 __device__ __forceinline__ void ps_load_scales(WideScales<R>& sc, const PsStream<R>& st,
                                                int64_t scale_shift, int u, int64_t K, int g) {
     const bool live = (int64_t)u * kRound + 256 * g < K;
-    const uint32_t ro = (uint32_t)(scale_shift + (int64_t)u * 64);  // vector offset: see ps_issue
+    const int so = uniform_offset(scale_shift + (int64_t)u * 64);
     sc.live = live;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r] + ro, 0, 0);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r], so, 0);
         sc.sc[r][0] = v.x;
         sc.sc[r][1] = v.y;
         sc.sc[r][2] = v.z;
@@ -781,8 +774,8 @@ __device__ __forceinline__ void ps_load_scales(WideScales<R>& sc, const PsStream
 // 128-byte line (rows are K/16 bytes, a multiple of 128 when K % 2048 == 0), requested by
 // two back-to-back loads per tile instead of one half a round apart, by when L2 may have
 // evicted the line.  A pair whose second round does not exist (odd round count) points
-// that load at an out-of-range vector offset: it reads nothing (zeros), and s1 is then
-// never used.
+// that load at an out-of-range vector offset: it reads nothing (zeros, no memory traffic),
+// and s1 is then never used.
 template <int R>
 __device__ __forceinline__ void ps_load_scale_pair(WideScales<R>& s0, WideScales<R>& s1,
                                                    const PsStream<R>& st, int64_t scale_shift,
@@ -790,12 +783,12 @@ __device__ __forceinline__ void ps_load_scale_pair(WideScales<R>& s0, WideScales
     s0.live = (int64_t)u * kRound + 256 * g < K;
     s1.live = (int64_t)(u + 1) * kRound + 256 * g < K;
     const bool second = (int64_t)(u + 1) * kRound < K;  // wave-uniform
-    const uint32_t ro = (uint32_t)(scale_shift + (int64_t)u * 64);  // vector offset: see ps_issue
+    const int so = uniform_offset(scale_shift + (int64_t)u * 64);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r] + ro, 0, 0);
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(st.scales, st.vo_scale[r], so, 0);
         const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(
-            st.scales, second ? st.vo_scale[r] + ro + 64u : kNoRecordOffset, 0, 0);
+            st.scales, second ? st.vo_scale[r] + 64u : kNoRecordOffset, so, 0);
         s0.sc[r][0] = v0.x;
         s0.sc[r][1] = v0.y;
         s0.sc[r][2] = v0.z;

@@ -41,7 +41,7 @@ constexpr uint32_t kHiMagic = kLutSlots == 32 ? 207127u : (kLutSlots == 16 ? 414
 constexpr int kLutGuard = kLutSlots == 32 ? 1 : 0;
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
 // Vector offset of a buffer load that must read nothing: at or above every record count
-// used here (< 2^31), so the range check returns zeros whatever the scalar offset adds.
+// used here (< 2^31), so the range check returns zeros without a memory access.
 constexpr uint32_t kNoRecordOffset = 0x80000000u;
 
 // Scalar (SOFFSET) operand of a buffer instruction: the value is wave-uniform by
