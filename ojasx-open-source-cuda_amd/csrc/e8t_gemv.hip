@@ -487,20 +487,24 @@ __device__ __forceinline__ void mk_issue(char* stg, __amdgpu_buffer_rsrc_t packe
 }
 
 // Loads scale block b (rounds 4b .. 4b+3) of R row tiles into registers: s[r][q] = the
-// 8 bytes of lane group g in round 4b + q.  Rounds past the last (K % 2048 != 0) do not
-// exist: their loads take an out-of-range vector offset and read nothing (zeros, no memory
-// traffic) rather than the next row's scales.  Every load is issued either way: a branch
-// around some of them would make the results' registers wait for the loads.
+// 8 bytes of lane group g in round 4b + q.  Scales of k past K (rounds past the last,
+// K % 2048 != 0, and lane groups past K in a partial last round) do not exist: their loads
+// take an out-of-range vector offset and read zeros (no memory traffic), which also
+// zeroes those lane groups' weights of a partial round (their codes are the next row's).
+// Every load is issued either way: a branch around some of them would make the results'
+// registers wait for the loads.
 template <int R>
 __device__ __forceinline__ void mk_load_scales(uint32_t (&s)[R][4][2],
                                                __amdgpu_buffer_rsrc_t scales,
-                                               const uint32_t (&vo_scale)[R], int b, int T) {
+                                               const uint32_t (&vo_scale)[R], int b, int64_t K,
+                                               int g) {
     const int so = uniform_offset((int64_t)b * 128);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint32_t o = 4 * b + q < T ? vo_scale[r] + 32u * q : kNoRecordOffset;
+            const bool live = (int64_t)(4 * b + q) * kMRound + 128 * g < K;
+            const uint32_t o = live ? vo_scale[r] + 32u * q : kNoRecordOffset;
             const auto v = __builtin_amdgcn_raw_buffer_load_b64(scales, o, so, 0);
             s[r][q][0] = v[0];
             s[r][q][1] = v[1];
@@ -624,13 +628,16 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
     char* const stg = stage[wave];
     uint32_t scb[R][4][2];
     mk_issue(stg, packed, ld_code, 0);
-    mk_load_scales<R>(scb, scales, vo_scale, 0, T);
+    mk_load_scales<R>(scb, scales, vo_scale, 0, K, g);
     mk_stage_x(xs_storage[0], xr, 0, M, K, wave, lane, W);
     vm_wait_all();
     __syncthreads();  // table, round-0 weights and activations ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + kLutBaseOffset;
 
-    for (int u = 0; u < T; ++u) {
+    // Round u = 4 v + Q (rounds unrolled by four, so that the scale block entry and the
+    // activation buffer of each round are compile-time choices); false after the last round.
+    auto round = [&](int u, auto qc) -> bool {
+        constexpr int Q = decltype(qc)::value;
         uint32_t cd[R][6], sc[R][2];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -640,37 +647,35 @@ __global__ __launch_bounds__(64 * W) void gemv_mask_kernel(GemvLaunch args) {
                 cd[r][2 * t] = v.x;
                 cd[r][2 * t + 1] = v.y;
             }
-            // round u's scales: block entry u % 4 (wave-uniform select)
-            const int q = u & 3;
-            uint32_t s0 = scb[r][0][0], s1 = scb[r][0][1];
-            s0 = q == 1 ? scb[r][1][0] : s0;
-            s1 = q == 1 ? scb[r][1][1] : s1;
-            s0 = q == 2 ? scb[r][2][0] : s0;
-            s1 = q == 2 ? scb[r][2][1] : s1;
-            s0 = q == 3 ? scb[r][3][0] : s0;
-            s1 = q == 3 ? scb[r][3][1] : s1;
-            // lane groups past K in a partial last round hold the next row's codes
-            const bool live = (int64_t)u * kMRound + 128 * g < K;
-            sc[r][0] = live ? s0 : 0u;
-            sc[r][1] = live ? s1 : 0u;
+            // zero for lane groups past K in a partial last round (mk_load_scales), whose
+            // codes are the next row's
+            sc[r][0] = scb[r][Q][0];
+            sc[r][1] = scb[r][Q][1];
         }
         lds_wait_all();  // the read-back has landed: the stage may be refilled
         const bool has = u + 1 < T;  // uniform over the workgroup
         if (has) {
             mk_issue(stg, packed, ld_code, u + 1);
-            mk_stage_x(xs_storage[(u + 1) & 1], xr, u + 1, M, K, wave, lane, W);
+            mk_stage_x(xs_storage[(Q + 1) & 1], xr, u + 1, M, K, wave, lane, W);
             // the block's last round has taken its scales: fetch the next block
-            if ((u & 3) == 3) mk_load_scales<R>(scb, scales, vo_scale, (u + 1) >> 2, T);
+            if constexpr (Q == 3) mk_load_scales<R>(scb, scales, vo_scale, (u + 1) >> 2, K, g);
         }
-        const char* xa_base = xs_storage[u & 1] + xa_off;
+        const char* xa_base = xs_storage[Q & 1] + xa_off;
         Ahead<R> ah;
         uint32_t sw[R][2];
         ahead_fill<R, 6>(ah, cd, lut, slot, xa_base);
         mk_steps<DT, 2>(cd, sc, lut, slot, xa_base, ah, sw, acc,
-                     std::make_integer_sequence<int, 16>{});
-        if (!has) break;
+                        std::make_integer_sequence<int, 16>{});
+        if (!has) return false;
         vm_wait_all();
         __syncthreads();  // next round's stage (own) and activations (shared) ready
+        return true;
+    };
+    for (int u = 0;; u += 4) {
+        if (!round(u, std::integral_constant<int, 0>{})) break;
+        if (!round(u + 1, std::integral_constant<int, 1>{})) break;
+        if (!round(u + 2, std::integral_constant<int, 2>{})) break;
+        if (!round(u + 3, std::integral_constant<int, 3>{})) break;
     }
 
     // lane (g, n) holds rows m = 4g + q of column n (MFMA 16x16 output layout)
