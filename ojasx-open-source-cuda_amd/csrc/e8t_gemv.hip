@@ -319,9 +319,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch args) {
 // one workgroup barrier per round.
 
 constexpr int kRound = 1024;                      // K per round
-// Post-scaled kernel: tile groups per workgroup.  Measured on MI355X (32-layer decode
-// stack, M = 1): 1 -> 3.7-3.8 TB/s, 2 -> 3.5, 4 -> 3.3, 8 -> 2.9; longer workgroups save
-// table fills and prologue latency but leave a longer tail of partly idle CUs.
+// Post-scaled kernel: tile groups per workgroup, one.  Measured on MI355X when the kernel
+// could take several (32-layer decode stack, M = 1): 1 -> 3.7-3.8 TB/s, 2 -> 3.5, 4 -> 3.3,
+// 8 -> 2.9; longer workgroups save table fills and prologue latency but leave a longer tail
+// of partly idle CUs.
 constexpr int kPsChunk = 1;
 // Waves per workgroup of the post-scaled kernel.
 constexpr int kPsWaves = 4;
@@ -951,13 +952,14 @@ __device__ __forceinline__ void ps_store(const GemvJob& job, void* ybase, int M,
 }
 
 // MM: activation rows handled (1 or 4; M <= MM); W: waves per workgroup.  A workgroup
-// runs args.chunk consecutive tile groups (W * R row tiles each) of one job, one
-// weight/activation prefetch pipeline across the tile-group boundaries, and fills its
-// table once.  Tile group c of the workgroup reads rows 16 W R c further down the same
-// buffers: the shift is a wave-uniform offset.
+// runs one tile group (W * R row tiles) of one job: its items are the tile group's rounds,
+// so the round of each item of the loop (unrolled by two) has a compile-time parity.
+// (Several tile groups per workgroup, one pipeline across them, measured slower: see
+// kPsChunk.)
 template <int DT, int R, int MM, int W>
 __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     static_assert(MM == 1 || MM == 4, "post-scaled layout holds at most 4 activation rows");
+    static_assert(kPsChunk == 1, "one tile group per workgroup: its items are its rounds");
     // Table slices: 32 at M = 1 (conflict-free 8-byte reads; the 20 KB table still leaves
     // three workgroups per CU), 16 at M <= 4, whose larger activation buffers need the LDS.
     constexpr int SL = MM == 1 ? kPsSlotsM1 : (R == kPsTiles ? kPsSlotsM4 : kLutSlots);
@@ -1000,12 +1002,7 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     const int M = args.M;
     const uint32_t rowbytes = (uint32_t)(K * 3 / 16);
     const uint32_t srowbytes = (uint32_t)(K / 16);
-    constexpr int64_t kGroupRows = 16 * W * R;
-    // tile groups of this workgroup: [c0, c1) of the job
-    const int64_t groups = (N + kGroupRows - 1) / kGroupRows;
-    const int64_t c0 = wg * args.chunk;
-    const int64_t c1 = c0 + args.chunk < groups ? c0 + args.chunk : groups;
-    const int64_t tile0 = (c0 * W + wave) * R;  // first row tile, tile group c0
+    const int64_t tile0 = (wg * W + wave) * R;  // this wave's first row tile
 
     PsStream<R> st;
     st.packed = __builtin_amdgcn_make_buffer_rsrc((void*)job.packed, (short)0,
@@ -1035,14 +1032,10 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     const char* xa0 = xsa + (a_live ? am * kXRow + 512 * g : kXBytes);
     const char* xa1 = xsb + (a_live ? am * kXRow + 512 * g : kXBytes);
 
-    // Items are (tile group c0 + c, round u), c-major; item (c, u) is processed while the
-    // next item's codes, scales and activations are fetched.  Items alternate between the
-    // activation buffers xsa and xsb (the loop is unrolled by two so that each buffer is a
-    // compile-time choice).
+    // Items are the rounds u; item u is processed while round u + 1's codes, scales and
+    // activations are fetched.  Items alternate between the activation buffers xsa and xsb
+    // (the loop is unrolled by two so that each buffer is a compile-time choice).
     const int T = (int)((K + kRound - 1) / kRound);
-    const int ngroups = (int)(c1 - c0);
-    const int64_t code_gshift = kGroupRows * (int64_t)rowbytes;
-    const int64_t scale_gshift = kGroupRows * (int64_t)srowbytes;
     float acc[R][MM];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -1060,38 +1053,37 @@ __global__ __launch_bounds__(64 * W) void gemv_ps_kernel(GemvLaunch args) {
     __syncthreads();  // table, zero blocks, round-0 weights and activations ready
     const char* lut = reinterpret_cast<const char*>(lut_storage) + G::kBaseOffset;
 
-    int c = 0, u = 0;
-    // one item: computes from the activation buffer behind xa_cur, fetches the next item
-    // into xs_next; false when there is no next item
-    auto item = [&](const char* xa_cur, char* xs_next) -> bool {
+    int u = 0;
+    // one item (round u, parity P = u % 2): computes from the activation buffer behind
+    // xa_cur, fetches round u + 1 into xs_next; false after the last round.  An odd item
+    // fetches the next scale pair, an even one takes the odd half of its own.
+    auto item = [&](const char* xa_cur, char* xs_next, auto pc) -> bool {
+        constexpr int P = decltype(pc)::value;
         ps_readback<R>(stg, st, w);
-        const int64_t tg = tile0 + (int64_t)c * W * R;
         uint32_t bv[R];
-        if (u == T - 1) ps_load_bias<DT, R>(job, tg, lane, bv);
+        if (u == T - 1) ps_load_bias<DT, R>(job, tile0, lane, bv);
         lds_wait_all();  // the read-back has landed: the stage may be refilled
-        const int cn = u + 1 == T ? c + 1 : c, un = u + 1 == T ? 0 : u + 1;
-        const bool has = cn < ngroups;  // uniform over the workgroup
+        const bool has = u + 1 < T;  // uniform over the workgroup
         if (has) {
-            ps_issue(stg_bytes, st.packed, st.ld_code, R, cn * code_gshift, un);
-            if ((un & 1) == 0)
-                ps_load_scale_pair<R>(sc_next, sc_odd, st, cn * scale_gshift, un, K, g);
+            ps_issue(stg_bytes, st.packed, st.ld_code, R, 0, u + 1);
+            if constexpr (P == 1)
+                ps_load_scale_pair<R>(sc_next, sc_odd, st, 0, u + 1, K, g);
             else
                 sc_next = sc_odd;
-            stage_x(xs_next, st.x, un, M, K, wave, lane, W);
+            stage_x(xs_next, st.x, u + 1, M, K, wave, lane, W);
         }
         ps_round<DT, R, MM, SL>(w, sc, lut, slot, xa_cur, acc);
-        if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tg, lane, acc, bv);
+        if (u == T - 1) ps_store<DT, R, MM>(job, ybase, M, tile0, lane, acc, bv);
         if (!has) return false;
         vm_wait_all();
         __syncthreads();  // next item's codes (own stage) and activations (shared) ready
         sc = sc_next;
-        c = cn;
-        u = un;
+        ++u;
         return true;
     };
     for (;;) {
-        if (!item(xa0, xsb)) break;
-        if (!item(xa1, xsa)) break;
+        if (!item(xa0, xsb, std::integral_constant<int, 0>{})) break;
+        if (!item(xa1, xsa, std::integral_constant<int, 1>{})) break;
     }
 }
 
@@ -3189,10 +3181,9 @@ static hipError_t launch_mask(const GemvLaunch& a, int64_t wgs, hipStream_t stre
 template <int DT, int R, int MM, int W>
 static hipError_t launch_ps(const GemvLaunch& a, const GemvPlan& p, int64_t wgs,
                             hipStream_t stream) {
-    GemvLaunch l = a;
-    l.chunk = p.C;
+    (void)p;  // the plan's tile groups per workgroup: kPsChunk, one
     hipLaunchKernelGGL((gemv_ps_kernel<DT, R, MM, W>), dim3((unsigned)wgs), dim3(64 * W), 0,
-                       stream, l);
+                       stream, a);
     return hipGetLastError();
 }
 

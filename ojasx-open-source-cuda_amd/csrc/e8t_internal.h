@@ -104,7 +104,6 @@ struct GemvLaunch {
     void* y;                       // default output
     int njobs;
     int M;
-    int chunk;                     // post-scaled kernel: tile groups per workgroup
     int lora_inline;               // staged-tile kernel, one round per wave: jobs with an
                                    // adapter form u from lora_a themselves (lora_u unused)
 };
