@@ -27,6 +27,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     return u >> 16;
 }
 
+// fp32 -> bf16 bits, round-nearest-even, by the hardware conversion (v_cvt_pk_bf16_f32):
+// one instruction instead of the integer sequence above.  For operands of the kernels' own
+// arithmetic (scales, 2-bit and 1-bit value words): finite values round as above, and a
+// NaN stays a NaN, whose bits never reach memory (stores go through f32_to_bf16_bits).
+__device__ __forceinline__ uint32_t bf16_bits_hw(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
 // fp32 -> fp16 bits, round-nearest-even (v_cvt_f16_f32), subnormals kept.
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
@@ -59,7 +67,7 @@ __device__ __forceinline__ void keep_f32(float& v) { asm volatile("" : "+v"(v));
 // value exactly, bf16 rounds it to bf16.
 template <int DT> __device__ __forceinline__ float scale_for(uint32_t s16) {
     float s = f16_bits_to_f32(s16);
-    if constexpr (DT == kBF16) s = bf16_bits_to_f32(f32_to_bf16_bits(s));
+    if constexpr (DT == kBF16) s = bf16_bits_to_f32(bf16_bits_hw(s));
     return s;
 }
 
@@ -133,7 +141,7 @@ template <int DT>
 __device__ __forceinline__ uint32_t rnd_bits(float v) {
     keep_f32(v);
     if constexpr (DT == kF16) return f32_to_f16_bits(v);
-    else return f32_to_bf16_bits(v);
+    else return bf16_bits_hw(v);
 }
 
 // Value words {S0, S1} of one 2-bit scale group (fp16 bits s16): the four weights -B, -A,
