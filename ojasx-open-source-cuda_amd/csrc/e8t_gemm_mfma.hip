@@ -808,7 +808,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_mfma_kernel(
 
     if constexpr (kTernary) fill_lut<C::THREADS>(lut_storage, kLutMasks);
     else if constexpr (FMT == kFmt2Bit) fill_sel2(reinterpret_cast<uint2*>(lut_storage), C::THREADS);
-    else fill_sel1(lut_storage, C::THREADS);
+    else fill_sel1<C::THREADS>(lut_storage);
 
     // ---- tile assignment: contiguous tile range per XCD, M-grouped within it
     const int64_t tm_n = (M + C::BM - 1) / C::BM, tn_n = (NO + C::BN - 1) / C::BN;

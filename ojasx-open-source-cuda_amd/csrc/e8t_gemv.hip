@@ -1470,22 +1470,46 @@ __device__ __forceinline__ void b1_load(uint4 (&cp)[4], uint4 (&sp)[4],
 }
 
 // The 1-bit post-scaled table: code -> its 8 coordinates (0, +-1, +-2) in the activation
-// dtype, C copies of each 16-byte entry.
-template <int DT, int C>
-__device__ __forceinline__ void fill_v1(uint4* tab, int nthreads) {
-    auto half = [](int c) -> uint32_t {
-        if constexpr (DT == kBF16)
-            return c == 0 ? 0u : c == 1 ? 0x3F80u : c == 2 ? 0x4000u : c == -1 ? 0xBF80u : 0xC000u;
-        else
-            return c == 0 ? 0u : c == 1 ? 0x3C00u : c == 2 ? 0x4000u : c == -1 ? 0xBC00u : 0xC000u;
-    };
-    for (int i = (int)threadIdx.x; i < kSel1Entries * C; i += nthreads) {
-        const int e = i / C;
-        uint32_t w[4];
-#pragma unroll
+// dtype (16 bytes per code), built at compile time for bf16 and fp16 and copied into LDS.
+constexpr uint32_t v1_half(bool bf16, int c) {
+    return bf16 ? (c == 0 ? 0u : c == 1 ? 0x3F80u : c == 2 ? 0x4000u : c == -1 ? 0xBF80u : 0xC000u)
+                : (c == 0 ? 0u : c == 1 ? 0x3C00u : c == 2 ? 0x4000u : c == -1 ? 0xBC00u : 0xC000u);
+}
+
+struct alignas(16) V1Tab {
+    uint32_t w[kSel1Entries * 4];
+};
+
+constexpr V1Tab make_v1_tab(bool bf16) {
+    V1Tab t{};
+    const RootTable r = make_root_table();
+    for (int e = 0; e < kSel1Entries; ++e)
         for (int h = 0; h < 4; ++h)
-            w[h] = half(kRootTable.c[e][2 * h]) | (half(kRootTable.c[e][2 * h + 1]) << 16);
-        tab[i] = make_uint4(w[0], w[1], w[2], w[3]);
+            t.w[4 * e + h] = v1_half(bf16, r.c[e][2 * h]) | (v1_half(bf16, r.c[e][2 * h + 1]) << 16);
+    return t;
+}
+
+static __device__ const V1Tab kV1Tab[2] = {make_v1_tab(true), make_v1_tab(false)};
+
+// Fills C copies of each entry (copy c of entry e at 16 (C e + c) bytes; lane l reads copy
+// l % C, spreading a read's lanes over C bank groups) from the device table (an L2 hit
+// after the first workgroup): every load of a thread is issued before its first write.
+// NT: threads of the workgroup.
+template <int DT, int C, int NT>
+__device__ __forceinline__ void fill_v1(uint4* tab) {
+    constexpr int kItems = kSel1Entries * C;
+    constexpr int kPer = (kItems + NT - 1) / NT;
+    const uint4* src = reinterpret_cast<const uint4*>(kV1Tab[DT == kBF16 ? 0 : 1].w);
+    uint4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        v[k] = src[(i < kItems ? i : 0) / C];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        if (i < kItems) tab[i] = v[k];
     }
 }
 
@@ -1521,7 +1545,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2_kernel(
     __shared__ __attribute__((aligned(16))) char xs1[kXsBytes + kB2ZeroBytes];
     __shared__ float red[kB2Waves][MM][64];
 
-    if constexpr (kRoot) fill_v1<DT, 1>(lut_storage, 64 * kB2Waves);
+    if constexpr (kRoot) fill_v1<DT, 1, 64 * kB2Waves>(lut_storage);
     else fill_b2lut<DT, 64 * kB2Waves>(lut_storage);
     for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * kB2Waves) {
         reinterpret_cast<uint4*>(xs0 + kXsBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -1915,7 +1939,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2m_kernel(
 
     if constexpr (FMT == kFmtTernary)
         fill_lut<64 * kB2Waves, kLutValidEntries>(lut_storage, kLutMasks);
-    else if constexpr (FMT == kFmtRoot) fill_sel1(lut_storage, 64 * kB2Waves);
+    else if constexpr (FMT == kFmtRoot) fill_sel1<64 * kB2Waves>(lut_storage);
     else fill_b2sel<64 * kB2Waves>(lut_storage);
 
     const int lane = threadIdx.x & 63;
@@ -2118,7 +2142,7 @@ __global__ __launch_bounds__(64 * kB2Waves) void gemv2s_kernel(
 
     if constexpr (FMT == kFmtTernary)
         fill_lut<64 * kB2Waves, kLutValidEntries>(lut_storage, kLutMasks);
-    else if constexpr (FMT == kFmtRoot) fill_sel1(lut_storage, 64 * kB2Waves);
+    else if constexpr (FMT == kFmtRoot) fill_sel1<64 * kB2Waves>(lut_storage);
     else fill_b2sel<64 * kB2Waves>(lut_storage);
 
     const int lane = threadIdx.x & 63;
@@ -3592,9 +3616,9 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     // entries hold four weights (post-scaled) or two selector words (B operand; 32 copies,
     // conflict-free, measured 2% slower at M = 1); one of the 4 KB 1-bit tables, whose
     // 16-byte entries hold a code's coordinates (post-scaled) or selector words (B operand):
-    // more copies cost more to fill than their bank conflicts (32-layer stack: coordinates
-    // 0.478 ms at M = 1 with one copy, 0.50 / 0.54 / 0.59 with 2 / 4 / 8; selectors 0.569
-    // against 0.585 ms with 8)
+    // more copies cost more than their bank conflicts (32-layer stack, coordinates copied
+    // from the compile-time table: 0.408 ms at M = 1 with one copy, 0.417 / 0.422 / 0.448 with
+    // 2 / 4 / 8; selectors 0.569 against 0.585 ms with 8)
     constexpr int BC = FMT == kFmtRoot ? 1 : 16;
     __shared__ uint4 lut_storage[FMT == kFmtRoot ? kSel1Entries * BC : kB2ByteLutU4<16>];
     // two activation stages, separate LDS objects; the post-scaled ones end in a zero block
@@ -3603,14 +3627,14 @@ __global__ __launch_bounds__(64 * W) void gemv2g_kernel(GemvLaunch args) {
     __shared__ __attribute__((aligned(128))) char xs1[G * kXBytes + (kPost ? kB2ZeroBytes : 0)];
 
     if constexpr (kPost) {
-        if constexpr (FMT == kFmtRoot) fill_v1<DT, BC>(lut_storage, 64 * W);
+        if constexpr (FMT == kFmtRoot) fill_v1<DT, BC, 64 * W>(lut_storage);
         else fill_b2blut<DT, 64 * W, BC>(lut_storage);
         for (int i = (int)threadIdx.x; i < kB2ZeroBytes / 16; i += 64 * W) {
             reinterpret_cast<uint4*>(xs0 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
             reinterpret_cast<uint4*>(xs1 + kXBytes)[i] = make_uint4(0u, 0u, 0u, 0u);
         }
     } else {
-        if constexpr (FMT == kFmtRoot) fill_sel1c<BC>(lut_storage, 64 * W);
+        if constexpr (FMT == kFmtRoot) fill_sel1<64 * W, BC>(lut_storage);
         else fill_b2bsel<64 * W, BC>(lut_storage);
     }
 

@@ -293,29 +293,43 @@ __host__ __device__ inline uint32_t root_code_fast(const float (&v)[8]) {
 // table (4 KB) maps a code to the four selector words of its 8 weights.
 constexpr int kSel1Entries = 256;
 
-__device__ __forceinline__ void fill_sel1(uint4* tab, int nthreads) {
-    for (int e = (int)threadIdx.x; e < kSel1Entries; e += nthreads) {
-        uint32_t w[4];
-#pragma unroll
+struct alignas(16) Sel1Tab {
+    uint32_t w[kSel1Entries * 4];
+};
+
+constexpr Sel1Tab make_sel1_tab() {
+    Sel1Tab t{};
+    const RootTable r = make_root_table();
+    for (int e = 0; e < kSel1Entries; ++e)
         for (int h = 0; h < 4; ++h)
-            w[h] = root_sel_pair(kRootTable.c[e][2 * h]) |
-                   (root_sel_pair(kRootTable.c[e][2 * h + 1]) << 16);
-        tab[e] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+            t.w[4 * e + h] = root_sel_pair(r.c[e][2 * h]) | (root_sel_pair(r.c[e][2 * h + 1]) << 16);
+    return t;
 }
 
-// The same table with C copies of each entry (entry stride 16 C bytes), lane l reading copy
-// l % C: with C = 8 the eight lanes a b128 read serves per cycle hit distinct banks.
-template <int C>
-__device__ __forceinline__ void fill_sel1c(uint4* tab, int nthreads) {
-    for (int i = (int)threadIdx.x; i < kSel1Entries * C; i += nthreads) {
-        const int e = i / C;
-        uint32_t w[4];
+// The selector table, built at compile time; kernels copy it into LDS (an L2 hit after the
+// first workgroup) instead of deriving every entry from the code table: per entry that took
+// eight byte loads and a select chain per coordinate.
+static __device__ const Sel1Tab kSel1Tab = make_sel1_tab();
+
+// Copies the table into LDS with C copies of each entry (entry stride 16 C bytes), lane l
+// reading copy l % C: with C = 8 the eight lanes a b128 read serves per cycle hit distinct
+// banks.  Every load of a thread is issued before its first write.  NT: threads of the
+// workgroup.
+template <int NT, int C = 1>
+__device__ __forceinline__ void fill_sel1(uint4* tab) {
+    constexpr int kItems = kSel1Entries * C;
+    constexpr int kPer = (kItems + NT - 1) / NT;
+    const uint4* src = reinterpret_cast<const uint4*>(kSel1Tab.w);
+    uint4 v[kPer];
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
-            w[h] = root_sel_pair(kRootTable.c[e][2 * h]) |
-                   (root_sel_pair(kRootTable.c[e][2 * h + 1]) << 16);
-        tab[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    for (int k = 0; k < kPer; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        v[k] = src[(i < kItems ? i : 0) / C];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        if (i < kItems) tab[i] = v[k];
     }
 }
 
